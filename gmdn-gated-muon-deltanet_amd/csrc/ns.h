@@ -1,0 +1,153 @@
+// Block-cooperative Newton-Schulz msign and its VJP for a D x D fp32 matrix
+// (reference fast_scan.py:63-69 forward, :107-131 VJP).
+//
+// D/16 waves; wave w owns rows 16w..16w+15 of every matrix and holds them as
+// D-layout tiles of the transpose (lane <-> row, registers <-> columns), the
+// same layout as the scan state.  Matrices that every wave reads in full are
+// published through a shared D x D store of layout L (swizzled LDS or a plain
+// global workspace), one barrier per publication.
+//
+// Forward step (P = X X^T is symmetric, so each wave's column block of P is
+// computable from the published X and its own rows):
+//   Pc  = P[:, rows]  = X_pub (row reads) x X^T_own
+//   P2c = (P P)[:, rows] = P_pub (row reads) x Pc
+//   X^T <- a X^T + X^T Z,  Z = b P + c P^2  (X_pub column reads x Zc)
+//
+// VJP step for iterate X_k with incoming Xbar (see oracle/scan.py msign_vjp):
+//   Bbar = Xbar X_k^T, Abar = b Bbar + c (Bbar P + P Bbar)
+//   Xbar <- a Xbar + Bm Xbar + (Abar + Abar^T) X_k,  Bm = b P + c P^2
+// Each wave forms the column block [:, rows] of Bm and of Abar + Abar^T from
+// its own rows plus the published X_k, Xbar, P and Bbar.
+#pragma once
+#include "prec.h"
+
+namespace gmdn {
+
+constexpr float NS_A = 3.4445f, NS_B = -4.7750f, NS_C = 2.0315f;  // fast_scan.py:32
+
+template <int NW>
+GMDN_DEV float block_sum(float x, float* red) {
+  x = wave_sum(x);
+  if (lane_id() == 0) red[wave_id()] = x;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int q = 0; q < NW; ++q) t += red[q];
+  __syncthreads();
+  return t;
+}
+
+template <class P, class L, int D>
+struct NSBlock {
+  static constexpr int NT = D / 16;
+  static constexpr int NKB = D / 32;
+  using Op = typename P::Op;
+
+  template <int N>
+  static GMDN_DEV void pack_all(const f32x4 (&t)[N], Op (&o)[N / 2]) {
+#pragma unroll
+    for (int kb = 0; kb < N / 2; ++kb) o[kb] = P::pack(t[2 * kb], t[2 * kb + 1]);
+  }
+
+  static GMDN_DEV void publish(float* M, const f32x4 (&t)[NT]) {
+    const int r0 = 16 * wave_id();
+#pragma unroll
+    for (int c = 0; c < NT; ++c) mat_store_tileT<L>(M, r0, 16 * c, t[c]);
+  }
+
+  // own rows of `pub` times the wave's operand: tile [r'][r] = sum_k pub[r'][k] B[k][r]
+  static GMDN_DEV f32x4 rowprod(const float* pub, int tr, const Op (&B)[NKB]) {
+    f32x4 acc = zero4();
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) acc = P::mma(row_op<P, L>(pub, 16 * tr, 32 * kb), B[kb], acc);
+    return acc;
+  }
+  // tile [c][r] = sum_k pub[k][c] B[k][r]
+  static GMDN_DEV f32x4 colprod(const float* pub, int tc, const Op (&B)[NKB], f32x4 acc) {
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) acc = P::mma(col_op<P, L>(pub, 32 * kb, 16 * tc), B[kb], acc);
+    return acc;
+  }
+
+  // One quintic step on the wave's rows XT (D-layout tiles of X^T).
+  static GMDN_DEV void step(f32x4 (&XT)[NT], float* XM, float* PM) {
+    const int r0 = 16 * wave_id();
+    publish(XM, XT);
+    __syncthreads();
+    Op Bx[NKB];
+    pack_all(XT, Bx);
+    f32x4 Pc[NT];
+#pragma unroll
+    for (int tr = 0; tr < NT; ++tr) Pc[tr] = rowprod(XM, tr, Bx);
+    // P is symmetric: the column block is also the wave's rows of P
+#pragma unroll
+    for (int tr = 0; tr < NT; ++tr) mat_store_tileT<L>(PM, r0, 16 * tr, Pc[tr]);
+    __syncthreads();
+    Op Bp[NKB];
+    pack_all(Pc, Bp);
+    f32x4 Z[NT];
+#pragma unroll
+    for (int tr = 0; tr < NT; ++tr) Z[tr] = NS_B * Pc[tr] + NS_C * rowprod(PM, tr, Bp);
+    Op Bz[NKB];
+    pack_all(Z, Bz);
+#pragma unroll
+    for (int tc = 0; tc < NT; ++tc) XT[tc] = colprod(XM, tc, Bz, NS_A * XT[tc]);
+    __syncthreads();
+  }
+
+  // One reverse step: XbT (D-layout tiles of Xbar^T, own rows) updated in
+  // place given iterate XkT (own rows).  Uses four shared stores.
+  static GMDN_DEV void vjp_step(const f32x4 (&XkT)[NT], f32x4 (&XbT)[NT], float* XM, float* PM,
+                                float* XbM, float* BM) {
+    const int r0 = 16 * wave_id();
+    publish(XM, XkT);
+    publish(XbM, XbT);
+    __syncthreads();
+    Op Bk[NKB], Bxb[NKB];
+    pack_all(XkT, Bk);
+    pack_all(XbT, Bxb);
+    f32x4 Pc[NT], BR[NT], BC[NT];
+#pragma unroll
+    for (int tr = 0; tr < NT; ++tr) {
+      Pc[tr] = rowprod(XM, tr, Bk);    // P[r'][r]
+      BR[tr] = rowprod(XM, tr, Bxb);   // Bbar[r][r'] (own row block, transposed)
+      BC[tr] = rowprod(XbM, tr, Bk);   // Bbar[r'][r] (own column block)
+    }
+#pragma unroll
+    for (int tr = 0; tr < NT; ++tr) {
+      mat_store_tileT<L>(PM, r0, 16 * tr, Pc[tr]);
+      mat_store_tileT<L>(BM, r0, 16 * tr, BR[tr]);  // rows of Bbar
+    }
+    __syncthreads();
+    Op Bp[NKB], Bbr[NKB], Bbc[NKB];
+    pack_all(Pc, Bp);
+    pack_all(BR, Bbr);
+    pack_all(BC, Bbc);
+    f32x4 Bm[NT], Ssym[NT];
+#pragma unroll
+    for (int tr = 0; tr < NT; ++tr) {
+      Bm[tr] = NS_B * Pc[tr] + NS_C * rowprod(PM, tr, Bp);
+      f32x4 t = rowprod(BM, tr, Bp);                      // sum Bbar[r'][r''] P[r''][r]
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+        const Op pr = row_op<P, L>(PM, 16 * tr, 32 * kb);  // P[r'][r'']
+        acc = P::mma(pr, Bbc[kb], acc);                  // sum P[r'][r''] Bbar[r''][r]
+        acc = P::mma(pr, Bbr[kb], acc);                  // sum P[r'][r''] Bbar[r][r'']
+        acc = P::mma(col_op<P, L>(BM, 32 * kb, 16 * tr), Bp[kb], acc);  // sum Bbar[r''][r'] P[r''][r]
+      }
+      Ssym[tr] = NS_B * (BC[tr] + BR[tr]) + NS_C * (t + acc);
+    }
+    Op Bbm[NKB], Bs[NKB];
+    pack_all(Bm, Bbm);
+    pack_all(Ssym, Bs);
+#pragma unroll
+    for (int tc = 0; tc < NT; ++tc) {
+      f32x4 acc = colprod(XbM, tc, Bbm, NS_A * XbT[tc]);
+      XbT[tc] = colprod(XM, tc, Bs, acc);
+    }
+    __syncthreads();
+  }
+};
+
+}  // namespace gmdn

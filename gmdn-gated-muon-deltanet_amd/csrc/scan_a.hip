@@ -1,0 +1,412 @@
+// Level A: the drop-in chunk state scan, fast_state_scan(U, K, a, b, m, n,
+// rule, ns) (reference fast_scan.py:403-414; kernels :206-331; math :72-186).
+//
+// Row-separable rules (delta, adam).  Row r of G_i = U_i - S_i K_i needs only
+// row r of S_i, and the delta/adam updates are elementwise, so every 16-row
+// tile of S is an independent recurrence.  One wave owns one row tile for the
+// whole sequence and keeps it in registers as D-layout tiles of S^T (lane <->
+// row r, registers <-> columns c); a workgroup of two waves shares one
+// LDS-staged copy of each chunk's K (fp32, swizzled, double buffered and
+// filled by global_load_lds_dwordx4 while the previous chunk computes).
+//
+//   forward, chunk i, wave tile rows r:
+//     G^T = U^T - K^T S^T       (MFMA tiles: A = K^T rows (LDS column reads),
+//                                B = -S^T from the wave's own tiles, pair order)
+//     delta: S^T <- a S^T + G^T
+//     adam : M^T <- m M^T + (1-m) G^T ; V^T <- n V^T + (1-n) G^T.^2 ;
+//            S^T <- a S^T + b M^T / (sqrt(V^T) + eps)
+//
+//   backward (reverse over chunks; Sb = dL/dS_{i+1}):
+//     delta: Gb = Sb
+//     adam : elementwise VJP of the moments (fast_scan.py:167-182)
+//     dU_i = Gb ;  Sb <- a Sb - Gb K^T + gS_i   (A = K rows (LDS row reads),
+//                                                B = -Gb^T from registers)
+//   dK_i = -S_i^T Gb_i and the scalar gradients are formed per chunk by a
+//   second, chunk-parallel kernel (contraction over all rows of S).
+#include "prec.h"
+#include "scan_a.h"
+
+namespace gmdn {
+
+constexpr int A_WAVES = 2;                 // row tiles per workgroup
+constexpr int A_THREADS = A_WAVES * 64;
+
+// blockIdx -> (bh, row block).  Workgroups are dispatched round-robin over
+// the 8 XCDs; keep all row blocks of one (b, h) on one XCD so they share its
+// K_i stream through that XCD's L2.
+GMDN_DEV void map_rows_block(int64_t BH, int nblk, int64_t& bh, int& blk) {
+  const int64_t x = blockIdx.x;
+  if (BH % 8 == 0) {
+    const int64_t xcd = x & 7, slot = x >> 3;
+    blk = (int)(slot % nblk);
+    bh = (slot / nblk) * 8 + xcd;
+  } else {
+    bh = x / nblk;
+    blk = (int)(x % nblk);
+  }
+}
+
+template <int D, int RULE, int PREC>
+__global__ void __launch_bounds__(A_THREADS)
+scan_fwd_rows(const float* __restrict__ U, const float* __restrict__ K,
+              const float* __restrict__ av, const float* __restrict__ bv,
+              const float* __restrict__ mv, const float* __restrict__ nv,
+              float* __restrict__ S_all, float* __restrict__ M_all,
+              float* __restrict__ V_all, int64_t BH, int N) {
+  using P = typename PrecSel<PREC>::T;
+  constexpr int NT = D / 16;   // 16-wide column tiles of a row tile
+  constexpr int NKB = D / 32;  // 32-wide k-blocks
+  extern __shared__ __align__(16) float smem[];
+
+  int64_t bh;
+  int blk;
+  map_rows_block(BH, D / (16 * A_WAVES), bh, blk);
+  const int l = lane_id(), G = l >> 4, rl = l & 15;
+  const int r0 = (blk * A_WAVES + wave_id()) * 16;  // first row of this wave's tile
+  const int64_t mat = (int64_t)D * D;
+  const float* Ub = U + bh * N * mat;
+  const float* Kb = K + bh * N * mat;
+
+  f32x4 S[NT], M[NT], V[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) S[t] = M[t] = V[t] = zero4();
+
+  // row r0+rl, columns 16t + 4G .. +3 of a (D x D) matrix at base
+  auto roff = [&](int t) { return (int64_t)(r0 + rl) * D + 16 * t + 4 * G; };
+
+  if (N > 0) lds_dma_matrix<D, A_THREADS>(smem, Kb);
+  f32x4 Unext[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) Unext[t] = *reinterpret_cast<const f32x4*>((Ub + roff(t)));
+  wait_vmem();
+  __syncthreads();
+
+  for (int i = 0; i < N; ++i) {
+    const float* kl = (smem + (i & 1) * D * D);
+    f32x4 Ucur[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) Ucur[t] = Unext[t];
+    if (i + 1 < N) {
+      lds_dma_matrix<D, A_THREADS>((smem + ((i + 1) & 1) * D * D), Kb + (i + 1) * mat);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) Unext[t] = *reinterpret_cast<const f32x4*>((Ub + (i + 1) * mat + roff(t)));
+    }
+    const int64_t si = bh * N + i;
+    // pre-update states
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      *reinterpret_cast<f32x4*>((S_all + si * mat + roff(t))) = S[t];
+      if constexpr (RULE == 2) {
+        if (M_all) *reinterpret_cast<f32x4*>((M_all + si * mat + roff(t))) = M[t];
+        if (V_all) *reinterpret_cast<f32x4*>((V_all + si * mat + roff(t))) = V[t];
+      }
+    }
+    // B operands: -S^T, one per k-block
+    typename P::Op Bop[NKB];
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) Bop[kb] = P::pack(-S[2 * kb], -S[2 * kb + 1]);
+    const float a = av[si];
+    float b = 0.f, m = 0.f, n = 0.f;
+    if constexpr (RULE == 2) {
+      b = bv[si];
+      m = mv[si];
+      n = nv[si];
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      f32x4 g = Ucur[t];  // G^T tile rows c = 16t.., cols = this wave's rows
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) g = P::mma(col_op<P, SwzMat<D>>(kl, 32 * kb, 16 * t), Bop[kb], g);
+      if constexpr (RULE == 0) {
+        S[t] = a * S[t] + g;
+      } else {
+        M[t] = m * M[t] + (1.f - m) * g;
+        V[t] = n * V[t] + (1.f - n) * g * g;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) S[t][j] = a * S[t][j] + b * M[t][j] / (sqrtf(V[t][j]) + 1e-6f);
+      }
+    }
+    wait_vmem();
+    __syncthreads();
+  }
+}
+
+// Reverse scan for the row-separable rules.  Writes dU (= Gb) for every
+// chunk, and for adam the per-row-tile partial sums of da, db, dm, dn into
+// part[(bh*N + i) * n_tiles + tile][4]; delta's da is formed later from dU
+// and S_all.
+template <int D, int RULE, int PREC>
+__global__ void __launch_bounds__(A_THREADS)
+scan_bwd_rows(const float* __restrict__ U, const float* __restrict__ K,
+              const float* __restrict__ av, const float* __restrict__ bv,
+              const float* __restrict__ mv, const float* __restrict__ nv,
+              const float* __restrict__ S_all, const float* __restrict__ M_all,
+              const float* __restrict__ V_all, const float* __restrict__ gS,
+              float* __restrict__ dU, float* __restrict__ part, int64_t BH, int N) {
+  using P = typename PrecSel<PREC>::T;
+  constexpr int NT = D / 16;
+  constexpr int NKB = D / 32;
+  constexpr int NTILES = D / 16;
+  extern __shared__ __align__(16) float smem[];
+
+  int64_t bh;
+  int blk;
+  map_rows_block(BH, D / (16 * A_WAVES), bh, blk);
+  const int l = lane_id(), G = l >> 4, rl = l & 15;
+  const int tile = blk * A_WAVES + wave_id();
+  const int r0 = tile * 16;
+  const int64_t mat = (int64_t)D * D;
+  const float* Kb = K + bh * N * mat;
+  auto roff = [&](int t) { return (int64_t)(r0 + rl) * D + 16 * t + 4 * G; };
+
+  f32x4 Sb[NT], Mb[NT], Vb[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) Sb[t] = Mb[t] = Vb[t] = zero4();
+
+  if (N > 0) lds_dma_matrix<D, A_THREADS>((smem + ((N - 1) & 1) * D * D), Kb + (int64_t)(N - 1) * mat);
+  wait_vmem();
+  __syncthreads();
+
+  for (int i = N - 1; i >= 0; --i) {
+    const float* kl = (smem + (i & 1) * D * D);
+    if (i > 0) lds_dma_matrix<D, A_THREADS>((smem + ((i - 1) & 1) * D * D), Kb + (int64_t)(i - 1) * mat);
+    const int64_t si = bh * N + i;
+    const float a = av[si];
+    f32x4 Gb[NT];
+    if constexpr (RULE == 0) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) Gb[t] = Sb[t];
+    } else {
+      // recompute G^T = U^T - K^T S_i^T from the saved pre-update state
+      const float b = bv[si], m = mv[si], n = nv[si];
+      f32x4 Si[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) Si[t] = *reinterpret_cast<const f32x4*>((S_all + si * mat + roff(t)));
+      typename P::Op Bop[NKB];
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) Bop[kb] = P::pack(-Si[2 * kb], -Si[2 * kb + 1]);
+      float pda = 0.f, pdb = 0.f, pdm = 0.f, pdn = 0.f;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        f32x4 g = *reinterpret_cast<const f32x4*>((U + si * mat + roff(t)));
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) g = P::mma(col_op<P, SwzMat<D>>(kl, 32 * kb, 16 * t), Bop[kb], g);
+        const f32x4 Mp = *reinterpret_cast<const f32x4*>((M_all + si * mat + roff(t)));
+        const f32x4 Vp = *reinterpret_cast<const f32x4*>((V_all + si * mat + roff(t)));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float gg = g[j];
+          const float Mi = m * Mp[j] + (1.f - m) * gg;
+          const float Vi = n * Vp[j] + (1.f - n) * gg * gg;
+          const float root = sqrtf(Vi);
+          const float den = root + 1e-6f;
+          const float sb = Sb[t][j];
+          pda += sb * Si[t][j];
+          pdb += sb * (Mi / den);
+          const float ub = b * sb;
+          const float Mtot = Mb[t][j] + ub / den;
+          const float Vtot = Vb[t][j] - ub * Mi / (den * den) / (2.f * fmaxf(root, 1e-12f));
+          pdm += Mtot * (Mp[j] - gg);
+          pdn += Vtot * (Vp[j] - gg * gg);
+          Mb[t][j] = m * Mtot;
+          Vb[t][j] = n * Vtot;
+          Gb[t][j] = (1.f - m) * Mtot + (1.f - n) * 2.f * gg * Vtot;
+        }
+      }
+      pda = wave_sum(pda);
+      pdb = wave_sum(pdb);
+      pdm = wave_sum(pdm);
+      pdn = wave_sum(pdn);
+      if (l == 0) {
+        float* pp = part + (si * NTILES + tile) * 4;
+        pp[0] = pda;
+        pp[1] = pdb;
+        pp[2] = pdm;
+        pp[3] = pdn;
+      }
+    }
+    // dU_i = Gb
+#pragma unroll
+    for (int t = 0; t < NT; ++t) *reinterpret_cast<f32x4*>((dU + si * mat + roff(t))) = Gb[t];
+    // Sb^T <- a Sb^T - K Gb^T + gS^T : output tile rows c' = 16t.., A = K rows, B = -Gb^T
+    typename P::Op Bop[NKB];
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) Bop[kb] = P::pack(-Gb[2 * kb], -Gb[2 * kb + 1]);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      f32x4 acc = a * Sb[t] + *reinterpret_cast<const f32x4*>((gS + si * mat + roff(t)));
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) acc = P::mma(row_op<P, SwzMat<D>>(kl, 16 * t, 32 * kb), Bop[kb], acc);
+      Sb[t] = acc;
+    }
+    wait_vmem();
+    __syncthreads();
+  }
+}
+
+// Chunk-parallel part of the backward: dK_i = -S_i^T Gb_i (contraction over
+// the rows of S) and the scalar gradients of chunk i.  One workgroup of
+// A_KWAVES waves per (bh, i); S_i and Gb_i are staged in swizzled LDS.
+constexpr int A_KWAVES = 4;
+constexpr int A_KTHREADS = A_KWAVES * 64;
+
+template <int D, int RULE, int PREC>
+__global__ void __launch_bounds__(A_KTHREADS)
+scan_bwd_dk(const float* __restrict__ S_all, const float* __restrict__ dU,
+            const float* __restrict__ part, float* __restrict__ dK,
+            float* __restrict__ da, float* __restrict__ db, float* __restrict__ dm,
+            float* __restrict__ dn, int64_t BH, int N) {
+  using P = typename PrecSel<PREC>::T;
+  constexpr int NT = D / 16;
+  constexpr int NKB = D / 32;
+  extern __shared__ __align__(16) float smem[];
+  float* Sl = smem;
+  float* Gl = smem + D * D;
+  __shared__ float red[A_KWAVES];
+  const int64_t si = blockIdx.x;  // = bh * N + i
+  const int64_t mat = (int64_t)D * D;
+  lds_dma_matrix<D, A_KTHREADS>(Sl, S_all + si * mat);
+  lds_dma_matrix<D, A_KTHREADS>(Gl, dU + si * mat);
+  wait_vmem();
+  __syncthreads();
+  const int w = wave_id(), l = lane_id();
+  // dK^T[c][c'] = -sum_r Gb[r][c] S[r][c'] ; tile (tc, tcp) with rows c.
+  // Stored as dK[c'][c]: lane (c', G) of the D-layout tile of dK^T^T...
+  // Output tile of dK (rows c' = 16 tr, cols c = 16 tc): A = S^T rows c'
+  // (k = r, column reads of S), B = Gb (k = r, column reads of Gb).
+  for (int tile = w; tile < NT * NT; tile += A_KWAVES) {
+    const int tr = tile / NT, tc = tile % NT;
+    f32x4 acc = zero4();
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+      acc = P::mma(col_op<P, SwzMat<D>>(Sl, 32 * kb, 16 * tr), col_op<P, SwzMat<D>>(Gl, 32 * kb, 16 * tc), acc);
+    // D-layout: lane (c = l%16, G) holds dK[16tr + 4G + j][16tc + c]
+    float* out = dK + si * mat + (int64_t)(16 * tr + 4 * (l >> 4)) * D + 16 * tc + (l & 15);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) out[(int64_t)j * D] = -acc[j];
+  }
+  if constexpr (RULE == 0) {
+    // da_i = <Sb_{i+1}, S_i> = <dU_i, S_i> for delta
+    float s = 0.f;
+    for (int e = threadIdx.x; e < D * D; e += A_KTHREADS) {
+      const int r = e / D, c = e % D;
+      s += Sl[SwzMat<D>::off(r, c)] * Gl[SwzMat<D>::off(r, c)];
+    }
+    s = wave_sum(s);
+    if (l == 0) red[w] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float t = 0.f;
+      for (int q = 0; q < A_KWAVES; ++q) t += red[q];
+      da[si] = t;
+      db[si] = 0.f;
+      dm[si] = 0.f;
+      dn[si] = 0.f;
+    }
+  } else if constexpr (RULE == 2) {
+    if (threadIdx.x < 4) {
+      float t = 0.f;
+      for (int q = 0; q < D / 16; ++q) t += part[(si * (D / 16) + q) * 4 + threadIdx.x];
+      float* dst = threadIdx.x == 0 ? da : threadIdx.x == 1 ? db : threadIdx.x == 2 ? dm : dn;
+      dst[si] = t;
+    }
+  }
+  // RULE == 1: the muon backward kernel writes the scalar gradients itself
+}
+
+// ---------------------------------------------------------------- launchers
+template <int D, int RULE, int PREC>
+static hipError_t launch_fwd_rows(const ScanArgs& s) {
+  const int nblk = D / (16 * A_WAVES);
+  const size_t lds = 2 * (size_t)D * D * sizeof(float);
+  auto kern = scan_fwd_rows<D, RULE, PREC>;
+  hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, dim3((unsigned)(s.BH * nblk)), dim3(A_THREADS), lds, s.stream, s.U, s.K, s.a,
+                     s.b, s.m, s.n, s.S_all, s.M_all, s.V_all, s.BH, (int)s.N);
+  return hipGetLastError();
+}
+
+template <int D, int RULE, int PREC>
+static hipError_t launch_bwd_rows(const ScanArgs& s, float* part) {
+  const int nblk = D / (16 * A_WAVES);
+  const size_t lds = 2 * (size_t)D * D * sizeof(float);
+  auto kern = scan_bwd_rows<D, RULE, PREC>;
+  hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, dim3((unsigned)(s.BH * nblk)), dim3(A_THREADS), lds, s.stream, s.U, s.K, s.a,
+                     s.b, s.m, s.n, s.S_all, s.M_all, s.V_all, s.gS, s.dU, part, s.BH, (int)s.N);
+  return hipGetLastError();
+}
+
+template <int D, int RULE, int PREC>
+static hipError_t launch_bwd_dk(const ScanArgs& s, const float* part) {
+  const size_t lds = 2 * (size_t)D * D * sizeof(float);
+  auto k2 = scan_bwd_dk<D, RULE, PREC>;
+  hipError_t e = hipFuncSetAttribute((const void*)k2, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k2, dim3((unsigned)(s.BH * s.N)), dim3(A_KTHREADS), lds, s.stream, s.S_all, s.dU, part,
+                     s.dK, s.da, s.db, s.dm, s.dn, s.BH, (int)s.N);
+  return hipGetLastError();
+}
+
+template <int D, int PREC>
+static hipError_t dk_rule(const ScanArgs& s, const float* part) {
+  switch (s.rule) {
+    case 0: return launch_bwd_dk<D, 0, PREC>(s, part);
+    case 1: return launch_bwd_dk<D, 1, PREC>(s, part);
+    default: return launch_bwd_dk<D, 2, PREC>(s, part);
+  }
+}
+
+template <int D>
+static hipError_t dk_prec(const ScanArgs& s, const float* part) {
+  return s.precision == 0 ? dk_rule<D, 0>(s, part) : dk_rule<D, 1>(s, part);
+}
+
+hipError_t scan_bwd_dk_launch(const ScanArgs& s, const float* part) {
+  switch (s.dh) {
+    case 32: return dk_prec<32>(s, part);
+    case 64: return dk_prec<64>(s, part);
+    case 128: return dk_prec<128>(s, part);
+  }
+  return hipErrorInvalidValue;
+}
+
+template <int D, int PREC>
+static hipError_t fwd_rows_rule(const ScanArgs& s) {
+  return s.rule == 0 ? launch_fwd_rows<D, 0, PREC>(s) : launch_fwd_rows<D, 2, PREC>(s);
+}
+template <int D, int PREC>
+static hipError_t bwd_rows_rule(const ScanArgs& s, float* part) {
+  return s.rule == 0 ? launch_bwd_rows<D, 0, PREC>(s, part) : launch_bwd_rows<D, 2, PREC>(s, part);
+}
+
+template <int D>
+static hipError_t fwd_rows_prec(const ScanArgs& s) {
+  return s.precision == 0 ? fwd_rows_rule<D, 0>(s) : fwd_rows_rule<D, 1>(s);
+}
+template <int D>
+static hipError_t bwd_rows_prec(const ScanArgs& s, float* part) {
+  return s.precision == 0 ? bwd_rows_rule<D, 0>(s, part) : bwd_rows_rule<D, 1>(s, part);
+}
+
+hipError_t scan_fwd_rows_launch(const ScanArgs& s) {
+  switch (s.dh) {
+    case 32: return fwd_rows_prec<32>(s);
+    case 64: return fwd_rows_prec<64>(s);
+    case 128: return fwd_rows_prec<128>(s);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t scan_bwd_rows_launch(const ScanArgs& s, float* part) {
+  switch (s.dh) {
+    case 32: return bwd_rows_prec<32>(s, part);
+    case 64: return bwd_rows_prec<64>(s, part);
+    case 128: return bwd_rows_prec<128>(s, part);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace gmdn

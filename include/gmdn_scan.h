@@ -1,0 +1,153 @@
+/*
+ * gmdn_scan.h -- C ABI of the MI355X (gfx950) fast-weight state scan.
+ *
+ * Plain C: no HIP or torch types.  `stream` is a hipStream_t passed as
+ * void* (NULL = the default stream).  All pointers are device pointers to
+ * caller-owned memory; the library never allocates and never synchronises
+ * the host.  Every entry point returns GMDN_OK (0) or one of the error codes
+ * below; gmdn_error_string() describes a code.  Calls are stateless and
+ * reentrant; calls on different streams may run concurrently.
+ *
+ * Layout conventions
+ *   Level A (the drop-in fast_state_scan): U, K, S_all, M_all, V_all, gS,
+ *     dU, dK are contiguous (BH, N, dh, dh) float32; scalar streams a, b, m,
+ *     n and their gradients are contiguous (BH, N) float32.  S is stored
+ *     with rows = d_v, columns = d_k, as the reference's S_all.
+ *   Level B (fused mixer core): q, k, v, o, dO, dq, dk, dv are (B, H, T, d)
+ *     with element strides given per tensor for the B, H and T dimensions
+ *     (d must be the unit-stride dimension); gate streams beta, g, gmu, gnu
+ *     and their gradients are contiguous (B, H, T) float32.
+ */
+#ifndef GMDN_SCAN_H
+#define GMDN_SCAN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* return codes */
+#define GMDN_OK 0
+#define GMDN_ERR_ARG 1         /* null pointer, bad size, bad rule/ns */
+#define GMDN_ERR_UNSUPPORTED 2 /* head dim / chunk / dtype combination not built */
+#define GMDN_ERR_WORKSPACE 3   /* workspace missing or too small */
+#define GMDN_ERR_LAUNCH 4      /* hipGetLastError() reported a launch failure */
+
+/* inner rules (reference train_ablation.py:179) */
+#define GMDN_RULE_DELTA 0
+#define GMDN_RULE_MUON 1
+#define GMDN_RULE_ADAM 2
+
+/* product precision of the state GEMMs (reference fast_scan.py:44, :196-199).
+ * gfx950 has no TF32 MFMA: 'tf32' maps to bf16x3 split products
+ * (hi*hi + hi*lo + lo*hi, fp32 accumulate, about 2^-16 relative error per
+ * product), 'ieee' to fp32 MFMA (v_mfma_f32_16x16x4_f32). */
+#define GMDN_PREC_TF32 0
+#define GMDN_PREC_IEEE 1
+
+/* element type of the Level-B token streams */
+#define GMDN_DTYPE_BF16 0
+#define GMDN_DTYPE_F32 1
+
+const char* gmdn_error_string(int code);
+
+/* Supported head dims of the Level-A kernels (the reference dispatches its
+ * kernels for power-of-two dh >= 16, fast_scan.py:406-408; this build has
+ * 32, 64 and 128).  Returns 1 if dh is supported, else 0. */
+int gmdn_scan_supported(int32_t dh);
+
+/* ------------------------------------------------------------------ Level A */
+
+/* Forward of the chunk state scan; replaces _TritonScan.forward and
+ * _scan_fwd_kernel (reference fast_scan.py:359-377, :206-248).
+ *
+ *   S_all[bh, i] = pre-update S_i, with S_0 = 0 and
+ *   G_i = U_i - S_i K_i;  delta: S_{i+1} = a_i S_i + G_i
+ *   muon: M_{i+1} = m_i M_i + G_i;  S_{i+1} = a_i S_i + b_i msign_ns(M_{i+1})
+ *   adam: M_{i+1} = m_i M_i + (1-m_i) G_i;  V_{i+1} = n_i V_i + (1-n_i) G_i^2;
+ *         S_{i+1} = a_i S_i + b_i M_{i+1} / (sqrt(V_{i+1}) + 1e-6)
+ *
+ * M_all (rules 1, 2) and V_all (rule 2) receive the pre-update moments that
+ * gmdn_scan_bwd needs; either may be NULL when no backward will follow.
+ * ns: Newton-Schulz steps for rule 1 (0..8).  b, m, n may be NULL for rule 0;
+ * n may be NULL for rule 1. */
+int gmdn_scan_fwd(const float* U, const float* K, const float* a, const float* b,
+                  const float* m, const float* n, float* S_all, float* M_all,
+                  float* V_all, int64_t BH, int64_t N, int32_t dh, int32_t rule,
+                  int32_t ns, int32_t precision, void* stream);
+
+/* Workspace bytes gmdn_scan_bwd needs for these sizes (0 if none): adam
+ * keeps per-row-tile partial sums of its scalar gradients, muon keeps the
+ * shared Newton-Schulz matrices and the ns stored iterates per (b, h). */
+size_t gmdn_scan_bwd_workspace_bytes(int64_t BH, int64_t N, int32_t dh, int32_t rule,
+                                     int32_t ns);
+
+/* Backward of the chunk state scan; replaces _TritonScan.backward and
+ * _scan_bwd_kernel (reference fast_scan.py:379-396, :269-331, derivation
+ * :134-186).  Inputs are the forward's inputs and saved S_all / M_all /
+ * V_all plus the cotangent gS of S_all.  Writes dU, dK (BH, N, dh, dh) and
+ * da, db, dm, dn (BH, N).  Gradients of scalars the rule does not use are
+ * written as zeros (the reference's Triton backward leaves them
+ * uninitialised, fast_scan.py:387-389). */
+int gmdn_scan_bwd(const float* U, const float* K, const float* a, const float* b,
+                  const float* m, const float* n, const float* S_all,
+                  const float* M_all, const float* V_all, const float* gS, float* dU,
+                  float* dK, float* da, float* db, float* dm, float* dn,
+                  void* workspace, size_t workspace_bytes, int64_t BH, int64_t N,
+                  int32_t dh, int32_t rule, int32_t ns, int32_t precision,
+                  void* stream);
+
+/* ------------------------------------------------------------------ Level B */
+
+/* Problem description of the fused chunk op (phases 1-3 of the reference
+ * mixer, train_ablation.py:142-187, in the E-form: per chunk
+ * E = V - K S^T, o = Q S^T + A E with A = tril(Q K^T) diag(beta),
+ * G = E^T diag(w) K, then the rule's state update). */
+typedef struct gmdn_chunk_desc {
+  int64_t B, H, T;      /* batch, heads, tokens (T % C == 0) */
+  int32_t d;            /* head dim (d_k = d_v) */
+  int32_t C;            /* chunk length (64) */
+  int32_t rule;         /* GMDN_RULE_* */
+  int32_t ns;           /* Newton-Schulz steps (rule 1) */
+  int32_t dtype;        /* GMDN_DTYPE_* of q, k, v, o, dO, dq, dk, dv */
+  int32_t reserved;
+  float eps;            /* adam denominator epsilon (reference: 1e-6) */
+  /* element strides (B, H, T) of each token stream; d is unit-stride */
+  int64_t sq[3], sk[3], sv[3], so[3];
+} gmdn_chunk_desc;
+
+/* Bytes of the per-chunk state checkpoint gmdn_chunk_fwd writes when
+ * `states` is non-NULL (what gmdn_chunk_bwd consumes). */
+size_t gmdn_chunk_states_bytes(const gmdn_chunk_desc* desc);
+
+/* Forward: o = mixer core(q, k, v, beta, g[, gmu][, gnu]).  g, gmu, gnu are
+ * log-gates; each is clamped at log(1e-6) as the reference clamps the gate
+ * at 1e-6 before its log (train_ablation.py:155, :170-175).  gmu is needed
+ * for rules 1 and 2, gnu for rule 2.  `states` (may be NULL) receives the
+ * pre-update state of every chunk for the backward. */
+int gmdn_chunk_fwd(const gmdn_chunk_desc* desc, const void* q, const void* k,
+                   const void* v, const float* beta, const float* g,
+                   const float* gmu, const float* gnu, void* o, void* states,
+                   void* stream);
+
+/* Workspace bytes gmdn_chunk_bwd needs. */
+size_t gmdn_chunk_bwd_workspace_bytes(const gmdn_chunk_desc* desc);
+
+/* Backward given dO (strides desc->so) and the forward's `states`.  Writes
+ * dq, dk, dv (strides desc->sq, sk, sv) and dbeta, dg[, dgmu][, dgnu]
+ * (contiguous (B, H, T) float32).  Matches torch autograd through the
+ * reference's phases 1-3 and scan_eager. */
+int gmdn_chunk_bwd(const gmdn_chunk_desc* desc, const void* q, const void* k,
+                   const void* v, const float* beta, const float* g,
+                   const float* gmu, const float* gnu, const void* states,
+                   const void* dO, void* dq, void* dk, void* dv, float* dbeta,
+                   float* dg, float* dgmu, float* dgnu, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GMDN_SCAN_H */

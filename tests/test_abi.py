@@ -1,0 +1,80 @@
+"""The C-ABI library loads, exports every declared symbol, and rejects bad
+arguments with the documented codes before launching anything (no GPU
+needed: validation runs on the host)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from gmdn_amd import _native
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "gmdn_scan.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(gmdn_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_expected_entry_points():
+    names = declared_functions()
+    for n in ("gmdn_scan_fwd", "gmdn_scan_bwd", "gmdn_chunk_fwd", "gmdn_chunk_bwd", "gmdn_error_string"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), f"{name} missing from libgmdn_scan.so"
+        assert name in _native.SIGNATURES, f"{name} has no ctypes signature"
+
+
+def test_error_strings():
+    lib = _native.load()
+    for code in range(5):
+        assert lib.gmdn_error_string(code)
+    assert b"unknown" in lib.gmdn_error_string(99)
+
+
+def test_supported_head_dims():
+    lib = _native.load()
+    assert [d for d in (16, 32, 48, 64, 128, 256) if lib.gmdn_scan_supported(d)] == [32, 64, 128]
+
+
+def _fwd(lib, rule=0, dh=64, ns=3, prec=0, BH=2, N=3, null=()):
+    p = [None if i in null else 0x1000 for i in range(9)]
+    return lib.gmdn_scan_fwd(*p, BH, N, dh, rule, ns, prec, None)
+
+
+def test_scan_fwd_argument_validation():
+    lib = _native.load()
+    assert _fwd(lib, rule=3) == 1
+    assert _fwd(lib, ns=-1) == 1
+    assert _fwd(lib, ns=9) == 1
+    assert _fwd(lib, prec=2) == 1
+    assert _fwd(lib, dh=48) == 2
+    assert _fwd(lib, null=(0,)) == 1            # U
+    assert _fwd(lib, null=(6,)) == 1            # S_all
+    assert _fwd(lib, rule=1, null=(3,)) == 1    # muon needs b
+    assert _fwd(lib, rule=2, null=(5,)) == 1    # adam needs n
+    assert _fwd(lib, BH=0) == 0                 # empty problem: nothing to launch
+    assert _fwd(lib, N=0) == 0
+
+
+def test_scan_bwd_workspace_contract():
+    lib = _native.load()
+    assert lib.gmdn_scan_bwd_workspace_bytes(4, 16, 64, 0, 3) == 0
+    assert lib.gmdn_scan_bwd_workspace_bytes(4, 16, 64, 2, 3) == 4 * 16 * 4 * 4 * 4
+    assert lib.gmdn_scan_bwd_workspace_bytes(4, 16, 64, 1, 3) == 4 * (4 + 3) * 64 * 64 * 4
+    p = [0x1000] * 16
+    # adam / muon without workspace -> GMDN_ERR_WORKSPACE
+    assert lib.gmdn_scan_bwd(*p, None, 0, 4, 16, 64, 2, 3, 0, None) == 3
+    assert lib.gmdn_scan_bwd(*p, None, 0, 4, 16, 64, 1, 3, 0, None) == 3
+
+
+def test_chunk_desc_layout_matches_header():
+    # 3 int64 + 6 int32 + float + pad + 12 int64
+    assert ctypes.sizeof(_native.ChunkDesc) == 3 * 8 + 6 * 4 + 4 + 4 + 12 * 8
