@@ -150,10 +150,10 @@ GMDN_DEV typename P::Op row_op(const float* X, int r0, int k0) {
 }
 
 // Asynchronous copy of a contiguous D x D fp32 matrix from global memory into
-// a swizzled LDS matrix with gfx950's global_load_lds_dwordx4: each wave
-// instruction writes 64 consecutive 16-byte LDS groups, and each lane fetches
-// the global group that belongs at its slot.  Caller waits (vmcnt) and
-// synchronises before reading.
+// a swizzled LDS matrix with gfx950's global_load_lds_dwordx4 (lds_dma16):
+// each wave instruction writes 64 consecutive 16-byte LDS groups, and each
+// lane fetches the global group that belongs at its slot.  Caller waits
+// (wait_vmem) and synchronises before reading.
 template <int D, int NTHREADS>
 GMDN_DEV void lds_dma_matrix(float* lds, const float* g) {
   constexpr int GROUPS = D * D / 4;        // 16-byte groups in the matrix
@@ -165,11 +165,8 @@ GMDN_DEV void lds_dma_matrix(float* lds, const float* g) {
     const int p = base + w * 64 + l;       // physical group this lane fills
     const int r = p / PER_ROW;
     const int q = SwzMat<D>::logical_group(r, p % PER_ROW);
-    typedef __attribute__((address_space(3))) void lds_void;
-    __builtin_amdgcn_global_load_lds(g + r * D + q * 4, (lds_void*)(lds + (base + w * 64) * 4), 16, 0, 0);
+    lds_dma16(g + r * D + q * 4, lds + (base + w * 64) * 4);
   }
 }
-
-GMDN_DEV void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 }  // namespace gmdn

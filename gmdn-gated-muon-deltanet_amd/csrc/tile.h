@@ -78,8 +78,8 @@ GMDN_DEV void split2(float x, bf16& hi, bf16& lo) {
   lo = (bf16)(x - (float)hi);
 }
 
-// Two D-layout tiles stacked along k (t0: k rows 0..15, t1: rows 16..31),
-// scaled per k-row by s0/s1 (lane's four rows each) -> pair-order operand.
+// Two D-layout tiles stacked along k (t0: k rows 0..15, t1: rows 16..31)
+// -> pair-order operand.
 template <int P>
 GMDN_DEV Op<P> pack_tiles(const f32x4& t0, const f32x4& t1) {
   Op<P> r;
@@ -101,64 +101,143 @@ GMDN_DEV Op<P> pack_tiles(const f32x4& t0, const f32x4& t1) {
   return r;
 }
 
-template <int P>
-GMDN_DEV Op<P> pack_tiles_scaled(const f32x4& t0, const f32x4& t1, const f32x4& s0, const f32x4& s1) {
-  return pack_tiles<P>(t0 * s0, t1 * s1);
-}
+// ------------------------------------------------- swizzled bf16 LDS tiles
+// Row-major bf16 tile with COLS elements per row, stored without padding; the
+// 16-byte group q of row r sits at group q ^ (r & MASK).  Row reads (16
+// rows, one 8-byte piece each) and transposing column reads (4 rows x 32
+// bytes per lane group) then spread over the LDS banks.
+template <int COLS>
+struct BSwz {
+  static constexpr int GPR = COLS / 8;  // 16-byte groups per row
+  static constexpr int MASK = (GPR < 16 ? GPR : 16) - 1;
+  static GMDN_DEV int off(int r, int c) { return r * COLS + ((((c >> 3) ^ (r & MASK)) << 3) | (c & 7)); }
+};
 
-// ------------------------------------------------------------ LDS readers
-// Row read: lane (r = l%16, G) takes X[r][k] for k in pair order of the
-// 32-wide block starting at column k0.  X is row-major bf16 with leading
-// dimension ld (elements).  Two 8-byte reads.
-GMDN_DEV bf16x8 lds_row(const bf16* X, int ld, int r0, int k0) {
-  const int l = lane_id();
-  const bf16* p = X + (r0 + (l & 15)) * ld + k0 + 4 * (l >> 4);
-  bf16x4 a = *reinterpret_cast<const bf16x4*>(p);
-  bf16x4 b = *reinterpret_cast<const bf16x4*>(p + 16);
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// lane (r, G) takes X[r0 + r][k0 + pair(G, s)], s = 0..7
+template <class L>
+GMDN_DEV bf16x8 b_row(const bf16* X, int r0, int k0) {
+  const int l = lane_id(), r = r0 + (l & 15), G = l >> 4;
+  const bf16x4 a = *reinterpret_cast<const bf16x4*>(X + L::off(r, k0 + 4 * G));
+  const bf16x4 b = *reinterpret_cast<const bf16x4*>(X + L::off(r, k0 + 16 + 4 * G));
   return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
-// Column read: lane (c = l%16, G) takes X[k][c0 + c] for k in pair order of
-// the 32-row block starting at row k0 (X row-major, leading dim ld).  Two
-// ds_read_b64_tr_b16.
-GMDN_DEV bf16x8 lds_col(const bf16* X, int ld, int k0, int c0) {
-  const int l = lane_id();
-  const int i = l & 15, G = l >> 4;
-  const bf16* p0 = X + (k0 + 4 * G + (i >> 2)) * ld + c0 + 4 * (i & 3);
-  const bf16* p1 = p0 + 16 * ld;
-  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-  s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p0));
-  s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p1));
-  bf16x4 ab = __builtin_bit_cast(bf16x4, a);
-  bf16x4 bb = __builtin_bit_cast(bf16x4, b);
+// lane (c, G) takes X[k0 + pair(G, s)][c0 + c] (two transposing reads)
+template <class L>
+GMDN_DEV bf16x8 b_col(const bf16* X, int k0, int c0) {
+  const int l = lane_id(), i = l & 15, G = l >> 4;
+  const int rr = k0 + 4 * G + (i >> 2), cc = c0 + 4 * (i & 3);
+  s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(X + L::off(rr, cc)));
+  s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(X + L::off(rr + 16, cc)));
+  const bf16x4 ab = __builtin_bit_cast(bf16x4, a), bb = __builtin_bit_cast(bf16x4, b);
   return bf16x8{ab[0], ab[1], ab[2], ab[3], bb[0], bb[1], bb[2], bb[3]};
 }
 
-// D-layout tile from a row-major bf16 LDS tile X[row][col]: lane (c, G)
-// gets X[r0 + 4G + j][c0 + c] (one transposing read).
-GMDN_DEV f32x4 lds_dtile(const bf16* X, int ld, int r0, int c0) {
-  const int l = lane_id();
-  const int i = l & 15, G = l >> 4;
-  const bf16* p = X + (r0 + 4 * G + (i >> 2)) * ld + c0 + 4 * (i & 3);
-  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-  s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
-  bf16x4 ab = __builtin_bit_cast(bf16x4, a);
+// D-layout tile of X: lane (c, G) gets X[r0 + 4G + j][c0 + c], j = 0..3
+template <class L>
+GMDN_DEV f32x4 b_dtile(const bf16* X, int r0, int c0) {
+  const int l = lane_id(), i = l & 15, G = l >> 4;
+  s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(X + L::off(r0 + 4 * G + (i >> 2), c0 + 4 * (i & 3))));
+  const bf16x4 ab = __builtin_bit_cast(bf16x4, a);
   return f32x4{(float)ab[0], (float)ab[1], (float)ab[2], (float)ab[3]};
 }
 
-template <int P>
-GMDN_DEV Op<P> lds_row_op(const bf16* const* planes, int ld, int r0, int k0) {
-  Op<P> r;
-#pragma unroll
-  for (int p = 0; p < P; ++p) r.v[p] = lds_row(planes[p], ld, r0, k0);
-  return r;
+// One 16-byte-per-lane LDS-DMA load (global_load_lds_dwordx4): lane l's 16
+// bytes at gptr land at lds + 16 l.  `lds` must be the same for the whole
+// wave.  Issued through inline asm on purpose: the compiler cannot tell the
+// ring-buffer stage being filled from the stage being read and would
+// otherwise wait for every in-flight copy before each LDS read; completion is
+// tracked explicitly by the callers (wait_vmem / wait_vmem_le + barrier).
+GMDN_DEV void lds_dma16(const void* gptr, void* lds) {
+  const uint32_t m0v = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)((__attribute__((address_space(3))) char*)lds));
+  asm volatile(
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, off"
+      :
+      : "v"(gptr), "{m0}"(m0v)
+      : "memory");
 }
-template <int P>
-GMDN_DEV Op<P> lds_col_op(const bf16* const* planes, int ld, int k0, int c0) {
-  Op<P> r;
+
+// Same copy with a wave-uniform 64-bit base (SGPRs) and a per-lane 32-bit
+// byte offset: the form the chunk loops use, with lane offsets computed once.
+GMDN_DEV void lds_dma16_s(const void* sbase, uint32_t voff, uint32_t m0v) {
+  asm volatile(
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, %1"
+      :
+      : "v"(voff), "s"(sbase), "{m0}"(m0v)
+      : "memory");
+}
+
+// LDS byte pointers.  Precomputed per-lane bases are kept as LDS pointers so
+// that base + compile-time offset is an in-bounds address computation, which
+// the compiler folds into the ds_read / ds_write immediate offset.
+typedef __attribute__((address_space(3))) char* lds_ptr;
+typedef const __attribute__((address_space(3))) char* lds_cptr;
+
+template <class T>
+GMDN_DEV T lds_ld(lds_cptr p) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) T*>(p);
+}
+template <class T>
+GMDN_DEV void lds_st(lds_ptr p, const T& v) {
+  *reinterpret_cast<__attribute__((address_space(3))) T*>(p) = v;
+}
+GMDN_DEV bf16x4 lds_tr16(lds_cptr p) {
+  const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+  return __builtin_bit_cast(bf16x4, x);
+}
+GMDN_DEV bf16x8 cat8(const bf16x4& a, const bf16x4& b) {
+  return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// LDS byte address of a pointer into LDS (wave-uniform when `p` is).
+GMDN_DEV uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)((const __attribute__((address_space(3))) char*)p);
+}
+GMDN_DEV lds_ptr lds_base(void* p) { return (lds_ptr)p; }
+
+// Plan of an asynchronous copy of a ROWS x COLS bf16 tile (global rows
+// `gstride` elements apart, 16-byte aligned) into a swizzled LDS tile:
+// NOPS = ROWS * COLS / 8 / NTHREADS LDS-DMA instructions per wave; lane l of
+// instruction k fills physical 16-byte group k NTHREADS + 64 w + l and
+// fetches the logical group stored there.  off[k] is that lane's byte offset
+// from the tile's first global row.
+template <class L, int ROWS, int NTHREADS>
+struct DmaPlan {
+  static constexpr int GROUPS = ROWS * L::GPR;
+  static_assert(GROUPS % NTHREADS == 0, "tile must split evenly over the block");
+  static constexpr int NOPS = GROUPS / NTHREADS;
+  uint32_t off[NOPS];
+  GMDN_DEV void init(int w, int64_t gstride) {
+    const int l = lane_id();
 #pragma unroll
-  for (int p = 0; p < P; ++p) r.v[p] = lds_col(planes[p], ld, k0, c0);
-  return r;
+    for (int k = 0; k < NOPS; ++k) {
+      const int p = k * NTHREADS + w * 64 + l;
+      const int r = p / L::GPR;
+      const int q = (p % L::GPR) ^ (r & L::MASK);
+      off[k] = (uint32_t)((r * gstride + q * 8) * 2);
+    }
+  }
+  // issue the copy of the tile whose first global row starts at `g`
+  GMDN_DEV void issue(const bf16* g, uint32_t lds_tile, int w) const {
+#pragma unroll
+    for (int k = 0; k < NOPS; ++k) lds_dma16_s(g, off[k], lds_tile + (k * NTHREADS + w * 64) * 16);
+  }
+};
+
+// Wait for this wave's outstanding vector-memory operations, including the
+// LDS-DMA loads above (the caller then synchronises the block).
+GMDN_DEV void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Wait until at most N vector-memory operations of this wave are in flight.
+template <int N>
+GMDN_DEV void wait_vmem_le() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
 // ------------------------------------------------------------ reductions

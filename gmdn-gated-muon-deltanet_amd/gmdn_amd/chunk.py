@@ -1,0 +1,137 @@
+"""Fused mixer-core op (Level B): phases 1-3 of the reference mixer in one
+HIP kernel per direction.
+
+``chunk_scan(q, k, v, beta, g, gmu=None, gnu=None, rule='delta', ns=3)``
+computes what ``FastWeightMixer.forward`` computes between its front-end and
+its per-head RMSNorm (reference train_ablation.py:142-187): the chunk
+transform A, Kw, Uv, Qt, Ov, the state scan, and ``o = Qt S^T + Ov``.
+
+* ``q, k, v``: (B, H, T, d) bfloat16, d contiguous (any strides over B, H, T
+  that are multiples of 8 elements), q and k L2-normalised per head.
+* ``beta``: (B, H, T) beta gate (sigmoid output).
+* ``g, gmu, gnu``: (B, H, T) log alpha, log mu, log nu gates.  The reference
+  clamps each gate at 1e-6 before its log (train_ablation.py:155, :170-175);
+  the kernel clamps the log at log(1e-6), which is the same function.
+  ``gmu`` is needed by the muon and adam rules, ``gnu`` by adam.
+* returns ``o`` (B, H, T, d) in q's dtype.
+
+Chunk length is 64 (the reference default and every configuration's).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _native as nat
+
+RULES = {"delta": 0, "muon": 1, "adam": 2}
+CHUNK = 64
+SUPPORTED_D = (64, 128)
+
+
+def _rule_id(rule) -> int:
+    if isinstance(rule, str):
+        if rule not in RULES:
+            raise ValueError(f"rule must be one of {tuple(RULES)}, got {rule!r}")
+        return RULES[rule]
+    if rule not in (0, 1, 2):
+        raise ValueError(f"rule must be 0, 1 or 2, got {rule}")
+    return int(rule)
+
+
+def _desc(q, k, v, o, rule, ns, eps):
+    B, H, T, d = q.shape
+    desc = nat.ChunkDesc()
+    desc.B, desc.H, desc.T, desc.d, desc.C = B, H, T, d, CHUNK
+    desc.rule, desc.ns, desc.dtype, desc.eps = rule, ns, nat.DTYPE_BF16, eps
+    for name, t in (("sq", q), ("sk", k), ("sv", v), ("so", o)):
+        arr = getattr(desc, name)
+        for i in range(3):
+            arr[i] = t.stride(i)
+    return desc
+
+
+def _check(q, k, v, beta, g, gmu, gnu, rule):
+    if not q.is_cuda:
+        raise RuntimeError("chunk_scan needs GPU tensors")
+    if q.dim() != 4 or k.shape != q.shape or v.shape != q.shape:
+        raise RuntimeError(f"q, k, v must be (B, H, T, d) of equal shape, got {tuple(q.shape)}, "
+                           f"{tuple(k.shape)}, {tuple(v.shape)}")
+    B, H, T, d = q.shape
+    if d not in SUPPORTED_D:
+        raise RuntimeError(f"chunk_scan supports head dims {SUPPORTED_D}, got {d}")
+    if T % CHUNK:
+        raise RuntimeError(f"T must be a multiple of the chunk length {CHUNK}, got {T}")
+    if any(t.dtype != torch.bfloat16 for t in (q, k, v)):
+        raise RuntimeError("chunk_scan takes bfloat16 q, k, v")
+    for name, t in (("beta", beta), ("g", g), ("gmu", gmu), ("gnu", gnu)):
+        if t is not None and tuple(t.shape) != (B, H, T):
+            raise RuntimeError(f"{name} must be (B, H, T) = {(B, H, T)}, got {tuple(t.shape)}")
+    if rule >= 1 and gmu is None:
+        raise RuntimeError("muon and adam rules need gmu")
+    if rule == 2 and gnu is None:
+        raise RuntimeError("adam rule needs gnu")
+
+
+def _tok(t):
+    """bf16 token stream with a unit-stride last dim and 16-byte-aligned rows."""
+    if t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:3]) or t.data_ptr() % 16:
+        t = t.contiguous()
+    return t
+
+
+def _gate(t):
+    """float32 (B, H, T) gate stream, contiguous and 16-byte aligned."""
+    if t is None:
+        return None
+    t = t.detach().to(torch.float32).contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+class ChunkScan(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, beta, g, gmu, gnu, rule, ns, eps):
+        _check(q, k, v, beta, g, gmu, gnu, rule)
+        lib = nat.load()
+        qc, kc, vc = _tok(q.detach()), _tok(k.detach()), _tok(v.detach())
+        bc, gc, mc, nc = _gate(beta), _gate(g), _gate(gmu), _gate(gnu)
+        o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        desc = _desc(qc, kc, vc, o, rule, ns, eps)
+        need_grad = any(ctx.needs_input_grad[:7])
+        states = None
+        if need_grad:
+            nbytes = lib.gmdn_chunk_states_bytes(desc)
+            states = torch.empty(nbytes // 4, dtype=torch.float32, device=q.device)
+        with torch.cuda.device(q.device):
+            rc = lib.gmdn_chunk_fwd(desc, nat.ptr(qc), nat.ptr(kc), nat.ptr(vc), nat.ptr(bc), nat.ptr(gc),
+                                    nat.ptr(mc), nat.ptr(nc), nat.ptr(o), nat.ptr(states), nat.stream_of(q))
+        nat.check(rc, "gmdn_chunk_fwd")
+        if need_grad:
+            ctx.save_for_backward(qc, kc, vc, bc, gc, mc, nc, states)
+        ctx.rule, ctx.ns, ctx.eps = rule, ns, eps
+        return o
+
+    @staticmethod
+    def backward(ctx, dO):
+        qc, kc, vc, bc, gc, mc, nc, states = ctx.saved_tensors
+        lib = nat.load()
+        dOc = _tok(dO.to(torch.bfloat16))
+        dq, dk, dv = (torch.empty_like(t, memory_format=torch.contiguous_format) for t in (qc, kc, vc))
+        dbeta, dg = torch.empty_like(bc), torch.empty_like(gc)
+        dgmu = torch.empty_like(mc) if mc is not None else None
+        dgnu = torch.empty_like(nc) if nc is not None else None
+        desc = _desc(qc, kc, vc, dOc, ctx.rule, ctx.ns, ctx.eps)
+        ws_bytes = lib.gmdn_chunk_bwd_workspace_bytes(desc)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=qc.device) if ws_bytes else None
+        with torch.cuda.device(qc.device):
+            rc = lib.gmdn_chunk_bwd(desc, nat.ptr(qc), nat.ptr(kc), nat.ptr(vc), nat.ptr(bc), nat.ptr(gc),
+                                    nat.ptr(mc), nat.ptr(nc), nat.ptr(states), nat.ptr(dOc), nat.ptr(dq),
+                                    nat.ptr(dk), nat.ptr(dv), nat.ptr(dbeta), nat.ptr(dg), nat.ptr(dgmu),
+                                    nat.ptr(dgnu), nat.ptr(ws), ws_bytes, nat.stream_of(qc))
+        nat.check(rc, "gmdn_chunk_bwd")
+        return dq, dk, dv, dbeta, dg, dgmu, dgnu, None, None, None
+
+
+def chunk_scan(q, k, v, beta, g, gmu=None, gnu=None, *, rule="delta", ns: int = 3, eps: float = 1e-6):
+    """Fused mixer core; see the module docstring."""
+    r = _rule_id(rule)
+    return ChunkScan.apply(q, k, v, beta, g, gmu if r >= 1 else None, gnu if r == 2 else None, r, ns, eps)
