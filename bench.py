@@ -1,0 +1,225 @@
+#!/usr/bin/env python3
+"""Throughput of the fused chunkwise mixer core on one MI355X.
+
+One step is one pass of the hot path over one batch of synthetic input: the
+fused mixer core (reference train_ablation.py:142-187 with the state scan of
+fast_scan.py:72-95) over B=4, H=16, T=4096, d=128, chunk 64, gated delta rule,
+bf16 q/k/v/o with fp32 state, forward and (where built) backward.  Inputs are
+resident in HBM before the timed region starts.
+
+    python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu-baseline]
+
+prints one JSON line.  ``value`` is tokens/s (B*T per step) of the forward +
+backward step when the backward kernel of the rule is built, else of the
+forward.  ``roofline`` prices the forward kernel's average launch duration,
+measured with HIP events on its launch stream inside the timed region,
+against MI355X's HBM bandwidth (8 TB/s); ``traffic`` is read from the
+committed FETCH_SIZE/WRITE_SIZE summary of the same kernel and workload.
+``cpu_baseline`` times the CPU restatement of the reference matrix form
+(float32, torch on the host cores) on the same workload.
+
+``--copy-calibration BYTES`` only runs a device copy of BYTES bytes a few
+times (the calibration kernel for the HBM byte counters).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "gmdn-gated-muon-deltanet_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "scan tokens/s at H16 d128 T4096 bf16 (fwd, fwd+bwd); % of MFMA/HBM peak"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+DEFAULT_WORKLOAD = "gated_delta_b4_h16_t4096_d128"
+GATES = {"delta": 2, "muon": 3, "adam": 4}
+
+
+def parse_args(argv=None):
+    p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--workload", default=DEFAULT_WORKLOAD)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work (about)")
+    p.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES")
+    return p.parse_args(argv)
+
+
+def fwd_bytes_per_token_head(w) -> int:
+    """q, k, v read and o written in bf16, plus the fp32 gate streams."""
+    return 3 * 2 * w.d + 2 * w.d + 4 * GATES[w.rule]
+
+
+def fwd_flops_per_chunk_head(w) -> int:
+    """E-form: A = QK^T, E = V - K S^T, o = QS^T + AE, G = E^T diag(w) K."""
+    C, d = w.chunk, w.d
+    f = 4 * C * C * d + 6 * C * d * d
+    if w.rule == "muon":
+        f += 6 * w.ns * d ** 3
+    return f
+
+
+def copy_calibration(nbytes: int) -> None:
+    import torch
+    # an elementwise kernel (MulFunctor) that reads nbytes and writes nbytes
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": nbytes}))
+
+
+def cpu_baseline(w, budget_s: float, with_bwd: bool):
+    """The CPU restatement of the reference matrix form in float32 (reference
+    train_ablation.py:142-187 and fast_scan.py:72-95, autograd for backward),
+    timed on this host's cores over the whole workload."""
+    import torch
+    from oracle import chunk as oc
+    from gmdn_amd.workloads import make_inputs
+
+    threads = max(1, min(len(os.sched_getaffinity(0)), 16))
+    torch.set_num_threads(threads)
+    inp = make_inputs(w, seed=0, dtype=torch.float32, with_grad_out=True)
+    rule = {"delta": 0, "muon": 1, "adam": 2}[w.rule]
+    names = ("q", "k", "v", "beta", "g", "gmu", "gnu")
+
+    def step():
+        xs = [None if inp[n] is None else inp[n].clone().requires_grad_(with_bwd) for n in names]
+        o = oc.mixer_core(*xs, rule=rule, ns=w.ns, C=w.chunk)
+        if with_bwd:
+            torch.autograd.grad(o, [x for x in xs if x is not None], inp["dO"])
+
+    step()  # warm-up
+    times, t_all = [], time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - t_all < budget_s and len(times) < 500):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_all > 3 * budget_s:
+            break
+    t = statistics.median(times)
+    return {"value": w.tokens / t, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"whole workload {w.name} ({'fwd+bwd' if with_bwd else 'fwd'}), float32 matrix form, "
+                      f"median of {len(times)} runs of {t * 1e3:.0f} ms"}
+
+
+def main(argv=None):
+    args = parse_args(argv)
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus > 1 or world > 1:
+        print(f"bench.py measures one GPU only; --gpus {max(args.gpus, world)} is not supported. "
+              f"The scan shards over (batch, head) with no exchange between GPUs, so the job's "
+              f"throughput is the one-GPU figure times the GPU count.", file=sys.stderr)
+        return 2
+
+    import torch
+    from gmdn_amd import _native, chunk, profiling
+    from gmdn_amd.workloads import WORKLOADS, make_inputs
+
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs a GPU (no HIP device visible)")
+    _native.load()
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return 0
+
+    w = WORKLOADS[args.workload]
+    dev = torch.device("cuda:0")
+    inp = make_inputs(w, seed=0, device=dev, with_grad_out=True)
+    names = ("q", "k", "v", "beta", "g", "gmu", "gnu")
+    with_bwd = chunk.backward_supported(w.rule)
+    xs = [inp[n] if inp[n] is None else inp[n].detach().requires_grad_(with_bwd) for n in names]
+    grads_of = [x for x in xs if x is not None]
+    dO = inp["dO"]
+    stream = torch.cuda.current_stream(dev)
+
+    def fwd():
+        return chunk.chunk_scan(*xs, rule=w.rule, ns=w.ns)
+
+    def step(ev=None):
+        if ev is not None:
+            ev[0].record(stream)
+        o = fwd()
+        if ev is not None:
+            ev[1].record(stream)
+        if with_bwd:
+            torch.autograd.grad(o, grads_of, dO)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(evs[i])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_step = elapsed * 1e3 / args.steps
+    k_ms = statistics.mean(e0.elapsed_time(e1) for e0, e1 in evs)
+
+    # forward-only throughput alongside the full step
+    fwd_ms = None
+    if with_bwd:
+        with torch.no_grad():
+            for _ in range(args.warmup):
+                fwd()
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            for _ in range(args.steps):
+                fwd()
+            torch.cuda.synchronize()
+            fwd_ms = (time.perf_counter() - t1) * 1e3 / args.steps
+    else:
+        fwd_ms = ms_step
+
+    units = w.B * w.H * w.T
+    alg_bytes = fwd_bytes_per_token_head(w) * units
+    alg_flops = fwd_flops_per_chunk_head(w) * w.B * w.H * (w.T // w.chunk)
+    if w.rule == "muon":
+        bound, achieved, peak, unit = "mfma", alg_flops / (k_ms * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s"
+    else:
+        bound, achieved, peak, unit = "hbm", alg_bytes / (k_ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s"
+    traffic = profiling.read_traffic(os.path.join(ROOT, "profiles", f"chunk_fwd_{w.name}_traffic.md"))
+
+    line = {
+        "metric": METRIC,
+        "value": w.tokens / (ms_step * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": w.name, "rule": w.rule, "B": w.B, "H": w.H, "T": w.T, "d": w.d,
+                   "chunk": w.chunk, "pass": "fwd+bwd" if with_bwd else "fwd",
+                   "state": "fp32", "global_batch": w.B, "seq_len": w.T, "parallelism": "none"},
+        "fwd_tokens_per_s": w.tokens / (fwd_ms * 1e-3),
+        "fwd_bwd_tokens_per_s": w.tokens / (ms_step * 1e-3) if with_bwd else None,
+        "roofline": {"kernel": f"chunk_fwd<{w.d},{ {'delta': 0, 'muon': 1, 'adam': 2}[w.rule]}>",
+                     "bound": bound, "achieved": achieved, "peak": peak, "unit": unit,
+                     "frac": achieved / peak, "traffic": traffic,
+                     "avg_launch_us": k_ms * 1e3, "alg_bytes": alg_bytes, "alg_flops": alg_flops},
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(w, args.cpu_budget, with_bwd)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

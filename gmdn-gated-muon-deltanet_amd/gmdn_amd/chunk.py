@@ -28,6 +28,13 @@ CHUNK = 64
 SUPPORTED_D = (64, 128)
 
 
+BWD_RULES = ()  # rules whose fused backward kernel is built
+
+
+def backward_supported(rule) -> bool:
+    return _rule_id(rule) in BWD_RULES
+
+
 def _rule_id(rule) -> int:
     if isinstance(rule, str):
         if rule not in RULES:

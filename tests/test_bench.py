@@ -1,0 +1,50 @@
+"""CPU checks of the benchmark's accounting and its one-GPU contract."""
+import os
+import subprocess
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, ROOT)
+
+import bench  # noqa: E402
+from gmdn_amd import profiling  # noqa: E402
+from gmdn_amd.workloads import WORKLOADS  # noqa: E402
+
+
+def test_algorithmic_bytes_and_flops():
+    w = WORKLOADS["gated_delta_b4_h16_t4096_d128"]
+    # q, k, v, o bf16 + beta, g fp32 per token-head
+    assert bench.fwd_bytes_per_token_head(w) == 1032
+    assert bench.fwd_bytes_per_token_head(w) * w.B * w.H * w.T == 270532608
+    # 4 C^2 d + 6 C d^2 per chunk-head = 8.39 MFLOP at C=64, d=128
+    assert bench.fwd_flops_per_chunk_head(w) == 4 * 64 * 64 * 128 + 6 * 64 * 128 * 128
+    wa = WORKLOADS["adam_b2_h8_t4096_d64"]
+    assert bench.fwd_bytes_per_token_head(wa) == 8 * 64 + 16
+
+
+def test_multi_gpu_is_refused():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr
+
+
+def test_read_traffic(tmp_path):
+    f = tmp_path / "t.md"
+    f.write_text("# x\n\ntraffic_bytes_per_launch: 12345\nread_bytes_per_launch: 1\n")
+    assert profiling.read_traffic(str(f)) == 12345.0
+    assert profiling.read_traffic(str(tmp_path / "missing.md")) is None
+
+
+def test_pmc_csv_parsing(tmp_path):
+    hdr = ('"Correlation_Id","Dispatch_Id","Agent_Id","Queue_Id","Process_Id","Thread_Id","Grid_Size",'
+           '"Kernel_Id","Kernel_Name","Workgroup_Size","LDS_Block_Size","Scratch_Size","VGPR_Count",'
+           '"Accum_VGPR_Count","SGPR_Count","Counter_Name","Counter_Value","Start_Timestamp","End_Timestamp"\n')
+    rows = [f'{i},{i},"Agent 1",1,1,1,64,1,"void k<1>(A)",256,0,0,1,0,1,"FETCH_SIZE",{v},0,1\n'
+            for i, v in ((1, 100.0), (2, 102.0))]
+    (tmp_path / "x_counter_collection.csv").write_text(hdr + "".join(rows))
+    assert profiling.counter_per_dispatch(str(tmp_path), "FETCH_SIZE", "k<1>") == [100.0, 102.0]
+    with pytest.raises(ValueError):
+        profiling.counter_per_dispatch(str(tmp_path), "WRITE_SIZE", "k<1>")
