@@ -25,27 +25,10 @@
 // T=4096, d=128.
 #include "../../include/gmdn_scan.h"
 #include "chunk_b.h"
-#include "tile.h"
 
 #include <type_traits>
 
 namespace gmdn {
-
-constexpr int CB_C = 64;  // chunk length
-constexpr int CB_WAVES = 4;
-constexpr int CB_THREADS = CB_WAVES * 64;
-constexpr float LOG_FLOOR = -13.815510557964274f;  // log(1e-6)
-
-struct ChunkArgs {
-  const bf16 *q, *k, *v;
-  const float *beta, *g, *gmu, *gnu;
-  bf16* o;
-  float* states;
-  int64_t B, H, T;
-  int N;
-  float eps;
-  int64_t sq[3], sk[3], sv[3], so[3];
-};
 
 // LDS carve-up of the forward kernel (bytes)
 // Chunk tiles (Q, K, the workgroup's 32 columns of V, and the gate chunk)
@@ -53,7 +36,7 @@ struct ChunkArgs {
 // chunks ahead, so HBM latency is covered by that many chunks of work.  The
 // chunk loop is unrolled over the ring, so every LDS read address is a
 // per-lane base register (computed once) plus an immediate offset.
-constexpr int FWD_STAGES = 3;
+constexpr int FWD_STAGES = RING;
 
 template <int D>
 struct FwdLds {
@@ -74,30 +57,6 @@ struct FwdLds {
   // LDS-DMA instructions one wave issues per chunk (Q, K, V; wave 0 also the gates)
   static constexpr int DMA_OPS = 2 * (CB_C * D / 8) / CB_THREADS + (CB_C * 32 / 8) / CB_THREADS;
 };
-
-GMDN_DEV void map_block(int64_t BH, int nblk, int64_t& bh, int& blk) {
-  const int64_t x = blockIdx.x;
-  if (BH % 8 == 0) {  // all row blocks of one (b, h) on one XCD (shared q/k in its L2)
-    const int64_t xcd = x & 7, slot = x >> 3;
-    blk = (int)(slot % nblk);
-    bh = (slot / nblk) * 8 + xcd;
-  } else {
-    bh = x / nblk;
-    blk = (int)(x % nblk);
-  }
-}
-
-template <class T>
-GMDN_DEV T lds_at(const char* base, uint32_t off) {
-  return *reinterpret_cast<const T*>(base + off);
-}
-
-// Lane part of the byte offset of a swizzled bf16 tile element read as an
-// 8-byte piece: row `r`, first column `c` (c % 4 == 0).
-template <class L>
-GMDN_DEV uint32_t swz_off(int r, int c) {
-  return (uint32_t)(2 * L::off(r, c));
-}
 
 template <int D, int RULE>
 __global__ void __launch_bounds__(CB_THREADS) chunk_fwd(ChunkArgs p) {
@@ -462,6 +421,11 @@ static hipError_t launch_fwd(const ChunkArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
+hipError_t chunk_fwd_launch(const ChunkArgs& a, int d, int rule, hipStream_t s) {
+  if (d == 128) return rule == 0 ? launch_fwd<128, 0>(a, s) : launch_fwd<128, 2>(a, s);
+  return rule == 0 ? launch_fwd<64, 0>(a, s) : launch_fwd<64, 2>(a, s);
+}
+
 }  // namespace gmdn
 
 using namespace gmdn;
@@ -536,22 +500,44 @@ int gmdn_chunk_fwd(const gmdn_chunk_desc* desc, const void* q, const void* k, co
   if (desc->rule == 1) return GMDN_ERR_UNSUPPORTED;
   const ChunkArgs a = make_args(desc, q, k, v, beta, g, gmu, gnu, o, states);
   hipStream_t s = (hipStream_t)stream;
-  hipError_t e;
-  if (desc->d == 128)
-    e = desc->rule == 0 ? launch_fwd<128, 0>(a, s) : launch_fwd<128, 2>(a, s);
-  else
-    e = desc->rule == 0 ? launch_fwd<64, 0>(a, s) : launch_fwd<64, 2>(a, s);
-  return e == hipSuccess ? GMDN_OK : GMDN_ERR_LAUNCH;
+  return chunk_fwd_launch(a, desc->d, desc->rule, s) == hipSuccess ? GMDN_OK : GMDN_ERR_LAUNCH;
 }
 
-size_t gmdn_chunk_bwd_workspace_bytes(const gmdn_chunk_desc* desc) { return 0; }
+size_t gmdn_chunk_bwd_workspace_bytes(const gmdn_chunk_desc* desc) {
+  // Gb_i, the cotangent of every chunk's state update (fp32 d x d per chunk)
+  return gmdn_chunk_states_bytes(desc);
+}
 
 int gmdn_chunk_bwd(const gmdn_chunk_desc* desc, const void* q, const void* k, const void* v,
                    const float* beta, const float* g, const float* gmu, const float* gnu,
                    const void* states, const void* dO, void* dq, void* dk, void* dv, float* dbeta,
                    float* dg, float* dgmu, float* dgnu, void* workspace, size_t workspace_bytes,
                    void* stream) {
-  return GMDN_ERR_UNSUPPORTED;
+  int rc = check_desc(desc);
+  if (rc != GMDN_OK) return rc;
+  if (desc->B * desc->H * desc->T == 0) return GMDN_OK;
+  if (!q || !k || !v || !beta || !g || !states || !dO || !dq || !dk || !dv || !dbeta || !dg)
+    return GMDN_ERR_ARG;
+  if (desc->rule >= 1 && (!gmu || !dgmu)) return GMDN_ERR_ARG;
+  if (desc->rule == 2 && (!gnu || !dgnu)) return GMDN_ERR_ARG;
+  if (desc->rule != 0) return GMDN_ERR_UNSUPPORTED;
+  if (desc->B * desc->H * (desc->T / CB_C) >= ((int64_t)1 << 31)) return GMDN_ERR_ARG;  // one workgroup per chunk
+  if (!workspace || workspace_bytes < gmdn_chunk_bwd_workspace_bytes(desc)) return GMDN_ERR_WORKSPACE;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dO) || !aligned16(dv) ||
+      !aligned16(beta) || !aligned16(g) || !aligned16(states) || !aligned16(workspace))
+    return GMDN_ERR_UNSUPPORTED;
+  ChunkArgs a = make_args(desc, q, k, v, beta, g, gmu, gnu, const_cast<void*>(dO),
+                          const_cast<void*>(states));
+  a.gb = (float*)workspace;
+  a.dq = (bf16*)dq;
+  a.dk = (bf16*)dk;
+  a.dv = (bf16*)dv;
+  a.dbeta = dbeta;
+  a.dg = dg;
+  a.dgmu = dgmu;
+  a.dgnu = dgnu;
+  return chunk_bwd_launch(a, desc->d, desc->rule, (hipStream_t)stream) == hipSuccess ? GMDN_OK
+                                                                                     : GMDN_ERR_LAUNCH;
 }
 
 }  // extern "C"

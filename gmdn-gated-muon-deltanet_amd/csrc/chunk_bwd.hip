@@ -1,0 +1,615 @@
+// Level B backward: the fused mixer core's VJP (reference train_ablation.py:142-187
+// differentiated through fast_scan.py:72-95 and :134-186).
+//
+// Per (b, h) and chunk i, with the forward's E-form quantities
+//   A = tril(Q K^T) diag(beta),  E = V - K S_i^T,  o = Q S_i^T + A E,
+//   G = E^T diag(w) K,  delta: S_{i+1} = a_i S_i + G,
+// and Sb_{i+1} = dL/dS_{i+1} (Sb_N = 0), the delta rule's cotangents are
+//   Gb  = Sb_{i+1}
+//   dE  = A^T dO + diag(w) K Gb^T          (= dV)
+//   Sb_i = a_i Sb_{i+1} + dO^T Q - dE^T K
+//   dA  = tril(dO E^T)                      (before the beta scaling)
+//   dQ  = dO S_i + (dA diag(beta)) K
+//   dK  = (dA diag(beta))^T Q - dE S_i + diag(w) E Gb
+//   dbeta_s = sum_t dA[t,s] (q_t . k_s) + [delta] (E Gb)[s,:] . k_s
+//   dg_t = <Sb_{i+1}, S_i> a_i [g_t >= log 1e-6]
+//
+// Two kernels:
+//  * chunk_bwd_state: the reverse recurrence of Sb.  Row r of Sb_i needs only
+//    row r of Sb_{i+1} (dE[:, r] = A^T dO[:, r] + diag(w) K Sb[r, :]^T), so it
+//    keeps the forward's work split (4 waves own 32 rows; wave (rt, h) holds
+//    16 rows x column half h in registers, LDS-DMA ring of Q, K and the
+//    workgroup's dO columns) and writes Gb_i for every chunk.
+//  * chunk_bwd_tok: chunk-parallel, one workgroup per (b, h, chunk).  From S_i
+//    (saved by the forward) and Gb_i it recomputes E, A and dE and forms dQ,
+//    dK, dV and the gate gradients; every contraction over the state's rows is
+//    local to the workgroup.
+#include "../../include/gmdn_scan.h"
+#include "chunk_b.h"
+
+#include <type_traits>
+
+namespace gmdn {
+
+// ------------------------------------------------------------------ helpers
+// lane (m, G) takes X[r][k0 + 8G .. k0 + 8G + 7] (natural k order, 16 bytes)
+template <class L>
+GMDN_DEV bf16x8 row8(const bf16* X, int r, int k0) {
+  return *reinterpret_cast<const bf16x8*>(X + L::off(r, k0 + 8 * (lane_id() >> 4)));
+}
+
+// lane (i, G) takes X[k0 + 8G + j][c0 + i], j = 0..7 (two transposing reads)
+template <class L>
+GMDN_DEV bf16x8 col8(const bf16* X, int k0, int c0) {
+  const int l = lane_id(), i = l & 15, G = l >> 4;
+  const int rr = k0 + 8 * G + (i >> 2), cc = c0 + 4 * (i & 3);
+  const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(X + L::off(rr, cc)));
+  const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(X + L::off(rr + 4, cc)));
+  return cat8(__builtin_bit_cast(bf16x4, a), __builtin_bit_cast(bf16x4, b));
+}
+
+// lane (i, G) takes X[k0 + pair(G, j)][c0 + i] (pair order: rows 4G.., 16+4G..)
+template <class L>
+GMDN_DEV bf16x8 col8_pair(const bf16* X, int k0, int c0) {
+  const int l = lane_id(), i = l & 15, G = l >> 4;
+  const int rr = k0 + 4 * G + (i >> 2), cc = c0 + 4 * (i & 3);
+  const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(X + L::off(rr, cc)));
+  const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(X + L::off(rr + 16, cc)));
+  return cat8(__builtin_bit_cast(bf16x4, a), __builtin_bit_cast(bf16x4, b));
+}
+
+GMDN_DEV float dot4(const f32x4& a, const f32x4& b) {
+  return a[0] * b[0] + a[1] * b[1] + a[2] * b[2] + a[3] * b[3];
+}
+
+// ============================================================ chunk_bwd_state
+template <int D>
+struct StateBwdLds {
+  static constexpr int NKBH = D / 64;
+  static constexpr int TILE = CB_C * D * 2;   // one Q or K chunk (bytes)
+  static constexpr int OT = CB_C * 32 * 2;    // the workgroup's 32 columns of dO
+  static constexpr int GT = 4 * CB_C * 4;     // gate chunk
+  static constexpr int Q0 = 0;
+  static constexpr int K0 = Q0 + RING * TILE;
+  static constexpr int O0 = K0 + RING * TILE;
+  static constexpr int G0 = O0 + RING * OT;
+  static constexpr int XS0 = G0 + RING * GT;                       // Sb^T operand exchange
+  static constexpr int XE0 = XS0 + CB_WAVES * NKBH * 2 * 1024;     // -dE operand exchange
+  static constexpr int BYTES = XE0 + CB_WAVES * 2 * 1024;
+  static_assert(BYTES <= 160 * 1024, "state backward LDS exceeds the 160 KiB of a CU");
+  static constexpr int DMA_OPS = 2 * (CB_C * D / 8) / CB_THREADS + (CB_C * 32 / 8) / CB_THREADS;
+};
+
+template <int D, int RULE>
+__global__ void __launch_bounds__(CB_THREADS) chunk_bwd_state(ChunkArgs p) {
+  using LQ = BSwz<D>;
+  using LO = BSwz<32>;
+  using L = StateBwdLds<D>;
+  constexpr int NKB = D / 32;   // k-blocks over the state's columns
+  constexpr int NTH = D / 32;   // column tiles in a half
+  constexpr int NKBH = L::NKBH;
+  constexpr int ROWB = D * 2;   // bytes per Q/K row
+  extern __shared__ __align__(16) char smem[];
+
+  int64_t bh;
+  int blk;
+  map_block(p.B * p.H, D / 32, bh, blk);
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = lane_id(), G = l >> 4, lc = l & 15;
+  const int rt = w >> 1, h = w & 1;
+  const int r0 = 32 * blk + 16 * rt;  // first state row of this wave
+  const int64_t bb = bh / p.H, hh = bh % p.H;
+  const bf16* qg = p.q + bb * p.sq[0] + hh * p.sq[1];
+  const bf16* kg = p.k + bb * p.sk[0] + hh * p.sk[1];
+  const bf16* og = p.o + bb * p.so[0] + hh * p.so[1] + 32 * blk;  // dO columns of the block
+  const float* gsrc = (G == 0 ? p.beta : G == 1 ? p.g : G == 2 ? (RULE == 2 ? p.gmu : p.beta)
+                                                               : (RULE == 2 ? p.gnu : p.beta)) +
+                      bh * p.T + 4 * lc;
+
+  // per-lane LDS byte offsets (stage, row-tile and k offsets are immediates)
+  uint32_t rowoff[NKB][2];
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) rowoff[kb][hf] = swz_off<LQ>(lc, 32 * kb + 16 * hf + 4 * G);
+  uint32_t coloff[NTH];
+#pragma unroll
+  for (int t = 0; t < NTH; ++t) coloff[t] = swz_off<LQ>(4 * G + (lc >> 2), 16 * (h * NTH + t) + 4 * (lc & 3));
+  // transposing reads of dO (rows 32 kbs + 16 u + 4G + lc/4, columns 16 rt + 4 (lc & 3))
+  const uint32_t ooff = swz_off<LO>(4 * G + (lc >> 2), 16 * rt + 4 * (lc & 3));
+  const uint32_t lds0 = lds_addr(smem);
+  const lds_ptr L0 = lds_base(smem);
+  lds_cptr qrow[NKB][2], krow[NKB][2];
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      qrow[kb][hf] = L0 + (rowoff[kb][hf] + L::Q0);
+      krow[kb][hf] = L0 + (rowoff[kb][hf] + L::K0);
+    }
+  lds_cptr qcol[NTH], kcol[NTH];
+#pragma unroll
+  for (int t = 0; t < NTH; ++t) {
+    qcol[t] = L0 + (coloff[t] + L::Q0);
+    kcol[t] = L0 + (coloff[t] + L::K0);
+  }
+  const lds_cptr oaddr = L0 + (ooff + L::O0);
+  const lds_ptr xsaddr = L0 + (16 * l + L::XS0);
+  const lds_ptr xeaddr = L0 + (16 * l + L::XE0);
+
+  DmaPlan<LQ, CB_C, CB_THREADS> dmq, dmk;
+  DmaPlan<LO, CB_C, CB_THREADS> dmo;
+  dmq.init(w, p.sq[2]);
+  dmk.init(w, p.sk[2]);
+  dmo.init(w, p.so[2]);
+  auto issue_loads = [&](int i, int stg) {
+    const int64_t t0 = (int64_t)i * CB_C;
+    dmq.issue(qg + t0 * p.sq[2], lds0 + L::Q0 + stg * L::TILE, w);
+    dmk.issue(kg + t0 * p.sk[2], lds0 + L::K0 + stg * L::TILE, w);
+    dmo.issue(og + t0 * p.so[2], lds0 + L::O0 + stg * L::OT, w);
+    if (w == 0) lds_dma16(gsrc + t0, smem + L::G0 + stg * L::GT);
+  };
+
+  f32x4 Sb[NTH];
+#pragma unroll
+  for (int t = 0; t < NTH; ++t) Sb[t] = zero4();
+  auto xs_addr = [&](int ww, int k) { return xsaddr + ((ww * NKBH + k) * 2) * 1024; };
+  auto xe_addr = [&](int ww) { return xeaddr + (ww * 2) * 1024; };
+  auto publish_Sb = [&]() {
+#pragma unroll
+    for (int kbl = 0; kbl < NKBH; ++kbl) {
+      const Op<2> x = pack_tiles<2>(Sb[2 * kbl], Sb[2 * kbl + 1]);
+      lds_st<bf16x8>(xs_addr(w, kbl), x.v[0]);
+      lds_st<bf16x8>(xs_addr(w, kbl) + 1024, x.v[1]);
+    }
+  };
+  auto read_op = [&](lds_cptr addr) {
+    Op<2> x;
+    x.v[0] = lds_ld<bf16x8>(addr);
+    x.v[1] = lds_ld<bf16x8>(addr + 1024);
+    return x;
+  };
+  float a = 0.f;
+  auto chunk_scalars = [&](int stg) {
+    const float* gg = reinterpret_cast<const float*>(smem + L::G0 + stg * L::GT);
+    a = expf(wave_sum(fmaxf(gg[CB_C + l], LOG_FLOOR)));
+  };
+
+  // chunks are visited in reverse: step j handles chunk N-1-j, ring stage j % RING
+  for (int j = 0; j < RING - 1 && j < p.N; ++j) issue_loads(p.N - 1 - j, j);
+  publish_Sb();
+  wait_vmem();
+  __syncthreads();
+  if (p.N > 0) chunk_scalars(0);
+
+  auto chunk = [&](auto stg_tag, int j) {
+    constexpr int STG = decltype(stg_tag)::value;
+    constexpr uint32_t SQK = STG * L::TILE;
+    constexpr uint32_t OC = STG * L::OT;
+    const float* gates = reinterpret_cast<const float*>(smem + L::G0 + STG * L::GT);
+    const int i = p.N - 1 - j;
+    const bool ahead = j + RING - 1 < p.N;
+    if (ahead) issue_loads(p.N - 1 - (j + RING - 1), (STG + RING - 1) % RING);
+    {  // Gb_i = Sb_{i+1}
+      float* gp = p.gb + ((bh * p.N + i) * D + r0 + lc) * (int64_t)D + 4 * G;
+#pragma unroll
+      for (int t = 0; t < NTH; ++t) *reinterpret_cast<f32x4*>(gp + 16 * (h * NTH + t)) = Sb[t];
+    }
+    auto rows = [&](const lds_cptr (&base)[NKB][2], int rowtile, int kb) {
+      return cat8(lds_ld<bf16x4>(base[kb][0] + SQK + rowtile * 16 * ROWB),
+                  lds_ld<bf16x4>(base[kb][1] + SQK + rowtile * 16 * ROWB));
+    };
+    // dO operand (k = tokens 32 kbs + pair order, n = this lane's state row)
+    auto dop = [&](int kbs) {
+      return cat8(lds_tr16(oaddr + (OC + (32 * kbs) * 64)), lds_tr16(oaddr + (OC + (32 * kbs + 16) * 64)));
+    };
+    // ---------------- segment 1: dE for this wave's tokens 32H .. 32H+31
+    auto segment1 = [&](auto rt_tag, auto h_tag) {
+      constexpr int RT = decltype(rt_tag)::value, H = decltype(h_tag)::value;
+      Op<2> Sop[NKB];
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) Sop[kb] = read_op(xs_addr(2 * RT + kb / NKBH, kb % NKBH));
+      f32x4 dE[2] = {zero4(), zero4()};
+      {  // diag(w) K Sb^T
+        bf16x8 Kr[2][NKB];
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int kb = 0; kb < NKB; ++kb) Kr[u][kb] = rows(krow, 2 * H + u, kb);
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+          for (int u = 0; u < 2; ++u) dE[u] = mma<1, 2>(Op<1>{{Kr[u][kb]}}, Sop[kb], dE[u]);
+        if constexpr (RULE == 0) {
+#pragma unroll
+          for (int u = 0; u < 2; ++u)
+            dE[u] = dE[u] * *reinterpret_cast<const f32x4*>(gates + 32 * H + 16 * u + 4 * G);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // + A^T dO over the token blocks kbs >= H (A[t][s] = 0 for t < s).  The
+      // A^T operand (m = s, k = t) is the D-layout of (Q K^T) tiles.
+#pragma unroll
+      for (int kbs = H; kbs < 2; ++kbs) {
+        const bf16x8 dO8 = dop(kbs);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int st = 2 * H + u;
+          const float bs = gates[16 * st + lc];
+          f32x4 X[2];
+#pragma unroll
+          for (int hf = 0; hf < 2; ++hf) {
+            const int tt = 2 * kbs + hf;
+            X[hf] = zero4();
+            if (tt >= st) {
+#pragma unroll
+              for (int kb = 0; kb < NKB; ++kb) X[hf] = mfma(rows(qrow, tt, kb), rows(krow, st, kb), X[hf]);
+#pragma unroll
+              for (int jj = 0; jj < 4; ++jj)
+                X[hf][jj] = (tt > st || 4 * G + jj >= lc) ? X[hf][jj] * bs : 0.f;
+            }
+          }
+          dE[u] = mma<2, 1>(pack_tiles<2>(X[0], X[1]), Op<1>{{dO8}}, dE[u]);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      const Op<2> nd = pack_tiles<2>(-dE[0], -dE[1]);
+      lds_st<bf16x8>(xe_addr(2 * RT + H), nd.v[0]);
+      lds_st<bf16x8>(xe_addr(2 * RT + H) + 1024, nd.v[1]);
+    };
+    using std::integral_constant;
+    using I0 = integral_constant<int, 0>;
+    using I1 = integral_constant<int, 1>;
+    switch (w) {
+      case 0: segment1(I0{}, I0{}); break;
+      case 1: segment1(I0{}, I1{}); break;
+      case 2: segment1(I1{}, I0{}); break;
+      default: segment1(I1{}, I1{}); break;
+    }
+    __syncthreads();  // -dE halves published
+    // ---------------- segment 2: Sb_i = a Sb_{i+1} + dO^T Q - dE^T K (column half h)
+    {
+      Op<2> ND[2];
+#pragma unroll
+      for (int hs = 0; hs < 2; ++hs) ND[hs] = read_op(xe_addr(2 * rt + hs));
+      f32x4 acc[NTH];
+#pragma unroll
+      for (int t = 0; t < NTH; ++t) acc[t] = a * Sb[t];
+#pragma unroll
+      for (int kbs = 0; kbs < 2; ++kbs) {
+        const bf16x8 dO8 = dop(kbs);
+#pragma unroll
+        for (int t = 0; t < NTH; ++t) {
+          const uint32_t ro = SQK + kbs * 32 * ROWB;
+          const bf16x8 qc = cat8(lds_tr16(qcol[t] + ro), lds_tr16(qcol[t] + ro + 16 * ROWB));
+          const bf16x8 kc = cat8(lds_tr16(kcol[t] + ro), lds_tr16(kcol[t] + ro + 16 * ROWB));
+          acc[t] = mfma(qc, dO8, acc[t]);
+          acc[t] = mma<1, 2>(Op<1>{{kc}}, ND[kbs], acc[t]);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < NTH; ++t) Sb[t] = acc[t];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    publish_Sb();
+    __builtin_amdgcn_sched_barrier(0);
+    if (ahead) {
+      if (w == 0)
+        wait_vmem_le<L::DMA_OPS + 1>();
+      else
+        wait_vmem_le<L::DMA_OPS>();
+    } else {
+      wait_vmem();
+    }
+    __syncthreads();  // next chunk's tiles landed, Sb_i halves published
+    if (j + 1 < p.N) chunk_scalars((STG + 1) % RING);
+  };
+
+  for (int j = 0; j < p.N; j += RING) {
+    chunk(std::integral_constant<int, 0>{}, j);
+    if (j + 1 < p.N) chunk(std::integral_constant<int, 1>{}, j + 1);
+    if (j + 2 < p.N) chunk(std::integral_constant<int, 2>{}, j + 2);
+  }
+}
+
+// ============================================================== chunk_bwd_tok
+template <int D>
+struct TokBwdLds {
+  static constexpr int TILE = CB_C * D * 2;
+  static constexpr int Q0 = 0, K0 = TILE, V0 = 2 * TILE, O0 = 3 * TILE;
+  static constexpr int EH0 = 4 * TILE, EL0 = 5 * TILE;    // E (rows s, columns r), hi / lo
+  static constexpr int DH0 = 6 * TILE, DL0 = 7 * TILE;    // dE
+  static constexpr int AP = CB_C * CB_C * 2;
+  static constexpr int AH0 = 8 * TILE, AL0 = AH0 + AP;    // dA diag(beta), transposed (rows s)
+  static constexpr int R0 = AL0 + AP;                     // floats: dbeta, beta, g, da
+  static constexpr int BYTES = R0 + (3 * CB_C + 4) * 4;
+  static_assert(BYTES <= 160 * 1024, "token backward LDS exceeds the 160 KiB of a CU");
+};
+
+template <int D, int RULE>
+__global__ void __launch_bounds__(CB_THREADS) chunk_bwd_tok(ChunkArgs p) {
+  using LQ = BSwz<D>;
+  using LA = BSwz<CB_C>;
+  using L = TokBwdLds<D>;
+  constexpr int NKB = D / 32;
+  constexpr int RPW = D / 64;  // 16-row (16-column) tiles of the state per wave
+  extern __shared__ __align__(16) char smem[];
+  const bf16* Qs = reinterpret_cast<const bf16*>(smem + L::Q0);
+  const bf16* Ks = reinterpret_cast<const bf16*>(smem + L::K0);
+  const bf16* Vs = reinterpret_cast<const bf16*>(smem + L::V0);
+  const bf16* Os = reinterpret_cast<const bf16*>(smem + L::O0);
+  bf16* Eh = reinterpret_cast<bf16*>(smem + L::EH0);
+  bf16* El = reinterpret_cast<bf16*>(smem + L::EL0);
+  bf16* Dh = reinterpret_cast<bf16*>(smem + L::DH0);
+  bf16* Dl = reinterpret_cast<bf16*>(smem + L::DL0);
+  bf16* Ah = reinterpret_cast<bf16*>(smem + L::AH0);
+  bf16* Al = reinterpret_cast<bf16*>(smem + L::AL0);
+  float* red = reinterpret_cast<float*>(smem + L::R0);
+  float* rdbeta = red;               // [64]
+  float* rbeta = red + CB_C;         // [64]
+  float* rg = red + 2 * CB_C;        // [64]
+  float* rda = red + 3 * CB_C;       // [1]
+
+  const int64_t bh = blockIdx.x / p.N;
+  const int i = (int)(blockIdx.x % p.N);
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = lane_id(), G = l >> 4, lc = l & 15;
+  const int64_t bb = bh / p.H, hh = bh % p.H;
+  const int64_t t0 = (int64_t)i * CB_C;
+  const float* S = p.states + (bh * p.N + i) * (int64_t)D * D;
+  const float* Gb = p.gb + (bh * p.N + i) * (int64_t)D * D;
+
+  // ---------------- phase 0: the chunk's q, k, v, dO tiles and gates
+  {
+    DmaPlan<LQ, CB_C, CB_THREADS> pq, pk, pv, po;
+    pq.init(w, p.sq[2]);
+    pk.init(w, p.sk[2]);
+    pv.init(w, p.sv[2]);
+    po.init(w, p.so[2]);
+    const uint32_t lds0 = lds_addr(smem);
+    pq.issue(p.q + bb * p.sq[0] + hh * p.sq[1] + t0 * p.sq[2], lds0 + L::Q0, w);
+    pk.issue(p.k + bb * p.sk[0] + hh * p.sk[1] + t0 * p.sk[2], lds0 + L::K0, w);
+    pv.issue(p.v + bb * p.sv[0] + hh * p.sv[1] + t0 * p.sv[2], lds0 + L::V0, w);
+    po.issue(p.o + bb * p.so[0] + hh * p.so[1] + t0 * p.so[2], lds0 + L::O0, w);
+    if (threadIdx.x < CB_C) {
+      const int e = threadIdx.x;
+      rdbeta[e] = 0.f;
+      rbeta[e] = p.beta[bh * p.T + t0 + e];
+      rg[e] = p.g[bh * p.T + t0 + e];
+      if (e == 0) rda[0] = 0.f;
+    }
+    wait_vmem();
+    __syncthreads();
+  }
+
+  // ---------------- phase I: E^T, (K Gb^T)^T and dE^T for this wave's state rows
+  {
+    // B-side operands of A = tril(Q K^T) diag(beta): (k = t in pair order, n = s),
+    // one per (s tile, 32-token block) that is not entirely above the diagonal
+    Op<2> Aop[4][2];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const float bs = rbeta[16 * st + lc];
+#pragma unroll
+      for (int kbt = 0; kbt < 2; ++kbt) {
+        if (32 * kbt + 31 < 16 * st) continue;
+        f32x4 X[2];
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          const int tt = 2 * kbt + hf;
+          X[hf] = zero4();
+          if (tt < st) continue;
+#pragma unroll
+          for (int kb = 0; kb < NKB; ++kb)
+            X[hf] = mfma(row8<LQ>(Qs, 16 * tt + lc, 32 * kb), row8<LQ>(Ks, 16 * st + lc, 32 * kb), X[hf]);
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) X[hf][jj] = (tt > st || 4 * G + jj >= lc) ? X[hf][jj] * bs : 0.f;
+        }
+        Aop[st][kbt] = pack_tiles<2>(X[0], X[1]);
+      }
+    }
+    float da_part = 0.f;
+    float dw_part[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int rho = 0; rho < RPW; ++rho) {
+      const int r0 = 16 * (RPW * w + rho);
+      Op<2> Sa[NKB], Ga[NKB];  // rows r0 + lc of S_i and Gb_i (m = r, natural k)
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+        const int64_t off = (int64_t)(r0 + lc) * D + 32 * kb + 8 * G;
+        const f32x4 s0 = *reinterpret_cast<const f32x4*>(S + off);
+        const f32x4 s1 = *reinterpret_cast<const f32x4*>(S + off + 4);
+        const f32x4 g0 = *reinterpret_cast<const f32x4*>(Gb + off);
+        const f32x4 g1 = *reinterpret_cast<const f32x4*>(Gb + off + 4);
+        da_part += dot4(s0, g0) + dot4(s1, g1);
+        Sa[kb] = pack_tiles<2>(s0, s1);
+        Ga[kb] = pack_tiles<2>(g0, g1);
+      }
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        // D layout: lane (s, G) holds rows r0 + 4G + jj
+        const bf16x4 vv = *reinterpret_cast<const bf16x4*>(Vs + LQ::off(16 * st + lc, r0 + 4 * G));
+        f32x4 Et = f32x4{-(float)vv[0], -(float)vv[1], -(float)vv[2], -(float)vv[3]};
+        f32x4 GK = zero4();
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+          const Op<1> kr{{row8<LQ>(Ks, 16 * st + lc, 32 * kb)}};
+          Et = mma<2, 1>(Sa[kb], kr, Et);
+          GK = mma<2, 1>(Ga[kb], kr, GK);
+        }
+        Et = -Et;  // E^T = V^T - S K^T
+        if constexpr (RULE == 0) dw_part[st] += dot4(Et, GK);
+        const float ws = RULE == 0 ? rbeta[16 * st + lc] : 1.f;
+        f32x4 dEt = GK * ws;
+#pragma unroll
+        for (int kbt = 0; kbt < 2; ++kbt) {
+          if (32 * kbt + 31 < 16 * st) continue;
+          const Op<1> dOt{{col8_pair<LQ>(Os, 32 * kbt, r0)}};  // dO^T (m = r, k = t)
+          dEt = mma<1, 2>(dOt, Aop[st][kbt], dEt);
+        }
+        bf16x4 eh, el, dh, dl;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          bf16 x, y;
+          split2(Et[jj], x, y);
+          eh[jj] = x;
+          el[jj] = y;
+          split2(dEt[jj], x, y);
+          dh[jj] = x;
+          dl[jj] = y;
+        }
+        const int eo = LQ::off(16 * st + lc, r0 + 4 * G);
+        *reinterpret_cast<bf16x4*>(Eh + eo) = eh;
+        *reinterpret_cast<bf16x4*>(El + eo) = el;
+        *reinterpret_cast<bf16x4*>(Dh + eo) = dh;
+        *reinterpret_cast<bf16x4*>(Dl + eo) = dl;
+      }
+    }
+    da_part = wave_sum(da_part);
+    if (l == 0) atomicAdd(rda, da_part);
+    if constexpr (RULE == 0) {
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const float v = group_sum(dw_part[st]);
+        if (G == 0) atomicAdd(rdbeta + 16 * st + lc, v);
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---------------- phase IIa: dA = tril(dO E^T), dbeta's A term, dA diag(beta) -> LDS
+  // tile (tt, st) goes to wave (tt + st) % 4; tiles above the diagonal are zeroed
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    const int st = (w - tt + 4) & 3;
+    bf16x4 ah, al;
+    if (tt < st) {
+      ah = al = bf16x4{(bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f};
+    } else {
+      f32x4 P = zero4(), QK = zero4();
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+        const Op<1> dOr{{row8<LQ>(Os, 16 * tt + lc, 32 * kb)}};
+        const Op<2> Er{{row8<LQ>(Eh, 16 * st + lc, 32 * kb), row8<LQ>(El, 16 * st + lc, 32 * kb)}};
+        P = mma<1, 2>(dOr, Er, P);
+        QK = mfma(row8<LQ>(Qs, 16 * tt + lc, 32 * kb), row8<LQ>(Ks, 16 * st + lc, 32 * kb), QK);
+      }
+      const float bs = rbeta[16 * st + lc];
+      float db = 0.f;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const float pv = (tt > st || 4 * G + jj >= lc) ? P[jj] : 0.f;
+        db += pv * QK[jj];
+        bf16 x, y;
+        split2(pv * bs, x, y);
+        ah[jj] = x;
+        al[jj] = y;
+      }
+      db = group_sum(db);
+      if (G == 0) atomicAdd(rdbeta + 16 * st + lc, db);
+    }
+    const int ao = LA::off(16 * st + lc, 16 * tt + 4 * G);
+    *reinterpret_cast<bf16x4*>(Ah + ao) = ah;
+    *reinterpret_cast<bf16x4*>(Al + ao) = al;
+  }
+  __syncthreads();
+
+  // ---------------- gate gradients and dV
+  if (w == 0) {
+    const float a = expf(wave_sum(fmaxf(rg[l], LOG_FLOOR)));
+    p.dbeta[bh * p.T + t0 + l] = rdbeta[l];
+    p.dg[bh * p.T + t0 + l] = rg[l] >= LOG_FLOOR ? rda[0] * a : 0.f;
+  }
+  {
+    bf16* dvg = p.dv + bb * p.sv[0] + hh * p.sv[1] + t0 * p.sv[2];
+    for (int e = threadIdx.x; e < CB_C * D / 8; e += CB_THREADS) {
+      const int r = e / (D / 8), c8 = (e % (D / 8)) * 8;
+      *reinterpret_cast<bf16x8*>(dvg + r * p.sv[2] + c8) = *reinterpret_cast<const bf16x8*>(Dh + LQ::off(r, c8));
+    }
+  }
+
+  // ---------------- phase IIb: dQ and dK for this wave's 16-column tiles
+  bf16* dqg = p.dq + bb * p.sq[0] + hh * p.sq[1] + t0 * p.sq[2];
+  bf16* dkg = p.dk + bb * p.sk[0] + hh * p.sk[1] + t0 * p.sk[2];
+#pragma unroll
+  for (int phi = 0; phi < RPW; ++phi) {
+    const int j0 = 16 * (RPW * w + phi);
+    Op<2> Sc[NKB], Gc[NKB];  // columns j0 + lc of S_i and Gb_i (k = r natural, n = j)
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      const float* sp = S + (int64_t)(32 * kb + 8 * G) * D + j0 + lc;
+      const float* gp = Gb + (int64_t)(32 * kb + 8 * G) * D + j0 + lc;
+      f32x4 s0, s1, g0, g1;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        s0[jj] = sp[jj * D];
+        s1[jj] = sp[(4 + jj) * D];
+        g0[jj] = gp[jj * D];
+        g1[jj] = gp[(4 + jj) * D];
+      }
+      Sc[kb] = pack_tiles<2>(s0, s1);
+      Gc[kb] = pack_tiles<2>(g0, g1);
+    }
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      // dQ = dO S + (dA diag(beta)) K
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) acc = mma<1, 2>(Op<1>{{row8<LQ>(Os, 16 * tt + lc, 32 * kb)}}, Sc[kb], acc);
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        if (32 * ks > 16 * tt + 15) continue;
+        const Op<2> dA{{col8<LA>(Ah, 32 * ks, 16 * tt), col8<LA>(Al, 32 * ks, 16 * tt)}};
+        acc = mma<2, 1>(dA, Op<1>{{col8<LQ>(Ks, 32 * ks, j0)}}, acc);
+      }
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) dqg[(16 * tt + 4 * G + jj) * p.sq[2] + j0 + lc] = (bf16)acc[jj];
+    }
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      // dK = (dA diag(beta))^T Q - dE S + diag(w) E Gb
+      f32x4 eg = zero4(), acc = zero4();
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+        const Op<2> Er{{row8<LQ>(Eh, 16 * st + lc, 32 * kb), row8<LQ>(El, 16 * st + lc, 32 * kb)}};
+        const Op<2> Dr{{row8<LQ>(Dh, 16 * st + lc, 32 * kb), row8<LQ>(Dl, 16 * st + lc, 32 * kb)}};
+        eg = mma<2, 2>(Er, Gc[kb], eg);
+        acc = mma<2, 2>(Dr, Sc[kb], acc);
+      }
+      if constexpr (RULE == 0) eg = eg * *reinterpret_cast<const f32x4*>(rbeta + 16 * st + 4 * G);
+      acc = eg - acc;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        if (32 * kt + 31 < 16 * st) continue;
+        const Op<2> dAT{{row8<LA>(Ah, 16 * st + lc, 32 * kt), row8<LA>(Al, 16 * st + lc, 32 * kt)}};
+        acc = mma<2, 1>(dAT, Op<1>{{col8<LQ>(Qs, 32 * kt, j0)}}, acc);
+      }
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) dkg[(16 * st + 4 * G + jj) * p.sk[2] + j0 + lc] = (bf16)acc[jj];
+    }
+  }
+}
+
+template <int D, int RULE>
+static hipError_t launch_bwd(const ChunkArgs& a, hipStream_t stream) {
+  auto k1 = chunk_bwd_state<D, RULE>;
+  hipError_t e = hipFuncSetAttribute((const void*)k1, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     StateBwdLds<D>::BYTES);
+  if (e != hipSuccess) return e;
+  auto k2 = chunk_bwd_tok<D, RULE>;
+  e = hipFuncSetAttribute((const void*)k2, hipFuncAttributeMaxDynamicSharedMemorySize, TokBwdLds<D>::BYTES);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k1, dim3((unsigned)(a.B * a.H * (D / 32))), dim3(CB_THREADS), StateBwdLds<D>::BYTES,
+                     stream, a);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k2, dim3((unsigned)(a.B * a.H * a.N)), dim3(CB_THREADS), TokBwdLds<D>::BYTES, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t chunk_bwd_launch(const ChunkArgs& a, int d, int rule, hipStream_t s) {
+  if (rule != 0) return hipErrorNotSupported;
+  return d == 128 ? launch_bwd<128, 0>(a, s) : launch_bwd<64, 0>(a, s);
+}
+
+}  // namespace gmdn

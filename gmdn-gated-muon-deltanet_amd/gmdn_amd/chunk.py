@@ -28,7 +28,7 @@ CHUNK = 64
 SUPPORTED_D = (64, 128)
 
 
-BWD_RULES = ()  # rules whose fused backward kernel is built
+BWD_RULES = (0,)  # rules whose fused backward kernel is built
 
 
 def backward_supported(rule) -> bool:
@@ -115,6 +115,7 @@ class ChunkScan(torch.autograd.Function):
         if need_grad:
             ctx.save_for_backward(qc, kc, vc, bc, gc, mc, nc, states)
         ctx.rule, ctx.ns, ctx.eps = rule, ns, eps
+        ctx.gate_dtypes = tuple(None if t is None else t.dtype for t in (beta, g, gmu, gnu))
         return o
 
     @staticmethod
@@ -122,7 +123,11 @@ class ChunkScan(torch.autograd.Function):
         qc, kc, vc, bc, gc, mc, nc, states = ctx.saved_tensors
         lib = nat.load()
         dOc = _tok(dO.to(torch.bfloat16))
-        dq, dk, dv = (torch.empty_like(t, memory_format=torch.contiguous_format) for t in (qc, kc, vc))
+        if ctx.rule not in BWD_RULES:
+            raise RuntimeError(f"the fused backward of rule {ctx.rule} is not built")
+        # gradients share the strides of q, k, v (the kernels write them with those strides)
+        dq, dk, dv = (torch.empty_strided(t.shape, t.stride(), dtype=t.dtype, device=t.device)
+                      for t in (qc, kc, vc))
         dbeta, dg = torch.empty_like(bc), torch.empty_like(gc)
         dgmu = torch.empty_like(mc) if mc is not None else None
         dgnu = torch.empty_like(nc) if nc is not None else None
@@ -135,7 +140,8 @@ class ChunkScan(torch.autograd.Function):
                                     nat.ptr(dk), nat.ptr(dv), nat.ptr(dbeta), nat.ptr(dg), nat.ptr(dgmu),
                                     nat.ptr(dgnu), nat.ptr(ws), ws_bytes, nat.stream_of(qc))
         nat.check(rc, "gmdn_chunk_bwd")
-        return dq, dk, dv, dbeta, dg, dgmu, dgnu, None, None, None
+        gates = [None if t is None else t.to(dt) for t, dt in zip((dbeta, dg, dgmu, dgnu), ctx.gate_dtypes)]
+        return (dq, dk, dv, *gates, None, None, None)
 
 
 def chunk_scan(q, k, v, beta, g, gmu=None, gnu=None, *, rule="delta", ns: int = 3, eps: float = 1e-6):
