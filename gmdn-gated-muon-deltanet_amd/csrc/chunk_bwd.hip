@@ -313,8 +313,13 @@ __global__ void __launch_bounds__(CB_THREADS) chunk_bwd_state(ChunkArgs p) {
 }
 
 // ============================================================== chunk_bwd_tok
+// One wave per 16 state rows (phase I) and per 16 state columns (phase IIb):
+// D / 16 waves, two per SIMD at d = 128, so one wave's global loads overlap
+// another's MFMA work (the workgroup's LDS allows one workgroup per CU).
 template <int D>
 struct TokBwdLds {
+  static constexpr int NW = D / 16;
+  static constexpr int NTHR = 64 * NW;
   static constexpr int TILE = CB_C * D * 2;
   static constexpr int Q0 = 0, K0 = TILE, V0 = 2 * TILE, O0 = 3 * TILE;
   static constexpr int EH0 = 4 * TILE, EL0 = 5 * TILE;    // E (rows s, columns r), hi / lo
@@ -327,12 +332,13 @@ struct TokBwdLds {
 };
 
 template <int D, int RULE>
-__global__ void __launch_bounds__(CB_THREADS) chunk_bwd_tok(ChunkArgs p) {
+__global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p) {
   using LQ = BSwz<D>;
   using LA = BSwz<CB_C>;
   using L = TokBwdLds<D>;
   constexpr int NKB = D / 32;
-  constexpr int RPW = D / 64;  // 16-row (16-column) tiles of the state per wave
+  constexpr int NW = L::NW;
+  constexpr int NTHR = L::NTHR;
   extern __shared__ __align__(16) char smem[];
   const bf16* Qs = reinterpret_cast<const bf16*>(smem + L::Q0);
   const bf16* Ks = reinterpret_cast<const bf16*>(smem + L::K0);
@@ -358,10 +364,23 @@ __global__ void __launch_bounds__(CB_THREADS) chunk_bwd_tok(ChunkArgs p) {
   const int64_t t0 = (int64_t)i * CB_C;
   const float* S = p.states + (bh * p.N + i) * (int64_t)D * D;
   const float* Gb = p.gb + (bh * p.N + i) * (int64_t)D * D;
+  const int r0 = 16 * w;  // this wave's state rows (phase I) ...
+  const int j0 = 16 * w;  // ... and state columns (phase IIb)
+
+  // rows r0 + lc of S_i and Gb_i (natural k order), loaded while the tiles arrive
+  f32x4 srow[NKB][2], grow[NKB][2];
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb) {
+    const int64_t off = (int64_t)(r0 + lc) * D + 32 * kb + 8 * G;
+    srow[kb][0] = *reinterpret_cast<const f32x4*>(S + off);
+    srow[kb][1] = *reinterpret_cast<const f32x4*>(S + off + 4);
+    grow[kb][0] = *reinterpret_cast<const f32x4*>(Gb + off);
+    grow[kb][1] = *reinterpret_cast<const f32x4*>(Gb + off + 4);
+  }
 
   // ---------------- phase 0: the chunk's q, k, v, dO tiles and gates
   {
-    DmaPlan<LQ, CB_C, CB_THREADS> pq, pk, pv, po;
+    DmaPlan<LQ, CB_C, NTHR> pq, pk, pv, po;
     pq.init(w, p.sq[2]);
     pk.init(w, p.sk[2]);
     pv.init(w, p.sv[2]);
@@ -382,7 +401,7 @@ __global__ void __launch_bounds__(CB_THREADS) chunk_bwd_tok(ChunkArgs p) {
     __syncthreads();
   }
 
-  // ---------------- phase I: E^T, (K Gb^T)^T and dE^T for this wave's state rows
+  // ---------------- phase I: E^T, (Gb K^T) and dE^T for this wave's 16 state rows
   {
     // B-side operands of A = tril(Q K^T) diag(beta): (k = t in pair order, n = s),
     // one per (s tile, 32-token block) that is not entirely above the diagonal
@@ -409,79 +428,81 @@ __global__ void __launch_bounds__(CB_THREADS) chunk_bwd_tok(ChunkArgs p) {
       }
     }
     float da_part = 0.f;
-    float dw_part[4] = {0.f, 0.f, 0.f, 0.f};
+    Op<2> Sa[NKB], Ga[NKB];  // (m = r, k = c natural)
 #pragma unroll
-    for (int rho = 0; rho < RPW; ++rho) {
-      const int r0 = 16 * (RPW * w + rho);
-      Op<2> Sa[NKB], Ga[NKB];  // rows r0 + lc of S_i and Gb_i (m = r, natural k)
+    for (int kb = 0; kb < NKB; ++kb) {
+      da_part += dot4(srow[kb][0], grow[kb][0]) + dot4(srow[kb][1], grow[kb][1]);
+      Sa[kb] = pack_tiles<2>(srow[kb][0], srow[kb][1]);
+      Ga[kb] = pack_tiles<2>(grow[kb][0], grow[kb][1]);
+    }
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      // D layout: lane (s, G) holds rows r0 + 4G + jj
+      const bf16x4 vv = *reinterpret_cast<const bf16x4*>(Vs + LQ::off(16 * st + lc, r0 + 4 * G));
+      f32x4 Et = f32x4{-(float)vv[0], -(float)vv[1], -(float)vv[2], -(float)vv[3]};
+      f32x4 GK = zero4();
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb) {
-        const int64_t off = (int64_t)(r0 + lc) * D + 32 * kb + 8 * G;
-        const f32x4 s0 = *reinterpret_cast<const f32x4*>(S + off);
-        const f32x4 s1 = *reinterpret_cast<const f32x4*>(S + off + 4);
-        const f32x4 g0 = *reinterpret_cast<const f32x4*>(Gb + off);
-        const f32x4 g1 = *reinterpret_cast<const f32x4*>(Gb + off + 4);
-        da_part += dot4(s0, g0) + dot4(s1, g1);
-        Sa[kb] = pack_tiles<2>(s0, s1);
-        Ga[kb] = pack_tiles<2>(g0, g1);
+        const Op<1> kr{{row8<LQ>(Ks, 16 * st + lc, 32 * kb)}};
+        Et = mma<2, 1>(Sa[kb], kr, Et);
+        GK = mma<2, 1>(Ga[kb], kr, GK);
       }
-#pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        // D layout: lane (s, G) holds rows r0 + 4G + jj
-        const bf16x4 vv = *reinterpret_cast<const bf16x4*>(Vs + LQ::off(16 * st + lc, r0 + 4 * G));
-        f32x4 Et = f32x4{-(float)vv[0], -(float)vv[1], -(float)vv[2], -(float)vv[3]};
-        f32x4 GK = zero4();
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb) {
-          const Op<1> kr{{row8<LQ>(Ks, 16 * st + lc, 32 * kb)}};
-          Et = mma<2, 1>(Sa[kb], kr, Et);
-          GK = mma<2, 1>(Ga[kb], kr, GK);
-        }
-        Et = -Et;  // E^T = V^T - S K^T
-        if constexpr (RULE == 0) dw_part[st] += dot4(Et, GK);
-        const float ws = RULE == 0 ? rbeta[16 * st + lc] : 1.f;
-        f32x4 dEt = GK * ws;
-#pragma unroll
-        for (int kbt = 0; kbt < 2; ++kbt) {
-          if (32 * kbt + 31 < 16 * st) continue;
-          const Op<1> dOt{{col8_pair<LQ>(Os, 32 * kbt, r0)}};  // dO^T (m = r, k = t)
-          dEt = mma<1, 2>(dOt, Aop[st][kbt], dEt);
-        }
-        bf16x4 eh, el, dh, dl;
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          bf16 x, y;
-          split2(Et[jj], x, y);
-          eh[jj] = x;
-          el[jj] = y;
-          split2(dEt[jj], x, y);
-          dh[jj] = x;
-          dl[jj] = y;
-        }
-        const int eo = LQ::off(16 * st + lc, r0 + 4 * G);
-        *reinterpret_cast<bf16x4*>(Eh + eo) = eh;
-        *reinterpret_cast<bf16x4*>(El + eo) = el;
-        *reinterpret_cast<bf16x4*>(Dh + eo) = dh;
-        *reinterpret_cast<bf16x4*>(Dl + eo) = dl;
+      Et = -Et;  // E^T = V^T - S K^T
+      if constexpr (RULE == 0) {
+        // dbeta's diag(w) term: sum_r E[s][r] (Gb k_s)[r]
+        const float v = group_sum(dot4(Et, GK));
+        if (G == 0) atomicAdd(rdbeta + 16 * st + lc, v);
       }
+      const float ws = RULE == 0 ? rbeta[16 * st + lc] : 1.f;
+      f32x4 dEt = GK * ws;
+#pragma unroll
+      for (int kbt = 0; kbt < 2; ++kbt) {
+        if (32 * kbt + 31 < 16 * st) continue;
+        const Op<1> dOt{{col8_pair<LQ>(Os, 32 * kbt, r0)}};  // dO^T (m = r, k = t)
+        dEt = mma<1, 2>(dOt, Aop[st][kbt], dEt);
+      }
+      bf16x4 eh, el, dh, dl;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        bf16 x, y;
+        split2(Et[jj], x, y);
+        eh[jj] = x;
+        el[jj] = y;
+        split2(dEt[jj], x, y);
+        dh[jj] = x;
+        dl[jj] = y;
+      }
+      const int eo = LQ::off(16 * st + lc, r0 + 4 * G);
+      *reinterpret_cast<bf16x4*>(Eh + eo) = eh;
+      *reinterpret_cast<bf16x4*>(El + eo) = el;
+      *reinterpret_cast<bf16x4*>(Dh + eo) = dh;
+      *reinterpret_cast<bf16x4*>(Dl + eo) = dl;
     }
     da_part = wave_sum(da_part);
     if (l == 0) atomicAdd(rda, da_part);
-    if constexpr (RULE == 0) {
+  }
+  // columns j0 + lc of S_i and Gb_i (k = r natural, n = j) for phase IIb,
+  // requested before the barrier so that they arrive during phase IIa
+  f32x4 scol[NKB][2], gcol[NKB][2];
 #pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        const float v = group_sum(dw_part[st]);
-        if (G == 0) atomicAdd(rdbeta + 16 * st + lc, v);
-      }
+  for (int kb = 0; kb < NKB; ++kb) {
+    const float* sp = S + (int64_t)(32 * kb + 8 * G) * D + j0 + lc;
+    const float* gp = Gb + (int64_t)(32 * kb + 8 * G) * D + j0 + lc;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      scol[kb][0][jj] = sp[jj * D];
+      scol[kb][1][jj] = sp[(4 + jj) * D];
+      gcol[kb][0][jj] = gp[jj * D];
+      gcol[kb][1][jj] = gp[(4 + jj) * D];
     }
   }
   __syncthreads();
 
   // ---------------- phase IIa: dA = tril(dO E^T), dbeta's A term, dA diag(beta) -> LDS
-  // tile (tt, st) goes to wave (tt + st) % 4; tiles above the diagonal are zeroed
+  // tiles k = 4 tt + st, k = w, w + NW, ...; tiles above the diagonal are zeroed
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt) {
-    const int st = (w - tt + 4) & 3;
+  for (int kk = 0; kk < 16 / NW; ++kk) {
+    const int k = w + NW * kk, tt = k >> 2, st = k & 3;
     bf16x4 ah, al;
     if (tt < st) {
       ah = al = bf16x4{(bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f};
@@ -522,71 +543,57 @@ __global__ void __launch_bounds__(CB_THREADS) chunk_bwd_tok(ChunkArgs p) {
   }
   {
     bf16* dvg = p.dv + bb * p.sv[0] + hh * p.sv[1] + t0 * p.sv[2];
-    for (int e = threadIdx.x; e < CB_C * D / 8; e += CB_THREADS) {
+    for (int e = threadIdx.x; e < CB_C * D / 8; e += NTHR) {
       const int r = e / (D / 8), c8 = (e % (D / 8)) * 8;
       *reinterpret_cast<bf16x8*>(dvg + r * p.sv[2] + c8) = *reinterpret_cast<const bf16x8*>(Dh + LQ::off(r, c8));
     }
   }
 
-  // ---------------- phase IIb: dQ and dK for this wave's 16-column tiles
+  // ---------------- phase IIb: dQ and dK for this wave's 16 state columns
   bf16* dqg = p.dq + bb * p.sq[0] + hh * p.sq[1] + t0 * p.sq[2];
   bf16* dkg = p.dk + bb * p.sk[0] + hh * p.sk[1] + t0 * p.sk[2];
+  Op<2> Sc[NKB], Gc[NKB];
 #pragma unroll
-  for (int phi = 0; phi < RPW; ++phi) {
-    const int j0 = 16 * (RPW * w + phi);
-    Op<2> Sc[NKB], Gc[NKB];  // columns j0 + lc of S_i and Gb_i (k = r natural, n = j)
+  for (int kb = 0; kb < NKB; ++kb) {
+    Sc[kb] = pack_tiles<2>(scol[kb][0], scol[kb][1]);
+    Gc[kb] = pack_tiles<2>(gcol[kb][0], gcol[kb][1]);
+  }
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    // dQ = dO S + (dA diag(beta)) K
+    f32x4 acc = zero4();
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) acc = mma<1, 2>(Op<1>{{row8<LQ>(Os, 16 * tt + lc, 32 * kb)}}, Sc[kb], acc);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      if (32 * ks > 16 * tt + 15) continue;
+      const Op<2> dA{{col8<LA>(Ah, 32 * ks, 16 * tt), col8<LA>(Al, 32 * ks, 16 * tt)}};
+      acc = mma<2, 1>(dA, Op<1>{{col8<LQ>(Ks, 32 * ks, j0)}}, acc);
+    }
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) dqg[(16 * tt + 4 * G + jj) * p.sq[2] + j0 + lc] = (bf16)acc[jj];
+  }
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+    // dK = (dA diag(beta))^T Q - dE S + diag(w) E Gb
+    f32x4 eg = zero4(), acc = zero4();
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
-      const float* sp = S + (int64_t)(32 * kb + 8 * G) * D + j0 + lc;
-      const float* gp = Gb + (int64_t)(32 * kb + 8 * G) * D + j0 + lc;
-      f32x4 s0, s1, g0, g1;
+      const Op<2> Er{{row8<LQ>(Eh, 16 * st + lc, 32 * kb), row8<LQ>(El, 16 * st + lc, 32 * kb)}};
+      const Op<2> Dr{{row8<LQ>(Dh, 16 * st + lc, 32 * kb), row8<LQ>(Dl, 16 * st + lc, 32 * kb)}};
+      eg = mma<2, 2>(Er, Gc[kb], eg);
+      acc = mma<2, 2>(Dr, Sc[kb], acc);
+    }
+    if constexpr (RULE == 0) eg = eg * *reinterpret_cast<const f32x4*>(rbeta + 16 * st + 4 * G);
+    acc = eg - acc;
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        s0[jj] = sp[jj * D];
-        s1[jj] = sp[(4 + jj) * D];
-        g0[jj] = gp[jj * D];
-        g1[jj] = gp[(4 + jj) * D];
-      }
-      Sc[kb] = pack_tiles<2>(s0, s1);
-      Gc[kb] = pack_tiles<2>(g0, g1);
+    for (int kt = 0; kt < 2; ++kt) {
+      if (32 * kt + 31 < 16 * st) continue;
+      const Op<2> dAT{{row8<LA>(Ah, 16 * st + lc, 32 * kt), row8<LA>(Al, 16 * st + lc, 32 * kt)}};
+      acc = mma<2, 1>(dAT, Op<1>{{col8<LQ>(Qs, 32 * kt, j0)}}, acc);
     }
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      // dQ = dO S + (dA diag(beta)) K
-      f32x4 acc = zero4();
-#pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) acc = mma<1, 2>(Op<1>{{row8<LQ>(Os, 16 * tt + lc, 32 * kb)}}, Sc[kb], acc);
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        if (32 * ks > 16 * tt + 15) continue;
-        const Op<2> dA{{col8<LA>(Ah, 32 * ks, 16 * tt), col8<LA>(Al, 32 * ks, 16 * tt)}};
-        acc = mma<2, 1>(dA, Op<1>{{col8<LQ>(Ks, 32 * ks, j0)}}, acc);
-      }
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) dqg[(16 * tt + 4 * G + jj) * p.sq[2] + j0 + lc] = (bf16)acc[jj];
-    }
-#pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      // dK = (dA diag(beta))^T Q - dE S + diag(w) E Gb
-      f32x4 eg = zero4(), acc = zero4();
-#pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) {
-        const Op<2> Er{{row8<LQ>(Eh, 16 * st + lc, 32 * kb), row8<LQ>(El, 16 * st + lc, 32 * kb)}};
-        const Op<2> Dr{{row8<LQ>(Dh, 16 * st + lc, 32 * kb), row8<LQ>(Dl, 16 * st + lc, 32 * kb)}};
-        eg = mma<2, 2>(Er, Gc[kb], eg);
-        acc = mma<2, 2>(Dr, Sc[kb], acc);
-      }
-      if constexpr (RULE == 0) eg = eg * *reinterpret_cast<const f32x4*>(rbeta + 16 * st + 4 * G);
-      acc = eg - acc;
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        if (32 * kt + 31 < 16 * st) continue;
-        const Op<2> dAT{{row8<LA>(Ah, 16 * st + lc, 32 * kt), row8<LA>(Al, 16 * st + lc, 32 * kt)}};
-        acc = mma<2, 1>(dAT, Op<1>{{col8<LQ>(Qs, 32 * kt, j0)}}, acc);
-      }
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) dkg[(16 * st + 4 * G + jj) * p.sk[2] + j0 + lc] = (bf16)acc[jj];
-    }
+    for (int jj = 0; jj < 4; ++jj) dkg[(16 * st + 4 * G + jj) * p.sk[2] + j0 + lc] = (bf16)acc[jj];
   }
 }
 
@@ -603,7 +610,8 @@ static hipError_t launch_bwd(const ChunkArgs& a, hipStream_t stream) {
                      stream, a);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k2, dim3((unsigned)(a.B * a.H * a.N)), dim3(CB_THREADS), TokBwdLds<D>::BYTES, stream, a);
+  hipLaunchKernelGGL(k2, dim3((unsigned)(a.B * a.H * a.N)), dim3(TokBwdLds<D>::NTHR), TokBwdLds<D>::BYTES,
+                     stream, a);
   return hipGetLastError();
 }
 
