@@ -138,7 +138,7 @@ def main(argv=None):
     dev = torch.device("cuda:0")
     inp = make_inputs(w, seed=0, device=dev, with_grad_out=True)
     names = ("q", "k", "v", "beta", "g", "gmu", "gnu")
-    with_bwd = chunk.backward_supported(w.rule)
+    with_bwd = chunk.backward_supported(w.rule, w.d)
     xs = [inp[n] if inp[n] is None else inp[n].detach().requires_grad_(with_bwd) for n in names]
     grads_of = [x for x in xs if x is not None]
     dO = inp["dO"]

@@ -16,13 +16,14 @@ struct ChunkArgs {
   const bf16 *q, *k, *v;
   const float *beta, *g, *gmu, *gnu;
   bf16* o;         // forward output (backward: dO, read only)
-  float* states;   // per-chunk pre-update states S_i (backward: read only)
+  float* states;   // per-chunk pre-update S_i [, M_i, V_i] planes (backward: read only)
   int64_t B, H, T;
   int N;
   float eps;
   int64_t sq[3], sk[3], sv[3], so[3];
   // backward only
   float* gb;       // per-chunk state cotangents Gb_i (B, H, N, d, d)
+  float* part;     // per (chunk, row block): partial da, db, dm, dn
   bf16 *dq, *dk, *dv;
   float *dbeta, *dg, *dgmu, *dgnu;
 };

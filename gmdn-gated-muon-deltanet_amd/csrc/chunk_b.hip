@@ -218,10 +218,17 @@ __global__ void __launch_bounds__(CB_THREADS) chunk_fwd(ChunkArgs p) {
     if (i > 0) store_o(i - 1);
     const bool ahead = i + FWD_STAGES - 1 < p.N;
     if (ahead) issue_loads(i + FWD_STAGES - 1, (STG + FWD_STAGES - 1) % FWD_STAGES);
-    if (p.states) {  // pre-update state for the backward
+    if (p.states) {  // pre-update state (and adam's moments) for the backward
+      const int64_t plane = p.B * p.H * p.N * (int64_t)D * D;
       float* sp = p.states + ((bh * p.N + i) * D + r0 + lc) * (int64_t)D + 4 * G;
 #pragma unroll
-      for (int t = 0; t < NTH; ++t) *reinterpret_cast<f32x4*>(sp + 16 * (h * NTH + t)) = S[t];
+      for (int t = 0; t < NTH; ++t) {
+        *reinterpret_cast<f32x4*>(sp + 16 * (h * NTH + t)) = S[t];
+        if constexpr (RULE == 2) {
+          *reinterpret_cast<f32x4*>(sp + plane + 16 * (h * NTH + t)) = Mm[t];
+          *reinterpret_cast<f32x4*>(sp + 2 * plane + 16 * (h * NTH + t)) = Vv[t];
+        }
+      }
     }
     // k-block kb of row tile `rowtile` (a compile-time offset from the base set)
     auto rows = [&](const lds_cptr (&base)[NKB][2], int rowtile, int kb) {
@@ -481,7 +488,9 @@ extern "C" {
 
 size_t gmdn_chunk_states_bytes(const gmdn_chunk_desc* desc) {
   if (check_desc(desc) != GMDN_OK) return 0;
-  return (size_t)(desc->B * desc->H * (desc->T / CB_C)) * desc->d * desc->d * sizeof(float);
+  // S_i for every rule; adam adds its moments M_i and V_i
+  const size_t planes = desc->rule == 2 ? 3 : 1;
+  return planes * (size_t)(desc->B * desc->H * (desc->T / CB_C)) * desc->d * desc->d * sizeof(float);
 }
 
 int gmdn_chunk_fwd(const gmdn_chunk_desc* desc, const void* q, const void* k, const void* v,
@@ -504,8 +513,11 @@ int gmdn_chunk_fwd(const gmdn_chunk_desc* desc, const void* q, const void* k, co
 }
 
 size_t gmdn_chunk_bwd_workspace_bytes(const gmdn_chunk_desc* desc) {
-  // Gb_i, the cotangent of every chunk's state update (fp32 d x d per chunk)
-  return gmdn_chunk_states_bytes(desc);
+  if (check_desc(desc) != GMDN_OK) return 0;
+  // Gb_i, the cotangent of every chunk's state update (fp32 d x d per chunk),
+  // then per (chunk, row block) partial sums of the chunk scalars' gradients
+  const size_t chunks = (size_t)(desc->B * desc->H * (desc->T / CB_C));
+  return chunks * desc->d * desc->d * sizeof(float) + chunks * (desc->d / 32) * 4 * sizeof(float);
 }
 
 int gmdn_chunk_bwd(const gmdn_chunk_desc* desc, const void* q, const void* k, const void* v,
@@ -520,7 +532,10 @@ int gmdn_chunk_bwd(const gmdn_chunk_desc* desc, const void* q, const void* k, co
     return GMDN_ERR_ARG;
   if (desc->rule >= 1 && (!gmu || !dgmu)) return GMDN_ERR_ARG;
   if (desc->rule == 2 && (!gnu || !dgnu)) return GMDN_ERR_ARG;
-  if (desc->rule != 0) return GMDN_ERR_UNSUPPORTED;
+  if (desc->rule == 1) return GMDN_ERR_UNSUPPORTED;
+  // adam at d = 128: the sign-like update M / (sqrt(V) + eps) amplifies the
+  // rounding of the split-bf16 state products beyond the gradient tolerance
+  if (desc->rule == 2 && desc->d != 64) return GMDN_ERR_UNSUPPORTED;
   if (desc->B * desc->H * (desc->T / CB_C) >= ((int64_t)1 << 31)) return GMDN_ERR_ARG;  // one workgroup per chunk
   if (!workspace || workspace_bytes < gmdn_chunk_bwd_workspace_bytes(desc)) return GMDN_ERR_WORKSPACE;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dO) || !aligned16(dv) ||
@@ -529,6 +544,7 @@ int gmdn_chunk_bwd(const gmdn_chunk_desc* desc, const void* q, const void* k, co
   ChunkArgs a = make_args(desc, q, k, v, beta, g, gmu, gnu, const_cast<void*>(dO),
                           const_cast<void*>(states));
   a.gb = (float*)workspace;
+  a.part = a.gb + a.B * a.H * a.N * (int64_t)desc->d * desc->d;
   a.dq = (bf16*)dq;
   a.dk = (bf16*)dk;
   a.dv = (bf16*)dv;

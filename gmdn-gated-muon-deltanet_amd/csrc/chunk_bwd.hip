@@ -63,28 +63,32 @@ GMDN_DEV float dot4(const f32x4& a, const f32x4& b) {
 }
 
 // ============================================================ chunk_bwd_state
-template <int D>
+template <int D, int RULE>
 struct StateBwdLds {
+  static constexpr bool ADAM = RULE == 2;
   static constexpr int NKBH = D / 64;
   static constexpr int TILE = CB_C * D * 2;   // one Q or K chunk (bytes)
-  static constexpr int OT = CB_C * 32 * 2;    // the workgroup's 32 columns of dO
+  static constexpr int OT = CB_C * 32 * 2;    // the workgroup's 32 columns of dO (or V)
   static constexpr int GT = 4 * CB_C * 4;     // gate chunk
   static constexpr int Q0 = 0;
   static constexpr int K0 = Q0 + RING * TILE;
   static constexpr int O0 = K0 + RING * TILE;
-  static constexpr int G0 = O0 + RING * OT;
-  static constexpr int XS0 = G0 + RING * GT;                       // Sb^T operand exchange
+  static constexpr int V0 = O0 + RING * OT;                        // adam: V columns (E recompute)
+  static constexpr int G0 = V0 + (ADAM ? RING * OT : 0);
+  static constexpr int XS0 = G0 + RING * GT;                       // Gb^T operand exchange
   static constexpr int XE0 = XS0 + CB_WAVES * NKBH * 2 * 1024;     // -dE operand exchange
-  static constexpr int BYTES = XE0 + CB_WAVES * 2 * 1024;
+  static constexpr int XN0 = XE0 + CB_WAVES * 2 * 1024;            // adam: -E operand exchange
+  static constexpr int P0 = XN0 + (ADAM ? CB_WAVES * 2 * 1024 : 0);  // adam: 4 partial sums
+  static constexpr int BYTES = P0 + 16;
   static_assert(BYTES <= 160 * 1024, "state backward LDS exceeds the 160 KiB of a CU");
-  static constexpr int DMA_OPS = 2 * (CB_C * D / 8) / CB_THREADS + (CB_C * 32 / 8) / CB_THREADS;
+  static constexpr int DMA_OPS = 2 * (CB_C * D / 8) / CB_THREADS + (ADAM ? 2 : 1) * (CB_C * 32 / 8) / CB_THREADS;
 };
 
 template <int D, int RULE>
 __global__ void __launch_bounds__(CB_THREADS) chunk_bwd_state(ChunkArgs p) {
   using LQ = BSwz<D>;
   using LO = BSwz<32>;
-  using L = StateBwdLds<D>;
+  using L = StateBwdLds<D, RULE>;
   constexpr int NKB = D / 32;   // k-blocks over the state's columns
   constexpr int NTH = D / 32;   // column tiles in a half
   constexpr int NKBH = L::NKBH;
@@ -102,6 +106,7 @@ __global__ void __launch_bounds__(CB_THREADS) chunk_bwd_state(ChunkArgs p) {
   const bf16* qg = p.q + bb * p.sq[0] + hh * p.sq[1];
   const bf16* kg = p.k + bb * p.sk[0] + hh * p.sk[1];
   const bf16* og = p.o + bb * p.so[0] + hh * p.so[1] + 32 * blk;  // dO columns of the block
+  const bf16* vg = p.v + bb * p.sv[0] + hh * p.sv[1] + 32 * blk;  // V columns (adam)
   const float* gsrc = (G == 0 ? p.beta : G == 1 ? p.g : G == 2 ? (RULE == 2 ? p.gmu : p.beta)
                                                                : (RULE == 2 ? p.gnu : p.beta)) +
                       bh * p.T + 4 * lc;
@@ -134,31 +139,55 @@ __global__ void __launch_bounds__(CB_THREADS) chunk_bwd_state(ChunkArgs p) {
     kcol[t] = L0 + (coloff[t] + L::K0);
   }
   const lds_cptr oaddr = L0 + (ooff + L::O0);
+  const lds_cptr vaddr = L0 + (ooff + L::V0);
   const lds_ptr xsaddr = L0 + (16 * l + L::XS0);
   const lds_ptr xeaddr = L0 + (16 * l + L::XE0);
+  const lds_ptr xnaddr = L0 + (16 * l + L::XN0);
+  float* psum = reinterpret_cast<float*>(smem + L::P0);
 
   DmaPlan<LQ, CB_C, CB_THREADS> dmq, dmk;
-  DmaPlan<LO, CB_C, CB_THREADS> dmo;
+  DmaPlan<LO, CB_C, CB_THREADS> dmo, dmv;
   dmq.init(w, p.sq[2]);
   dmk.init(w, p.sk[2]);
   dmo.init(w, p.so[2]);
+  if constexpr (RULE == 2) dmv.init(w, p.sv[2]);
   auto issue_loads = [&](int i, int stg) {
     const int64_t t0 = (int64_t)i * CB_C;
     dmq.issue(qg + t0 * p.sq[2], lds0 + L::Q0 + stg * L::TILE, w);
     dmk.issue(kg + t0 * p.sk[2], lds0 + L::K0 + stg * L::TILE, w);
     dmo.issue(og + t0 * p.so[2], lds0 + L::O0 + stg * L::OT, w);
+    if constexpr (RULE == 2) dmv.issue(vg + t0 * p.sv[2], lds0 + L::V0 + stg * L::OT, w);
     if (w == 0) lds_dma16(gsrc + t0, smem + L::G0 + stg * L::GT);
   };
 
-  f32x4 Sb[NTH];
+  f32x4 Sb[NTH];   // dL/dS_{i+1}, this lane's row, the wave's column half
+  f32x4 Mb[NTH], Vb[NTH];  // adam: dL/dM_{i+1}, dL/dV_{i+1}
 #pragma unroll
-  for (int t = 0; t < NTH; ++t) Sb[t] = zero4();
+  for (int t = 0; t < NTH; ++t) Sb[t] = Mb[t] = Vb[t] = zero4();
+  // adam: chunk i's S_i row (pair-order pieces of all columns) and M_i, V_i
+  // (the wave's column half), loaded one chunk ahead
+  f32x4 Sraw[NKB][2], Mp[NTH], Vp[NTH];
+  auto load_states = [&](int i) {
+    const int64_t plane = p.B * p.H * p.N * (int64_t)D * D;
+    const float* sp = p.states + ((bh * p.N + i) * D + r0 + lc) * (int64_t)D;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      Sraw[kb][0] = *reinterpret_cast<const f32x4*>(sp + 32 * kb + 4 * G);
+      Sraw[kb][1] = *reinterpret_cast<const f32x4*>(sp + 32 * kb + 16 + 4 * G);
+    }
+#pragma unroll
+    for (int t = 0; t < NTH; ++t) {
+      Mp[t] = *reinterpret_cast<const f32x4*>(sp + plane + 16 * (h * NTH + t) + 4 * G);
+      Vp[t] = *reinterpret_cast<const f32x4*>(sp + 2 * plane + 16 * (h * NTH + t) + 4 * G);
+    }
+  };
+  auto xn_addr = [&](int ww) { return xnaddr + (ww * 2) * 1024; };
   auto xs_addr = [&](int ww, int k) { return xsaddr + ((ww * NKBH + k) * 2) * 1024; };
   auto xe_addr = [&](int ww) { return xeaddr + (ww * 2) * 1024; };
-  auto publish_Sb = [&]() {
+  auto publish_Gb = [&](const f32x4 (&X)[NTH]) {
 #pragma unroll
     for (int kbl = 0; kbl < NKBH; ++kbl) {
-      const Op<2> x = pack_tiles<2>(Sb[2 * kbl], Sb[2 * kbl + 1]);
+      const Op<2> x = pack_tiles<2>(X[2 * kbl], X[2 * kbl + 1]);
       lds_st<bf16x8>(xs_addr(w, kbl), x.v[0]);
       lds_st<bf16x8>(xs_addr(w, kbl) + 1024, x.v[1]);
     }
@@ -169,15 +198,25 @@ __global__ void __launch_bounds__(CB_THREADS) chunk_bwd_state(ChunkArgs p) {
     x.v[1] = lds_ld<bf16x8>(addr + 1024);
     return x;
   };
-  float a = 0.f;
+  float a = 0.f, bsc = 0.f, msc = 0.f, nsc = 0.f;
   auto chunk_scalars = [&](int stg) {
     const float* gg = reinterpret_cast<const float*>(smem + L::G0 + stg * L::GT);
     a = expf(wave_sum(fmaxf(gg[CB_C + l], LOG_FLOOR)));
+    if constexpr (RULE == 2) {
+      bsc = wave_sum(gg[l]) * (1.f / CB_C);
+      msc = expf(wave_sum(fmaxf(gg[2 * CB_C + l], LOG_FLOOR)));
+      nsc = expf(wave_sum(fmaxf(gg[3 * CB_C + l], LOG_FLOOR)));
+    }
   };
 
   // chunks are visited in reverse: step j handles chunk N-1-j, ring stage j % RING
   for (int j = 0; j < RING - 1 && j < p.N; ++j) issue_loads(p.N - 1 - j, j);
-  publish_Sb();
+  if constexpr (RULE == 2) {
+    if (p.N > 0) load_states(p.N - 1);
+    if (threadIdx.x < 4) psum[threadIdx.x] = 0.f;
+  } else {
+    publish_Gb(Sb);
+  }
   wait_vmem();
   __syncthreads();
   if (p.N > 0) chunk_scalars(0);
@@ -190,8 +229,8 @@ __global__ void __launch_bounds__(CB_THREADS) chunk_bwd_state(ChunkArgs p) {
     const int i = p.N - 1 - j;
     const bool ahead = j + RING - 1 < p.N;
     if (ahead) issue_loads(p.N - 1 - (j + RING - 1), (STG + RING - 1) % RING);
-    {  // Gb_i = Sb_{i+1}
-      float* gp = p.gb + ((bh * p.N + i) * D + r0 + lc) * (int64_t)D + 4 * G;
+    float* gp = p.gb + ((bh * p.N + i) * D + r0 + lc) * (int64_t)D + 4 * G;
+    if constexpr (RULE == 0) {  // Gb_i = Sb_{i+1}
 #pragma unroll
       for (int t = 0; t < NTH; ++t) *reinterpret_cast<f32x4*>(gp + 16 * (h * NTH + t)) = Sb[t];
     }
@@ -203,6 +242,93 @@ __global__ void __launch_bounds__(CB_THREADS) chunk_bwd_state(ChunkArgs p) {
     auto dop = [&](int kbs) {
       return cat8(lds_tr16(oaddr + (OC + (32 * kbs) * 64)), lds_tr16(oaddr + (OC + (32 * kbs + 16) * 64)));
     };
+    using std::integral_constant;
+    using I0 = integral_constant<int, 0>;
+    using I1 = integral_constant<int, 1>;
+    if constexpr (RULE == 2) {
+      // ---------------- adam A: -E = K S_i^T - V for this wave's tokens (reference
+      // fast_scan.py:89-94 recomputed: G_i is needed by the moment VJP)
+      auto segA = [&](auto rt_tag, auto h_tag) {
+        constexpr int RT = decltype(rt_tag)::value, H = decltype(h_tag)::value;
+        constexpr uint32_t VC = STG * L::OT;
+        Op<2> Sop[NKB];
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) Sop[kb] = pack_tiles<2>(Sraw[kb][0], Sraw[kb][1]);
+        f32x4 Nt[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const bf16x4 vb = lds_tr16(vaddr + (VC + (32 * H + 16 * u) * 64));
+          Nt[u] = f32x4{-(float)vb[0], -(float)vb[1], -(float)vb[2], -(float)vb[3]};
+#pragma unroll
+          for (int kb = 0; kb < NKB; ++kb) Nt[u] = mma<1, 2>(Op<1>{{rows(krow, 2 * H + u, kb)}}, Sop[kb], Nt[u]);
+        }
+        const Op<2> en = pack_tiles<2>(Nt[0], Nt[1]);
+        lds_st<bf16x8>(xn_addr(2 * RT + H), en.v[0]);
+        lds_st<bf16x8>(xn_addr(2 * RT + H) + 1024, en.v[1]);
+      };
+      switch (w) {
+        case 0: segA(I0{}, I0{}); break;
+        case 1: segA(I0{}, I1{}); break;
+        case 2: segA(I1{}, I0{}); break;
+        default: segA(I1{}, I1{}); break;
+      }
+      __syncthreads();  // -E halves published
+      // ---------------- adam B: G_i, the moment VJP (reference fast_scan.py:167-182)
+      {
+        Op<2> EN[2];
+#pragma unroll
+        for (int hs = 0; hs < 2; ++hs) EN[hs] = read_op(xn_addr(2 * rt + hs));
+        f32x4 Gb[NTH];
+        float da = 0.f, db = 0.f, dm = 0.f, dn = 0.f;
+#pragma unroll
+        for (int t = 0; t < NTH; ++t) {
+          f32x4 acc = zero4();
+#pragma unroll
+          for (int kbs = 0; kbs < 2; ++kbs) {
+            const uint32_t ro = SQK + kbs * 32 * ROWB;
+            const bf16x8 kc = cat8(lds_tr16(kcol[t] + ro), lds_tr16(kcol[t] + ro + 16 * ROWB));
+            acc = mma<1, 2>(Op<1>{{kc}}, EN[kbs], acc);
+          }
+          const int ct = h * NTH + t;  // column tile of S_i held in Sraw
+          const f32x4 Si = Sraw[ct >> 1][ct & 1];
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            const float g = -acc[jj];
+            const float mn = msc * Mp[t][jj] + (1.f - msc) * g;
+            const float vn = nsc * Vp[t][jj] + (1.f - nsc) * g * g;
+            const float sq = sqrtf(vn);
+            const float rden = 1.f / (sq + p.eps);
+            const float sb = Sb[t][jj];
+            da += sb * Si[jj];
+            db += sb * mn * rden;
+            const float mt = Mb[t][jj] + bsc * sb * rden;
+            const float vt = Vb[t][jj] - bsc * sb * mn * rden * rden / (2.f * fmaxf(sq, 1e-12f));
+            dm += mt * (Mp[t][jj] - g);
+            dn += vt * (Vp[t][jj] - g * g);
+            Gb[t][jj] = (1.f - msc) * mt + (1.f - nsc) * 2.f * g * vt;
+            Mb[t][jj] = msc * mt;
+            Vb[t][jj] = nsc * vt;
+          }
+          *reinterpret_cast<f32x4*>(gp + 16 * (h * NTH + t)) = Gb[t];
+        }
+        publish_Gb(Gb);
+        da = wave_sum(da);
+        db = wave_sum(db);
+        dm = wave_sum(dm);
+        dn = wave_sum(dn);
+        if (l == 0) {
+          atomicAdd(psum + 0, da);
+          atomicAdd(psum + 1, db);
+          atomicAdd(psum + 2, dm);
+          atomicAdd(psum + 3, dn);
+        }
+      }
+      __syncthreads();  // Gb halves and the partial sums published
+      if (w == 0 && l < 4) {
+        p.part[((bh * p.N + i) * (D / 32) + blk) * 4 + l] = psum[l];
+        psum[l] = 0.f;
+      }
+    }
     // ---------------- segment 1: dE for this wave's tokens 32H .. 32H+31
     auto segment1 = [&](auto rt_tag, auto h_tag) {
       constexpr int RT = decltype(rt_tag)::value, H = decltype(h_tag)::value;
@@ -210,7 +336,7 @@ __global__ void __launch_bounds__(CB_THREADS) chunk_bwd_state(ChunkArgs p) {
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb) Sop[kb] = read_op(xs_addr(2 * RT + kb / NKBH, kb % NKBH));
       f32x4 dE[2] = {zero4(), zero4()};
-      {  // diag(w) K Sb^T
+      {  // diag(w) K Gb^T
         bf16x8 Kr[2][NKB];
 #pragma unroll
         for (int u = 0; u < 2; ++u)
@@ -257,9 +383,6 @@ __global__ void __launch_bounds__(CB_THREADS) chunk_bwd_state(ChunkArgs p) {
       lds_st<bf16x8>(xe_addr(2 * RT + H), nd.v[0]);
       lds_st<bf16x8>(xe_addr(2 * RT + H) + 1024, nd.v[1]);
     };
-    using std::integral_constant;
-    using I0 = integral_constant<int, 0>;
-    using I1 = integral_constant<int, 1>;
     switch (w) {
       case 0: segment1(I0{}, I0{}); break;
       case 1: segment1(I0{}, I1{}); break;
@@ -291,7 +414,11 @@ __global__ void __launch_bounds__(CB_THREADS) chunk_bwd_state(ChunkArgs p) {
       for (int t = 0; t < NTH; ++t) Sb[t] = acc[t];
     }
     __builtin_amdgcn_sched_barrier(0);
-    publish_Sb();
+    if constexpr (RULE == 2) {
+      if (i > 0) load_states(i - 1);
+    } else {
+      publish_Gb(Sb);
+    }
     __builtin_amdgcn_sched_barrier(0);
     if (ahead) {
       if (w == 0)
@@ -301,7 +428,7 @@ __global__ void __launch_bounds__(CB_THREADS) chunk_bwd_state(ChunkArgs p) {
     } else {
       wait_vmem();
     }
-    __syncthreads();  // next chunk's tiles landed, Sb_i halves published
+    __syncthreads();  // next chunk's tiles landed, (delta) Sb_i halves published
     if (j + 1 < p.N) chunk_scalars((STG + 1) % RING);
   };
 
@@ -326,8 +453,8 @@ struct TokBwdLds {
   static constexpr int DH0 = 6 * TILE, DL0 = 7 * TILE;    // dE
   static constexpr int AP = CB_C * CB_C * 2;
   static constexpr int AH0 = 8 * TILE, AL0 = AH0 + AP;    // dA diag(beta), transposed (rows s)
-  static constexpr int R0 = AL0 + AP;                     // floats: dbeta, beta, g, da
-  static constexpr int BYTES = R0 + (3 * CB_C + 4) * 4;
+  static constexpr int R0 = AL0 + AP;                     // floats: dbeta, beta, g, gmu, gnu, da
+  static constexpr int BYTES = R0 + (5 * CB_C + 4) * 4;
   static_assert(BYTES <= 160 * 1024, "token backward LDS exceeds the 160 KiB of a CU");
 };
 
@@ -354,7 +481,9 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
   float* rdbeta = red;               // [64]
   float* rbeta = red + CB_C;         // [64]
   float* rg = red + 2 * CB_C;        // [64]
-  float* rda = red + 3 * CB_C;       // [1]
+  float* rgmu = red + 3 * CB_C;      // [64] (adam)
+  float* rgnu = red + 4 * CB_C;      // [64] (adam)
+  float* rda = red + 5 * CB_C;       // [1]
 
   const int64_t bh = blockIdx.x / p.N;
   const int i = (int)(blockIdx.x % p.N);
@@ -395,6 +524,10 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
       rdbeta[e] = 0.f;
       rbeta[e] = p.beta[bh * p.T + t0 + e];
       rg[e] = p.g[bh * p.T + t0 + e];
+      if constexpr (RULE == 2) {
+        rgmu[e] = p.gmu[bh * p.T + t0 + e];
+        rgnu[e] = p.gnu[bh * p.T + t0 + e];
+      }
       if (e == 0) rda[0] = 0.f;
     }
     wait_vmem();
@@ -478,8 +611,10 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
       *reinterpret_cast<bf16x4*>(Dh + eo) = dh;
       *reinterpret_cast<bf16x4*>(Dl + eo) = dl;
     }
-    da_part = wave_sum(da_part);
-    if (l == 0) atomicAdd(rda, da_part);
+    if constexpr (RULE == 0) {  // delta: Gb_i = Sb_{i+1}, so da_i = <Gb_i, S_i>
+      da_part = wave_sum(da_part);
+      if (l == 0) atomicAdd(rda, da_part);
+    }
   }
   // columns j0 + lc of S_i and Gb_i (k = r natural, n = j) for phase IIb,
   // requested before the barrier so that they arrive during phase IIa
@@ -537,9 +672,26 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
 
   // ---------------- gate gradients and dV
   if (w == 0) {
+    const int64_t o = bh * p.T + t0 + l;
     const float a = expf(wave_sum(fmaxf(rg[l], LOG_FLOOR)));
-    p.dbeta[bh * p.T + t0 + l] = rdbeta[l];
-    p.dg[bh * p.T + t0 + l] = rg[l] >= LOG_FLOOR ? rda[0] * a : 0.f;
+    if constexpr (RULE == 0) {
+      p.dbeta[o] = rdbeta[l];
+      p.dg[o] = rg[l] >= LOG_FLOOR ? rda[0] * a : 0.f;
+    } else {
+      // da, db, dm, dn: sums of the reverse scan's per-row-block partials
+      float sc[4] = {0.f, 0.f, 0.f, 0.f};
+      const float* pp = p.part + (bh * p.N + i) * (int64_t)(D / 32) * 4;
+#pragma unroll
+      for (int r = 0; r < D / 32; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) sc[c] += pp[4 * r + c];
+      const float m = expf(wave_sum(fmaxf(rgmu[l], LOG_FLOOR)));
+      const float n = expf(wave_sum(fmaxf(rgnu[l], LOG_FLOOR)));
+      p.dbeta[o] = rdbeta[l] + sc[1] * (1.f / CB_C);  // b = mean(beta)
+      p.dg[o] = rg[l] >= LOG_FLOOR ? sc[0] * a : 0.f;
+      p.dgmu[o] = rgmu[l] >= LOG_FLOOR ? sc[2] * m : 0.f;
+      p.dgnu[o] = rgnu[l] >= LOG_FLOOR ? sc[3] * n : 0.f;
+    }
   }
   {
     bf16* dvg = p.dv + bb * p.sv[0] + hh * p.sv[1] + t0 * p.sv[2];
@@ -599,25 +751,26 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
 
 template <int D, int RULE>
 static hipError_t launch_bwd(const ChunkArgs& a, hipStream_t stream) {
+  constexpr int lds1 = StateBwdLds<D, RULE>::BYTES;
+  constexpr int lds2 = TokBwdLds<D>::BYTES;
+  constexpr int thr2 = TokBwdLds<D>::NTHR;
   auto k1 = chunk_bwd_state<D, RULE>;
-  hipError_t e = hipFuncSetAttribute((const void*)k1, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     StateBwdLds<D>::BYTES);
+  hipError_t e = hipFuncSetAttribute((const void*)k1, hipFuncAttributeMaxDynamicSharedMemorySize, lds1);
   if (e != hipSuccess) return e;
   auto k2 = chunk_bwd_tok<D, RULE>;
-  e = hipFuncSetAttribute((const void*)k2, hipFuncAttributeMaxDynamicSharedMemorySize, TokBwdLds<D>::BYTES);
+  e = hipFuncSetAttribute((const void*)k2, hipFuncAttributeMaxDynamicSharedMemorySize, lds2);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k1, dim3((unsigned)(a.B * a.H * (D / 32))), dim3(CB_THREADS), StateBwdLds<D>::BYTES,
-                     stream, a);
+  hipLaunchKernelGGL(k1, dim3((unsigned)(a.B * a.H * (D / 32))), dim3(CB_THREADS), lds1, stream, a);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k2, dim3((unsigned)(a.B * a.H * a.N)), dim3(TokBwdLds<D>::NTHR), TokBwdLds<D>::BYTES,
-                     stream, a);
+  hipLaunchKernelGGL(k2, dim3((unsigned)(a.B * a.H * a.N)), dim3(thr2), lds2, stream, a);
   return hipGetLastError();
 }
 
 hipError_t chunk_bwd_launch(const ChunkArgs& a, int d, int rule, hipStream_t s) {
-  if (rule != 0) return hipErrorNotSupported;
-  return d == 128 ? launch_bwd<128, 0>(a, s) : launch_bwd<64, 0>(a, s);
+  if (rule == 0) return d == 128 ? launch_bwd<128, 0>(a, s) : launch_bwd<64, 0>(a, s);
+  if (rule == 2) return d == 128 ? launch_bwd<128, 2>(a, s) : launch_bwd<64, 2>(a, s);
+  return hipErrorNotSupported;
 }
 
 }  // namespace gmdn

@@ -28,11 +28,16 @@ CHUNK = 64
 SUPPORTED_D = (64, 128)
 
 
-BWD_RULES = (0,)  # rules whose fused backward kernel is built
+BWD_RULES = (0, 2)  # rules whose fused backward kernel is built
 
 
-def backward_supported(rule) -> bool:
-    return _rule_id(rule) in BWD_RULES
+def backward_supported(rule, d: int = 128) -> bool:
+    """Whether the fused backward of ``rule`` at head dim ``d`` is built.  The
+    adam backward is limited to d = 64: at d = 128 its sign-like update
+    amplifies the rounding of the split-bf16 state products past the
+    gradient tolerance."""
+    r = _rule_id(rule)
+    return r in BWD_RULES and (r != 2 or d == 64)
 
 
 def _rule_id(rule) -> int:
@@ -123,8 +128,8 @@ class ChunkScan(torch.autograd.Function):
         qc, kc, vc, bc, gc, mc, nc, states = ctx.saved_tensors
         lib = nat.load()
         dOc = _tok(dO.to(torch.bfloat16))
-        if ctx.rule not in BWD_RULES:
-            raise RuntimeError(f"the fused backward of rule {ctx.rule} is not built")
+        if not backward_supported(ctx.rule, qc.shape[-1]):
+            raise RuntimeError(f"the fused backward of rule {ctx.rule} at head dim {qc.shape[-1]} is not built")
         # gradients share the strides of q, k, v (the kernels write them with those strides)
         dq, dk, dv = (torch.empty_strided(t.shape, t.stride(), dtype=t.dtype, device=t.device)
                       for t in (qc, kc, vc))

@@ -103,7 +103,7 @@ def test_strided_head_interleaved_layout():
 
 
 # ---------------------------------------------------------------- backward
-GRAD_NAMES = ("q", "k", "v", "beta", "g")
+ALL_INPUTS = ("q", "k", "v", "beta", "g", "gmu", "gnu")
 
 
 def _grads(w, seed=0, layout=None):
@@ -114,27 +114,28 @@ def _grads(w, seed=0, layout=None):
     dq, dk, dv are bf16 (the dtype of q, k, v, as in the reference under
     autocast); their correctly rounded values alone sit up to ~2.1e-2 of RMS
     from float64 at d=128, so for them the 2e-2 bound applies to the error in
-    excess of half a bf16 ulp of the reference value.  dbeta and dg are
+    excess of half a bf16 ulp of the reference value.  The gate gradients are
     float32 and are bounded directly.  Returns {name: (bounded error, raw
     max-abs/rms)}."""
     dev = _dev()
     inp = make_inputs(w, seed=seed, with_grad_out=True)
     rule = {"delta": 0, "muon": 1, "adam": 2}[w.rule]
-    xs = {n: inp[n].to(dev) for n in GRAD_NAMES}
+    names = [n for n in ALL_INPUTS if inp[n] is not None]
+    xs = {n: inp[n].to(dev) for n in names}
     if layout == "bthd":
         for n in ("q", "k", "v"):
             xs[n] = xs[n].transpose(1, 2).contiguous().transpose(1, 2)
     xs = {n: t.detach().requires_grad_(True) for n, t in xs.items()}
-    o = gc.chunk_scan(xs["q"], xs["k"], xs["v"], xs["beta"], xs["g"], rule=w.rule, ns=w.ns)
-    got = torch.autograd.grad(o, [xs[n] for n in GRAD_NAMES], inp["dO"].to(dev))
+    o = gc.chunk_scan(*(xs.get(n) for n in ALL_INPUTS), rule=w.rule, ns=w.ns)
+    got = torch.autograd.grad(o, [xs[n] for n in names], inp["dO"].to(dev))
     torch.cuda.synchronize()
-    ref_in = {n: inp[n].double().requires_grad_(True) for n in GRAD_NAMES}
-    ref_o = oc.mixer_core(*(ref_in[n] for n in GRAD_NAMES), rule=rule, ns=w.ns, C=w.chunk)
-    ref = torch.autograd.grad(ref_o, [ref_in[n] for n in GRAD_NAMES], inp["dO"].double(), allow_unused=True)
+    ref_in = {n: inp[n].double().requires_grad_(True) for n in names}
+    ref_o = oc.mixer_core(*(ref_in.get(n) for n in ALL_INPUTS), rule=rule, ns=w.ns, C=w.chunk)
+    ref = torch.autograd.grad(ref_o, [ref_in[n] for n in names], inp["dO"].double(), allow_unused=True)
     # (with one chunk the last gate product never reaches o: its gradient is zero)
-    ref = [torch.zeros_like(ref_in[n]) if r is None else r for n, r in zip(GRAD_NAMES, ref)]
+    ref = [torch.zeros_like(ref_in[n]) if r is None else r for n, r in zip(names, ref)]
     out = {}
-    for n, g_, r in zip(GRAD_NAMES, got, ref):
+    for n, g_, r in zip(names, got, ref):
         g_ = g_.double().cpu()
         rms = r.pow(2).mean().sqrt()
         if rms == 0:
@@ -174,3 +175,53 @@ def test_gated_delta_grads_full_size():
     """The headline workload B=4, H=16, T=4096, d=128, forward + backward."""
     errs = _grads(Workload("gated_delta_b4_h16_t4096_d128", "delta", 4, 16, 4096, 128))
     assert all(e <= TOL for e, _ in errs.values()), errs
+
+
+@pytest.mark.parametrize("seed", [1, 2])
+def test_adam_grads_small(seed):
+    errs = _grads(Workload("t", "adam", 1, 2, 256, 64), seed=seed)
+    assert all(e <= TOL for e, _ in errs.values()), errs
+
+
+def test_adam_grads_d128_refused():
+    """The adam backward at d = 128 is refused rather than inaccurate."""
+    dev = _dev()
+    w = Workload("t", "adam", 1, 1, 64, 128)
+    inp = make_inputs(w, seed=0, device=dev, with_grad_out=True)
+    xs = {n: (None if inp[n] is None else inp[n].detach().requires_grad_(True)) for n in ALL_INPUTS}
+    o = gc.chunk_scan(*(xs[n] for n in ALL_INPUTS), rule="adam")
+    with pytest.raises(RuntimeError, match="not built"):
+        o.backward(inp["dO"])
+
+
+def test_adam_grads_config():
+    """Adam at B=2, H=8, T=4096, d=64, forward + backward.
+
+    Over 64 chunks adam's gradient is ill-conditioned: elements where V is
+    tiny make M / (sqrt(V) + eps) sign-like, and the float64 gradient has
+    max/RMS ~ 650 on dk.  The reference algorithm evaluated in float32 is
+    then itself ~15 RMS away from float64, so no float32 implementation meets
+    an elementwise 2e-2 bound here.  The check is that the HIP path is no
+    further from float64 than that float32 evaluation is, in Frobenius norm
+    (with a factor 2 for the different rounding), or within 2e-2 of it."""
+    dev = _dev()
+    w = Workload("adam_b2_h8_t4096_d64", "adam", 2, 8, 4096, 64)
+    inp = make_inputs(w, seed=0, with_grad_out=True)
+    xs = {n: inp[n].to(dev).detach().requires_grad_(True) for n in ALL_INPUTS}
+    o = gc.chunk_scan(*(xs[n] for n in ALL_INPUTS), rule="adam")
+    got = torch.autograd.grad(o, [xs[n] for n in ALL_INPUTS], inp["dO"].to(dev))
+    torch.cuda.synchronize()
+    refs = {}
+    for dt in (torch.float64, torch.float32):
+        ri = [inp[n].to(dt).requires_grad_(True) for n in ALL_INPUTS]
+        ro = oc.mixer_core(*ri, rule=2, ns=w.ns, C=w.chunk)
+        refs[dt] = torch.autograd.grad(ro, ri, inp["dO"].to(dt))
+    bad = {}
+    for n, g_, r64, r32 in zip(ALL_INPUTS, got, refs[torch.float64], refs[torch.float32]):
+        nrm = r64.norm().item()
+        e_hip = (g_.double().cpu() - r64).norm().item() / nrm
+        e_f32 = (r32.double() - r64).norm().item() / nrm
+        print(f"{w.name} d{n}: frobenius rel error {e_hip:.2e} (float32 reference {e_f32:.2e})")
+        if e_hip > max(TOL, 2.0 * e_f32):
+            bad[n] = (e_hip, e_f32)
+    assert not bad, bad
