@@ -16,19 +16,30 @@ transform A, Kw, Uv, Qt, Ov, the state scan, and ``o = Qt S^T + Ov``.
 * returns ``o`` (B, H, T, d) in q's dtype.
 
 Chunk length is 64 (the reference default and every configuration's).
+
+Delta and adam run as one fused HIP kernel per direction (forward: the
+chunk transform, the scan and the output; backward: a reverse scan of the
+state cotangent and a chunk-parallel token-gradient kernel).  Muon's msign
+couples the whole state, so its recurrence runs in the drop-in scan's muon
+kernel (Newton-Schulz fused into the scan step) with phases 1 and 3 as
+batched GEMMs around it.
 """
 from __future__ import annotations
+
+import math
 
 import torch
 
 from . import _native as nat
+from .scan import HipScan
 
 RULES = {"delta": 0, "muon": 1, "adam": 2}
 CHUNK = 64
+LOG_FLOOR = math.log(1e-6)
 SUPPORTED_D = (64, 128)
 
 
-BWD_RULES = (0, 2)  # rules whose fused backward kernel is built
+BWD_RULES = (0, 1, 2)  # rules with a backward (muon: through the scan kernel's VJP)
 
 
 def backward_supported(rule, d: int = 128) -> bool:
@@ -149,7 +160,41 @@ class ChunkScan(torch.autograd.Function):
         return (dq, dk, dv, *gates, None, None, None)
 
 
+def _muon_core(q, k, v, beta, g, gmu, ns):
+    """The muon rule's mixer core.  msign couples every entry of the d x d
+    state, so the recurrence runs as the drop-in scan's muon kernel (one
+    workgroup per (b, h), Newton-Schulz fused into the scan step); phases 1
+    and 3 of the reference mixer (train_ablation.py:150-167, :184-187) are
+    plain batched GEMMs in float32 around it.  Autograd supplies the
+    backward, through the scan kernel's fused msign VJP."""
+    B, H, T, d = q.shape
+    N = T // CHUNK
+    qf, kf, vf = (t.float().reshape(B, H, N, CHUNK, d) for t in (q, k, v))
+    bt = beta.float().reshape(B, H, N, CHUNK)
+    lg = torch.clamp(g.float(), min=LOG_FLOOR).reshape(B, H, N, CHUNK)
+    lmu = torch.clamp(gmu.float(), min=LOG_FLOOR).reshape(B, H, N, CHUNK)
+    a = lg.sum(-1).exp()
+    b = bt.mean(-1)
+    m = lmu.sum(-1).exp()
+    n = torch.ones_like(m)
+    # token weights prod_{s' > s} mu_{s'} (train_ablation.py:154-156)
+    w = torch.exp(torch.flip(torch.cumsum(torch.flip(lmu, [-1]), -1), [-1]) - lmu)
+    causal = torch.tril(torch.ones(CHUNK, CHUNK, dtype=torch.bool, device=q.device))
+    kT = kf.transpose(-1, -2).contiguous()
+    A = torch.where(causal, torch.matmul(qf, kT) * bt.unsqueeze(-2), 0.0)
+    Kw = torch.matmul((kf * w.unsqueeze(-1)).transpose(-1, -2).contiguous(), kf)
+    Uv = torch.matmul((vf * w.unsqueeze(-1)).transpose(-1, -2).contiguous(), kf)
+    Qt = qf - torch.matmul(A, kf)
+    Ov = torch.matmul(A, vf)
+    S_all = HipScan.apply(Uv, Kw, a, b, m, n, 1, ns)
+    o = torch.matmul(Qt, S_all.transpose(-1, -2).contiguous()) + Ov
+    return o.reshape(B, H, T, d).to(q.dtype)
+
+
 def chunk_scan(q, k, v, beta, g, gmu=None, gnu=None, *, rule="delta", ns: int = 3, eps: float = 1e-6):
     """Fused mixer core; see the module docstring."""
     r = _rule_id(rule)
+    if r == 1:
+        _check(q, k, v, beta, g, gmu, gnu, r)
+        return _muon_core(q, k, v, beta, g, gmu, ns)
     return ChunkScan.apply(q, k, v, beta, g, gmu if r >= 1 else None, gnu if r == 2 else None, r, ns, eps)

@@ -225,3 +225,23 @@ def test_adam_grads_config():
         if e_hip > max(TOL, 2.0 * e_f32):
             bad[n] = (e_hip, e_f32)
     assert not bad, bad
+
+
+# ---------------------------------------------------------------- muon
+def test_muon_forward_small():
+    err, _, excess = _forward(Workload("t", "muon", 1, 2, 256, 128, ns=5), seed=3)
+    assert err <= TOL
+
+
+def test_muon_forward_config():
+    """Muon at B=2, H=16, T=8192, d=128, ns=5.  Here the bf16 rounding of the
+    exact output alone is 2.5e-2 of RMS, so the bound applies to the error
+    in excess of half a bf16 ulp."""
+    _, _, excess = _forward(Workload("muon_b2_h16_t8192_d128", "muon", 2, 16, 8192, 128, ns=5))
+    assert excess <= TOL
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_muon_grads_small(d):
+    errs = _grads(Workload("t", "muon", 1, 2, 256, d, ns=5), seed=2)
+    assert all(e <= TOL for e, _ in errs.values()), errs
