@@ -30,14 +30,25 @@
 
 namespace gmdn {
 
+// Roles.  The forward runs 8 waves per workgroup, two per SIMD: four state
+// waves carry the recurrence (E, then G and the state update) and four
+// output waves everything that hangs off it (the A tiles, o = Q S^T + A E,
+// the o stores, the chunk's gate scalars and all LDS-DMA traffic), so the
+// serial chain of each chunk holds only the recurrence's own products.
+// Per chunk i:
+//   state : [X_i] S_i^T operands, -E (token half h) -> XE   [Y_i]  G, update, S_{i+1} halves -> XS  [X_{i+1}]
+//   output: [X_i] DMA chunk i+2, gate scalars, S_i^T operands,
+//                 -A tiles -> A planes                     [Y_i]  o_i = Q S^T + A E, staged through
+//                                                                 the chunk's (now dead) V slot, stored  [X_{i+1}]
+constexpr int FW_WAVES = 8;
+constexpr int FW_THREADS = 64 * FW_WAVES;
+
 // LDS carve-up of the forward kernel (bytes)
 // Chunk tiles (Q, K, the workgroup's 32 columns of V, and the gate chunk)
-// live in a ring of FWD_STAGES LDS buffers filled by LDS-DMA FWD_STAGES - 1
-// chunks ahead, so HBM latency is covered by that many chunks of work.  The
-// chunk loop is unrolled over the ring, so every LDS read address is a
-// per-lane base register (computed once) plus an immediate offset.
-constexpr int FWD_STAGES = RING;
-
+// live in a ring of RING LDS buffers filled by LDS-DMA RING - 1 chunks
+// ahead, so HBM latency is covered by that many chunks of work.  The chunk
+// loop is unrolled over the ring, so every LDS read address is a per-lane
+// base register (computed once) plus an immediate offset.
 template <int D>
 struct FwdLds {
   static constexpr int NKBH = D / 64;            // k-blocks in a column half
@@ -45,21 +56,23 @@ struct FwdLds {
   static constexpr int VT = CB_C * 32 * 2;       // the workgroup's V columns
   static constexpr int GT = 4 * CB_C * 4;        // beta, g, gmu, gnu
   static constexpr int Q0 = 0;
-  static constexpr int K0 = Q0 + FWD_STAGES * TILE;
-  static constexpr int V0 = K0 + FWD_STAGES * TILE;
-  static constexpr int G0 = V0 + FWD_STAGES * VT;
-  static constexpr int A0 = G0 + FWD_STAGES * GT;  // -A hi plane, then lo plane
+  static constexpr int K0 = Q0 + RING * TILE;
+  static constexpr int V0 = K0 + RING * TILE;
+  static constexpr int G0 = V0 + RING * VT;
+  static constexpr int A0 = G0 + RING * GT;        // -A hi plane, then lo plane
   static constexpr int AP = CB_C * CB_C * 2;
   static constexpr int XS0 = A0 + 2 * AP;          // S^T operand exchange
   static constexpr int XE0 = XS0 + CB_WAVES * NKBH * 2 * 1024;  // E operand exchange
-  static constexpr int BYTES = XE0 + CB_WAVES * 2 * 2 * 1024;
+  static constexpr int SC0 = XE0 + CB_WAVES * 2 * 2 * 1024;  // chunk scalars a, b, m, n per stage
+  static constexpr int BYTES = SC0 + RING * 16;
   static_assert(BYTES <= 160 * 1024, "forward LDS exceeds the 160 KiB of a CU");
-  // LDS-DMA instructions one wave issues per chunk (Q, K, V; wave 0 also the gates)
+  // LDS-DMA instructions one output wave issues per chunk (Q, K, V; the
+  // first output wave also the gates)
   static constexpr int DMA_OPS = 2 * (CB_C * D / 8) / CB_THREADS + (CB_C * 32 / 8) / CB_THREADS;
 };
 
 template <int D, int RULE>
-__global__ void __launch_bounds__(CB_THREADS) chunk_fwd(ChunkArgs p) {
+__global__ void __launch_bounds__(FW_THREADS) chunk_fwd(ChunkArgs p) {
   using LQ = BSwz<D>;
   using LV = BSwz<32>;
   using LA = BSwz<CB_C>;
@@ -76,8 +89,10 @@ __global__ void __launch_bounds__(CB_THREADS) chunk_fwd(ChunkArgs p) {
   int blk;
   map_block(p.B * p.H, D / 32, bh, blk);
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const bool state_wave = w < CB_WAVES;
+  const int sw = w & (CB_WAVES - 1);  // index within the role
   const int l = lane_id(), G = l >> 4, lc = l & 15;
-  const int rt = w >> 1, h = w & 1;
+  const int rt = sw >> 1, h = sw & 1;
   const int r0 = 32 * blk + 16 * rt;  // first state row of this wave
   const int64_t bb = bh / p.H, hh = bh % p.H;
   const bf16* qg = p.q + bb * p.sq[0] + hh * p.sq[1];
@@ -103,9 +118,9 @@ __global__ void __launch_bounds__(CB_THREADS) chunk_fwd(ChunkArgs p) {
 #pragma unroll
   for (int t = 0; t < NTH; ++t) coloff[t] = swz_off<LQ>(4 * G + (lc >> 2), 16 * (h * NTH + t) + 4 * (lc & 3));
   // transposing reads of V (rows 32h + 16u + 4G + lc/4, columns 16 rt + 4 (lc & 3))
-  // (the row part 32h + 16u is added as an immediate in segment 1: whole
-  // multiples of 4 rows leave the swizzle term unchanged; the column part
-  // 16 rt is not additive under the XOR and stays in the base)
+  // (the row part 32h + 16u is added as an immediate: whole multiples of 4
+  // rows leave the swizzle term unchanged; the column part 16 rt is not
+  // additive under the XOR and stays in the base)
   const uint32_t voff = swz_off<LV>(4 * G + (lc >> 2), 16 * rt + 4 * (lc & 3));
   // row reads of -A (rows 16 tt + lc, tt = 2h + u; columns 32 kbs + 16 hf + 4G)
   uint32_t aoff[2][2];
@@ -139,7 +154,7 @@ __global__ void __launch_bounds__(CB_THREADS) chunk_fwd(ChunkArgs p) {
   const lds_ptr xeaddr = L0 + (xoff + L::XE0);
 
   // the strictly-upper tiles of -A are never written: zero them once
-  for (int e = threadIdx.x; e < CB_C * CB_C; e += CB_THREADS) {
+  for (int e = threadIdx.x; e < CB_C * CB_C; e += FW_THREADS) {
     const int r = e / CB_C, c = e % CB_C;
     if ((c >> 4) > (r >> 4)) {
       Ahi[LA::off(r, c)] = (bf16)0.f;
@@ -147,43 +162,34 @@ __global__ void __launch_bounds__(CB_THREADS) chunk_fwd(ChunkArgs p) {
     }
   }
 
+  // LDS-DMA: issued by the output waves only (index sw among them)
   DmaPlan<LQ, CB_C, CB_THREADS> dq, dk;
   DmaPlan<LV, CB_C, CB_THREADS> dv;
-  dq.init(w, p.sq[2]);
-  dk.init(w, p.sk[2]);
-  dv.init(w, p.sv[2]);
+  dq.init(sw, p.sq[2]);
+  dk.init(sw, p.sk[2]);
+  dv.init(sw, p.sv[2]);
   auto issue_loads = [&](int i, int stg) {
     const int64_t t0 = (int64_t)i * CB_C;
-    dq.issue(qg + t0 * p.sq[2], lds0 + L::Q0 + stg * L::TILE, w);
-    dk.issue(kg + t0 * p.sk[2], lds0 + L::K0 + stg * L::TILE, w);
-    dv.issue(vg + t0 * p.sv[2], lds0 + L::V0 + stg * L::VT, w);
-    if (w == 0) lds_dma16(gsrc + t0, smem + L::G0 + stg * L::GT);
+    dq.issue(qg + t0 * p.sq[2], lds0 + L::Q0 + stg * L::TILE, sw);
+    dk.issue(kg + t0 * p.sk[2], lds0 + L::K0 + stg * L::TILE, sw);
+    dv.issue(vg + t0 * p.sv[2], lds0 + L::V0 + stg * L::VT, sw);
+    if (sw == 0) lds_dma16(gsrc + t0, smem + L::G0 + stg * L::GT);
   };
 
+  // state waves: S (and adam's M, V) for row r0 + lc, columns of half h
   f32x4 S[NTH], Mm[NTH], Vv[NTH];
 #pragma unroll
   for (int t = 0; t < NTH; ++t) S[t] = Mm[t] = Vv[t] = zero4();
-  // o of a chunk is stored at the start of the next one, so that the wait for
-  // the next chunk's tiles (vmcnt counts stores too on gfx9) does not also
-  // wait for this chunk's stores to be acknowledged.
-  f32x4 O[2] = {zero4(), zero4()};
-  auto store_o = [&](int i) {
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      bf16* op = og + ((int64_t)i * CB_C + 16 * (2 * h + u) + 4 * G) * p.so[2];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) op[j * p.so[2]] = (bf16)O[u][j];
-    }
-  };
-  // exchange slot (16 bytes per lane) of wave ww, piece k
+  f32x4 O[2] = {zero4(), zero4()};  // output waves: o tiles of the chunk
+  // exchange slot (16 bytes per lane) of state wave ww, piece k
   auto xs_addr = [&](int ww, int k) { return xsaddr + ((ww * NKBH + k) * 2) * 1024; };
   auto xe_addr = [&](int ww, int k) { return xeaddr + ((ww * 2 + k) * 2) * 1024; };
   auto publish_S = [&]() {
 #pragma unroll
     for (int kbl = 0; kbl < NKBH; ++kbl) {
       const Op<2> x = pack_tiles<2>(S[2 * kbl], S[2 * kbl + 1]);
-      lds_st<bf16x8>(xs_addr(w, kbl), x.v[0]);
-      lds_st<bf16x8>(xs_addr(w, kbl) + 1024, x.v[1]);
+      lds_st<bf16x8>(xs_addr(sw, kbl), x.v[0]);
+      lds_st<bf16x8>(xs_addr(sw, kbl) + 1024, x.v[1]);
     }
   };
   auto read_op = [&](lds_cptr addr) {
@@ -192,32 +198,50 @@ __global__ void __launch_bounds__(CB_THREADS) chunk_fwd(ChunkArgs p) {
     x.v[1] = lds_ld<bf16x8>(addr + 1024);
     return x;
   };
-  float a = 0.f, bsc = 0.f, msc = 0.f, nsc = 0.f;
+  // chunk scalars a = exp(sum max(g, log 1e-6)), and for adam b = mean(beta),
+  // m, n: reduced by one output wave into the stage's scalar slot
+  float* const scal = reinterpret_cast<float*>(smem + L::SC0);
   auto chunk_scalars = [&](int stg) {
     const float* gg = reinterpret_cast<const float*>(smem + L::G0 + stg * L::GT);
-    a = expf(wave_sum(fmaxf(gg[CB_C + l], LOG_FLOOR)));
+    const float a = expf(wave_sum(fmaxf(gg[CB_C + l], LOG_FLOOR)));
+    float bs = 0.f, ms = 0.f, ns = 0.f;
     if constexpr (RULE == 2) {
-      bsc = wave_sum(gg[l]) * (1.f / CB_C);
-      msc = expf(wave_sum(fmaxf(gg[2 * CB_C + l], LOG_FLOOR)));
-      nsc = expf(wave_sum(fmaxf(gg[3 * CB_C + l], LOG_FLOOR)));
+      bs = wave_sum(gg[l]) * (1.f / CB_C);
+      ms = expf(wave_sum(fmaxf(gg[2 * CB_C + l], LOG_FLOOR)));
+      ns = expf(wave_sum(fmaxf(gg[3 * CB_C + l], LOG_FLOOR)));
     }
+    if (l == 0) *reinterpret_cast<f32x4*>(scal + 4 * stg) = f32x4{a, bs, ms, ns};
   };
 
-  for (int j = 0; j < FWD_STAGES - 1 && j < p.N; ++j) issue_loads(j, j);
-  publish_S();
-  wait_vmem();
+  if (state_wave) {
+    publish_S();
+  } else {
+    for (int j = 0; j < RING - 1 && j < p.N; ++j) issue_loads(j, j);
+    wait_vmem();
+  }
   __syncthreads();  // X_0
-  if (p.N > 0) chunk_scalars(0);
 
-  // One chunk; STG = i % FWD_STAGES is a compile-time constant.
-  auto chunk = [&](auto stg_tag, int i) {
+  // One chunk of each role; STG = i % RING is a compile-time constant.  The
+  // roles run separate loops (so that the register allocator never holds
+  // one role's loop state in the other's) with the same barrier sequence.
+  auto state_chunk = [&](auto stg_tag, int i) {
     constexpr int STG = decltype(stg_tag)::value;
     constexpr uint32_t SQK = STG * L::TILE;  // stage offsets within the regions
     constexpr uint32_t VC = STG * L::VT;
     const float* gates = reinterpret_cast<const float*>(smem + L::G0 + STG * L::GT);
-    if (i > 0) store_o(i - 1);
-    const bool ahead = i + FWD_STAGES - 1 < p.N;
-    if (ahead) issue_loads(i + FWD_STAGES - 1, (STG + FWD_STAGES - 1) % FWD_STAGES);
+    const bool ahead = i + RING - 1 < p.N;
+    // k-block kb of row tile `rowtile` (a compile-time offset from the base set)
+    auto rows = [&](const lds_cptr (&base)[NKB][2], int rowtile, int kb) {
+      return cat8(lds_ld<bf16x4>(base[kb][0] + SQK + rowtile * 16 * ROWB),
+                  lds_ld<bf16x4>(base[kb][1] + SQK + rowtile * 16 * ROWB));
+    };
+    using std::integral_constant;
+    using I0 = integral_constant<int, 0>;
+    using I1 = integral_constant<int, 1>;
+    using I2 = integral_constant<int, 2>;
+    using I3 = integral_constant<int, 3>;
+    Op<2> Sop[NKB];  // S_i^T operands of every k-block (rows of this row tile)
+    // ================= state, before Y_i: -E for this wave's tokens
     if (p.states) {  // pre-update state (and adam's moments) for the backward
       const int64_t plane = p.B * p.H * p.N * (int64_t)D * D;
       float* sp = p.states + ((bh * p.N + i) * D + r0 + lc) * (int64_t)D + 4 * G;
@@ -230,191 +254,198 @@ __global__ void __launch_bounds__(CB_THREADS) chunk_fwd(ChunkArgs p) {
         }
       }
     }
+    auto segE = [&](auto rt_tag, auto h_tag) {
+      constexpr int RT = decltype(rt_tag)::value, H = decltype(h_tag)::value;
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) Sop[kb] = read_op(xs_addr(2 * RT + kb / NKBH, kb % NKBH));
+      // N = K S^T - V = -E for this wave's tokens 32H .. 32H+31 (two chains)
+      f32x4 Nt[2];
+      bf16x8 Kr[2][NKB];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const bf16x4 vb = lds_tr16(vaddr + (VC + (32 * H + 16 * u) * 64));
+        Nt[u] = f32x4{-(float)vb[0], -(float)vb[1], -(float)vb[2], -(float)vb[3]};
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) Kr[u][kb] = rows(krowa, 2 * H + u, kb);
+      }
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) Nt[u] = mma<1, 2>(Op<1>{{Kr[u][kb]}}, Sop[kb], Nt[u]);
+      // publish the E operands: N (for A E) and -w N (for G), w per token row
+      const f32x4 b0 = *reinterpret_cast<const f32x4*>(gates + 32 * H + 4 * G);
+      const f32x4 b1 = *reinterpret_cast<const f32x4*>(gates + 32 * H + 16 + 4 * G);
+      const f32x4 w0 = RULE == 0 ? -b0 : f32x4{-1.f, -1.f, -1.f, -1.f};
+      const f32x4 w1 = RULE == 0 ? -b1 : f32x4{-1.f, -1.f, -1.f, -1.f};
+      const Op<2> en = pack_tiles<2>(Nt[0], Nt[1]);
+      const Op<2> we = pack_tiles<2>(Nt[0] * w0, Nt[1] * w1);
+      lds_st<bf16x8>(xe_addr(2 * RT + H, 0), en.v[0]);
+      lds_st<bf16x8>(xe_addr(2 * RT + H, 0) + 1024, en.v[1]);
+      lds_st<bf16x8>(xe_addr(2 * RT + H, 1), we.v[0]);
+      lds_st<bf16x8>(xe_addr(2 * RT + H, 1) + 1024, we.v[1]);
+    };
+    switch (sw) {
+      case 0: segE(I0{}, I0{}); break;
+      case 1: segE(I0{}, I1{}); break;
+      case 2: segE(I1{}, I0{}); break;
+      default: segE(I1{}, I1{}); break;
+    }
+    __syncthreads();  // Y_i: E halves and -A published
+    // ================= state, after Y_i: G^T for this wave's column half, update
+    Op<2> WE[2];
+#pragma unroll
+    for (int hs = 0; hs < 2; ++hs) WE[hs] = read_op(xe_addr(2 * rt + hs, 1));
+    bf16x8 Kcol[NTH][2];
+#pragma unroll
+    for (int t = 0; t < NTH; ++t)
+#pragma unroll
+      for (int kbs = 0; kbs < 2; ++kbs) {
+        Kcol[t][kbs] = cat8(lds_tr16(colp[t] + SQK + kbs * 32 * ROWB),
+                            lds_tr16(colp[t] + SQK + kbs * 32 * ROWB + 16 * ROWB));
+      }
+    const f32x4 sc = *reinterpret_cast<const f32x4*>(scal + 4 * STG);
+    const float a = sc[0], bsc = sc[1], msc = sc[2], nsc = sc[3];
+    f32x4 acc[NTH];
+#pragma unroll
+    for (int t = 0; t < NTH; ++t) acc[t] = RULE == 0 ? a * S[t] : zero4();
+#pragma unroll
+    for (int kbs = 0; kbs < 2; ++kbs)
+#pragma unroll
+      for (int t = 0; t < NTH; ++t) acc[t] = mma<1, 2>(Op<1>{{Kcol[t][kbs]}}, WE[kbs], acc[t]);
+#pragma unroll
+    for (int t = 0; t < NTH; ++t) {
+      if constexpr (RULE == 0) {
+        S[t] = acc[t];
+      } else {
+        Mm[t] = msc * Mm[t] + (1.f - msc) * acc[t];
+        Vv[t] = nsc * Vv[t] + (1.f - nsc) * acc[t] * acc[t];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) S[t][j] = a * S[t][j] + bsc * Mm[t][j] / (sqrtf(Vv[t][j]) + p.eps);
+      }
+    }
+    publish_S();  // S_{i+1}^T half, read after X_{i+1}
+    __syncthreads();  // X_{i+1}: next chunk's tiles landed, S_{i+1} halves published
+  };
+  auto output_chunk = [&](auto stg_tag, int i) {
+    constexpr int STG = decltype(stg_tag)::value;
+    constexpr uint32_t SQK = STG * L::TILE;  // stage offsets within the regions
+    constexpr uint32_t VC = STG * L::VT;
+    const float* gates = reinterpret_cast<const float*>(smem + L::G0 + STG * L::GT);
+    const bool ahead = i + RING - 1 < p.N;
     // k-block kb of row tile `rowtile` (a compile-time offset from the base set)
     auto rows = [&](const lds_cptr (&base)[NKB][2], int rowtile, int kb) {
       return cat8(lds_ld<bf16x4>(base[kb][0] + SQK + rowtile * 16 * ROWB),
                   lds_ld<bf16x4>(base[kb][1] + SQK + rowtile * 16 * ROWB));
-    };
-    // ================= segment 1 (specialised per wave: RT, H compile-time)
-    auto segment1 = [&](auto rt_tag, auto h_tag, auto tiles) {
-      constexpr int RT = decltype(rt_tag)::value, H = decltype(h_tag)::value;
-      // S_i^T operand of every k-block, from the slot of the wave owning it
-      // (row tile rt, column half kb / NKBH)
-      Op<2> Sop[NKB];
-  #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) Sop[kb] = read_op(xs_addr(2 * RT + kb / NKBH, kb % NKBH));
-      // N = K S^T - V = -E for this wave's tokens 32h .. 32h+31 (two chains)
-      f32x4 Nt[2];
-      {
-        bf16x8 Kr[2][NKB];
-  #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const bf16x4 vb = lds_tr16(vaddr + (VC + (32 * H + 16 * u) * 64));
-          Nt[u] = f32x4{-(float)vb[0], -(float)vb[1], -(float)vb[2], -(float)vb[3]};
-  #pragma unroll
-          for (int kb = 0; kb < NKB; ++kb) Kr[u][kb] = rows(krowa, 2 * H + u, kb);
-        }
-  #pragma unroll
-        for (int kb = 0; kb < NKB; ++kb)
-  #pragma unroll
-          for (int u = 0; u < 2; ++u) Nt[u] = mma<1, 2>(Op<1>{{Kr[u][kb]}}, Sop[kb], Nt[u]);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      // o = Q S^T for this wave's tokens (two chains)
-      {
-        bf16x8 Qr[2][NKB];
-  #pragma unroll
-        for (int u = 0; u < 2; ++u)
-  #pragma unroll
-          for (int kb = 0; kb < NKB; ++kb) Qr[u][kb] = rows(qrow, 2 * H + u, kb);
-        O[0] = O[1] = zero4();
-  #pragma unroll
-        for (int kb = 0; kb < NKB; ++kb)
-  #pragma unroll
-          for (int u = 0; u < 2; ++u) O[u] = mma<1, 2>(Op<1>{{Qr[u][kb]}}, Sop[kb], O[u]);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      // publish the E operands: N (for A E) and -w N (for G), w per token row
-      {
-        const f32x4 b0 = *reinterpret_cast<const f32x4*>(gates + 32 * H + 4 * G);
-        const f32x4 b1 = *reinterpret_cast<const f32x4*>(gates + 32 * H + 16 + 4 * G);
-        const f32x4 w0 = RULE == 0 ? -b0 : f32x4{-1.f, -1.f, -1.f, -1.f};
-        const f32x4 w1 = RULE == 0 ? -b1 : f32x4{-1.f, -1.f, -1.f, -1.f};
-        const Op<2> en = pack_tiles<2>(Nt[0], Nt[1]);
-        const Op<2> we = pack_tiles<2>(Nt[0] * w0, Nt[1] * w1);
-        lds_st<bf16x8>(xe_addr(2 * RT + H, 0), en.v[0]);
-        lds_st<bf16x8>(xe_addr(2 * RT + H, 0) + 1024, en.v[1]);
-        lds_st<bf16x8>(xe_addr(2 * RT + H, 1), we.v[0]);
-        lds_st<bf16x8>(xe_addr(2 * RT + H, 1) + 1024, we.v[1]);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      // this wave's tiles of -A^T = -(K Q^T) diag(beta), restricted to s <= t.
-      // Tile idx = w + 4k of the causal list; the switch makes st, tt constant.
-      auto a_tile = [&](auto st_tag, auto tt_tag) {
-        constexpr int st = decltype(st_tag)::value, tt = decltype(tt_tag)::value;
-        bf16x8 ka[NKB], qa[NKB];
-  #pragma unroll
-        for (int kb = 0; kb < NKB; ++kb) {
-          ka[kb] = rows(krowa, st, kb);
-          qa[kb] = rows(qrow, tt, kb);
-        }
-        f32x4 acc = zero4();
-  #pragma unroll
-        for (int kb = 0; kb < NKB; ++kb) acc = mfma(ka[kb], qa[kb], acc);
-        // lane (t, G) holds (Q K^T)[t][s] for s = 16 st + 4G + j
-        const f32x4 bs = *reinterpret_cast<const f32x4*>(gates + 16 * st + 4 * G);
-        bf16x4 hi4, lo4;
-  #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float val = (st < tt || 4 * G + j <= lc) ? -acc[j] * bs[j] : 0.f;
-          bf16 hv, lv;
-          split2(val, hv, lv);
-          hi4[j] = hv;
-          lo4[j] = lv;
-        }
-        const int ao = LA::off(16 * tt + lc, 16 * st + 4 * G);
-        *reinterpret_cast<bf16x4*>(Ahi + ao) = hi4;
-        *reinterpret_cast<bf16x4*>(Alo + ao) = lo4;
-        __builtin_amdgcn_sched_barrier(0);
-      };
-      tiles(a_tile);
     };
     using std::integral_constant;
     using I0 = integral_constant<int, 0>;
     using I1 = integral_constant<int, 1>;
     using I2 = integral_constant<int, 2>;
     using I3 = integral_constant<int, 3>;
-    // causal tiles (st, tt) of -A per wave: w0 {00 12 23}, w1 {01 22 33}, w2 {11 03}, w3 {02 13}
-    switch (w) {
-      case 0:
-        segment1(I0{}, I0{}, [&](auto&& f) { f(I0{}, I0{}); f(I1{}, I2{}); f(I2{}, I3{}); });
-        break;
-      case 1:
-        segment1(I0{}, I1{}, [&](auto&& f) { f(I0{}, I1{}); f(I2{}, I2{}); f(I3{}, I3{}); });
-        break;
-      case 2:
-        segment1(I1{}, I0{}, [&](auto&& f) { f(I1{}, I1{}); f(I0{}, I3{}); });
-        break;
-      default:
-        segment1(I1{}, I1{}, [&](auto&& f) { f(I0{}, I2{}); f(I1{}, I3{}); });
-        break;
+    Op<2> Sop[NKB];  // S_i^T operands of every k-block (rows of this row tile)
+    // ================= output, before Y_i: DMA, gate scalars, S^T operands, -A tiles
+    if (ahead) issue_loads(i + RING - 1, (STG + RING - 1) % RING);
+    if (sw == 0) chunk_scalars(STG);
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) Sop[kb] = read_op(xs_addr(2 * rt + kb / NKBH, kb % NKBH));
+    // this wave's tiles of -A^T = -(K Q^T) diag(beta), restricted to s <= t
+    auto a_tile = [&](auto st_tag, auto tt_tag) {
+      constexpr int st = decltype(st_tag)::value, tt = decltype(tt_tag)::value;
+      bf16x8 ka[NKB], qa[NKB];
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+        ka[kb] = rows(krowa, st, kb);
+        qa[kb] = rows(qrow, tt, kb);
+      }
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) acc = mfma(ka[kb], qa[kb], acc);
+      // lane (t, G) holds (Q K^T)[t][s] for s = 16 st + 4G + j
+      const f32x4 bs = *reinterpret_cast<const f32x4*>(gates + 16 * st + 4 * G);
+      bf16x4 hi4, lo4;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float val = (st < tt || 4 * G + j <= lc) ? -acc[j] * bs[j] : 0.f;
+        bf16 hv, lv;
+        split2(val, hv, lv);
+        hi4[j] = hv;
+        lo4[j] = lv;
+      }
+      const int ao = LA::off(16 * tt + lc, 16 * st + 4 * G);
+      *reinterpret_cast<bf16x4*>(Ahi + ao) = hi4;
+      *reinterpret_cast<bf16x4*>(Alo + ao) = lo4;
+    };
+    // causal tiles (st, tt) of -A per output wave: {00 12 23}, {01 22 33}, {11 03}, {02 13}
+    switch (sw) {
+      case 0: a_tile(I0{}, I0{}); a_tile(I1{}, I2{}); a_tile(I2{}, I3{}); break;
+      case 1: a_tile(I0{}, I1{}); a_tile(I2{}, I2{}); a_tile(I3{}, I3{}); break;
+      case 2: a_tile(I1{}, I1{}); a_tile(I0{}, I3{}); break;
+      default: a_tile(I0{}, I2{}); a_tile(I1{}, I3{}); break;
     }
     __syncthreads();  // Y_i: E halves and -A published
-    // ================= segment 2
-    // E operands of both token halves (slots of waves (rt, 0) and (rt, 1))
-    Op<2> EN[2], WE[2];
+    // ================= output, after Y_i: o = Q S^T + (-A)(-E) for this wave's tokens
+    Op<2> EN[2];
 #pragma unroll
-    for (int hs = 0; hs < 2; ++hs) {
-      EN[hs] = read_op(xe_addr(2 * rt + hs, 0));
-      WE[hs] = read_op(xe_addr(2 * rt + hs, 1));
-    }
-    // G^T for this wave's column half (NTH chains) and the state update
+    for (int kbs = 0; kbs < 2; ++kbs) EN[kbs] = read_op(xe_addr(2 * rt + kbs, 0));
+    auto outp = [&](auto h_tag) {
+      constexpr int H = decltype(h_tag)::value;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        O[u] = zero4();
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) O[u] = mma<1, 2>(Op<1>{{rows(qrow, 2 * H + u, kb)}}, Sop[kb], O[u]);
+#pragma unroll
+        for (int kbs = 0; kbs <= H; ++kbs) {
+          auto arow = [&](uint32_t plane) {
+            return cat8(lds_ld<bf16x4>(ap[kbs][0] + (plane + u * 16 * CB_C * 2)),
+                        lds_ld<bf16x4>(ap[kbs][1] + (plane + u * 16 * CB_C * 2)));
+          };
+          O[u] = mma<2, 2>(Op<2>{{arow(0), arow(L::AP)}}, EN[kbs], O[u]);
+        }
+      }
+    };
+    if (h == 0)
+      outp(I0{});
+    else
+      outp(I1{});
+    // o for tokens 32h .. 32h+31, columns r0 .. r0+15: staged through this
+    // wave's 1 KiB of the chunk's V slot (read only before Y_i, refilled
+    // only after X_{i+1}) and stored as one 16-byte piece per lane
     {
-      bf16x8 Kcol[NTH][2];
+      bf16* stage = reinterpret_cast<bf16*>(smem + L::V0 + STG * L::VT) + sw * 512;
 #pragma unroll
-      for (int t = 0; t < NTH; ++t)
+      for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int kbs = 0; kbs < 2; ++kbs) {
-          Kcol[t][kbs] = cat8(lds_tr16(colp[t] + SQK + kbs * 32 * ROWB),
-                              lds_tr16(colp[t] + SQK + kbs * 32 * ROWB + 16 * ROWB));
-        }
-      f32x4 acc[NTH];
-#pragma unroll
-      for (int t = 0; t < NTH; ++t) acc[t] = RULE == 0 ? a * S[t] : zero4();
-#pragma unroll
-      for (int kbs = 0; kbs < 2; ++kbs)
-#pragma unroll
-        for (int t = 0; t < NTH; ++t) acc[t] = mma<1, 2>(Op<1>{{Kcol[t][kbs]}}, WE[kbs], acc[t]);
-#pragma unroll
-      for (int t = 0; t < NTH; ++t) {
-        if constexpr (RULE == 0) {
-          S[t] = acc[t];
-        } else {
-          Mm[t] = msc * Mm[t] + (1.f - msc) * acc[t];
-          Vv[t] = nsc * Vv[t] + (1.f - nsc) * acc[t] * acc[t];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) S[t][j] = a * S[t][j] + bsc * Mm[t][j] / (sqrtf(Vv[t][j]) + p.eps);
-        }
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    publish_S();  // S_{i+1}^T half, read after X_{i+1}
-    __builtin_amdgcn_sched_barrier(0);
-    // o += (-A)(-E) over the causal token blocks kbs <= h
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-#pragma unroll
-      for (int kbs = 0; kbs < 2; ++kbs) {
-        if (kbs > h) continue;
-        auto arow = [&](uint32_t plane) {
-          return cat8(lds_ld<bf16x4>(ap[kbs][0] + (plane + u * 16 * CB_C * 2)),
-                      lds_ld<bf16x4>(ap[kbs][1] + (plane + u * 16 * CB_C * 2)));
-        };
-        O[u] = mma<2, 2>(Op<2>{{arow(0), arow(L::AP)}}, EN[kbs], O[u]);
-      }
+        for (int j = 0; j < 4; ++j) stage[(16 * u + 4 * G + j) * 16 + lc] = (bf16)O[u][j];
+      const int tok = l >> 1, half = l & 1;  // lanes: 32 tokens x 2 pieces of 8 columns
+      const bf16x8 piece = *reinterpret_cast<const bf16x8*>(stage + tok * 16 + 8 * half);
+      *reinterpret_cast<bf16x8*>(og - lc + ((int64_t)i * CB_C + 32 * h + tok) * p.so[2] + 8 * half) = piece;
     }
     // chunk i+1's tiles must have landed; the loads issued after them (for
-    // chunk i+FWD_STAGES-1) may stay in flight.  Vector loads complete in
-    // issue order, so vmcnt <= (loads issued since) suffices; stores only
-    // make the count more conservative.
+    // chunk i+RING-1, and this chunk's one o store) may stay in flight.
+    // Vector memory operations complete in issue order for this count:
+    // vmcnt <= (operations issued since) suffices.
     if (ahead) {
-      if (w == 0)
-        wait_vmem_le<L::DMA_OPS + 1>();
+      if (sw == 0)
+        wait_vmem_le<L::DMA_OPS + 2>();
       else
-        wait_vmem_le<L::DMA_OPS>();
+        wait_vmem_le<L::DMA_OPS + 1>();
     } else {
       wait_vmem();
     }
     __syncthreads();  // X_{i+1}: next chunk's tiles landed, S_{i+1} halves published
-    if (i + 1 < p.N) chunk_scalars((STG + 1) % FWD_STAGES);
   };
-
-  for (int i = 0; i < p.N; i += FWD_STAGES) {
-    chunk(std::integral_constant<int, 0>{}, i);
-    if (i + 1 < p.N) chunk(std::integral_constant<int, 1>{}, i + 1);
-    if (i + 2 < p.N) chunk(std::integral_constant<int, 2>{}, i + 2);
-  }
-  if (p.N > 0) store_o(p.N - 1);
+  auto run = [&](auto&& chunk) {
+    for (int i = 0; i < p.N; i += RING) {
+      chunk(std::integral_constant<int, 0>{}, i);
+      if (i + 1 < p.N) chunk(std::integral_constant<int, 1>{}, i + 1);
+      if (i + 2 < p.N) chunk(std::integral_constant<int, 2>{}, i + 2);
+    }
+  };
+  if (state_wave)
+    run(state_chunk);
+  else
+    run(output_chunk);
 }
 
 template <int D, int RULE>
@@ -424,7 +455,7 @@ static hipError_t launch_fwd(const ChunkArgs& a, hipStream_t stream) {
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   if (e != hipSuccess) return e;
   const int64_t grid = a.B * a.H * (D / 32);
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(CB_THREADS), lds, stream, a);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(FW_THREADS), lds, stream, a);
   return hipGetLastError();
 }
 
@@ -506,6 +537,8 @@ int gmdn_chunk_fwd(const gmdn_chunk_desc* desc, const void* q, const void* k, co
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(beta) || !aligned16(g) ||
       (gmu && !aligned16(gmu)) || (gnu && !aligned16(gnu)))
     return GMDN_ERR_UNSUPPORTED;
+  // o is written in 16-byte pieces along d
+  if (!aligned16(o) || (desc->so[0] & 7) || (desc->so[1] & 7) || (desc->so[2] & 7)) return GMDN_ERR_UNSUPPORTED;
   if (desc->rule == 1) return GMDN_ERR_UNSUPPORTED;
   const ChunkArgs a = make_args(desc, q, k, v, beta, g, gmu, gnu, o, states);
   hipStream_t s = (hipStream_t)stream;

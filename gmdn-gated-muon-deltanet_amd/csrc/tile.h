@@ -241,10 +241,28 @@ GMDN_DEV void wait_vmem_le() {
 }
 
 // ------------------------------------------------------------ reductions
+// DPP move of a float within the wave (CTRL: quad_perm 0x00-0xff, row_ror:n
+// 0x120 + n); every lane must be active.
+template <int CTRL>
+GMDN_DEV float dpp_mov(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over the 64 lanes, wave-uniform result: two quad-permute and two
+// row-rotate steps leave every lane of a 16-lane row holding the row's sum,
+// then the four row sums are read into scalar registers.  No LDS traffic
+// (a shuffle-based reduction costs six dependent LDS permutes).
 GMDN_DEV float wave_sum(float x) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
-  return x;
+  x += dpp_mov<0xB1>(x);   // quad_perm [1,0,3,2]
+  x += dpp_mov<0x4E>(x);   // quad_perm [2,3,0,1]
+  x += dpp_mov<0x124>(x);  // row_ror:4
+  x += dpp_mov<0x128>(x);  // row_ror:8
+  const int xi = __builtin_bit_cast(int, x);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 48));
+  return (r0 + r1) + (r2 + r3);
 }
 
 // Sum over the 4 lane groups (G) of a value held per lane: result equal in
