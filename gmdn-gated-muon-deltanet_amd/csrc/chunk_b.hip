@@ -61,9 +61,11 @@ struct FwdLds {
   static constexpr int G0 = V0 + RING * VT;
   static constexpr int A0 = G0 + RING * GT;        // -A hi plane, then lo plane
   static constexpr int AP = CB_C * CB_C * 2;
-  static constexpr int XS0 = A0 + 2 * AP;          // S^T operand exchange
-  static constexpr int XE0 = XS0 + CB_WAVES * NKBH * 2 * 1024;  // E operand exchange
-  static constexpr int SC0 = XE0 + CB_WAVES * 2 * 2 * 1024;  // chunk scalars a, b, m, n per stage
+  static constexpr int XSP = 32 * D * 2;          // S exchange: [32 rows][D] bf16, hi plane then lo
+  static constexpr int XS0 = A0 + 2 * AP;
+  static constexpr int XEP = 32 * CB_C * 2;        // E exchange: [32 rows][64 tokens] bf16 planes
+  static constexpr int XE0 = XS0 + 2 * XSP;        // N hi, N lo, -wN hi, -wN lo
+  static constexpr int SC0 = XE0 + 4 * XEP;        // chunk scalars a, b, m, n per stage
   static constexpr int BYTES = SC0 + RING * 16;
   static_assert(BYTES <= 160 * 1024, "forward LDS exceeds the 160 KiB of a CU");
   // LDS-DMA instructions one output wave issues per chunk (Q, K, V; the
@@ -106,52 +108,64 @@ __global__ void __launch_bounds__(FW_THREADS) chunk_fwd(ChunkArgs p) {
                       bh * p.T + 4 * lc;
 
   // ---- per-lane LDS byte offsets (stage, row-tile and k offsets are immediates)
-  // row reads of Q / K: lane (r, G) reads row r of a 16-row tile at columns
-  // k0 + 4G (half 0) and k0 + 16 + 4G (half 1), k0 = 32 kb
-  uint32_t rowoff[NKB][2];
+  // Every MFMA operand is read in natural k order: lane (m, G) takes
+  // X[m][k0 + 8G .. k0 + 8G + 7] in one 16-byte read, or (column operands)
+  // X[k0 + 8G .. k0 + 8G + 7][c] in two transposing reads.  The exchanges
+  // between waves are row-major matrices in LDS, so no operand needs a
+  // register shuffle.
+  using LX = BSwz<CB_C>;  // E exchange planes (64 token columns)
+  uint32_t rowb[NKB];     // row lc of a 16-row tile, columns 32 kb + 8G
 #pragma unroll
-  for (int kb = 0; kb < NKB; ++kb)
+  for (int kb = 0; kb < NKB; ++kb) rowb[kb] = swz_off<LQ>(lc, 32 * kb + 8 * G);
+  // transposing reads of K columns 16 ct + i for this wave's column tiles:
+  // rows 8G + lc/4 (first read) and 8G + 4 + lc/4 (second)
+  uint32_t kc0[NTH], kc1[NTH];
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf) rowoff[kb][hf] = swz_off<LQ>(lc, 32 * kb + 16 * hf + 4 * G);
-  // transposing reads of K columns 16 ct .. for this wave's column tiles
-  uint32_t coloff[NTH];
-#pragma unroll
-  for (int t = 0; t < NTH; ++t) coloff[t] = swz_off<LQ>(4 * G + (lc >> 2), 16 * (h * NTH + t) + 4 * (lc & 3));
+  for (int t = 0; t < NTH; ++t) {
+    kc0[t] = swz_off<LQ>(8 * G + (lc >> 2), 16 * (h * NTH + t) + 4 * (lc & 3));
+    kc1[t] = swz_off<LQ>(8 * G + 4 + (lc >> 2), 16 * (h * NTH + t) + 4 * (lc & 3));
+  }
   // transposing reads of V (rows 32h + 16u + 4G + lc/4, columns 16 rt + 4 (lc & 3))
   // (the row part 32h + 16u is added as an immediate: whole multiples of 4
   // rows leave the swizzle term unchanged; the column part 16 rt is not
   // additive under the XOR and stays in the base)
   const uint32_t voff = swz_off<LV>(4 * G + (lc >> 2), 16 * rt + 4 * (lc & 3));
-  // row reads of -A (rows 16 tt + lc, tt = 2h + u; columns 32 kbs + 16 hf + 4G)
-  uint32_t aoff[2][2];
+  // row reads of -A (rows 32h + 16u + lc, columns 32 kbs + 8G)
+  uint32_t aoff[2];
 #pragma unroll
-  for (int kbs = 0; kbs < 2; ++kbs)
+  for (int kbs = 0; kbs < 2; ++kbs) aoff[kbs] = swz_off<LA>(32 * h + lc, 32 * kbs + 8 * G);
+  // S exchange: this state wave writes row 16 rt + lc, columns 16 (h NTH + t) + 4G
+  uint32_t xsw[NTH];
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf) aoff[kbs][hf] = swz_off<LA>(32 * h + lc, 32 * kbs + 16 * hf + 4 * G);
-  const uint32_t xoff = 16 * l;  // exchange slots: one 16-byte piece per lane
+  for (int t = 0; t < NTH; ++t) xsw[t] = swz_off<LQ>(16 * rt + lc, 16 * (h * NTH + t) + 4 * G);
+  // E exchange: row 16 rt + lc; written at tokens 32h + 16u + 4G, read at 32 kbs + 8G
+  uint32_t xew[2], xer[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    xew[u] = swz_off<LX>(16 * rt + lc, 32 * h + 16 * u + 4 * G);
+    xer[u] = swz_off<LX>(16 * rt + lc, 32 * u + 8 * G);
+  }
   // LDS pointers, one set per region, so that the stage, row-tile and k
   // offsets added inside the loop stay within the 16-bit immediate
   const uint32_t lds0 = lds_addr(smem);
   const lds_ptr L0 = lds_base(smem);
-  lds_cptr qrow[NKB][2], krowa[NKB][2];
+  lds_cptr qrow[NKB], krow[NKB], xsr[NKB];
 #pragma unroll
-  for (int kb = 0; kb < NKB; ++kb)
+  for (int kb = 0; kb < NKB; ++kb) {
+    qrow[kb] = L0 + (rowb[kb] + L::Q0);
+    krow[kb] = L0 + (rowb[kb] + L::K0);
+    xsr[kb] = L0 + (rowb[kb] + L::XS0);
+  }
+  lds_cptr kcol0[NTH], kcol1[NTH];
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
-      qrow[kb][hf] = L0 + (rowoff[kb][hf] + L::Q0);
-      krowa[kb][hf] = L0 + (rowoff[kb][hf] + L::K0);
-    }
-  lds_cptr colp[NTH];
-#pragma unroll
-  for (int t = 0; t < NTH; ++t) colp[t] = L0 + (coloff[t] + L::K0);
+  for (int t = 0; t < NTH; ++t) {
+    kcol0[t] = L0 + (kc0[t] + L::K0);
+    kcol1[t] = L0 + (kc1[t] + L::K0);
+  }
   const lds_cptr vaddr = L0 + (voff + L::V0);
-  lds_cptr ap[2][2];
+  lds_cptr ap[2];
 #pragma unroll
-  for (int kbs = 0; kbs < 2; ++kbs)
-#pragma unroll
-    for (int hf = 0; hf < 2; ++hf) ap[kbs][hf] = L0 + (aoff[kbs][hf] + L::A0);
-  const lds_ptr xsaddr = L0 + (xoff + L::XS0);
-  const lds_ptr xeaddr = L0 + (xoff + L::XE0);
+  for (int kbs = 0; kbs < 2; ++kbs) ap[kbs] = L0 + (aoff[kbs] + L::A0);
 
   // the strictly-upper tiles of -A are never written: zero them once
   for (int e = threadIdx.x; e < CB_C * CB_C; e += FW_THREADS) {
@@ -181,21 +195,29 @@ __global__ void __launch_bounds__(FW_THREADS) chunk_fwd(ChunkArgs p) {
 #pragma unroll
   for (int t = 0; t < NTH; ++t) S[t] = Mm[t] = Vv[t] = zero4();
   f32x4 O[2] = {zero4(), zero4()};  // output waves: o tiles of the chunk
-  // exchange slot (16 bytes per lane) of state wave ww, piece k
-  auto xs_addr = [&](int ww, int k) { return xsaddr + ((ww * NKBH + k) * 2) * 1024; };
-  auto xe_addr = [&](int ww, int k) { return xeaddr + ((ww * 2 + k) * 2) * 1024; };
+  // split a D-layout tile into hi / lo bf16 and store both 8-byte pieces
+  auto put_split = [&](uint32_t off, uint32_t plane, const f32x4& x) {
+    bf16x4 hi, lo;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      bf16 a_, b_;
+      split2(x[j], a_, b_);
+      hi[j] = a_;
+      lo[j] = b_;
+    }
+    lds_st<bf16x4>(L0 + off, hi);
+    lds_st<bf16x4>(L0 + (off + plane), lo);
+  };
+  // S_{i+1}^T half of this state wave -> the S exchange (row-major, split)
   auto publish_S = [&]() {
 #pragma unroll
-    for (int kbl = 0; kbl < NKBH; ++kbl) {
-      const Op<2> x = pack_tiles<2>(S[2 * kbl], S[2 * kbl + 1]);
-      lds_st<bf16x8>(xs_addr(sw, kbl), x.v[0]);
-      lds_st<bf16x8>(xs_addr(sw, kbl) + 1024, x.v[1]);
-    }
+    for (int t = 0; t < NTH; ++t) put_split(xsw[t] + L::XS0, L::XSP, S[t]);
   };
-  auto read_op = [&](lds_cptr addr) {
+  // split operand at a base pointer: hi plane, lo plane `plane` bytes later
+  auto read_op = [&](lds_cptr addr, uint32_t plane) {
     Op<2> x;
     x.v[0] = lds_ld<bf16x8>(addr);
-    x.v[1] = lds_ld<bf16x8>(addr + 1024);
+    x.v[1] = lds_ld<bf16x8>(addr + plane);
     return x;
   };
   // chunk scalars a = exp(sum max(g, log 1e-6)), and for adam b = mean(beta),
@@ -230,11 +252,6 @@ __global__ void __launch_bounds__(FW_THREADS) chunk_fwd(ChunkArgs p) {
     constexpr uint32_t VC = STG * L::VT;
     const float* gates = reinterpret_cast<const float*>(smem + L::G0 + STG * L::GT);
     const bool ahead = i + RING - 1 < p.N;
-    // k-block kb of row tile `rowtile` (a compile-time offset from the base set)
-    auto rows = [&](const lds_cptr (&base)[NKB][2], int rowtile, int kb) {
-      return cat8(lds_ld<bf16x4>(base[kb][0] + SQK + rowtile * 16 * ROWB),
-                  lds_ld<bf16x4>(base[kb][1] + SQK + rowtile * 16 * ROWB));
-    };
     using std::integral_constant;
     using I0 = integral_constant<int, 0>;
     using I1 = integral_constant<int, 1>;
@@ -257,7 +274,7 @@ __global__ void __launch_bounds__(FW_THREADS) chunk_fwd(ChunkArgs p) {
     auto segE = [&](auto rt_tag, auto h_tag) {
       constexpr int RT = decltype(rt_tag)::value, H = decltype(h_tag)::value;
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) Sop[kb] = read_op(xs_addr(2 * RT + kb / NKBH, kb % NKBH));
+      for (int kb = 0; kb < NKB; ++kb) Sop[kb] = read_op(xsr[kb] + RT * 16 * ROWB, L::XSP);
       // N = K S^T - V = -E for this wave's tokens 32H .. 32H+31 (two chains)
       f32x4 Nt[2];
       bf16x8 Kr[2][NKB];
@@ -266,23 +283,20 @@ __global__ void __launch_bounds__(FW_THREADS) chunk_fwd(ChunkArgs p) {
         const bf16x4 vb = lds_tr16(vaddr + (VC + (32 * H + 16 * u) * 64));
         Nt[u] = f32x4{-(float)vb[0], -(float)vb[1], -(float)vb[2], -(float)vb[3]};
 #pragma unroll
-        for (int kb = 0; kb < NKB; ++kb) Kr[u][kb] = rows(krowa, 2 * H + u, kb);
+        for (int kb = 0; kb < NKB; ++kb) Kr[u][kb] = lds_ld<bf16x8>(krow[kb] + SQK + (2 * H + u) * 16 * ROWB);
       }
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
         for (int u = 0; u < 2; ++u) Nt[u] = mma<1, 2>(Op<1>{{Kr[u][kb]}}, Sop[kb], Nt[u]);
       // publish the E operands: N (for A E) and -w N (for G), w per token row
-      const f32x4 b0 = *reinterpret_cast<const f32x4*>(gates + 32 * H + 4 * G);
-      const f32x4 b1 = *reinterpret_cast<const f32x4*>(gates + 32 * H + 16 + 4 * G);
-      const f32x4 w0 = RULE == 0 ? -b0 : f32x4{-1.f, -1.f, -1.f, -1.f};
-      const f32x4 w1 = RULE == 0 ? -b1 : f32x4{-1.f, -1.f, -1.f, -1.f};
-      const Op<2> en = pack_tiles<2>(Nt[0], Nt[1]);
-      const Op<2> we = pack_tiles<2>(Nt[0] * w0, Nt[1] * w1);
-      lds_st<bf16x8>(xe_addr(2 * RT + H, 0), en.v[0]);
-      lds_st<bf16x8>(xe_addr(2 * RT + H, 0) + 1024, en.v[1]);
-      lds_st<bf16x8>(xe_addr(2 * RT + H, 1), we.v[0]);
-      lds_st<bf16x8>(xe_addr(2 * RT + H, 1) + 1024, we.v[1]);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const f32x4 bt = *reinterpret_cast<const f32x4*>(gates + 32 * H + 16 * u + 4 * G);
+        const f32x4 wt = RULE == 0 ? -bt : f32x4{-1.f, -1.f, -1.f, -1.f};
+        put_split(xew[u] + L::XE0, L::XEP, Nt[u]);
+        put_split(xew[u] + L::XE0 + 2 * L::XEP, L::XEP, Nt[u] * wt);
+      }
     };
     switch (sw) {
       case 0: segE(I0{}, I0{}); break;
@@ -294,14 +308,13 @@ __global__ void __launch_bounds__(FW_THREADS) chunk_fwd(ChunkArgs p) {
     // ================= state, after Y_i: G^T for this wave's column half, update
     Op<2> WE[2];
 #pragma unroll
-    for (int hs = 0; hs < 2; ++hs) WE[hs] = read_op(xe_addr(2 * rt + hs, 1));
+    for (int kbs = 0; kbs < 2; ++kbs) WE[kbs] = read_op(L0 + (xer[kbs] + L::XE0 + 2 * L::XEP), L::XEP);
     bf16x8 Kcol[NTH][2];
 #pragma unroll
     for (int t = 0; t < NTH; ++t)
 #pragma unroll
       for (int kbs = 0; kbs < 2; ++kbs) {
-        Kcol[t][kbs] = cat8(lds_tr16(colp[t] + SQK + kbs * 32 * ROWB),
-                            lds_tr16(colp[t] + SQK + kbs * 32 * ROWB + 16 * ROWB));
+        Kcol[t][kbs] = cat8(lds_tr16(kcol0[t] + SQK + kbs * 32 * ROWB), lds_tr16(kcol1[t] + SQK + kbs * 32 * ROWB));
       }
     const f32x4 sc = *reinterpret_cast<const f32x4*>(scal + 4 * STG);
     const float a = sc[0], bsc = sc[1], msc = sc[2], nsc = sc[3];
@@ -332,11 +345,6 @@ __global__ void __launch_bounds__(FW_THREADS) chunk_fwd(ChunkArgs p) {
     constexpr uint32_t VC = STG * L::VT;
     const float* gates = reinterpret_cast<const float*>(smem + L::G0 + STG * L::GT);
     const bool ahead = i + RING - 1 < p.N;
-    // k-block kb of row tile `rowtile` (a compile-time offset from the base set)
-    auto rows = [&](const lds_cptr (&base)[NKB][2], int rowtile, int kb) {
-      return cat8(lds_ld<bf16x4>(base[kb][0] + SQK + rowtile * 16 * ROWB),
-                  lds_ld<bf16x4>(base[kb][1] + SQK + rowtile * 16 * ROWB));
-    };
     using std::integral_constant;
     using I0 = integral_constant<int, 0>;
     using I1 = integral_constant<int, 1>;
@@ -347,15 +355,15 @@ __global__ void __launch_bounds__(FW_THREADS) chunk_fwd(ChunkArgs p) {
     if (ahead) issue_loads(i + RING - 1, (STG + RING - 1) % RING);
     if (sw == 0) chunk_scalars(STG);
 #pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) Sop[kb] = read_op(xs_addr(2 * rt + kb / NKBH, kb % NKBH));
+    for (int kb = 0; kb < NKB; ++kb) Sop[kb] = read_op(xsr[kb] + rt * 16 * ROWB, L::XSP);
     // this wave's tiles of -A^T = -(K Q^T) diag(beta), restricted to s <= t
     auto a_tile = [&](auto st_tag, auto tt_tag) {
       constexpr int st = decltype(st_tag)::value, tt = decltype(tt_tag)::value;
       bf16x8 ka[NKB], qa[NKB];
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb) {
-        ka[kb] = rows(krowa, st, kb);
-        qa[kb] = rows(qrow, tt, kb);
+        ka[kb] = lds_ld<bf16x8>(krow[kb] + SQK + st * 16 * ROWB);
+        qa[kb] = lds_ld<bf16x8>(qrow[kb] + SQK + tt * 16 * ROWB);
       }
       f32x4 acc = zero4();
 #pragma unroll
@@ -386,22 +394,18 @@ __global__ void __launch_bounds__(FW_THREADS) chunk_fwd(ChunkArgs p) {
     // ================= output, after Y_i: o = Q S^T + (-A)(-E) for this wave's tokens
     Op<2> EN[2];
 #pragma unroll
-    for (int kbs = 0; kbs < 2; ++kbs) EN[kbs] = read_op(xe_addr(2 * rt + kbs, 0));
+    for (int kbs = 0; kbs < 2; ++kbs) EN[kbs] = read_op(L0 + (xer[kbs] + L::XE0), L::XEP);
     auto outp = [&](auto h_tag) {
       constexpr int H = decltype(h_tag)::value;
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         O[u] = zero4();
 #pragma unroll
-        for (int kb = 0; kb < NKB; ++kb) O[u] = mma<1, 2>(Op<1>{{rows(qrow, 2 * H + u, kb)}}, Sop[kb], O[u]);
+        for (int kb = 0; kb < NKB; ++kb)
+          O[u] = mma<1, 2>(Op<1>{{lds_ld<bf16x8>(qrow[kb] + SQK + (2 * H + u) * 16 * ROWB)}}, Sop[kb], O[u]);
 #pragma unroll
-        for (int kbs = 0; kbs <= H; ++kbs) {
-          auto arow = [&](uint32_t plane) {
-            return cat8(lds_ld<bf16x4>(ap[kbs][0] + (plane + u * 16 * CB_C * 2)),
-                        lds_ld<bf16x4>(ap[kbs][1] + (plane + u * 16 * CB_C * 2)));
-          };
-          O[u] = mma<2, 2>(Op<2>{{arow(0), arow(L::AP)}}, EN[kbs], O[u]);
-        }
+        for (int kbs = 0; kbs <= H; ++kbs)
+          O[u] = mma<2, 2>(read_op(ap[kbs] + u * 16 * CB_C * 2, L::AP), EN[kbs], O[u]);
       }
     };
     if (h == 0)
