@@ -243,6 +243,37 @@ __global__ void __launch_bounds__(FW_THREADS) chunk_fwd(ChunkArgs p) {
   }
   __syncthreads();  // X_0
 
+  // one tile of -A^T = -(K Q^T) diag(beta), restricted to s <= t
+  auto a_tile = [&](auto stg_tag, auto st_tag, auto tt_tag) {
+    constexpr int STG = decltype(stg_tag)::value;
+    constexpr uint32_t SQK = STG * L::TILE;
+    const float* gates = reinterpret_cast<const float*>(smem + L::G0 + STG * L::GT);
+    constexpr int st = decltype(st_tag)::value, tt = decltype(tt_tag)::value;
+    bf16x8 ka[NKB], qa[NKB];
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      ka[kb] = lds_ld<bf16x8>(krow[kb] + SQK + st * 16 * ROWB);
+      qa[kb] = lds_ld<bf16x8>(qrow[kb] + SQK + tt * 16 * ROWB);
+    }
+    f32x4 acc = zero4();
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) acc = mfma(ka[kb], qa[kb], acc);
+    // lane (t, G) holds (Q K^T)[t][s] for s = 16 st + 4G + j
+    const f32x4 bs = *reinterpret_cast<const f32x4*>(gates + 16 * st + 4 * G);
+    bf16x4 hi4, lo4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float val = (st < tt || 4 * G + j <= lc) ? -acc[j] * bs[j] : 0.f;
+      bf16 hv, lv;
+      split2(val, hv, lv);
+      hi4[j] = hv;
+      lo4[j] = lv;
+    }
+    const int ao = LA::off(16 * tt + lc, 16 * st + 4 * G);
+    *reinterpret_cast<bf16x4*>(Ahi + ao) = hi4;
+    *reinterpret_cast<bf16x4*>(Alo + ao) = lo4;
+  };
+
   // One chunk of each role; STG = i % RING is a compile-time constant.  The
   // roles run separate loops (so that the register allocator never holds
   // one role's loop state in the other's) with the same barrier sequence.
@@ -299,10 +330,10 @@ __global__ void __launch_bounds__(FW_THREADS) chunk_fwd(ChunkArgs p) {
       }
     };
     switch (sw) {
-      case 0: segE(I0{}, I0{}); break;
-      case 1: segE(I0{}, I1{}); break;
-      case 2: segE(I1{}, I0{}); break;
-      default: segE(I1{}, I1{}); break;
+      case 0: segE(I0{}, I0{}); a_tile(stg_tag, I0{}, I0{}); break;
+      case 1: segE(I0{}, I1{}); a_tile(stg_tag, I1{}, I1{}); break;
+      case 2: segE(I1{}, I0{}); a_tile(stg_tag, I2{}, I2{}); break;
+      default: segE(I1{}, I1{}); a_tile(stg_tag, I3{}, I3{}); break;
     }
     __syncthreads();  // Y_i: E halves and -A published
     // ================= state, after Y_i: G^T for this wave's column half, update
@@ -353,42 +384,16 @@ __global__ void __launch_bounds__(FW_THREADS) chunk_fwd(ChunkArgs p) {
     Op<2> Sop[NKB];  // S_i^T operands of every k-block (rows of this row tile)
     // ================= output, before Y_i: DMA, gate scalars, S^T operands, -A tiles
     if (ahead) issue_loads(i + RING - 1, (STG + RING - 1) % RING);
-    if (sw == 0) chunk_scalars(STG);
+    if (sw == 3) chunk_scalars(STG);
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) Sop[kb] = read_op(xsr[kb] + rt * 16 * ROWB, L::XSP);
-    // this wave's tiles of -A^T = -(K Q^T) diag(beta), restricted to s <= t
-    auto a_tile = [&](auto st_tag, auto tt_tag) {
-      constexpr int st = decltype(st_tag)::value, tt = decltype(tt_tag)::value;
-      bf16x8 ka[NKB], qa[NKB];
-#pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) {
-        ka[kb] = lds_ld<bf16x8>(krow[kb] + SQK + st * 16 * ROWB);
-        qa[kb] = lds_ld<bf16x8>(qrow[kb] + SQK + tt * 16 * ROWB);
-      }
-      f32x4 acc = zero4();
-#pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) acc = mfma(ka[kb], qa[kb], acc);
-      // lane (t, G) holds (Q K^T)[t][s] for s = 16 st + 4G + j
-      const f32x4 bs = *reinterpret_cast<const f32x4*>(gates + 16 * st + 4 * G);
-      bf16x4 hi4, lo4;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float val = (st < tt || 4 * G + j <= lc) ? -acc[j] * bs[j] : 0.f;
-        bf16 hv, lv;
-        split2(val, hv, lv);
-        hi4[j] = hv;
-        lo4[j] = lv;
-      }
-      const int ao = LA::off(16 * tt + lc, 16 * st + 4 * G);
-      *reinterpret_cast<bf16x4*>(Ahi + ao) = hi4;
-      *reinterpret_cast<bf16x4*>(Alo + ao) = lo4;
-    };
-    // causal tiles (st, tt) of -A per output wave: {00 12 23}, {01 22 33}, {11 03}, {02 13}
+    // causal tiles (st, tt) of -A: the diagonal ones go to the state waves,
+    // the rest to the output waves: {01 02}, {03 12}, {13}, {23}
     switch (sw) {
-      case 0: a_tile(I0{}, I0{}); a_tile(I1{}, I2{}); a_tile(I2{}, I3{}); break;
-      case 1: a_tile(I0{}, I1{}); a_tile(I2{}, I2{}); a_tile(I3{}, I3{}); break;
-      case 2: a_tile(I1{}, I1{}); a_tile(I0{}, I3{}); break;
-      default: a_tile(I0{}, I2{}); a_tile(I1{}, I3{}); break;
+      case 0: a_tile(stg_tag, I0{}, I1{}); a_tile(stg_tag, I0{}, I2{}); break;
+      case 1: a_tile(stg_tag, I0{}, I3{}); a_tile(stg_tag, I1{}, I2{}); break;
+      case 2: a_tile(stg_tag, I1{}, I3{}); break;
+      default: a_tile(stg_tag, I2{}, I3{}); break;
     }
     __syncthreads();  // Y_i: E halves and -A published
     // ================= output, after Y_i: o = Q S^T + (-A)(-E) for this wave's tokens
