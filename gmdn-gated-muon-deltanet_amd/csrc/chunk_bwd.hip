@@ -48,16 +48,6 @@ GMDN_DEV bf16x8 col8(const bf16* X, int k0, int c0) {
   return cat8(__builtin_bit_cast(bf16x4, a), __builtin_bit_cast(bf16x4, b));
 }
 
-// lane (i, G) takes X[k0 + pair(G, j)][c0 + i] (pair order: rows 4G.., 16+4G..)
-template <class L>
-GMDN_DEV bf16x8 col8_pair(const bf16* X, int k0, int c0) {
-  const int l = lane_id(), i = l & 15, G = l >> 4;
-  const int rr = k0 + 4 * G + (i >> 2), cc = c0 + 4 * (i & 3);
-  const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(X + L::off(rr, cc)));
-  const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(X + L::off(rr + 16, cc)));
-  return cat8(__builtin_bit_cast(bf16x4, a), __builtin_bit_cast(bf16x4, b));
-}
-
 GMDN_DEV float dot4(const f32x4& a, const f32x4& b) {
   return a[0] * b[0] + a[1] * b[1] + a[2] * b[2] + a[3] * b[3];
 }
@@ -534,32 +524,39 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
     __syncthreads();
   }
 
-  // ---------------- phase I: E^T, (Gb K^T) and dE^T for this wave's 16 state rows
-  {
-    // B-side operands of A = tril(Q K^T) diag(beta): (k = t in pair order, n = s),
-    // one per (s tile, 32-token block) that is not entirely above the diagonal
-    Op<2> Aop[4][2];
+  // ---------------- phase I': A^T = (tril(Q K^T) diag(beta))^T, split, into the
+  // dA planes (free until phase IIa): tile (tt, st), k = 4 tt + st, goes to
+  // wave k % NW; tiles above the diagonal are written as zeros
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
+  for (int kk = 0; kk < 16 / NW; ++kk) {
+    const int k = w + NW * kk, tt = k >> 2, st = k & 3;
+    bf16x4 ah, al;
+    if (tt < st) {
+      ah = al = bf16x4{(bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f};
+    } else {
+      f32x4 X = zero4();
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb)
+        X = mfma(row8<LQ>(Qs, 16 * tt + lc, 32 * kb), row8<LQ>(Ks, 16 * st + lc, 32 * kb), X);
+      // lane (s, G) holds A[t = 16 tt + 4G + jj][s = 16 st + lc]
       const float bs = rbeta[16 * st + lc];
 #pragma unroll
-      for (int kbt = 0; kbt < 2; ++kbt) {
-        if (32 * kbt + 31 < 16 * st) continue;
-        f32x4 X[2];
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-          const int tt = 2 * kbt + hf;
-          X[hf] = zero4();
-          if (tt < st) continue;
-#pragma unroll
-          for (int kb = 0; kb < NKB; ++kb)
-            X[hf] = mfma(row8<LQ>(Qs, 16 * tt + lc, 32 * kb), row8<LQ>(Ks, 16 * st + lc, 32 * kb), X[hf]);
-#pragma unroll
-          for (int jj = 0; jj < 4; ++jj) X[hf][jj] = (tt > st || 4 * G + jj >= lc) ? X[hf][jj] * bs : 0.f;
-        }
-        Aop[st][kbt] = pack_tiles<2>(X[0], X[1]);
+      for (int jj = 0; jj < 4; ++jj) {
+        const float x = (tt > st || 4 * G + jj >= lc) ? X[jj] * bs : 0.f;
+        bf16 hi, lo;
+        split2(x, hi, lo);
+        ah[jj] = hi;
+        al[jj] = lo;
       }
     }
+    const int ao = LA::off(16 * st + lc, 16 * tt + 4 * G);
+    *reinterpret_cast<bf16x4*>(Ah + ao) = ah;
+    *reinterpret_cast<bf16x4*>(Al + ao) = al;
+  }
+  __syncthreads();
+
+  // ---------------- phase I: E^T, (Gb K^T) and dE^T for this wave's 16 state rows
+  {
     float da_part = 0.f;
     Op<2> Sa[NKB], Ga[NKB];  // (m = r, k = c natural)
 #pragma unroll
@@ -591,8 +588,9 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
 #pragma unroll
       for (int kbt = 0; kbt < 2; ++kbt) {
         if (32 * kbt + 31 < 16 * st) continue;
-        const Op<1> dOt{{col8_pair<LQ>(Os, 32 * kbt, r0)}};  // dO^T (m = r, k = t)
-        dEt = mma<1, 2>(dOt, Aop[st][kbt], dEt);
+        const Op<1> dOt{{col8<LQ>(Os, 32 * kbt, r0)}};  // dO^T (m = r, k = t)
+        const Op<2> At{{row8<LA>(Ah, 16 * st + lc, 32 * kbt), row8<LA>(Al, 16 * st + lc, 32 * kbt)}};
+        dEt = mma<1, 2>(dOt, At, dEt);  // (k = t, n = s)
       }
       bf16x4 eh, el, dh, dl;
 #pragma unroll
