@@ -10,16 +10,19 @@ resident in HBM before the timed region starts.
     python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu-baseline]
 
 prints one JSON line.  ``value`` is tokens/s (B*T per step) of the forward +
-backward step when the backward kernel of the rule is built, else of the
-forward.  ``roofline`` prices the forward kernel's average launch duration,
-measured with HIP events on its launch stream inside the timed region,
-against MI355X's HBM bandwidth (8 TB/s); ``traffic`` is read from the
-committed FETCH_SIZE/WRITE_SIZE summary of the same kernel and workload.
+backward step when the backward of the rule is built, else of the forward.
+``roofline`` prices the dominant part of the step -- the backward pass (its
+two kernels) -- and ``roofline_fwd`` the inference forward kernel: average
+durations measured with HIP events on the launch stream inside the timed
+regions, algorithmic bytes of the op's own inputs and outputs, against
+MI355X's HBM bandwidth (8 TB/s); ``traffic`` is read from the committed
+FETCH_SIZE/WRITE_SIZE summaries of the same kernels and workload.
 ``cpu_baseline`` times the CPU restatement of the reference matrix form
 (float32, torch on the host cores) on the same workload.
 
-``--copy-calibration BYTES`` only runs a device copy of BYTES bytes a few
-times (the calibration kernel for the HBM byte counters).
+``--fwd-only`` times the inference forward alone; ``--copy-calibration
+BYTES`` only runs a device copy of BYTES bytes a few times (the calibration
+kernel for the HBM byte counters).
 """
 from __future__ import annotations
 
@@ -50,6 +53,7 @@ def parse_args(argv=None):
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--workload", default=DEFAULT_WORKLOAD)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--fwd-only", action="store_true", help="time the inference forward only")
     p.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work (about)")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES")
     return p.parse_args(argv)
@@ -58,6 +62,11 @@ def parse_args(argv=None):
 def fwd_bytes_per_token_head(w) -> int:
     """q, k, v read and o written in bf16, plus the fp32 gate streams."""
     return 3 * 2 * w.d + 2 * w.d + 4 * GATES[w.rule]
+
+
+def bwd_bytes_per_token_head(w) -> int:
+    """Reads dO, q, k, v and the gates; writes dq, dk, dv and the gate gradients."""
+    return 4 * 2 * w.d + 3 * 2 * w.d + 2 * 4 * GATES[w.rule]
 
 
 def fwd_flops_per_chunk_head(w) -> int:
@@ -138,7 +147,7 @@ def main(argv=None):
     dev = torch.device("cuda:0")
     inp = make_inputs(w, seed=0, device=dev, with_grad_out=True)
     names = ("q", "k", "v", "beta", "g", "gmu", "gnu")
-    with_bwd = chunk.backward_supported(w.rule, w.d)
+    with_bwd = chunk.backward_supported(w.rule, w.d) and not args.fwd_only
     xs = [inp[n] if inp[n] is None else inp[n].detach().requires_grad_(with_bwd) for n in names]
     grads_of = [x for x in xs if x is not None]
     dO = inp["dO"]
@@ -155,42 +164,64 @@ def main(argv=None):
             ev[1].record(stream)
         if with_bwd:
             torch.autograd.grad(o, grads_of, dO)
+            if ev is not None:
+                ev[2].record(stream)
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    evs = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(3)) for _ in range(args.steps)]
     t0 = time.perf_counter()
     for i in range(args.steps):
         step(evs[i])
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_step = elapsed * 1e3 / args.steps
-    k_ms = statistics.mean(e0.elapsed_time(e1) for e0, e1 in evs)
+    # HIP events on the launch stream: the forward launch (which also writes the
+    # state checkpoint when a backward follows) and the backward's two launches
+    fwd_train_ms = statistics.mean(e[0].elapsed_time(e[1]) for e in evs)
+    bwd_ms = statistics.mean(e[1].elapsed_time(e[2]) for e in evs) if with_bwd else None
 
-    # forward-only throughput alongside the full step
-    fwd_ms = None
-    if with_bwd:
-        with torch.no_grad():
-            for _ in range(args.warmup):
-                fwd()
-            torch.cuda.synchronize()
-            t1 = time.perf_counter()
-            for _ in range(args.steps):
-                fwd()
-            torch.cuda.synchronize()
-            fwd_ms = (time.perf_counter() - t1) * 1e3 / args.steps
-    else:
-        fwd_ms = ms_step
+    # inference forward (no state checkpoint), timed the same way
+    fwd_evs = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(2)) for _ in range(args.steps)]
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            fwd()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        for e in fwd_evs:
+            e[0].record(stream)
+            fwd()
+            e[1].record(stream)
+        torch.cuda.synchronize()
+        fwd_ms = (time.perf_counter() - t1) * 1e3 / args.steps
+    fwd_kernel_ms = statistics.mean(e[0].elapsed_time(e[1]) for e in fwd_evs)
 
     units = w.B * w.H * w.T
-    alg_bytes = fwd_bytes_per_token_head(w) * units
-    alg_flops = fwd_flops_per_chunk_head(w) * w.B * w.H * (w.T // w.chunk)
-    if w.rule == "muon":
-        bound, achieved, peak, unit = "mfma", alg_flops / (k_ms * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s"
+    rid = {"delta": 0, "muon": 1, "adam": 2}[w.rule]
+
+    def roof(kernel, alg_bytes, alg_flops, ms, traffic_file):
+        if w.rule == "muon":
+            bound, ach, peak, unit = "mfma", alg_flops / (ms * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s"
+        else:
+            bound, ach, peak, unit = "hbm", alg_bytes / (ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s"
+        traffic = profiling.read_traffic(os.path.join(ROOT, "profiles", traffic_file))
+        return {"kernel": kernel, "bound": bound, "achieved": ach, "peak": peak, "unit": unit,
+                "frac": ach / peak, "traffic": traffic, "avg_launch_us": ms * 1e3,
+                "alg_bytes": alg_bytes, "alg_flops": alg_flops}
+
+    roof_fwd = roof(f"chunk_fwd<{w.d},{rid}>", fwd_bytes_per_token_head(w) * units,
+                    fwd_flops_per_chunk_head(w) * w.B * w.H * (w.T // w.chunk), fwd_kernel_ms,
+                    f"chunk_fwd_{w.name}_traffic.md")
+    if with_bwd:
+        # the backward pass dominates the step: its two kernels, priced on the
+        # op's own backward inputs and outputs (states are intermediates)
+        roof_main = roof(f"chunk_bwd_state<{w.d},{rid}> + chunk_bwd_tok<{w.d},{rid}>",
+                         bwd_bytes_per_token_head(w) * units,
+                         2 * fwd_flops_per_chunk_head(w) * w.B * w.H * (w.T // w.chunk), bwd_ms,
+                         f"chunk_bwd_{w.name}_traffic.md")
     else:
-        bound, achieved, peak, unit = "hbm", alg_bytes / (k_ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s"
-    traffic = profiling.read_traffic(os.path.join(ROOT, "profiles", f"chunk_fwd_{w.name}_traffic.md"))
+        roof_main = roof_fwd
 
     line = {
         "metric": METRIC,
@@ -210,10 +241,10 @@ def main(argv=None):
                    "state": "fp32", "global_batch": w.B, "seq_len": w.T, "parallelism": "none"},
         "fwd_tokens_per_s": w.tokens / (fwd_ms * 1e-3),
         "fwd_bwd_tokens_per_s": w.tokens / (ms_step * 1e-3) if with_bwd else None,
-        "roofline": {"kernel": f"chunk_fwd<{w.d},{ {'delta': 0, 'muon': 1, 'adam': 2}[w.rule]}>",
-                     "bound": bound, "achieved": achieved, "peak": peak, "unit": unit,
-                     "frac": achieved / peak, "traffic": traffic,
-                     "avg_launch_us": k_ms * 1e3, "alg_bytes": alg_bytes, "alg_flops": alg_flops},
+        "step_us": {"fwd_with_checkpoint": fwd_train_ms * 1e3, "bwd": None if bwd_ms is None else bwd_ms * 1e3,
+                    "fwd_inference": fwd_kernel_ms * 1e3},
+        "roofline": roof_main,
+        "roofline_fwd": roof_fwd,
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(w, args.cpu_budget, with_bwd)

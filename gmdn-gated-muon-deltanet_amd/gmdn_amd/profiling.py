@@ -8,7 +8,8 @@ Usage, after ``rocprofv3 ... --output-format csv -d DIR -o NAME -- <program>``:
         --copy-bytes N
 
 ``traffic`` turns the FETCH_SIZE / WRITE_SIZE derived counters (KiB per
-dispatch) into HBM bytes per launch of the kernel matching REGEX.  Each
+dispatch) into HBM bytes per launch of the kernels matching REGEX (summed
+over the kernels when the op runs several).  Each
 counter is scaled by what it reads for a plain device copy of N bytes
 (N read + N written), so the figure is in the same units as the algorithmic
 bytes.  The output is markdown; its ``traffic_bytes_per_launch:`` line is
@@ -57,6 +58,30 @@ def counter_per_dispatch(d: str, counter: str, kernel_regex: str):
     return list(vals.values())
 
 
+def counter_by_kernel(d: str, counter: str, kernel_regex: str):
+    """{kernel name: per-dispatch values of ``counter``} for matching kernels."""
+    pat = re.compile(kernel_regex)
+    per = {}
+    with open(_find(d, "counter_collection.csv")) as f:
+        for r in csv.DictReader(f):
+            if r["Counter_Name"] != counter or not pat.search(r["Kernel_Name"]):
+                continue
+            k = (r["Kernel_Name"], r["Dispatch_Id"])
+            per[k] = per.get(k, 0.0) + float(r["Counter_Value"])
+    out = {}
+    for (name, _), v in per.items():
+        out.setdefault(name, []).append(v)
+    if not out:
+        raise ValueError(f"no {counter} rows for /{kernel_regex}/ under {d}")
+    return out
+
+
+def _per_launch(d: str, counter: str, kernel_regex: str) -> float:
+    """Sum over the matching kernels of each one's median per-dispatch value:
+    the counter for one launch of the op when it runs those kernels once each."""
+    return sum(statistics.median(v) for v in counter_by_kernel(d, counter, kernel_regex).values())
+
+
 def _stats_md(d: str) -> str:
     out = ["| kernel | calls | avg us | min us | max us | % time |", "|---|---|---|---|---|---|"]
     for name, calls, avg, mn, mx, pct in kernel_stats(d):
@@ -66,8 +91,8 @@ def _stats_md(d: str) -> str:
 
 def _traffic_md(a) -> str:
     kib = 1024.0
-    fetch = statistics.median(counter_per_dispatch(a.fetch, "FETCH_SIZE", a.kernel))
-    write = statistics.median(counter_per_dispatch(a.write, "WRITE_SIZE", a.kernel))
+    fetch = _per_launch(a.fetch, "FETCH_SIZE", a.kernel)
+    write = _per_launch(a.write, "WRITE_SIZE", a.kernel)
     cf = statistics.median(counter_per_dispatch(a.copy_fetch, "FETCH_SIZE", a.copy_kernel))
     cw = statistics.median(counter_per_dispatch(a.copy_write, "WRITE_SIZE", a.copy_kernel))
     sf, sw = a.copy_bytes / (cf * kib), a.copy_bytes / (cw * kib)
