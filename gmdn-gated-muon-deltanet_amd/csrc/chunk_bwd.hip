@@ -556,9 +556,9 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
   __syncthreads();
 
   // ---------------- phase I: E^T, (Gb K^T) and dE^T for this wave's 16 state rows
+  Op<2> Sa[NKB], Ga[NKB];  // rows r0 + lc of S_i, Gb_i (m = r, k = c natural); reused in IIb
   {
     float da_part = 0.f;
-    Op<2> Sa[NKB], Ga[NKB];  // (m = r, k = c natural)
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
       da_part += dot4(srow[kb][0], grow[kb][0]) + dot4(srow[kb][1], grow[kb][1]);
@@ -612,21 +612,6 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
     if constexpr (RULE == 0) {  // delta: Gb_i = Sb_{i+1}, so da_i = <Gb_i, S_i>
       da_part = wave_sum(da_part);
       if (l == 0) atomicAdd(rda, da_part);
-    }
-  }
-  // columns j0 + lc of S_i and Gb_i (k = r natural, n = j) for phase IIb,
-  // requested before the barrier so that they arrive during phase IIa
-  f32x4 scol[NKB][2], gcol[NKB][2];
-#pragma unroll
-  for (int kb = 0; kb < NKB; ++kb) {
-    const float* sp = S + (int64_t)(32 * kb + 8 * G) * D + j0 + lc;
-    const float* gp = Gb + (int64_t)(32 * kb + 8 * G) * D + j0 + lc;
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      scol[kb][0][jj] = sp[jj * D];
-      scol[kb][1][jj] = sp[(4 + jj) * D];
-      gcol[kb][0][jj] = gp[jj * D];
-      gcol[kb][1][jj] = gp[(4 + jj) * D];
     }
   }
   __syncthreads();
@@ -700,48 +685,77 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
   }
 
   // ---------------- phase IIb: dQ and dK for this wave's 16 state columns
+  //   dQ = (dA diag(beta)) K + dO S,   dK = (dA diag(beta))^T Q - dE S + diag(w) E Gb
   bf16* dqg = p.dq + bb * p.sq[0] + hh * p.sq[1] + t0 * p.sq[2];
   bf16* dkg = p.dk + bb * p.sk[0] + hh * p.sk[1] + t0 * p.sk[2];
-  Op<2> Sc[NKB], Gc[NKB];
-#pragma unroll
-  for (int kb = 0; kb < NKB; ++kb) {
-    Sc[kb] = pack_tiles<2>(scol[kb][0], scol[kb][1]);
-    Gc[kb] = pack_tiles<2>(gcol[kb][0], gcol[kb][1]);
-  }
+  f32x4 dqa[4], dka[4], des[4], eg[4];
+  // the dA terms first: they are the last readers of the Q and K tiles
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt) {
-    // dQ = dO S + (dA diag(beta)) K
-    f32x4 acc = zero4();
-#pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) acc = mma<1, 2>(Op<1>{{row8<LQ>(Os, 16 * tt + lc, 32 * kb)}}, Sc[kb], acc);
+    dqa[tt] = zero4();
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       if (32 * ks > 16 * tt + 15) continue;
       const Op<2> dA{{col8<LA>(Ah, 32 * ks, 16 * tt), col8<LA>(Al, 32 * ks, 16 * tt)}};
-      acc = mma<2, 1>(dA, Op<1>{{col8<LQ>(Ks, 32 * ks, j0)}}, acc);
+      dqa[tt] = mma<2, 1>(dA, Op<1>{{col8<LQ>(Ks, 32 * ks, j0)}}, dqa[tt]);
     }
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) dqg[(16 * tt + 4 * G + jj) * p.sq[2] + j0 + lc] = (bf16)acc[jj];
   }
 #pragma unroll
   for (int st = 0; st < 4; ++st) {
-    // dK = (dA diag(beta))^T Q - dE S + diag(w) E Gb
-    f32x4 eg = zero4(), acc = zero4();
-#pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) {
-      const Op<2> Er{{row8<LQ>(Eh, 16 * st + lc, 32 * kb), row8<LQ>(El, 16 * st + lc, 32 * kb)}};
-      const Op<2> Dr{{row8<LQ>(Dh, 16 * st + lc, 32 * kb), row8<LQ>(Dl, 16 * st + lc, 32 * kb)}};
-      eg = mma<2, 2>(Er, Gc[kb], eg);
-      acc = mma<2, 2>(Dr, Sc[kb], acc);
-    }
-    if constexpr (RULE == 0) eg = eg * *reinterpret_cast<const f32x4*>(rbeta + 16 * st + 4 * G);
-    acc = eg - acc;
+    dka[st] = des[st] = eg[st] = zero4();
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
       if (32 * kt + 31 < 16 * st) continue;
       const Op<2> dAT{{row8<LA>(Ah, 16 * st + lc, 32 * kt), row8<LA>(Al, 16 * st + lc, 32 * kt)}};
-      acc = mma<2, 1>(dAT, Op<1>{{col8<LQ>(Qs, 32 * kt, j0)}}, acc);
+      dka[st] = mma<2, 1>(dAT, Op<1>{{col8<LQ>(Qs, 32 * kt, j0)}}, dka[st]);
     }
+  }
+  // The products over the state's rows need S_i and Gb_i by columns.  They
+  // are transposed on chip: the rows still held from phase I pass through
+  // the (now free) Q and K tiles one 32-row block at a time, split planes
+  // of [32 rows][D], and every wave reads its 16 columns back transposed.
+  bf16* Sh = reinterpret_cast<bf16*>(smem + L::Q0);
+  bf16* Sl = Sh + 32 * D;
+  bf16* Gh = reinterpret_cast<bf16*>(smem + L::K0);
+  bf16* Gl = Gh + 32 * D;
+  __syncthreads();  // Q and K tiles free
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb) {
+    if ((w >> 1) == kb) {  // waves 2kb, 2kb+1 hold rows 32 kb .. 32 kb + 31
+      const int lr = 16 * (w & 1) + lc;
+#pragma unroll
+      for (int kc = 0; kc < NKB; ++kc) {
+        const int so = LQ::off(lr, 32 * kc + 8 * G);
+        *reinterpret_cast<bf16x8*>(Sh + so) = Sa[kc].v[0];
+        *reinterpret_cast<bf16x8*>(Sl + so) = Sa[kc].v[1];
+        *reinterpret_cast<bf16x8*>(Gh + so) = Ga[kc].v[0];
+        *reinterpret_cast<bf16x8*>(Gl + so) = Ga[kc].v[1];
+      }
+    }
+    __syncthreads();
+    // columns j0 + lc, rows 32 kb + (k = 8G .. 8G + 7): (k = r natural, n = j)
+    const Op<2> sc{{col8<LQ>(Sh, 0, j0), col8<LQ>(Sl, 0, j0)}};
+    const Op<2> gc{{col8<LQ>(Gh, 0, j0), col8<LQ>(Gl, 0, j0)}};
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) dqa[tt] = mma<1, 2>(Op<1>{{row8<LQ>(Os, 16 * tt + lc, 32 * kb)}}, sc, dqa[tt]);
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const Op<2> Er{{row8<LQ>(Eh, 16 * st + lc, 32 * kb), row8<LQ>(El, 16 * st + lc, 32 * kb)}};
+      const Op<2> Dr{{row8<LQ>(Dh, 16 * st + lc, 32 * kb), row8<LQ>(Dl, 16 * st + lc, 32 * kb)}};
+      eg[st] = mma<2, 2>(Er, gc, eg[st]);
+      des[st] = mma<2, 2>(Dr, sc, des[st]);
+    }
+    if (kb + 1 < NKB) __syncthreads();  // before the next block overwrites the staging planes
+  }
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) dqg[(16 * tt + 4 * G + jj) * p.sq[2] + j0 + lc] = (bf16)dqa[tt][jj];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+    f32x4 e = eg[st];
+    if constexpr (RULE == 0) e = e * *reinterpret_cast<const f32x4*>(rbeta + 16 * st + 4 * G);
+    const f32x4 acc = dka[st] - des[st] + e;
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) dkg[(16 * st + 4 * G + jj) * p.sk[2] + j0 + lc] = (bf16)acc[jj];
   }
