@@ -839,18 +839,19 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
   const int r0 = 16 * w;  // this wave's state rows (phase I) ...
   const int j0 = 16 * w;  // ... and state columns (phase IIb)
 
-  // rows r0 + lc of S_i and Gb_i (natural k order), loaded while the tiles arrive
-  f32x4 srow[NKB][2], grow[NKB][2];
-#pragma unroll
-  for (int kb = 0; kb < NKB; ++kb) {
-    const int64_t off = (int64_t)(r0 + lc) * D + 32 * kb + 8 * G;
-    srow[kb][0] = *reinterpret_cast<const f32x4*>(S + off);
-    srow[kb][1] = *reinterpret_cast<const f32x4*>(S + off + 4);
-    grow[kb][0] = *reinterpret_cast<const f32x4*>(Gb + off);
-    grow[kb][1] = *reinterpret_cast<const f32x4*>(Gb + off + 4);
+  // ---------------- phase 0: gates, then the q, k tiles (all phase I' needs),
+  // the v, dO tiles and the rows r0 + lc of S_i and Gb_i (natural k order),
+  // which arrive while phase I' runs
+  float gv[4];
+  if (threadIdx.x < CB_C) {
+    const int64_t e = bh * p.T + t0 + threadIdx.x;
+    gv[0] = p.beta[e];
+    gv[1] = p.g[e];
+    if constexpr (RULE == 2) {
+      gv[2] = p.gmu[e];
+      gv[3] = p.gnu[e];
+    }
   }
-
-  // ---------------- phase 0: the chunk's q, k, v, dO tiles and gates
   {
     DmaPlan<LQ, CB_C, NTHR> pq, pk, pv, po;
     pq.init(w, p.sq[2]);
@@ -862,20 +863,31 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
     pk.issue(p.k + bb * p.sk[0] + hh * p.sk[1] + t0 * p.sk[2], lds0 + L::K0, w);
     pv.issue(p.v + bb * p.sv[0] + hh * p.sv[1] + t0 * p.sv[2], lds0 + L::V0, w);
     po.issue(p.o + bb * p.so[0] + hh * p.so[1] + t0 * p.so[2], lds0 + L::O0, w);
-    if (threadIdx.x < CB_C) {
-      const int e = threadIdx.x;
-      rdbeta[e] = 0.f;
-      rbeta[e] = p.beta[bh * p.T + t0 + e];
-      rg[e] = p.g[bh * p.T + t0 + e];
-      if constexpr (RULE == 2) {
-        rgmu[e] = p.gmu[bh * p.T + t0 + e];
-        rgnu[e] = p.gnu[bh * p.T + t0 + e];
-      }
-      if (e == 0) rda[0] = 0.f;
-    }
-    wait_vmem();
-    __syncthreads();
   }
+  f32x4 srow[NKB][2], grow[NKB][2];
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb) {
+    const int64_t off = (int64_t)(r0 + lc) * D + 32 * kb + 8 * G;
+    srow[kb][0] = *reinterpret_cast<const f32x4*>(S + off);
+    srow[kb][1] = *reinterpret_cast<const f32x4*>(S + off + 4);
+    grow[kb][0] = *reinterpret_cast<const f32x4*>(Gb + off);
+    grow[kb][1] = *reinterpret_cast<const f32x4*>(Gb + off + 4);
+  }
+  // vector-memory operations complete in issue order: with the 4 NKB row
+  // loads still in flight, the gates and the four tiles have landed
+  wait_vmem_le<4 * NKB>();
+  if (threadIdx.x < CB_C) {
+    const int e = threadIdx.x;
+    rdbeta[e] = 0.f;
+    rbeta[e] = gv[0];
+    rg[e] = gv[1];
+    if constexpr (RULE == 2) {
+      rgmu[e] = gv[2];
+      rgnu[e] = gv[3];
+    }
+    if (e == 0) rda[0] = 0.f;
+  }
+  __syncthreads();
 
   // ---------------- phase I': A^T = (tril(Q K^T) diag(beta))^T, split, into the
   // dA planes (free until phase IIa): tile (tt, st), k = 4 tt + st, goes to
@@ -906,6 +918,7 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
     *reinterpret_cast<bf16x4*>(Ah + ao) = ah;
     *reinterpret_cast<bf16x4*>(Al + ao) = al;
   }
+  wait_vmem();  // the rows of S_i and Gb_i
   __syncthreads();
 
   // ---------------- phase I: E^T, (Gb K^T) and dE^T for this wave's 16 state rows
@@ -1100,17 +1113,28 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
     }
     if (kb + 1 < NKB) __syncthreads();  // before the next block overwrites the staging planes
   }
+  // dQ and dK: staged as [64 tokens][D] bf16 tiles in the V tile and the dA
+  // planes (both free since phase I / the dA terms), then stored in rows
+  bf16* dqs = reinterpret_cast<bf16*>(smem + L::V0);
+  bf16* dks = Ah;
+  static_assert(2 * L::AP >= L::TILE, "the dA planes hold one [64][D] bf16 tile");
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) dqg[(16 * tt + 4 * G + jj) * p.sq[2] + j0 + lc] = (bf16)dqa[tt][jj];
+    for (int jj = 0; jj < 4; ++jj) dqs[LQ::off(16 * tt + 4 * G + jj, j0 + lc)] = (bf16)dqa[tt][jj];
 #pragma unroll
   for (int st = 0; st < 4; ++st) {
     f32x4 e = eg[st];
     if constexpr (RULE == 0) e = e * *reinterpret_cast<const f32x4*>(rbeta + 16 * st + 4 * G);
     const f32x4 acc = dka[st] - des[st] + e;
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) dkg[(16 * st + 4 * G + jj) * p.sk[2] + j0 + lc] = (bf16)acc[jj];
+    for (int jj = 0; jj < 4; ++jj) dks[LQ::off(16 * st + 4 * G + jj, j0 + lc)] = (bf16)acc[jj];
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < CB_C * D / 8; e += NTHR) {
+    const int r = e / (D / 8), c8 = (e % (D / 8)) * 8;
+    *reinterpret_cast<bf16x8*>(dqg + r * p.sq[2] + c8) = *reinterpret_cast<const bf16x8*>(dqs + LQ::off(r, c8));
+    *reinterpret_cast<bf16x8*>(dkg + r * p.sk[2] + c8) = *reinterpret_cast<const bf16x8*>(dks + LQ::off(r, c8));
   }
 }
 
