@@ -295,7 +295,7 @@ __global__ void __launch_bounds__(FW_THREADS) chunk_fwd(ChunkArgs p) {
       float* sp = p.states + ((bh * p.N + i) * D + r0 + lc) * (int64_t)D + 4 * G;
 #pragma unroll
       for (int t = 0; t < NTH; ++t) {
-        *reinterpret_cast<f32x4*>(sp + 16 * (h * NTH + t)) = S[t];
+        *reinterpret_cast<bf16x8*>(sp + 16 * (h * NTH + t)) = split_piece(S[t]);
         if constexpr (RULE == 2) {
           *reinterpret_cast<f32x4*>(sp + plane + 16 * (h * NTH + t)) = Mm[t];
           *reinterpret_cast<f32x4*>(sp + 2 * plane + 16 * (h * NTH + t)) = Vv[t];

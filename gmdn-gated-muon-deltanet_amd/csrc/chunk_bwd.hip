@@ -165,8 +165,8 @@ __global__ void __launch_bounds__(CB_THREADS) chunk_bwd_state(ChunkArgs p) {
     const float* sp = p.states + ((bh * p.N + i) * D + r0 + lc) * (int64_t)D;
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
-      Sraw[kb][0] = *reinterpret_cast<const f32x4*>(sp + 32 * kb + 4 * G);
-      Sraw[kb][1] = *reinterpret_cast<const f32x4*>(sp + 32 * kb + 16 + 4 * G);
+      Sraw[kb][0] = unsplit_piece(*reinterpret_cast<const bf16x8*>(sp + 32 * kb + 4 * G));
+      Sraw[kb][1] = unsplit_piece(*reinterpret_cast<const bf16x8*>(sp + 32 * kb + 16 + 4 * G));
     }
 #pragma unroll
     for (int t = 0; t < NTH; ++t) {
@@ -294,7 +294,7 @@ __global__ void __launch_bounds__(CB_THREADS) chunk_bwd_state(ChunkArgs p) {
             Mb[t][jj] = msc * mt;
             Vb[t][jj] = nsc * vt;
           }
-          *reinterpret_cast<f32x4*>(gp + 16 * (h * NTH + t)) = Gb[t];
+          *reinterpret_cast<bf16x8*>(gp + 16 * (h * NTH + t)) = split_piece(Gb[t]);
         }
         publish_Gb(Gb);
         da = wave_sum(da);
@@ -734,25 +734,20 @@ __global__ void __launch_bounds__(DS_THREADS) chunk_bwd_dstate(ChunkArgs p) {
     uint32_t xso[NG];
 #pragma unroll
     for (int k = 0; k < NG; ++k) xso[k] = swz_off<LQ>((64 * k + l) / GPR, 8 * ((64 * k + l) % GPR));
-    auto store_gb = [&](int i) {
-      f32x4 hi_lo[NG][2];
+    auto store_gb = [&](int i) {  // split pieces, copied from the exchange planes
+      bf16x8 hi[NG], lo[NG];
 #pragma unroll
       for (int k = 0; k < NG; ++k) {
-        const bf16x8 hi = lds_ld<bf16x8>(L0 + (xso[k] + L::XS0));
-        const bf16x8 lo = lds_ld<bf16x8>(L0 + (xso[k] + L::XS0 + L::XSP));
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          hi_lo[k][0][jj] = (float)hi[jj] + (float)lo[jj];
-          hi_lo[k][1][jj] = (float)hi[4 + jj] + (float)lo[4 + jj];
-        }
+        hi[k] = lds_ld<bf16x8>(L0 + (xso[k] + L::XS0));
+        lo[k] = lds_ld<bf16x8>(L0 + (xso[k] + L::XS0 + L::XSP));
       }
       float* gp = p.gb + ((bh * p.N + i) * D + 32 * blk) * (int64_t)D;
 #pragma unroll
       for (int k = 0; k < NG; ++k) {
         const int g = 64 * k + l;
         float* dst = gp + (g / GPR) * D + 8 * (g % GPR);
-        *reinterpret_cast<f32x4*>(dst) = hi_lo[k][0];
-        *reinterpret_cast<f32x4*>(dst + 4) = hi_lo[k][1];
+        *reinterpret_cast<bf16x8*>(dst) = __builtin_shufflevector(hi[k], lo[k], 0, 1, 2, 3, 8, 9, 10, 11);
+        *reinterpret_cast<bf16x8*>(dst + 4) = __builtin_shufflevector(hi[k], lo[k], 4, 5, 6, 7, 12, 13, 14, 15);
       }
     };
 
@@ -864,14 +859,14 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
     pv.issue(p.v + bb * p.sv[0] + hh * p.sv[1] + t0 * p.sv[2], lds0 + L::V0, w);
     po.issue(p.o + bb * p.so[0] + hh * p.so[1] + t0 * p.so[2], lds0 + L::O0, w);
   }
-  f32x4 srow[NKB][2], grow[NKB][2];
+  bf16x8 srow[NKB][2], grow[NKB][2];  // split pieces of columns 32 kb + 8G .. +3, +4 .. +7
 #pragma unroll
   for (int kb = 0; kb < NKB; ++kb) {
     const int64_t off = (int64_t)(r0 + lc) * D + 32 * kb + 8 * G;
-    srow[kb][0] = *reinterpret_cast<const f32x4*>(S + off);
-    srow[kb][1] = *reinterpret_cast<const f32x4*>(S + off + 4);
-    grow[kb][0] = *reinterpret_cast<const f32x4*>(Gb + off);
-    grow[kb][1] = *reinterpret_cast<const f32x4*>(Gb + off + 4);
+    srow[kb][0] = *reinterpret_cast<const bf16x8*>(S + off);
+    srow[kb][1] = *reinterpret_cast<const bf16x8*>(S + off + 4);
+    grow[kb][0] = *reinterpret_cast<const bf16x8*>(Gb + off);
+    grow[kb][1] = *reinterpret_cast<const bf16x8*>(Gb + off + 4);
   }
   // vector-memory operations complete in issue order: with the 4 NKB row
   // loads still in flight, the gates and the four tiles have landed
@@ -924,13 +919,16 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
   // ---------------- phase I: E^T, (Gb K^T) and dE^T for this wave's 16 state rows
   Op<2> Sa[NKB], Ga[NKB];  // rows r0 + lc of S_i, Gb_i (m = r, k = c natural); reused in IIb
   {
-    float da_part = 0.f;
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
-      da_part += dot4(srow[kb][0], grow[kb][0]) + dot4(srow[kb][1], grow[kb][1]);
-      Sa[kb] = pack_tiles<2>(srow[kb][0], srow[kb][1]);
-      Ga[kb] = pack_tiles<2>(grow[kb][0], grow[kb][1]);
+      Sa[kb] = join_pieces(srow[kb][0], srow[kb][1]);
+      Ga[kb] = join_pieces(grow[kb][0], grow[kb][1]);
     }
+    // the loop below has no cross-lane step, so the LDS reads of one token
+    // tile overlap the MFMA chains of the previous one
+    float ws[4], dbp[4];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) ws[st] = RULE == 0 ? rbeta[16 * st + lc] : 1.f;
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
       // D layout: lane (s, G) holds rows r0 + 4G + jj
@@ -944,13 +942,8 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
         GK = mma<2, 1>(Ga[kb], kr, GK);
       }
       Et = -Et;  // E^T = V^T - S K^T
-      if constexpr (RULE == 0) {
-        // dbeta's diag(w) term: sum_r E[s][r] (Gb k_s)[r]
-        const float v = group_sum(dot4(Et, GK));
-        if (G == 0) atomicAdd(rdbeta + 16 * st + lc, v);
-      }
-      const float ws = RULE == 0 ? rbeta[16 * st + lc] : 1.f;
-      f32x4 dEt = GK * ws;
+      dbp[st] = dot4(Et, GK);  // dbeta's diag(w) term, this lane's 4 rows
+      f32x4 dEt = GK * ws[st];
 #pragma unroll
       for (int kbt = 0; kbt < 2; ++kbt) {
         if (32 * kbt + 31 < 16 * st) continue;
@@ -975,17 +968,33 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
       *reinterpret_cast<bf16x4*>(Dh + eo) = dh;
       *reinterpret_cast<bf16x4*>(Dl + eo) = dl;
     }
-    if constexpr (RULE == 0) {  // delta: Gb_i = Sb_{i+1}, so da_i = <Gb_i, S_i>
-      da_part = wave_sum(da_part);
-      if (l == 0) atomicAdd(rda, da_part);
+    if constexpr (RULE == 0) {
+      // dbeta's diag(w) term: sum_r E[s][r] (Gb k_s)[r] over the wave's rows
+#pragma unroll
+      for (int st = 0; st < 4; ++st) dbp[st] = group_sum(dbp[st]);
+      if (G == 0) {
+#pragma unroll
+        for (int st = 0; st < 4; ++st) atomicAdd(rdbeta + 16 * st + lc, dbp[st]);
+      }
+      // delta: Gb_i = Sb_{i+1}, so da_i = <Gb_i, S_i>: the trace of this
+      // wave's 16 x 16 diagonal block of Gb_i S_i^T (A = Gb rows, B = S rows)
+      f32x4 T = zero4();
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) T = mma<2, 2>(Ga[kb], Sa[kb], T);
+      // lane (n, G) holds entries (4G + jj, n): the diagonal is jj = n - 4G
+      const float dpart = (lc >> 2) == G ? T[lc & 3] : 0.f;
+      const float da_w = wave_sum(dpart);
+      if (l == 0) atomicAdd(rda, da_w);
     }
   }
   __syncthreads();
 
   // ---------------- phase IIa: dA = tril(dO E^T), dbeta's A term, dA diag(beta) -> LDS
   // tiles k = 4 tt + st, k = w, w + NW, ...; tiles above the diagonal are zeroed
+  float dbk[16 / NW];
 #pragma unroll
   for (int kk = 0; kk < 16 / NW; ++kk) {
+    dbk[kk] = 0.f;
     const int k = w + NW * kk, tt = k >> 2, st = k & 3;
     bf16x4 ah, al;
     if (tt < st) {
@@ -1010,12 +1019,17 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
         ah[jj] = x;
         al[jj] = y;
       }
-      db = group_sum(db);
-      if (G == 0) atomicAdd(rdbeta + 16 * st + lc, db);
+      dbk[kk] = db;
     }
     const int ao = LA::off(16 * st + lc, 16 * tt + 4 * G);
     *reinterpret_cast<bf16x4*>(Ah + ao) = ah;
     *reinterpret_cast<bf16x4*>(Al + ao) = al;
+  }
+#pragma unroll
+  for (int kk = 0; kk < 16 / NW; ++kk) {
+    const int k = w + NW * kk, tt = k >> 2, st = k & 3;
+    const float db = group_sum(dbk[kk]);
+    if (tt >= st && G == 0) atomicAdd(rdbeta + 16 * st + lc, db);
   }
   __syncthreads();
 

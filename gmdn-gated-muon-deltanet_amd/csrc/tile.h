@@ -194,6 +194,34 @@ GMDN_DEV bf16x8 cat8(const bf16x4& a, const bf16x4& b) {
   return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
+// Split-state pieces: the chunk kernels keep fp32 state matrices in memory
+// as 16-byte pieces {hi[0..3], lo[0..3]} of four consecutive columns
+// (x = hi + lo, hi = bf16(x), lo = bf16(x - hi)), the form their MFMA
+// operands take, in the bytes the fp32 values would occupy.
+GMDN_DEV bf16x8 split_piece(const f32x4& x) {
+  bf16x8 r;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    bf16 hi, lo;
+    split2(x[j], hi, lo);
+    r[j] = hi;
+    r[4 + j] = lo;
+  }
+  return r;
+}
+GMDN_DEV bf16x8 split_piece(const bf16x4& hi, const bf16x4& lo) { return cat8(hi, lo); }
+GMDN_DEV f32x4 unsplit_piece(const bf16x8& p) {
+  return f32x4{(float)p[0] + (float)p[4], (float)p[1] + (float)p[5], (float)p[2] + (float)p[6],
+               (float)p[3] + (float)p[7]};
+}
+// Pieces of columns k0 .. k0+3 and k0+4 .. k0+7 -> split operand, natural k order
+GMDN_DEV Op<2> join_pieces(const bf16x8& a, const bf16x8& b) {
+  Op<2> r;
+  r.v[0] = __builtin_shufflevector(a, b, 0, 1, 2, 3, 8, 9, 10, 11);
+  r.v[1] = __builtin_shufflevector(a, b, 4, 5, 6, 7, 12, 13, 14, 15);
+  return r;
+}
+
 // LDS byte address of a pointer into LDS (wave-uniform when `p` is).
 GMDN_DEV uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)((const __attribute__((address_space(3))) char*)p);

@@ -119,7 +119,8 @@ typedef struct gmdn_chunk_desc {
 } gmdn_chunk_desc;
 
 /* Bytes of the per-chunk state checkpoint gmdn_chunk_fwd writes when
- * `states` is non-NULL (what gmdn_chunk_bwd consumes). */
+ * `states` is non-NULL (what gmdn_chunk_bwd consumes; its layout is private
+ * to the library). */
 size_t gmdn_chunk_states_bytes(const gmdn_chunk_desc* desc);
 
 /* Forward: o = mixer core(q, k, v, beta, g[, gmu][, gnu]).  g, gmu, gnu are
