@@ -290,13 +290,12 @@ __global__ void __launch_bounds__(FW_THREADS) chunk_fwd(ChunkArgs p) {
     using I3 = integral_constant<int, 3>;
     Op<2> Sop[NKB];  // S_i^T operands of every k-block (rows of this row tile)
     // ================= state, before Y_i: -E for this wave's tokens
-    if (p.states) {  // pre-update state (and adam's moments) for the backward
-      const int64_t plane = p.B * p.H * p.N * (int64_t)D * D;
-      float* sp = p.states + ((bh * p.N + i) * D + r0 + lc) * (int64_t)D + 4 * G;
+    if constexpr (RULE == 2) {
+      if (p.states) {  // adam's moments for the backward (S_i itself: the output waves)
+        const int64_t plane = p.B * p.H * p.N * (int64_t)D * D;
+        float* sp = p.states + ((bh * p.N + i) * D + r0 + lc) * (int64_t)D + 4 * G;
 #pragma unroll
-      for (int t = 0; t < NTH; ++t) {
-        *reinterpret_cast<bf16x8*>(sp + 16 * (h * NTH + t)) = split_piece(S[t]);
-        if constexpr (RULE == 2) {
+        for (int t = 0; t < NTH; ++t) {
           *reinterpret_cast<f32x4*>(sp + plane + 16 * (h * NTH + t)) = Mm[t];
           *reinterpret_cast<f32x4*>(sp + 2 * plane + 16 * (h * NTH + t)) = Vv[t];
         }
@@ -382,7 +381,7 @@ __global__ void __launch_bounds__(FW_THREADS) chunk_fwd(ChunkArgs p) {
     using I2 = integral_constant<int, 2>;
     using I3 = integral_constant<int, 3>;
     Op<2> Sop[NKB];  // S_i^T operands of every k-block (rows of this row tile)
-    // ================= output, before Y_i: DMA, gate scalars, S^T operands, -A tiles
+    // ================= output, before Y_i: DMA, gate scalars, S^T operands, -A tiles, Q S^T
     if (ahead) issue_loads(i + RING - 1, (STG + RING - 1) % RING);
     if (sw == 3) chunk_scalars(STG);
 #pragma unroll
@@ -395,12 +394,8 @@ __global__ void __launch_bounds__(FW_THREADS) chunk_fwd(ChunkArgs p) {
       case 2: a_tile(stg_tag, I1{}, I3{}); break;
       default: a_tile(stg_tag, I2{}, I3{}); break;
     }
-    __syncthreads();  // Y_i: E halves and -A published
-    // ================= output, after Y_i: o = Q S^T + (-A)(-E) for this wave's tokens
-    Op<2> EN[2];
-#pragma unroll
-    for (int kbs = 0; kbs < 2; ++kbs) EN[kbs] = read_op(L0 + (xer[kbs] + L::XE0), L::XEP);
-    auto outp = [&](auto h_tag) {
+    // o = Q S^T + (-A)(-E) for this wave's tokens; Q S^T needs no E: before Y_i
+    auto qs = [&](auto h_tag) {
       constexpr int H = decltype(h_tag)::value;
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
@@ -408,15 +403,29 @@ __global__ void __launch_bounds__(FW_THREADS) chunk_fwd(ChunkArgs p) {
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb)
           O[u] = mma<1, 2>(Op<1>{{lds_ld<bf16x8>(qrow[kb] + SQK + (2 * H + u) * 16 * ROWB)}}, Sop[kb], O[u]);
-#pragma unroll
-        for (int kbs = 0; kbs <= H; ++kbs)
-          O[u] = mma<2, 2>(read_op(ap[kbs] + u * 16 * CB_C * 2, L::AP), EN[kbs], O[u]);
       }
     };
     if (h == 0)
-      outp(I0{});
+      qs(I0{});
     else
-      outp(I1{});
+      qs(I1{});
+    __syncthreads();  // Y_i: E halves and -A published
+    // ================= output, after Y_i: the (-A)(-E) term
+    Op<2> EN[2];
+#pragma unroll
+    for (int kbs = 0; kbs < 2; ++kbs) EN[kbs] = read_op(L0 + (xer[kbs] + L::XE0), L::XEP);
+    auto ae = [&](auto h_tag) {
+      constexpr int H = decltype(h_tag)::value;
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int kbs = 0; kbs <= H; ++kbs)
+          O[u] = mma<2, 2>(read_op(ap[kbs] + u * 16 * CB_C * 2, L::AP), EN[kbs], O[u]);
+    };
+    if (h == 0)
+      ae(I0{});
+    else
+      ae(I1{});
     // o for tokens 32h .. 32h+31, columns r0 .. r0+15: staged through this
     // wave's 1 KiB of the chunk's V slot (read only before Y_i, refilled
     // only after X_{i+1}) and stored as one 16-byte piece per lane
@@ -430,15 +439,37 @@ __global__ void __launch_bounds__(FW_THREADS) chunk_fwd(ChunkArgs p) {
       const bf16x8 piece = *reinterpret_cast<const bf16x8*>(stage + tok * 16 + 8 * half);
       *reinterpret_cast<bf16x8*>(og - lc + ((int64_t)i * CB_C + 32 * h + tok) * p.so[2] + 8 * half) = piece;
     }
-    // chunk i+1's tiles must have landed; the loads issued after them (for
-    // chunk i+RING-1, and this chunk's one o store) may stay in flight.
-    // Vector memory operations complete in issue order for this count:
-    // vmcnt <= (operations issued since) suffices.
+    // the checkpoint of S_i for the backward, from the split operands this
+    // wave holds (rows r0 .. r0+15, k-blocks of column half h), so that the
+    // state waves never wait on vector memory
+    constexpr int CK = NKB;  // 16-byte pieces per lane
+    if (p.states) {
+      float* sp = p.states + ((bh * p.N + i) * D + r0 + lc) * (int64_t)D + 8 * G;
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+        if ((2 * kb >= NKB) != (h == 1)) continue;
+        *reinterpret_cast<bf16x8*>(sp + 32 * kb) =
+            __builtin_shufflevector(Sop[kb].v[0], Sop[kb].v[1], 0, 1, 2, 3, 8, 9, 10, 11);
+        *reinterpret_cast<bf16x8*>(sp + 32 * kb + 4) =
+            __builtin_shufflevector(Sop[kb].v[0], Sop[kb].v[1], 4, 5, 6, 7, 12, 13, 14, 15);
+      }
+    }
+    // chunk i+1's tiles must have landed; the operations issued after them
+    // (the loads for chunk i+RING-1, this chunk's o store and checkpoint
+    // pieces) may stay in flight.  Vector memory operations complete in issue
+    // order for this count: vmcnt <= (operations issued since) suffices.
     if (ahead) {
-      if (sw == 0)
-        wait_vmem_le<L::DMA_OPS + 2>();
-      else
-        wait_vmem_le<L::DMA_OPS + 1>();
+      if (p.states) {
+        if (sw == 0)
+          wait_vmem_le<L::DMA_OPS + CK + 2>();
+        else
+          wait_vmem_le<L::DMA_OPS + CK + 1>();
+      } else {
+        if (sw == 0)
+          wait_vmem_le<L::DMA_OPS + 2>();
+        else
+          wait_vmem_le<L::DMA_OPS + 1>();
+      }
     } else {
       wait_vmem();
     }
