@@ -216,7 +216,8 @@ def main(argv=None):
     if with_bwd:
         # the backward pass dominates the step: its two kernels, priced on the
         # op's own backward inputs and outputs (states are intermediates)
-        roof_main = roof(f"chunk_bwd_state<{w.d},{rid}> + chunk_bwd_tok<{w.d},{rid}>",
+        state_kernel = f"chunk_bwd_dstate<{w.d}>" if rid == 0 else f"chunk_bwd_state<{w.d},{rid}>"
+        roof_main = roof(f"{state_kernel} + chunk_bwd_tok<{w.d},{rid}>",
                          bwd_bytes_per_token_head(w) * units,
                          2 * fwd_flops_per_chunk_head(w) * w.B * w.H * (w.T // w.chunk), bwd_ms,
                          f"chunk_bwd_{w.name}_traffic.md")

@@ -112,14 +112,16 @@ def _gate(t):
 
 class ChunkScan(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, q, k, v, beta, g, gmu, gnu, rule, ns, eps):
+    def forward(ctx, q, k, v, beta, g, gmu, gnu, rule, ns, eps, record):
         _check(q, k, v, beta, g, gmu, gnu, rule)
         lib = nat.load()
         qc, kc, vc = _tok(q.detach()), _tok(k.detach()), _tok(v.detach())
         bc, gc, mc, nc = _gate(beta), _gate(g), _gate(gmu), _gate(gnu)
         o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
         desc = _desc(qc, kc, vc, o, rule, ns, eps)
-        need_grad = any(ctx.needs_input_grad[:7])
+        # `record`: grad mode was on at the call (inside forward it is always
+        # off, and needs_input_grad ignores it), so a backward may follow
+        need_grad = record and any(ctx.needs_input_grad[:7])
         states = None
         if need_grad:
             nbytes = lib.gmdn_chunk_states_bytes(desc)
@@ -157,7 +159,7 @@ class ChunkScan(torch.autograd.Function):
                                     nat.ptr(dgnu), nat.ptr(ws), ws_bytes, nat.stream_of(qc))
         nat.check(rc, "gmdn_chunk_bwd")
         gates = [None if t is None else t.to(dt) for t, dt in zip((dbeta, dg, dgmu, dgnu), ctx.gate_dtypes)]
-        return (dq, dk, dv, *gates, None, None, None)
+        return (dq, dk, dv, *gates, None, None, None, None)
 
 
 def _muon_core(q, k, v, beta, g, gmu, ns):
@@ -197,4 +199,5 @@ def chunk_scan(q, k, v, beta, g, gmu=None, gnu=None, *, rule="delta", ns: int = 
     if r == 1:
         _check(q, k, v, beta, g, gmu, gnu, r)
         return _muon_core(q, k, v, beta, g, gmu, ns)
-    return ChunkScan.apply(q, k, v, beta, g, gmu if r >= 1 else None, gnu if r == 2 else None, r, ns, eps)
+    return ChunkScan.apply(q, k, v, beta, g, gmu if r >= 1 else None, gnu if r == 2 else None, r, ns, eps,
+                           torch.is_grad_enabled())

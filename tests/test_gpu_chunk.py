@@ -88,6 +88,21 @@ def test_adam_config():
     assert excess <= TOL
 
 
+def test_inference_forward_matches_training_forward():
+    """Under torch.no_grad the forward writes no state checkpoint (nothing
+    will read it); its output is bit-identical to the forward that does."""
+    dev = _dev()
+    w = Workload("t", "delta", 2, 4, 512, 128)
+    inp = make_inputs(w, seed=3, with_grad_out=False)
+    xs = [inp[n].to(dev).requires_grad_(True) for n in ("q", "k", "v", "beta", "g")]
+    o_train = gc.chunk_scan(*xs, rule="delta")
+    with torch.no_grad():
+        o_infer = gc.chunk_scan(*xs, rule="delta")
+    torch.cuda.synchronize()
+    assert o_train.grad_fn is not None and o_infer.grad_fn is None
+    assert torch.equal(o_train.detach(), o_infer)
+
+
 def test_strided_head_interleaved_layout():
     """q, k, v as (B, T, H, d) storage viewed as (B, H, T, d), the layout the
     mixer's projection produces (train_ablation.py:127-129)."""
