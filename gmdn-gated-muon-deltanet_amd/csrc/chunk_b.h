@@ -43,13 +43,6 @@ GMDN_DEV void map_block(int64_t BH, int nblk, int64_t& bh, int& blk) {
   }
 }
 
-// Byte offset of element (r, c) of a swizzled bf16 tile (c % 4 == 0 for the
-// 8-byte pieces the kernels read).
-template <class L>
-GMDN_DEV uint32_t swz_off(int r, int c) {
-  return (uint32_t)(2 * L::off(r, c));
-}
-
 hipError_t chunk_fwd_launch(const ChunkArgs& a, int d, int rule, hipStream_t s);
 hipError_t chunk_bwd_launch(const ChunkArgs& a, int d, int rule, hipStream_t s);
 

@@ -150,4 +150,142 @@ struct NSBlock {
   }
 };
 
+// The forward quintic step with bf16x3 products and the shared matrices kept
+// as split bf16 planes in LDS (hi plane then lo plane, each D x D in the
+// 16-byte-group XOR swizzle of the chunk kernels).  The publishing wave splits
+// its own rows once; every operand read is then two 8-byte row reads or two
+// transposing reads per plane, in the pair k order of the register operands.
+// A row's swizzle depends only on the row modulo 16, so each lane keeps one
+// LDS base per distinct column pattern and row tiles are immediate offsets.
+template <int D>
+struct NSSplit {
+  static constexpr int NT = D / 16;
+  static constexpr int NKB = D / 32;
+  static constexpr uint32_t PLANE = (uint32_t)D * D * 2;  // bytes of one plane
+  static constexpr uint32_t BYTES = 2 * PLANE;             // one published matrix
+  static constexpr uint32_t ROWB = D * 2;                  // bytes per row of a plane
+  using L = BSwz<D>;
+  using P = PrecX3;
+  using Op = P::Op;
+  static_assert(L::MASK < 16, "row tiles of 16 must keep the swizzle");
+
+  uint32_t prow[NKB][2];  // row reads: row lc, columns 32 kb + 16 h + 4G
+  uint32_t pcol[NT];      // column reads: row 4G + lc/4, columns 16 tc + 4 (lc & 3)
+  uint32_t ppub[NT];      // publishing: row 16 w + lc, columns 16 c + 4G
+
+  GMDN_DEV NSSplit() {
+    const int l = lane_id(), lc = l & 15, G = l >> 4, w = wave_id();
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) prow[kb][h] = swz_off<L>(lc, 32 * kb + 16 * h + 4 * G);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      pcol[t] = swz_off<L>(4 * G + (lc >> 2), 16 * t + 4 * (lc & 3));
+      ppub[t] = swz_off<L>(16 * w + lc, 16 * t + 4 * G);
+    }
+  }
+
+  template <int N>
+  static GMDN_DEV void pack_all(const f32x4 (&t)[N], Op (&o)[N / 2]) {
+#pragma unroll
+    for (int kb = 0; kb < N / 2; ++kb) o[kb] = P::pack(t[2 * kb], t[2 * kb + 1]);
+  }
+  // All NTHR threads: a row-major fp32 D x D matrix in global memory -> split
+  // planes at m (16-byte loads; thread j takes pieces j, j + NTHR, ...).
+  template <int NTHR>
+  static GMDN_DEV void stage(lds_ptr m, const float* g) {
+    constexpr int PR = D / 4;  // 4-float pieces per row
+    static_assert((D * PR) % NTHR == 0 && NTHR % PR == 0 && (NTHR / PR) % 16 == 0,
+                  "pieces split evenly, in row steps that keep the swizzle");
+    const int j = threadIdx.x, r = j / PR, c = (j % PR) * 4;
+    const float* src = g + r * D + c;
+    const uint32_t dst = swz_off<L>(r, c);
+    constexpr int NQ = D * PR / NTHR, RSTEP = NTHR / PR;
+    f32x4 x[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) x[q] = *reinterpret_cast<const f32x4*>(src + q * RSTEP * D);
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      bf16x4 hi, lo;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        bf16 h_, l_;
+        split2(x[q][e], h_, l_);
+        hi[e] = h_;
+        lo[e] = l_;
+      }
+      lds_st<bf16x4>(m + (dst + q * RSTEP * ROWB), hi);
+      lds_st<bf16x4>(m + (dst + q * RSTEP * ROWB + PLANE), lo);
+    }
+  }
+  // the wave's rows 16 w .. 16 w + 15 (D-layout tiles t of M^T) -> planes at m
+  GMDN_DEV void publish(lds_ptr m, const f32x4 (&t)[NT]) const {
+#pragma unroll
+    for (int c = 0; c < NT; ++c) {
+      bf16x4 hi, lo;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        bf16 h_, l_;
+        split2(t[c][j], h_, l_);
+        hi[j] = h_;
+        lo[j] = l_;
+      }
+      lds_st<bf16x4>(m + ppub[c], hi);
+      lds_st<bf16x4>(m + (ppub[c] + PLANE), lo);
+    }
+  }
+  // lane (r, G) takes M[16 tr + r][32 kb + pair(G, s)]
+  GMDN_DEV Op row(lds_cptr m, int tr, int kb) const {
+    const lds_cptr a = m + prow[kb][0] + tr * 16 * ROWB, b = m + prow[kb][1] + tr * 16 * ROWB;
+    Op o;
+    o.hi = cat8(lds_ld<bf16x4>(a), lds_ld<bf16x4>(b));
+    o.lo = cat8(lds_ld<bf16x4>(a + PLANE), lds_ld<bf16x4>(b + PLANE));
+    return o;
+  }
+  // lane (c, G) takes M[32 kb + pair(G, s)][16 tc + c]
+  GMDN_DEV Op col(lds_cptr m, int kb, int tc) const {
+    const lds_cptr a = m + pcol[tc] + kb * 32 * ROWB, b = a + 16 * ROWB;
+    Op o;
+    o.hi = cat8(lds_tr16(a), lds_tr16(b));
+    o.lo = cat8(lds_tr16(a + PLANE), lds_tr16(b + PLANE));
+    return o;
+  }
+  GMDN_DEV f32x4 rowprod(lds_cptr pub, int tr, const Op (&B)[NKB]) const {
+    f32x4 acc = zero4();
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) acc = P::mma(row(pub, tr, kb), B[kb], acc);
+    return acc;
+  }
+  GMDN_DEV f32x4 colprod(lds_cptr pub, int tc, const Op (&B)[NKB], f32x4 acc) const {
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) acc = P::mma(col(pub, kb, tc), B[kb], acc);
+    return acc;
+  }
+  // One quintic step on the wave's rows XT (D-layout tiles of X^T); the same
+  // products as NSBlock::step.
+  GMDN_DEV void step(f32x4 (&XT)[NT], lds_ptr XM, lds_ptr PM) const {
+    publish(XM, XT);
+    __syncthreads();
+    Op Bx[NKB];
+    pack_all(XT, Bx);
+    f32x4 Pc[NT];
+#pragma unroll
+    for (int tr = 0; tr < NT; ++tr) Pc[tr] = rowprod(XM, tr, Bx);
+    // P is symmetric: the column block is also the wave's rows of P
+    publish(PM, Pc);
+    __syncthreads();
+    Op Bp[NKB];
+    pack_all(Pc, Bp);
+    // Z = b P + c P^2, in place of the wave's block of P (now held by Bp)
+#pragma unroll
+    for (int tr = 0; tr < NT; ++tr) Pc[tr] = NS_B * Pc[tr] + NS_C * rowprod(PM, tr, Bp);
+    Op Bz[NKB];
+    pack_all(Pc, Bz);
+#pragma unroll
+    for (int tc = 0; tc < NT; ++tc) XT[tc] = colprod(XM, tc, Bz, NS_A * XT[tc]);
+    __syncthreads();
+  }
+};
+
 }  // namespace gmdn

@@ -4,8 +4,9 @@
 // M (D-layout tiles of the transposes) and the waves cooperate on the
 // Newton-Schulz iterations through shared matrices.
 //
-// Forward: X and P live in swizzled LDS (2 D^2 fp32); K_i is read straight
-// from global memory (it is used once per chunk).
+// Forward: X and P live in LDS (2 D^2 fp32 worth): as split bf16 planes for
+// the bf16x3 precision, as swizzled fp32 for the exact one; K_i is read
+// straight from global memory (it is used once per chunk).
 // Backward: X_k, P, Xbar and Bbar (4 D^2) exceed LDS at D = 128, so they live
 // in a per-(b, h) global workspace (L2 resident), followed by the ns stored
 // iterates X_0 .. X_{ns-1} (written and re-read by the same lanes).
@@ -37,6 +38,7 @@ scan_fwd_muon(const float* __restrict__ U, const float* __restrict__ K,
   f32x4 S[NT], M[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) S[t] = M[t] = zero4();
+  const NSSplit<D> nsx;  // per-lane LDS bases of the bf16x3 engine
 
   for (int i = 0; i < N; ++i) {
     const int64_t si = bh * N + i;
@@ -50,12 +52,23 @@ scan_fwd_muon(const float* __restrict__ U, const float* __restrict__ K,
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) Bop[kb] = P::pack(-S[2 * kb], -S[2 * kb + 1]);
     const float a = av[si], b = bv[si], m = mv[si];
+    if constexpr (PREC == 0) {
+      // K_i as split planes in the P store (free until the first NS step
+      // publishes P), read back as column operands
+      NSSplit<D>::template stage<D * 4>(lds_base(smem) + NSSplit<D>::BYTES, Ki);
+      __syncthreads();
+    }
     float sq = 0.f;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       f32x4 g = *reinterpret_cast<const f32x4*>((U + si * mat + roff(t)));
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) g = P::mma(col_op<P, PlainMat<D>>(Ki, 32 * kb, 16 * t), Bop[kb], g);
+      for (int kb = 0; kb < NKB; ++kb) {
+        if constexpr (PREC == 0)
+          g = P::mma(nsx.col(lds_base(smem) + NSSplit<D>::BYTES, kb, t), Bop[kb], g);
+        else
+          g = P::mma(col_op<P, PlainMat<D>>(Ki, 32 * kb, 16 * t), Bop[kb], g);
+      }
       M[t] = m * M[t] + g;
       sq += M[t][0] * M[t][0] + M[t][1] * M[t][1] + M[t][2] * M[t][2] + M[t][3] * M[t][3];
     }
@@ -63,7 +76,12 @@ scan_fwd_muon(const float* __restrict__ U, const float* __restrict__ K,
     f32x4 X[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) X[t] = M[t] * scale;
-    for (int s = 0; s < ns; ++s) NS::step(X, XM, PM);
+    if constexpr (PREC == 0) {
+      const lds_ptr base = lds_base(smem);
+      for (int s = 0; s < ns; ++s) nsx.step(X, base, base + NSSplit<D>::BYTES);
+    } else {
+      for (int s = 0; s < ns; ++s) NS::step(X, XM, PM);
+    }
 #pragma unroll
     for (int t = 0; t < NT; ++t) S[t] = a * S[t] + b * X[t];
   }

@@ -113,6 +113,13 @@ struct BSwz {
   static GMDN_DEV int off(int r, int c) { return r * COLS + ((((c >> 3) ^ (r & MASK)) << 3) | (c & 7)); }
 };
 
+// Byte offset of element (r, c) of a swizzled bf16 tile (c % 4 == 0 for the
+// 8-byte pieces the kernels read).
+template <class L>
+GMDN_DEV uint32_t swz_off(int r, int c) {
+  return (uint32_t)(2 * L::off(r, c));
+}
+
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 // lane (r, G) takes X[r0 + r][k0 + pair(G, s)], s = 0..7
