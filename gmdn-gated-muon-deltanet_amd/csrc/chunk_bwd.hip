@@ -913,35 +913,42 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
     *reinterpret_cast<bf16x4*>(Ah + ao) = ah;
     *reinterpret_cast<bf16x4*>(Al + ao) = al;
   }
-  wait_vmem();  // the rows of S_i and Gb_i
-  __syncthreads();
+  __syncthreads();  // the A planes published (the state rows may still be arriving)
 
   // ---------------- phase I: E^T, (Gb K^T) and dE^T for this wave's 16 state rows
   Op<2> Sa[NKB], Ga[NKB];  // rows r0 + lc of S_i, Gb_i (m = r, k = c natural); reused in IIb
   {
-#pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) {
-      Sa[kb] = join_pieces(srow[kb][0], srow[kb][1]);
-      Ga[kb] = join_pieces(grow[kb][0], grow[kb][1]);
-    }
-    // the loop below has no cross-lane step, so the LDS reads of one token
-    // tile overlap the MFMA chains of the previous one
     float ws[4], dbp[4];
 #pragma unroll
     for (int st = 0; st < 4; ++st) ws[st] = RULE == 0 ? rbeta[16 * st + lc] : 1.f;
+    // column block by column block: the MFMA chains of block kb start as soon
+    // as its rows have landed (the loads complete in issue order)
+    f32x4 Ets[4], GKs[4];
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
       // D layout: lane (s, G) holds rows r0 + 4G + jj
       const bf16x4 vv = *reinterpret_cast<const bf16x4*>(Vs + LQ::off(16 * st + lc, r0 + 4 * G));
-      f32x4 Et = f32x4{-(float)vv[0], -(float)vv[1], -(float)vv[2], -(float)vv[3]};
-      f32x4 GK = zero4();
+      Ets[st] = f32x4{-(float)vv[0], -(float)vv[1], -(float)vv[2], -(float)vv[3]};
+      GKs[st] = zero4();
+    }
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) {
+    for (int kb = 0; kb < NKB; ++kb) {
+      Sa[kb] = join_pieces(srow[kb][0], srow[kb][1]);
+      Ga[kb] = join_pieces(grow[kb][0], grow[kb][1]);
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
         const Op<1> kr{{row8<LQ>(Ks, 16 * st + lc, 32 * kb)}};
-        Et = mma<2, 1>(Sa[kb], kr, Et);
-        GK = mma<2, 1>(Ga[kb], kr, GK);
+        Ets[st] = mma<2, 1>(Sa[kb], kr, Ets[st]);
+        GKs[st] = mma<2, 1>(Ga[kb], kr, GKs[st]);
       }
-      Et = -Et;  // E^T = V^T - S K^T
+      __builtin_amdgcn_sched_barrier(0);  // keep each block's wait after the previous block's MFMAs
+    }
+    // the loop below has no cross-lane step, so the LDS reads of one token
+    // tile overlap the MFMA chains of the previous one
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const f32x4 Et = -Ets[st];  // E^T = V^T - S K^T
+      const f32x4 GK = GKs[st];
       dbp[st] = dot4(Et, GK);  // dbeta's diag(w) term, this lane's 4 rows
       f32x4 dEt = GK * ws[st];
 #pragma unroll
