@@ -131,6 +131,182 @@ scan_fwd_rows(const float* __restrict__ U, const float* __restrict__ K,
   }
 }
 
+// ------------------------------------- forward, 8 waves per 32 rows (bf16x3)
+// The same recurrence with one workgroup of 8 waves per 32 rows of S: wave
+// (rt, cq) holds rows 32 blk + 16 rt + lc and column quarter cq as D-layout
+// tiles of S^T.  The contraction G = U - S K runs over all columns of S, so
+// the workgroup's rows are exchanged each chunk as split bf16 planes in LDS;
+// K_i is staged once per chunk, as split bf16 planes (double buffered), by
+// all 512 threads from fp32 loads issued one chunk ahead.  Every MFMA operand
+// is then a plain LDS read.
+template <int D>
+struct Rows8Lds {
+  static constexpr int PLANE = D * D * 2;   // one bf16 plane of K_i (bytes)
+  static constexpr int K0 = 0;              // [buffer][hi | lo]
+  static constexpr int XSP = 32 * D * 2;    // the workgroup's S rows, one plane
+  static constexpr int XS0 = K0 + 4 * PLANE;
+  static constexpr int BYTES = XS0 + 2 * XSP;
+  static_assert(BYTES <= 160 * 1024, "row scan LDS exceeds the 160 KiB of a CU");
+};
+constexpr int A8_THREADS = 512;
+
+template <int D, int RULE>
+__global__ void __launch_bounds__(A8_THREADS)
+scan_fwd_rows8(const float* __restrict__ U, const float* __restrict__ K,
+               const float* __restrict__ av, const float* __restrict__ bv,
+               const float* __restrict__ mv, const float* __restrict__ nv,
+               float* __restrict__ S_all, float* __restrict__ M_all,
+               float* __restrict__ V_all, int64_t BH, int N) {
+  using L = BSwz<D>;
+  using R = Rows8Lds<D>;
+  using P = PrecX3;
+  constexpr int NKB = D / 32;                // k-blocks over all columns of S
+  constexpr int TPW = D / 64;                // column tiles per wave
+  constexpr int ROWB = D * 2;                // bytes per row of a plane
+  constexpr int PR = D / 4;                  // fp32 pieces per row of K
+  constexpr int NQ = D * PR / A8_THREADS;    // pieces of K_i per thread
+  constexpr int RSTEP = A8_THREADS / PR;     // rows between a thread's pieces
+  static_assert(NQ * A8_THREADS == D * PR && RSTEP % 16 == 0, "K pieces split in swizzle-keeping row steps");
+  extern __shared__ __align__(16) float smem[];
+
+  int64_t bh;
+  int blk;
+  map_rows_block(BH, D / 32, bh, blk);
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = lane_id(), G = l >> 4, lc = l & 15;
+  const int rt = w >> 2, cq = w & 3;
+  const int row = 32 * blk + 16 * rt + lc;   // this lane's row of S
+  const int64_t mat = (int64_t)D * D;
+  const float* Ub = U + bh * N * mat;
+  const float* Kb = K + bh * N * mat;
+  const lds_ptr L0 = lds_base(smem);
+
+  // per-lane LDS offsets (row tiles, k-blocks and planes are immediates)
+  uint32_t kcol[TPW], xsw[TPW], xsr[NKB][2];
+#pragma unroll
+  for (int u = 0; u < TPW; ++u) {
+    const int ct = cq * TPW + u;
+    kcol[u] = swz_off<L>(4 * G + (lc >> 2), 16 * ct + 4 * (lc & 3));
+    xsw[u] = swz_off<L>(16 * rt + lc, 16 * ct + 4 * G);
+  }
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) xsr[kb][h] = swz_off<L>(16 * rt + lc, 32 * kb + 16 * h + 4 * G);
+  // K staging: thread j takes pieces (j / PR + q RSTEP, 4 (j % PR))
+  const int kr = threadIdx.x / PR, kc = (threadIdx.x % PR) * 4;
+  const uint32_t kdst = swz_off<L>(kr, kc);
+  const int64_t ksrc = (int64_t)kr * D + kc;
+  auto roff = [&](int u) { return (int64_t)row * D + 16 * (cq * TPW + u) + 4 * G; };
+
+  f32x4 Kpre[NQ];
+  auto load_k = [&](int i) {
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) Kpre[q] = *reinterpret_cast<const f32x4*>(Kb + i * mat + ksrc + q * RSTEP * D);
+  };
+  auto stage_k = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      bf16x4 hi, lo;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        bf16 h_, l_;
+        split2(Kpre[q][e], h_, l_);
+        hi[e] = h_;
+        lo[e] = l_;
+      }
+      const uint32_t o = R::K0 + buf * 2 * R::PLANE + kdst + q * RSTEP * ROWB;
+      lds_st<bf16x4>(L0 + o, hi);
+      lds_st<bf16x4>(L0 + (o + R::PLANE), lo);
+    }
+  };
+
+  f32x4 S[TPW], M[TPW], V[TPW], Unext[TPW];
+#pragma unroll
+  for (int u = 0; u < TPW; ++u) S[u] = M[u] = V[u] = Unext[u] = zero4();
+  if (N > 0) {
+    load_k(0);
+    stage_k(0);
+#pragma unroll
+    for (int u = 0; u < TPW; ++u) Unext[u] = *reinterpret_cast<const f32x4*>(Ub + roff(u));
+  }
+  if (N > 1) load_k(1);
+  __syncthreads();
+
+  for (int i = 0; i < N; ++i) {
+    const int buf = i & 1;
+    const int64_t si = bh * N + i;
+    f32x4 Ucur[TPW];
+#pragma unroll
+    for (int u = 0; u < TPW; ++u) {
+      Ucur[u] = Unext[u];
+      // pre-update state (and adam's moments)
+      *reinterpret_cast<f32x4*>(S_all + si * mat + roff(u)) = S[u];
+      if constexpr (RULE == 2) {
+        if (M_all) *reinterpret_cast<f32x4*>(M_all + si * mat + roff(u)) = M[u];
+        if (V_all) *reinterpret_cast<f32x4*>(V_all + si * mat + roff(u)) = V[u];
+      }
+      // this wave's split S tile -> the exchange planes
+      bf16x4 hi, lo;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        bf16 h_, l_;
+        split2(S[u][j], h_, l_);
+        hi[j] = h_;
+        lo[j] = l_;
+      }
+      lds_st<bf16x4>(L0 + (R::XS0 + xsw[u]), hi);
+      lds_st<bf16x4>(L0 + (R::XS0 + xsw[u] + R::XSP), lo);
+    }
+    __syncthreads();  // S rows published (K_i staged by the last barrier)
+    // B operands: this lane's row of S over every k-block (pair order)
+    P::Op Sop[NKB];
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      Sop[kb].hi = cat8(lds_ld<bf16x4>(L0 + (R::XS0 + xsr[kb][0])), lds_ld<bf16x4>(L0 + (R::XS0 + xsr[kb][1])));
+      Sop[kb].lo = cat8(lds_ld<bf16x4>(L0 + (R::XS0 + R::XSP + xsr[kb][0])),
+                        lds_ld<bf16x4>(L0 + (R::XS0 + R::XSP + xsr[kb][1])));
+    }
+    const float a = av[si];
+    float b = 0.f, m = 0.f, n = 0.f;
+    if constexpr (RULE == 2) {
+      b = bv[si];
+      m = mv[si];
+      n = nv[si];
+    }
+#pragma unroll
+    for (int u = 0; u < TPW; ++u) {
+      // (S K)^T tile: A = K^T (column reads of K_i), B = S^T
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+        const uint32_t o = R::K0 + buf * 2 * R::PLANE + kcol[u] + kb * 32 * ROWB;
+        P::Op A;
+        A.hi = cat8(lds_tr16(L0 + o), lds_tr16(L0 + (o + 16 * ROWB)));
+        A.lo = cat8(lds_tr16(L0 + (o + R::PLANE)), lds_tr16(L0 + (o + R::PLANE + 16 * ROWB)));
+        acc = P::mma(A, Sop[kb], acc);
+      }
+      const f32x4 g = Ucur[u] - acc;  // G^T = U^T - K^T S^T
+      if constexpr (RULE == 0) {
+        S[u] = a * S[u] + g;
+      } else {
+        M[u] = m * M[u] + (1.f - m) * g;
+        V[u] = n * V[u] + (1.f - n) * g * g;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) S[u][j] = a * S[u][j] + b * M[u][j] / (sqrtf(V[u][j]) + 1e-6f);
+      }
+    }
+    // K_{i+1} into the other buffer (last read in chunk i-1); loads of K_{i+2}, U_{i+1}
+    if (i + 1 < N) {
+      stage_k(buf ^ 1);
+#pragma unroll
+      for (int u = 0; u < TPW; ++u) Unext[u] = *reinterpret_cast<const f32x4*>(Ub + (i + 1) * mat + roff(u));
+    }
+    if (i + 2 < N) load_k(i + 2);
+    __syncthreads();  // K_{i+1} staged; the exchange planes free
+  }
+}
+
 // Reverse scan for the row-separable rules.  Writes dU (= Gb) for every
 // chunk, and for adam the per-row-tile partial sums of da, db, dm, dn into
 // part[(bh*N + i) * n_tiles + tile][4]; delta's da is formed later from dU
@@ -373,9 +549,23 @@ hipError_t scan_bwd_dk_launch(const ScanArgs& s, const float* part) {
   return hipErrorInvalidValue;
 }
 
+template <int D, int RULE>
+static hipError_t launch_fwd_rows8(const ScanArgs& s) {
+  const int lds = Rows8Lds<D>::BYTES;
+  auto kern = scan_fwd_rows8<D, RULE>;
+  hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, dim3((unsigned)(s.BH * (D / 32))), dim3(A8_THREADS), lds, s.stream, s.U, s.K, s.a,
+                     s.b, s.m, s.n, s.S_all, s.M_all, s.V_all, s.BH, (int)s.N);
+  return hipGetLastError();
+}
+
 template <int D, int PREC>
 static hipError_t fwd_rows_rule(const ScanArgs& s) {
-  return s.rule == 0 ? launch_fwd_rows<D, 0, PREC>(s) : launch_fwd_rows<D, 2, PREC>(s);
+  if constexpr (PREC == 0 && D >= 64)  // bf16x3: the 8-wave kernel
+    return s.rule == 0 ? launch_fwd_rows8<D, 0>(s) : launch_fwd_rows8<D, 2>(s);
+  else
+    return s.rule == 0 ? launch_fwd_rows<D, 0, PREC>(s) : launch_fwd_rows<D, 2, PREC>(s);
 }
 template <int D, int PREC>
 static hipError_t bwd_rows_rule(const ScanArgs& s, float* part) {
