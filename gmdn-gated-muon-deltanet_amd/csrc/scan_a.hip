@@ -490,6 +490,135 @@ scan_bwd_dk(const float* __restrict__ S_all, const float* __restrict__ dU,
   // RULE == 1: the muon backward kernel writes the scalar gradients itself
 }
 
+// The chunk-parallel part with 8 waves: S_i and Gb_i staged as split bf16
+// planes (loaded as 16-byte fp32 pieces by all threads, which also form
+// delta's da = <Gb_i, S_i> in fp32 on the way), every operand a transposing
+// LDS read, and each output tile formed transposed, (Gb^T S)[c][c'] =
+// -dK[c'][c], so that a lane writes four consecutive columns of dK.
+template <int D>
+struct Dk8Lds {
+  static constexpr int PLANE = D * D * 2;
+  static constexpr int S0 = 0;          // S_i hi, lo
+  static constexpr int G0 = 2 * PLANE;  // Gb_i hi, lo
+  static constexpr int RED = 4 * PLANE; // per-wave partial sums
+  static constexpr int BYTES = RED + 8 * 4;
+  static_assert(BYTES <= 160 * 1024, "dK LDS exceeds the 160 KiB of a CU");
+};
+
+template <int D, int RULE>
+__global__ void __launch_bounds__(A8_THREADS)
+scan_bwd_dk8(const float* __restrict__ S_all, const float* __restrict__ dU,
+             const float* __restrict__ part, float* __restrict__ dK,
+             float* __restrict__ da, float* __restrict__ db, float* __restrict__ dm,
+             float* __restrict__ dn, int64_t BH, int N) {
+  using L = BSwz<D>;
+  using R = Dk8Lds<D>;
+  using P = PrecX3;
+  constexpr int NT = D / 16;
+  constexpr int NKB = D / 32;
+  constexpr int ROWB = D * 2;
+  constexpr int PR = D / 4;
+  constexpr int NQ = D * PR / A8_THREADS;
+  constexpr int RSTEP = A8_THREADS / PR;
+  constexpr int NW = A8_THREADS / 64;
+  static_assert(NQ * A8_THREADS == D * PR && RSTEP % 16 == 0, "pieces split in swizzle-keeping row steps");
+  static_assert((NT * NT) % NW == 0, "output tiles split evenly over the waves");
+  extern __shared__ __align__(16) float smem[];
+  const lds_ptr L0 = lds_base(smem);
+  const int64_t si = blockIdx.x;  // = bh * N + i
+  const int64_t mat = (int64_t)D * D;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = lane_id(), G = l >> 4, lc = l & 15;
+
+  // ---- staging (and delta's da from the fp32 values)
+  {
+    const int kr = threadIdx.x / PR, kc = (threadIdx.x % PR) * 4;
+    const float* sg = S_all + si * mat + (int64_t)kr * D + kc;
+    const float* gg = dU + si * mat + (int64_t)kr * D + kc;
+    const uint32_t dst = swz_off<L>(kr, kc);
+    f32x4 xs[NQ], xg[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      xs[q] = *reinterpret_cast<const f32x4*>(sg + q * RSTEP * D);
+      xg[q] = *reinterpret_cast<const f32x4*>(gg + q * RSTEP * D);
+    }
+    float dot = 0.f;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const uint32_t o = dst + q * RSTEP * ROWB;
+      bf16x4 hi, lo;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        bf16 h_, l_;
+        split2(xs[q][e], h_, l_);
+        hi[e] = h_;
+        lo[e] = l_;
+      }
+      lds_st<bf16x4>(L0 + (R::S0 + o), hi);
+      lds_st<bf16x4>(L0 + (R::S0 + R::PLANE + o), lo);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        bf16 h_, l_;
+        split2(xg[q][e], h_, l_);
+        hi[e] = h_;
+        lo[e] = l_;
+      }
+      lds_st<bf16x4>(L0 + (R::G0 + o), hi);
+      lds_st<bf16x4>(L0 + (R::G0 + R::PLANE + o), lo);
+      if constexpr (RULE == 0) dot += xs[q][0] * xg[q][0] + xs[q][1] * xg[q][1] + xs[q][2] * xg[q][2] + xs[q][3] * xg[q][3];
+    }
+    if constexpr (RULE == 0) {
+      dot = wave_sum(dot);
+      if (l == 0) reinterpret_cast<float*>(smem + R::RED / 4)[w] = dot;
+    }
+  }
+  __syncthreads();
+
+  // ---- dK tiles: (Gb^T S) tile (tc, tr) = -dK^T; A = Gb columns, B = S columns
+  uint32_t pcol[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) pcol[t] = swz_off<L>(4 * G + (lc >> 2), 16 * t + 4 * (lc & 3));
+  auto colop = [&](uint32_t base, int kb, int t) {
+    const uint32_t o = base + pcol[t] + kb * 32 * ROWB;
+    P::Op x;
+    x.hi = cat8(lds_tr16(L0 + o), lds_tr16(L0 + (o + 16 * ROWB)));
+    x.lo = cat8(lds_tr16(L0 + (o + R::PLANE)), lds_tr16(L0 + (o + R::PLANE + 16 * ROWB)));
+    return x;
+  };
+  float* const dKi = dK + si * mat;
+#pragma unroll
+  for (int q = 0; q < NT * NT / NW; ++q) {
+    const int tile = w + NW * q, tr = tile / NT, tc = tile % NT;
+    f32x4 acc = zero4();
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) acc = P::mma(colop(R::G0, kb, tc), colop(R::S0, kb, tr), acc);
+    // lane (c', G) holds (Gb^T S)[16 tc + 4G + j][16 tr + c'] = -dK[16 tr + c'][16 tc + 4G + j]
+    *reinterpret_cast<f32x4*>(dKi + (int64_t)(16 * tr + lc) * D + 16 * tc + 4 * G) = -acc;
+  }
+
+  // ---- scalar gradients of the chunk
+  if constexpr (RULE == 0) {
+    if (threadIdx.x == 0) {
+      const float* red = reinterpret_cast<const float*>(smem + R::RED / 4);
+      float t = 0.f;
+#pragma unroll
+      for (int q = 0; q < NW; ++q) t += red[q];
+      da[si] = t;
+      db[si] = 0.f;
+      dm[si] = 0.f;
+      dn[si] = 0.f;
+    }
+  } else if constexpr (RULE == 2) {
+    if (threadIdx.x < 4) {
+      float t = 0.f;
+      for (int q = 0; q < D / 16; ++q) t += part[(si * (D / 16) + q) * 4 + threadIdx.x];
+      float* dst = threadIdx.x == 0 ? da : threadIdx.x == 1 ? db : threadIdx.x == 2 ? dm : dn;
+      dst[si] = t;
+    }
+  }
+  // RULE == 1: the muon backward kernel writes the scalar gradients itself
+}
+
 // ---------------------------------------------------------------- launchers
 template <int D, int RULE, int PREC>
 static hipError_t launch_fwd_rows(const ScanArgs& s) {
@@ -517,6 +646,15 @@ static hipError_t launch_bwd_rows(const ScanArgs& s, float* part) {
 
 template <int D, int RULE, int PREC>
 static hipError_t launch_bwd_dk(const ScanArgs& s, const float* part) {
+  if constexpr (PREC == 0 && D >= 64) {  // bf16x3: the 8-wave kernel
+    const int lds = Dk8Lds<D>::BYTES;
+    auto k8 = scan_bwd_dk8<D, RULE>;
+    hipError_t e = hipFuncSetAttribute((const void*)k8, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k8, dim3((unsigned)(s.BH * s.N)), dim3(A8_THREADS), lds, s.stream, s.S_all, s.dU, part,
+                       s.dK, s.da, s.db, s.dm, s.dn, s.BH, (int)s.N);
+    return hipGetLastError();
+  }
   const size_t lds = 2 * (size_t)D * D * sizeof(float);
   auto k2 = scan_bwd_dk<D, RULE, PREC>;
   hipError_t e = hipFuncSetAttribute((const void*)k2, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
