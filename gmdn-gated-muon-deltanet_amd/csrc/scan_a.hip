@@ -420,6 +420,246 @@ scan_bwd_rows(const float* __restrict__ U, const float* __restrict__ K,
   }
 }
 
+// ------------------------------------ reverse scan, 8 waves per 32 rows (bf16x3)
+// Wave (rt, cq) holds rows 32 blk + 16 rt + lc and column quarter cq of Sb as
+// D-layout tiles of Sb^T (adam: also of its moment adjoints).  Per chunk the
+// workgroup's -Gb rows are exchanged as split bf16 planes in LDS, since the
+// update Sb <- a Sb - Gb K^T + gS contracts over every column of Gb; K_i is
+// staged as split planes (double buffered) by all threads from fp32 loads
+// issued one chunk ahead, read by rows for that update and by columns (adam)
+// for recomputing G = U - S_i K_i, whose S_i row pieces a lane loads itself in
+// the operand's k order.  Every chunk operand (gS, and adam's U, M, V, S_i)
+// is loaded one chunk ahead.
+template <int D, int RULE>
+__global__ void __launch_bounds__(A8_THREADS)
+scan_bwd_rows8(const float* __restrict__ U, const float* __restrict__ K,
+               const float* __restrict__ av, const float* __restrict__ bv,
+               const float* __restrict__ mv, const float* __restrict__ nv,
+               const float* __restrict__ S_all, const float* __restrict__ M_all,
+               const float* __restrict__ V_all, const float* __restrict__ gS,
+               float* __restrict__ dU, float* __restrict__ part, int64_t BH, int N) {
+  using L = BSwz<D>;
+  using R = Rows8Lds<D>;
+  using P = PrecX3;
+  constexpr int NKB = D / 32;
+  constexpr int TPW = D / 64;
+  constexpr int ROWB = D * 2;
+  constexpr int PR = D / 4;
+  constexpr int NQ = D * PR / A8_THREADS;
+  constexpr int RSTEP = A8_THREADS / PR;
+  constexpr int NTILES = D / 16;
+  constexpr int RED = R::BYTES;  // adam: [rt][cq][4] partial sums after the planes
+  static_assert(NQ * A8_THREADS == D * PR && RSTEP % 16 == 0, "K pieces split in swizzle-keeping row steps");
+  static_assert(RULE == 0 || R::BYTES + 32 * 4 <= 160 * 1024, "adam partial sums exceed the LDS");
+  extern __shared__ __align__(16) float smem[];
+
+  int64_t bh;
+  int blk;
+  map_rows_block(BH, D / 32, bh, blk);
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = lane_id(), G = l >> 4, lc = l & 15;
+  const int rt = w >> 2, cq = w & 3;
+  const int row = 32 * blk + 16 * rt + lc;
+  const int64_t mat = (int64_t)D * D;
+  const float* Kb = K + bh * N * mat;
+  const lds_ptr L0 = lds_base(smem);
+
+  // per-lane LDS offsets: K rows 16 ct + lc over k-block kb (both halves of
+  // the pair order), K columns (adam), exchange-plane writes and reads
+  uint32_t krow[NKB][2], kcol[TPW], xsw[TPW], xsr[NKB][2];
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      krow[kb][h] = swz_off<L>(lc, 32 * kb + 16 * h + 4 * G);
+      xsr[kb][h] = swz_off<L>(16 * rt + lc, 32 * kb + 16 * h + 4 * G);
+    }
+#pragma unroll
+  for (int u = 0; u < TPW; ++u) {
+    const int ct = cq * TPW + u;
+    kcol[u] = swz_off<L>(4 * G + (lc >> 2), 16 * ct + 4 * (lc & 3));
+    xsw[u] = swz_off<L>(16 * rt + lc, 16 * ct + 4 * G);
+  }
+  const int kr = threadIdx.x / PR, kc = (threadIdx.x % PR) * 4;
+  const uint32_t kdst = swz_off<L>(kr, kc);
+  const int64_t ksrc = (int64_t)kr * D + kc;
+  auto roff = [&](int u) { return (int64_t)row * D + 16 * (cq * TPW + u) + 4 * G; };
+
+  f32x4 Kpre[NQ];
+  auto load_k = [&](int i) {
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) Kpre[q] = *reinterpret_cast<const f32x4*>(Kb + i * mat + ksrc + q * RSTEP * D);
+  };
+  auto stage_k = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      bf16x4 hi, lo;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        bf16 h_, l_;
+        split2(Kpre[q][e], h_, l_);
+        hi[e] = h_;
+        lo[e] = l_;
+      }
+      const uint32_t o = R::K0 + buf * 2 * R::PLANE + kdst + q * RSTEP * ROWB;
+      lds_st<bf16x4>(L0 + o, hi);
+      lds_st<bf16x4>(L0 + (o + R::PLANE), lo);
+    }
+  };
+  // chunk operands of this lane: gS tiles; adam: U, M, V tiles and the S_i row
+  // pieces of every k-block (columns 32 kb + 16 h + 4G .. +3)
+  f32x4 gsn[TPW], un[TPW], mn[TPW], vn[TPW], sn[NKB][2];
+  auto load_chunk = [&](int i) {
+    const int64_t base = (bh * N + i) * mat;
+#pragma unroll
+    for (int u = 0; u < TPW; ++u) gsn[u] = *reinterpret_cast<const f32x4*>(gS + base + roff(u));
+    if constexpr (RULE == 2) {
+#pragma unroll
+      for (int u = 0; u < TPW; ++u) {
+        un[u] = *reinterpret_cast<const f32x4*>(U + base + roff(u));
+        mn[u] = *reinterpret_cast<const f32x4*>(M_all + base + roff(u));
+        vn[u] = *reinterpret_cast<const f32x4*>(V_all + base + roff(u));
+      }
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          sn[kb][h] = *reinterpret_cast<const f32x4*>(S_all + base + (int64_t)row * D + 32 * kb + 16 * h + 4 * G);
+    }
+  };
+
+  f32x4 Sb[TPW], Mb[TPW], Vb[TPW];
+#pragma unroll
+  for (int u = 0; u < TPW; ++u) Sb[u] = Mb[u] = Vb[u] = zero4();
+  if (N > 0) {
+    load_k(N - 1);
+    stage_k((N - 1) & 1);
+    load_chunk(N - 1);
+  }
+  if (N > 1) load_k(N - 2);
+  __syncthreads();
+
+  for (int i = N - 1; i >= 0; --i) {
+    const int buf = i & 1;
+    const int64_t si = bh * N + i;
+    const float a = av[si];
+    f32x4 gsc[TPW], Gb[TPW];
+#pragma unroll
+    for (int u = 0; u < TPW; ++u) gsc[u] = gsn[u];
+    if constexpr (RULE == 0) {
+#pragma unroll
+      for (int u = 0; u < TPW; ++u) Gb[u] = Sb[u];
+    } else {
+      const float b = bv[si], m = mv[si], n = nv[si];
+      P::Op Sop[NKB];
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) Sop[kb] = P::pack(-sn[kb][0], -sn[kb][1]);
+      float pda = 0.f, pdb = 0.f, pdm = 0.f, pdn = 0.f;
+#pragma unroll
+      for (int u = 0; u < TPW; ++u) {
+        // G^T = U^T - K^T S_i^T : A = K^T (column reads), B = -S_i^T
+        f32x4 g = un[u];
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+          const uint32_t o = R::K0 + buf * 2 * R::PLANE + kcol[u] + kb * 32 * ROWB;
+          P::Op A;
+          A.hi = cat8(lds_tr16(L0 + o), lds_tr16(L0 + (o + 16 * ROWB)));
+          A.lo = cat8(lds_tr16(L0 + (o + R::PLANE)), lds_tr16(L0 + (o + R::PLANE + 16 * ROWB)));
+          g = P::mma(A, Sop[kb], g);
+        }
+        const int ct = cq * TPW + u;  // this tile's S_i pieces, selected with constant indices
+        f32x4 Si = sn[0][0];
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            if (2 * kb + h == ct) Si = sn[kb][h];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float gg = g[j];
+          const float Mi = m * mn[u][j] + (1.f - m) * gg;
+          const float Vi = n * vn[u][j] + (1.f - n) * gg * gg;
+          const float root = sqrtf(Vi);
+          const float den = root + 1e-6f;
+          const float sb = Sb[u][j];
+          pda += sb * Si[j];
+          pdb += sb * (Mi / den);
+          const float ub = b * sb;
+          const float Mtot = Mb[u][j] + ub / den;
+          const float Vtot = Vb[u][j] - ub * Mi / (den * den) / (2.f * fmaxf(root, 1e-12f));
+          pdm += Mtot * (mn[u][j] - gg);
+          pdn += Vtot * (vn[u][j] - gg * gg);
+          Mb[u][j] = m * Mtot;
+          Vb[u][j] = n * Vtot;
+          Gb[u][j] = (1.f - m) * Mtot + (1.f - n) * 2.f * gg * Vtot;
+        }
+      }
+      pda = wave_sum(pda);
+      pdb = wave_sum(pdb);
+      pdm = wave_sum(pdm);
+      pdn = wave_sum(pdn);
+      if (l < 4) {
+        const float v = l == 0 ? pda : l == 1 ? pdb : l == 2 ? pdm : pdn;
+        lds_st<float>(L0 + (RED + (w * 4 + l) * 4), v);
+      }
+    }
+    // dU_i = Gb ; -Gb (split) -> the exchange planes
+#pragma unroll
+    for (int u = 0; u < TPW; ++u) {
+      *reinterpret_cast<f32x4*>(dU + si * mat + roff(u)) = Gb[u];
+      bf16x4 hi, lo;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        bf16 h_, l_;
+        split2(-Gb[u][j], h_, l_);
+        hi[j] = h_;
+        lo[j] = l_;
+      }
+      lds_st<bf16x4>(L0 + (R::XS0 + xsw[u]), hi);
+      lds_st<bf16x4>(L0 + (R::XS0 + xsw[u] + R::XSP), lo);
+    }
+    __syncthreads();  // -Gb rows (and adam's partial sums) published
+    if constexpr (RULE == 2) {
+      if (cq == 0 && l < 4) {
+        float t = 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) t += lds_ld<float>(L0 + (RED + ((4 * rt + q) * 4 + l) * 4));
+        part[(si * NTILES + 2 * blk + rt) * 4 + l] = t;
+      }
+    }
+    P::Op Gop[NKB];
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      Gop[kb].hi = cat8(lds_ld<bf16x4>(L0 + (R::XS0 + xsr[kb][0])), lds_ld<bf16x4>(L0 + (R::XS0 + xsr[kb][1])));
+      Gop[kb].lo = cat8(lds_ld<bf16x4>(L0 + (R::XS0 + R::XSP + xsr[kb][0])),
+                        lds_ld<bf16x4>(L0 + (R::XS0 + R::XSP + xsr[kb][1])));
+    }
+    // Sb^T <- a Sb^T - K Gb^T + gS^T : A = K rows 16 ct.., B = -Gb^T
+#pragma unroll
+    for (int u = 0; u < TPW; ++u) {
+      const int ct = cq * TPW + u;
+      f32x4 acc = a * Sb[u] + gsc[u];
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+        const uint32_t o0 = R::K0 + buf * 2 * R::PLANE + 16 * ct * ROWB;
+        P::Op A;
+        A.hi = cat8(lds_ld<bf16x4>(L0 + (o0 + krow[kb][0])), lds_ld<bf16x4>(L0 + (o0 + krow[kb][1])));
+        A.lo = cat8(lds_ld<bf16x4>(L0 + (o0 + R::PLANE + krow[kb][0])),
+                    lds_ld<bf16x4>(L0 + (o0 + R::PLANE + krow[kb][1])));
+        acc = P::mma(A, Gop[kb], acc);
+      }
+      Sb[u] = acc;
+    }
+    // K_{i-1} into the other buffer (last read in chunk i+1); loads of K_{i-2} and chunk i-1
+    if (i > 0) {
+      stage_k(buf ^ 1);
+      load_chunk(i - 1);
+    }
+    if (i > 1) load_k(i - 2);
+    __syncthreads();  // K_{i-1} staged; the exchange planes free
+  }
+}
+
 // Chunk-parallel part of the backward: dK_i = -S_i^T Gb_i (contraction over
 // the rows of S) and the scalar gradients of chunk i.  One workgroup of
 // A_KWAVES waves per (bh, i); S_i and Gb_i are staged in swizzled LDS.
@@ -705,8 +945,24 @@ static hipError_t fwd_rows_rule(const ScanArgs& s) {
   else
     return s.rule == 0 ? launch_fwd_rows<D, 0, PREC>(s) : launch_fwd_rows<D, 2, PREC>(s);
 }
+template <int D, int RULE>
+static hipError_t launch_bwd_rows8(const ScanArgs& s, float* part) {
+  const int lds = Rows8Lds<D>::BYTES + (RULE == 2 ? 32 * 4 : 0);
+  auto kern = scan_bwd_rows8<D, RULE>;
+  hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, dim3((unsigned)(s.BH * (D / 32))), dim3(A8_THREADS), lds, s.stream, s.U, s.K, s.a,
+                     s.b, s.m, s.n, s.S_all, s.M_all, s.V_all, s.gS, s.dU, part, s.BH, (int)s.N);
+  return hipGetLastError();
+}
+
 template <int D, int PREC>
 static hipError_t bwd_rows_rule(const ScanArgs& s, float* part) {
+  // bf16x3: the 8-wave kernel (adam's at D = 128 would spill: the 2-wave one)
+  if constexpr (PREC == 0 && D >= 64) {
+    if (s.rule == 0) return launch_bwd_rows8<D, 0>(s, part);
+    if constexpr (D == 64) return launch_bwd_rows8<D, 2>(s, part);
+  }
   return s.rule == 0 ? launch_bwd_rows<D, 0, PREC>(s, part) : launch_bwd_rows<D, 2, PREC>(s, part);
 }
 
