@@ -262,9 +262,53 @@ struct NSSplit {
     for (int kb = 0; kb < NKB; ++kb) acc = P::mma(col(pub, kb, tc), B[kb], acc);
     return acc;
   }
+  // The wave's rows of a matrix kept in global memory as split pieces (the
+  // layout `store_own` writes) -> planes at m
+  GMDN_DEV void stage_own(lds_ptr m, const float* g) const {
+    const int l = lane_id(), row = 16 * wave_id() + (l & 15);
+    bf16x8 pc[NT];
+#pragma unroll
+    for (int c = 0; c < NT; ++c) pc[c] = *reinterpret_cast<const bf16x8*>(g + row * D + 16 * c + 4 * (l >> 4));
+#pragma unroll
+    for (int c = 0; c < NT; ++c) {
+      lds_st<bf16x4>(m + ppub[c], __builtin_shufflevector(pc[c], pc[c], 0, 1, 2, 3));
+      lds_st<bf16x4>(m + (ppub[c] + PLANE), __builtin_shufflevector(pc[c], pc[c], 4, 5, 6, 7));
+    }
+  }
+  // the wave's rows (D-layout tiles t of M^T) -> split pieces in global memory
+  static GMDN_DEV void store_own(float* g, const f32x4 (&t)[NT]) {
+    const int l = lane_id(), row = 16 * wave_id() + (l & 15);
+#pragma unroll
+    for (int c = 0; c < NT; ++c) *reinterpret_cast<bf16x8*>(g + row * D + 16 * c + 4 * (l >> 4)) = split_piece(t[c]);
+  }
+  // operands of the wave's rows from those pieces (the split of pack_all)
+  static GMDN_DEV void load_own(const float* g, Op (&o)[NKB]) {
+    const int l = lane_id(), row = 16 * wave_id() + (l & 15);
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      const bf16x8 a = *reinterpret_cast<const bf16x8*>(g + row * D + 32 * kb + 4 * (l >> 4));
+      const bf16x8 b = *reinterpret_cast<const bf16x8*>(g + row * D + 32 * kb + 16 + 4 * (l >> 4));
+      o[kb].hi = __builtin_shufflevector(a, b, 0, 1, 2, 3, 8, 9, 10, 11);
+      o[kb].lo = __builtin_shufflevector(a, b, 4, 5, 6, 7, 12, 13, 14, 15);
+    }
+  }
+  // D-layout tile [r'][r] (r' = 16 tr + .., r = the wave's rows) of the
+  // transpose of the matrix at m: transposing reads at the wave's columns
+  // (tb = the lane's base for them, `tbase`)
+  GMDN_DEV static uint32_t tbase() {
+    const int l = lane_id(), lc = l & 15;
+    return swz_off<L>(4 * (l >> 4) + (lc >> 2), 16 * wave_id() + 4 * (lc & 3));
+  }
+  static GMDN_DEV f32x4 tview(lds_cptr m, uint32_t tb, int tr) {
+    const lds_cptr a = m + tb + tr * 16 * ROWB;
+    const bf16x4 h = lds_tr16(a), o = lds_tr16(a + PLANE);
+    return f32x4{(float)h[0] + (float)o[0], (float)h[1] + (float)o[1], (float)h[2] + (float)o[2],
+                 (float)h[3] + (float)o[3]};
+  }
   // One quintic step on the wave's rows XT (D-layout tiles of X^T); the same
-  // products as NSBlock::step.
-  GMDN_DEV void step(f32x4 (&XT)[NT], lds_ptr XM, lds_ptr PM) const {
+  // products as NSBlock::step.  With zst, Z = b P + c P^2 (symmetric) is also
+  // stored as the wave's rows in split pieces.
+  GMDN_DEV void step(f32x4 (&XT)[NT], lds_ptr XM, lds_ptr PM, float* zst = nullptr) const {
     publish(XM, XT);
     __syncthreads();
     Op Bx[NKB];
@@ -280,6 +324,7 @@ struct NSSplit {
     // Z = b P + c P^2, in place of the wave's block of P (now held by Bp)
 #pragma unroll
     for (int tr = 0; tr < NT; ++tr) Pc[tr] = NS_B * Pc[tr] + NS_C * rowprod(PM, tr, Bp);
+    if (zst) store_own(zst, Pc);
     Op Bz[NKB];
     pack_all(Pc, Bz);
 #pragma unroll

@@ -24,7 +24,10 @@ hipError_t scan_bwd_dk_launch(const ScanArgs& s, const float* part);
 hipError_t scan_fwd_muon_launch(const ScanArgs& s);
 hipError_t scan_bwd_muon_launch(const ScanArgs& s, float* ws);
 
-// workspace floats per (b, h) for the muon backward
-inline int64_t muon_bwd_ws_floats(int dh, int ns) { return (int64_t)(4 + ns) * dh * dh; }
+// workspace floats per (b, h) for the muon backward: the bf16x3 kernel keeps
+// 2 ns + 2 matrices (iterates X_k, products Z_k, M_i, Mbar), the fp32 one 4 + ns
+__host__ __device__ inline int64_t muon_bwd_ws_floats(int dh, int ns) {
+  return (int64_t)(2 * ns + 2 > 4 + ns ? 2 * ns + 2 : 4 + ns) * dh * dh;
+}
 
 }  // namespace gmdn

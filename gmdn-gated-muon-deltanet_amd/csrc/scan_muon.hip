@@ -211,6 +211,210 @@ scan_bwd_muon(const float* __restrict__ U, const float* __restrict__ K,
   }
 }
 
+// The backward with bf16x3 products.  Per chunk (reverse order), on the
+// NSSplit engine with two LDS slots of one split matrix each (A, B):
+//   1. K_i staged into B; G = U - S_i K_i (column reads of K_i); M_i, X_0.
+//   2. The ns forward steps again, storing each iterate X_k and each
+//      Z_k = b P_k + c P_k^2 as the wave's rows in split pieces (workspace).
+//   3. The VJP steps, k = ns-1 .. 0, with Xbar published in A and X_k in B:
+//        Q    = a Xbar + Z_k Xbar                 (A column reads, Z_k rows)
+//        Bs   = Bbar + Bbar^T, Bbar = Xbar X_k^T  (A and B row reads)
+//        Y    = X_k (X_k^T Bs) = P_k Bs           (B column, then row reads)
+//        Y^T  read back transposed after publishing Y in A
+//        Xbar <- Q + (b Bs + c (Y + Y^T)) X_k     (B column reads)
+//      (P_k, Bs and Z_k are symmetric.)  Six D^3 products per step.
+//   4. The normalisation VJP, Gb = dU_i, and Sb <- a Sb - Gb K_i^T + gS with
+//      K_i staged into B again (row reads).
+// M_i and Mbar pass through the workspace as fp32 rows of their wave.
+template <int D>
+__global__ void __launch_bounds__(D * 4)
+scan_bwd_muon_x3(const float* __restrict__ U, const float* __restrict__ K,
+                 const float* __restrict__ av, const float* __restrict__ bv,
+                 const float* __restrict__ mv, const float* __restrict__ S_all,
+                 const float* __restrict__ M_all, const float* __restrict__ gS,
+                 float* __restrict__ dU, float* __restrict__ da, float* __restrict__ db,
+                 float* __restrict__ dm, float* __restrict__ dn, float* __restrict__ ws, int N,
+                 int ns) {
+  using NSX = NSSplit<D>;
+  using P = PrecX3;
+  using Op = P::Op;
+  constexpr int NT = D / 16, NKB = D / 32, NW = D / 16;
+  extern __shared__ __align__(16) float smem[];
+  const lds_ptr SA = lds_base(smem), SB = SA + NSX::BYTES;
+  float* red = smem + 2 * NSX::BYTES / 4;
+
+  const NSX nsx;
+  const uint32_t tb = NSX::tbase();
+  const int64_t bh = blockIdx.x;
+  const int l = lane_id(), G = l >> 4, rl = l & 15;
+  const int r0 = 16 * wave_id();
+  const int64_t mat = (int64_t)D * D;
+  float* wsb = ws + bh * muon_bwd_ws_floats(D, ns);
+  float* WX = wsb;                           // X_0 .. X_{ns-1}
+  float* WZ = wsb + ns * mat;                // Z_0 .. Z_{ns-1}
+  float* WM = wsb + 2 * ns * mat;            // M_i
+  float* WMb = wsb + (2 * ns + 1) * mat;     // Mbar carried to chunk i-1
+  auto roff = [&](int t) { return (int64_t)(r0 + rl) * D + 16 * t + 4 * G; };
+
+  f32x4 Sb[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) Sb[t] = zero4();
+
+  for (int i = N - 1; i >= 0; --i) {
+    const int64_t si = bh * N + i;
+    const float* Ki = K + si * mat;
+    const float ga = av[si], gb = bv[si], gm = mv[si];
+    // ---- 1. G, M_i, X_0
+    NSX::template stage<D * 4>(SB, Ki);
+    float pda = 0.f;
+    Op Bop[NKB];
+    {
+      f32x4 Si[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        Si[t] = *reinterpret_cast<const f32x4*>(S_all + si * mat + roff(t));
+        pda += Sb[t][0] * Si[t][0] + Sb[t][1] * Si[t][1] + Sb[t][2] * Si[t][2] + Sb[t][3] * Si[t][3];
+      }
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) Bop[kb] = P::pack(-Si[2 * kb], -Si[2 * kb + 1]);
+    }
+    __syncthreads();  // K_i staged
+    f32x4 X[NT];
+    float sq = 0.f;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      f32x4 g = *reinterpret_cast<const f32x4*>(U + si * mat + roff(t));
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) g = P::mma(nsx.col(SB, kb, t), Bop[kb], g);
+      const f32x4 Mp = *reinterpret_cast<const f32x4*>(M_all + si * mat + roff(t));
+      X[t] = gm * Mp + g;
+      *reinterpret_cast<f32x4*>(WM + roff(t)) = X[t];
+      sq += X[t][0] * X[t][0] + X[t][1] * X[t][1] + X[t][2] * X[t][2] + X[t][3] * X[t][3];
+    }
+    const float nf = sqrtf(block_sum<NW>(sq, red));
+    const float nrm = nf + 1e-7f;
+    const float scale = 1.f / nrm;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) X[t] = X[t] * scale;
+    // ---- 2. the forward iterates again (B's K_i is dead after the sum's barriers)
+    for (int k = 0; k < ns; ++k) {
+      NSX::store_own(WX + k * mat, X);
+      nsx.step(X, SA, SB, WZ + k * mat);
+    }
+    // db_i = <Sb, msign(M_i)>, da_i = <Sb, S_i>
+    float pdb = 0.f;
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+      pdb += Sb[t][0] * X[t][0] + Sb[t][1] * X[t][1] + Sb[t][2] * X[t][2] + Sb[t][3] * X[t][3];
+    const float dbv = block_sum<NW>(pdb, red);
+    const float dav = block_sum<NW>(pda, red);
+    // ---- 3. Xbar = b Sb pulled back through the ns steps (X is its register home)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) X[t] = gb * Sb[t];
+    if (ns > 0) {
+      nsx.publish(SA, X);
+      nsx.stage_own(SB, WX + (ns - 1) * mat);
+      __syncthreads();
+    }
+    for (int k = ns - 1; k >= 0; --k) {
+      f32x4 Q[NT], Bs[NT];
+      {
+        Op Bxb[NKB], Bz[NKB];
+        NSX::pack_all(X, Bxb);
+        NSX::load_own(WZ + k * mat, Bz);
+#pragma unroll
+        for (int tc = 0; tc < NT; ++tc) Q[tc] = nsx.colprod(SA, tc, Bz, NS_A * X[tc]);
+        __builtin_amdgcn_sched_barrier(0);  // keep the phases' operand loads apart
+        Op Bk[NKB];
+        NSX::load_own(WX + k * mat, Bk);
+#pragma unroll
+        for (int tr = 0; tr < NT; ++tr) {
+          f32x4 acc = zero4();
+#pragma unroll
+          for (int kb = 0; kb < NKB; ++kb) {
+            acc = P::mma(nsx.row(SA, tr, kb), Bk[kb], acc);   // Bbar[r'][r]
+            acc = P::mma(nsx.row(SB, tr, kb), Bxb[kb], acc);  // Bbar[r][r']
+          }
+          Bs[tr] = acc;
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      f32x4 Y[NT];
+      {
+        Op Bso[NKB], Wo[NKB];
+        NSX::pack_all(Bs, Bso);
+        f32x4 W[NT];
+#pragma unroll
+        for (int tc = 0; tc < NT; ++tc) W[tc] = nsx.colprod(SB, tc, Bso, zero4());  // (X_k^T Bs)[c][r]
+        NSX::pack_all(W, Wo);
+#pragma unroll
+        for (int tr = 0; tr < NT; ++tr) Y[tr] = nsx.rowprod(SB, tr, Wo);  // (X_k W)[r'][r]
+      }
+      __syncthreads();  // every read of Xbar in A done
+      nsx.publish(SA, Y);  // A holds Y^T
+      __syncthreads();
+      {
+        Op So[NKB];
+#pragma unroll
+        for (int tr = 0; tr < NT; ++tr) Bs[tr] = NS_B * Bs[tr] + NS_C * (Y[tr] + NSX::tview(SA, tb, tr));
+        NSX::pack_all(Bs, So);
+#pragma unroll
+        for (int tc = 0; tc < NT; ++tc) X[tc] = nsx.colprod(SB, tc, So, Q[tc]);
+      }
+      __syncthreads();  // every read of A and B done
+      if (k > 0) {
+        nsx.publish(SA, X);
+        nsx.stage_own(SB, WX + (k - 1) * mat);
+        __syncthreads();
+      }
+    }
+    // ---- 4. normalisation: Mbar = Xbar/nrm - <Xbar, M_i>/nrm^2 * M_i/max(|M_i|, 1e-12)
+    float pdot = 0.f;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const f32x4 Mi = *reinterpret_cast<const f32x4*>(WM + roff(t));
+      pdot += X[t][0] * Mi[0] + X[t][1] * Mi[1] + X[t][2] * Mi[2] + X[t][3] * Mi[3];
+    }
+    const float dot = block_sum<NW>(pdot, red);
+    const float cM = dot / (nrm * nrm) / fmaxf(nf, 1e-12f);
+    float pdm = 0.f;
+    NSX::template stage<D * 4>(SB, Ki);  // K_i again, for the row reads of the Sb update
+    Op Bg[NKB];
+    {
+      f32x4 Gb[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const f32x4 Mi = *reinterpret_cast<const f32x4*>(WM + roff(t));
+        const f32x4 Mp = *reinterpret_cast<const f32x4*>(M_all + si * mat + roff(t));
+        const f32x4 Mb = i == N - 1 ? zero4() : *reinterpret_cast<const f32x4*>(WMb + roff(t));
+        const f32x4 Mtot = Mb + X[t] / nrm - cM * Mi;
+        pdm += Mtot[0] * Mp[0] + Mtot[1] * Mp[1] + Mtot[2] * Mp[2] + Mtot[3] * Mp[3];
+        *reinterpret_cast<f32x4*>(WMb + roff(t)) = gm * Mtot;
+        Gb[t] = Mtot;
+        *reinterpret_cast<f32x4*>(dU + si * mat + roff(t)) = Mtot;
+      }
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) Bg[kb] = P::pack(-Gb[2 * kb], -Gb[2 * kb + 1]);
+    }
+    const float dmv = block_sum<NW>(pdm, red);  // (its barriers also publish K_i in B)
+    // Sb <- a Sb - Gb K^T + gS : A = K rows
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      f32x4 acc = ga * Sb[t] + *reinterpret_cast<const f32x4*>(gS + si * mat + roff(t));
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) acc = P::mma(nsx.row(SB, t, kb), Bg[kb], acc);
+      Sb[t] = acc;
+    }
+    if (threadIdx.x == 0) {
+      da[si] = dav;
+      db[si] = dbv;
+      dm[si] = dmv;
+      dn[si] = 0.f;
+    }
+    __syncthreads();  // B's K_i read by every wave before chunk i-1 restages it
+  }
+}
+
 template <int D, int PREC>
 static hipError_t launch_fwd_muon(const ScanArgs& s) {
   const size_t lds = 2 * (size_t)D * D * sizeof(float);
@@ -224,6 +428,15 @@ static hipError_t launch_fwd_muon(const ScanArgs& s) {
 
 template <int D, int PREC>
 static hipError_t launch_bwd_muon(const ScanArgs& s, float* ws) {
+  if constexpr (PREC == 0) {
+    const int lds = 2 * NSSplit<D>::BYTES + 64;
+    auto k3 = scan_bwd_muon_x3<D>;
+    hipError_t e = hipFuncSetAttribute((const void*)k3, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k3, dim3((unsigned)s.BH), dim3(D * 4), lds, s.stream, s.U, s.K, s.a, s.b, s.m,
+                       s.S_all, s.M_all, s.gS, s.dU, s.da, s.db, s.dm, s.dn, ws, (int)s.N, s.ns);
+    return hipGetLastError();
+  }
   auto kern = scan_bwd_muon<D, PREC>;
   hipLaunchKernelGGL(kern, dim3((unsigned)s.BH), dim3(D * 4), 0, s.stream, s.U, s.K, s.a, s.b, s.m,
                      s.S_all, s.M_all, s.gS, s.dU, s.da, s.db, s.dm, s.dn, ws, (int)s.N, s.ns);
