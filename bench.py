@@ -17,7 +17,9 @@ durations measured with HIP events on the launch stream inside the timed
 regions, algorithmic bytes of the op's own inputs and outputs, against
 MI355X's HBM bandwidth (8 TB/s); ``traffic`` is read from the committed
 FETCH_SIZE/WRITE_SIZE summaries of the same kernels and workload.
-``cpu_baseline`` times the CPU restatement of the reference matrix form
+``drop_in`` times the drop-in scan ``fast_state_scan`` on the same chunk
+grid (fp32 d x d inputs per chunk), forward and forward + backward, with its
+own roofline.  ``cpu_baseline`` times the CPU restatement of the reference matrix form
 (float32, torch on the host cores) on the same workload.
 
 ``--fwd-only`` times the inference forward alone; ``--copy-calibration
@@ -53,6 +55,7 @@ def parse_args(argv=None):
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--workload", default=DEFAULT_WORKLOAD)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-drop-in", action="store_true", help="skip the drop-in scan (fast_state_scan) leg")
     p.add_argument("--fwd-only", action="store_true", help="time the inference forward only")
     p.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work (about)")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES")
@@ -75,6 +78,98 @@ def fwd_flops_per_chunk_head(w) -> int:
     f = 4 * C * C * d + 6 * C * d * d
     if w.rule == "muon":
         f += 6 * w.ns * d ** 3
+    return f
+
+
+def drop_in_bytes_per_chunk(d: int):
+    """The drop-in scan's own I/O per chunk: forward reads U, K and the four
+    gate scalars and writes S (3 d^2 fp32 + 16 B); the backward reads gS and
+    writes dU, dK and the four scalar gradients, besides reading U, K, S and
+    the gates again (5 d^2 fp32 + 32 B)."""
+    return 3 * d * d * 4 + 16, 8 * d * d * 4 + 48
+
+
+def drop_in_flops_per_chunk(rule: str, d: int, ns: int):
+    """Minimal flops per chunk, forward and backward: delta 2 d^3 and 4 d^3,
+    adam 2 d^3 and 6 d^3, muon (2 + 6 ns) d^3 and (6 + 16 ns) d^3."""
+    fwd = {"delta": 2, "adam": 2, "muon": 2 + 6 * ns}[rule]
+    bwd = {"delta": 4, "adam": 6, "muon": 6 + 16 * ns}[rule]
+    return fwd * d ** 3, bwd * d ** 3
+
+
+def drop_in_leg(w, steps: int, warmup: int) -> dict:
+    """The drop-in scan ``fast_state_scan(U, K, a, b, m, n, rule, ns)``
+    (reference fast_scan.py:403-414) on the workload's chunk grid: B*H scans of
+    T/chunk chunks of d x d fp32 ``U``, ``K`` (K = X X^T / 2d, X ~ N(0, 1)) and
+    gate scalars in (0.9, 1), forward and forward + backward against a
+    N(0, 1) state cotangent, timed with HIP events on the launch stream.
+    Priced per chunk on the op's own I/O (3 d^2 fp32 + 4 scalars forward,
+    5 d^2 + 8 scalars backward) against HBM, or for muon on its minimal flops
+    ((2 + 6 ns) d^3 forward, (6 + 16 ns) d^3 backward) against bf16 MFMA."""
+    import torch
+    import fast_scan
+
+    B, H, N, d = w.B, w.H, w.T // w.chunk, w.d
+    rid = {"delta": 0, "muon": 1, "adam": 2}[w.rule]
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(0)
+    X = torch.randn(B * H * N, d, d, device=dev, generator=gen)
+    K = torch.bmm(X, X.transpose(1, 2).contiguous()).div_(2 * d).view(B, H, N, d, d)
+    del X
+    U = torch.randn(B, H, N, d, d, device=dev, generator=gen)
+    gates = [0.9 + 0.1 * torch.rand(B, H, N, device=dev, generator=gen) for _ in range(4)]
+    gS = torch.randn(B, H, N, d, d, device=dev, generator=gen)
+    xs = [t.requires_grad_(True) for t in [U, K] + gates]
+    fast_scan.set_backend("triton")  # the native path, never eager
+    fast_scan.set_precision("tf32")
+    stream = torch.cuda.current_stream(dev)
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        for e in evs:
+            e[0].record(stream)
+            fn()
+            e[1].record(stream)
+        torch.cuda.synchronize()
+        return statistics.mean(e[0].elapsed_time(e[1]) for e in evs)
+
+    try:
+        with torch.no_grad():
+            fwd_ms = timed(lambda: fast_scan.fast_state_scan(*xs, rid, w.ns))
+        fb_ms = timed(lambda: torch.autograd.grad(fast_scan.fast_state_scan(*xs, rid, w.ns), xs, gS))
+    finally:
+        fast_scan.set_backend("auto")
+    chunks = B * H * N
+
+    def roof(ms, nbytes, flops):
+        if w.rule == "muon":
+            ach, peak, unit, bound = flops / (ms * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s", "mfma"
+        else:
+            ach, peak, unit, bound = nbytes / (ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s", "hbm"
+        return {"bound": bound, "achieved": ach, "peak": peak, "unit": unit, "frac": ach / peak,
+                "alg_bytes": nbytes, "alg_flops": flops, "avg_us": ms * 1e3}
+
+    fwd_b, fb_b = drop_in_bytes_per_chunk(d)
+    fwd_f, bwd_f = drop_in_flops_per_chunk(w.rule, d, w.ns)
+    fwd_flops, bwd_flops = fwd_f * chunks, bwd_f * chunks
+    return {"op": "fast_state_scan", "shape": {"B": B, "H": H, "N": N, "d": d, "rule": w.rule, "ns": w.ns},
+            "precision": "tf32 (bf16x3 split products)",
+            "fwd_tokens_per_s": B * N * w.chunk / (fwd_ms * 1e-3),
+            "fwd_bwd_tokens_per_s": B * N * w.chunk / (fb_ms * 1e-3),
+            "roofline_fwd": roof(fwd_ms, fwd_b * chunks, fwd_flops),
+            "roofline_fwd_bwd": roof(fb_ms, fb_b * chunks, fwd_flops + bwd_flops)}
+
+
+def bwd_flops_per_chunk_head(w) -> int:
+    """Twice the forward's GEMMs; for muon the msign VJP adds (2 + 16 ns) d^3
+    (in place of twice the forward Newton-Schulz)."""
+    C, d = w.chunk, w.d
+    f = 2 * (4 * C * C * d + 6 * C * d * d)
+    if w.rule == "muon":
+        f += (2 + 16 * w.ns) * d ** 3
     return f
 
 
@@ -210,16 +305,22 @@ def main(argv=None):
                 "frac": ach / peak, "traffic": traffic, "avg_launch_us": ms * 1e3,
                 "alg_bytes": alg_bytes, "alg_flops": alg_flops}
 
-    roof_fwd = roof(f"chunk_fwd<{w.d},{rid}>", fwd_bytes_per_token_head(w) * units,
+    # muon: the drop-in scan's muon kernels with the mixer's phase-1/3 GEMMs
+    # (torch, fp32) around them; the other rules: the fused chunk kernels
+    fwd_name = (f"scan_fwd_muon<{w.d}> + phase-1/3 GEMMs" if rid == 1 else f"chunk_fwd<{w.d},{rid}>")
+    roof_fwd = roof(fwd_name, fwd_bytes_per_token_head(w) * units,
                     fwd_flops_per_chunk_head(w) * w.B * w.H * (w.T // w.chunk), fwd_kernel_ms,
                     f"chunk_fwd_{w.name}_traffic.md")
     if with_bwd:
         # the backward pass dominates the step: its two kernels, priced on the
         # op's own backward inputs and outputs (states are intermediates)
-        state_kernel = f"chunk_bwd_dstate<{w.d}>" if rid == 0 else f"chunk_bwd_state<{w.d},{rid}>"
-        roof_main = roof(f"{state_kernel} + chunk_bwd_tok<{w.d},{rid}>",
-                         bwd_bytes_per_token_head(w) * units,
-                         2 * fwd_flops_per_chunk_head(w) * w.B * w.H * (w.T // w.chunk), bwd_ms,
+        if rid == 1:
+            bwd_name = f"scan_bwd_muon_x3<{w.d}> + scan_bwd_dk8<{w.d},1> + autograd GEMMs"
+        else:
+            state_kernel = f"chunk_bwd_dstate<{w.d}>" if rid == 0 else f"chunk_bwd_state<{w.d},{rid}>"
+            bwd_name = f"{state_kernel} + chunk_bwd_tok<{w.d},{rid}>"
+        roof_main = roof(bwd_name, bwd_bytes_per_token_head(w) * units,
+                         bwd_flops_per_chunk_head(w) * w.B * w.H * (w.T // w.chunk), bwd_ms,
                          f"chunk_bwd_{w.name}_traffic.md")
     else:
         roof_main = roof_fwd
@@ -247,6 +348,8 @@ def main(argv=None):
         "roofline": roof_main,
         "roofline_fwd": roof_fwd,
     }
+    if not (args.no_drop_in or args.fwd_only):
+        line["drop_in"] = drop_in_leg(w, min(args.steps, 20), max(args.warmup, 1))
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(w, args.cpu_budget, with_bwd)
     print(json.dumps(line), flush=True)

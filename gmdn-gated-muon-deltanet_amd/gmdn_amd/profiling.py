@@ -2,7 +2,7 @@
 
 Usage, after ``rocprofv3 ... --output-format csv -d DIR -o NAME -- <program>``:
 
-    python -m gmdn_amd.profiling stats DIR                # per-kernel durations
+    python -m gmdn_amd.profiling stats DIR [--kernel REGEX]  # per-kernel durations
     python -m gmdn_amd.profiling traffic --kernel REGEX \\
         --fetch DIR1 --write DIR2 --copy-fetch DIR3 --copy-write DIR4 \\
         --copy-bytes N
@@ -82,9 +82,12 @@ def _per_launch(d: str, counter: str, kernel_regex: str) -> float:
     return sum(statistics.median(v) for v in counter_by_kernel(d, counter, kernel_regex).values())
 
 
-def _stats_md(d: str) -> str:
+def _stats_md(d: str, kernel_regex: str = "") -> str:
     out = ["| kernel | calls | avg us | min us | max us | % time |", "|---|---|---|---|---|---|"]
+    pat = re.compile(kernel_regex)
     for name, calls, avg, mn, mx, pct in kernel_stats(d):
+        if not pat.search(name):
+            continue
         out.append(f"| `{name}` | {calls} | {avg / 1e3:.1f} | {mn / 1e3:.1f} | {mx / 1e3:.1f} | {pct:.1f} |")
     return "\n".join(out)
 
@@ -125,6 +128,7 @@ def main(argv=None):
     sub = p.add_subparsers(dest="cmd", required=True)
     s = sub.add_parser("stats")
     s.add_argument("dir")
+    s.add_argument("--kernel", default="", help="only kernels whose name matches this regex")
     t = sub.add_parser("traffic")
     t.add_argument("--kernel", required=True)
     t.add_argument("--copy-kernel", default="copy|elementwise")
@@ -134,7 +138,7 @@ def main(argv=None):
     t.add_argument("--copy-write", required=True)
     t.add_argument("--copy-bytes", type=int, required=True)
     a = p.parse_args(argv)
-    print(_stats_md(a.dir) if a.cmd == "stats" else _traffic_md(a))
+    print(_stats_md(a.dir, a.kernel) if a.cmd == "stats" else _traffic_md(a))
 
 
 if __name__ == "__main__":

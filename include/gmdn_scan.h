@@ -79,8 +79,10 @@ int gmdn_scan_fwd(const float* U, const float* K, const float* a, const float* b
                   int32_t ns, int32_t precision, void* stream);
 
 /* Workspace bytes gmdn_scan_bwd needs for these sizes (0 if none): adam
- * keeps per-row-tile partial sums of its scalar gradients, muon keeps the
- * shared Newton-Schulz matrices and the ns stored iterates per (b, h). */
+ * keeps per-row-tile partial sums of its scalar gradients, muon keeps per
+ * (b, h) the ns Newton-Schulz iterates and products of the chunk being
+ * differentiated plus two state-sized matrices (max(2 ns + 2, 4 + ns) dh^2
+ * floats). */
 size_t gmdn_scan_bwd_workspace_bytes(int64_t BH, int64_t N, int32_t dh, int32_t rule,
                                      int32_t ns);
 

@@ -68,7 +68,9 @@ def test_scan_bwd_workspace_contract():
     lib = _native.load()
     assert lib.gmdn_scan_bwd_workspace_bytes(4, 16, 64, 0, 3) == 0
     assert lib.gmdn_scan_bwd_workspace_bytes(4, 16, 64, 2, 3) == 4 * 16 * 4 * 4 * 4
-    assert lib.gmdn_scan_bwd_workspace_bytes(4, 16, 64, 1, 3) == 4 * (4 + 3) * 64 * 64 * 4
+    # muon: max(2 ns + 2, 4 + ns) d x d matrices per (b, h)
+    assert lib.gmdn_scan_bwd_workspace_bytes(4, 16, 64, 1, 3) == 4 * 8 * 64 * 64 * 4
+    assert lib.gmdn_scan_bwd_workspace_bytes(4, 16, 64, 1, 1) == 4 * 5 * 64 * 64 * 4
     p = [0x1000] * 16
     # adam / muon without workspace -> GMDN_ERR_WORKSPACE
     assert lib.gmdn_scan_bwd(*p, None, 0, 4, 16, 64, 2, 3, 0, None) == 3

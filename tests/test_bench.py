@@ -24,6 +24,27 @@ def test_algorithmic_bytes_and_flops():
     assert bench.fwd_bytes_per_token_head(wa) == 8 * 64 + 16
 
 
+def test_backward_flops():
+    w = WORKLOADS["gated_delta_b4_h16_t4096_d128"]
+    assert bench.bwd_flops_per_chunk_head(w) == 2 * bench.fwd_flops_per_chunk_head(w)
+    wm = WORKLOADS["muon_b2_h16_t8192_d128"]
+    gemms = 4 * 64 * 64 * 128 + 6 * 64 * 128 * 128
+    assert bench.bwd_flops_per_chunk_head(wm) == 2 * gemms + (2 + 16 * 5) * 128 ** 3
+
+
+def test_drop_in_accounting():
+    # whole-workload totals of the drop-in scan at B=4, H=16, N=64, d=128:
+    # 805.4 MB forward and 2.148 GB forward + backward; 17.2 / 51.5 GFLOP (delta)
+    chunks = 4 * 16 * 64
+    fwd_b, fb_b = bench.drop_in_bytes_per_chunk(128)
+    assert fwd_b * chunks == 805371904
+    assert fb_b * chunks == 2147680256
+    f, b = bench.drop_in_flops_per_chunk("delta", 128, 5)
+    assert round(f * chunks / 1e9, 1) == 17.2 and round((f + b) * chunks / 1e9, 1) == 51.5
+    f, b = bench.drop_in_flops_per_chunk("muon", 128, 5)
+    assert (f, b) == (32 * 128 ** 3, 86 * 128 ** 3)
+
+
 def test_multi_gpu_is_refused():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
                        capture_output=True, text=True, timeout=120)
