@@ -33,7 +33,7 @@ from __future__ import annotations
 import torch
 
 from gmdn_amd import _native
-from gmdn_amd.scan import HipScan, SUPPORTED_DH
+from gmdn_amd.scan import HipScan, SUPPORTED_DH, hip_state_scan
 from gmdn_amd import scan as _scan_mod
 
 NS_A, NS_B, NS_C = 3.4445, -4.7750, 2.0315
@@ -186,7 +186,7 @@ def fast_state_scan(U, K, a, b, m, n, rule: int, ns: int) -> torch.Tensor:
         if U.shape[-1] not in SUPPORTED_DH:
             raise RuntimeError(f"native scan supports head dims {SUPPORTED_DH}, got {U.shape[-1]}; "
                                "set_backend('eager') to run this size eagerly")
-        return HipScan.apply(U, K, a, b, m, n, rule, ns)
+        return hip_state_scan(U, K, a, b, m, n, rule, ns)
     if _BACKEND == "triton":
         raise RuntimeError("native backend requested but unavailable for CPU tensors "
                            "(needs GPU tensors and libgmdn_scan.so)")

@@ -30,8 +30,8 @@ import math
 
 import torch
 
-from . import _native as nat
-from .scan import HipScan
+from . import ops  # noqa: F401  -- registers torch.ops.gmdn.*
+from .scan import hip_state_scan
 
 RULES = {"delta": 0, "muon": 1, "adam": 2}
 CHUNK = 64
@@ -61,18 +61,6 @@ def _rule_id(rule) -> int:
     return int(rule)
 
 
-def _desc(q, k, v, o, rule, ns, eps):
-    B, H, T, d = q.shape
-    desc = nat.ChunkDesc()
-    desc.B, desc.H, desc.T, desc.d, desc.C = B, H, T, d, CHUNK
-    desc.rule, desc.ns, desc.dtype, desc.eps = rule, ns, nat.DTYPE_BF16, eps
-    for name, t in (("sq", q), ("sk", k), ("sv", v), ("so", o)):
-        arr = getattr(desc, name)
-        for i in range(3):
-            arr[i] = t.stride(i)
-    return desc
-
-
 def _check(q, k, v, beta, g, gmu, gnu, rule):
     if not q.is_cuda:
         raise RuntimeError("chunk_scan needs GPU tensors")
@@ -93,73 +81,6 @@ def _check(q, k, v, beta, g, gmu, gnu, rule):
         raise RuntimeError("muon and adam rules need gmu")
     if rule == 2 and gnu is None:
         raise RuntimeError("adam rule needs gnu")
-
-
-def _tok(t):
-    """bf16 token stream with a unit-stride last dim and 16-byte-aligned rows."""
-    if t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:3]) or t.data_ptr() % 16:
-        t = t.contiguous()
-    return t
-
-
-def _gate(t):
-    """float32 (B, H, T) gate stream, contiguous and 16-byte aligned."""
-    if t is None:
-        return None
-    t = t.detach().to(torch.float32).contiguous()
-    return t if t.data_ptr() % 16 == 0 else t.clone()
-
-
-class ChunkScan(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, q, k, v, beta, g, gmu, gnu, rule, ns, eps, record):
-        _check(q, k, v, beta, g, gmu, gnu, rule)
-        lib = nat.load()
-        qc, kc, vc = _tok(q.detach()), _tok(k.detach()), _tok(v.detach())
-        bc, gc, mc, nc = _gate(beta), _gate(g), _gate(gmu), _gate(gnu)
-        o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-        desc = _desc(qc, kc, vc, o, rule, ns, eps)
-        # `record`: grad mode was on at the call (inside forward it is always
-        # off, and needs_input_grad ignores it), so a backward may follow
-        need_grad = record and any(ctx.needs_input_grad[:7])
-        states = None
-        if need_grad:
-            nbytes = lib.gmdn_chunk_states_bytes(desc)
-            states = torch.empty(nbytes // 4, dtype=torch.float32, device=q.device)
-        with torch.cuda.device(q.device):
-            rc = lib.gmdn_chunk_fwd(desc, nat.ptr(qc), nat.ptr(kc), nat.ptr(vc), nat.ptr(bc), nat.ptr(gc),
-                                    nat.ptr(mc), nat.ptr(nc), nat.ptr(o), nat.ptr(states), nat.stream_of(q))
-        nat.check(rc, "gmdn_chunk_fwd")
-        if need_grad:
-            ctx.save_for_backward(qc, kc, vc, bc, gc, mc, nc, states)
-        ctx.rule, ctx.ns, ctx.eps = rule, ns, eps
-        ctx.gate_dtypes = tuple(None if t is None else t.dtype for t in (beta, g, gmu, gnu))
-        return o
-
-    @staticmethod
-    def backward(ctx, dO):
-        qc, kc, vc, bc, gc, mc, nc, states = ctx.saved_tensors
-        lib = nat.load()
-        dOc = _tok(dO.to(torch.bfloat16))
-        if not backward_supported(ctx.rule, qc.shape[-1]):
-            raise RuntimeError(f"the fused backward of rule {ctx.rule} at head dim {qc.shape[-1]} is not built")
-        # gradients share the strides of q, k, v (the kernels write them with those strides)
-        dq, dk, dv = (torch.empty_strided(t.shape, t.stride(), dtype=t.dtype, device=t.device)
-                      for t in (qc, kc, vc))
-        dbeta, dg = torch.empty_like(bc), torch.empty_like(gc)
-        dgmu = torch.empty_like(mc) if mc is not None else None
-        dgnu = torch.empty_like(nc) if nc is not None else None
-        desc = _desc(qc, kc, vc, dOc, ctx.rule, ctx.ns, ctx.eps)
-        ws_bytes = lib.gmdn_chunk_bwd_workspace_bytes(desc)
-        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=qc.device) if ws_bytes else None
-        with torch.cuda.device(qc.device):
-            rc = lib.gmdn_chunk_bwd(desc, nat.ptr(qc), nat.ptr(kc), nat.ptr(vc), nat.ptr(bc), nat.ptr(gc),
-                                    nat.ptr(mc), nat.ptr(nc), nat.ptr(states), nat.ptr(dOc), nat.ptr(dq),
-                                    nat.ptr(dk), nat.ptr(dv), nat.ptr(dbeta), nat.ptr(dg), nat.ptr(dgmu),
-                                    nat.ptr(dgnu), nat.ptr(ws), ws_bytes, nat.stream_of(qc))
-        nat.check(rc, "gmdn_chunk_bwd")
-        gates = [None if t is None else t.to(dt) for t, dt in zip((dbeta, dg, dgmu, dgnu), ctx.gate_dtypes)]
-        return (dq, dk, dv, *gates, None, None, None, None)
 
 
 def _muon_core(q, k, v, beta, g, gmu, ns):
@@ -188,7 +109,7 @@ def _muon_core(q, k, v, beta, g, gmu, ns):
     Uv = torch.matmul((vf * w.unsqueeze(-1)).transpose(-1, -2).contiguous(), kf)
     Qt = qf - torch.matmul(A, kf)
     Ov = torch.matmul(A, vf)
-    S_all = HipScan.apply(Uv, Kw, a, b, m, n, 1, ns)
+    S_all = hip_state_scan(Uv, Kw, a, b, m, n, 1, ns)
     o = torch.matmul(Qt, S_all.transpose(-1, -2).contiguous()) + Ov
     return o.reshape(B, H, T, d).to(q.dtype)
 
@@ -199,5 +120,11 @@ def chunk_scan(q, k, v, beta, g, gmu=None, gnu=None, *, rule="delta", ns: int = 
     if r == 1:
         _check(q, k, v, beta, g, gmu, gnu, r)
         return _muon_core(q, k, v, beta, g, gmu, ns)
-    return ChunkScan.apply(q, k, v, beta, g, gmu if r >= 1 else None, gnu if r == 2 else None, r, ns, eps,
-                           torch.is_grad_enabled())
+    gmu = gmu if r >= 1 else None
+    gnu = gnu if r == 2 else None
+    _check(q, k, v, beta, g, gmu, gnu, r)
+    gates = [None if t is None else t.to(torch.float32) for t in (beta, g, gmu, gnu)]
+    # the state checkpoint is written only when a backward can follow
+    record = torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (q, k, v, beta, g, gmu, gnu))
+    o, _ = torch.ops.gmdn.chunk_fwd(q, k, v, *gates, r, ns, eps, record)
+    return o

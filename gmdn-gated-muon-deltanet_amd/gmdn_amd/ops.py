@@ -1,0 +1,248 @@
+"""``torch.ops.gmdn.*``: the C-ABI entry points as registered torch operators.
+
+Each operator wraps one call of ``libgmdn_scan.so`` (include/gmdn_scan.h) on
+the tensors' current stream, with a shape-only fake implementation so that
+``torch.compile`` traces through the scan without a graph break (the
+reference trainer compiles its model, train_ablation.py:420-422), and with
+autograd registered on the forward operators:
+
+* ``gmdn::state_scan(U, K, a, b, m, n, rule, ns, precision, save_moments)
+  -> (S_all, M_all, V_all)`` -- the drop-in scan's forward (reference
+  ``_TritonScan.forward``, fast_scan.py:360-377).  Inputs are float32 and
+  contiguous; ``M_all`` / ``V_all`` are the moment stacks the backward needs
+  (empty unless ``save_moments`` and the rule keeps them).
+* ``gmdn::state_scan_bwd(...) -> (dU, dK, da, db, dm, dn)`` (reference
+  ``_TritonScan.backward``, fast_scan.py:379-396).
+* ``gmdn::chunk_fwd(q, k, v, beta, g, gmu, gnu, rule, ns, eps, record)
+  -> (o, states)`` -- the fused mixer core (reference train_ablation.py:142-187);
+  ``states`` is the library-private state checkpoint (empty unless
+  ``record``).
+* ``gmdn::chunk_bwd(...) -> (dq, dk, dv, dbeta, dg, dgmu, dgnu)``.
+
+Operators cannot return ``None``: absent optional results are empty tensors.
+There is no CPU implementation; CPU tensors never reach these operators (the
+drop-in dispatcher sends them to its eager path).
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+from torch import Tensor
+
+from . import _native as nat
+
+CHUNK = 64
+
+
+def _empty(like: Tensor) -> Tensor:
+    return like.new_empty((0,), dtype=torch.float32)
+
+
+# ------------------------------------------------------------------ Level A
+@torch.library.custom_op("gmdn::state_scan", mutates_args=(), device_types="cuda")
+def state_scan(U: Tensor, K: Tensor, a: Tensor, b: Tensor, m: Tensor, n: Tensor, rule: int, ns: int,
+               precision: int, save_moments: bool) -> tuple[Tensor, Tensor, Tensor]:
+    lib = nat.load()
+    B, H, N, dh, _ = U.shape
+    S_all = torch.empty_like(U)
+    M_all = torch.empty_like(U) if (rule != 0 and save_moments) else _empty(U)
+    V_all = torch.empty_like(U) if (rule == 2 and save_moments) else _empty(U)
+    with torch.cuda.device(U.device):
+        rc = lib.gmdn_scan_fwd(
+            nat.ptr(U), nat.ptr(K), nat.ptr(a), nat.ptr(b), nat.ptr(m), nat.ptr(n), nat.ptr(S_all),
+            nat.ptr(M_all) if M_all.numel() else None, nat.ptr(V_all) if V_all.numel() else None,
+            B * H, N, dh, rule, ns, precision, nat.stream_of(U))
+    nat.check(rc, "gmdn_scan_fwd")
+    return S_all, M_all, V_all
+
+
+@state_scan.register_fake
+def _state_scan_fake(U, K, a, b, m, n, rule, ns, precision, save_moments):
+    S_all = torch.empty_like(U)
+    M_all = torch.empty_like(U) if (rule != 0 and save_moments) else _empty(U)
+    V_all = torch.empty_like(U) if (rule == 2 and save_moments) else _empty(U)
+    return S_all, M_all, V_all
+
+
+@torch.library.custom_op("gmdn::state_scan_bwd", mutates_args=(), device_types="cuda")
+def state_scan_bwd(U: Tensor, K: Tensor, a: Tensor, b: Tensor, m: Tensor, n: Tensor, S_all: Tensor,
+                   M_all: Tensor, V_all: Tensor, gS: Tensor, rule: int, ns: int,
+                   precision: int) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    lib = nat.load()
+    B, H, N, dh, _ = U.shape
+    gS = gS.to(torch.float32).contiguous()
+    dU, dK = torch.empty_like(U), torch.empty_like(K)
+    da, db, dm, dn = (torch.empty_like(a) for _ in range(4))
+    ws_bytes = lib.gmdn_scan_bwd_workspace_bytes(B * H, N, dh, rule, ns)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=U.device) if ws_bytes else None
+    with torch.cuda.device(U.device):
+        rc = lib.gmdn_scan_bwd(
+            nat.ptr(U), nat.ptr(K), nat.ptr(a), nat.ptr(b), nat.ptr(m), nat.ptr(n), nat.ptr(S_all),
+            nat.ptr(M_all) if M_all.numel() else None, nat.ptr(V_all) if V_all.numel() else None,
+            nat.ptr(gS), nat.ptr(dU), nat.ptr(dK), nat.ptr(da), nat.ptr(db), nat.ptr(dm), nat.ptr(dn),
+            nat.ptr(ws), ws_bytes, B * H, N, dh, rule, ns, precision, nat.stream_of(U))
+    nat.check(rc, "gmdn_scan_bwd")
+    return dU, dK, da, db, dm, dn
+
+
+@state_scan_bwd.register_fake
+def _state_scan_bwd_fake(U, K, a, b, m, n, S_all, M_all, V_all, gS, rule, ns, precision):
+    return (torch.empty_like(U), torch.empty_like(K), *(torch.empty_like(a) for _ in range(4)))
+
+
+def _state_scan_setup(ctx, inputs, output):
+    U, K, a, b, m, n, rule, ns, precision, save_moments = inputs
+    S_all, M_all, V_all = output
+    # the moment stacks are saved intermediates: no cotangent is formed for
+    # them (materialised zeros would cost a d x d memset per chunk)
+    ctx.mark_non_differentiable(M_all, V_all)
+    ctx.set_materialize_grads(False)
+    ctx.save_for_backward(U, K, a, b, m, n, S_all, M_all, V_all)
+    ctx.rule, ctx.ns, ctx.precision = rule, ns, precision
+
+
+def _state_scan_backward(ctx, gS, gM, gV):
+    U, K, a, b, m, n, S_all, M_all, V_all = ctx.saved_tensors
+    if gS is None:
+        gS = torch.zeros_like(S_all)
+    grads = torch.ops.gmdn.state_scan_bwd(U, K, a, b, m, n, S_all, M_all, V_all, gS, ctx.rule, ctx.ns,
+                                          ctx.precision)
+    return (*grads, None, None, None, None)
+
+
+state_scan.register_autograd(_state_scan_backward, setup_context=_state_scan_setup)
+
+
+# ------------------------------------------------------------------ Level B
+def chunk_desc(q: Tensor, k: Tensor, v: Tensor, o: Tensor, rule: int, ns: int, eps: float):
+    """The ``gmdn_chunk_desc`` of a call: sizes, rule and the element strides
+    of the (B, H, T, d) token streams."""
+    B, H, T, d = q.shape
+    desc = nat.ChunkDesc()
+    desc.B, desc.H, desc.T, desc.d, desc.C = B, H, T, d, CHUNK
+    desc.rule, desc.ns, desc.dtype, desc.eps = rule, ns, nat.DTYPE_BF16, eps
+    for name, t in (("sq", q), ("sk", k), ("sv", v), ("so", o)):
+        arr = getattr(desc, name)
+        for i in range(3):
+            arr[i] = t.stride(i)
+    return desc
+
+
+def _tok(t: Tensor) -> Tensor:
+    """bf16 token stream with a unit-stride last dim and 16-byte-aligned rows."""
+    if t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:3]) or t.data_ptr() % 16:
+        t = t.contiguous()
+    return t
+
+
+def _gate(t: Optional[Tensor]) -> Optional[Tensor]:
+    """float32 (B, H, T) gate stream, contiguous and 16-byte aligned."""
+    if t is None:
+        return None
+    t = t.to(torch.float32).contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+def _states_numel(q: Tensor, rule: int, ns: int, eps: float) -> int:
+    # the checkpoint size depends on the sizes and the rule only
+    return nat.load().gmdn_chunk_states_bytes(chunk_desc(q, q, q, q, rule, ns, eps)) // 4
+
+
+@torch.library.custom_op("gmdn::chunk_fwd", mutates_args=(), device_types="cuda")
+def chunk_fwd(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, g: Tensor, gmu: Optional[Tensor],
+              gnu: Optional[Tensor], rule: int, ns: int, eps: float, record: bool) -> tuple[Tensor, Tensor]:
+    lib = nat.load()
+    qc, kc, vc = _tok(q), _tok(k), _tok(v)
+    bc, gc, mc, nc = _gate(beta), _gate(g), _gate(gmu), _gate(gnu)
+    o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    desc = chunk_desc(qc, kc, vc, o, rule, ns, eps)
+    states = (torch.empty(lib.gmdn_chunk_states_bytes(desc) // 4, dtype=torch.float32, device=q.device)
+              if record else _empty(q))
+    with torch.cuda.device(q.device):
+        rc = lib.gmdn_chunk_fwd(desc, nat.ptr(qc), nat.ptr(kc), nat.ptr(vc), nat.ptr(bc), nat.ptr(gc),
+                                nat.ptr(mc), nat.ptr(nc), nat.ptr(o),
+                                nat.ptr(states) if record else None, nat.stream_of(q))
+    nat.check(rc, "gmdn_chunk_fwd")
+    return o, states
+
+
+@chunk_fwd.register_fake
+def _chunk_fwd_fake(q, k, v, beta, g, gmu, gnu, rule, ns, eps, record):
+    o = q.new_empty(q.shape)
+    states = q.new_empty((_states_numel(q, rule, ns, eps),), dtype=torch.float32) if record else _empty(q)
+    return o, states
+
+
+@torch.library.custom_op("gmdn::chunk_bwd", mutates_args=(), device_types="cuda")
+def chunk_bwd(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, g: Tensor, gmu: Optional[Tensor],
+              gnu: Optional[Tensor], states: Tensor, dO: Tensor, rule: int, ns: int,
+              eps: float) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    lib = nat.load()
+    qc, kc, vc = _tok(q), _tok(k), _tok(v)
+    bc, gc, mc, nc = _gate(beta), _gate(g), _gate(gmu), _gate(gnu)
+    dOc = _tok(dO.to(torch.bfloat16))
+    # the kernels write dq, dk, dv with the strides of q, k, v
+    dq, dk, dv = (torch.empty_strided(t.shape, t.stride(), dtype=t.dtype, device=t.device) for t in (qc, kc, vc))
+    dbeta, dg = torch.empty_like(bc), torch.empty_like(gc)
+    dgmu = torch.empty_like(mc) if mc is not None else _empty(q)
+    dgnu = torch.empty_like(nc) if nc is not None else _empty(q)
+    desc = chunk_desc(qc, kc, vc, dOc, rule, ns, eps)
+    ws_bytes = lib.gmdn_chunk_bwd_workspace_bytes(desc)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
+    with torch.cuda.device(q.device):
+        rc = lib.gmdn_chunk_bwd(desc, nat.ptr(qc), nat.ptr(kc), nat.ptr(vc), nat.ptr(bc), nat.ptr(gc),
+                                nat.ptr(mc), nat.ptr(nc), nat.ptr(states), nat.ptr(dOc), nat.ptr(dq),
+                                nat.ptr(dk), nat.ptr(dv), nat.ptr(dbeta), nat.ptr(dg),
+                                nat.ptr(dgmu) if mc is not None else None,
+                                nat.ptr(dgnu) if nc is not None else None,
+                                nat.ptr(ws), ws_bytes, nat.stream_of(q))
+    nat.check(rc, "gmdn_chunk_bwd")
+    return dq, dk, dv, dbeta, dg, dgmu, dgnu
+
+
+def _kernel_strides(t: Tensor):
+    """The strides ``_tok`` leaves a token stream with (it copies a stream
+    whose rows are not 16-byte aligned; a fake tensor is taken as aligned)."""
+    if t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:3]):
+        return t.new_empty(t.shape).stride()
+    return t.stride()
+
+
+@chunk_bwd.register_fake
+def _chunk_bwd_fake(q, k, v, beta, g, gmu, gnu, states, dO, rule, ns, eps):
+    dq, dk, dv = (t.new_empty_strided(t.shape, _kernel_strides(t)) for t in (q, k, v))
+    dbeta = beta.new_empty(beta.shape, dtype=torch.float32)
+    dg = g.new_empty(g.shape, dtype=torch.float32)
+    dgmu = gmu.new_empty(gmu.shape, dtype=torch.float32) if gmu is not None else _empty(q)
+    dgnu = gnu.new_empty(gnu.shape, dtype=torch.float32) if gnu is not None else _empty(q)
+    return dq, dk, dv, dbeta, dg, dgmu, dgnu
+
+
+def _chunk_fwd_setup(ctx, inputs, output):
+    q, k, v, beta, g, gmu, gnu, rule, ns, eps, record = inputs
+    o, states = output
+    # the checkpoint is a saved intermediate (see _state_scan_setup)
+    ctx.mark_non_differentiable(states)
+    ctx.set_materialize_grads(False)
+    ctx.save_for_backward(q, k, v, beta, g, gmu, gnu, states)
+    ctx.rule, ctx.ns, ctx.eps, ctx.record = rule, ns, eps, record
+
+
+def _chunk_fwd_backward(ctx, dO, dstates):
+    q, k, v, beta, g, gmu, gnu, states = ctx.saved_tensors
+    if dO is None:
+        dO = torch.zeros_like(q)
+    if not ctx.record:
+        raise RuntimeError("gmdn::chunk_fwd ran without recording its state checkpoint "
+                           "(grad mode was off at the call); it has no backward")
+    if ctx.rule == 2 and q.shape[-1] != 64:
+        raise RuntimeError(f"the fused backward of rule 2 at head dim {q.shape[-1]} is not built "
+                           "(adam's backward is built at d = 64)")
+    dq, dk, dv, dbeta, dg, dgmu, dgnu = torch.ops.gmdn.chunk_bwd(q, k, v, beta, g, gmu, gnu, states, dO,
+                                                                 ctx.rule, ctx.ns, ctx.eps)
+    return (dq, dk, dv, dbeta, dg, dgmu if gmu is not None else None, dgnu if gnu is not None else None,
+            None, None, None, None)
+
+
+chunk_fwd.register_autograd(_chunk_fwd_backward, setup_context=_chunk_fwd_setup)

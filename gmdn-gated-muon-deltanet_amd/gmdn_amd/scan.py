@@ -4,14 +4,18 @@
 semantics of the reference's ``_TritonScan`` (fast_scan.py:334-396): U, K are
 (B, H, N, dh, dh), a, b, m, n are (B, H, N); the result is the stack of
 pre-update states S_0..S_{N-1}, and the backward returns gradients for the
-six tensor inputs (``None`` for rule and ns).  Both directions run the HIP
-kernels of ``libgmdn_scan.so`` on the tensors' current stream.
+six tensor inputs (``None`` for rule and ns).  ``hip_state_scan`` is the same
+computation through the registered operator's autograd, which
+``torch.compile`` traces.  Both run the HIP kernels of ``libgmdn_scan.so``
+(``torch.ops.gmdn.state_scan`` / ``state_scan_bwd``) on the tensors'
+current stream.
 """
 from __future__ import annotations
 
 import torch
 
 from . import _native as nat
+from . import ops  # noqa: F401  -- registers torch.ops.gmdn.*
 
 SUPPORTED_DH = (32, 64, 128)
 _state = {"precision": "tf32"}
@@ -50,50 +54,36 @@ def _check_inputs(U, K, a, b, m, n, rule, ns):
 
 
 def _f32(t):
-    return t.detach().to(torch.float32).contiguous()
+    return t.to(torch.float32).contiguous()
+
+
+def hip_state_scan(U, K, a, b, m, n, rule: int, ns: int):
+    """The scan through ``torch.ops.gmdn.state_scan`` and its registered
+    autograd: float32 contiguous copies of the inputs (differentiable casts),
+    the pre-update states in U's dtype.  Traceable by ``torch.compile``."""
+    _check_inputs(U, K, a, b, m, n, rule, ns)
+    ins = [_f32(t) for t in (U, K, a, b, m, n)]
+    save = torch.is_grad_enabled() and any(t.requires_grad for t in (U, K, a, b, m, n))
+    S_all, _, _ = torch.ops.gmdn.state_scan(*ins, rule, ns, _prec_code(), save)
+    return S_all if U.dtype == torch.float32 else S_all.to(U.dtype)
 
 
 class HipScan(torch.autograd.Function):
+    """``_TritonScan``'s interface over the same two operators."""
+
     @staticmethod
     def forward(ctx, U, K, a, b, m, n, rule, ns):
         _check_inputs(U, K, a, b, m, n, rule, ns)
-        lib = nat.load()
-        B, H, N, dh, _ = U.shape
-        Uc, Kc = _f32(U), _f32(K)
-        ac, bc, mc, nc = (_f32(t) for t in (a, b, m, n))
-        S_all = torch.empty_like(Uc)
-        need_grad = any(ctx.needs_input_grad[:6])
-        M_all = torch.empty_like(Uc) if (rule != 0 and need_grad) else None
-        V_all = torch.empty_like(Uc) if (rule == 2 and need_grad) else None
+        ins = [_f32(t.detach()) for t in (U, K, a, b, m, n)]
         prec = _prec_code()
-        with torch.cuda.device(U.device):
-            rc = lib.gmdn_scan_fwd(
-                nat.ptr(Uc), nat.ptr(Kc), nat.ptr(ac), nat.ptr(bc), nat.ptr(mc), nat.ptr(nc),
-                nat.ptr(S_all), nat.ptr(M_all), nat.ptr(V_all),
-                B * H, N, dh, rule, ns, prec, nat.stream_of(U))
-        nat.check(rc, "gmdn_scan_fwd")
-        ctx.save_for_backward(Uc, Kc, ac, bc, mc, nc, S_all, M_all, V_all)
+        S_all, M_all, V_all = torch.ops.gmdn.state_scan(*ins, rule, ns, prec, any(ctx.needs_input_grad[:6]))
+        ctx.save_for_backward(*ins, S_all, M_all, V_all)
         ctx.rule, ctx.ns, ctx.prec = rule, ns, prec
         ctx.dtypes = tuple(t.dtype for t in (U, K, a, b, m, n))
         return S_all if U.dtype == torch.float32 else S_all.to(U.dtype)
 
     @staticmethod
     def backward(ctx, gS):
-        Uc, Kc, ac, bc, mc, nc, S_all, M_all, V_all = ctx.saved_tensors
-        lib = nat.load()
-        B, H, N, dh, _ = Uc.shape
-        gSc = _f32(gS)
-        dU, dK = torch.empty_like(Uc), torch.empty_like(Kc)
-        da, db, dm, dn = (torch.empty_like(ac) for _ in range(4))
-        ws_bytes = lib.gmdn_scan_bwd_workspace_bytes(B * H, N, dh, ctx.rule, ctx.ns)
-        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=Uc.device) if ws_bytes else None
-        with torch.cuda.device(Uc.device):
-            rc = lib.gmdn_scan_bwd(
-                nat.ptr(Uc), nat.ptr(Kc), nat.ptr(ac), nat.ptr(bc), nat.ptr(mc), nat.ptr(nc),
-                nat.ptr(S_all), nat.ptr(M_all), nat.ptr(V_all), nat.ptr(gSc),
-                nat.ptr(dU), nat.ptr(dK), nat.ptr(da), nat.ptr(db), nat.ptr(dm), nat.ptr(dn),
-                nat.ptr(ws), ws_bytes, B * H, N, dh, ctx.rule, ctx.ns, ctx.prec,
-                nat.stream_of(Uc))
-        nat.check(rc, "gmdn_scan_bwd")
-        grads = [g if g.dtype == dt else g.to(dt) for g, dt in zip((dU, dK, da, db, dm, dn), ctx.dtypes)]
+        grads = torch.ops.gmdn.state_scan_bwd(*ctx.saved_tensors, gS, ctx.rule, ctx.ns, ctx.prec)
+        grads = [g if g.dtype == dt else g.to(dt) for g, dt in zip(grads, ctx.dtypes)]
         return (*grads, None, None)

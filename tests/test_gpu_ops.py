@@ -1,0 +1,81 @@
+"""GPU checks of the registered operators: torch.library.opcheck (schema,
+fake implementation and autograd registration against the real kernels) and
+a torch.compile'd forward + backward (whole graph, aot_eager: torch's
+autograd tracing with no code generation) equal to the eager call."""
+import pytest
+import torch
+
+from gmdn_amd import chunk, ops  # noqa: F401
+from gmdn_amd.workloads import Workload, make_inputs
+from oracle import scan as osc
+
+pytestmark = pytest.mark.gpu
+
+STATIC_CHECKS = ("test_schema", "test_autograd_registration", "test_faketensor", "test_aot_dispatch_static")
+
+
+def _dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda:0")
+
+
+def _scan_inputs(dev, rule, dh=32):
+    gen = torch.Generator().manual_seed(rule)
+    return [t.to(dev) for t in osc.make_scan_inputs(1, 2, 3, 16, dh, generator=gen)]
+
+
+@pytest.mark.parametrize("rule", [0, 1, 2])
+def test_opcheck_state_scan(rule):
+    dev = _dev()
+    ins = [t.requires_grad_(True) for t in _scan_inputs(dev, rule)]
+    torch.library.opcheck(torch.ops.gmdn.state_scan.default, (*ins, rule, 2, 0, True), test_utils=STATIC_CHECKS)
+
+
+@pytest.mark.parametrize("rule,d", [("delta", 64), ("adam", 64)])
+def test_opcheck_chunk_fwd(rule, d):
+    dev = _dev()
+    inp = make_inputs(Workload("t", rule, 1, 2, 128, d), seed=0, device=dev)
+    r = chunk.RULES[rule]
+    args = (inp["q"], inp["k"], inp["v"], inp["beta"], inp["g"], inp["gmu"] if r >= 1 else None,
+            inp["gnu"] if r == 2 else None)
+    args = tuple(t if t is None else t.detach().requires_grad_(True) for t in args)
+    torch.library.opcheck(torch.ops.gmdn.chunk_fwd.default, (*args, r, 3, 1e-6, True), test_utils=STATIC_CHECKS)
+
+
+def _compiled_vs_eager(fn, xs, cot):
+    def step(f):
+        ys = [x.detach().requires_grad_(True) for x in xs]
+        out = f(*ys)
+        grads = torch.autograd.grad(out, ys, cot)
+        return out.detach(), grads
+
+    torch._dynamo.reset()
+    out_e, g_e = step(fn)
+    out_c, g_c = step(torch.compile(fn, backend="aot_eager", fullgraph=True))
+    # the same kernels run both ways; the gate gradients' LDS atomics may
+    # sum in another order, hence a tolerance of a few fp32 ulps
+    torch.testing.assert_close(out_c, out_e, rtol=1e-5, atol=1e-6)
+    for a, b in zip(g_c, g_e):
+        torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("rule", [0, 1, 2])
+def test_compiled_state_scan_matches_eager(rule):
+    import fast_scan
+    dev = _dev()
+    fast_scan.set_backend("triton")
+    try:
+        ins = _scan_inputs(dev, rule, dh=64)
+        gS = torch.randn(ins[0].shape, generator=torch.Generator().manual_seed(9)).to(dev)
+        _compiled_vs_eager(lambda *x: fast_scan.fast_state_scan(*x, rule, 3), ins, gS)
+    finally:
+        fast_scan.set_backend("auto")
+
+
+@pytest.mark.parametrize("rule", ["delta", "adam", "muon"])
+def test_compiled_chunk_scan_matches_eager(rule):
+    dev = _dev()
+    inp = make_inputs(Workload("t", rule, 1, 2, 256, 64), seed=1, device=dev, with_grad_out=True)
+    names = ["q", "k", "v", "beta", "g"] + (["gmu"] if rule != "delta" else []) + (["gnu"] if rule == "adam" else [])
+    _compiled_vs_eager(lambda *x: chunk.chunk_scan(*x, rule=rule, ns=3), [inp[n] for n in names], inp["dO"])
