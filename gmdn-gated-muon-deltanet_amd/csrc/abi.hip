@@ -62,7 +62,7 @@ int gmdn_scan_fwd(const float* U, const float* K, const float* a, const float* b
 size_t gmdn_scan_bwd_workspace_bytes(int64_t BH, int64_t N, int32_t dh, int32_t rule, int32_t ns) {
   if (BH <= 0 || N <= 0 || !dh_ok(dh) || ns < 0) return 0;
   if (rule == 2) return (size_t)(BH * N * (dh / 16) * 4) * sizeof(float);
-  if (rule == 1) return (size_t)(BH * muon_bwd_ws_floats(dh, ns)) * sizeof(float);
+  if (rule == 1) return (size_t)muon_bwd_ws_total(BH, N, dh, ns) * sizeof(float);
   return 0;
 }
 

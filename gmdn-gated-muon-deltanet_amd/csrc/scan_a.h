@@ -24,10 +24,16 @@ hipError_t scan_bwd_dk_launch(const ScanArgs& s, const float* part);
 hipError_t scan_fwd_muon_launch(const ScanArgs& s);
 hipError_t scan_bwd_muon_launch(const ScanArgs& s, float* ws);
 
-// workspace floats per (b, h) for the muon backward: the bf16x3 kernel keeps
-// 2 ns + 2 matrices (iterates X_k, products Z_k, M_i, Mbar), the fp32 one 4 + ns
-__host__ __device__ inline int64_t muon_bwd_ws_floats(int dh, int ns) {
-  return (int64_t)(2 * ns + 2 > 4 + ns ? 2 * ns + 2 : 4 + ns) * dh * dh;
+// workspace floats per (b, h) of the fp32 ('ieee') muon backward: 4 + ns matrices
+__host__ __device__ inline int64_t muon_bwd_ws_floats(int dh, int ns) { return (int64_t)(4 + ns) * dh * dh; }
+// workspace floats of the whole muon backward, either precision: the bf16x3
+// kernels keep per chunk the iterates X_0 .. X_ns, the products Z_0 .. Z_{ns-1}
+// and M_i (2 ns + 2 matrices), per (b, h) the carried Mbar, per chunk |M_i|
+inline int64_t muon_bwd_ws_total(int64_t BH, int64_t N, int dh, int ns) {
+  const int64_t mat = (int64_t)dh * dh;
+  const int64_t x3 = BH * N * (2 * ns + 2) * mat + BH * mat + BH * N;
+  const int64_t f32 = BH * muon_bwd_ws_floats(dh, ns);
+  return x3 > f32 ? x3 : f32;
 }
 
 }  // namespace gmdn

@@ -7,9 +7,11 @@
 // Forward: X and P live in LDS (2 D^2 fp32 worth): as split bf16 planes for
 // the bf16x3 precision, as swizzled fp32 for the exact one; K_i is read
 // straight from global memory (it is used once per chunk).
-// Backward: X_k, P, Xbar and Bbar (4 D^2) exceed LDS at D = 128, so they live
-// in a per-(b, h) global workspace (L2 resident), followed by the ns stored
-// iterates X_0 .. X_{ns-1} (written and re-read by the same lanes).
+// Backward with fp32 products (precision 'ieee'): X_k, P, Xbar and Bbar
+// (4 D^2) exceed LDS at D = 128, so they live in a per-(b, h) global workspace
+// (L2 resident), followed by the ns stored iterates X_0 .. X_{ns-1} (written
+// and re-read by the same lanes).  The bf16x3 backward is described at its
+// kernels.
 #include "ns.h"
 #include "scan_a.h"
 
@@ -211,30 +213,105 @@ scan_bwd_muon(const float* __restrict__ U, const float* __restrict__ K,
   }
 }
 
-// The backward with bf16x3 products.  Per chunk (reverse order), on the
-// NSSplit engine with two LDS slots of one split matrix each (A, B):
-//   1. K_i staged into B; G = U - S_i K_i (column reads of K_i); M_i, X_0.
-//   2. The ns forward steps again, storing each iterate X_k and each
-//      Z_k = b P_k + c P_k^2 as the wave's rows in split pieces (workspace).
-//   3. The VJP steps, k = ns-1 .. 0, with Xbar published in A and X_k in B:
+// The backward with bf16x3 products, in two kernels on the NSSplit engine
+// (two LDS slots of one split matrix each, A and B).
+//
+// scan_bwd_muon_pre, one workgroup per (b, h, chunk): the forward iterates do
+// not depend on the cotangent, so they are rebuilt for every chunk at once
+// across the chip.  K_i staged into B; G = U - S_i K_i; M_i = m M_{i-1} + G;
+// X_0 = M_i / (|M_i| + eps); then the ns steps, storing each iterate X_k
+// (k = 0 .. ns) and each Z_k = b P_k + c P_k^2 as the wave's rows in split
+// pieces, M_i in fp32 and |M_i|.  Workspace per chunk: 2 ns + 2 matrices.
+//
+// scan_bwd_muon_x3, one workgroup per (b, h), chunks in reverse order:
+//   1. da_i = <Sb, S_i>, db_i = <Sb, X_ns>; Xbar = b Sb.
+//   2. The VJP steps, k = ns-1 .. 0, with Xbar published in A and X_k in B:
 //        Q    = a Xbar + Z_k Xbar                 (A column reads, Z_k rows)
 //        Bs   = Bbar + Bbar^T, Bbar = Xbar X_k^T  (A and B row reads)
 //        Y    = X_k (X_k^T Bs) = P_k Bs           (B column, then row reads)
 //        Y^T  read back transposed after publishing Y in A
 //        Xbar <- Q + (b Bs + c (Y + Y^T)) X_k     (B column reads)
 //      (P_k, Bs and Z_k are symmetric.)  Six D^3 products per step.
-//   4. The normalisation VJP, Gb = dU_i, and Sb <- a Sb - Gb K_i^T + gS with
-//      K_i staged into B again (row reads).
-// M_i and Mbar pass through the workspace as fp32 rows of their wave.
+//   3. The normalisation VJP, Gb = dU_i, and Sb <- a Sb - Gb K_i^T + gS with
+//      K_i staged into B (row reads).
+// Mbar passes from chunk to chunk through the workspace as fp32 rows of their
+// wave.
+template <int D>
+struct MuonBwdWs {
+  // per chunk: X_0 .. X_ns, Z_0 .. Z_{ns-1}, M_i; then Mbar per (b, h); then |M_i| per chunk
+  int64_t mat, per_chunk, BH, N;
+  GMDN_DEV MuonBwdWs(int64_t BH_, int64_t N_, int ns) : mat((int64_t)D * D), per_chunk((2 * ns + 2) * mat), BH(BH_), N(N_) {}
+  GMDN_DEV float* X(float* ws, int64_t si, int k) const { return ws + si * per_chunk + k * mat; }
+  GMDN_DEV float* Z(float* ws, int64_t si, int ns, int k) const { return ws + si * per_chunk + (ns + 1 + k) * mat; }
+  GMDN_DEV float* M(float* ws, int64_t si, int ns) const { return ws + si * per_chunk + (2 * ns + 1) * mat; }
+  GMDN_DEV float* Mbar(float* ws, int64_t bh) const { return ws + BH * N * per_chunk + bh * mat; }
+  GMDN_DEV float* norm(float* ws) const { return ws + BH * N * per_chunk + BH * mat; }
+};
+
 template <int D>
 __global__ void __launch_bounds__(D * 4)
-scan_bwd_muon_x3(const float* __restrict__ U, const float* __restrict__ K,
-                 const float* __restrict__ av, const float* __restrict__ bv,
-                 const float* __restrict__ mv, const float* __restrict__ S_all,
-                 const float* __restrict__ M_all, const float* __restrict__ gS,
-                 float* __restrict__ dU, float* __restrict__ da, float* __restrict__ db,
-                 float* __restrict__ dm, float* __restrict__ dn, float* __restrict__ ws, int N,
-                 int ns) {
+scan_bwd_muon_pre(const float* __restrict__ U, const float* __restrict__ K,
+                  const float* __restrict__ mv, const float* __restrict__ S_all,
+                  const float* __restrict__ M_all, float* __restrict__ ws, int64_t BH, int N, int ns) {
+  using NSX = NSSplit<D>;
+  using P = PrecX3;
+  using Op = P::Op;
+  constexpr int NT = D / 16, NKB = D / 32, NW = D / 16;
+  extern __shared__ __align__(16) float smem[];
+  const lds_ptr SA = lds_base(smem), SB = SA + NSX::BYTES;
+  float* red = smem + 2 * NSX::BYTES / 4;
+  const NSX nsx;
+  const MuonBwdWs<D> W(BH, N, ns);
+  const int64_t si = blockIdx.x;  // = bh * N + i
+  const int l = lane_id(), G = l >> 4, rl = l & 15;
+  const int r0 = 16 * wave_id();
+  const int64_t mat = (int64_t)D * D;
+  auto roff = [&](int t) { return (int64_t)(r0 + rl) * D + 16 * t + 4 * G; };
+
+  NSX::template stage<D * 4>(SB, K + si * mat);
+  Op Bop[NKB];
+  {
+    f32x4 Si[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) Si[t] = *reinterpret_cast<const f32x4*>(S_all + si * mat + roff(t));
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) Bop[kb] = P::pack(-Si[2 * kb], -Si[2 * kb + 1]);
+  }
+  __syncthreads();  // K_i staged
+  const float gm = mv[si];
+  float* WM = W.M(ws, si, ns);
+  f32x4 X[NT];
+  float sq = 0.f;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    f32x4 g = *reinterpret_cast<const f32x4*>(U + si * mat + roff(t));
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) g = P::mma(nsx.col(SB, kb, t), Bop[kb], g);
+    const f32x4 Mp = *reinterpret_cast<const f32x4*>(M_all + si * mat + roff(t));
+    X[t] = gm * Mp + g;
+    *reinterpret_cast<f32x4*>(WM + roff(t)) = X[t];
+    sq += X[t][0] * X[t][0] + X[t][1] * X[t][1] + X[t][2] * X[t][2] + X[t][3] * X[t][3];
+  }
+  const float nf = sqrtf(block_sum<NW>(sq, red));  // (its barriers also retire B's K_i reads)
+  if (threadIdx.x == 0) W.norm(ws)[si] = nf;
+  const float scale = 1.f / (nf + 1e-7f);
+#pragma unroll
+  for (int t = 0; t < NT; ++t) X[t] = X[t] * scale;
+  for (int k = 0; k < ns; ++k) {
+    NSX::store_own(W.X(ws, si, k), X);
+    nsx.step(X, SA, SB, W.Z(ws, si, ns, k));
+  }
+  NSX::store_own(W.X(ws, si, ns), X);
+}
+
+template <int D>
+__global__ void __launch_bounds__(D * 4)
+scan_bwd_muon_x3(const float* __restrict__ K, const float* __restrict__ av,
+                 const float* __restrict__ bv, const float* __restrict__ mv,
+                 const float* __restrict__ S_all, const float* __restrict__ M_all,
+                 const float* __restrict__ gS, float* __restrict__ dU, float* __restrict__ da,
+                 float* __restrict__ db, float* __restrict__ dm, float* __restrict__ dn,
+                 float* __restrict__ ws, int64_t BH, int N, int ns) {
   using NSX = NSSplit<D>;
   using P = PrecX3;
   using Op = P::Op;
@@ -245,15 +322,12 @@ scan_bwd_muon_x3(const float* __restrict__ U, const float* __restrict__ K,
 
   const NSX nsx;
   const uint32_t tb = NSX::tbase();
+  const MuonBwdWs<D> W(BH, N, ns);
   const int64_t bh = blockIdx.x;
   const int l = lane_id(), G = l >> 4, rl = l & 15;
   const int r0 = 16 * wave_id();
   const int64_t mat = (int64_t)D * D;
-  float* wsb = ws + bh * muon_bwd_ws_floats(D, ns);
-  float* WX = wsb;                           // X_0 .. X_{ns-1}
-  float* WZ = wsb + ns * mat;                // Z_0 .. Z_{ns-1}
-  float* WM = wsb + 2 * ns * mat;            // M_i
-  float* WMb = wsb + (2 * ns + 1) * mat;     // Mbar carried to chunk i-1
+  float* WMb = W.Mbar(ws, bh);  // Mbar carried to chunk i-1
   auto roff = [&](int t) { return (int64_t)(r0 + rl) * D + 16 * t + 4 * G; };
 
   f32x4 Sb[NT];
@@ -262,58 +336,28 @@ scan_bwd_muon_x3(const float* __restrict__ U, const float* __restrict__ K,
 
   for (int i = N - 1; i >= 0; --i) {
     const int64_t si = bh * N + i;
-    const float* Ki = K + si * mat;
     const float ga = av[si], gb = bv[si], gm = mv[si];
-    // ---- 1. G, M_i, X_0
-    NSX::template stage<D * 4>(SB, Ki);
-    float pda = 0.f;
-    Op Bop[NKB];
+    // ---- 1. da_i = <Sb, S_i>, db_i = <Sb, msign(M_i)>
+    float pda = 0.f, pdb = 0.f;
     {
-      f32x4 Si[NT];
+      const float* Xs = W.X(ws, si, ns);
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        Si[t] = *reinterpret_cast<const f32x4*>(S_all + si * mat + roff(t));
-        pda += Sb[t][0] * Si[t][0] + Sb[t][1] * Si[t][1] + Sb[t][2] * Si[t][2] + Sb[t][3] * Si[t][3];
+        const f32x4 Si = *reinterpret_cast<const f32x4*>(S_all + si * mat + roff(t));
+        const f32x4 Xn = unsplit_piece(*reinterpret_cast<const bf16x8*>(Xs + roff(t)));
+        pda += Sb[t][0] * Si[0] + Sb[t][1] * Si[1] + Sb[t][2] * Si[2] + Sb[t][3] * Si[3];
+        pdb += Sb[t][0] * Xn[0] + Sb[t][1] * Xn[1] + Sb[t][2] * Xn[2] + Sb[t][3] * Xn[3];
       }
-#pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) Bop[kb] = P::pack(-Si[2 * kb], -Si[2 * kb + 1]);
     }
-    __syncthreads();  // K_i staged
-    f32x4 X[NT];
-    float sq = 0.f;
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      f32x4 g = *reinterpret_cast<const f32x4*>(U + si * mat + roff(t));
-#pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) g = P::mma(nsx.col(SB, kb, t), Bop[kb], g);
-      const f32x4 Mp = *reinterpret_cast<const f32x4*>(M_all + si * mat + roff(t));
-      X[t] = gm * Mp + g;
-      *reinterpret_cast<f32x4*>(WM + roff(t)) = X[t];
-      sq += X[t][0] * X[t][0] + X[t][1] * X[t][1] + X[t][2] * X[t][2] + X[t][3] * X[t][3];
-    }
-    const float nf = sqrtf(block_sum<NW>(sq, red));
-    const float nrm = nf + 1e-7f;
-    const float scale = 1.f / nrm;
-#pragma unroll
-    for (int t = 0; t < NT; ++t) X[t] = X[t] * scale;
-    // ---- 2. the forward iterates again (B's K_i is dead after the sum's barriers)
-    for (int k = 0; k < ns; ++k) {
-      NSX::store_own(WX + k * mat, X);
-      nsx.step(X, SA, SB, WZ + k * mat);
-    }
-    // db_i = <Sb, msign(M_i)>, da_i = <Sb, S_i>
-    float pdb = 0.f;
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-      pdb += Sb[t][0] * X[t][0] + Sb[t][1] * X[t][1] + Sb[t][2] * X[t][2] + Sb[t][3] * X[t][3];
     const float dbv = block_sum<NW>(pdb, red);
     const float dav = block_sum<NW>(pda, red);
-    // ---- 3. Xbar = b Sb pulled back through the ns steps (X is its register home)
+    // ---- 2. Xbar = b Sb pulled back through the ns steps (X is its register home)
+    f32x4 X[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) X[t] = gb * Sb[t];
     if (ns > 0) {
       nsx.publish(SA, X);
-      nsx.stage_own(SB, WX + (ns - 1) * mat);
+      nsx.stage_own(SB, W.X(ws, si, ns - 1));
       __syncthreads();
     }
     for (int k = ns - 1; k >= 0; --k) {
@@ -321,12 +365,12 @@ scan_bwd_muon_x3(const float* __restrict__ U, const float* __restrict__ K,
       {
         Op Bxb[NKB], Bz[NKB];
         NSX::pack_all(X, Bxb);
-        NSX::load_own(WZ + k * mat, Bz);
+        NSX::load_own(W.Z(ws, si, ns, k), Bz);
 #pragma unroll
         for (int tc = 0; tc < NT; ++tc) Q[tc] = nsx.colprod(SA, tc, Bz, NS_A * X[tc]);
         __builtin_amdgcn_sched_barrier(0);  // keep the phases' operand loads apart
         Op Bk[NKB];
-        NSX::load_own(WX + k * mat, Bk);
+        NSX::load_own(W.X(ws, si, k), Bk);
 #pragma unroll
         for (int tr = 0; tr < NT; ++tr) {
           f32x4 acc = zero4();
@@ -343,10 +387,10 @@ scan_bwd_muon_x3(const float* __restrict__ U, const float* __restrict__ K,
       {
         Op Bso[NKB], Wo[NKB];
         NSX::pack_all(Bs, Bso);
-        f32x4 W[NT];
+        f32x4 Wt[NT];
 #pragma unroll
-        for (int tc = 0; tc < NT; ++tc) W[tc] = nsx.colprod(SB, tc, Bso, zero4());  // (X_k^T Bs)[c][r]
-        NSX::pack_all(W, Wo);
+        for (int tc = 0; tc < NT; ++tc) Wt[tc] = nsx.colprod(SB, tc, Bso, zero4());  // (X_k^T Bs)[c][r]
+        NSX::pack_all(Wt, Wo);
 #pragma unroll
         for (int tr = 0; tr < NT; ++tr) Y[tr] = nsx.rowprod(SB, tr, Wo);  // (X_k W)[r'][r]
       }
@@ -364,21 +408,24 @@ scan_bwd_muon_x3(const float* __restrict__ U, const float* __restrict__ K,
       __syncthreads();  // every read of A and B done
       if (k > 0) {
         nsx.publish(SA, X);
-        nsx.stage_own(SB, WX + (k - 1) * mat);
+        nsx.stage_own(SB, W.X(ws, si, k - 1));
         __syncthreads();
       }
     }
-    // ---- 4. normalisation: Mbar = Xbar/nrm - <Xbar, M_i>/nrm^2 * M_i/max(|M_i|, 1e-12)
+    // ---- 3. normalisation: Mbar = Xbar/nrm - <Xbar, M_i>/nrm^2 * M_i/max(|M_i|, 1e-12)
+    const float* WM = W.M(ws, si, ns);
+    const float nf = W.norm(ws)[si];
+    const float nrm = nf + 1e-7f;
     float pdot = 0.f;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const f32x4 Mi = *reinterpret_cast<const f32x4*>(WM + roff(t));
       pdot += X[t][0] * Mi[0] + X[t][1] * Mi[1] + X[t][2] * Mi[2] + X[t][3] * Mi[3];
     }
-    const float dot = block_sum<NW>(pdot, red);
+    NSX::template stage<D * 4>(SB, K + si * mat);  // K_i, for the row reads of the Sb update
+    const float dot = block_sum<NW>(pdot, red);     // (its barriers also publish K_i in B)
     const float cM = dot / (nrm * nrm) / fmaxf(nf, 1e-12f);
     float pdm = 0.f;
-    NSX::template stage<D * 4>(SB, Ki);  // K_i again, for the row reads of the Sb update
     Op Bg[NKB];
     {
       f32x4 Gb[NT];
@@ -396,7 +443,7 @@ scan_bwd_muon_x3(const float* __restrict__ U, const float* __restrict__ K,
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb) Bg[kb] = P::pack(-Gb[2 * kb], -Gb[2 * kb + 1]);
     }
-    const float dmv = block_sum<NW>(pdm, red);  // (its barriers also publish K_i in B)
+    const float dmv = block_sum<NW>(pdm, red);
     // Sb <- a Sb - Gb K^T + gS : A = K rows
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -411,7 +458,7 @@ scan_bwd_muon_x3(const float* __restrict__ U, const float* __restrict__ K,
       dm[si] = dmv;
       dn[si] = 0.f;
     }
-    __syncthreads();  // B's K_i read by every wave before chunk i-1 restages it
+    __syncthreads();  // B's K_i read by every wave before chunk i-1 publishes into A and B
   }
 }
 
@@ -430,11 +477,15 @@ template <int D, int PREC>
 static hipError_t launch_bwd_muon(const ScanArgs& s, float* ws) {
   if constexpr (PREC == 0) {
     const int lds = 2 * NSSplit<D>::BYTES + 64;
+    auto kp = scan_bwd_muon_pre<D>;
     auto k3 = scan_bwd_muon_x3<D>;
-    hipError_t e = hipFuncSetAttribute((const void*)k3, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    hipError_t e = hipFuncSetAttribute((const void*)kp, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (e == hipSuccess) e = hipFuncSetAttribute((const void*)k3, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k3, dim3((unsigned)s.BH), dim3(D * 4), lds, s.stream, s.U, s.K, s.a, s.b, s.m,
-                       s.S_all, s.M_all, s.gS, s.dU, s.da, s.db, s.dm, s.dn, ws, (int)s.N, s.ns);
+    hipLaunchKernelGGL(kp, dim3((unsigned)(s.BH * s.N)), dim3(D * 4), lds, s.stream, s.U, s.K, s.m, s.S_all,
+                       s.M_all, ws, s.BH, (int)s.N, s.ns);
+    hipLaunchKernelGGL(k3, dim3((unsigned)s.BH), dim3(D * 4), lds, s.stream, s.K, s.a, s.b, s.m, s.S_all,
+                       s.M_all, s.gS, s.dU, s.da, s.db, s.dm, s.dn, ws, s.BH, (int)s.N, s.ns);
     return hipGetLastError();
   }
   auto kern = scan_bwd_muon<D, PREC>;

@@ -68,9 +68,13 @@ def test_scan_bwd_workspace_contract():
     lib = _native.load()
     assert lib.gmdn_scan_bwd_workspace_bytes(4, 16, 64, 0, 3) == 0
     assert lib.gmdn_scan_bwd_workspace_bytes(4, 16, 64, 2, 3) == 4 * 16 * 4 * 4 * 4
-    # muon: max(2 ns + 2, 4 + ns) d x d matrices per (b, h)
-    assert lib.gmdn_scan_bwd_workspace_bytes(4, 16, 64, 1, 3) == 4 * 8 * 64 * 64 * 4
-    assert lib.gmdn_scan_bwd_workspace_bytes(4, 16, 64, 1, 1) == 4 * 5 * 64 * 64 * 4
+    # muon: per chunk 2 ns + 2 d x d matrices and |M_i|, per (b, h) one matrix
+    # (at least the 4 + ns matrices per (b, h) of the fp32 kernel)
+    BH, N, mat = 4, 16, 64 * 64
+    for ns in (1, 3, 5):
+        x3 = BH * N * (2 * ns + 2) * mat + BH * mat + BH * N
+        assert lib.gmdn_scan_bwd_workspace_bytes(BH, N, 64, 1, ns) == 4 * max(x3, BH * (4 + ns) * mat)
+    assert lib.gmdn_scan_bwd_workspace_bytes(1, 1, 64, 1, 0) == 4 * max(2 * mat + mat + 1, 4 * mat)
     p = [0x1000] * 16
     # adam / muon without workspace -> GMDN_ERR_WORKSPACE
     assert lib.gmdn_scan_bwd(*p, None, 0, 4, 16, 64, 2, 3, 0, None) == 3
