@@ -363,23 +363,26 @@ scan_bwd_muon_x3(const float* __restrict__ K, const float* __restrict__ av,
     for (int k = ns - 1; k >= 0; --k) {
       f32x4 Q[NT], Bs[NT];
       {
-        Op Bxb[NKB], Bz[NKB];
-        NSX::pack_all(X, Bxb);
+        Op Bz[NKB];
         NSX::load_own(W.Z(ws, si, ns, k), Bz);
 #pragma unroll
         for (int tc = 0; tc < NT; ++tc) Q[tc] = nsx.colprod(SA, tc, Bz, NS_A * X[tc]);
-        __builtin_amdgcn_sched_barrier(0);  // keep the phases' operand loads apart
-        Op Bk[NKB];
-        NSX::load_own(W.X(ws, si, k), Bk);
+      }
+      __builtin_amdgcn_sched_barrier(0);  // keep the phases' operands apart
+      {
+        // the wave's own rows of X_k (B) and Xbar (A) as B operands, read
+        // from the published planes one k-block at a time
+        const int w = wave_id();
 #pragma unroll
-        for (int tr = 0; tr < NT; ++tr) {
-          f32x4 acc = zero4();
+        for (int tr = 0; tr < NT; ++tr) Bs[tr] = zero4();
 #pragma unroll
-          for (int kb = 0; kb < NKB; ++kb) {
-            acc = P::mma(nsx.row(SA, tr, kb), Bk[kb], acc);   // Bbar[r'][r]
-            acc = P::mma(nsx.row(SB, tr, kb), Bxb[kb], acc);  // Bbar[r][r']
+        for (int kb = 0; kb < NKB; ++kb) {
+          const Op ok = nsx.row(SB, w, kb), ox = nsx.row(SA, w, kb);
+#pragma unroll
+          for (int tr = 0; tr < NT; ++tr) {
+            Bs[tr] = P::mma(nsx.row(SA, tr, kb), ok, Bs[tr]);  // Bbar[r'][r]
+            Bs[tr] = P::mma(nsx.row(SB, tr, kb), ox, Bs[tr]);  // Bbar[r][r']
           }
-          Bs[tr] = acc;
         }
       }
       __builtin_amdgcn_sched_barrier(0);
