@@ -152,11 +152,14 @@ struct NSBlock {
 
 // The forward quintic step with bf16x3 products and the shared matrices kept
 // as split bf16 planes in LDS (hi plane then lo plane, each D x D in the
-// 16-byte-group XOR swizzle of the chunk kernels).  The publishing wave splits
-// its own rows once; every operand read is then two 8-byte row reads or two
-// transposing reads per plane, in the pair k order of the register operands.
-// A row's swizzle depends only on the row modulo 16, so each lane keeps one
-// LDS base per distinct column pattern and row tiles are immediate offsets.
+// 16-byte-group XOR swizzle of the chunk kernels).  Within every 32 columns
+// the 4-column blocks are stored in the order 0 4 1 5 2 6 3 7, so the eight
+// values of a row operand in the pair k order of the register operands
+// (columns 4G .. 4G+3 and 16+4G .. 16+4G+3) are one 16-byte row read per
+// plane; column operands are two transposing reads per plane.  The
+// publishing wave splits its own rows once.  A row's swizzle depends only on
+// the row modulo 16, so each lane keeps one LDS base per distinct column
+// pattern and row tiles are immediate offsets.
 template <int D>
 struct NSSplit {
   static constexpr int NT = D / 16;
@@ -169,20 +172,26 @@ struct NSSplit {
   using Op = P::Op;
   static_assert(L::MASK < 16, "row tiles of 16 must keep the swizzle");
 
-  uint32_t prow[NKB][2];  // row reads: row lc, columns 32 kb + 16 h + 4G
-  uint32_t pcol[NT];      // column reads: row 4G + lc/4, columns 16 tc + 4 (lc & 3)
-  uint32_t ppub[NT];      // publishing: row 16 w + lc, columns 16 c + 4G
+  uint32_t prow[NKB];  // row reads: row lc, columns 32 kb + {4G .. 4G+3, 16+4G .. 16+4G+3}
+  uint32_t pcol[NT];   // column reads: row 4G + lc/4, columns 16 tc + 4 (lc & 3) ..
+  uint32_t ppub[NT];   // publishing: row 16 w + lc, columns 16 c + 4G ..
+
+  // stored column of the 4-column block that starts at column c
+  static GMDN_DEV int scol(int c) {
+    const int b = (c >> 2) & 7;
+    return (c & ~31) + 4 * (2 * (b & 3) + (b >> 2));
+  }
+  // LDS byte offset of (row r, the block starting at column c) in a plane
+  static GMDN_DEV uint32_t off(int r, int c) { return swz_off<L>(r, scol(c)); }
 
   GMDN_DEV NSSplit() {
     const int l = lane_id(), lc = l & 15, G = l >> 4, w = wave_id();
 #pragma unroll
-    for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) prow[kb][h] = swz_off<L>(lc, 32 * kb + 16 * h + 4 * G);
+    for (int kb = 0; kb < NKB; ++kb) prow[kb] = swz_off<L>(lc, 32 * kb + 8 * G);  // stored slots 2G, 2G+1
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      pcol[t] = swz_off<L>(4 * G + (lc >> 2), 16 * t + 4 * (lc & 3));
-      ppub[t] = swz_off<L>(16 * w + lc, 16 * t + 4 * G);
+      pcol[t] = off(4 * G + (lc >> 2), 16 * t + 4 * (lc & 3));
+      ppub[t] = off(16 * w + lc, 16 * t + 4 * G);
     }
   }
 
@@ -200,7 +209,7 @@ struct NSSplit {
                   "pieces split evenly, in row steps that keep the swizzle");
     const int j = threadIdx.x, r = j / PR, c = (j % PR) * 4;
     const float* src = g + r * D + c;
-    const uint32_t dst = swz_off<L>(r, c);
+    const uint32_t dst = off(r, c);
     constexpr int NQ = D * PR / NTHR, RSTEP = NTHR / PR;
     f32x4 x[NQ];
 #pragma unroll
@@ -237,10 +246,10 @@ struct NSSplit {
   }
   // lane (r, G) takes M[16 tr + r][32 kb + pair(G, s)]
   GMDN_DEV Op row(lds_cptr m, int tr, int kb) const {
-    const lds_cptr a = m + prow[kb][0] + tr * 16 * ROWB, b = m + prow[kb][1] + tr * 16 * ROWB;
+    const lds_cptr a = m + prow[kb] + tr * 16 * ROWB;
     Op o;
-    o.hi = cat8(lds_ld<bf16x4>(a), lds_ld<bf16x4>(b));
-    o.lo = cat8(lds_ld<bf16x4>(a + PLANE), lds_ld<bf16x4>(b + PLANE));
+    o.hi = lds_ld<bf16x8>(a);
+    o.lo = lds_ld<bf16x8>(a + PLANE);
     return o;
   }
   // lane (c, G) takes M[32 kb + pair(G, s)][16 tc + c]
@@ -297,7 +306,7 @@ struct NSSplit {
   // (tb = the lane's base for them, `tbase`)
   GMDN_DEV static uint32_t tbase() {
     const int l = lane_id(), lc = l & 15;
-    return swz_off<L>(4 * (l >> 4) + (lc >> 2), 16 * wave_id() + 4 * (lc & 3));
+    return off(4 * (l >> 4) + (lc >> 2), 16 * wave_id() + 4 * (lc & 3));
   }
   static GMDN_DEV f32x4 tview(lds_cptr m, uint32_t tb, int tr) {
     const lds_cptr a = m + tb + tr * 16 * ROWB;

@@ -490,11 +490,12 @@ static hipError_t launch_bwd_muon(const ScanArgs& s, float* ws) {
     hipLaunchKernelGGL(k3, dim3((unsigned)s.BH), dim3(D * 4), lds, s.stream, s.K, s.a, s.b, s.m, s.S_all,
                        s.M_all, s.gS, s.dU, s.da, s.db, s.dm, s.dn, ws, s.BH, (int)s.N, s.ns);
     return hipGetLastError();
+  } else {
+    auto kern = scan_bwd_muon<D, PREC>;
+    hipLaunchKernelGGL(kern, dim3((unsigned)s.BH), dim3(D * 4), 0, s.stream, s.U, s.K, s.a, s.b, s.m,
+                       s.S_all, s.M_all, s.gS, s.dU, s.da, s.db, s.dm, s.dn, ws, (int)s.N, s.ns);
+    return hipGetLastError();
   }
-  auto kern = scan_bwd_muon<D, PREC>;
-  hipLaunchKernelGGL(kern, dim3((unsigned)s.BH), dim3(D * 4), 0, s.stream, s.U, s.K, s.a, s.b, s.m,
-                     s.S_all, s.M_all, s.gS, s.dU, s.da, s.db, s.dm, s.dn, ws, (int)s.N, s.ns);
-  return hipGetLastError();
 }
 
 hipError_t scan_fwd_muon_launch(const ScanArgs& s) {
