@@ -271,6 +271,22 @@ struct NSSplit {
     for (int kb = 0; kb < NKB; ++kb) acc = P::mma(col(pub, kb, tc), B[kb], acc);
     return acc;
   }
+  // All NT tiles of a product at once, k-block outer: consecutive MFMAs go
+  // to independent accumulators and a k-block's reads issue together.
+  // acc[tr] += tile [r'][r] = sum_k pub[r'][k] B[k][r]
+  GMDN_DEV void rowprod_all(lds_cptr pub, const Op (&B)[NKB], f32x4 (&acc)[NT]) const {
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+      for (int tr = 0; tr < NT; ++tr) acc[tr] = P::mma(row(pub, tr, kb), B[kb], acc[tr]);
+  }
+  // acc[tc] += tile [c][r] = sum_k pub[k][c] B[k][r]
+  GMDN_DEV void colprod_all(lds_cptr pub, const Op (&B)[NKB], f32x4 (&acc)[NT]) const {
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+      for (int tc = 0; tc < NT; ++tc) acc[tc] = P::mma(col(pub, kb, tc), B[kb], acc[tc]);
+  }
   // The wave's rows of a matrix kept in global memory as split pieces (the
   // layout `store_own` writes) -> planes at m
   GMDN_DEV void stage_own(lds_ptr m, const float* g) const {
@@ -324,20 +340,26 @@ struct NSSplit {
     pack_all(XT, Bx);
     f32x4 Pc[NT];
 #pragma unroll
-    for (int tr = 0; tr < NT; ++tr) Pc[tr] = rowprod(XM, tr, Bx);
+    for (int tr = 0; tr < NT; ++tr) Pc[tr] = zero4();
+    rowprod_all(XM, Bx, Pc);
     // P is symmetric: the column block is also the wave's rows of P
     publish(PM, Pc);
     __syncthreads();
     Op Bp[NKB];
     pack_all(Pc, Bp);
     // Z = b P + c P^2, in place of the wave's block of P (now held by Bp)
+    // as c ((b / c) P + P^2), accumulating P^2 onto the scaled block
 #pragma unroll
-    for (int tr = 0; tr < NT; ++tr) Pc[tr] = NS_B * Pc[tr] + NS_C * rowprod(PM, tr, Bp);
+    for (int tr = 0; tr < NT; ++tr) Pc[tr] = (NS_B / NS_C) * Pc[tr];
+    rowprod_all(PM, Bp, Pc);
+#pragma unroll
+    for (int tr = 0; tr < NT; ++tr) Pc[tr] = NS_C * Pc[tr];
     if (zst) store_own(zst, Pc);
     Op Bz[NKB];
     pack_all(Pc, Bz);
 #pragma unroll
-    for (int tc = 0; tc < NT; ++tc) XT[tc] = colprod(XM, tc, Bz, NS_A * XT[tc]);
+    for (int tc = 0; tc < NT; ++tc) XT[tc] = NS_A * XT[tc];
+    colprod_all(XM, Bz, XT);
     __syncthreads();
   }
 };

@@ -366,7 +366,8 @@ scan_bwd_muon_x3(const float* __restrict__ K, const float* __restrict__ av,
         Op Bz[NKB];
         NSX::load_own(W.Z(ws, si, ns, k), Bz);
 #pragma unroll
-        for (int tc = 0; tc < NT; ++tc) Q[tc] = nsx.colprod(SA, tc, Bz, NS_A * X[tc]);
+        for (int tc = 0; tc < NT; ++tc) Q[tc] = NS_A * X[tc];
+        nsx.colprod_all(SA, Bz, Q);
       }
       __builtin_amdgcn_sched_barrier(0);  // keep the phases' operands apart
       {
@@ -392,10 +393,12 @@ scan_bwd_muon_x3(const float* __restrict__ K, const float* __restrict__ av,
         NSX::pack_all(Bs, Bso);
         f32x4 Wt[NT];
 #pragma unroll
-        for (int tc = 0; tc < NT; ++tc) Wt[tc] = nsx.colprod(SB, tc, Bso, zero4());  // (X_k^T Bs)[c][r]
+        for (int tc = 0; tc < NT; ++tc) Wt[tc] = zero4();
+        nsx.colprod_all(SB, Bso, Wt);  // (X_k^T Bs)[c][r]
         NSX::pack_all(Wt, Wo);
 #pragma unroll
-        for (int tr = 0; tr < NT; ++tr) Y[tr] = nsx.rowprod(SB, tr, Wo);  // (X_k W)[r'][r]
+        for (int tr = 0; tr < NT; ++tr) Y[tr] = zero4();
+        nsx.rowprod_all(SB, Wo, Y);    // (X_k W)[r'][r]
       }
       __syncthreads();  // every read of Xbar in A done
       nsx.publish(SA, Y);  // A holds Y^T
@@ -405,8 +408,9 @@ scan_bwd_muon_x3(const float* __restrict__ K, const float* __restrict__ av,
 #pragma unroll
         for (int tr = 0; tr < NT; ++tr) Bs[tr] = NS_B * Bs[tr] + NS_C * (Y[tr] + NSX::tview(SA, tb, tr));
         NSX::pack_all(Bs, So);
+        nsx.colprod_all(SB, So, Q);
 #pragma unroll
-        for (int tc = 0; tc < NT; ++tc) X[tc] = nsx.colprod(SB, tc, So, Q[tc]);
+        for (int tc = 0; tc < NT; ++tc) X[tc] = Q[tc];
       }
       __syncthreads();  // every read of A and B done
       if (k > 0) {
