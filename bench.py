@@ -22,6 +22,9 @@ grid (fp32 d x d inputs per chunk), forward and forward + backward, with its
 own roofline.  ``cpu_baseline`` times the CPU restatement of the reference matrix form
 (float32, torch on the host cores) on the same workload.
 
+``--workload lm_b8_t2048_muon`` times the 12-layer LM stack around the
+fused core end to end (forward + backward, tokens/s only).
+
 ``--fwd-only`` times the inference forward alone; ``--copy-calibration
 BYTES`` only runs a device copy of BYTES bytes a few times (the calibration
 kernel for the HBM byte counters).
@@ -173,6 +176,67 @@ def bwd_flops_per_chunk_head(w) -> int:
     return f
 
 
+LM_WORKLOAD = "lm_b8_t2048_muon"
+
+
+def lm_line(args) -> dict:
+    """The 12-layer GMDN stack (d_model 1024, 8 heads x 128, muon inner rule,
+    ns = 3 -- the trainer's default, train_ablation.py:556-558), vocab 32000,
+    B = 8, T = 2048, bf16 weights from the reference's N(0, 0.02) init,
+    token ids uniform over the vocabulary, next-token cross entropy; one step
+    is forward + backward (no optimiser).  End-to-end tokens/s only: the
+    step is mostly library GEMMs and the muon core, so no single roofline
+    applies."""
+    import torch
+    from gmdn_amd.mixer import LM
+
+    B, T, vocab, d_model, layers, heads, ns = 8, 2048, 32000, 1024, 12, 8, 3
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    model = LM(vocab, d_model, layers, heads, "muon", ns_steps=ns).to(dev, torch.bfloat16)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    idx = torch.randint(0, vocab, (B, T + 1), device=dev, generator=gen)
+    stream = torch.cuda.current_stream(dev)
+
+    def step():
+        _, loss = model(idx[:, :-1], idx[:, 1:])
+        loss.backward()
+        for p in model.parameters():
+            p.grad = None
+        return loss
+
+    def timed(fn, steps, warmup):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        t0 = time.perf_counter()
+        for e in evs:
+            e[0].record(stream)
+            fn()
+            e[1].record(stream)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / steps, statistics.mean(e[0].elapsed_time(e[1]) for e in evs) / 1e3
+
+    steps, warmup = min(args.steps, 10), max(args.warmup, 1)
+    wall, ev = timed(step, steps, warmup)
+    with torch.no_grad():
+        _, fwd_ev = timed(lambda: model(idx[:, :-1]), steps, warmup)
+    tokens = B * T
+    return {
+        "metric": METRIC, "value": tokens / wall, "unit": "tokens/s", "n_gpus": 1, "steps": steps,
+        "warmup": warmup, "ms_per_step": wall * 1e3, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": LM_WORKLOAD, "layers": layers, "d_model": d_model, "heads": heads,
+                   "head_dim": d_model // heads, "rule": "muon", "ns": ns, "B": B, "T": T, "vocab": vocab,
+                   "pass": "fwd+bwd", "global_batch": B, "seq_len": T, "parallelism": "none"},
+        "fwd_tokens_per_s": tokens / fwd_ev, "fwd_bwd_tokens_per_s": tokens / ev,
+        "step_us": {"fwd_bwd": ev * 1e6, "fwd_inference": fwd_ev * 1e6},
+        "roofline": None, "roofline_note": "end-to-end stack: tokens/s only",
+        "cpu_baseline": None,
+    }
+
+
 def copy_calibration(nbytes: int) -> None:
     import torch
     # an elementwise kernel (MulFunctor) that reads nbytes and writes nbytes
@@ -238,6 +302,9 @@ def main(argv=None):
         copy_calibration(args.copy_calibration)
         return 0
 
+    if args.workload == LM_WORKLOAD:
+        print(json.dumps(lm_line(args)), flush=True)
+        return 0
     w = WORKLOADS[args.workload]
     dev = torch.device("cuda:0")
     inp = make_inputs(w, seed=0, device=dev, with_grad_out=True)
