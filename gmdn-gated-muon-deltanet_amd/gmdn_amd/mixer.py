@@ -24,6 +24,22 @@ import torch.nn.functional as F
 from .chunk import CHUNK, LOG_FLOOR, chunk_scan
 
 
+def causal_depthwise_conv(y: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
+    """``conv(y.transpose(1, 2))[..., :T].transpose(1, 2)`` of the reference
+    (train_ablation.py:93-94, :124) for a depthwise Conv1d with left padding
+    kernel - 1: out[t, c] = bias[c] + sum_j weight[c, 0, j] y[t - (kernel - 1) + j, c],
+    as kernel shifted multiply-adds over (B, T, channels) in place of the
+    library's im2col convolution."""
+    K = weight.shape[-1]
+    T = y.shape[1]
+    w = weight.view(-1, K).to(y.dtype)
+    yp = F.pad(y, (0, 0, K - 1, 0))  # K - 1 zero steps before t = 0
+    out = bias.to(y.dtype) + yp[:, 0:T] * w[:, 0]
+    for j in range(1, K):
+        out = out + yp[:, j:j + T] * w[:, j]
+    return out
+
+
 class FastWeightMixer(nn.Module):
     """Token mixing via per-head fast weights (train_ablation.py:80-108)."""
 
@@ -61,8 +77,7 @@ class FastWeightMixer(nn.Module):
         the log gates clamped at log 1e-6 (train_ablation.py:124-134, 155, 170-175)."""
         B, T, D = x.shape
         H, dh = self.h, self.dh
-        qkv = self.conv(self.qkv(x).transpose(1, 2))[..., :T].transpose(1, 2)
-        qkv = F.silu(qkv)
+        qkv = F.silu(causal_depthwise_conv(self.qkv(x), self.conv.weight, self.conv.bias))
         q, k, v = qkv.chunk(3, dim=-1)
         q = F.normalize(q.reshape(B, T, H, dh), dim=-1).transpose(1, 2)
         k = F.normalize(k.reshape(B, T, H, dh), dim=-1).transpose(1, 2)
