@@ -1,4 +1,5 @@
-"""ctypes binding of ``libgmdn_scan.so`` (the C ABI declared in include/gmdn_scan.h).
+"""ctypes binding of ``libgmdn_scan.so`` (the C ABI declared in include/gmdn_scan.h
+and include/gmdn_front.h).
 
 The library is built in-tree by ``gmdn_amd.build`` and loaded after torch, so
 its HIP runtime dependency (soname ``libamdhip64.so.7``) binds to the runtime
@@ -52,6 +53,10 @@ SIGNATURES = {
     "gmdn_chunk_fwd": (c_i32, [ctypes.POINTER(ChunkDesc)] + [c_vp] * 10),
     "gmdn_chunk_bwd_workspace_bytes": (c_size, [ctypes.POINTER(ChunkDesc)]),
     "gmdn_chunk_bwd": (c_i32, [ctypes.POINTER(ChunkDesc)] + [c_vp] * 17 + [c_size, c_vp]),
+    # include/gmdn_front.h
+    "gmdn_front_fwd": (c_i32, [c_vp] * 6 + [c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_vp]),
+    "gmdn_front_bwd_workspace_floats": (c_size, [c_i64, c_i64, c_i32, c_i32]),
+    "gmdn_front_bwd": (c_i32, [c_vp] * 8 + [c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_vp]),
 }
 
 

@@ -4,10 +4,12 @@
 with the same constructor arguments, parameter names and shapes (so a
 reference ``state_dict`` loads unchanged), the same front-end (qkv
 projection, causal depthwise conv, SiLU, per-head L2 norm, gate sigmoids),
-tail (per-head RMSNorm, output projection) and initialisation.  Phases 1-3
-of the mixer (train_ablation.py:142-187: gate reductions, the intra-chunk
-products, the state scan and the output) are one call of
-``chunk_scan`` -- the fused HIP core.
+tail (per-head RMSNorm, output projection) and initialisation.  The conv,
+SiLU and norms run as one HIP kernel per direction
+(``torch.ops.gmdn.front_fwd``); phases 1-3 of the mixer
+(train_ablation.py:142-187: gate reductions, the intra-chunk products, the
+state scan and the output) are one call of ``chunk_scan`` -- the fused HIP
+core.
 
 The stack is the end-to-end harness for the 12-layer, d_model 1024, 8-head,
 muon configuration: it measures the whole training step around the core.
@@ -21,23 +23,8 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from . import ops  # noqa: F401  -- registers torch.ops.gmdn.*
 from .chunk import CHUNK, LOG_FLOOR, chunk_scan
-
-
-def causal_depthwise_conv(y: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
-    """``conv(y.transpose(1, 2))[..., :T].transpose(1, 2)`` of the reference
-    (train_ablation.py:93-94, :124) for a depthwise Conv1d with left padding
-    kernel - 1: out[t, c] = bias[c] + sum_j weight[c, 0, j] y[t - (kernel - 1) + j, c],
-    as kernel shifted multiply-adds over (B, T, channels) in place of the
-    library's im2col convolution."""
-    K = weight.shape[-1]
-    T = y.shape[1]
-    w = weight.view(-1, K).to(y.dtype)
-    yp = F.pad(y, (0, 0, K - 1, 0))  # K - 1 zero steps before t = 0
-    out = bias.to(y.dtype) + yp[:, 0:T] * w[:, 0]
-    for j in range(1, K):
-        out = out + yp[:, j:j + T] * w[:, j]
-    return out
 
 
 class FastWeightMixer(nn.Module):
@@ -77,11 +64,9 @@ class FastWeightMixer(nn.Module):
         the log gates clamped at log 1e-6 (train_ablation.py:124-134, 155, 170-175)."""
         B, T, D = x.shape
         H, dh = self.h, self.dh
-        qkv = F.silu(causal_depthwise_conv(self.qkv(x), self.conv.weight, self.conv.bias))
-        q, k, v = qkv.chunk(3, dim=-1)
-        q = F.normalize(q.reshape(B, T, H, dh), dim=-1).transpose(1, 2)
-        k = F.normalize(k.reshape(B, T, H, dh), dim=-1).transpose(1, 2)
-        v = v.reshape(B, T, H, dh).transpose(1, 2)
+        # conv, SiLU and the q / k norms in one HIP kernel per direction
+        q, k, v = torch.ops.gmdn.front_fwd(self.qkv(x), self.conv.weight, self.conv.bias, dh)
+        q, k, v = (t.view(B, T, H, dh).transpose(1, 2) for t in (q, k, v))
         gl = self.gates(x).float().view(B, T, self.n_gates, H).permute(2, 0, 3, 1)  # (nG, B, H, T)
         # log sigmoid = log of the gate, with the reference's 1e-6 floor
         lg = torch.clamp(F.logsigmoid(gl), min=LOG_FLOOR)

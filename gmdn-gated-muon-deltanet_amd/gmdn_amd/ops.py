@@ -246,3 +246,79 @@ def _chunk_fwd_backward(ctx, dO, dstates):
 
 
 chunk_fwd.register_autograd(_chunk_fwd_backward, setup_context=_chunk_fwd_setup)
+
+
+# ------------------------------------------------------- mixer front-end
+def _dtype_code(t: Tensor) -> int:
+    if t.dtype == torch.bfloat16:
+        return nat.DTYPE_BF16
+    if t.dtype == torch.float32:
+        return nat.DTYPE_F32
+    raise RuntimeError(f"the mixer front-end kernels take bfloat16 or float32, got {t.dtype}")
+
+
+@torch.library.custom_op("gmdn::front_fwd", mutates_args=(), device_types="cuda")
+def front_fwd(y: Tensor, weight: Tensor, bias: Tensor, dh: int) -> tuple[Tensor, Tensor, Tensor]:
+    """q, k, v (B, T, D) from the qkv projection output y (B, T, 3 D):
+    causal depthwise conv (weight (3 D, 1, K), bias), SiLU, per-head L2 norm
+    of q and k (reference train_ablation.py:124-128)."""
+    lib = nat.load()
+    B, T, C3 = y.shape
+    D, K = C3 // 3, weight.shape[-1]
+    yc = y.contiguous()
+    w = weight.reshape(C3, K).to(torch.float32).contiguous()
+    bc = bias.to(torch.float32).contiguous()
+    q, k, v = (torch.empty(B, T, D, dtype=y.dtype, device=y.device) for _ in range(3))
+    with torch.cuda.device(y.device):
+        rc = lib.gmdn_front_fwd(nat.ptr(yc), nat.ptr(w), nat.ptr(bc), nat.ptr(q), nat.ptr(k), nat.ptr(v), B, T, D,
+                                dh, K, _dtype_code(y), nat.stream_of(y))
+    nat.check(rc, "gmdn_front_fwd")
+    return q, k, v
+
+
+@front_fwd.register_fake
+def _front_fwd_fake(y, weight, bias, dh):
+    B, T, C3 = y.shape
+    return tuple(y.new_empty(B, T, C3 // 3) for _ in range(3))
+
+
+@torch.library.custom_op("gmdn::front_bwd", mutates_args=(), device_types="cuda")
+def front_bwd(y: Tensor, weight: Tensor, bias: Tensor, dq: Tensor, dk: Tensor, dv: Tensor,
+              dh: int) -> tuple[Tensor, Tensor, Tensor]:
+    """dy, dweight, dbias of ``front_fwd`` given the cotangents of q, k, v."""
+    lib = nat.load()
+    B, T, C3 = y.shape
+    D, K = C3 // 3, weight.shape[-1]
+    yc = y.contiguous()
+    w = weight.reshape(C3, K).to(torch.float32).contiguous()
+    bc = bias.to(torch.float32).contiguous()
+    g = [t.to(y.dtype).contiguous() for t in (dq, dk, dv)]
+    dy = torch.empty_like(yc)
+    partial = torch.empty(lib.gmdn_front_bwd_workspace_floats(B, T, D, K), dtype=torch.float32, device=y.device)
+    with torch.cuda.device(y.device):
+        rc = lib.gmdn_front_bwd(nat.ptr(yc), nat.ptr(w), nat.ptr(bc), *(nat.ptr(t) for t in g), nat.ptr(dy),
+                                nat.ptr(partial), B, T, D, dh, K, _dtype_code(y), nat.stream_of(y))
+    nat.check(rc, "gmdn_front_bwd")
+    sums = partial.view(-1, C3, K + 1).sum(0)
+    return dy, sums[:, :K].reshape(weight.shape).to(weight.dtype), sums[:, K].to(bias.dtype).contiguous()
+
+
+@front_bwd.register_fake
+def _front_bwd_fake(y, weight, bias, dq, dk, dv, dh):
+    return y.new_empty(y.shape), torch.empty_like(weight), torch.empty_like(bias)
+
+
+def _front_setup(ctx, inputs, output):
+    y, weight, bias, dh = inputs
+    ctx.save_for_backward(y, weight, bias)
+    ctx.dh = dh
+
+
+def _front_backward(ctx, dq, dk, dv):
+    y, weight, bias = ctx.saved_tensors
+    dq, dk, dv = (torch.zeros_like(t) if g is None else g for g, t in zip((dq, dk, dv), (y, y, y)))
+    dy, dw, db = torch.ops.gmdn.front_bwd(y, weight, bias, dq, dk, dv, ctx.dh)
+    return dy, dw, db, None
+
+
+front_fwd.register_autograd(_front_backward, setup_context=_front_setup)

@@ -2,6 +2,7 @@
 arguments with the documented codes before launching anything (no GPU
 needed: validation runs on the host)."""
 import ctypes
+import glob
 import os
 import re
 
@@ -10,18 +11,21 @@ import pytest
 from gmdn_amd import _native
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "gmdn_scan.h")
+HEADERS = sorted(glob.glob(os.path.join(ROOT, "include", "*.h")))
 
 
 def declared_functions():
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(gmdn_[a-z0-9_]+)\s*\(", text)))
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names |= set(re.findall(r"\b(gmdn_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 def test_header_declares_expected_entry_points():
     names = declared_functions()
-    for n in ("gmdn_scan_fwd", "gmdn_scan_bwd", "gmdn_chunk_fwd", "gmdn_chunk_bwd", "gmdn_error_string"):
+    for n in ("gmdn_scan_fwd", "gmdn_scan_bwd", "gmdn_chunk_fwd", "gmdn_chunk_bwd", "gmdn_error_string",
+              "gmdn_front_fwd", "gmdn_front_bwd"):
         assert n in names
 
 
@@ -84,3 +88,18 @@ def test_scan_bwd_workspace_contract():
 def test_chunk_desc_layout_matches_header():
     # 3 int64 + 6 int32 + float + pad + 12 int64
     assert ctypes.sizeof(_native.ChunkDesc) == 3 * 8 + 6 * 4 + 4 + 4 + 12 * 8
+
+
+def test_front_argument_checks():
+    lib = _native.load()
+    p = 0x1000
+    # y, weight, bias, q, k, v, B, T, D, dh, K, dtype, stream
+    assert lib.gmdn_front_fwd(p, p, p, p, p, p, 2, 64, 256, 96, 4, 0, None) == 2   # dh not built
+    assert lib.gmdn_front_fwd(p, p, p, p, p, p, 2, 64, 200, 128, 4, 0, None) == 1  # D not a multiple of dh
+    assert lib.gmdn_front_fwd(p, p, p, p, p, p, 2, 64, 256, 128, 5, 0, None) == 1  # kernel above 4
+    assert lib.gmdn_front_fwd(p, p, p, p, p, p, 2, 64, 256, 128, 4, 7, None) == 2  # dtype
+    assert lib.gmdn_front_fwd(None, p, p, p, p, p, 2, 64, 256, 128, 4, 0, None) == 1
+    assert lib.gmdn_front_fwd(p + 2, p, p, p, p, p, 2, 64, 256, 128, 4, 0, None) == 1  # misaligned y
+    assert lib.gmdn_front_fwd(None, None, None, None, None, None, 0, 64, 256, 128, 4, 0, None) == 0  # empty
+    assert lib.gmdn_front_bwd(p, p, p, p, p, p, p, None, 2, 64, 256, 128, 4, 0, None) == 1  # no workspace
+    assert lib.gmdn_front_bwd_workspace_floats(2, 65, 256, 4) == 2 * 2 * 768 * 5

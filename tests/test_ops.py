@@ -15,7 +15,7 @@ sys.path.insert(0, os.path.join(ROOT, "gmdn-gated-muon-deltanet_amd"))
 import fast_scan  # noqa: E402
 from gmdn_amd import _native, chunk, ops  # noqa: E402,F401
 
-OPS = ("state_scan", "state_scan_bwd", "chunk_fwd", "chunk_bwd")
+OPS = ("state_scan", "state_scan_bwd", "chunk_fwd", "chunk_bwd", "front_fwd", "front_bwd")
 
 
 def _capture(fn, *args):
@@ -94,3 +94,13 @@ def test_cpu_tensors_never_reach_the_ops():
     gg = torch.zeros(1, 1, 64)
     with pytest.raises(RuntimeError, match="GPU tensors"):
         chunk.chunk_scan(q, q, q, gg, gg, rule="delta")
+
+
+def test_front_fake_shapes():
+    with FakeTensorMode():
+        y = torch.empty(2, 100, 768, device="cuda", dtype=torch.bfloat16)
+        w, b = torch.empty(768, 1, 4, device="cuda"), torch.empty(768, device="cuda")
+        q, k, v = torch.ops.gmdn.front_fwd(y, w, b, 128)
+        assert all(tuple(t.shape) == (2, 100, 256) and t.dtype == torch.bfloat16 for t in (q, k, v))
+        dy, dw, db = torch.ops.gmdn.front_bwd(y, w, b, q, k, v, 128)
+        assert dy.shape == y.shape and dw.shape == w.shape and db.shape == b.shape
