@@ -23,6 +23,8 @@ constexpr int FT_WC = 64 * FT_LC;         // channels per wave
 constexpr int FT_WAVES = 4;               // waves per workgroup
 constexpr int FT_KMAX = 4;                // conv taps held in the window
 constexpr float FT_EPS = 1e-12f;          // F.normalize's eps
+constexpr int FT_GF = 8;                  // forward: rows loaded ahead per group
+constexpr int FT_GB = 4;                  // backward: tokens (2 rows each) per group
 
 template <typename T>
 struct Row8;
@@ -56,11 +58,52 @@ struct Row8<float> {
   }
 };
 
-// sum over the dh / 8 lanes of one head (all lanes of the wave take part)
+// A lane's 8 channels of one row as loaded (converted when used), so that
+// a group of rows can be in flight at once
+template <typename T>
+struct Raw8;
+template <>
+struct Raw8<bf16> {
+  bf16x8 v;
+  GMDN_DEV void load(const bf16* p) { v = *reinterpret_cast<const bf16x8*>(p); }
+  GMDN_DEV void zero() { v = bf16x8{}; }
+  GMDN_DEV void get(float (&x)[8]) const {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = (float)v[j];
+  }
+};
+template <>
+struct Raw8<float> {
+  f32x4 a, b;
+  GMDN_DEV void load(const float* p) {
+    a = *reinterpret_cast<const f32x4*>(p);
+    b = *reinterpret_cast<const f32x4*>(p + 4);
+  }
+  GMDN_DEV void zero() { a = b = f32x4{0.f, 0.f, 0.f, 0.f}; }
+  GMDN_DEV void get(float (&x)[8]) const {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      x[j] = a[j];
+      x[4 + j] = b[j];
+    }
+  }
+};
+
+// sum over the dh / 8 lanes of one head, in DPP moves (all lanes of the
+// wave take part): the two quad-permute steps sum each quad; a 128-wide head
+// is a 16-lane row (row_ror 4 and 8 add the other quads), a 64-wide head a
+// half-row (row_half_mirror adds the other quad of the 8)
 template <int DH>
 GMDN_DEV float head_sum(float s) {
-#pragma unroll
-  for (int o = 1; o < DH / FT_LC; o <<= 1) s += __shfl_xor(s, o);
+  static_assert(DH == 64 || DH == 128, "head dims 64 and 128");
+  s += dpp_mov<0xB1>(s);  // quad_perm [1,0,3,2]
+  s += dpp_mov<0x4E>(s);  // quad_perm [2,3,0,1]
+  if constexpr (DH == 64) {
+    s += dpp_mov<0x141>(s);  // row_half_mirror
+  } else {
+    s += dpp_mov<0x124>(s);  // row_ror:4
+    s += dpp_mov<0x128>(s);  // row_ror:8
+  }
   return s;
 }
 
@@ -76,14 +119,32 @@ struct Lane {
     on = c0 < C3;
     part = on ? c0 / D : 0;
     cc = c0 - part * D;
+    if (on && K == FT_KMAX) {  // the common kernel size: one 16-byte load per channel
 #pragma unroll
-    for (int j = 0; j < FT_LC; ++j) {
-      br[j] = on ? bias[c0 + j] : 0.f;
+      for (int j = 0; j < FT_LC; ++j) {
+        const f32x4 r = *reinterpret_cast<const f32x4*>(w + (int64_t)(c0 + j) * FT_KMAX);
 #pragma unroll
-      for (int s = 0; s < FT_KMAX; ++s) {
-        const int i = s - (FT_KMAX - K);
-        wr[j][s] = (on && i >= 0) ? w[(int64_t)(c0 + j) * K + i] : 0.f;
+        for (int s = 0; s < FT_KMAX; ++s) wr[j][s] = r[s];
       }
+    } else {
+#pragma unroll
+      for (int j = 0; j < FT_LC; ++j)
+#pragma unroll
+        for (int s = 0; s < FT_KMAX; ++s) {
+          const int i = s - (FT_KMAX - K);
+          wr[j][s] = (on && i >= 0) ? w[(int64_t)(c0 + j) * K + i] : 0.f;
+        }
+    }
+    if (on) {
+      const f32x4 b0 = *reinterpret_cast<const f32x4*>(bias + c0), b1 = *reinterpret_cast<const f32x4*>(bias + c0 + 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        br[j] = b0[j];
+        br[4 + j] = b1[j];
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < FT_LC; ++j) br[j] = 0.f;
     }
   }
 };
@@ -113,32 +174,40 @@ front_fwd(const T* __restrict__ y, const float* __restrict__ w, const float* __r
     }
   }
   const int t1 = min(t0 + FT_TOK, T_);
-  for (int t = t0; t < t1; ++t) {
-    float cur[FT_LC], a[FT_LC];
-    if (ln.on) {
-      Row8<T>::load(yb + (int64_t)t * C3, cur);
-    } else {
+  for (int tg = t0; tg < t1; tg += FT_GF) {
+    // the group's rows in flight together, then the tokens in order
+    Raw8<T> rows[FT_GF];
 #pragma unroll
-      for (int j = 0; j < FT_LC; ++j) cur[j] = 0.f;
+    for (int g = 0; g < FT_GF; ++g) {
+      if (ln.on && tg + g < t1)
+        rows[g].load(yb + (int64_t)(tg + g) * C3);
+      else
+        rows[g].zero();
     }
+#pragma unroll
+    for (int g = 0; g < FT_GF; ++g) {
+    const int t = tg + g;
+    float cur[FT_LC], a[FT_LC];
+    rows[g].get(cur);
     float ss = 0.f;
 #pragma unroll
     for (int j = 0; j < FT_LC; ++j) {
       const float z = ln.br[j] + ln.wr[j][0] * win[0][j] + ln.wr[j][1] * win[1][j] + ln.wr[j][2] * win[2][j] +
                       ln.wr[j][3] * cur[j];
-      a[j] = z / (1.f + __expf(-z));
+      a[j] = z * __builtin_amdgcn_rcpf(1.f + __expf(-z));  // silu, v_rcp_f32 (1 ulp)
       ss += a[j] * a[j];
     }
     ss = head_sum<DH>(ss);
-    const float sc = norm ? 1.f / fmaxf(sqrtf(ss), FT_EPS) : 1.f;
+    const float sc = norm ? __builtin_amdgcn_rcpf(fmaxf(sqrtf(ss), FT_EPS)) : 1.f;
 #pragma unroll
     for (int j = 0; j < FT_LC; ++j) a[j] *= sc;
-    if (ln.on) Row8<T>::store(dst + (int64_t)t * D, a);
+    if (ln.on && t < t1) Row8<T>::store(dst + (int64_t)t * D, a);
 #pragma unroll
     for (int j = 0; j < FT_LC; ++j) {
       win[0][j] = win[1][j];
       win[1][j] = win[2][j];
       win[2][j] = cur[j];
+    }
     }
   }
 }
@@ -178,22 +247,33 @@ front_bwd(const T* __restrict__ y, const float* __restrict__ w, const float* __r
 
   // tokens t0 .. t0 + 66: the tile's own dz, then the 3 after it that its
   // last dy rows need (zero beyond T)
-  for (int t = t0; t < t0 + FT_TOK + FT_KMAX - 1; ++t) {
-    const bool tv = t < T_;
-    float cur[FT_LC], du[FT_LC];
-    if (ln.on && tv) {
-      Row8<T>::load(yb + (int64_t)t * C3, cur);
-      Row8<T>::load(gb + (int64_t)t * D, du);
-    } else {
+  constexpr int NT_B = FT_TOK + FT_KMAX - 1;
+  for (int tg = t0; tg < t0 + NT_B; tg += FT_GB) {
+    Raw8<T> ry[FT_GB], rg[FT_GB];
 #pragma unroll
-      for (int j = 0; j < FT_LC; ++j) cur[j] = du[j] = 0.f;
+    for (int g = 0; g < FT_GB; ++g) {
+      const int t = tg + g;
+      if (ln.on && t < T_ && t < t0 + NT_B) {
+        ry[g].load(yb + (int64_t)t * C3);
+        rg[g].load(gb + (int64_t)t * D);
+      } else {
+        ry[g].zero();
+        rg[g].zero();
+      }
     }
+#pragma unroll
+    for (int g = 0; g < FT_GB; ++g) {
+    const int t = tg + g;
+    const bool tv = t < T_ && t < t0 + NT_B;
+    float cur[FT_LC], du[FT_LC];
+    ry[g].get(cur);
+    rg[g].get(du);
     float z[FT_LC], sg[FT_LC], a[FT_LC], ss = 0.f, sd = 0.f;
 #pragma unroll
     for (int j = 0; j < FT_LC; ++j) {
       z[j] = ln.br[j] + ln.wr[j][0] * win[0][j] + ln.wr[j][1] * win[1][j] + ln.wr[j][2] * win[2][j] +
              ln.wr[j][3] * cur[j];
-      sg[j] = 1.f / (1.f + __expf(-z[j]));
+      sg[j] = __builtin_amdgcn_rcpf(1.f + __expf(-z[j]));
       a[j] = z[j] * sg[j];
       ss += a[j] * a[j];
       sd += a[j] * du[j];
@@ -206,7 +286,7 @@ front_bwd(const T* __restrict__ y, const float* __restrict__ w, const float* __r
       // da = (du - u (u . du)) / n for n > eps, da = du / eps otherwise
       const float n = sqrtf(ss);
       const bool big = n > FT_EPS;
-      const float inv = big ? 1.f / n : 1.f / FT_EPS;
+      const float inv = big ? __builtin_amdgcn_rcpf(n) : 1.f / FT_EPS;
       const float ud = big ? sd * inv : 0.f;
 #pragma unroll
       for (int j = 0; j < FT_LC; ++j) {
@@ -227,7 +307,7 @@ front_bwd(const T* __restrict__ y, const float* __restrict__ w, const float* __r
     }
     // dy[s] = sum over the taps of w (slot) dz[s + 3 - slot], complete at t = s + 3
     const int s = t - (FT_KMAX - 1);
-    if (ln.on && s >= t0 && s < T_) {
+    if (ln.on && s >= t0 && s < t0 + FT_TOK && s < T_) {  // only the tile's own rows
       float g[FT_LC];
 #pragma unroll
       for (int j = 0; j < FT_LC; ++j)
@@ -242,6 +322,7 @@ front_bwd(const T* __restrict__ y, const float* __restrict__ w, const float* __r
       dzw[0][j] = dzw[1][j];
       dzw[1][j] = dzw[2][j];
       dzw[2][j] = dz[j];
+    }
     }
   }
   if (ln.on) {
@@ -267,7 +348,7 @@ int check_front(const void* y, const float* w, const float* bias, int64_t B, int
   if (dtype != GMDN_DTYPE_BF16 && dtype != GMDN_DTYPE_F32) return GMDN_ERR_UNSUPPORTED;
   if (B * T == 0) return GMDN_OK;
   if (B * T > ((int64_t)1 << 31) / 3 || (int64_t)D * 3 > (1 << 24)) return GMDN_ERR_ARG;
-  if (!y || !w || !bias || !aligned16(y)) return GMDN_ERR_ARG;
+  if (!y || !w || !bias || !aligned16(y) || !aligned16(w) || !aligned16(bias)) return GMDN_ERR_ARG;
   return GMDN_OK;
 }
 

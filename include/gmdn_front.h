@@ -10,7 +10,8 @@
  * Layouts: y is the projection output (B, T, 3 D) with D = H dh, contiguous;
  * q, k, v are (B, T, D) contiguous (the (B, H, T, dh) operands of the scan
  * are their transposed views); weight is (3 D, K) float32 (the Conv1d weight
- * (3 D, 1, K) squeezed), bias (3 D) float32.  dtype is GMDN_DTYPE_BF16 or
+ * (3 D, 1, K) squeezed), bias (3 D) float32.  Every pointer is 16-byte
+ * aligned.  dtype is GMDN_DTYPE_BF16 or
  * GMDN_DTYPE_F32 for y, q, k, v and their gradients.
  */
 #ifndef GMDN_FRONT_H
