@@ -363,7 +363,7 @@ __global__ void __launch_bounds__(FW_THREADS) chunk_fwd(ChunkArgs p) {
         Mm[t] = msc * Mm[t] + (1.f - msc) * acc[t];
         Vv[t] = nsc * Vv[t] + (1.f - nsc) * acc[t] * acc[t];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) S[t][j] = a * S[t][j] + bsc * Mm[t][j] / (sqrtf(Vv[t][j]) + p.eps);
+        for (int j = 0; j < 4; ++j) S[t][j] = a * S[t][j] + bsc * Mm[t][j] * hw_rcp(hw_sqrt(Vv[t][j]) + p.eps);
       }
     }
     publish_S();  // S_{i+1}^T half, read after X_{i+1}

@@ -281,13 +281,13 @@ __global__ void __launch_bounds__(CB_THREADS) chunk_bwd_state(ChunkArgs p) {
             const float g = -acc[jj];
             const float mn = msc * Mp[t][jj] + (1.f - msc) * g;
             const float vn = nsc * Vp[t][jj] + (1.f - nsc) * g * g;
-            const float sq = sqrtf(vn);
-            const float rden = 1.f / (sq + p.eps);
+            const float sq = hw_sqrt(vn);
+            const float rden = hw_rcp(sq + p.eps);
             const float sb = Sb[t][jj];
             da += sb * Si[jj];
             db += sb * mn * rden;
             const float mt = Mb[t][jj] + bsc * sb * rden;
-            const float vt = Vb[t][jj] - bsc * sb * mn * rden * rden / (2.f * fmaxf(sq, 1e-12f));
+            const float vt = Vb[t][jj] - bsc * sb * mn * rden * rden * hw_rcp(2.f * fmaxf(sq, 1e-12f));
             dm += mt * (Mp[t][jj] - g);
             dn += vt * (Vp[t][jj] - g * g);
             Gb[t][jj] = (1.f - msc) * mt + (1.f - nsc) * 2.f * g * vt;

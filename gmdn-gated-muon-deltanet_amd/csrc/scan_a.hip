@@ -293,7 +293,7 @@ scan_fwd_rows8(const float* __restrict__ U, const float* __restrict__ K,
         M[u] = m * M[u] + (1.f - m) * g;
         V[u] = n * V[u] + (1.f - n) * g * g;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) S[u][j] = a * S[u][j] + b * M[u][j] / (sqrtf(V[u][j]) + 1e-6f);
+        for (int j = 0; j < 4; ++j) S[u][j] = a * S[u][j] + b * M[u][j] * hw_rcp(hw_sqrt(V[u][j]) + 1e-6f);
       }
     }
     // K_{i+1} into the other buffer (last read in chunk i-1); loads of K_{i+2}, U_{i+1}
@@ -579,14 +579,14 @@ scan_bwd_rows8(const float* __restrict__ U, const float* __restrict__ K,
           const float gg = g[j];
           const float Mi = m * mn[u][j] + (1.f - m) * gg;
           const float Vi = n * vn[u][j] + (1.f - n) * gg * gg;
-          const float root = sqrtf(Vi);
-          const float den = root + 1e-6f;
+          const float root = hw_sqrt(Vi);
+          const float rden = hw_rcp(root + 1e-6f);
           const float sb = Sb[u][j];
           pda += sb * Si[j];
-          pdb += sb * (Mi / den);
+          pdb += sb * (Mi * rden);
           const float ub = b * sb;
-          const float Mtot = Mb[u][j] + ub / den;
-          const float Vtot = Vb[u][j] - ub * Mi / (den * den) / (2.f * fmaxf(root, 1e-12f));
+          const float Mtot = Mb[u][j] + ub * rden;
+          const float Vtot = Vb[u][j] - ub * Mi * rden * rden * hw_rcp(2.f * fmaxf(root, 1e-12f));
           pdm += Mtot * (mn[u][j] - gg);
           pdn += Vtot * (vn[u][j] - gg * gg);
           Mb[u][j] = m * Mtot;

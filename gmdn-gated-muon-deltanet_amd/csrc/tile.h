@@ -275,6 +275,12 @@ GMDN_DEV void wait_vmem_le() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// Hardware square root and reciprocal (v_sqrt_f32, v_rcp_f32: 1 ulp) in
+// place of the correctly rounded library sequences (about ten instructions
+// each), for the bf16x3 paths' elementwise state updates.
+GMDN_DEV float hw_sqrt(float x) { return __builtin_amdgcn_sqrtf(x); }
+GMDN_DEV float hw_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+
 // ------------------------------------------------------------ reductions
 // DPP move of a float within the wave (CTRL: quad_perm 0x00-0xff, row_ror:n
 // 0x120 + n); every lane must be active.
