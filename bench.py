@@ -100,6 +100,41 @@ def drop_in_flops_per_chunk(rule: str, d: int, ns: int):
     return fwd * d ** 3, bwd * d ** 3
 
 
+def drop_in_cpu_baseline(w, budget_s: float) -> dict:
+    """The restated reference scan (scan_eager: fast_scan.py:72-95, float32
+    torch on the host cores, autograd for the backward) on a bounded sample
+    of the drop-in workload's heads; per-head time scaled to all B * H heads."""
+    import torch
+    from oracle import scan as osc
+
+    threads = max(1, min(len(os.sched_getaffinity(0)), 16))
+    torch.set_num_threads(threads)
+    rid = {"delta": 0, "muon": 1, "adam": 2}[w.rule]
+    N, d = w.T // w.chunk, w.d
+    gen = torch.Generator().manual_seed(0)
+
+    def sample(nh):
+        X = torch.randn(nh, 1, N, d, d, generator=gen)
+        K = (X @ X.transpose(-1, -2)) / (2 * d)
+        U = torch.randn(nh, 1, N, d, d, generator=gen)
+        gates = [0.9 + 0.1 * torch.rand(nh, 1, N, generator=gen) for _ in range(4)]
+        xs = [t.requires_grad_(True) for t in [U, K] + gates]
+        gS = torch.randn(nh, 1, N, d, d, generator=gen)
+        t0 = time.perf_counter()
+        S = osc.scan_forward(*xs, rid, w.ns)
+        torch.autograd.grad(S, xs, gS, allow_unused=True)  # (the rule's unused gates)
+        return time.perf_counter() - t0
+
+    t1 = sample(1)  # warm-up and size the sample
+    nh = max(1, min(w.B * w.H, int(budget_s / max(t1, 1e-3))))
+    t = sample(nh) / nh
+    total = t * w.B * w.H
+    return {"value": w.B * w.T / total, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{nh} of {w.B * w.H} heads of the drop-in workload (N={N}, d={d}, rule {w.rule}), "
+                      f"fwd+bwd, float32 scan_eager restatement with autograd; {t * 1e3:.0f} ms per head, "
+                      f"scaled to all heads"}
+
+
 def drop_in_leg(w, steps: int, warmup: int) -> dict:
     """The drop-in scan ``fast_state_scan(U, K, a, b, m, n, rule, ns)``
     (reference fast_scan.py:403-414) on the workload's chunk grid: B*H scans of
@@ -417,6 +452,8 @@ def main(argv=None):
     }
     if not (args.no_drop_in or args.fwd_only):
         line["drop_in"] = drop_in_leg(w, min(args.steps, 20), max(args.warmup, 1))
+        if not args.no_cpu_baseline:
+            line["drop_in"]["cpu_baseline"] = drop_in_cpu_baseline(w, args.cpu_budget / 2)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(w, args.cpu_budget, with_bwd)
     print(json.dumps(line), flush=True)

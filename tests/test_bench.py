@@ -69,3 +69,10 @@ def test_pmc_csv_parsing(tmp_path):
     assert profiling.counter_per_dispatch(str(tmp_path), "FETCH_SIZE", "k<1>") == [100.0, 102.0]
     with pytest.raises(ValueError):
         profiling.counter_per_dispatch(str(tmp_path), "WRITE_SIZE", "k<1>")
+
+
+def test_drop_in_cpu_baseline_runs_on_a_small_workload():
+    w = WORKLOADS["delta_fp32_small"]
+    cb = bench.drop_in_cpu_baseline(w, 0.2)
+    assert cb["value"] > 0 and cb["kind"] == "port" and cb["cores"] >= 1
+    assert "heads" in cb["sample"]
