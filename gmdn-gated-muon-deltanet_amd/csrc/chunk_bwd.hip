@@ -1073,6 +1073,9 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
 
   // ---------------- phase IIb: dQ and dK for this wave's 16 state columns
   //   dQ = (dA diag(beta)) K + dO S,   dK = (dA diag(beta))^T Q - dE S + diag(w) E Gb
+  // Every product has its operands swapped, so the tiles are the transposes
+  // (lane <-> token, registers <-> 4 consecutive state columns) and each
+  // leaves in one 8-byte store.
   bf16* dqg = p.dq + bb * p.sq[0] + hh * p.sq[1] + t0 * p.sq[2];
   bf16* dkg = p.dk + bb * p.sk[0] + hh * p.sk[1] + t0 * p.sk[2];
   f32x4 dqa[4], dka[4], des[4], eg[4];
@@ -1084,7 +1087,7 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
     for (int ks = 0; ks < 2; ++ks) {
       if (32 * ks > 16 * tt + 15) continue;
       const Op<2> dA{{col8<LA>(Ah, 32 * ks, 16 * tt), col8<LA>(Al, 32 * ks, 16 * tt)}};
-      dqa[tt] = mma<2, 1>(dA, Op<1>{{col8<LQ>(Ks, 32 * ks, j0)}}, dqa[tt]);
+      dqa[tt] = mma<1, 2>(Op<1>{{col8<LQ>(Ks, 32 * ks, j0)}}, dA, dqa[tt]);
     }
   }
 #pragma unroll
@@ -1094,7 +1097,7 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
     for (int kt = 0; kt < 2; ++kt) {
       if (32 * kt + 31 < 16 * st) continue;
       const Op<2> dAT{{row8<LA>(Ah, 16 * st + lc, 32 * kt), row8<LA>(Al, 16 * st + lc, 32 * kt)}};
-      dka[st] = mma<2, 1>(dAT, Op<1>{{col8<LQ>(Qs, 32 * kt, j0)}}, dka[st]);
+      dka[st] = mma<1, 2>(Op<1>{{col8<LQ>(Qs, 32 * kt, j0)}}, dAT, dka[st]);
     }
   }
   // The products over the state's rows need S_i and Gb_i by columns.  They
@@ -1124,13 +1127,13 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
     const Op<2> sc{{col8<LQ>(Sh, 0, j0), col8<LQ>(Sl, 0, j0)}};
     const Op<2> gc{{col8<LQ>(Gh, 0, j0), col8<LQ>(Gl, 0, j0)}};
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) dqa[tt] = mma<1, 2>(Op<1>{{row8<LQ>(Os, 16 * tt + lc, 32 * kb)}}, sc, dqa[tt]);
+    for (int tt = 0; tt < 4; ++tt) dqa[tt] = mma<2, 1>(sc, Op<1>{{row8<LQ>(Os, 16 * tt + lc, 32 * kb)}}, dqa[tt]);
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
       const Op<2> Er{{row8<LQ>(Eh, 16 * st + lc, 32 * kb), row8<LQ>(El, 16 * st + lc, 32 * kb)}};
       const Op<2> Dr{{row8<LQ>(Dh, 16 * st + lc, 32 * kb), row8<LQ>(Dl, 16 * st + lc, 32 * kb)}};
-      eg[st] = mma<2, 2>(Er, gc, eg[st]);
-      des[st] = mma<2, 2>(Dr, sc, des[st]);
+      eg[st] = mma<2, 2>(gc, Er, eg[st]);
+      des[st] = mma<2, 2>(sc, Dr, des[st]);
     }
     if (kb + 1 < NKB) __syncthreads();  // before the next block overwrites the staging planes
   }
@@ -1139,17 +1142,18 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
   bf16* dqs = reinterpret_cast<bf16*>(smem + L::V0);
   bf16* dks = Ah;
   static_assert(2 * L::AP >= L::TILE, "the dA planes hold one [64][D] bf16 tile");
+  // lane (t, G) of transposed tile tt holds dQ[16 tt + t][j0 + 4G .. +3]
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) dqs[LQ::off(16 * tt + 4 * G + jj, j0 + lc)] = (bf16)dqa[tt][jj];
+    *reinterpret_cast<bf16x4*>(dqs + LQ::off(16 * tt + lc, j0 + 4 * G)) =
+        bf16x4{(bf16)dqa[tt][0], (bf16)dqa[tt][1], (bf16)dqa[tt][2], (bf16)dqa[tt][3]};
 #pragma unroll
   for (int st = 0; st < 4; ++st) {
     f32x4 e = eg[st];
-    if constexpr (RULE == 0) e = e * *reinterpret_cast<const f32x4*>(rbeta + 16 * st + 4 * G);
+    if constexpr (RULE == 0) e = e * rbeta[16 * st + lc];  // diag(w) E Gb, w = beta of token 16 st + lc
     const f32x4 acc = dka[st] - des[st] + e;
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) dks[LQ::off(16 * st + 4 * G + jj, j0 + lc)] = (bf16)acc[jj];
+    *reinterpret_cast<bf16x4*>(dks + LQ::off(16 * st + lc, j0 + 4 * G)) =
+        bf16x4{(bf16)acc[0], (bf16)acc[1], (bf16)acc[2], (bf16)acc[3]};
   }
   __syncthreads();
   for (int e = threadIdx.x; e < CB_C * D / 8; e += NTHR) {
