@@ -402,7 +402,7 @@ __global__ void __launch_bounds__(FW_THREADS) chunk_fwd(ChunkArgs p) {
         O[u] = zero4();
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb)
-          O[u] = mma<1, 2>(Op<1>{{lds_ld<bf16x8>(qrow[kb] + SQK + (2 * H + u) * 16 * ROWB)}}, Sop[kb], O[u]);
+          O[u] = mma<2, 1>(Sop[kb], Op<1>{{lds_ld<bf16x8>(qrow[kb] + SQK + (2 * H + u) * 16 * ROWB)}}, O[u]);
       }
     };
     if (h == 0)
@@ -420,7 +420,7 @@ __global__ void __launch_bounds__(FW_THREADS) chunk_fwd(ChunkArgs p) {
       for (int u = 0; u < 2; ++u)
 #pragma unroll
         for (int kbs = 0; kbs <= H; ++kbs)
-          O[u] = mma<2, 2>(read_op(ap[kbs] + u * 16 * CB_C * 2, L::AP), EN[kbs], O[u]);
+          O[u] = mma<2, 2>(EN[kbs], read_op(ap[kbs] + u * 16 * CB_C * 2, L::AP), O[u]);
     };
     if (h == 0)
       ae(I0{});
@@ -428,13 +428,15 @@ __global__ void __launch_bounds__(FW_THREADS) chunk_fwd(ChunkArgs p) {
       ae(I1{});
     // o for tokens 32h .. 32h+31, columns r0 .. r0+15: staged through this
     // wave's 1 KiB of the chunk's V slot (read only before Y_i, refilled
-    // only after X_{i+1}) and stored as one 16-byte piece per lane
+    // only after X_{i+1}) and stored as one 16-byte piece per lane.  Both
+    // products above have their operands swapped, so O[u] is the transposed
+    // tile: lane (t, G) holds token 16u + t, columns r0 + 4G .. r0 + 4G + 3.
     {
       bf16* stage = reinterpret_cast<bf16*>(smem + L::V0 + STG * L::VT) + sw * 512;
 #pragma unroll
       for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) stage[(16 * u + 4 * G + j) * 16 + lc] = (bf16)O[u][j];
+        *reinterpret_cast<bf16x4*>(stage + (16 * u + lc) * 16 + 4 * G) =
+            bf16x4{(bf16)O[u][0], (bf16)O[u][1], (bf16)O[u][2], (bf16)O[u][3]};
       const int tok = l >> 1, half = l & 1;  // lanes: 32 tokens x 2 pieces of 8 columns
       const bf16x8 piece = *reinterpret_cast<const bf16x8*>(stage + tok * 16 + 8 * half);
       *reinterpret_cast<bf16x8*>(og - lc + ((int64_t)i * CB_C + 32 * h + tok) * p.so[2] + 8 * half) = piece;
