@@ -18,6 +18,11 @@ autograd registered on the forward operators:
   ``states`` is the library-private state checkpoint (empty unless
   ``record``).
 * ``gmdn::chunk_bwd(...) -> (dq, dk, dv, dbeta, dg, dgmu, dgnu)``.
+* ``gmdn::front_fwd`` / ``gmdn::front_bwd`` -- the mixer front-end (causal
+  depthwise conv, SiLU, q/k norms; train_ablation.py:124-128).
+* ``gmdn::msign(M, steps, eps) -> X`` -- the outer Muon optimizer's msign of
+  a batch of matrices (train_ablation.py:60-73); no autograd (the optimizer
+  runs it under ``no_grad``).
 
 Operators cannot return ``None``: absent optional results are empty tensors.
 There is no CPU implementation; CPU tensors never reach these operators (the
@@ -322,3 +327,32 @@ def _front_backward(ctx, dq, dk, dv):
 
 
 front_fwd.register_autograd(_front_backward, setup_context=_front_setup)
+
+
+# ------------------------------------------------------------ outer msign
+@torch.library.custom_op("gmdn::msign", mutates_args=(), device_types="cuda")
+def msign(M: Tensor, steps: int, eps: float) -> Tensor:
+    """msign of each matrix of ``M`` (..., rows, cols), float32 or bfloat16,
+    result in ``M``'s dtype (reference train_ablation.py:60-73)."""
+    lib = nat.load()
+    if M.dim() < 2:
+        raise RuntimeError(f"msign needs a matrix or a batch of matrices, got shape {tuple(M.shape)}")
+    if M.dtype not in (torch.float32, torch.bfloat16):
+        raise RuntimeError(f"gmdn::msign takes float32 or bfloat16, got {M.dtype}")
+    rows, cols = M.shape[-2], M.shape[-1]
+    Mc = M.contiguous()
+    out = torch.empty_like(Mc)
+    batch = Mc.numel() // max(rows * cols, 1) if rows * cols else 0
+    if batch == 0:
+        return out
+    ws = torch.empty(lib.gmdn_msign_workspace_bytes(batch, rows, cols), dtype=torch.uint8, device=M.device)
+    with torch.cuda.device(M.device):
+        rc = lib.gmdn_msign(nat.ptr(Mc), nat.ptr(out), batch, rows, cols, steps, eps, _dtype_code(Mc), nat.ptr(ws),
+                            ws.numel(), nat.stream_of(Mc))
+    nat.check(rc, "gmdn_msign")
+    return out
+
+
+@msign.register_fake
+def _msign_fake(M, steps, eps):
+    return torch.empty_like(M, memory_format=torch.contiguous_format)

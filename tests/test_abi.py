@@ -103,3 +103,29 @@ def test_front_argument_checks():
     assert lib.gmdn_front_fwd(None, None, None, None, None, None, 0, 64, 256, 128, 4, 0, None) == 0  # empty
     assert lib.gmdn_front_bwd(p, p, p, p, p, p, p, None, 2, 64, 256, 128, 4, 0, None) == 1  # no workspace
     assert lib.gmdn_front_bwd_workspace_floats(2, 65, 256, 4) == 2 * 2 * 768 * 5
+
+
+def test_msign_workspace_and_argument_validation():
+    lib = _native.load()
+    assert lib.gmdn_msign_workspace_bytes(0, 4, 4) == 0
+    assert lib.gmdn_msign_workspace_bytes(1, 0, 4) == 0
+    assert lib.gmdn_msign_workspace_bytes(1, 40000, 4) == 0
+    # 24 x 1024 pads to 128 x 1024: two X buffers, A and Bm (128 x 128), 64 partial sums, 256-aligned
+    x, a = 128 * 1024 * 4, 128 * 128 * 4
+    assert lib.gmdn_msign_workspace_bytes(1, 24, 1024) == 2 * x + 2 * a + 256
+    assert lib.gmdn_msign_workspace_bytes(3, 1024, 24) == 2 * 3 * x + 2 * 3 * a + 768
+    p = 0x1000
+
+    def call(M=p, out=p, batch=2, rows=8, cols=8, steps=5, eps=1e-7, dtype=1, ws=0x100000, wsb=1 << 30):
+        return lib.gmdn_msign(M, out, batch, rows, cols, steps, eps, dtype, ws, wsb, None)
+
+    assert call(batch=-1) == 1
+    assert call(steps=-1) == 1 and call(steps=65) == 1
+    assert call(eps=float("nan")) == 1 and call(eps=-1.0) == 1
+    assert call(dtype=7) == 2
+    assert call(rows=40000) == 2
+    assert call(M=None) == 1 and call(out=None) == 1
+    assert call(ws=None) == 3
+    assert call(wsb=16) == 3
+    assert call(ws=0x100010) == 3  # workspace not 256-byte aligned
+    assert call(batch=0) == 0 and call(rows=0) == 0  # empty: nothing to do, nothing launched
