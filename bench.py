@@ -24,6 +24,8 @@ own roofline.  ``cpu_baseline`` times the CPU restatement of the reference matri
 
 ``--workload lm_b8_t2048_muon`` times the 12-layer LM stack around the
 fused core end to end (forward + backward, tokens/s only).
+``--workload outer_muon_lm12_d1024`` times one outer Muon optimizer step
+(msign of the LM's 60 hidden weights) in fp32-equivalent TFLOP/s.
 
 ``--fwd-only`` times the inference forward alone; ``--copy-calibration
 BYTES`` only runs a device copy of BYTES bytes a few times (the calibration
@@ -272,6 +274,98 @@ def lm_line(args) -> dict:
     }
 
 
+MSIGN_WORKLOAD = "outer_muon_lm12_d1024"
+
+
+def msign_flops(rows: int, cols: int, steps: int) -> int:
+    """Algorithmic flops of msign on one rows x cols matrix: per NS step
+    X X^T (2 m^2 n), A A (2 m^3) and B X (2 m^2 n), m = min, n = max."""
+    m, n = min(rows, cols), max(rows, cols)
+    return steps * (4 * m * m * n + 2 * m ** 3)
+
+
+def lm_hidden_shapes(layers=12, d_model=1024, heads=8, gates=3):
+    """The 2-D weights the reference hands to Muon in the LM stack
+    (train_ablation.py:291-300): per layer the qkv, gate, out and the two MLP
+    projections (the embedding and the tied head go to AdamW)."""
+    per = [(3 * d_model, d_model), (gates * heads, d_model), (d_model, d_model), (4 * d_model, d_model),
+           (d_model, 4 * d_model)]
+    return [s for _ in range(layers) for s in per]
+
+
+def msign_line(args) -> dict:
+    """One outer Muon step (train_ablation.py:271-288, ns_steps 5) over the
+    LM's 60 hidden weights, fp32 parameters and N(0, 1) gradients; the
+    updates of each shape are orthogonalised in one batched msign call."""
+    import torch
+    from gmdn_amd.muon import Muon
+
+    dev = torch.device("cuda:0")
+    shapes = lm_hidden_shapes()
+    gen = torch.Generator(device=dev).manual_seed(0)
+    params = [torch.nn.Parameter(torch.randn(s, device=dev, generator=gen) * 0.02) for s in shapes]
+    for p in params:
+        p.grad = torch.randn(p.shape, device=dev, generator=gen)
+    opt = Muon(params, lr=0.02, momentum=0.95, nesterov=True, weight_decay=0.1, ns_steps=5)
+    flops = sum(msign_flops(*s, 5) for s in shapes)
+    stream = torch.cuda.current_stream(dev)
+    for _ in range(max(args.warmup, 1)):
+        opt.step()
+    torch.cuda.synchronize()
+    steps = min(args.steps, 20)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for e in evs:
+        e[0].record(stream)
+        opt.step()
+        e[1].record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    ev = statistics.mean(e[0].elapsed_time(e[1]) for e in evs) / 1e3
+    achieved = flops / ev / 1e12
+    line = {
+        "metric": METRIC, "value": flops / wall / 1e12, "unit": "TFLOP/s (msign, fp32-equivalent)", "n_gpus": 1,
+        "steps": steps, "warmup": max(args.warmup, 1), "ms_per_step": wall * 1e3, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32 (split bf16 products)", "data": "synthetic",
+        "config": {"workload": MSIGN_WORKLOAD, "matrices": len(shapes), "ns_steps": 5,
+                   "shapes": sorted({f"{r}x{c}" for r, c in shapes}), "parallelism": "none"},
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / BF16_PEAK_TFLOPS, "traffic": None},
+        "roofline_note": "algorithmic fp32-equivalent flops of the whole optimizer step (HIP events) against the "
+                         "bf16 MFMA peak; three split products per multiply cap frac at 1/3",
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = msign_cpu_baseline(shapes, args.cpu_budget)
+    return line
+
+
+def msign_cpu_baseline(shapes, budget_s: float) -> dict:
+    """The oracle's float32 msign (train_ablation.py:60-73 restated, torch on
+    the host cores) on one layer's five weights, scaled to all layers."""
+    import torch
+    from oracle import muon as om
+
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    layer = shapes[:5]
+    flops = sum(msign_flops(*s, 5) for s in layer)
+    gen = torch.Generator().manual_seed(0)
+    mats = [torch.randn(s, generator=gen) for s in layer]
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        for M in mats:
+            om.msign(M, 5)
+        reps += 1
+        if time.perf_counter() - t0 > min(budget_s, 30.0) or reps >= 3:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    return {"value": flops / dt / 1e12, "unit": "TFLOP/s (msign, fp32-equivalent)",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"one layer's 5 hidden weights, float32 torch matmuls, {reps} repetition(s); "
+                      f"a full optimizer step would take {dt * len(shapes) / len(layer) * 1e3:.0f} ms"}
+
+
 def copy_calibration(nbytes: int) -> None:
     import torch
     # an elementwise kernel (MulFunctor) that reads nbytes and writes nbytes
@@ -339,6 +433,9 @@ def main(argv=None):
 
     if args.workload == LM_WORKLOAD:
         print(json.dumps(lm_line(args)), flush=True)
+        return 0
+    if args.workload == MSIGN_WORKLOAD:
+        print(json.dumps(msign_line(args)), flush=True)
         return 0
     w = WORKLOADS[args.workload]
     dev = torch.device("cuda:0")

@@ -15,13 +15,17 @@
 //   Bm = b A + c A A           (A is symmetric, so A A = A A^T: by rows)
 //   X' = a X + Bm X            (X read by columns: transposing LDS reads)
 //
-// ns_gemm forms a 128 x 128 output tile per workgroup of four waves (64 x 64
-// each) from 32-wide contraction blocks that arrive by LDS-DMA in a 3-stage
-// ring.  The pieces copy to LDS unchanged (no conversion on the way), and
-// every MFMA operand is then one or two LDS reads.  The products are split
-// (hi hi + hi lo + lo hi); the MFMA operands are swapped so that each
-// lane's accumulator is four consecutive columns of one output row, which
-// leaves as one 16-byte piece.
+// A and Bm are symmetric: their launches form only the tiles on and above
+// the diagonal and write each off-diagonal tile twice, the mirror through an
+// LDS transpose.  ns_gemm forms a 128 x 128 output tile per workgroup of four
+// waves (64 x 64 each) from 32-wide contraction blocks that arrive by LDS-DMA
+// in a 2-stage ring (64 KiB, two workgroups per CU).  The pieces copy to LDS
+// unchanged (no conversion on the way), and every MFMA operand is then one
+// or two LDS reads.  The products are split (hi hi + hi lo + lo hi); the MFMA
+// operands are swapped so that each lane's accumulator is four consecutive
+// columns of one output row, which leaves as one 16-byte piece.  The
+// normalisation and the final unpacking move tall matrices through 64 x 64
+// LDS transposes.
 #include "../../include/gmdn_msign.h"
 #include "tile.h"
 
@@ -40,8 +44,11 @@ struct MsLds {
   static constexpr int PIECES = MS_TILE * MS_KB / 4;  // 16-byte pieces per operand tile
   static constexpr int OPB = PIECES * 16;             // 16 KiB
   static constexpr int STAGE = 2 * OPB;               // P tile, then Q tile
-  static constexpr int BYTES = MS_STAGES * STAGE;     // 96 KiB
   static constexpr int NOPS = PIECES / MS_THREADS;    // LDS-DMA copies per thread and tile
+  static constexpr int MIRROR_LD = 68;                // words per row of a wave's transposed 64 x 64 tile
+  static constexpr int MIRROR = 64 * MIRROR_LD * 4;   // bytes of it, one per wave after the loop
+  static constexpr int RING = MS_STAGES * STAGE;
+  static constexpr int BYTES = RING > 4 * MIRROR ? RING : 4 * MIRROR;
 };
 
 int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
@@ -49,19 +56,37 @@ int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 template <typename T>
 GMDN_DEV float ld_elem(const T* p) { return (float)*p; }
 
-// ------------------------------------------------------------------ norm
-// Partial sums of squares: workgroup (blk, b) takes elements blk*256 + t,
-// strided by MS_NPART * 256, of matrix b.
+// four consecutive elements (16-byte aligned for float, 8-byte for bf16)
 template <typename T>
+GMDN_DEV f32x4 ld4(const T* p);
+template <>
+GMDN_DEV f32x4 ld4<float>(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+template <>
+GMDN_DEV f32x4 ld4<bf16>(const bf16* p) {
+  const bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
+  return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+}
+
+// ------------------------------------------------------------------ norm
+// Partial sums of squares: workgroup (blk, b) takes elements (VEC: groups of
+// four) blk*256 + t, strided by MS_NPART * 256, of matrix b.
+template <typename T, bool VEC>
 __global__ void __launch_bounds__(256) ns_norm_partial(const T* __restrict__ M, float* __restrict__ part,
                                                        int64_t per) {
   __shared__ float red[4];
   const int64_t b = blockIdx.y;
   const T* Mb = M + b * per;
   float s = 0.f;
-  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < per; e += (int64_t)MS_NPART * 256) {
-    const float v = ld_elem(Mb + e);
-    s += v * v;
+  if constexpr (VEC) {
+    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; 4 * e < per; e += (int64_t)MS_NPART * 256) {
+      const f32x4 v = ld4(Mb + 4 * e);
+      s += (v[0] * v[0] + v[1] * v[1]) + (v[2] * v[2] + v[3] * v[3]);
+    }
+  } else {
+    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < per; e += (int64_t)MS_NPART * 256) {
+      const float v = ld_elem(Mb + e);
+      s += v * v;
+    }
   }
   s = wave_sum(s);
   if (lane_id() == 0) red[wave_id()] = s;
@@ -69,58 +94,117 @@ __global__ void __launch_bounds__(256) ns_norm_partial(const T* __restrict__ M, 
   if (threadIdx.x == 0) part[b * MS_NPART + blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
 }
 
-// ------------------------------------------------------------------ pack
-// X0 = X / (|X|_F + eps) as split pieces, zero-padded to mp x np.  TR: X = M^T
-// (M is rows x cols with rows > cols); consecutive threads then take
-// consecutive rows of X, so that the reads of M are coalesced.
-template <typename T, bool TR>
-__global__ void __launch_bounds__(256) ns_pack(const T* __restrict__ M, const float* __restrict__ part,
-                                               char* __restrict__ X, int64_t x_bs, int m, int n, int mp,
-                                               int np, int cols, float eps) {
-  __shared__ float nrm_s;
-  const int64_t b = blockIdx.y;
+GMDN_DEV float block_norm(const float* part, int64_t b, float* nrm_s) {
   if (threadIdx.x < 64) {
     const float t = wave_sum(part[b * MS_NPART + threadIdx.x]);
-    if (threadIdx.x == 0) nrm_s = sqrtf(t);
+    if (threadIdx.x == 0) *nrm_s = sqrtf(t);
   }
   __syncthreads();
-  const float den = nrm_s + eps;
+  return *nrm_s;
+}
+
+// ------------------------------------------------------------------ pack
+// X0 = X / (|X|_F + eps) as split pieces, zero-padded to mp x np, X = M
+// (rows <= cols).  One thread per piece; VEC: cols % 4 == 0, so a piece is
+// one aligned load of M.
+template <typename T, bool VEC>
+__global__ void __launch_bounds__(256) ns_pack(const T* __restrict__ M, const float* __restrict__ part,
+                                               char* __restrict__ X, int64_t x_bs, int m, int n, int mp,
+                                               int np, float eps) {
+  __shared__ float nrm_s;
+  const int64_t b = blockIdx.y;
+  const float den = block_norm(part, b, &nrm_s) + eps;
   const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int nq = np / 4;
   if (p >= (int64_t)mp * nq) return;
-  int r, q;
-  if constexpr (TR) {
-    r = (int)(p % mp);
-    q = (int)(p / mp);
-  } else {
-    r = (int)(p / nq);
-    q = (int)(p % nq);
-  }
+  const int r = (int)(p / nq), q = (int)(p % nq);
   const T* Mb = M + b * (int64_t)m * n;
-  f32x4 v;
+  f32x4 v = zero4();
+  if constexpr (VEC) {
+    if (r < m && 4 * q < n) v = ld4(Mb + (int64_t)r * n + 4 * q);
+  } else {
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int c = 4 * q + e;
-    float x = 0.f;
-    if (r < m && c < n) x = TR ? ld_elem(Mb + (int64_t)c * cols + r) : ld_elem(Mb + (int64_t)r * cols + c);
-    v[e] = x / den;  // the reference divides (train_ablation.py:65)
+    for (int e = 0; e < 4; ++e)
+      if (r < m && 4 * q + e < n) v[e] = ld_elem(Mb + (int64_t)r * n + 4 * q + e);
   }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = v[e] / den;  // the reference divides (train_ablation.py:65)
   *reinterpret_cast<bf16x8*>(X + b * x_bs + ((int64_t)r * np + 4 * q) * 4) = split_piece(v);
 }
 
+// Transposing pack, X = M^T (M is n x m with n > m): workgroup (tile, b)
+// moves a 64 x 64 block through LDS; rows of M are read and rows of X
+// written 256 contiguous bytes per wave instruction.
+template <typename T>
+__global__ void __launch_bounds__(256) ns_pack_tr(const T* __restrict__ M, const float* __restrict__ part,
+                                                  char* __restrict__ X, int64_t x_bs, int m, int n, int mp,
+                                                  int np, float eps) {
+  __shared__ float nrm_s;
+  __shared__ float tile[64][65];  // [row of M][column of M]
+  const int64_t b = blockIdx.y;
+  const float den = block_norm(part, b, &nrm_s) + eps;
+  const int tx = mp / 64;
+  const int r0 = (int)(blockIdx.x % tx) * 64;  // first row of X (= column of M)
+  const int c0 = (int)(blockIdx.x / tx) * 64;  // first column of X (= row of M)
+  const T* Mb = M + b * (int64_t)m * n;
+  const int t = threadIdx.x, lr = t >> 6, lcol = t & 63;
+#pragma unroll
+  for (int it = 0; it < 16; ++it) {
+    const int mr = c0 + 4 * it + lr, mc = r0 + lcol;
+    tile[4 * it + lr][lcol] = (mr < n && mc < m) ? ld_elem(Mb + (int64_t)mr * m + mc) : 0.f;
+  }
+  __syncthreads();
+  const int q = t & 15;
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int rl = (t >> 4) + 16 * it;
+    f32x4 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = tile[4 * q + e][rl] / den;
+    *reinterpret_cast<bf16x8*>(X + b * x_bs + ((int64_t)(r0 + rl) * np + c0 + 4 * q) * 4) = split_piece(v);
+  }
+}
+
 // ---------------------------------------------------------------- unpack
-// out (rows x cols, dtype T) from the padded pieces of X; TR: out = X^T.
-template <typename T, bool TR>
+// out (rows x cols, dtype T) = X from the padded pieces.
+template <typename T>
 __global__ void __launch_bounds__(256) ns_unpack(const char* __restrict__ X, T* __restrict__ out, int64_t x_bs,
                                                  int rows, int cols, int np) {
   const int64_t b = blockIdx.y;
   const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (e >= (int64_t)rows * cols) return;
   const int orow = (int)(e / cols), ocol = (int)(e % cols);
-  const int xr = TR ? ocol : orow, xc = TR ? orow : ocol;
-  const bf16* pc = reinterpret_cast<const bf16*>(X + b * x_bs + ((int64_t)xr * np + (xc & ~3)) * 4);
-  const float v = (float)pc[xc & 3] + (float)pc[4 + (xc & 3)];
+  const bf16* pc = reinterpret_cast<const bf16*>(X + b * x_bs + ((int64_t)orow * np + (ocol & ~3)) * 4);
+  const float v = (float)pc[ocol & 3] + (float)pc[4 + (ocol & 3)];
   out[b * (int64_t)rows * cols + e] = (T)v;
+}
+
+// Transposing unpack, out = X^T (out is rows x cols with rows > cols, X is
+// cols x rows): 64 x 64 blocks through LDS, both sides row-contiguous.
+template <typename T>
+__global__ void __launch_bounds__(256) ns_unpack_tr(const char* __restrict__ X, T* __restrict__ out, int64_t x_bs,
+                                                    int rows, int cols, int mp, int np) {
+  __shared__ float tile[64][65];  // [row of X][column of X]
+  const int64_t b = blockIdx.y;
+  const int tx = mp / 64;
+  const int xr0 = (int)(blockIdx.x % tx) * 64;  // first row of X (= column of out)
+  const int xc0 = (int)(blockIdx.x / tx) * 64;  // first column of X (= row of out)
+  const int t = threadIdx.x, q = t & 15;
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int rl = (t >> 4) + 16 * it;
+    const f32x4 v = unsplit_piece(*reinterpret_cast<const bf16x8*>(X + b * x_bs + ((int64_t)(xr0 + rl) * np + xc0 + 4 * q) * 4));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) tile[rl][4 * q + e] = v[e];
+  }
+  __syncthreads();
+  const int lr = t >> 6, lcol = t & 63;
+  T* ob = out + b * (int64_t)rows * cols;
+#pragma unroll
+  for (int it = 0; it < 16; ++it) {
+    const int orow = xc0 + 4 * it + lr, ocol = xr0 + lcol;
+    if (orow < rows && ocol < cols) ob[(int64_t)orow * cols + ocol] = (T)tile[lcol][4 * it + lr];
+  }
 }
 
 // ------------------------------------------------------------------ GEMM
@@ -152,7 +236,7 @@ GMDN_DEV f32x4 mma3(const PieceOp& a, const PieceOp& b, f32x4 acc) {
   return acc;
 }
 
-template <bool NN, bool EPI>
+template <bool NN, bool EPI, bool SYM>
 __global__ void __launch_bounds__(MS_THREADS)
 ns_gemm(const char* __restrict__ P, const char* __restrict__ Q, const char* __restrict__ Dm,
         char* __restrict__ Cm, int64_t p_bs, int64_t q_bs, int64_t c_bs, int p_ld, int q_ld, int c_ld, int mt,
@@ -164,9 +248,21 @@ ns_gemm(const char* __restrict__ P, const char* __restrict__ Q, const char* __re
   // tile order, so the workgroups of one P row panel share an L2.
   const int64_t total = gridDim.x, x = blockIdx.x;
   const int64_t t = (total % 8 == 0) ? (x % 8) * (total / 8) + x / 8 : x;
-  const int tiles = mt * nt;
+  // SYM (square symmetric C, mt == nt): only the tiles ti <= tj, in row order
+  const int tiles = SYM ? mt * (mt + 1) / 2 : mt * nt;
   const int64_t b = t / tiles;
-  const int rem = (int)(t % tiles), ti = rem / nt, tj = rem % nt;
+  int rem = (int)(t % tiles), ti, tj;
+  if constexpr (SYM) {
+    ti = 0;
+    while (rem >= mt - ti) {
+      rem -= mt - ti;
+      ++ti;
+    }
+    tj = ti + rem;
+  } else {
+    ti = rem / nt;
+    tj = rem % nt;
+  }
   const int w = __builtin_amdgcn_readfirstlane(wave_id());
   const int l = lane_id(), G = l >> 4, lc = l & 15;
   const int wi = w >> 1, wj = w & 1;
@@ -233,17 +329,22 @@ ns_gemm(const char* __restrict__ P, const char* __restrict__ Q, const char* __re
 #pragma unroll
     for (int v = 0; v < 4; ++v) acc[u][v] = zero4();
 
+  // blocks are copied MS_STAGES - 1 ahead; block kb + MS_STAGES - 1 reuses
+  // the stage of block kb - 1
+  constexpr int AHEAD = MS_STAGES - 1;
+  static_assert(AHEAD == 1 || AHEAD == 2, "ring of 2 or 3 stages");
   const int nkb = K / MS_KB;
-  issue(0, 0);
-  if (nkb > 1) issue(1, 1);
+#pragma unroll
+  for (int s = 0; s < AHEAD; ++s)
+    if (s < nkb) issue(s, s);
   for (int kb = 0; kb < nkb; ++kb) {
     const int stage = kb % MS_STAGES;
-    if (kb + 1 < nkb)
+    if (AHEAD == 2 && kb + 1 < nkb)
       wait_vmem_le<2 * Lp::NOPS>();  // this wave's copies of block kb landed; kb+1's may still fly
     else
       wait_vmem();
     __syncthreads();  // every wave's copies of block kb visible; block kb-1's stage free
-    if (kb + 2 < nkb) issue(kb + 2, (kb + 2) % MS_STAGES);
+    if (kb + AHEAD < nkb) issue(kb + AHEAD, (kb + AHEAD) % MS_STAGES);
     const lds_cptr Ls = L0 + stage * Lp::STAGE;
     PieceOp po[4], qo[4];
 #pragma unroll
@@ -281,6 +382,31 @@ ns_gemm(const char* __restrict__ P, const char* __restrict__ Q, const char* __re
         for (int e = 0; e < 4; ++e) r[e] = alpha * r[e] + beta * d[e];
       }
       *reinterpret_cast<bf16x8*>(Cm + off) = split_piece(r);
+      acc[u][v] = r;
+    }
+  }
+  if constexpr (SYM) {
+    // the mirror tile (tj, ti): each wave transposes its 64 x 64 block
+    // through its own LDS rows, T[j][i] at word 68 j + i
+    if (ti != tj) {
+      __syncthreads();  // every wave is done with the ring
+      const lds_ptr Tw = L0 + w * Lp::MIRROR;
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            lds_st<float>(Tw + ((16 * v + 4 * G + e) * Lp::MIRROR_LD + 16 * u + lc) * 4, acc[u][v][e]);
+      __syncthreads();
+      const int i4 = l & 15, jj = l >> 4;
+#pragma unroll
+      for (int it = 0; it < 16; ++it) {
+        const int j = 4 * it + jj;
+        const f32x4 r = lds_ld<f32x4>(Tw + (j * Lp::MIRROR_LD + 4 * i4) * 4);
+        const int64_t row = (int64_t)tj * MS_TILE + 64 * wj + j, col = (int64_t)ti * MS_TILE + 64 * wi + 4 * i4;
+        *reinterpret_cast<bf16x8*>(Cm + b * c_bs + (row * c_ld + col) * 4) = split_piece(r);
+      }
     }
   }
 }
@@ -306,15 +432,16 @@ bool plan(int64_t batch, int64_t rows, int64_t cols, MsPlan& p) {
   return true;
 }
 
-template <bool NN, bool EPI>
+template <bool NN, bool EPI, bool SYM = false>
 hipError_t launch_gemm(const char* P, const char* Q, const char* D, char* C, int64_t batch, int64_t p_bs,
                        int64_t q_bs, int64_t c_bs, int p_ld, int q_ld, int c_ld, int M, int N, int K, float alpha,
                        float beta, hipStream_t st) {
-  auto kern = ns_gemm<NN, EPI>;
+  auto kern = ns_gemm<NN, EPI, SYM>;
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, MsLds::BYTES);
   if (e != hipSuccess) return e;
   const int mt = M / MS_TILE, nt = N / MS_TILE;
-  hipLaunchKernelGGL(kern, dim3((unsigned)(batch * mt * nt)), dim3(MS_THREADS), MsLds::BYTES, st, P, Q, D, C, p_bs,
+  const int64_t tiles = SYM ? (int64_t)mt * (mt + 1) / 2 : (int64_t)mt * nt;
+  hipLaunchKernelGGL(kern, dim3((unsigned)(batch * tiles)), dim3(MS_THREADS), MsLds::BYTES, st, P, Q, D, C, p_bs,
                      q_bs, c_bs, p_ld, q_ld, c_ld, mt, nt, K, alpha, beta);
   return hipGetLastError();
 }
@@ -332,25 +459,37 @@ hipError_t run_msign(const T* M, T* out, int64_t batch, int64_t rows, int64_t co
   const int64_t xb = (int64_t)p.x_bytes, ab = (int64_t)p.a_bytes;
   const int mp = (int)p.mp, np = (int)p.np;
 
-  hipLaunchKernelGGL(ns_norm_partial<T>, dim3(MS_NPART, (unsigned)batch), dim3(256), 0, st, M, part, rows * cols);
+  const bool vec = (rows * cols) % 4 == 0 && ((uintptr_t)M % (4 * sizeof(T))) == 0;
+  if (vec)
+    hipLaunchKernelGGL((ns_norm_partial<T, true>), dim3(MS_NPART, (unsigned)batch), dim3(256), 0, st, M, part,
+                       rows * cols);
+  else
+    hipLaunchKernelGGL((ns_norm_partial<T, false>), dim3(MS_NPART, (unsigned)batch), dim3(256), 0, st, M, part,
+                       rows * cols);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const unsigned pack_blocks = (unsigned)((p.mp * (p.np / 4) + 255) / 256);
-  if (tr)
-    hipLaunchKernelGGL((ns_pack<T, true>), dim3(pack_blocks, (unsigned)batch), dim3(256), 0, st, M, part, X[0], xb,
-                       (int)p.m, (int)p.n, mp, np, (int)cols, eps);
-  else
-    hipLaunchKernelGGL((ns_pack<T, false>), dim3(pack_blocks, (unsigned)batch), dim3(256), 0, st, M, part, X[0],
-                       xb, (int)p.m, (int)p.n, mp, np, (int)cols, eps);
+  if (tr) {
+    const unsigned blocks = (unsigned)((p.mp / 64) * (p.np / 64));
+    hipLaunchKernelGGL(ns_pack_tr<T>, dim3(blocks, (unsigned)batch), dim3(256), 0, st, M, part, X[0], xb, (int)p.m,
+                       (int)p.n, mp, np, eps);
+  } else {
+    const unsigned blocks = (unsigned)((p.mp * (p.np / 4) + 255) / 256);
+    if (vec && cols % 4 == 0)
+      hipLaunchKernelGGL((ns_pack<T, true>), dim3(blocks, (unsigned)batch), dim3(256), 0, st, M, part, X[0], xb,
+                         (int)p.m, (int)p.n, mp, np, eps);
+    else
+      hipLaunchKernelGGL((ns_pack<T, false>), dim3(blocks, (unsigned)batch), dim3(256), 0, st, M, part, X[0], xb,
+                         (int)p.m, (int)p.n, mp, np, eps);
+  }
   if ((e = hipGetLastError()) != hipSuccess) return e;
   int cur = 0;
   for (int s = 0; s < steps; ++s) {
     // A = X X^T
-    e = launch_gemm<false, false>(X[cur], X[cur], nullptr, A, batch, xb, xb, ab, np, np, mp, mp, mp, np, 1.f, 0.f,
+    e = launch_gemm<false, false, true>(X[cur], X[cur], nullptr, A, batch, xb, xb, ab, np, np, mp, mp, mp, np, 1.f, 0.f,
                                   st);
     if (e != hipSuccess) return e;
     // Bm = b A + c A A
-    e = launch_gemm<false, true>(A, A, A, Bm, batch, ab, ab, ab, mp, mp, mp, mp, mp, mp, NS_C, NS_B, st);
+    e = launch_gemm<false, true, true>(A, A, A, Bm, batch, ab, ab, ab, mp, mp, mp, mp, mp, mp, NS_C, NS_B, st);
     if (e != hipSuccess) return e;
     // X' = a X + Bm X
     e = launch_gemm<true, true>(Bm, X[cur], X[cur], X[cur ^ 1], batch, ab, xb, xb, mp, np, np, mp, np, mp, 1.f,
@@ -358,13 +497,15 @@ hipError_t run_msign(const T* M, T* out, int64_t batch, int64_t rows, int64_t co
     if (e != hipSuccess) return e;
     cur ^= 1;
   }
-  const unsigned out_blocks = (unsigned)((rows * cols + 255) / 256);
-  if (tr)
-    hipLaunchKernelGGL((ns_unpack<T, true>), dim3(out_blocks, (unsigned)batch), dim3(256), 0, st, X[cur], out, xb,
-                       (int)rows, (int)cols, np);
-  else
-    hipLaunchKernelGGL((ns_unpack<T, false>), dim3(out_blocks, (unsigned)batch), dim3(256), 0, st, X[cur], out, xb,
-                       (int)rows, (int)cols, np);
+  if (tr) {
+    const unsigned blocks = (unsigned)((p.mp / 64) * (p.np / 64));
+    hipLaunchKernelGGL(ns_unpack_tr<T>, dim3(blocks, (unsigned)batch), dim3(256), 0, st, X[cur], out, xb, (int)rows,
+                       (int)cols, mp, np);
+  } else {
+    const unsigned blocks = (unsigned)((rows * cols + 255) / 256);
+    hipLaunchKernelGGL(ns_unpack<T>, dim3(blocks, (unsigned)batch), dim3(256), 0, st, X[cur], out, xb, (int)rows,
+                       (int)cols, np);
+  }
   return hipGetLastError();
 }
 

@@ -76,3 +76,18 @@ def test_drop_in_cpu_baseline_runs_on_a_small_workload():
     cb = bench.drop_in_cpu_baseline(w, 0.2)
     assert cb["value"] > 0 and cb["kind"] == "port" and cb["cores"] >= 1
     assert "heads" in cb["sample"]
+
+
+def test_msign_accounting():
+    # per NS step: X X^T (2 m^2 n) + A A (2 m^3) + B X (2 m^2 n), m = min(rows, cols)
+    assert bench.msign_flops(3072, 1024, 5) == bench.msign_flops(1024, 3072, 5) == 5 * (4 * 1024 ** 2 * 3072 + 2 * 1024 ** 3)
+    shapes = bench.lm_hidden_shapes()
+    assert len(shapes) == 60 and shapes[:5] == [(3072, 1024), (24, 1024), (1024, 1024), (4096, 1024), (1024, 4096)]
+    # about 3.6 TFLOP per outer optimizer step at the LM shapes
+    assert round(sum(bench.msign_flops(*s, 5) for s in shapes) / 1e12, 2) == 3.61
+
+
+def test_msign_cpu_baseline_runs():
+    shapes = [(48, 32), (8, 32), (32, 32), (64, 32), (32, 64)]
+    r = bench.msign_cpu_baseline(shapes, 0.1)
+    assert r["kind"] == "port" and r["value"] > 0 and r["cores"] >= 1
