@@ -103,14 +103,16 @@ def _muon_core(q, k, v, beta, g, gmu, ns):
     # token weights prod_{s' > s} mu_{s'} (train_ablation.py:154-156)
     w = torch.exp(torch.flip(torch.cumsum(torch.flip(lmu, [-1]), -1), [-1]) - lmu)
     causal = torch.tril(torch.ones(CHUNK, CHUNK, dtype=torch.bool, device=q.device))
-    kT = kf.transpose(-1, -2).contiguous()
-    A = torch.where(causal, torch.matmul(qf, kT) * bt.unsqueeze(-2), 0.0)
-    Kw = torch.matmul((kf * w.unsqueeze(-1)).transpose(-1, -2).contiguous(), kf)
-    Uv = torch.matmul((vf * w.unsqueeze(-1)).transpose(-1, -2).contiguous(), kf)
+    # float32 batched products take the transposed views as they are (strided
+    # GEMM operands), so no transposed copy is made of k, the weighted tiles
+    # or the (B, H, N, d, d) state stack
+    A = torch.where(causal, torch.matmul(qf, kf.transpose(-1, -2)) * bt.unsqueeze(-2), 0.0)
+    Kw = torch.matmul((kf * w.unsqueeze(-1)).transpose(-1, -2), kf)
+    Uv = torch.matmul((vf * w.unsqueeze(-1)).transpose(-1, -2), kf)
     Qt = qf - torch.matmul(A, kf)
     Ov = torch.matmul(A, vf)
     S_all = hip_state_scan(Uv, Kw, a, b, m, n, 1, ns)
-    o = torch.matmul(Qt, S_all.transpose(-1, -2).contiguous()) + Ov
+    o = torch.matmul(Qt, S_all.transpose(-1, -2)) + Ov
     return o.reshape(B, H, T, d).to(q.dtype)
 
 
