@@ -421,13 +421,14 @@ __global__ void __launch_bounds__(CB_THREADS) chunk_bwd_state(ChunkArgs p) {
 //    LDS operands (no global memory access);
 //  * token waves 4..6: one step ahead, the state-independent part of dE,
 //    P = A^T dO, for the token tiles st = 0 | 1 | 2, 3 of both row tiles;
-//  * memory wave 7: every LDS-DMA load, the gate scalar a_i and the Gb_i
-//    stores.  Vector-memory issue is limited per CU, so the waves that
-//    compute never wait behind it.
+//  * memory wave 7: every LDS-DMA load and the gate scalar a_i; token waves
+//    4 and 5 store Gb_i (half each).  Vector-memory issue is limited per
+//    wave and per CU, so the state waves never wait behind it.
 // Per step j (chunk i = N-1-j), between the barriers X (end of step j-1) and Y:
 //   state : dE = diag(beta) K Gb_i^T + P_i (tokens 32h.., rows rt) -> XE
-//   token : (Q K^T) tiles of step j+1
-//   memory: loads of step j+2; a_i; Gb_i = Sb_{i+1} read back from XS and stored
+//   token : (Q K^T) tiles of step j+1; waves 4, 5: Gb_i = Sb_{i+1} read back
+//           from XS and stored
+//   memory: loads of step j+2; a_i
 // and between Y and X:
 //   state : Sb_i = a_i Sb_{i+1} + dO^T Q - dE^T K (column half h) -> XS
 //   token : P of step j+1 -> P slots
@@ -686,9 +687,38 @@ __global__ void __launch_bounds__(DS_THREADS) chunk_bwd_dstate(ChunkArgs p) {
         pmul(ns_tag, I3{}, A1);
       }
     };
-    auto step = [&](auto ns_tag, bool next) {  // step j: P of step j+1 (stage NS)
+    // Gb_i = Sb_{i+1}, published at the last X, stored as split pieces by
+    // token waves 0 and 1 (half of the 32 x D exchange each, 16-byte groups
+    // g = 64 k + l), so that the memory wave issues loads only
+    constexpr int GPR = D / 8, NG = 32 * GPR / 64, NGW = NG / 2;
+    static_assert(NG % 2 == 0, "Gb groups split over two waves");
+    uint32_t xso[NGW];
+#pragma unroll
+    for (int k = 0; k < NGW; ++k) {
+      const int g = 64 * (NGW * tw + k) + l;
+      xso[k] = swz_off<LQ>(g / GPR, 8 * (g % GPR));
+    }
+    auto store_gb = [&](int i) {
+      bf16x8 hi[NGW], lo[NGW];
+#pragma unroll
+      for (int k = 0; k < NGW; ++k) {
+        hi[k] = lds_ld<bf16x8>(L0 + (xso[k] + L::XS0));
+        lo[k] = lds_ld<bf16x8>(L0 + (xso[k] + L::XS0 + L::XSP));
+      }
+      float* gp = p.gb + ((bh * p.N + i) * D + 32 * blk) * (int64_t)D;
+#pragma unroll
+      for (int k = 0; k < NGW; ++k) {
+        const int g = 64 * (NGW * tw + k) + l;
+        float* dst = gp + (g / GPR) * D + 8 * (g % GPR);
+        *reinterpret_cast<bf16x8*>(dst) = __builtin_shufflevector(hi[k], lo[k], 0, 1, 2, 3, 8, 9, 10, 11);
+        *reinterpret_cast<bf16x8*>(dst + 4) = __builtin_shufflevector(hi[k], lo[k], 4, 5, 6, 7, 12, 13, 14, 15);
+      }
+    };
+    auto step = [&](auto ns_tag, int j) {  // step j: P of step j+1 (stage NS)
+      const bool next = j + 1 < p.N;
       Op<2> A0[2], A1[2];
       if (next) share_tiles(ns_tag, A0, A1);
+      if (tw < 2) store_gb(p.N - 1 - j);  // reads the exchange before Y overwrites it
       __syncthreads();  // Y
       if (next) share_p(ns_tag, A0, A1);
       __syncthreads();  // X
@@ -701,9 +731,9 @@ __global__ void __launch_bounds__(DS_THREADS) chunk_bwd_dstate(ChunkArgs p) {
     }
     __syncthreads();  // step 0's P published
     for (int j = 0; j < p.N; j += RING) {
-      step(I1{}, j + 1 < p.N);
-      if (j + 1 < p.N) step(I2{}, j + 2 < p.N);
-      if (j + 2 < p.N) step(I0{}, j + 3 < p.N);
+      step(I1{}, j);
+      if (j + 1 < p.N) step(I2{}, j + 1);
+      if (j + 2 < p.N) step(I0{}, j + 2);
     }
   } else {
     // ================================================================ memory
@@ -729,28 +759,6 @@ __global__ void __launch_bounds__(DS_THREADS) chunk_bwd_dstate(ChunkArgs p) {
       }
       lds_dma16(gsrc + t0, smem + L::G0 + stg * L::GT);
     };
-    // Gb rows: lane l takes the 16-byte groups g = 64 k + l of the 32 x D exchange
-    constexpr int GPR = D / 8, NG = 32 * GPR / 64;
-    uint32_t xso[NG];
-#pragma unroll
-    for (int k = 0; k < NG; ++k) xso[k] = swz_off<LQ>((64 * k + l) / GPR, 8 * ((64 * k + l) % GPR));
-    auto store_gb = [&](int i) {  // split pieces, copied from the exchange planes
-      bf16x8 hi[NG], lo[NG];
-#pragma unroll
-      for (int k = 0; k < NG; ++k) {
-        hi[k] = lds_ld<bf16x8>(L0 + (xso[k] + L::XS0));
-        lo[k] = lds_ld<bf16x8>(L0 + (xso[k] + L::XS0 + L::XSP));
-      }
-      float* gp = p.gb + ((bh * p.N + i) * D + 32 * blk) * (int64_t)D;
-#pragma unroll
-      for (int k = 0; k < NG; ++k) {
-        const int g = 64 * k + l;
-        float* dst = gp + (g / GPR) * D + 8 * (g % GPR);
-        *reinterpret_cast<bf16x8*>(dst) = __builtin_shufflevector(hi[k], lo[k], 0, 1, 2, 3, 8, 9, 10, 11);
-        *reinterpret_cast<bf16x8*>(dst + 4) = __builtin_shufflevector(hi[k], lo[k], 4, 5, 6, 7, 12, 13, 14, 15);
-      }
-    };
-
     for (int j = 0; j < RING - 1 && j < p.N; ++j) issue_loads(p.N - 1 - j, j);
     wait_vmem();
     __syncthreads();
@@ -764,10 +772,9 @@ __global__ void __launch_bounds__(DS_THREADS) chunk_bwd_dstate(ChunkArgs p) {
         const float a = expf(wave_sum(fmaxf(gg[CB_C + l], LOG_FLOOR)));
         if (l == 0) scal[4 * STG] = a;
       }
-      store_gb(p.N - 1 - j);  // Gb_i = Sb_{i+1}, published at the last X
-      __syncthreads();        // Y
-      wait_vmem();            // step j+2's tiles (and the Gb stores)
-      __syncthreads();        // X
+      __syncthreads();  // Y
+      wait_vmem();      // step j+2's tiles
+      __syncthreads();  // X
     };
     for (int j = 0; j < p.N; j += RING) {
       step(integral_constant<int, 0>{}, j);
