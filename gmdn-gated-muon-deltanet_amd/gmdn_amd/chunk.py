@@ -22,7 +22,8 @@ chunk transform, the scan and the output; backward: a reverse scan of the
 state cotangent and a chunk-parallel token-gradient kernel).  Muon's msign
 couples the whole state, so its recurrence runs in the drop-in scan's muon
 kernel (Newton-Schulz fused into the scan step) with phases 1 and 3 as
-batched GEMMs around it.
+batched GEMMs around it; adam at d = 128 trains the same way, with the scan
+in exact float32 (its inference forward stays fused).
 """
 from __future__ import annotations
 
@@ -43,12 +44,18 @@ BWD_RULES = (0, 1, 2)  # rules with a backward (muon: through the scan kernel's 
 
 
 def backward_supported(rule, d: int = 128) -> bool:
-    """Whether the fused backward of ``rule`` at head dim ``d`` is built.  The
-    adam backward is limited to d = 64: at d = 128 its sign-like update
-    amplifies the rounding of the split-bf16 state products past the
-    gradient tolerance."""
+    """Whether ``rule`` at head dim ``d`` has a backward: every rule and head
+    dim.  (The fused adam backward kernel is limited to d = 64 -- at d = 128
+    its sign-like update amplifies the rounding of the split-bf16 state
+    products past the gradient tolerance -- so adam at d = 128 trains through
+    the composed path of ``_composed_core``.)"""
+    return _rule_id(rule) in BWD_RULES
+
+
+def fused_backward(rule, d: int) -> bool:
+    """Whether the fused backward kernels cover ``rule`` at head dim ``d``."""
     r = _rule_id(rule)
-    return r in BWD_RULES and (r != 2 or d == 64)
+    return r == 0 or (r == 2 and d == 64)
 
 
 def _rule_id(rule) -> int:
@@ -83,13 +90,18 @@ def _check(q, k, v, beta, g, gmu, gnu, rule):
         raise RuntimeError("adam rule needs gnu")
 
 
-def _muon_core(q, k, v, beta, g, gmu, ns):
-    """The muon rule's mixer core.  msign couples every entry of the d x d
-    state, so the recurrence runs as the drop-in scan's muon kernel (one
-    workgroup per (b, h), Newton-Schulz fused into the scan step); phases 1
-    and 3 of the reference mixer (train_ablation.py:150-167, :184-187) are
-    plain batched GEMMs in float32 around it.  Autograd supplies the
-    backward, through the scan kernel's fused msign VJP."""
+def _composed_core(q, k, v, beta, g, gmu, gnu, rule, ns, precision=None):
+    """The mixer core as the reference composes it: phases 1 and 3
+    (train_ablation.py:150-167, :184-187) as plain batched GEMMs in float32
+    around the drop-in scan kernels, with autograd supplying the backward
+    through the scan's own backward kernels.
+
+    Muon always runs this way: msign couples every entry of the d x d state,
+    so the recurrence runs as the drop-in scan's muon kernel (one workgroup
+    per (b, h), Newton-Schulz fused into the scan step, msign VJP fused into
+    its reverse scan).  Adam at d = 128 trains this way with the scan in
+    exact float32 (precision 'ieee'), where the fused kernels' split products
+    would exceed the gradient tolerance."""
     B, H, T, d = q.shape
     N = T // CHUNK
     qf, kf, vf = (t.float().reshape(B, H, N, CHUNK, d) for t in (q, k, v))
@@ -99,9 +111,13 @@ def _muon_core(q, k, v, beta, g, gmu, ns):
     a = lg.sum(-1).exp()
     b = bt.mean(-1)
     m = lmu.sum(-1).exp()
-    n = torch.ones_like(m)
-    # token weights prod_{s' > s} mu_{s'} (train_ablation.py:154-156)
-    w = torch.exp(torch.flip(torch.cumsum(torch.flip(lmu, [-1]), -1), [-1]) - lmu)
+    if rule == 2:
+        n = torch.clamp(gnu.float(), min=LOG_FLOOR).reshape(B, H, N, CHUNK).sum(-1).exp()
+        w = torch.ones_like(bt)  # adam weighs every token of a chunk equally (train_ablation.py:158)
+    else:
+        n = torch.ones_like(m)
+        # token weights prod_{s' > s} mu_{s'} (train_ablation.py:154-156)
+        w = torch.exp(torch.flip(torch.cumsum(torch.flip(lmu, [-1]), -1), [-1]) - lmu)
     causal = torch.tril(torch.ones(CHUNK, CHUNK, dtype=torch.bool, device=q.device))
     # float32 batched products take the transposed views as they are (strided
     # GEMM operands), so no transposed copy is made of k, the weighted tiles
@@ -111,7 +127,7 @@ def _muon_core(q, k, v, beta, g, gmu, ns):
     Uv = torch.matmul((vf * w.unsqueeze(-1)).transpose(-1, -2), kf)
     Qt = qf - torch.matmul(A, kf)
     Ov = torch.matmul(A, vf)
-    S_all = hip_state_scan(Uv, Kw, a, b, m, n, 1, ns)
+    S_all = hip_state_scan(Uv, Kw, a, b, m, n, rule, ns, precision)
     o = torch.matmul(Qt, S_all.transpose(-1, -2)) + Ov
     return o.reshape(B, H, T, d).to(q.dtype)
 
@@ -121,12 +137,17 @@ def chunk_scan(q, k, v, beta, g, gmu=None, gnu=None, *, rule="delta", ns: int = 
     r = _rule_id(rule)
     if r == 1:
         _check(q, k, v, beta, g, gmu, gnu, r)
-        return _muon_core(q, k, v, beta, g, gmu, ns)
+        return _composed_core(q, k, v, beta, g, gmu, None, 1, ns)
     gmu = gmu if r >= 1 else None
     gnu = gnu if r == 2 else None
     _check(q, k, v, beta, g, gmu, gnu, r)
-    gates = [None if t is None else t.to(torch.float32) for t in (beta, g, gmu, gnu)]
     # the state checkpoint is written only when a backward can follow
     record = torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (q, k, v, beta, g, gmu, gnu))
+    if record and not fused_backward(r, q.shape[-1]):
+        if eps != 1e-6:
+            raise RuntimeError("adam at d = 128 trains through the drop-in scan, whose epsilon is 1e-6 "
+                               f"(fast_scan.py:94); got eps={eps}")
+        return _composed_core(q, k, v, beta, g, gmu, gnu, r, ns, precision="ieee")
+    gates = [None if t is None else t.to(torch.float32) for t in (beta, g, gmu, gnu)]
     o, _ = torch.ops.gmdn.chunk_fwd(q, k, v, *gates, r, ns, eps, record)
     return o

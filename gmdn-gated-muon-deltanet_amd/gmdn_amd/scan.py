@@ -33,7 +33,13 @@ def get_precision() -> str:
 
 
 def _prec_code() -> int:
-    return nat.PREC_TF32 if _state["precision"] == "tf32" else nat.PREC_IEEE
+    return _prec_code_of(_state["precision"])
+
+
+def _prec_code_of(precision: str) -> int:
+    if precision not in ("tf32", "ieee"):
+        raise ValueError(f"precision must be 'tf32' or 'ieee', got {precision!r}")
+    return nat.PREC_TF32 if precision == "tf32" else nat.PREC_IEEE
 
 
 def _check_inputs(U, K, a, b, m, n, rule, ns):
@@ -57,14 +63,16 @@ def _f32(t):
     return t.to(torch.float32).contiguous()
 
 
-def hip_state_scan(U, K, a, b, m, n, rule: int, ns: int):
+def hip_state_scan(U, K, a, b, m, n, rule: int, ns: int, precision: str | None = None):
     """The scan through ``torch.ops.gmdn.state_scan`` and its registered
     autograd: float32 contiguous copies of the inputs (differentiable casts),
-    the pre-update states in U's dtype.  Traceable by ``torch.compile``."""
+    the pre-update states in U's dtype.  Traceable by ``torch.compile``.
+    ``precision`` ('tf32' or 'ieee') overrides the process-wide setting."""
     _check_inputs(U, K, a, b, m, n, rule, ns)
     ins = [_f32(t) for t in (U, K, a, b, m, n)]
     save = torch.is_grad_enabled() and any(t.requires_grad for t in (U, K, a, b, m, n))
-    S_all, _, _ = torch.ops.gmdn.state_scan(*ins, rule, ns, _prec_code(), save)
+    prec = _prec_code() if precision is None else _prec_code_of(precision)
+    S_all, _, _ = torch.ops.gmdn.state_scan(*ins, rule, ns, prec, save)
     return S_all if U.dtype == torch.float32 else S_all.to(U.dtype)
 
 

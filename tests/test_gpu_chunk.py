@@ -198,30 +198,14 @@ def test_adam_grads_small(seed):
     assert all(e <= TOL for e, _ in errs.values()), errs
 
 
-def test_adam_grads_d128_refused():
-    """The adam backward at d = 128 is refused rather than inaccurate."""
+def _adam_grads_vs_f32(w, seed=0):
+    """Adam's gradients against float64 autograd of the oracle, bounded by
+    the float32 evaluation of the same reference algorithm: the HIP path may
+    be no further from float64 than that, in Frobenius norm (with a factor 2
+    for the different rounding), or within 2e-2 of it.  Returns the cases
+    that fail."""
     dev = _dev()
-    w = Workload("t", "adam", 1, 1, 64, 128)
-    inp = make_inputs(w, seed=0, device=dev, with_grad_out=True)
-    xs = {n: (None if inp[n] is None else inp[n].detach().requires_grad_(True)) for n in ALL_INPUTS}
-    o = gc.chunk_scan(*(xs[n] for n in ALL_INPUTS), rule="adam")
-    with pytest.raises(RuntimeError, match="not built"):
-        o.backward(inp["dO"])
-
-
-def test_adam_grads_config():
-    """Adam at B=2, H=8, T=4096, d=64, forward + backward.
-
-    Over 64 chunks adam's gradient is ill-conditioned: elements where V is
-    tiny make M / (sqrt(V) + eps) sign-like, and the float64 gradient has
-    max/RMS ~ 650 on dk.  The reference algorithm evaluated in float32 is
-    then itself ~15 RMS away from float64, so no float32 implementation meets
-    an elementwise 2e-2 bound here.  The check is that the HIP path is no
-    further from float64 than that float32 evaluation is, in Frobenius norm
-    (with a factor 2 for the different rounding), or within 2e-2 of it."""
-    dev = _dev()
-    w = Workload("adam_b2_h8_t4096_d64", "adam", 2, 8, 4096, 64)
-    inp = make_inputs(w, seed=0, with_grad_out=True)
+    inp = make_inputs(w, seed=seed, with_grad_out=True)
     xs = {n: inp[n].to(dev).detach().requires_grad_(True) for n in ALL_INPUTS}
     o = gc.chunk_scan(*(xs[n] for n in ALL_INPUTS), rule="adam")
     got = torch.autograd.grad(o, [xs[n] for n in ALL_INPUTS], inp["dO"].to(dev))
@@ -239,6 +223,33 @@ def test_adam_grads_config():
         print(f"{w.name} d{n}: frobenius rel error {e_hip:.2e} (float32 reference {e_f32:.2e})")
         if e_hip > max(TOL, 2.0 * e_f32):
             bad[n] = (e_hip, e_f32)
+    return bad
+
+
+@pytest.mark.parametrize("seed", [1, 2])
+def test_adam_grads_d128(seed):
+    """Adam at d = 128 trains through the composed path (float32 batched
+    GEMMs around the drop-in scan in exact float32), since the fused
+    kernels' split products exceed the gradient tolerance there.  Its
+    sign-like update makes dk and dv ill-conditioned already at T = 256 (the
+    bf16 rounding of the float64 gradient alone is 0.11 and 0.15 of RMS), so
+    the gradients are bounded as in the full-size adam case."""
+    assert not gc.fused_backward("adam", 128) and gc.backward_supported("adam", 128)
+    bad = _adam_grads_vs_f32(Workload("t", "adam", 1, 2, 256, 128), seed=seed)
+    assert not bad, bad
+
+
+def test_adam_grads_config():
+    """Adam at B=2, H=8, T=4096, d=64, forward + backward.
+
+    Over 64 chunks adam's gradient is ill-conditioned: elements where V is
+    tiny make M / (sqrt(V) + eps) sign-like, and the float64 gradient has
+    max/RMS ~ 650 on dk.  The reference algorithm evaluated in float32 is
+    then itself ~15 RMS away from float64, so no float32 implementation meets
+    an elementwise 2e-2 bound here.  The check is that the HIP path is no
+    further from float64 than that float32 evaluation is, in Frobenius norm
+    (with a factor 2 for the different rounding), or within 2e-2 of it."""
+    bad = _adam_grads_vs_f32(Workload("adam_b2_h8_t4096_d64", "adam", 2, 8, 4096, 64))
     assert not bad, bad
 
 
