@@ -220,26 +220,44 @@ def lm_line(args) -> dict:
     """The 12-layer GMDN stack (d_model 1024, 8 heads x 128, muon inner rule,
     ns = 3 -- the trainer's default, train_ablation.py:556-558), vocab 32000,
     B = 8, T = 2048, bf16 weights from the reference's N(0, 0.02) init,
-    token ids uniform over the vocabulary, next-token cross entropy; one step
-    is forward + backward (no optimiser).  End-to-end tokens/s only: the
-    step is mostly library GEMMs and the muon core, so no single roofline
-    applies."""
+    token ids uniform over the vocabulary, next-token cross entropy.  One
+    step is the trainer's (train_ablation.py:458-474): forward, backward,
+    gradient clipping at norm 1, then the outer Muon step on the hidden 2-D
+    weights and AdamW on the rest (build_optimizers, :291-307, with the
+    trainer's default rates).  The forward + backward alone and the
+    inference forward are reported beside it.  End-to-end tokens/s only: the
+    step is mostly library GEMMs, the muon core and the outer msign, so no
+    single roofline applies."""
+    import types
+
     import torch
     from gmdn_amd.mixer import LM
+    from gmdn_amd.muon import build_optimizers
 
     B, T, vocab, d_model, layers, heads, ns = 8, 2048, 32000, 1024, 12, 8, 3
     dev = torch.device("cuda:0")
     torch.manual_seed(0)
     model = LM(vocab, d_model, layers, heads, "muon", ns_steps=ns).to(dev, torch.bfloat16)
+    opts = build_optimizers(model, "muon", types.SimpleNamespace(muon_lr=0.02, adam_lr=4e-4, weight_decay=0.1))
     gen = torch.Generator(device=dev).manual_seed(0)
     idx = torch.randint(0, vocab, (B, T + 1), device=dev, generator=gen)
     stream = torch.cuda.current_stream(dev)
 
-    def step():
+    def fwd_bwd():
         _, loss = model(idx[:, :-1], idx[:, 1:])
         loss.backward()
         for p in model.parameters():
             p.grad = None
+        return loss
+
+    def train_step():
+        for opt in opts:
+            opt.zero_grad(set_to_none=True)
+        _, loss = model(idx[:, :-1], idx[:, 1:])
+        loss.backward()
+        torch.nn.utils.clip_grad_norm_(model.parameters(), 1.0)
+        for opt in opts:
+            opt.step()
         return loss
 
     def timed(fn, steps, warmup):
@@ -256,7 +274,8 @@ def lm_line(args) -> dict:
         return (time.perf_counter() - t0) / steps, statistics.mean(e[0].elapsed_time(e[1]) for e in evs) / 1e3
 
     steps, warmup = min(args.steps, 10), max(args.warmup, 1)
-    wall, ev = timed(step, steps, warmup)
+    wall, ev = timed(train_step, steps, warmup)
+    _, fb_ev = timed(fwd_bwd, steps, warmup)
     with torch.no_grad():
         _, fwd_ev = timed(lambda: model(idx[:, :-1]), steps, warmup)
     tokens = B * T
@@ -266,9 +285,11 @@ def lm_line(args) -> dict:
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
         "config": {"workload": LM_WORKLOAD, "layers": layers, "d_model": d_model, "heads": heads,
                    "head_dim": d_model // heads, "rule": "muon", "ns": ns, "B": B, "T": T, "vocab": vocab,
-                   "pass": "fwd+bwd", "global_batch": B, "seq_len": T, "parallelism": "none"},
-        "fwd_tokens_per_s": tokens / fwd_ev, "fwd_bwd_tokens_per_s": tokens / ev,
-        "step_us": {"fwd_bwd": ev * 1e6, "fwd_inference": fwd_ev * 1e6},
+                   "pass": "fwd+bwd+clip+optimizer (Muon + AdamW)", "global_batch": B, "seq_len": T,
+                   "parallelism": "none"},
+        "train_step_tokens_per_s": tokens / ev, "fwd_tokens_per_s": tokens / fwd_ev,
+        "fwd_bwd_tokens_per_s": tokens / fb_ev,
+        "step_us": {"train_step": ev * 1e6, "fwd_bwd": fb_ev * 1e6, "fwd_inference": fwd_ev * 1e6},
         "roofline": None, "roofline_note": "end-to-end stack: tokens/s only",
         "cpu_baseline": None,
     }
