@@ -7,6 +7,15 @@ Usage, after ``rocprofv3 ... --output-format csv -d DIR -o NAME -- <program>``:
         --fetch DIR1 --write DIR2 --copy-fetch DIR3 --copy-write DIR4 \\
         --copy-bytes N
 
+    python -m gmdn_amd.profiling mfma DIR [--kernel REGEX] [--simds 1024]
+
+``mfma`` reads one PMC pass of SQ_INSTS_VALU_MFMA_MOPS_BF16,
+SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE and gives per kernel (medians
+over its dispatches): the bf16 MFMA flops issued (MOPS x 512), their rate
+over the dispatch's own duration, that rate as a fraction of the 2.5 PFLOP/s
+dense bf16 peak, and MfmaUtil = busy cycles / (one XCD's GUI-active cycles
+x SIMDs), rocprofv3's own definition.
+
 ``traffic`` turns the FETCH_SIZE / WRITE_SIZE derived counters (KiB per
 dispatch) into HBM bytes per launch of the kernels matching REGEX (summed
 over the kernels when the op runs several).  Each
@@ -123,6 +132,48 @@ def read_traffic(path: str):
     return None
 
 
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def mfma_by_kernel(d: str, kernel_regex: str = "", simds: int = 1024, xcds: int = 8):
+    """{kernel: dict(dispatches, flops, us, tflops, frac, util)} from one PMC
+    pass of the three MFMA counters (medians over the kernel's dispatches).
+    rocprofv3 reports GRBM_GUI_ACTIVE summed over the XCDs; MfmaUtil takes
+    one XCD's count (its expression reduces the counter with max)."""
+    pat = re.compile(kernel_regex)
+    disp = {}
+    with open(_find(d, "counter_collection.csv")) as f:
+        for r in csv.DictReader(f):
+            if not pat.search(r["Kernel_Name"]):
+                continue
+            key = (r["Kernel_Name"], r["Dispatch_Id"])
+            e = disp.setdefault(key, {"ns": int(r["End_Timestamp"]) - int(r["Start_Timestamp"])})
+            e[r["Counter_Name"]] = e.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    per = {}
+    for (name, _), e in disp.items():
+        per.setdefault(name, []).append(e)
+    out = {}
+    for name, es in per.items():
+        flops = statistics.median(e.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0.0) * 512 for e in es)
+        ns = statistics.median(e["ns"] for e in es)
+        busy = statistics.median(e.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) for e in es)
+        gui = statistics.median(e.get("GRBM_GUI_ACTIVE", 0.0) for e in es)
+        tflops = flops / ns / 1e3 if ns else 0.0
+        out[name] = {"dispatches": len(es), "flops": flops, "us": ns / 1e3, "tflops": tflops,
+                     "frac": tflops / BF16_PEAK_TFLOPS,
+                     "util": 100.0 * busy / (gui / xcds * simds) if gui else 0.0}
+    return out
+
+
+def _mfma_md(d: str, kernel_regex: str, simds: int, xcds: int) -> str:
+    rows = ["| kernel | dispatches | bf16 MFMA GFLOP issued | us | TFLOP/s | of bf16 peak | MfmaUtil % |",
+            "|---|---|---|---|---|---|---|"]
+    for name, m in sorted(mfma_by_kernel(d, kernel_regex, simds, xcds).items(), key=lambda kv: -kv[1]["flops"]):
+        rows.append(f"| `{name}` | {m['dispatches']} | {m['flops'] / 1e9:.2f} | {m['us']:.1f} | {m['tflops']:.1f} | "
+                    f"{m['frac']:.3f} | {m['util']:.1f} |")
+    return "\n".join(rows)
+
+
 def main(argv=None):
     p = argparse.ArgumentParser(prog="python -m gmdn_amd.profiling")
     sub = p.add_subparsers(dest="cmd", required=True)
@@ -137,8 +188,18 @@ def main(argv=None):
     t.add_argument("--copy-fetch", required=True)
     t.add_argument("--copy-write", required=True)
     t.add_argument("--copy-bytes", type=int, required=True)
+    m = sub.add_parser("mfma")
+    m.add_argument("dir")
+    m.add_argument("--kernel", default="", help="only kernels whose name matches this regex")
+    m.add_argument("--simds", type=int, default=1024, help="SIMDs of the device (MI355X: 256 CUs x 4)")
+    m.add_argument("--xcds", type=int, default=8, help="XCDs whose GRBM_GUI_ACTIVE counts are summed")
     a = p.parse_args(argv)
-    print(_stats_md(a.dir, a.kernel) if a.cmd == "stats" else _traffic_md(a))
+    if a.cmd == "stats":
+        print(_stats_md(a.dir, a.kernel))
+    elif a.cmd == "mfma":
+        print(_mfma_md(a.dir, a.kernel, a.simds, a.xcds))
+    else:
+        print(_traffic_md(a))
 
 
 if __name__ == "__main__":

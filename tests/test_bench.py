@@ -91,3 +91,19 @@ def test_msign_cpu_baseline_runs():
     shapes = [(48, 32), (8, 32), (32, 32), (64, 32), (32, 64)]
     r = bench.msign_cpu_baseline(shapes, 0.1)
     assert r["kind"] == "port" and r["value"] > 0 and r["cores"] >= 1
+
+
+def test_mfma_counter_summary(tmp_path):
+    hdr = ('"Correlation_Id","Dispatch_Id","Agent_Id","Queue_Id","Process_Id","Thread_Id","Grid_Size","Kernel_Id",'
+           '"Kernel_Name","Workgroup_Size","LDS_Block_Size","Scratch_Size","VGPR_Count","Accum_VGPR_Count","SGPR_Count",'
+           '"Counter_Name","Counter_Value","Start_Timestamp","End_Timestamp"\n')
+    rows = []
+    for disp, (mops, busy, gui, ns) in enumerate([(1e6, 512, 1, 1000), (3e6, 1024, 1, 3000), (2e6, 768, 1, 2000)]):
+        for c, v in (("SQ_INSTS_VALU_MFMA_MOPS_BF16", mops), ("SQ_VALU_MFMA_BUSY_CYCLES", busy),
+                     ("GRBM_GUI_ACTIVE", gui)):
+            rows.append(f'1,{disp},"Agent 1",1,1,1,1,1,"kA",256,0,0,1,0,1,"{c}",{v},0,{ns}\n')
+    (tmp_path / "x_counter_collection.csv").write_text(hdr + "".join(rows))
+    m = profiling.mfma_by_kernel(str(tmp_path), "kA", simds=1024, xcds=1)["kA"]
+    # medians: 2e6 MOPS x 512 flops over 2000 ns; 768 busy cycles over 1 GUI cycle x 1024 SIMDs
+    assert m["dispatches"] == 3 and m["flops"] == 2e6 * 512 and m["us"] == 2.0
+    assert abs(m["tflops"] - 512.0) < 1e-9 and abs(m["util"] - 75.0) < 1e-9
