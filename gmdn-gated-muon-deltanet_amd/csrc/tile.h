@@ -110,8 +110,37 @@ template <int COLS>
 struct BSwz {
   static constexpr int GPR = COLS / 8;  // 16-byte groups per row
   static constexpr int MASK = (GPR < 16 ? GPR : 16) - 1;
-  static GMDN_DEV int off(int r, int c) { return r * COLS + ((((c >> 3) ^ (r & MASK)) << 3) | (c & 7)); }
+  static GMDN_DEV int xr(int r) { return r & MASK; }  // the row's XOR pattern
+  static GMDN_DEV int off(int r, int c) { return r * COLS + ((((c >> 3) ^ xr(r)) << 3) | (c & 7)); }
 };
+
+// Row swizzle for tiles read by columns: the 16-byte group q of row r sits
+// at q ^ f(r), with f a bijection of r mod 16.  The transposing column reads
+// touch, per 16 lanes, four consecutive rows x four consecutive groups; under
+// q ^ (r mod 16) the low bits of row and group cancel and those 16 reads land
+// in four groups (a 4-way bank conflict, measured at half of the LDS-active
+// cycles).  Here f moves the row's low two bits above the group's: for
+// 256-byte rows (D = 128) f swaps the two 2-bit halves of r mod 16, giving 16
+// distinct groups; for 128-byte rows (D = 64, two rows per 256-byte bank
+// sweep) f(r) = 4 ((r >> 1) & 1) + ((r >> 2) & 3), giving 16 distinct (bank
+// half, group) pairs.  Row reads and publishes (16 rows, one group) stay
+// conflict-free since f is a bijection.
+template <int COLS>
+struct NSwz {
+  static constexpr int GPR = COLS / 8;  // 16-byte groups per row
+  static constexpr int MASK = 15;       // the pattern repeats every 16 rows
+  static GMDN_DEV int f(int r) {
+    if constexpr (COLS == 128)
+      return ((r & 3) << 2) | ((r >> 2) & 3);
+    else if constexpr (COLS == 64)
+      return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+    else
+      return r & (GPR < 16 ? GPR - 1 : 15);
+  }
+  static GMDN_DEV int xr(int r) { return f(r); }  // the row's XOR pattern
+  static GMDN_DEV int off(int r, int c) { return r * COLS + ((((c >> 3) ^ f(r)) << 3) | (c & 7)); }
+};
+
 
 // Byte offset of element (r, c) of a swizzled bf16 tile (c % 4 == 0 for the
 // 8-byte pieces the kernels read).
@@ -253,7 +282,7 @@ struct DmaPlan {
     for (int k = 0; k < NOPS; ++k) {
       const int p = k * NTHREADS + w * 64 + l;
       const int r = p / L::GPR;
-      const int q = (p % L::GPR) ^ (r & L::MASK);
+      const int q = (p % L::GPR) ^ L::xr(r);
       off[k] = (uint32_t)((r * gstride + q * 8) * 2);
     }
   }
