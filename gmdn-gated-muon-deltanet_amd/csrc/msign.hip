@@ -528,7 +528,7 @@ int gmdn_msign(const void* M, void* out, int64_t batch, int64_t rows, int64_t co
   if (rows > MS_MAXDIM || cols > MS_MAXDIM) return GMDN_ERR_UNSUPPORTED;
   if (!(eps >= 0.f)) return GMDN_ERR_ARG;
   if (batch == 0 || rows == 0 || cols == 0) return GMDN_OK;
-  if (batch > ((int64_t)1 << 24)) return GMDN_ERR_ARG;
+  if (batch > 65535) return GMDN_ERR_ARG;  // the batch is the grid's y dimension
   if (!M || !out) return GMDN_ERR_ARG;
   MsPlan p;
   if (!plan(batch, rows, cols, p)) return GMDN_ERR_ARG;

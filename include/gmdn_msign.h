@@ -37,7 +37,7 @@ size_t gmdn_msign_workspace_bytes(int64_t batch, int64_t rows, int64_t cols);
  * input dtype, as the reference's X.to(dt)); they must not overlap the
  * workspace, which is 256-byte aligned and at least
  * gmdn_msign_workspace_bytes(batch, rows, cols) long (GMDN_ERR_WORKSPACE
- * otherwise).  rows, cols <= 32768; steps in [0, 64]. */
+ * otherwise).  batch <= 65535; rows, cols <= 32768; steps in [0, 64]. */
 int gmdn_msign(const void* M, void* out, int64_t batch, int64_t rows, int64_t cols, int32_t steps, float eps,
                int32_t dtype, void* workspace, size_t workspace_bytes, void* stream);
 

@@ -119,7 +119,7 @@ def test_msign_workspace_and_argument_validation():
     def call(M=p, out=p, batch=2, rows=8, cols=8, steps=5, eps=1e-7, dtype=1, ws=0x100000, wsb=1 << 30):
         return lib.gmdn_msign(M, out, batch, rows, cols, steps, eps, dtype, ws, wsb, None)
 
-    assert call(batch=-1) == 1
+    assert call(batch=-1) == 1 and call(batch=65536) == 1
     assert call(steps=-1) == 1 and call(steps=65) == 1
     assert call(eps=float("nan")) == 1 and call(eps=-1.0) == 1
     assert call(dtype=7) == 2
