@@ -84,22 +84,23 @@ def test_msign_lm_shapes(rows, cols):
     assert torch.equal(alone[0], got[2])
 
 
-def test_muon_optimizer_matches_oracle():
+@pytest.mark.parametrize("nesterov,wd", [(True, 0.1), (False, 0.0)])
+def test_muon_optimizer_matches_oracle(nesterov, wd):
     from gmdn_amd.muon import Muon
     g = torch.Generator().manual_seed(8)
     shapes = [(64, 96), (96, 64), (32, 32), (32, 32), (24, 128)]
     init = [torch.randn(*s, generator=g) * 0.02 for s in shapes]
     grads = [[torch.randn(*s, generator=g) for s in shapes] for _ in range(3)]
     params = [torch.nn.Parameter(p.clone().to(DEV)) for p in init]
-    opt = Muon(params, lr=0.02, momentum=0.95, nesterov=True, weight_decay=0.1, ns_steps=5)
+    opt = Muon(params, lr=0.02, momentum=0.95, nesterov=nesterov, weight_decay=wd, ns_steps=5)
     ref = [p.clone().double() for p in init]
     bufs = [None] * len(shapes)
     for step in range(3):
         for p, gr in zip(params, grads[step]):
             p.grad = gr.to(DEV)
         opt.step()
-        bufs = om.muon_step(ref, [gr.double() for gr in grads[step]], bufs, lr=0.02, momentum=0.95, nesterov=True,
-                            weight_decay=0.1, ns_steps=5, compute_dtype=torch.float64)
+        bufs = om.muon_step(ref, [gr.double() for gr in grads[step]], bufs, lr=0.02, momentum=0.95, nesterov=nesterov,
+                            weight_decay=wd, ns_steps=5, compute_dtype=torch.float64)
     for i, (p, r, p0) in enumerate(zip(params, ref, init)):
         upd, upd_ref = p.detach().cpu().double() - p0.double(), r - p0.double()
         assert rel_err(upd, upd_ref) <= 1e-4
