@@ -23,7 +23,7 @@ ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 
 # Packed fp32 ops are disabled: hipcc -O3 forms v_pk_{add,mul,fma}_f32 on its
-# own, and this build keeps to scalar fp32 VALU for the state arithmetic.
+# own, and the library keeps to scalar fp32 VALU for the state arithmetic.
 # MFMA results stay in arch VGPRs (no v_accvgpr moves before the VALU work
 # on them: the scan kernels pack every product into the next operand).
 COMMON_FLAGS = [

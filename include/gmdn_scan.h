@@ -54,8 +54,8 @@ extern "C" {
 const char* gmdn_error_string(int code);
 
 /* Supported head dims of the Level-A kernels (the reference dispatches its
- * kernels for power-of-two dh >= 16, fast_scan.py:406-408; this build has
- * 32, 64 and 128).  Returns 1 if dh is supported, else 0. */
+ * kernels for power-of-two dh >= 16, fast_scan.py:406-408; this library
+ * has 32, 64 and 128).  Returns 1 if dh is supported, else 0. */
 int gmdn_scan_supported(int32_t dh);
 
 /* ------------------------------------------------------------------ Level A */

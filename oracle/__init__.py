@@ -2,8 +2,9 @@
 
 TEST INFRASTRUCTURE ONLY.  Nothing in the shipped package imports this
 directory; only ``tests/``, ``__graft_entry__.smoke()`` and the
-``cpu_baseline`` leg of ``bench.py`` use it, and only as the checker (or, in
-the bench, as the timed CPU baseline), never as a product path.
+``cpu_baseline`` leg of ``bench.py`` use it, and only as the reference the
+kernels are compared with (or, in the bench, as the timed CPU baseline),
+never as a product path.
 
 The oracle restates the reference algorithm in PyTorch on the CPU (any float
 dtype; tests use float64 for tight checks and float32 for the reference's own
