@@ -228,20 +228,25 @@ struct NSSplit {
       lds_st<bf16x4>(m + (dst + q * RSTEP * ROWB + PLANE), lo);
     }
   }
-  // the wave's rows 16 w .. 16 w + 15 (D-layout tiles t of M^T) -> planes at m
+  // the wave's rows 16 w .. 16 w + 15 (D-layout tiles t of M^T) -> planes at m.
+  // In the stored block order a lane's columns of tiles 2k and 2k+1 are
+  // adjacent (blocks G and 4+G of a 32-column group sit at 8G and 8G+4), so
+  // each pair leaves as one 16-byte store per plane.
   GMDN_DEV void publish(lds_ptr m, const f32x4 (&t)[NT]) const {
 #pragma unroll
-    for (int c = 0; c < NT; ++c) {
-      bf16x4 hi, lo;
+    for (int c = 0; c < NT; c += 2) {
+      bf16x8 hi, lo;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        bf16 h_, l_;
-        split2(t[c][j], h_, l_);
-        hi[j] = h_;
-        lo[j] = l_;
-      }
-      lds_st<bf16x4>(m + ppub[c], hi);
-      lds_st<bf16x4>(m + (ppub[c] + PLANE), lo);
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          bf16 h_, l_;
+          split2(t[c + h][j], h_, l_);
+          hi[4 * h + j] = h_;
+          lo[4 * h + j] = l_;
+        }
+      lds_st<bf16x8>(m + ppub[c], hi);
+      lds_st<bf16x8>(m + (ppub[c] + PLANE), lo);
     }
   }
   // lane (r, G) takes M[16 tr + r][32 kb + pair(G, s)]
