@@ -5,6 +5,7 @@
 #include "scan_a.h"
 #include "chunk_b.h"
 
+
 using namespace gmdn;
 
 namespace {
@@ -55,6 +56,12 @@ int gmdn_scan_fwd(const float* U, const float* K, const float* a, const float* b
   s.U = U; s.K = K; s.a = a; s.b = b; s.m = m; s.n = n;
   s.S_all = S_all; s.M_all = M_all; s.V_all = V_all;
   s.BH = BH; s.N = N; s.dh = dh; s.rule = rule; s.ns = ns; s.precision = precision;
+  // adam's backward amplifies the rounding of the moments it is handed:
+  // with split-bf16 products in the forward, dK is 0.29 (Frobenius) from
+  // float64 at BH = 64, N = 64, dh = 128 where exact float32 products give
+  // 3e-3.  When the moments are kept for a backward, the forward runs in
+  // exact float32.
+  if (rule == 2 && (M_all || V_all)) s.precision = GMDN_PREC_IEEE;
   s.stream = (hipStream_t)stream;
   return launch_status(rule == 1 ? scan_fwd_muon_launch(s) : scan_fwd_rows_launch(s));
 }

@@ -613,9 +613,13 @@ int gmdn_chunk_bwd(const gmdn_chunk_desc* desc, const void* q, const void* k, co
   if (desc->rule == 2 && desc->d != 64) return GMDN_ERR_UNSUPPORTED;
   if (desc->B * desc->H * (desc->T / CB_C) >= ((int64_t)1 << 31)) return GMDN_ERR_ARG;  // one workgroup per chunk
   if (!workspace || workspace_bytes < gmdn_chunk_bwd_workspace_bytes(desc)) return GMDN_ERR_WORKSPACE;
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dO) || !aligned16(dv) ||
-      !aligned16(beta) || !aligned16(g) || !aligned16(states) || !aligned16(workspace))
+  // dO tiles arrive by 16-byte LDS-DMA loads and dq, dk, dv leave in 16-byte
+  // row pieces: every stream needs 16-byte aligned rows
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dO) || !aligned16(dq) ||
+      !aligned16(dk) || !aligned16(dv) || !aligned16(beta) || !aligned16(g) || !aligned16(states) ||
+      !aligned16(workspace) || (gmu && !aligned16(gmu)) || (gnu && !aligned16(gnu)))
     return GMDN_ERR_UNSUPPORTED;
+  if ((desc->so[0] & 7) || (desc->so[1] & 7) || (desc->so[2] & 7)) return GMDN_ERR_UNSUPPORTED;
   ChunkArgs a = make_args(desc, q, k, v, beta, g, gmu, gnu, const_cast<void*>(dO),
                           const_cast<void*>(states));
   a.gb = (float*)workspace;

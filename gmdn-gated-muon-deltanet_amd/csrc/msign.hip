@@ -35,7 +35,7 @@ namespace {
 constexpr int MS_TILE = 128;                // output tile edge; padding unit
 constexpr int MS_KB = 32;                   // contraction per ring stage
 constexpr int MS_THREADS = 256;             // 4 waves as 2 x 2 blocks of 64 x 64
-constexpr int MS_STAGES = 3;
+constexpr int MS_STAGES = 2;
 constexpr int MS_NPART = 64;                // norm partial sums per matrix
 constexpr int MS_MAXDIM = 32768;
 constexpr float NS_A = 3.4445f, NS_B = -4.7750f, NS_C = 2.0315f;  // train_ablation.py:66

@@ -15,14 +15,17 @@ mirrors reference ``fast_scan.py``:
 * ``HAS_TRITON`` -- True when the native library is loadable (the flag
   callers test before requesting the kernel backend, reference :36-41).
 * ``_TritonScan`` -- the autograd op, here the HIP one (reference :334-396).
-* ``scan_eager``, ``manual_backward``, ``NS_A/NS_B/NS_C``, ``_EPS_NORM``,
-  ``_EPS_ADAM`` (reference :32-34, :59-186).
+* ``scan_eager``, ``manual_backward``, ``_msign_sq``, ``_msign_vjp``,
+  ``_ns_step``, ``NS_A/NS_B/NS_C``, ``_EPS_NORM``, ``_EPS_ADAM`` (reference
+  :32-34, :59-186), written here around a carried state tuple per rule.
 
 Differences from the reference, on purpose:
 
-* A GPU tensor never silently takes the eager path: if the native library
-  is missing, or dh is not one of the built sizes (32, 64, 128), the call
-  raises ``RuntimeError`` unless the backend was set to 'eager' explicitly.
+* A GPU tensor never silently takes the eager path because the native
+  library is missing: that raises ``RuntimeError`` unless the backend was
+  set to 'eager' explicitly.  Head dims without kernels run eagerly under
+  'auto' and raise under 'triton', as the reference dispatches (:403-414);
+  the kernels cover 32, 64 and 128, and 16 by zero-padding to 32.
 * gfx950 has no TF32 MFMA; 'tf32' maps to bf16x3 split products (more
   accurate than TF32) and 'ieee' to fp32 MFMA.
 * Gradients of gates the rule does not use are zeros (the reference's Triton
@@ -65,129 +68,170 @@ def set_backend(name: str):
 
 
 # ---------------------------------------------------------------------------
-# Eager implementation (CPU tensors, or backend 'eager')
+# Eager implementation (CPU tensors, backend 'eager', head dims without kernels)
+#
+# The scan carries per (b, h) a state tuple through the chunks: (S,) for
+# delta, (S, M) for muon, (S, M, V) for adam.  ``_advance`` applies one
+# chunk's update to the tuple; ``manual_backward`` walks the chunks in
+# reverse, carrying the cotangents of the same tuple, with ``_retreat`` the
+# VJP of one chunk's update.  Gates are viewed once as (B, H, N, 1, 1).
 # ---------------------------------------------------------------------------
 
+def _gate_views(*gates):
+    return [g[..., None, None] for g in gates]
+
+
 def _ns_step(X):
-    P = X @ X.mT
-    return NS_A * X + (NS_B * P + NS_C * (P @ P)) @ X
+    """One quintic Newton-Schulz step X -> a X + b (P X) + c P (P X), P = X X^T."""
+    PX = (X @ X.mT) @ X
+    return NS_A * X + NS_B * PX + NS_C * ((X @ X.mT) @ PX)
+
+
+def _normalise(M):
+    """M / (||M||_F + eps) and the norm itself."""
+    nf = torch.linalg.matrix_norm(M)[..., None, None]
+    return M / (nf + _EPS_NORM), nf
 
 
 def _msign_sq(M: torch.Tensor, ns: int) -> torch.Tensor:
-    """Frobenius-normalised quintic Newton-Schulz for square matrices."""
-    X = M / (M.norm(dim=(-2, -1), keepdim=True) + _EPS_NORM)
+    """Frobenius-normalised quintic Newton-Schulz of square matrices."""
+    X, _ = _normalise(M)
     for _ in range(ns):
         X = _ns_step(X)
     return X
 
 
+def _advance(rule, ns, carry, G, ai, bi, mi, ni):
+    """One chunk's update of the carried (S[, M[, V]]) given G = U - S K."""
+    S = carry[0]
+    if rule == 0:
+        return (ai * S + G,)
+    if rule == 1:
+        M = mi * carry[1] + G
+        return (ai * S + bi * _msign_sq(M, ns), M)
+    M = torch.lerp(G, carry[1], mi)            # m M + (1 - m) G
+    V = torch.lerp(G * G, carry[2], ni)        # n V + (1 - n) G^2
+    return (ai * S + bi * (M / (V.sqrt() + _EPS_ADAM)), M, V)
+
+
 def scan_eager(U, K, a, b, m, n, rule: int, ns: int) -> torch.Tensor:
-    """Pre-update state stack by a Python loop over chunks; autograd
-    differentiates it.  U, K: (B, H, N, dh, dh); a, b, m, n: (B, H, N)."""
-    B, H, N, dh, _ = U.shape
-    S = U.new_zeros(B, H, dh, dh)
-    M = torch.zeros_like(S)
-    V = torch.zeros_like(S)
-    out = []
+    """Stack of pre-update states (B, H, N, dh, dh) by a loop over chunks;
+    autograd differentiates it.  U, K: (B, H, N, dh, dh); a, b, m, n: (B, H, N)."""
+    Bn, Hn, N, dh, _ = U.shape
+    zero = U.new_zeros(Bn, Hn, dh, dh)
+    carry = (zero,) if rule == 0 else (zero, zero) if rule == 1 else (zero, zero, zero)
+    av, bv, mv, nv = _gate_views(a, b, m, n)
+    pre = []
     for i in range(N):
-        out.append(S)
-        G = U[:, :, i] - S @ K[:, :, i]
-        ai = a[:, :, i, None, None]
-        if rule == 0:
-            S = ai * S + G
-        elif rule == 1:
-            M = m[:, :, i, None, None] * M + G
-            S = ai * S + b[:, :, i, None, None] * _msign_sq(M, ns)
-        else:
-            mi, ni = m[:, :, i, None, None], n[:, :, i, None, None]
-            M = mi * M + (1 - mi) * G
-            V = ni * V + (1 - ni) * G * G
-            S = ai * S + b[:, :, i, None, None] * M / (V.sqrt() + _EPS_ADAM)
-    return torch.stack(out, dim=2)
+        pre.append(carry[0])
+        G = U.select(2, i) - carry[0] @ K.select(2, i)
+        carry = _advance(rule, ns, carry, G, av.select(2, i), bv.select(2, i), mv.select(2, i),
+                         nv.select(2, i))
+    if N == 0:
+        return U.new_zeros(U.shape)
+    return torch.stack(pre, dim=2)
 
 
 def _msign_vjp(Mi, Ybar, ns: int):
-    """VJP of msign with the iterates kept from one forward pass."""
-    nf = Mi.norm(dim=(-2, -1), keepdim=True)
-    nrm = nf + _EPS_NORM
-    X = Mi / nrm
-    its = []
-    for _ in range(ns):
-        its.append(X)
-        X = _ns_step(X)
+    """Cotangent of M for Y = msign(M), given Ybar.  The iterates X_0..X_{ns-1}
+    are kept from one forward pass.  Per step, with P = X X^T and
+    Z = b P + c P^2, the cotangent Xbar of X' = a X + Z X becomes
+        Bs = Xbar X^T + X Xbar^T,  Y = P Bs,
+        Xbar <- a Xbar + Z Xbar + (b Bs + c (Y + Y^T)) X.
+    Normalisation X_0 = M / n, n = ||M|| + eps:
+        Mbar = (Xbar_0 - <Xbar_0, X_0> M / ||M||) / n."""
+    X, nf = _normalise(Mi)
+    iterates = [X]
+    for _ in range(ns - 1):
+        iterates.append(_ns_step(iterates[-1]))
     Xbar = Ybar
-    for Xk in reversed(its):
+    for Xk in (reversed(iterates) if ns > 0 else ()):
         P = Xk @ Xk.mT
-        Bm = NS_B * P + NS_C * (P @ P)
-        Bbar = Xbar @ Xk.mT
-        Abar = NS_B * Bbar + NS_C * (Bbar @ P + P @ Bbar)
-        Xbar = NS_A * Xbar + Bm @ Xbar + (Abar + Abar.mT) @ Xk
-    dot = (Xbar * Mi).sum(dim=(-2, -1), keepdim=True)
-    return Xbar / nrm - dot / nrm.square() * (Mi / nf.clamp_min(1e-12))
+        Z = NS_B * P + NS_C * (P @ P)
+        Bs = Xbar @ Xk.mT
+        Bs = Bs + Bs.mT
+        Y = P @ Bs
+        Xbar = NS_A * Xbar + Z @ Xbar + (NS_B * Bs + NS_C * (Y + Y.mT)) @ Xk
+    X0 = iterates[0]
+    proj = (Xbar * X0).sum(dim=(-2, -1), keepdim=True)
+    return (Xbar - proj * Mi / nf.clamp_min(1e-12)) / (nf + _EPS_NORM)
+
+
+def _retreat(rule, ns, Sbar, carry_bar, G, M_prev, V_prev, bi, mi, ni):
+    """VJP of one chunk's update except the a S term: from the cotangent
+    Sbar of S_{i+1} and the carried cotangents of M_{i+1} (and V_{i+1}),
+    returns (Gbar, dbeta, dmu, dnu, cotangents of M_i[, V_i])."""
+    zero = Sbar.new_zeros(Sbar.shape[:-2])
+    if rule == 0:
+        return Sbar, zero, zero, zero, ()
+    if rule == 1:
+        M = mi * M_prev + G
+        Y = _msign_sq(M, ns)
+        Mtot = carry_bar[0] + _msign_vjp(M, bi * Sbar, ns)
+        return (Mtot, (Sbar * Y).sum(dim=(-2, -1)), (Mtot * M_prev).sum(dim=(-2, -1)), zero,
+                (mi * Mtot,))
+    M = torch.lerp(G, M_prev, mi)
+    V = torch.lerp(G * G, V_prev, ni)
+    root = V.sqrt()
+    inv = 1.0 / (root + _EPS_ADAM)
+    ubar = bi * Sbar
+    Mtot = carry_bar[0] + ubar * inv
+    Vtot = carry_bar[1] - 0.5 * ubar * M * inv * inv / root.clamp_min(1e-12)
+    Gbar = (1 - mi) * Mtot + 2 * (1 - ni) * G * Vtot
+    return (Gbar, (Sbar * M * inv).sum(dim=(-2, -1)), (Mtot * (M_prev - G)).sum(dim=(-2, -1)),
+            (Vtot * (V_prev - G * G)).sum(dim=(-2, -1)), (mi * Mtot, ni * Vtot))
 
 
 def manual_backward(U, K, a, b, m, n, S_all, M_all, V_all, gS, rule: int, ns: int):
-    """Hand-derived reverse scan in PyTorch; returns dU, dK, da, db, dm, dn."""
-    B, H, N, dh, _ = U.shape
-    dU, dK = torch.zeros_like(U), torch.zeros_like(K)
-    da, db, dm, dn = (torch.zeros_like(t) for t in (a, b, m, n))
-    Sb = U.new_zeros(B, H, dh, dh)
-    Mb, Vb = torch.zeros_like(Sb), torch.zeros_like(Sb)
-    for i in reversed(range(N)):
-        S, Ki = S_all[:, :, i], K[:, :, i]
-        ai, bi, mi = (t[:, :, i, None, None] for t in (a, b, m))
-        G = U[:, :, i] - S @ Ki
-        da[:, :, i] = (Sb * S).sum(dim=(-2, -1))
-        if rule == 0:
-            Gb = Sb
-        elif rule == 1:
-            Mp = M_all[:, :, i]
-            Mi = mi * Mp + G
-            db[:, :, i] = (Sb * _msign_sq(Mi, ns)).sum(dim=(-2, -1))
-            Mtot = Mb + _msign_vjp(Mi, bi * Sb, ns)
-            dm[:, :, i] = (Mtot * Mp).sum(dim=(-2, -1))
-            Mb = mi * Mtot
-            Gb = Mtot
-        else:
-            ni = n[:, :, i, None, None]
-            Mp, Vp = M_all[:, :, i], V_all[:, :, i]
-            Mi = mi * Mp + (1 - mi) * G
-            Vi = ni * Vp + (1 - ni) * G * G
-            root = Vi.sqrt()
-            den = root + _EPS_ADAM
-            db[:, :, i] = (Sb * Mi / den).sum(dim=(-2, -1))
-            ub = bi * Sb
-            Mtot = Mb + ub / den
-            Vtot = Vb - ub * Mi / den.square() / (2 * root.clamp_min(1e-12))
-            dm[:, :, i] = (Mtot * (Mp - G)).sum(dim=(-2, -1))
-            dn[:, :, i] = (Vtot * (Vp - G * G)).sum(dim=(-2, -1))
-            Mb, Vb = mi * Mtot, ni * Vtot
-            Gb = (1 - mi) * Mtot + (1 - ni) * 2 * G * Vtot
-        dU[:, :, i] = Gb
-        dK[:, :, i] = -S.mT @ Gb
-        Sb = ai * Sb - Gb @ Ki.mT + gS[:, :, i]
-    return dU, dK, da, db, dm, dn
+    """Hand-derived reverse scan: returns dU, dK, da, db, dm, dn.  S_all,
+    M_all, V_all hold the pre-update values of every chunk."""
+    N = U.shape[2]
+    grads = {name: torch.zeros_like(t) for name, t in (("U", U), ("K", K), ("a", a), ("b", b), ("m", m),
+                                                       ("n", n))}
+    if N == 0:
+        return tuple(grads[k] for k in ("U", "K", "a", "b", "m", "n"))
+    av, bv, mv, nv = _gate_views(a, b, m, n)
+    Sbar = torch.zeros_like(U.select(2, 0))
+    carry_bar = () if rule == 0 else (torch.zeros_like(Sbar),) if rule == 1 else (torch.zeros_like(Sbar),) * 2
+    for i in range(N - 1, -1, -1):
+        S, Ki = S_all.select(2, i), K.select(2, i)
+        G = U.select(2, i) - S @ Ki
+        M_prev = M_all.select(2, i) if rule else None
+        V_prev = V_all.select(2, i) if rule == 2 else None
+        Gbar, dbi, dmi, dni, carry_bar = _retreat(rule, ns, Sbar, carry_bar, G, M_prev, V_prev, bv.select(2, i),
+                                                  mv.select(2, i), nv.select(2, i))
+        grads["a"][:, :, i] = (Sbar * S).sum(dim=(-2, -1))
+        grads["b"][:, :, i], grads["m"][:, :, i], grads["n"][:, :, i] = dbi, dmi, dni
+        grads["U"][:, :, i] = Gbar
+        grads["K"][:, :, i] = -(S.mT @ Gbar)
+        Sbar = av.select(2, i) * Sbar - Gbar @ Ki.mT + gS.select(2, i)
+    return tuple(grads[k] for k in ("U", "K", "a", "b", "m", "n"))
 
 
 # ---------------------------------------------------------------------------
-# Dispatcher
+# Dispatcher (reference fast_scan.py:403-414)
 # ---------------------------------------------------------------------------
 
 def fast_state_scan(U, K, a, b, m, n, rule: int, ns: int) -> torch.Tensor:
-    """Pre-update state stack (B, H, N, dh, dh).  GPU tensors run the HIP
-    kernels (backend 'auto' or 'triton'); CPU tensors run scan_eager unless
-    the native backend was forced, which raises."""
+    """Pre-update state stack (B, H, N, dh, dh).
+
+    * backend 'eager': ``scan_eager``.
+    * GPU tensors whose head dim has kernels (16, 32, 64, 128): the HIP
+      kernels.  A GPU tensor never runs eagerly because the native library
+      is missing: that raises.
+    * otherwise (CPU tensors, other head dims): ``scan_eager`` under 'auto';
+      under 'triton' (the native backend forced) a ``RuntimeError``, as the
+      reference raises when its kernel cannot run.
+    """
     if _BACKEND == "eager":
         return scan_eager(U, K, a, b, m, n, rule, ns)
-    if U.is_cuda:
-        if not HAS_NATIVE:
-            raise RuntimeError("GPU tensors need the native gmdn kernels, but libgmdn_scan.so "
-                               "is not built; build it or set_backend('eager') explicitly")
-        if U.shape[-1] not in SUPPORTED_DH:
-            raise RuntimeError(f"native scan supports head dims {SUPPORTED_DH}, got {U.shape[-1]}; "
-                               "set_backend('eager') to run this size eagerly")
+    if U.is_cuda and not HAS_NATIVE:
+        raise RuntimeError("GPU tensors need the native gmdn kernels, but libgmdn_scan.so "
+                           "is not built; build it or set_backend('eager') explicitly")
+    if U.is_cuda and U.shape[-1] in SUPPORTED_DH:
         return hip_state_scan(U, K, a, b, m, n, rule, ns)
     if _BACKEND == "triton":
-        raise RuntimeError("native backend requested but unavailable for CPU tensors "
-                           "(needs GPU tensors and libgmdn_scan.so)")
+        raise RuntimeError("native backend requested but unavailable (needs GPU tensors, libgmdn_scan.so "
+                           f"and a head dim in {SUPPORTED_DH}; got dh={U.shape[-1]}, "
+                           f"device {U.device})")
     return scan_eager(U, K, a, b, m, n, rule, ns)

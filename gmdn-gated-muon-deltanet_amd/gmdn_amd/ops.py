@@ -141,6 +141,16 @@ def _tok(t: Tensor) -> Tensor:
     return t
 
 
+def _check_tokens(*ts: Tensor) -> None:
+    """The fused core reads and writes bf16 token streams only (the C ABI's
+    dtype is fixed to bfloat16 by ``chunk_desc``)."""
+    for t in ts:
+        if t.dtype != torch.bfloat16:
+            raise RuntimeError(f"gmdn::chunk_fwd / chunk_bwd take bfloat16 q, k, v, got {t.dtype}")
+        if t.dim() != 4:
+            raise RuntimeError(f"token streams are (B, H, T, d), got shape {tuple(t.shape)}")
+
+
 def _gate(t: Optional[Tensor]) -> Optional[Tensor]:
     """float32 (B, H, T) gate stream, contiguous and 16-byte aligned."""
     if t is None:
@@ -158,6 +168,7 @@ def _states_numel(q: Tensor, rule: int, ns: int, eps: float) -> int:
 def chunk_fwd(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, g: Tensor, gmu: Optional[Tensor],
               gnu: Optional[Tensor], rule: int, ns: int, eps: float, record: bool) -> tuple[Tensor, Tensor]:
     lib = nat.load()
+    _check_tokens(q, k, v)
     qc, kc, vc = _tok(q), _tok(k), _tok(v)
     bc, gc, mc, nc = _gate(beta), _gate(g), _gate(gmu), _gate(gnu)
     o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
@@ -184,6 +195,7 @@ def chunk_bwd(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, g: Tensor, gmu: Opt
               gnu: Optional[Tensor], states: Tensor, dO: Tensor, rule: int, ns: int,
               eps: float) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
     lib = nat.load()
+    _check_tokens(q, k, v)
     qc, kc, vc = _tok(q), _tok(k), _tok(v)
     bc, gc, mc, nc = _gate(beta), _gate(g), _gate(gmu), _gate(gnu)
     dOc = _tok(dO.to(torch.bfloat16))
@@ -203,15 +215,29 @@ def chunk_bwd(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, g: Tensor, gmu: Opt
                                 nat.ptr(dgnu) if nc is not None else None,
                                 nat.ptr(ws), ws_bytes, nat.stream_of(q))
     nat.check(rc, "gmdn_chunk_bwd")
+    # the fake implementation cannot see data pointers: a stream that _tok
+    # copied only for its alignment gets its gradient back in the strides the
+    # fake reports
+    dq, dk, dv = (_as_strided_like(d_, t) for d_, t in ((dq, q), (dk, k), (dv, v)))
     return dq, dk, dv, dbeta, dg, dgmu, dgnu
 
 
 def _kernel_strides(t: Tensor):
-    """The strides ``_tok`` leaves a token stream with (it copies a stream
-    whose rows are not 16-byte aligned; a fake tensor is taken as aligned)."""
+    """The strides of the gradient of token stream ``t``: its own when they
+    suit the kernels (unit-stride d, B/H/T strides in multiples of 8
+    elements), else contiguous.  Alignment of the data pointer does not
+    enter, so the real and fake implementations agree."""
     if t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:3]):
         return t.new_empty(t.shape).stride()
     return t.stride()
+
+
+def _as_strided_like(x: Tensor, t: Tensor) -> Tensor:
+    """``x`` laid out with ``_kernel_strides(t)`` (a copy only when they differ)."""
+    want = _kernel_strides(t)
+    if x.stride() == want:
+        return x
+    return torch.empty_strided(x.shape, want, dtype=x.dtype, device=x.device).copy_(x)
 
 
 @chunk_bwd.register_fake

@@ -17,8 +17,22 @@ import torch
 from . import _native as nat
 from . import ops  # noqa: F401  -- registers torch.ops.gmdn.*
 
-SUPPORTED_DH = (32, 64, 128)
+KERNEL_DH = (32, 64, 128)       # head dims the kernels are built for
+SUPPORTED_DH = (16,) + KERNEL_DH  # 16: zero-padded to 32 on the way in
 _state = {"precision": "tf32"}
+
+
+def _padded_dh(dh: int) -> int:
+    """Kernel head dim that serves ``dh``.  Zero-padding U and K to 32 x 32
+    is exact for every rule: the padded state, moments, Newton-Schulz
+    iterates and gradients stay block-diagonal with the dh x dh problem in
+    the leading block (rows and columns past dh are identically zero)."""
+    return 32 if dh < 32 else dh
+
+
+def _pad_sq(x, d: int):
+    p = d - x.shape[-1]
+    return x if p == 0 else torch.nn.functional.pad(x, (0, p, 0, p))
 
 
 def set_precision(name: str) -> None:
@@ -69,10 +83,14 @@ def hip_state_scan(U, K, a, b, m, n, rule: int, ns: int, precision: str | None =
     the pre-update states in U's dtype.  Traceable by ``torch.compile``.
     ``precision`` ('tf32' or 'ieee') overrides the process-wide setting."""
     _check_inputs(U, K, a, b, m, n, rule, ns)
-    ins = [_f32(t) for t in (U, K, a, b, m, n)]
+    dh = U.shape[-1]
+    kd = _padded_dh(dh)
+    ins = [_f32(t) for t in (_pad_sq(U, kd), _pad_sq(K, kd), a, b, m, n)]
     save = torch.is_grad_enabled() and any(t.requires_grad for t in (U, K, a, b, m, n))
     prec = _prec_code() if precision is None else _prec_code_of(precision)
     S_all, _, _ = torch.ops.gmdn.state_scan(*ins, rule, ns, prec, save)
+    if kd != dh:
+        S_all = S_all[..., :dh, :dh]
     return S_all if U.dtype == torch.float32 else S_all.to(U.dtype)
 
 
@@ -82,16 +100,24 @@ class HipScan(torch.autograd.Function):
     @staticmethod
     def forward(ctx, U, K, a, b, m, n, rule, ns):
         _check_inputs(U, K, a, b, m, n, rule, ns)
-        ins = [_f32(t.detach()) for t in (U, K, a, b, m, n)]
+        dh = U.shape[-1]
+        kd = _padded_dh(dh)
+        ins = [_f32(t.detach()) for t in (_pad_sq(U, kd), _pad_sq(K, kd), a, b, m, n)]
         prec = _prec_code()
         S_all, M_all, V_all = torch.ops.gmdn.state_scan(*ins, rule, ns, prec, any(ctx.needs_input_grad[:6]))
         ctx.save_for_backward(*ins, S_all, M_all, V_all)
-        ctx.rule, ctx.ns, ctx.prec = rule, ns, prec
+        ctx.rule, ctx.ns, ctx.prec, ctx.dh = rule, ns, prec, dh
         ctx.dtypes = tuple(t.dtype for t in (U, K, a, b, m, n))
+        if kd != dh:
+            S_all = S_all[..., :dh, :dh]
         return S_all if U.dtype == torch.float32 else S_all.to(U.dtype)
 
     @staticmethod
     def backward(ctx, gS):
-        grads = torch.ops.gmdn.state_scan_bwd(*ctx.saved_tensors, gS, ctx.rule, ctx.ns, ctx.prec)
+        kd = ctx.saved_tensors[0].shape[-1]
+        grads = torch.ops.gmdn.state_scan_bwd(*ctx.saved_tensors, _pad_sq(gS.float(), kd), ctx.rule, ctx.ns,
+                                              ctx.prec)
+        dh = ctx.dh
+        grads = [g[..., :dh, :dh] if i < 2 and kd != dh else g for i, g in enumerate(grads)]
         grads = [g if g.dtype == dt else g.to(dt) for g, dt in zip(grads, ctx.dtypes)]
         return (*grads, None, None)

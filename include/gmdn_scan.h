@@ -55,7 +55,9 @@ const char* gmdn_error_string(int code);
 
 /* Supported head dims of the Level-A kernels (the reference dispatches its
  * kernels for power-of-two dh >= 16, fast_scan.py:406-408; this library
- * has 32, 64 and 128).  Returns 1 if dh is supported, else 0. */
+ * has 32, 64 and 128, and the Python host serves dh = 16 by zero-padding
+ * U and K to 32, which is exact for every rule).  Returns 1 if dh is
+ * supported, else 0. */
 int gmdn_scan_supported(int32_t dh);
 
 /* ------------------------------------------------------------------ Level A */
@@ -71,6 +73,9 @@ int gmdn_scan_supported(int32_t dh);
  *
  * M_all (rules 1, 2) and V_all (rule 2) receive the pre-update moments that
  * gmdn_scan_bwd needs; either may be NULL when no backward will follow.
+ * Adam with M_all or V_all requested runs in exact float32 (GMDN_PREC_IEEE)
+ * whatever `precision` says: its backward amplifies the rounding of the
+ * saved moments past the gradient tolerance under split-bf16 products.
  * ns: Newton-Schulz steps for rule 1 (0..8).  b, m, n may be NULL for rule 0;
  * n may be NULL for rule 1. */
 int gmdn_scan_fwd(const float* U, const float* K, const float* a, const float* b,

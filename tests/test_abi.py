@@ -129,3 +129,37 @@ def test_msign_workspace_and_argument_validation():
     assert call(wsb=16) == 3
     assert call(ws=0x100010) == 3  # workspace not 256-byte aligned
     assert call(batch=0) == 0 and call(rows=0) == 0  # empty: nothing to do, nothing launched
+
+
+def _chunk_desc(rule=0, d=64, T=128, so=None):
+    desc = _native.ChunkDesc()
+    desc.B, desc.H, desc.T, desc.d, desc.C = 1, 2, T, d, 64
+    desc.rule, desc.ns, desc.dtype, desc.eps = rule, 3, _native.DTYPE_BF16, 1e-6
+    st = (2 * T * d, T * d, d)
+    for name in ("sq", "sk", "sv", "so"):
+        arr = getattr(desc, name)
+        for i in range(3):
+            arr[i] = (so if (name == "so" and so is not None) else st)[i]
+    return desc
+
+
+def test_chunk_bwd_rejects_misaligned_streams():
+    """dO tiles are LDS-DMA loads planned from its strides, dq and dk leave in
+    16-byte pieces: unaligned strides or pointers are refused with
+    GMDN_ERR_UNSUPPORTED before anything is launched."""
+    lib = _native.load()
+    p, ws = 0x1000, 0x100000
+
+    def call(desc, dq=p, dk=p, dv=p, dO=p):
+        need = lib.gmdn_chunk_bwd_workspace_bytes(desc)
+        return lib.gmdn_chunk_bwd(desc, p, p, p, p, p, None, None, p, dO, dq, dk, dv, p, p, None, None, ws,
+                                  need, None)
+
+    good = _chunk_desc()
+    assert lib.gmdn_chunk_bwd_workspace_bytes(good) > 0
+    assert call(_chunk_desc(so=(2 * 128 * 64, 128 * 64, 68))) == 2   # dO token stride not 8 elements
+    assert call(_chunk_desc(so=(2 * 128 * 64 + 4, 128 * 64, 64))) == 2  # dO batch stride
+    assert call(good, dq=p + 2) == 2
+    assert call(good, dk=p + 8) == 2
+    assert call(good, dv=p + 4) == 2
+    assert call(good, dO=p + 2) == 2

@@ -66,3 +66,38 @@ def test_manual_backward_matches_oracle(rule):
     ref = osc.scan_backward(*ins, S_all, M_all, V_all, gS, rule, 3)
     for a, b in zip(mine, ref):
         assert torch.allclose(a, b, atol=1e-12)
+
+
+@pytest.mark.parametrize("rule,ns", [(0, 3), (1, 0), (1, 1), (1, 5), (2, 3)])
+def test_manual_backward_matches_autograd_of_scan_eager(rule, ns):
+    """The hand-derived reverse scan against torch.autograd through the
+    module's own eager forward (two derivations of the same VJP)."""
+    gen = torch.Generator().manual_seed(7)
+    ins = [t.double().requires_grad_(True) for t in osc.make_scan_inputs(1, 2, 4, 16, 8, generator=gen)]
+    S = fast_scan.scan_eager(*ins, rule, ns)
+    gS = torch.randn(S.shape, generator=gen, dtype=torch.float64)
+    auto = torch.autograd.grad(S, ins, gS, allow_unused=True)
+    auto = [torch.zeros_like(t) if g is None else g for g, t in zip(auto, ins)]
+    _, M_all, V_all = osc.scan_forward(*[t.detach() for t in ins], rule, ns, return_moments=True)
+    mine = fast_scan.manual_backward(*[t.detach() for t in ins], S.detach(), M_all, V_all, gS, rule, ns)
+    for name, a, b in zip("U K a b m n".split(), mine, auto):
+        assert torch.allclose(a, b, atol=1e-10, rtol=1e-9), name
+
+
+def test_eager_msign_matches_svd_closed_form():
+    """_msign_sq against the SVD form P p^{ns}(sigma / (|M|_F + eps)) R^T."""
+    gen = torch.Generator().manual_seed(3)
+    M = torch.randn(3, 8, 8, generator=gen, dtype=torch.float64)
+    for ns in (0, 1, 3, 5):
+        X = fast_scan._msign_sq(M, ns)
+        for j in range(3):
+            ref = torch.from_numpy(osc.msign_svd(M[j].numpy(), ns))
+            assert torch.allclose(X[j], ref, atol=1e-10)
+
+
+def test_empty_sequence():
+    ins = osc.make_scan_inputs(1, 2, 0, 16, 8)
+    for rule in (0, 1, 2):
+        assert fast_scan.scan_eager(*ins, rule, 3).shape == (1, 2, 0, 8, 8)
+        grads = fast_scan.manual_backward(*ins, *(torch.zeros(1, 2, 0, 8, 8),) * 4, rule, 3)
+        assert [tuple(g.shape) for g in grads] == [tuple(t.shape) for t in ins]

@@ -25,7 +25,7 @@ from gmdn_amd.mixer import LM, FastWeightMixer
 from oracle import chunk as oc
 
 pytestmark = pytest.mark.gpu
-CASES = [("delta", 256), ("muon", 256), ("adam", 128)]
+CASES = [("delta", 256, 2), ("muon", 256, 2), ("adam", 128, 2), ("muon", 1024, 8)]
 
 
 def _dev():
@@ -49,19 +49,21 @@ def _reference_front_end(m: FastWeightMixer, x: torch.Tensor):
     return q, k, v, g[1], logs[0], logs[2], logs[3] if m.n_gates == 4 else None
 
 
-def _layer(inner, d_model, dev):
+def _layer(inner, d_model, dev, heads=2):
     torch.manual_seed(0)
-    ref = FastWeightMixer(d_model, 2, inner, ns_steps=3)
+    ref = FastWeightMixer(d_model, heads, inner, ns_steps=3)
     with torch.no_grad():  # weights off the zero-bias init
         for p in ref.parameters():
             p.add_(0.02 * torch.randn_like(p))
     return ref, copy.deepcopy(ref).to(dev)
 
 
-@pytest.mark.parametrize("inner,d_model", CASES)
-def test_mixer_parts_match_reference(inner, d_model):
+@pytest.mark.parametrize("inner,d_model,heads", CASES)
+def test_mixer_parts_match_reference(inner, d_model, heads):
+    """Layer parts at d_model 256 / 128 with two heads, and at the LM's
+    layer shape (d_model 1024, 8 heads x 128, muon, ns = 3) on one batch row."""
     dev = _dev()
-    ref, mine = _layer(inner, d_model, dev)
+    ref, mine = _layer(inner, d_model, dev, heads)
     x = torch.randn(1, 256, d_model)
     with torch.no_grad():
         want = _reference_front_end(ref, x)
@@ -90,10 +92,10 @@ def test_mixer_parts_match_reference(inner, d_model):
         torch.testing.assert_close(y, y_tail, rtol=1e-4, atol=1e-5)
 
 
-@pytest.mark.parametrize("inner,d_model", CASES)
-def test_mixer_backward_reaches_every_parameter(inner, d_model):
+@pytest.mark.parametrize("inner,d_model,heads", CASES)
+def test_mixer_backward_reaches_every_parameter(inner, d_model, heads):
     dev = _dev()
-    _, mine = _layer(inner, d_model, dev)
+    _, mine = _layer(inner, d_model, dev, heads)
     x = torch.randn(1, 256, d_model, device=dev, requires_grad=True)
     mine(x).square().mean().backward()
     assert torch.isfinite(x.grad).all() and x.grad.abs().max() > 0
@@ -114,3 +116,26 @@ def test_lm_step_bf16():
     loss.backward()
     for name, p in model.named_parameters():
         assert p.grad is not None and torch.isfinite(p.grad).all(), name
+
+
+def test_lm_full_size_step():
+    """The 12-layer LM at its benchmark size: d_model 1024, 8 heads x 128,
+    muon inner rule with ns = 3, vocab 32000, B = 8, T = 2048, bf16 weights
+    from the reference's N(0, 0.02) init (train_ablation.py:212-246), token
+    ids uniform over the vocabulary.  The next-token loss at init is within
+    0.5 of ln 32000, and the backward reaches every parameter with finite,
+    non-zero gradients."""
+    dev = _dev()
+    torch.manual_seed(0)
+    vocab, B, T = 32000, 8, 2048
+    model = LM(vocab, 1024, 12, 8, "muon", ns_steps=3).to(dev, torch.bfloat16)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    idx = torch.randint(0, vocab, (B, T + 1), device=dev, generator=gen)
+    _, loss = model(idx[:, :-1], idx[:, 1:])
+    print(f"LM 12L d1024 B8 T2048: loss at init {loss.item():.4f} (ln 32000 = {math.log(vocab):.4f})")
+    assert abs(loss.item() - math.log(vocab)) < 0.5
+    loss.backward()
+    for name, p in model.named_parameters():
+        assert p.grad is not None, name
+        assert torch.isfinite(p.grad).all(), name
+        assert p.grad.abs().max() > 0, name

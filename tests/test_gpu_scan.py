@@ -152,3 +152,111 @@ def test_scan_unused_gate_grads_are_zero():
                 assert torch.count_nonzero(grads[i]).item() == 0
     finally:
         fast_scan.set_backend("auto")
+
+
+def _frob_errs(rule, ns, precision, B, H, N, dh, seed):
+    """Frobenius-relative errors of the HIP path and of the float32 oracle
+    against float64 (the bar of ill-conditioned cases: long adam and muon
+    sequences, where max-based errors of any float32 evaluation grow)."""
+    import fast_scan
+    dev = _dev()
+    fast_scan.set_backend("triton")
+    fast_scan.set_precision(precision)
+    try:
+        gen = torch.Generator().manual_seed(seed)
+        ins = osc.make_scan_inputs(B, H, N, 64, dh, generator=gen)
+        gS = torch.randn(B, H, N, dh, dh, generator=gen, dtype=torch.float64)
+        S64, g64 = _oracle(ins, gS, rule, ns, torch.float64)
+        S32, g32 = _oracle(ins, gS, rule, ns, torch.float32)
+        ins_d = [t.to(dev).requires_grad_(True) for t in ins]
+        S = fast_scan.fast_state_scan(*ins_d, rule, ns)
+        grads = torch.autograd.grad(S, ins_d, gS.float().to(dev))
+    finally:
+        fast_scan.set_backend("auto")
+        fast_scan.set_precision("tf32")
+    out = {}
+    for name, got, r64, r32 in zip(NAMES, [S.detach()] + list(grads), [S64] + g64, [S32] + g32):
+        nrm = r64.norm().item()
+        if nrm == 0:
+            out[name] = (got.abs().max().item(), 0.0)
+            continue
+        out[name] = ((got.double().cpu() - r64).norm().item() / nrm, (r32.double() - r64).norm().item() / nrm)
+    print(f"rule={rule} ns={ns} {precision} B{B} H{H} N{N} d{dh}: "
+          + " ".join(f"{k}={v[0]:.1e}(f32 {v[1]:.1e})" for k, v in out.items()))
+    return out
+
+
+@pytest.mark.parametrize("precision", ["ieee", "tf32"])
+@pytest.mark.parametrize("rule", [0, 2])
+def test_scan_bench_shape(rule, precision):
+    """The drop-in leg of bench.py's default line: B=4, H=16, N=64, d=128
+    (delta and adam, forward and all gradients).  Delta keeps the elementwise
+    bars of the short cases; adam's sign-like update over 64 chunks makes
+    max-based errors of any float32 evaluation grow, so it is bounded in
+    Frobenius norm by twice the float32 oracle's own error (or 1e-4 for
+    'ieee', 1e-2 for 'tf32')."""
+    if rule == 0:
+        mine, floor = _run(rule, 3, precision, 4, 16, 64, 128, seed=4)
+        _report(f"bench shape rule={rule} {precision}", mine, floor)
+        bad = _check(mine, floor, rule, precision)
+        assert not bad, bad
+        return
+    errs = _frob_errs(rule, 3, precision, 4, 16, 64, 128, seed=4)
+    tol = 1e-4 if precision == "ieee" else 1e-2
+    bad = {k: v for k, v in errs.items() if not v[0] <= max(tol, 2 * v[1])}
+    assert not bad, bad
+
+
+@pytest.mark.parametrize("precision", ["ieee", "tf32"])
+def test_scan_muon_long_sequence(precision):
+    """Muon forward and backward over N = 128 chunks at d = 128, ns = 5 (the
+    sequence length of the muon workload B=2, H=16, T=8192): the serial
+    msign VJP kernel and the chunk-parallel iterate kernel over a long
+    reverse scan.  The float32 oracle itself is 1.1e-5 (states) to 1.7e-4
+    (gradients) from float64 in Frobenius norm here, above the 1e-4 bar, and
+    another float32 evaluation with its own summation order lands about as
+    far again (measured 2.1x for the fp32 MFMA kernels).  Bounded by three
+    times the float32 oracle's error, or 1e-4 ('ieee') / 1e-2 ('tf32')."""
+    errs = _frob_errs(1, 5, precision, 1, 2, 128, 128, seed=5)
+    tol = 1e-4 if precision == "ieee" else 1e-2
+    bad = {k: v for k, v in errs.items() if not v[0] <= max(tol, 3 * v[1])}
+    assert not bad, bad
+
+
+def test_dispatcher_head_dims():
+    """dh = 16 runs the HIP kernels (zero-padded to 32; the eager path is
+    disabled for the call); dh = 48 has no kernels: 'auto' returns the eager
+    result on the GPU tensors, a forced native backend raises (reference
+    fast_scan.py:403-414)."""
+    import fast_scan
+    dev = _dev()
+    gen = torch.Generator().manual_seed(6)
+    real_eager = fast_scan.scan_eager
+
+    def no_eager(*a, **k):
+        raise AssertionError("eager path taken")
+
+    for rule in (0, 1, 2):
+        ins = osc.make_scan_inputs(2, 2, 5, 64, 16, generator=gen)
+        gS = torch.randn(2, 2, 5, 16, 16, generator=gen, dtype=torch.float64)
+        S64, g64 = _oracle(ins, gS, rule, 3, torch.float64)
+        xs = [t.to(dev).requires_grad_(True) for t in ins]
+        fast_scan.scan_eager = no_eager
+        try:
+            S = fast_scan.fast_state_scan(*xs, rule, 3)
+            grads = torch.autograd.grad(S, xs, gS.float().to(dev))
+        finally:
+            fast_scan.scan_eager = real_eager
+        errs = _errs(S.detach().cpu(), [g.cpu() for g in grads], S64, g64)
+        print(f"dh=16 rule={rule}: " + " ".join(f"{k}={v:.1e}" for k, v in errs.items()))
+        assert all(v <= TF32_TOL[rule] for v in errs.values()), errs
+
+    ins = [t.to(dev) for t in osc.make_scan_inputs(1, 2, 3, 64, 48, generator=gen)]
+    S = fast_scan.fast_state_scan(*ins, 0, 3)
+    assert torch.allclose(S, fast_scan.scan_eager(*ins, 0, 3))
+    fast_scan.set_backend("triton")
+    try:
+        with pytest.raises(RuntimeError):
+            fast_scan.fast_state_scan(*ins, 0, 3)
+    finally:
+        fast_scan.set_backend("auto")

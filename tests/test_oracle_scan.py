@@ -131,6 +131,68 @@ def test_muon_zero_momentum_is_msign_of_chunk_gradient():
     assert np.allclose(S[0, 0, 1].numpy(), 0.5 * osc.msign_svd(U[0, 0, 0].numpy(), 5), atol=1e-10)
 
 
+def _diag_scalar_scan(u, k, a, b, m, n, rule, ns):
+    """Closed form of the scan on diagonal U_i, K_i: every matrix stays
+    diagonal, so each diagonal entry follows its own scalar recurrence, and
+    msign of a diagonal matrix D is diag(sign(d) p^ns(|d| / (|d|_2 + eps)))
+    (its SVD is the entries' magnitudes).  u, k: (N, dh) numpy; a..n: (N,)."""
+    ca, cb, cc = osc.NS_COEFFS
+    N, dh = u.shape
+    s, mm, vv = np.zeros(dh), np.zeros(dh), np.zeros(dh)
+    out = []
+    for i in range(N):
+        out.append(s.copy())
+        g = u[i] - s * k[i]
+        if rule == 0:
+            s = a[i] * s + g
+        elif rule == 1:
+            mm = m[i] * mm + g
+            x = np.abs(mm) / (np.sqrt((mm ** 2).sum()) + osc.EPS_NORM)
+            for _ in range(ns):
+                x = ca * x + cb * x ** 3 + cc * x ** 5
+            s = a[i] * s + b[i] * np.sign(mm) * x
+        else:
+            mm = m[i] * mm + (1 - m[i]) * g
+            vv = n[i] * vv + (1 - n[i]) * g * g
+            s = a[i] * s + b[i] * mm / (np.sqrt(vv) + osc.EPS_ADAM)
+    return np.stack(out)
+
+
+@pytest.mark.parametrize("rule,ns", [(0, 0), (1, 1), (1, 3), (1, 5), (2, 0)])
+def test_diagonal_inputs_reduce_to_scalar_recurrences(rule, ns):
+    """Diagonal U_i, K_i with momentum gates m far from 0 (0.3 .. 0.95) and
+    signs of U mixed, so the momentum and moment recurrences change both the
+    relative sizes and the signs of the entries that msign / the adam ratio
+    see: pins the m != 0 recurrences of muon and adam in closed form."""
+    gen = torch.Generator().manual_seed(11)
+    N, dh = 7, 6
+    u = torch.randn(N, dh, generator=gen, dtype=D64).numpy()
+    k = (0.5 * torch.rand(N, dh, generator=gen, dtype=D64)).numpy()
+    a, b, m, n = (0.3 + 0.65 * torch.rand(N, generator=gen, dtype=D64) for _ in range(4))
+    U = torch.diag_embed(torch.from_numpy(u))[None, None]
+    K = torch.diag_embed(torch.from_numpy(k))[None, None]
+    S = osc.scan_forward(U, K, a[None, None], b[None, None], m[None, None], n[None, None], rule, ns)[0, 0]
+    want = _diag_scalar_scan(u, k, a.numpy(), b.numpy(), m.numpy(), n.numpy(), rule, ns)
+    assert np.allclose(torch.diagonal(S, dim1=-2, dim2=-1).numpy(), want, atol=1e-12)
+    off = S - torch.diag_embed(torch.diagonal(S, dim1=-2, dim2=-1))
+    assert off.abs().max().item() == 0.0
+
+
+def test_diagonal_pin_catches_dropped_muon_momentum(monkeypatch):
+    """Plant m = 0 in the oracle's muon update: the diagonal closed form must
+    reject it."""
+    gen = torch.Generator().manual_seed(12)
+    N, dh = 6, 5
+    u = torch.randn(N, dh, generator=gen, dtype=D64).numpy()
+    k = np.zeros((N, dh))
+    a, b, m, n = (0.5 + 0.4 * torch.rand(N, generator=gen, dtype=D64) for _ in range(4))
+    U = torch.diag_embed(torch.from_numpy(u))[None, None]
+    K = torch.zeros_like(U)
+    want = _diag_scalar_scan(u, k, a.numpy(), b.numpy(), m.numpy(), n.numpy(), 1, 3)
+    S = osc.scan_forward(U, K, a[None, None], b[None, None], torch.zeros_like(m)[None, None], n[None, None], 1, 3)
+    assert not np.allclose(torch.diagonal(S[0, 0], dim1=-2, dim2=-1).numpy(), want, atol=1e-6)
+
+
 @pytest.mark.parametrize("rule,ns", [(0, 0), (1, 0), (1, 2), (1, 3), (2, 0)])
 def test_manual_backward_equals_autograd(rule, ns):
     """Two derivations of the VJP: the hand reverse scan (fast_scan.py:134-186)
