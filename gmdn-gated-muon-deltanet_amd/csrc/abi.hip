@@ -5,8 +5,17 @@
 #include "scan_a.h"
 #include "chunk_b.h"
 
+#include <mutex>
 
 using namespace gmdn;
+
+// Scratch of gmdn_scan_bwd_noalloc: the backward's workspace (adam's
+// partial sums, muon's iterates) in a file-scope device array, one copy per
+// GPU, held until the process ends.  Host code never passes `scratch` itself
+// to a kernel (in host code the name is a stand-in, not a device address):
+// it uses the address hipGetSymbolAddress returns for the current device.
+static_assert(GMDN_NOALLOC_SCRATCH_BYTES % 256 == 0, "scratch size");
+static __device__ __align__(256) char scratch[GMDN_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -26,6 +35,25 @@ int check_scan_common(const float* U, const float* K, const float* a, const floa
   if (!U || !K || !a) return GMDN_ERR_ARG;
   if (rule >= 1 && (!b || !m)) return GMDN_ERR_ARG;
   if (rule == 2 && !n) return GMDN_ERR_ARG;
+  return GMDN_OK;
+}
+
+constexpr int MAX_DEVICES = 64;
+std::mutex scratch_mu;
+void* scratch_ptr[MAX_DEVICES] = {};
+
+// The device address of the current device's scratch (looked up once per
+// device, with that device current); GMDN_ERR_LAUNCH when the runtime fails.
+int scratch_of_current_device(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return GMDN_ERR_LAUNCH;
+  std::lock_guard<std::mutex> g(scratch_mu);
+  if (!scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return GMDN_ERR_LAUNCH;
+    scratch_ptr[dev] = p;
+  }
+  *out = scratch_ptr[dev];
   return GMDN_OK;
 }
 
@@ -101,6 +129,21 @@ int gmdn_scan_bwd(const float* U, const float* K, const float* a, const float* b
   }
   if (e != hipSuccess) return GMDN_ERR_LAUNCH;
   return launch_status(scan_bwd_dk_launch(s, part));
+}
+
+int gmdn_scan_bwd_noalloc(const float* U, const float* K, const float* a, const float* b,
+                          const float* m, const float* n, const float* S_all, const float* M_all,
+                          const float* V_all, const float* gS, float* dU, float* dK, float* da,
+                          float* db, float* dm, float* dn, int64_t BH, int64_t N, int32_t dh,
+                          int32_t rule, int32_t ns, int32_t precision, void* stream) {
+  int rc = check_scan_common(U, K, a, b, m, n, BH, N, dh, rule, ns, precision);
+  if (rc != GMDN_OK || BH * N == 0) return rc;
+  if (gmdn_scan_bwd_workspace_bytes(BH, N, dh, rule, ns) > GMDN_NOALLOC_SCRATCH_BYTES) return GMDN_ERR_WORKSPACE;
+  void* ws = nullptr;
+  rc = scratch_of_current_device(&ws);
+  if (rc != GMDN_OK) return rc;
+  return gmdn_scan_bwd(U, K, a, b, m, n, S_all, M_all, V_all, gS, dU, dK, da, db, dm, dn, ws,
+                       GMDN_NOALLOC_SCRATCH_BYTES, BH, N, dh, rule, ns, precision, stream);
 }
 
 }  // extern "C"

@@ -49,6 +49,7 @@ SIGNATURES = {
     "gmdn_scan_fwd": (c_i32, [c_f32p] * 9 + [c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_vp]),
     "gmdn_scan_bwd_workspace_bytes": (c_size, [c_i64, c_i64, c_i32, c_i32, c_i32]),
     "gmdn_scan_bwd": (c_i32, [c_f32p] * 16 + [c_vp, c_size, c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_vp]),
+    "gmdn_scan_bwd_noalloc": (c_i32, [c_f32p] * 16 + [c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_vp]),
     "gmdn_chunk_states_bytes": (c_size, [ctypes.POINTER(ChunkDesc)]),
     "gmdn_chunk_fwd": (c_i32, [ctypes.POINTER(ChunkDesc)] + [c_vp] * 10),
     "gmdn_chunk_bwd_workspace_bytes": (c_size, [ctypes.POINTER(ChunkDesc)]),

@@ -106,6 +106,28 @@ int gmdn_scan_bwd(const float* U, const float* K, const float* a, const float* b
                   int32_t dh, int32_t rule, int32_t ns, int32_t precision,
                   void* stream);
 
+/* Size of the library's own device scratch for gmdn_scan_bwd_noalloc. */
+#define GMDN_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+
+/* gmdn_scan_bwd without a workspace argument.  No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * workspace lives in a file-scope device array of GMDN_NOALLOC_SCRATCH_BYTES
+ * (64 MiB), one per GPU the library runs on, held until the process ends;
+ * the call allocates nothing.  Problems whose workspace
+ * (gmdn_scan_bwd_workspace_bytes) exceeds that size are refused with
+ * GMDN_ERR_WORKSPACE before any launch.  Every call on one GPU shares that
+ * GPU's scratch: calls that overlap on one GPU (other streams, other host
+ * threads) race and must be serialised by the caller.  Nothing a previous
+ * call left in the scratch is read.  Same arguments, results and error codes
+ * as gmdn_scan_bwd otherwise. */
+int gmdn_scan_bwd_noalloc(const float* U, const float* K, const float* a, const float* b,
+                          const float* m, const float* n, const float* S_all,
+                          const float* M_all, const float* V_all, const float* gS,
+                          float* dU, float* dK, float* da, float* db, float* dm, float* dn,
+                          int64_t BH, int64_t N, int32_t dh, int32_t rule, int32_t ns,
+                          int32_t precision, void* stream);
+
 /* ------------------------------------------------------------------ Level B */
 
 /* Problem description of the fused chunk op (phases 1-3 of the reference
