@@ -22,6 +22,15 @@ grid (fp32 d x d inputs per chunk), forward and forward + backward, with its
 own roofline.  ``cpu_baseline`` times the CPU restatement of the reference matrix form
 (float32, torch on the host cores) on the same workload.
 
+``configs`` (default workload only; ``--no-configs`` skips it) holds one
+sub-object per other configuration: the muon rule at B=2, H=16, T=8192,
+d=128, ns=5 and the adam rule at B=2, H=8, T=4096, d=64 (inference forward
+and forward + backward, their rooflines and a CPU baseline on a bounded
+sample), and the 12-layer LM's training step (tokens/s only).  The CPU
+baselines use every CPU of the process's affinity, capped by
+OMP_NUM_THREADS when set, and report the host (lscpu model, sockets,
+physical cores, torch threads).
+
 ``--workload lm_b8_t2048_muon`` times the 12-layer LM stack around the
 fused core end to end (forward + backward, tokens/s only).
 ``--workload outer_muon_lm12_d1024`` times one outer Muon optimizer step
@@ -62,6 +71,8 @@ def parse_args(argv=None):
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-drop-in", action="store_true", help="skip the drop-in scan (fast_state_scan) leg")
     p.add_argument("--fwd-only", action="store_true", help="time the inference forward only")
+    p.add_argument("--no-configs", action="store_true",
+                   help="skip the other configurations' sub-objects (muon, adam, LM) of the default line")
     p.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work (about)")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES")
     return p.parse_args(argv)
@@ -109,7 +120,7 @@ def drop_in_cpu_baseline(w, budget_s: float) -> dict:
     import torch
     from oracle import scan as osc
 
-    threads = max(1, min(len(os.sched_getaffinity(0)), 16))
+    threads = cpu_threads()
     torch.set_num_threads(threads)
     rid = {"delta": 0, "muon": 1, "adam": 2}[w.rule]
     N, d = w.T // w.chunk, w.d
@@ -367,7 +378,7 @@ def msign_cpu_baseline(shapes, budget_s: float) -> dict:
     import torch
     from oracle import muon as om
 
-    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    torch.set_num_threads(cpu_threads())
     layer = shapes[:5]
     flops = sum(msign_flops(*s, 5) for s in layer)
     gen = torch.Generator().manual_seed(0)
@@ -398,17 +409,57 @@ def copy_calibration(nbytes: int) -> None:
     print(json.dumps({"copy_calibration_bytes": nbytes}))
 
 
-def cpu_baseline(w, budget_s: float, with_bwd: bool):
+def cpu_info() -> dict:
+    """The host the CPU baseline ran on: lscpu model, sockets, physical
+    cores, the process's CPU affinity and torch's thread count."""
+    import subprocess
+
+    import torch
+    info = {"affinity_cpus": len(os.sched_getaffinity(0)), "torch_threads": torch.get_num_threads()}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        kv = {}
+        for line in out.splitlines():
+            if ":" in line:
+                k, v = line.split(":", 1)
+                kv[k.strip()] = v.strip()
+        info["model"] = kv.get("Model name")
+        sockets = int(kv.get("Socket(s)", "0") or 0)
+        per = int(kv.get("Core(s) per socket", "0") or 0)
+        info["sockets"] = sockets
+        info["physical_cores"] = sockets * per if sockets and per else None
+    except (OSError, ValueError, subprocess.SubprocessError):
+        info["model"] = None
+    return info
+
+
+def cpu_threads() -> int:
+    """Threads for the CPU baseline: every CPU of the process's affinity,
+    capped by OMP_NUM_THREADS when the environment sets it (the host's CPU
+    share per GPU)."""
+    n = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return max(1, n)
+
+
+def cpu_baseline(w, budget_s: float, with_bwd: bool, max_heads: int | None = None):
     """The CPU restatement of the reference matrix form in float32 (reference
     train_ablation.py:142-187 and fast_scan.py:72-95, autograd for backward),
-    timed on this host's cores over the whole workload."""
+    timed on this host's cores over the whole workload, or over its first
+    ``max_heads`` heads of one batch row scaled to all B * H heads."""
+    import dataclasses
+
     import torch
     from oracle import chunk as oc
     from gmdn_amd.workloads import make_inputs
 
-    threads = max(1, min(len(os.sched_getaffinity(0)), 16))
+    threads = cpu_threads()
     torch.set_num_threads(threads)
-    inp = make_inputs(w, seed=0, dtype=torch.float32, with_grad_out=True)
+    ws = w if max_heads is None else dataclasses.replace(w, B=1, H=min(max_heads, w.H))
+    scale = (w.B * w.H) / (ws.B * ws.H)
+    inp = make_inputs(ws, seed=0, dtype=torch.float32, with_grad_out=True)
     rule = {"delta": 0, "muon": 1, "adam": 2}[w.rule]
     names = ("q", "k", "v", "beta", "g", "gmu", "gnu")
 
@@ -426,10 +477,129 @@ def cpu_baseline(w, budget_s: float, with_bwd: bool):
         times.append(time.perf_counter() - t0)
         if time.perf_counter() - t_all > 3 * budget_s:
             break
-    t = statistics.median(times)
+    t = statistics.median(times) * scale
+    what = (f"whole workload {w.name}" if max_heads is None else
+            f"{ws.H} of {w.B * w.H} heads of {w.name}, scaled to all heads")
     return {"value": w.tokens / t, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"whole workload {w.name} ({'fwd+bwd' if with_bwd else 'fwd'}), float32 matrix form, "
-                      f"median of {len(times)} runs of {t * 1e3:.0f} ms"}
+            "sample": f"{what} ({'fwd+bwd' if with_bwd else 'fwd'}), float32 matrix form, "
+                      f"median of {len(times)} runs ({t * 1e3:.0f} ms for the workload)",
+            "host": cpu_info()}
+
+
+def chunk_leg(w, steps: int, warmup: int, with_bwd: bool) -> dict:
+    """Time the fused mixer core ``chunk_scan`` on workload ``w``: the
+    training step (forward with the state checkpoint, then the backward)
+    when ``with_bwd``, and the inference forward, with HIP events on the
+    launch stream inside the timed regions.  Returns the timings and the
+    roofline objects of the backward (the dominant part of a step) and of
+    the inference forward."""
+    import torch
+    from gmdn_amd import chunk, profiling
+    from gmdn_amd.workloads import make_inputs
+
+    dev = torch.device("cuda:0")
+    inp = make_inputs(w, seed=0, device=dev, with_grad_out=True)
+    names = ("q", "k", "v", "beta", "g", "gmu", "gnu")
+    xs = [inp[n] if inp[n] is None else inp[n].detach().requires_grad_(with_bwd) for n in names]
+    grads_of = [x for x in xs if x is not None]
+    dO = inp["dO"]
+    stream = torch.cuda.current_stream(dev)
+
+    def fwd():
+        return chunk.chunk_scan(*xs, rule=w.rule, ns=w.ns)
+
+    out = {}
+    if with_bwd:
+        def step(ev=None):
+            if ev is not None:
+                ev[0].record(stream)
+            o = fwd()
+            if ev is not None:
+                ev[1].record(stream)
+            torch.autograd.grad(o, grads_of, dO)
+            if ev is not None:
+                ev[2].record(stream)
+
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        evs = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(3)) for _ in range(steps)]
+        t0 = time.perf_counter()
+        for i in range(steps):
+            step(evs[i])
+        torch.cuda.synchronize()
+        out["ms_step"] = (time.perf_counter() - t0) * 1e3 / steps
+        # the forward launch (which also writes the state checkpoint) and the backward
+        out["fwd_train_ms"] = statistics.mean(e[0].elapsed_time(e[1]) for e in evs)
+        out["bwd_ms"] = statistics.mean(e[1].elapsed_time(e[2]) for e in evs)
+
+    # inference forward (no state checkpoint), timed the same way
+    fwd_evs = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(2)) for _ in range(steps)]
+    with torch.no_grad():
+        for _ in range(warmup):
+            fwd()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        for e in fwd_evs:
+            e[0].record(stream)
+            fwd()
+            e[1].record(stream)
+        torch.cuda.synchronize()
+        out["fwd_ms"] = (time.perf_counter() - t1) * 1e3 / steps
+    out["fwd_kernel_ms"] = statistics.mean(e[0].elapsed_time(e[1]) for e in fwd_evs)
+
+    units = w.B * w.H * w.T
+    rid = {"delta": 0, "muon": 1, "adam": 2}[w.rule]
+
+    def roof(kernel, alg_bytes, alg_flops, ms, traffic_file):
+        if w.rule == "muon":
+            bound, ach, peak, unit = "mfma", alg_flops / (ms * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s"
+        else:
+            bound, ach, peak, unit = "hbm", alg_bytes / (ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s"
+        traffic = profiling.read_traffic(os.path.join(ROOT, "profiles", traffic_file))
+        return {"kernel": kernel, "bound": bound, "achieved": ach, "peak": peak, "unit": unit,
+                "frac": ach / peak, "traffic": traffic, "avg_launch_us": ms * 1e3,
+                "alg_bytes": alg_bytes, "alg_flops": alg_flops}
+
+    chunks = w.B * w.H * (w.T // w.chunk)
+    fwd_name = (f"scan_fwd_muon<{w.d}> + phase-1/3 GEMMs" if rid == 1 else f"chunk_fwd<{w.d},{rid}>")
+    out["roofline_fwd"] = roof(fwd_name, fwd_bytes_per_token_head(w) * units,
+                               fwd_flops_per_chunk_head(w) * chunks, out["fwd_kernel_ms"],
+                               f"chunk_fwd_{w.name}_traffic.md")
+    if with_bwd:
+        if rid == 1:
+            bwd_name = f"scan_bwd_muon_x3<{w.d}> + scan_bwd_dk8<{w.d},1> + autograd GEMMs"
+        elif chunk.fused_backward(w.rule, w.d):
+            state_kernel = f"chunk_bwd_dstate<{w.d}>" if rid == 0 else f"chunk_bwd_state<{w.d},{rid}>"
+            bwd_name = f"{state_kernel} + chunk_bwd_tok<{w.d},{rid}>"
+        else:
+            bwd_name = "drop-in scan backward + autograd GEMMs"
+        out["roofline"] = roof(bwd_name, bwd_bytes_per_token_head(w) * units,
+                               bwd_flops_per_chunk_head(w) * chunks, out["bwd_ms"],
+                               f"chunk_bwd_{w.name}_traffic.md")
+    return out
+
+
+def config_leg(name: str, steps: int, warmup: int, cpu_budget: float | None, with_bwd: bool,
+               max_heads: int | None = None) -> dict:
+    """One sub-object of the default line: another configuration of the
+    fused core, its tokens/s, rooflines and (when a budget is given) a CPU
+    baseline on a bounded sample."""
+    from gmdn_amd.workloads import WORKLOADS
+
+    w = WORKLOADS[name]
+    r = chunk_leg(w, steps, warmup, with_bwd)
+    leg = {"workload": name, "rule": w.rule, "B": w.B, "H": w.H, "T": w.T, "d": w.d, "ns": w.ns if w.rule == "muon" else None,
+           "fwd_tokens_per_s": w.tokens / (r["fwd_ms"] * 1e-3),
+           "step_us": {"fwd_inference": r["fwd_kernel_ms"] * 1e3},
+           "roofline_fwd": r["roofline_fwd"]}
+    if with_bwd:
+        leg["fwd_bwd_tokens_per_s"] = w.tokens / (r["ms_step"] * 1e-3)
+        leg["step_us"].update(fwd_with_checkpoint=r["fwd_train_ms"] * 1e3, bwd=r["bwd_ms"] * 1e3)
+        leg["roofline"] = r["roofline"]
+    if cpu_budget:
+        leg["cpu_baseline"] = cpu_baseline(w, cpu_budget, with_bwd, max_heads)
+    return leg
 
 
 def main(argv=None):
@@ -459,92 +629,9 @@ def main(argv=None):
         print(json.dumps(msign_line(args)), flush=True)
         return 0
     w = WORKLOADS[args.workload]
-    dev = torch.device("cuda:0")
-    inp = make_inputs(w, seed=0, device=dev, with_grad_out=True)
-    names = ("q", "k", "v", "beta", "g", "gmu", "gnu")
     with_bwd = chunk.backward_supported(w.rule, w.d) and not args.fwd_only
-    xs = [inp[n] if inp[n] is None else inp[n].detach().requires_grad_(with_bwd) for n in names]
-    grads_of = [x for x in xs if x is not None]
-    dO = inp["dO"]
-    stream = torch.cuda.current_stream(dev)
-
-    def fwd():
-        return chunk.chunk_scan(*xs, rule=w.rule, ns=w.ns)
-
-    def step(ev=None):
-        if ev is not None:
-            ev[0].record(stream)
-        o = fwd()
-        if ev is not None:
-            ev[1].record(stream)
-        if with_bwd:
-            torch.autograd.grad(o, grads_of, dO)
-            if ev is not None:
-                ev[2].record(stream)
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    evs = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(3)) for _ in range(args.steps)]
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(evs[i])
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    ms_step = elapsed * 1e3 / args.steps
-    # HIP events on the launch stream: the forward launch (which also writes the
-    # state checkpoint when a backward follows) and the backward's two launches
-    fwd_train_ms = statistics.mean(e[0].elapsed_time(e[1]) for e in evs)
-    bwd_ms = statistics.mean(e[1].elapsed_time(e[2]) for e in evs) if with_bwd else None
-
-    # inference forward (no state checkpoint), timed the same way
-    fwd_evs = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(2)) for _ in range(args.steps)]
-    with torch.no_grad():
-        for _ in range(args.warmup):
-            fwd()
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
-        for e in fwd_evs:
-            e[0].record(stream)
-            fwd()
-            e[1].record(stream)
-        torch.cuda.synchronize()
-        fwd_ms = (time.perf_counter() - t1) * 1e3 / args.steps
-    fwd_kernel_ms = statistics.mean(e[0].elapsed_time(e[1]) for e in fwd_evs)
-
-    units = w.B * w.H * w.T
-    rid = {"delta": 0, "muon": 1, "adam": 2}[w.rule]
-
-    def roof(kernel, alg_bytes, alg_flops, ms, traffic_file):
-        if w.rule == "muon":
-            bound, ach, peak, unit = "mfma", alg_flops / (ms * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s"
-        else:
-            bound, ach, peak, unit = "hbm", alg_bytes / (ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s"
-        traffic = profiling.read_traffic(os.path.join(ROOT, "profiles", traffic_file))
-        return {"kernel": kernel, "bound": bound, "achieved": ach, "peak": peak, "unit": unit,
-                "frac": ach / peak, "traffic": traffic, "avg_launch_us": ms * 1e3,
-                "alg_bytes": alg_bytes, "alg_flops": alg_flops}
-
-    # muon: the drop-in scan's muon kernels with the mixer's phase-1/3 GEMMs
-    # (torch, fp32) around them; the other rules: the fused chunk kernels
-    fwd_name = (f"scan_fwd_muon<{w.d}> + phase-1/3 GEMMs" if rid == 1 else f"chunk_fwd<{w.d},{rid}>")
-    roof_fwd = roof(fwd_name, fwd_bytes_per_token_head(w) * units,
-                    fwd_flops_per_chunk_head(w) * w.B * w.H * (w.T // w.chunk), fwd_kernel_ms,
-                    f"chunk_fwd_{w.name}_traffic.md")
-    if with_bwd:
-        # the backward pass dominates the step: its two kernels, priced on the
-        # op's own backward inputs and outputs (states are intermediates)
-        if rid == 1:
-            bwd_name = f"scan_bwd_muon_x3<{w.d}> + scan_bwd_dk8<{w.d},1> + autograd GEMMs"
-        else:
-            state_kernel = f"chunk_bwd_dstate<{w.d}>" if rid == 0 else f"chunk_bwd_state<{w.d},{rid}>"
-            bwd_name = f"{state_kernel} + chunk_bwd_tok<{w.d},{rid}>"
-        roof_main = roof(bwd_name, bwd_bytes_per_token_head(w) * units,
-                         bwd_flops_per_chunk_head(w) * w.B * w.H * (w.T // w.chunk), bwd_ms,
-                         f"chunk_bwd_{w.name}_traffic.md")
-    else:
-        roof_main = roof_fwd
-
+    r = chunk_leg(w, args.steps, args.warmup, with_bwd)
+    ms_step = r["ms_step"] if with_bwd else r["fwd_ms"]
     line = {
         "metric": METRIC,
         "value": w.tokens / (ms_step * 1e-3),
@@ -561,12 +648,13 @@ def main(argv=None):
         "config": {"workload": w.name, "rule": w.rule, "B": w.B, "H": w.H, "T": w.T, "d": w.d,
                    "chunk": w.chunk, "pass": "fwd+bwd" if with_bwd else "fwd",
                    "state": "fp32", "global_batch": w.B, "seq_len": w.T, "parallelism": "none"},
-        "fwd_tokens_per_s": w.tokens / (fwd_ms * 1e-3),
-        "fwd_bwd_tokens_per_s": w.tokens / (ms_step * 1e-3) if with_bwd else None,
-        "step_us": {"fwd_with_checkpoint": fwd_train_ms * 1e3, "bwd": None if bwd_ms is None else bwd_ms * 1e3,
-                    "fwd_inference": fwd_kernel_ms * 1e3},
-        "roofline": roof_main,
-        "roofline_fwd": roof_fwd,
+        "fwd_tokens_per_s": w.tokens / (r["fwd_ms"] * 1e-3),
+        "fwd_bwd_tokens_per_s": w.tokens / (r["ms_step"] * 1e-3) if with_bwd else None,
+        "step_us": {"fwd_with_checkpoint": r["fwd_train_ms"] * 1e3 if with_bwd else None,
+                    "bwd": r["bwd_ms"] * 1e3 if with_bwd else None,
+                    "fwd_inference": r["fwd_kernel_ms"] * 1e3},
+        "roofline": r["roofline"] if with_bwd else r["roofline_fwd"],
+        "roofline_fwd": r["roofline_fwd"],
     }
     if not (args.no_drop_in or args.fwd_only):
         line["drop_in"] = drop_in_leg(w, min(args.steps, 20), max(args.warmup, 1))
@@ -574,6 +662,20 @@ def main(argv=None):
             line["drop_in"]["cpu_baseline"] = drop_in_cpu_baseline(w, args.cpu_budget / 2)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(w, args.cpu_budget, with_bwd)
+    if args.workload == DEFAULT_WORKLOAD and not (args.fwd_only or args.no_configs):
+        # the other configurations: muon (forward, and forward + backward),
+        # adam (forward, forward + backward) and the 12-layer LM's training step
+        budget = None if args.no_cpu_baseline else args.cpu_budget / 2
+        steps = min(args.steps, 10)
+        line["configs"] = {
+            "muon_b2_h16_t8192_d128": config_leg("muon_b2_h16_t8192_d128", steps, max(args.warmup, 1), budget,
+                                                 True, max_heads=2),
+            "adam_b2_h8_t4096_d64": config_leg("adam_b2_h8_t4096_d64", args.steps, args.warmup, budget, True),
+        }
+        lm = lm_line(args)
+        line["configs"][LM_WORKLOAD] = {k: lm[k] for k in ("value", "unit", "ms_per_step", "config",
+                                                           "train_step_tokens_per_s", "fwd_tokens_per_s",
+                                                           "fwd_bwd_tokens_per_s", "step_us", "roofline_note")}
     print(json.dumps(line), flush=True)
     return 0
 
