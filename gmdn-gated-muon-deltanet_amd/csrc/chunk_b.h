@@ -44,6 +44,9 @@ GMDN_DEV void map_block(int64_t BH, int nblk, int64_t& bh, int& blk) {
 }
 
 hipError_t chunk_fwd_launch(const ChunkArgs& a, int d, int rule, hipStream_t s);
+// rule 1: the serial muon scan (S_i, M_i of every chunk to S_out, M_out;
+// M_out may be null) and the chunk-parallel output kernel
+hipError_t chunk_fwd_muon_launch(const ChunkArgs& a, int d, float* S_out, float* M_out, int ns, hipStream_t s);
 hipError_t chunk_bwd_launch(const ChunkArgs& a, int d, int rule, hipStream_t s);
 
 }  // namespace gmdn

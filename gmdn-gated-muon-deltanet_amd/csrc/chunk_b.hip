@@ -561,8 +561,8 @@ extern "C" {
 
 size_t gmdn_chunk_states_bytes(const gmdn_chunk_desc* desc) {
   if (check_desc(desc) != GMDN_OK) return 0;
-  // S_i for every rule; adam adds its moments M_i and V_i
-  const size_t planes = desc->rule == 2 ? 3 : 1;
+  // S_i for every rule; muon adds its momentum M_i, adam its moments M_i and V_i
+  const size_t planes = desc->rule == 2 ? 3 : desc->rule == 1 ? 2 : 1;
   return planes * (size_t)(desc->B * desc->H * (desc->T / CB_C)) * desc->d * desc->d * sizeof(float);
 }
 
@@ -581,9 +581,17 @@ int gmdn_chunk_fwd(const gmdn_chunk_desc* desc, const void* q, const void* k, co
     return GMDN_ERR_UNSUPPORTED;
   // o is written in 16-byte pieces along d
   if (!aligned16(o) || (desc->so[0] & 7) || (desc->so[1] & 7) || (desc->so[2] & 7)) return GMDN_ERR_UNSUPPORTED;
-  if (desc->rule == 1) return GMDN_ERR_UNSUPPORTED;
   const ChunkArgs a = make_args(desc, q, k, v, beta, g, gmu, gnu, o, states);
   hipStream_t s = (hipStream_t)stream;
+  if (desc->rule == 1) {
+    // muon: the output kernel reads the chunk states from `states`, which is
+    // therefore required for inference too
+    if (!states || !aligned16(states)) return GMDN_ERR_ARG;
+    if (desc->ns > 8) return GMDN_ERR_ARG;
+    float* S_out = static_cast<float*>(states);
+    float* M_out = S_out + a.B * a.H * a.N * (int64_t)desc->d * desc->d;
+    return chunk_fwd_muon_launch(a, desc->d, S_out, M_out, desc->ns, s) == hipSuccess ? GMDN_OK : GMDN_ERR_LAUNCH;
+  }
   return chunk_fwd_launch(a, desc->d, desc->rule, s) == hipSuccess ? GMDN_OK : GMDN_ERR_LAUNCH;
 }
 

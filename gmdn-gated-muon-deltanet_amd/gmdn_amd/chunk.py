@@ -20,10 +20,13 @@ Chunk length is 64 (the reference default and every configuration's).
 Delta and adam run as one fused HIP kernel per direction (forward: the
 chunk transform, the scan and the output; backward: a reverse scan of the
 state cotangent and a chunk-parallel token-gradient kernel).  Muon's msign
-couples the whole state, so its recurrence runs in the drop-in scan's muon
-kernel (Newton-Schulz fused into the scan step) with phases 1 and 3 as
-batched GEMMs around it; adam at d = 128 trains the same way, with the scan
-in exact float32 (its inference forward stays fused).
+couples the whole state: its forward is a serial HIP kernel per (b, h) that
+streams the k, v tiles and forms each chunk's update in the E-form before
+the Newton-Schulz steps, plus a chunk-parallel output kernel; its backward
+recomputes phases 1 and 3 in float32 around the drop-in muon scan's
+backward kernels.  Adam at d = 128 trains through the drop-in scan with
+phases 1 and 3 as batched GEMMs around it, the scan in exact float32 (its
+inference forward stays fused).
 """
 from __future__ import annotations
 
@@ -53,9 +56,11 @@ def backward_supported(rule, d: int = 128) -> bool:
 
 
 def fused_backward(rule, d: int) -> bool:
-    """Whether the fused backward kernels cover ``rule`` at head dim ``d``."""
+    """Whether ``rule`` at head dim ``d`` trains through the fused forward
+    (delta and adam at d = 64: fused backward kernels; muon: phases 1 and 3
+    recomputed around the drop-in scan's backward kernels)."""
     r = _rule_id(rule)
-    return r == 0 or (r == 2 and d == 64)
+    return r in (0, 1) or (r == 2 and d == 64)
 
 
 def _rule_id(rule) -> int:
@@ -96,12 +101,9 @@ def _composed_core(q, k, v, beta, g, gmu, gnu, rule, ns, precision=None):
     around the drop-in scan kernels, with autograd supplying the backward
     through the scan's own backward kernels.
 
-    Muon always runs this way: msign couples every entry of the d x d state,
-    so the recurrence runs as the drop-in scan's muon kernel (one workgroup
-    per (b, h), Newton-Schulz fused into the scan step, msign VJP fused into
-    its reverse scan).  Adam at d = 128 trains this way with the scan in
-    exact float32 (precision 'ieee'), where the fused kernels' split products
-    would exceed the gradient tolerance."""
+    Adam at d = 128 trains this way with the scan in exact float32
+    (precision 'ieee'), where the fused kernels' split products would exceed
+    the gradient tolerance."""
     B, H, T, d = q.shape
     N = T // CHUNK
     qf, kf, vf = (t.float().reshape(B, H, N, CHUNK, d) for t in (q, k, v))
@@ -135,9 +137,6 @@ def _composed_core(q, k, v, beta, g, gmu, gnu, rule, ns, precision=None):
 def chunk_scan(q, k, v, beta, g, gmu=None, gnu=None, *, rule="delta", ns: int = 3, eps: float = 1e-6):
     """Fused mixer core; see the module docstring."""
     r = _rule_id(rule)
-    if r == 1:
-        _check(q, k, v, beta, g, gmu, gnu, r)
-        return _composed_core(q, k, v, beta, g, gmu, None, 1, ns)
     gmu = gmu if r >= 1 else None
     gnu = gnu if r == 2 else None
     _check(q, k, v, beta, g, gmu, gnu, r)

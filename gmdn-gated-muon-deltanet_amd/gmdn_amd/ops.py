@@ -173,12 +173,14 @@ def chunk_fwd(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, g: Tensor, gmu: Opt
     bc, gc, mc, nc = _gate(beta), _gate(g), _gate(gmu), _gate(gnu)
     o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     desc = chunk_desc(qc, kc, vc, o, rule, ns, eps)
+    # muon's output kernel reads the chunk states: they are written for inference too
+    keep = record or rule == 1
     states = (torch.empty(lib.gmdn_chunk_states_bytes(desc) // 4, dtype=torch.float32, device=q.device)
-              if record else _empty(q))
+              if keep else _empty(q))
     with torch.cuda.device(q.device):
         rc = lib.gmdn_chunk_fwd(desc, nat.ptr(qc), nat.ptr(kc), nat.ptr(vc), nat.ptr(bc), nat.ptr(gc),
                                 nat.ptr(mc), nat.ptr(nc), nat.ptr(o),
-                                nat.ptr(states) if record else None, nat.stream_of(q))
+                                nat.ptr(states) if keep else None, nat.stream_of(q))
     nat.check(rc, "gmdn_chunk_fwd")
     return o, states
 
@@ -186,7 +188,8 @@ def chunk_fwd(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, g: Tensor, gmu: Opt
 @chunk_fwd.register_fake
 def _chunk_fwd_fake(q, k, v, beta, g, gmu, gnu, rule, ns, eps, record):
     o = q.new_empty(q.shape)
-    states = q.new_empty((_states_numel(q, rule, ns, eps),), dtype=torch.float32) if record else _empty(q)
+    keep = record or rule == 1
+    states = q.new_empty((_states_numel(q, rule, ns, eps),), dtype=torch.float32) if keep else _empty(q)
     return o, states
 
 
@@ -270,6 +273,11 @@ def _chunk_fwd_backward(ctx, dO, dstates):
     if ctx.rule == 2 and q.shape[-1] != 64:
         raise RuntimeError(f"the fused backward of rule 2 at head dim {q.shape[-1]} is not built "
                            "(adam's backward is built at d = 64)")
+    if ctx.rule == 1:
+        from .scan import _prec_code
+        dq, dk, dv, dbeta, dg, dgmu = torch.ops.gmdn.chunk_bwd_muon(q, k, v, beta, g, gmu, states, dO, ctx.ns,
+                                                                    _prec_code())
+        return dq, dk, dv, dbeta, dg, dgmu, None, None, None, None, None
     dq, dk, dv, dbeta, dg, dgmu, dgnu = torch.ops.gmdn.chunk_bwd(q, k, v, beta, g, gmu, gnu, states, dO,
                                                                  ctx.rule, ctx.ns, ctx.eps)
     return (dq, dk, dv, dbeta, dg, dgmu if gmu is not None else None, dgnu if gnu is not None else None,
@@ -277,6 +285,37 @@ def _chunk_fwd_backward(ctx, dO, dstates):
 
 
 chunk_fwd.register_autograd(_chunk_fwd_backward, setup_context=_chunk_fwd_setup)
+
+
+@torch.library.custom_op("gmdn::chunk_bwd_muon", mutates_args=(), device_types="cuda")
+def chunk_bwd_muon(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, g: Tensor, gmu: Tensor, states: Tensor,
+                   dO: Tensor, ns: int, precision: int) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Backward of the fused muon core given the forward's chunk states
+    (S_i, M_i): phases 1 and 3 recomputed and differentiated in float32
+    (``phases.py``) around the drop-in muon scan's backward kernels
+    (``gmdn_scan_bwd``, Newton-Schulz VJP on the GPU)."""
+    from . import phases
+    B, H, T, d = q.shape
+    N = T // CHUNK
+    plane = B * H * N * d * d
+    S_all = states[:plane].view(B, H, N, d, d)
+    M_all = states[plane:2 * plane].view(B, H, N, d, d)
+    ph = phases.phase1(q, k, v, beta, g, gmu)
+    dQt, dOv, gS = phases.phase3_vjp(ph, S_all, dO)
+    ones = torch.ones_like(ph["a"])
+    dUv, dKw, da, db, dm, _ = torch.ops.gmdn.state_scan_bwd(ph["Uv"], ph["Kw"], ph["a"].contiguous(),
+                                                            ph["b"].contiguous(), ph["m"].contiguous(), ones,
+                                                            S_all, M_all, _empty(q), gS.contiguous(), 1, ns,
+                                                            precision)
+    dq, dk, dv, dbeta, dg, dgmu = phases.phase1_vjp(ph, g, gmu, dKw, dUv, dQt, dOv, da, db, dm)
+    return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dbeta.to(beta.dtype), dg.to(g.dtype),
+            dgmu.to(gmu.dtype))
+
+
+@chunk_bwd_muon.register_fake
+def _chunk_bwd_muon_fake(q, k, v, beta, g, gmu, states, dO, ns, precision):
+    return (q.new_empty(q.shape), k.new_empty(k.shape), v.new_empty(v.shape), beta.new_empty(beta.shape),
+            g.new_empty(g.shape), gmu.new_empty(gmu.shape))
 
 
 # ------------------------------------------------------- mixer front-end

@@ -32,7 +32,7 @@ def test_opcheck_state_scan(rule):
     torch.library.opcheck(torch.ops.gmdn.state_scan.default, (*ins, rule, 2, 0, True), test_utils=STATIC_CHECKS)
 
 
-@pytest.mark.parametrize("rule,d", [("delta", 64), ("adam", 64)])
+@pytest.mark.parametrize("rule,d", [("delta", 64), ("adam", 64), ("muon", 64), ("muon", 128)])
 def test_opcheck_chunk_fwd(rule, d):
     dev = _dev()
     inp = make_inputs(Workload("t", rule, 1, 2, 128, d), seed=0, device=dev)

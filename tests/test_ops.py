@@ -15,7 +15,7 @@ sys.path.insert(0, os.path.join(ROOT, "gmdn-gated-muon-deltanet_amd"))
 import fast_scan  # noqa: E402
 from gmdn_amd import _native, chunk, ops  # noqa: E402,F401
 
-OPS = ("state_scan", "state_scan_bwd", "chunk_fwd", "chunk_bwd", "front_fwd", "front_bwd")
+OPS = ("state_scan", "state_scan_bwd", "chunk_fwd", "chunk_bwd", "chunk_bwd_muon", "front_fwd", "front_bwd", "msign")
 
 
 def _capture(fn, *args):
@@ -53,8 +53,8 @@ def test_chunk_scan_compiles_to_one_graph(rule, d):
         q, k, v = (torch.empty(1, 2, 128, d, device="cuda", dtype=torch.bfloat16) for _ in range(3))
         gates = [torch.empty(1, 2, 128, device="cuda") for _ in range(4)]
         out, targets = _capture(lambda *x: chunk.chunk_scan(*x, rule=rule, ns=3), q, k, v, *gates)
-    # muon's core is the drop-in scan between batched GEMMs
-    assert ("gmdn.state_scan" if rule == "muon" else "gmdn.chunk_fwd") in targets
+    # every rule's forward is the one fused operator
+    assert "gmdn.chunk_fwd" in targets
     assert tuple(out.shape) == (1, 2, 128, d) and out.dtype == torch.bfloat16
 
 
