@@ -155,8 +155,12 @@ size_t gmdn_chunk_states_bytes(const gmdn_chunk_desc* desc);
 /* Forward: o = mixer core(q, k, v, beta, g[, gmu][, gnu]).  g, gmu, gnu are
  * log-gates; each is clamped at log(1e-6) as the reference clamps the gate
  * at 1e-6 before its log (train_ablation.py:155, :170-175).  gmu is needed
- * for rules 1 and 2, gnu for rule 2.  `states` (may be NULL) receives the
- * pre-update state of every chunk for the backward. */
+ * for rules 1 and 2, gnu for rule 2.  `states` receives the pre-update state
+ * of every chunk for the backward; it may be NULL for rules 0 and 2 when no
+ * backward follows.  Rule 1 (muon) always needs it: its output kernel reads
+ * the chunk states (S_i, M_i float32 (B, H, N, d, d) planes, the layout
+ * gmdn_scan_bwd takes as S_all, M_all).  Rule 1 has no gmdn_chunk_bwd: its
+ * backward runs the drop-in muon backward (gmdn_scan_bwd) on those states. */
 int gmdn_chunk_fwd(const gmdn_chunk_desc* desc, const void* q, const void* k,
                    const void* v, const float* beta, const float* g,
                    const float* gmu, const float* gnu, void* o, void* states,
