@@ -1,5 +1,5 @@
 """ctypes binding of ``libgmdn_scan.so`` (the C ABI declared in include/gmdn_scan.h,
-include/gmdn_front.h and include/gmdn_msign.h).
+include/gmdn_front.h, include/gmdn_tail.h and include/gmdn_msign.h).
 
 The library is built in-tree by ``gmdn_amd.build`` and loaded after torch, so
 its HIP runtime dependency (soname ``libamdhip64.so.7``) binds to the runtime
@@ -58,6 +58,12 @@ SIGNATURES = {
     "gmdn_front_fwd": (c_i32, [c_vp] * 6 + [c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_vp]),
     "gmdn_front_bwd_workspace_floats": (c_size, [c_i64, c_i64, c_i32, c_i32]),
     "gmdn_front_bwd": (c_i32, [c_vp] * 8 + [c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_vp]),
+    # include/gmdn_tail.h
+    "gmdn_gates_fwd": (c_i32, [c_vp, c_vp, c_i64, c_i64, c_i32, c_i32, c_i32, c_vp]),
+    "gmdn_gates_bwd": (c_i32, [c_vp, c_vp, c_vp, c_i64, c_i64, c_i32, c_i32, c_i32, c_vp]),
+    "gmdn_head_norm_fwd": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i32, ctypes.c_float, c_i32, c_vp]),
+    "gmdn_head_norm_bwd_workspace_floats": (c_size, [c_i64, c_i32]),
+    "gmdn_head_norm_bwd": (c_i32, [c_vp] * 7 + [c_size, c_i64, c_i32, c_i32, c_vp]),
     # include/gmdn_msign.h
     "gmdn_msign_workspace_bytes": (c_size, [c_i64, c_i64, c_i64]),
     "gmdn_msign": (c_i32, [c_vp, c_vp, c_i64, c_i64, c_i64, c_i32, ctypes.c_float, c_i32, c_vp, c_size, c_vp]),

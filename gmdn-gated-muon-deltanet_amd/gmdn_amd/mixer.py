@@ -6,10 +6,12 @@ reference ``state_dict`` loads unchanged), the same front-end (qkv
 projection, causal depthwise conv, SiLU, per-head L2 norm, gate sigmoids),
 tail (per-head RMSNorm, output projection) and initialisation.  The conv,
 SiLU and norms run as one HIP kernel per direction
-(``torch.ops.gmdn.front_fwd``); phases 1-3 of the mixer
-(train_ablation.py:142-187: gate reductions, the intra-chunk products, the
-state scan and the output) are one call of ``chunk_scan`` -- the fused HIP
-core.
+(``torch.ops.gmdn.front_fwd``), the gate activations as another
+(``gates_fwd``); phases 1-3 of the mixer (train_ablation.py:142-187: gate
+reductions, the intra-chunk products, the state scan and the output) are one
+call of ``chunk_scan`` -- the fused HIP core -- whose output lands in the
+(B, T, H, dh) layout that the per-head RMSNorm kernel (``head_norm_fwd``)
+and the output projection read.
 
 The stack is the end-to-end harness for the 12-layer, d_model 1024, 8-head,
 muon configuration: it measures the whole training step around the core.
@@ -24,7 +26,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import ops  # noqa: F401  -- registers torch.ops.gmdn.*
-from .chunk import CHUNK, LOG_FLOOR, chunk_scan
+from .chunk import CHUNK, chunk_scan
 
 
 class FastWeightMixer(nn.Module):
@@ -67,12 +69,11 @@ class FastWeightMixer(nn.Module):
         # conv, SiLU and the q / k norms in one HIP kernel per direction
         q, k, v = torch.ops.gmdn.front_fwd(self.qkv(x), self.conv.weight, self.conv.bias, dh)
         q, k, v = (t.view(B, T, H, dh).transpose(1, 2) for t in (q, k, v))
-        gl = self.gates(x).float().view(B, T, self.n_gates, H).permute(2, 0, 3, 1)  # (nG, B, H, T)
-        # log sigmoid = log of the gate, with the reference's 1e-6 floor
-        lg = torch.clamp(F.logsigmoid(gl), min=LOG_FLOOR)
-        beta = torch.sigmoid(gl[1])
-        log_nu = lg[3] if self.n_gates == 4 else None
-        return q, k, v, beta, lg[0], lg[2], log_nu
+        # beta = sigmoid and the other gates' logs (log sigmoid, the reference's
+        # 1e-6 floor) as (B, H, T) float32 rows, in one HIP pass per direction
+        gs = torch.ops.gmdn.gates_fwd(self.gates(x), H, self.n_gates)  # (nG, B, H, T)
+        log_nu = gs[3] if self.n_gates == 4 else None
+        return q, k, v, gs[1], gs[0], gs[2], log_nu
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         B, T, D = x.shape
@@ -82,8 +83,12 @@ class FastWeightMixer(nn.Module):
         dt = torch.bfloat16
         o = chunk_scan(q.to(dt), k.to(dt), v.to(dt), beta, log_alpha, log_mu, log_nu, rule=self.inner,
                        ns=self.ns_steps)
-        o = self.norm(o.to(self.norm.weight.dtype)).to(x.dtype)
-        return self.out(o.transpose(1, 2).reshape(B, T, D))
+        # per-head RMSNorm (HIP) on o's (B, T, H, dh) storage: the output is
+        # already the (B, T, D) input of the projection
+        ot = o.transpose(1, 2).to(self.norm.weight.dtype)
+        eps = self.norm.eps if self.norm.eps is not None else torch.finfo(ot.dtype).eps
+        y, _ = torch.ops.gmdn.head_norm_fwd(ot, self.norm.weight.float(), eps)
+        return self.out(y.view(B, T, D).to(x.dtype))
 
 
 class Block(nn.Module):

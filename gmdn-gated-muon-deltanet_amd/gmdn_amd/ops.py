@@ -20,6 +20,10 @@ autograd registered on the forward operators:
 * ``gmdn::chunk_bwd(...) -> (dq, dk, dv, dbeta, dg, dgmu, dgnu)``.
 * ``gmdn::front_fwd`` / ``gmdn::front_bwd`` -- the mixer front-end (causal
   depthwise conv, SiLU, q/k norms; train_ablation.py:124-128).
+* ``gmdn::gates_fwd`` / ``gmdn::gates_bwd`` -- the gate activations and their
+  clamped logs (train_ablation.py:131-134); ``gmdn::head_norm_fwd`` /
+  ``gmdn::head_norm_bwd`` -- the per-head RMSNorm of the output (:188).
+* ``gmdn::chunk_bwd_muon`` -- the muon core's backward.
 * ``gmdn::msign(M, steps, eps) -> X`` -- the outer Muon optimizer's msign of
   a batch of matrices (train_ablation.py:60-73); no autograd (the optimizer
   runs it under ``no_grad``).
@@ -171,7 +175,9 @@ def chunk_fwd(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, g: Tensor, gmu: Opt
     _check_tokens(q, k, v)
     qc, kc, vc = _tok(q), _tok(k), _tok(v)
     bc, gc, mc, nc = _gate(beta), _gate(g), _gate(gmu), _gate(gnu)
-    o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    # o takes q's layout (the mixer's (B, T, H, d) storage, so that the head
+    # norm and output projection read it without a transposing copy)
+    o = torch.empty_strided(q.shape, _kernel_strides(q), dtype=q.dtype, device=q.device)
     desc = chunk_desc(qc, kc, vc, o, rule, ns, eps)
     # muon's output kernel reads the chunk states: they are written for inference too
     keep = record or rule == 1
@@ -187,7 +193,7 @@ def chunk_fwd(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, g: Tensor, gmu: Opt
 
 @chunk_fwd.register_fake
 def _chunk_fwd_fake(q, k, v, beta, g, gmu, gnu, rule, ns, eps, record):
-    o = q.new_empty(q.shape)
+    o = q.new_empty_strided(q.shape, _kernel_strides(q))
     keep = record or rule == 1
     states = q.new_empty((_states_numel(q, rule, ns, eps),), dtype=torch.float32) if keep else _empty(q)
     return o, states
@@ -392,6 +398,128 @@ def _front_backward(ctx, dq, dk, dv):
 
 
 front_fwd.register_autograd(_front_backward, setup_context=_front_setup)
+
+
+# ------------------------------------------------ gates and head norm
+@torch.library.custom_op("gmdn::gates_fwd", mutates_args=(), device_types="cuda")
+def gates_fwd(y: Tensor, heads: int, n_gates: int) -> Tensor:
+    """(n_gates, B, H, T) float32 from the gate projection y (B, T, n_gates H):
+    sigmoid for gate 1 (beta), log sigmoid clamped at log 1e-6 for the others
+    (reference train_ablation.py:131-134, :155, :169-175)."""
+    lib = nat.load()
+    B, T, C = y.shape
+    yc = y.contiguous()
+    out = torch.empty(n_gates, B, heads, T, dtype=torch.float32, device=y.device)
+    with torch.cuda.device(y.device):
+        rc = lib.gmdn_gates_fwd(nat.ptr(yc), nat.ptr(out), B, T, heads, n_gates, _dtype_code(yc), nat.stream_of(y))
+    nat.check(rc, "gmdn_gates_fwd")
+    return out
+
+
+@gates_fwd.register_fake
+def _gates_fwd_fake(y, heads, n_gates):
+    B, T, C = y.shape
+    return y.new_empty((n_gates, B, heads, T), dtype=torch.float32)
+
+
+@torch.library.custom_op("gmdn::gates_bwd", mutates_args=(), device_types="cuda")
+def gates_bwd(y: Tensor, dout: Tensor, heads: int, n_gates: int) -> Tensor:
+    lib = nat.load()
+    B, T, C = y.shape
+    yc = y.contiguous()
+    dc = dout.to(torch.float32).contiguous()
+    dy = torch.empty_like(yc)
+    with torch.cuda.device(y.device):
+        rc = lib.gmdn_gates_bwd(nat.ptr(yc), nat.ptr(dc), nat.ptr(dy), B, T, heads, n_gates, _dtype_code(yc),
+                                nat.stream_of(y))
+    nat.check(rc, "gmdn_gates_bwd")
+    return dy
+
+
+@gates_bwd.register_fake
+def _gates_bwd_fake(y, dout, heads, n_gates):
+    return torch.empty_like(y, memory_format=torch.contiguous_format)
+
+
+def _gates_setup(ctx, inputs, output):
+    y, heads, n_gates = inputs
+    ctx.save_for_backward(y)
+    ctx.heads, ctx.n_gates = heads, n_gates
+
+
+def _gates_backward(ctx, dout):
+    (y,) = ctx.saved_tensors
+    return torch.ops.gmdn.gates_bwd(y, dout, ctx.heads, ctx.n_gates), None, None
+
+
+gates_fwd.register_autograd(_gates_backward, setup_context=_gates_setup)
+
+
+@torch.library.custom_op("gmdn::head_norm_fwd", mutates_args=(), device_types="cuda")
+def head_norm_fwd(x: Tensor, weight: Tensor, eps: float) -> tuple[Tensor, Tensor]:
+    """RMSNorm of every row of d elements of x (..., d) with a float32 weight
+    (d): the mixer's per-head output norm (train_ablation.py:188).  Returns
+    the output (x's dtype and shape, contiguous) and 1 / rms per row."""
+    lib = nat.load()
+    d = x.shape[-1]
+    xc = x.contiguous()
+    rows = xc.numel() // d if d else 0
+    out = torch.empty_like(xc)
+    rstd = torch.empty(xc.shape[:-1], dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        rc = lib.gmdn_head_norm_fwd(nat.ptr(xc), nat.ptr(weight.contiguous()), nat.ptr(out), nat.ptr(rstd), rows, d,
+                                    eps, _dtype_code(xc), nat.stream_of(x))
+    nat.check(rc, "gmdn_head_norm_fwd")
+    return out, rstd
+
+
+@head_norm_fwd.register_fake
+def _head_norm_fwd_fake(x, weight, eps):
+    return (torch.empty_like(x, memory_format=torch.contiguous_format),
+            x.new_empty(x.shape[:-1], dtype=torch.float32))
+
+
+@torch.library.custom_op("gmdn::head_norm_bwd", mutates_args=(), device_types="cuda")
+def head_norm_bwd(x: Tensor, weight: Tensor, rstd: Tensor, dout: Tensor) -> tuple[Tensor, Tensor]:
+    lib = nat.load()
+    d = x.shape[-1]
+    xc = x.contiguous()
+    rows = xc.numel() // d
+    dc = dout.to(x.dtype).contiguous()
+    dx = torch.empty_like(xc)
+    dw = torch.empty(d, dtype=torch.float32, device=x.device)
+    ws = torch.empty(max(lib.gmdn_head_norm_bwd_workspace_floats(rows, d), 1), dtype=torch.float32,
+                     device=x.device)
+    with torch.cuda.device(x.device):
+        rc = lib.gmdn_head_norm_bwd(nat.ptr(xc), nat.ptr(weight.contiguous()), nat.ptr(rstd.contiguous()),
+                                    nat.ptr(dc), nat.ptr(dx), nat.ptr(dw), nat.ptr(ws), ws.numel(), rows, d,
+                                    _dtype_code(xc), nat.stream_of(x))
+    nat.check(rc, "gmdn_head_norm_bwd")
+    return dx, dw
+
+
+@head_norm_bwd.register_fake
+def _head_norm_bwd_fake(x, weight, rstd, dout):
+    return torch.empty_like(x, memory_format=torch.contiguous_format), weight.new_empty(weight.shape)
+
+
+def _head_norm_setup(ctx, inputs, output):
+    x, weight, eps = inputs
+    out, rstd = output
+    ctx.mark_non_differentiable(rstd)
+    ctx.set_materialize_grads(False)
+    ctx.save_for_backward(x, weight, rstd)
+
+
+def _head_norm_backward(ctx, dout, drstd):
+    x, weight, rstd = ctx.saved_tensors
+    if dout is None:
+        return None, None, None
+    dx, dw = torch.ops.gmdn.head_norm_bwd(x, weight, rstd, dout)
+    return dx, dw, None
+
+
+head_norm_fwd.register_autograd(_head_norm_backward, setup_context=_head_norm_setup)
 
 
 # ------------------------------------------------------------ outer msign
