@@ -47,6 +47,9 @@ hipError_t chunk_fwd_launch(const ChunkArgs& a, int d, int rule, hipStream_t s);
 // rule 1: the serial muon scan (S_i, M_i of every chunk to S_out, M_out;
 // M_out may be null) and the chunk-parallel output kernel
 hipError_t chunk_fwd_muon_launch(const ChunkArgs& a, int d, float* S_out, float* M_out, int ns, hipStream_t s);
+// exact WY/UT mode: prep kernel, the delta scan, output kernel (workspace in floats)
+size_t wy_workspace_floats(int64_t B, int64_t H, int64_t T, int d);
+hipError_t wy_fwd_launch(const ChunkArgs& a, int d, float* ws, hipStream_t s);
 hipError_t chunk_bwd_launch(const ChunkArgs& a, int d, int rule, hipStream_t s);
 
 }  // namespace gmdn

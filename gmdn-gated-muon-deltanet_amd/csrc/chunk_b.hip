@@ -595,6 +595,27 @@ int gmdn_chunk_fwd(const gmdn_chunk_desc* desc, const void* q, const void* k, co
   return chunk_fwd_launch(a, desc->d, desc->rule, s) == hipSuccess ? GMDN_OK : GMDN_ERR_LAUNCH;
 }
 
+size_t gmdn_wy_fwd_workspace_bytes(const gmdn_chunk_desc* desc) {
+  if (check_desc(desc) != GMDN_OK) return 0;
+  return wy_workspace_floats(desc->B, desc->H, desc->T, desc->d) * sizeof(float);
+}
+
+int gmdn_wy_fwd(const gmdn_chunk_desc* desc, const void* q, const void* k, const void* v, const float* beta,
+                const float* g, void* o, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_desc(desc);
+  if (rc != GMDN_OK) return rc;
+  if (desc->B * desc->H * desc->T == 0) return GMDN_OK;
+  if (!q || !k || !v || !beta || !g || !o) return GMDN_ERR_ARG;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return GMDN_ERR_UNSUPPORTED;
+  if ((desc->so[0] & 7) || (desc->so[1] & 7) || (desc->so[2] & 7)) return GMDN_ERR_UNSUPPORTED;
+  if (!workspace || !aligned16(workspace) || workspace_bytes < gmdn_wy_fwd_workspace_bytes(desc))
+    return GMDN_ERR_WORKSPACE;
+  const ChunkArgs a = make_args(desc, q, k, v, beta, g, nullptr, nullptr, o, nullptr);
+  return wy_fwd_launch(a, desc->d, static_cast<float*>(workspace), (hipStream_t)stream) == hipSuccess
+             ? GMDN_OK
+             : GMDN_ERR_LAUNCH;
+}
+
 size_t gmdn_chunk_bwd_workspace_bytes(const gmdn_chunk_desc* desc) {
   if (check_desc(desc) != GMDN_OK) return 0;
   // Gb_i, the cotangent of every chunk's state update (fp32 d x d per chunk),

@@ -166,6 +166,19 @@ int gmdn_chunk_fwd(const gmdn_chunk_desc* desc, const void* q, const void* k,
                    const float* gmu, const float* gnu, void* o, void* states,
                    void* stream);
 
+/* Exact WY/UT mode (no counterpart in the reference, which trains the
+ * chunk-frozen form above and leaves this transform out,
+ * train_ablation.py:12-18): o of the token-exact gated delta rule
+ *   S_t = alpha_t S_{t-1} (I - beta_t k_t k_t^T) + beta_t v_t k_t^T,  o_t = S_t q_t,
+ * alpha_t = exp(max(g_t, log 1e-6)), chunked by the WY/UT transform
+ * (T = (I + strict_lower(diag(beta) (K K^T * Gamma)))^-1, U = T diag(beta) V,
+ * W = T diag(beta gamma) K) with exact float32 products.  desc->rule, ns and
+ * eps are ignored; q, k, v, o bf16 with the strides of desc. */
+size_t gmdn_wy_fwd_workspace_bytes(const gmdn_chunk_desc* desc);
+int gmdn_wy_fwd(const gmdn_chunk_desc* desc, const void* q, const void* k, const void* v,
+                const float* beta, const float* g, void* o, void* workspace,
+                size_t workspace_bytes, void* stream);
+
 /* Workspace bytes gmdn_chunk_bwd needs. */
 size_t gmdn_chunk_bwd_workspace_bytes(const gmdn_chunk_desc* desc);
 

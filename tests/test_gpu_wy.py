@@ -1,0 +1,84 @@
+"""GPU parity of the exact WY/UT mode (gmdn_amd/wy.py: gmdn_wy_fwd's prep,
+delta-scan and output kernels; the composed training path) against the
+oracle's token-exact gated delta recurrence in float64 (oracle/wy.py), on
+the bf16-rounded inputs the kernels see.  Bar: the error in excess of half a
+bf16 ulp of the reference (the output's own rounding) at most 2e-2 of its
+RMS; gate gradients (float32) directly."""
+import pytest
+import torch
+
+from gmdn_amd import wy as gwy
+from oracle import wy as owy
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-2
+
+
+def _dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda:0")
+
+
+def _half_ulp(x):
+    return torch.pow(2.0, torch.floor(torch.log2(x.abs().clamp_min(1e-30))) - 8)
+
+
+def _inputs(B, H, T, d, seed):
+    gen = torch.Generator().manual_seed(seed)
+    q, k, v, beta, g = owy.make_wy_inputs(B, H, T, d, generator=gen, dtype=torch.float32)
+    q, k, v = (t.to(torch.bfloat16) for t in (q, k, v))
+    return q, k, v, beta, g
+
+
+def _excess(got, ref):
+    rms = ref.pow(2).mean().sqrt()
+    raw = ((got - ref).abs().max() / rms).item()
+    exc = (((got - ref).abs() - _half_ulp(ref)).clamp_min(0).max() / rms).item()
+    return raw, exc
+
+
+@pytest.mark.parametrize("B,H,T,d", [(1, 2, 64, 64), (1, 2, 256, 128), (2, 4, 1024, 128), (2, 2, 512, 64)])
+def test_wy_forward_matches_token_recurrence(B, H, T, d):
+    dev = _dev()
+    q, k, v, beta, g = _inputs(B, H, T, d, seed=T + d)
+    ref = owy.token_scan(*(t.double() for t in (q, k, v, beta, g)))
+    with torch.no_grad():
+        o = gwy.wy_scan(*(t.to(dev) for t in (q, k, v, beta, g)))
+    torch.cuda.synchronize()
+    raw, exc = _excess(o.double().cpu(), ref)
+    print(f"wy B{B} H{H} T{T} d{d}: max-abs/rms {raw:.2e}, excess over half-ulp {exc:.2e}")
+    assert exc <= TOL
+
+
+def test_wy_composed_forward_equals_kernel_forward():
+    """The training path (float32 chunk algebra around the delta scan) and the
+    inference kernels agree."""
+    dev = _dev()
+    q, k, v, beta, g = (t.to(dev) for t in _inputs(1, 2, 512, 128, seed=7))
+    with torch.no_grad():
+        o_k = gwy.wy_scan(q, k, v, beta, g)
+    xs = [t.detach().requires_grad_(True) for t in (q, k, v, beta, g)]
+    o_c = gwy.wy_scan(*xs)
+    torch.cuda.synchronize()
+    assert o_c.grad_fn is not None
+    rms = o_c.float().pow(2).mean().sqrt()
+    assert ((o_c.float() - o_k.float()).abs().max() / rms).item() <= 1e-2
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_wy_gradients_match_token_recurrence(d):
+    dev = _dev()
+    q, k, v, beta, g = _inputs(1, 2, 128, d, seed=11 + d)
+    # the cotangent as the bf16 output's gradient arrives: bf16, on both sides
+    dO = torch.randn(1, 2, 128, d, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16)
+    xs = [t.to(dev).requires_grad_(True) for t in (q, k, v, beta, g)]
+    o = gwy.wy_scan(*xs)
+    got = torch.autograd.grad(o, xs, dO.to(dev))
+    rs = [t.double().requires_grad_(True) for t in (q, k, v, beta, g)]
+    ro = owy.token_scan(*rs)
+    ref = torch.autograd.grad(ro, rs, dO.double())
+    for name, a, r in zip(("q", "k", "v", "beta", "g"), got, ref):
+        raw, exc = _excess(a.double().cpu(), r)
+        print(f"wy d{d} d{name}: max-abs/rms {raw:.2e}, excess {exc:.2e}")
+        assert (exc if name in ("q", "k", "v") else raw) <= TOL, name
