@@ -570,8 +570,8 @@ def chunk_leg(w, steps: int, warmup: int, with_bwd: bool) -> dict:
         if rid == 1:
             bwd_name = f"scan_bwd_muon_x3<{w.d}> + scan_bwd_dk8<{w.d},1> + autograd GEMMs"
         elif chunk.fused_backward(w.rule, w.d):
-            state_kernel = f"chunk_bwd_dstate<{w.d}>" if rid == 0 else f"chunk_bwd_state<{w.d},{rid}>"
-            bwd_name = f"{state_kernel} + chunk_bwd_tok<{w.d},{rid}>"
+            bwd_name = (f"chunk_bwd_dstate<{w.d}> + chunk_bwd_pair<{w.d}>" if rid == 0
+                        else f"chunk_bwd_state<{w.d},{rid}> + chunk_bwd_tok<{w.d},{rid}>")
         else:
             bwd_name = "drop-in scan backward + autograd GEMMs"
         out["roofline"] = roof(bwd_name, bwd_bytes_per_token_head(w) * units,

@@ -43,6 +43,42 @@ GMDN_DEV void map_block(int64_t BH, int nblk, int64_t& bh, int& blk) {
   }
 }
 
+// ------------------------------------------------- LDS operand helpers
+// lane (m, G) takes X[r][k0 + 8G .. k0 + 8G + 7] (natural k order, 16 bytes)
+template <class L>
+GMDN_DEV bf16x8 row8(const bf16* X, int r, int k0) {
+  return *reinterpret_cast<const bf16x8*>(X + L::off(r, k0 + 8 * (lane_id() >> 4)));
+}
+
+// lane (i, G) takes X[k0 + 8G + j][c0 + i], j = 0..7 (two transposing reads)
+template <class L>
+GMDN_DEV bf16x8 col8(const bf16* X, int k0, int c0) {
+  const int l = lane_id(), i = l & 15, G = l >> 4;
+  const int rr = k0 + 8 * G + (i >> 2), cc = c0 + 4 * (i & 3);
+  const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(X + L::off(rr, cc)));
+  const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(X + L::off(rr + 4, cc)));
+  return cat8(__builtin_bit_cast(bf16x4, a), __builtin_bit_cast(bf16x4, b));
+}
+
+GMDN_DEV float dot4(const f32x4& a, const f32x4& b) {
+  return a[0] * b[0] + a[1] * b[1] + a[2] * b[2] + a[3] * b[3];
+}
+
+// Column operand whose output lane i stands for column cb + 8 (i / 4) + i % 4:
+// lane (i, G) takes X[k0 + 8G + j][cb + 8 (i / 4) + i % 4], j = 0..7.  With
+// cb = 32 kb + 4u, output row 4G' + jj of the product is column
+// 32 kb + 8 G' + 4u + jj, so tiles u = 0, 1 hold, per lane group G', the
+// eight consecutive columns 32 kb + 8 G' .. +7 of one pair of state-row
+// pieces (the order the checkpoints keep).
+template <class L>
+GMDN_DEV bf16x8 col8p(const bf16* X, int k0, int cb) {
+  const int l = lane_id(), i = l & 15, G = l >> 4;
+  const int rr = k0 + 8 * G + (i >> 2), cc = cb + 8 * (i & 3);
+  const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(X + L::off(rr, cc)));
+  const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(X + L::off(rr + 4, cc)));
+  return cat8(__builtin_bit_cast(bf16x4, a), __builtin_bit_cast(bf16x4, b));
+}
+
 hipError_t chunk_fwd_launch(const ChunkArgs& a, int d, int rule, hipStream_t s);
 // rule 1: the serial muon scan (S_i, M_i of every chunk to S_out, M_out;
 // M_out may be null) and the chunk-parallel output kernel
@@ -51,5 +87,8 @@ hipError_t chunk_fwd_muon_launch(const ChunkArgs& a, int d, float* S_out, float*
 size_t wy_workspace_floats(int64_t B, int64_t H, int64_t T, int d);
 hipError_t wy_fwd_launch(const ChunkArgs& a, int d, float* ws, hipStream_t s);
 hipError_t chunk_bwd_launch(const ChunkArgs& a, int d, int rule, hipStream_t s);
+// delta rule: token gradients of chunk pairs (i0 = 2p from the forward's
+// checkpoint, i1 = 2p + 1 from the reverse scan's Gb)
+hipError_t chunk_bwd_pair_launch(const ChunkArgs& a, int d, hipStream_t s);
 
 }  // namespace gmdn

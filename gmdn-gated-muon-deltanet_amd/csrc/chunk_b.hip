@@ -443,10 +443,13 @@ __global__ void __launch_bounds__(FW_THREADS) chunk_fwd(ChunkArgs p) {
     }
     // the checkpoint of S_i for the backward, from the split operands this
     // wave holds (rows r0 .. r0+15, k-blocks of column half h), so that the
-    // state waves never wait on vector memory
+    // state waves never wait on vector memory.  The delta rule keeps the even
+    // chunks only (plane i / 2): its backward rebuilds S_{i+1} on chip.
     constexpr int CK = NKB;  // 16-byte pieces per lane
-    if (p.states) {
-      float* sp = p.states + ((bh * p.N + i) * D + r0 + lc) * (int64_t)D + 8 * G;
+    const bool ck = p.states && (RULE != 0 || (i & 1) == 0);
+    if (ck) {
+      const int64_t plane = RULE == 0 ? bh * ((p.N + 1) / 2) + i / 2 : bh * p.N + i;
+      float* sp = p.states + (plane * D + r0 + lc) * (int64_t)D + 8 * G;
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb) {
         if ((2 * kb >= NKB) != (h == 1)) continue;
@@ -461,7 +464,7 @@ __global__ void __launch_bounds__(FW_THREADS) chunk_fwd(ChunkArgs p) {
     // pieces) may stay in flight.  Vector memory operations complete in issue
     // order for this count: vmcnt <= (operations issued since) suffices.
     if (ahead) {
-      if (p.states) {
+      if (ck) {
         if (sw == 0)
           wait_vmem_le<L::DMA_OPS + CK + 2>();
         else
@@ -555,15 +558,26 @@ ChunkArgs make_args(const gmdn_chunk_desc* d, const void* q, const void* k, cons
   return a;
 }
 
+// d x d planes of Gb in the backward's workspace
+size_t gb_planes(const gmdn_chunk_desc* desc) {
+  const int64_t N = desc->T / CB_C;
+  return (size_t)(desc->B * desc->H * (desc->rule == 0 ? N / 2 : N));
+}
+
 }  // namespace
 
 extern "C" {
 
 size_t gmdn_chunk_states_bytes(const gmdn_chunk_desc* desc) {
   if (check_desc(desc) != GMDN_OK) return 0;
-  // S_i for every rule; muon adds its momentum M_i, adam its moments M_i and V_i
-  const size_t planes = desc->rule == 2 ? 3 : desc->rule == 1 ? 2 : 1;
-  return planes * (size_t)(desc->B * desc->H * (desc->T / CB_C)) * desc->d * desc->d * sizeof(float);
+  // delta: S_i of the even chunks (the backward rebuilds the odd ones);
+  // muon: S_i and its momentum M_i, adam: S_i and the moments M_i, V_i, of
+  // every chunk
+  const int64_t N = desc->T / CB_C;
+  const size_t sq = (size_t)desc->d * desc->d * sizeof(float);
+  if (desc->rule == 0) return (size_t)(desc->B * desc->H * ((N + 1) / 2)) * sq;
+  const size_t planes = desc->rule == 2 ? 3 : 2;
+  return planes * (size_t)(desc->B * desc->H * N) * sq;
 }
 
 int gmdn_chunk_fwd(const gmdn_chunk_desc* desc, const void* q, const void* k, const void* v,
@@ -618,10 +632,11 @@ int gmdn_wy_fwd(const gmdn_chunk_desc* desc, const void* q, const void* k, const
 
 size_t gmdn_chunk_bwd_workspace_bytes(const gmdn_chunk_desc* desc) {
   if (check_desc(desc) != GMDN_OK) return 0;
-  // Gb_i, the cotangent of every chunk's state update (fp32 d x d per chunk),
-  // then per (chunk, row block) partial sums of the chunk scalars' gradients
+  // Gb_i, the cotangent of a chunk's state update (fp32 d x d per chunk; the
+  // delta rule keeps the odd chunks' only), then per (chunk, row block)
+  // partial sums of the chunk scalars' gradients
   const size_t chunks = (size_t)(desc->B * desc->H * (desc->T / CB_C));
-  return chunks * desc->d * desc->d * sizeof(float) + chunks * (desc->d / 32) * 4 * sizeof(float);
+  return gb_planes(desc) * desc->d * desc->d * sizeof(float) + chunks * (desc->d / 32) * 4 * sizeof(float);
 }
 
 int gmdn_chunk_bwd(const gmdn_chunk_desc* desc, const void* q, const void* k, const void* v,
@@ -652,7 +667,7 @@ int gmdn_chunk_bwd(const gmdn_chunk_desc* desc, const void* q, const void* k, co
   ChunkArgs a = make_args(desc, q, k, v, beta, g, gmu, gnu, const_cast<void*>(dO),
                           const_cast<void*>(states));
   a.gb = (float*)workspace;
-  a.part = a.gb + a.B * a.H * a.N * (int64_t)desc->d * desc->d;
+  a.part = a.gb + (int64_t)gb_planes(desc) * desc->d * desc->d;
   a.dq = (bf16*)dq;
   a.dk = (bf16*)dk;
   a.dv = (bf16*)dv;

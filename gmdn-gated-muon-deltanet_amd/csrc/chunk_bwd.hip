@@ -32,27 +32,6 @@
 
 namespace gmdn {
 
-// ------------------------------------------------------------------ helpers
-// lane (m, G) takes X[r][k0 + 8G .. k0 + 8G + 7] (natural k order, 16 bytes)
-template <class L>
-GMDN_DEV bf16x8 row8(const bf16* X, int r, int k0) {
-  return *reinterpret_cast<const bf16x8*>(X + L::off(r, k0 + 8 * (lane_id() >> 4)));
-}
-
-// lane (i, G) takes X[k0 + 8G + j][c0 + i], j = 0..7 (two transposing reads)
-template <class L>
-GMDN_DEV bf16x8 col8(const bf16* X, int k0, int c0) {
-  const int l = lane_id(), i = l & 15, G = l >> 4;
-  const int rr = k0 + 8 * G + (i >> 2), cc = c0 + 4 * (i & 3);
-  const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(X + L::off(rr, cc)));
-  const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(X + L::off(rr + 4, cc)));
-  return cat8(__builtin_bit_cast(bf16x4, a), __builtin_bit_cast(bf16x4, b));
-}
-
-GMDN_DEV float dot4(const f32x4& a, const f32x4& b) {
-  return a[0] * b[0] + a[1] * b[1] + a[2] * b[2] + a[3] * b[3];
-}
-
 // ============================================================ chunk_bwd_state
 // The adam rule's reverse scan (the delta rule's is chunk_bwd_dstate below).
 template <int D, int RULE>
@@ -689,7 +668,8 @@ __global__ void __launch_bounds__(DS_THREADS) chunk_bwd_dstate(ChunkArgs p) {
     };
     // Gb_i = Sb_{i+1}, published at the last X, stored as split pieces by
     // token waves 0 and 1 (half of the 32 x D exchange each, 16-byte groups
-    // g = 64 k + l), so that the memory wave issues loads only
+    // g = 64 k + l), so that the memory wave issues loads only.  Only the odd
+    // chunks' (plane i / 2): the token kernel forms Gb of the even ones.
     constexpr int GPR = D / 8, NG = 32 * GPR / 64, NGW = NG / 2;
     static_assert(NG % 2 == 0, "Gb groups split over two waves");
     uint32_t xso[NGW];
@@ -705,7 +685,7 @@ __global__ void __launch_bounds__(DS_THREADS) chunk_bwd_dstate(ChunkArgs p) {
         hi[k] = lds_ld<bf16x8>(L0 + (xso[k] + L::XS0));
         lo[k] = lds_ld<bf16x8>(L0 + (xso[k] + L::XS0 + L::XSP));
       }
-      float* gp = p.gb + ((bh * p.N + i) * D + 32 * blk) * (int64_t)D;
+      float* gp = p.gb + ((bh * (p.N / 2) + i / 2) * D + 32 * blk) * (int64_t)D;
 #pragma unroll
       for (int k = 0; k < NGW; ++k) {
         const int g = 64 * (NGW * tw + k) + l;
@@ -718,7 +698,7 @@ __global__ void __launch_bounds__(DS_THREADS) chunk_bwd_dstate(ChunkArgs p) {
       const bool next = j + 1 < p.N;
       Op<2> A0[2], A1[2];
       if (next) share_tiles(ns_tag, A0, A1);
-      if (tw < 2) store_gb(p.N - 1 - j);  // reads the exchange before Y overwrites it
+      if (tw < 2 && ((p.N - 1 - j) & 1)) store_gb(p.N - 1 - j);  // reads the exchange before Y overwrites it
       __syncthreads();  // Y
       if (next) share_p(ns_tag, A0, A1);
       __syncthreads();  // X
@@ -1184,11 +1164,13 @@ static hipError_t launch_bwd(const ChunkArgs& a, hipStream_t stream) {
     k1 = chunk_bwd_state<D, RULE>;
   hipError_t e = hipFuncSetAttribute((const void*)k1, hipFuncAttributeMaxDynamicSharedMemorySize, lds1);
   if (e != hipSuccess) return e;
-  auto k2 = chunk_bwd_tok<D, RULE>;
-  e = hipFuncSetAttribute((const void*)k2, hipFuncAttributeMaxDynamicSharedMemorySize, lds2);
-  if (e != hipSuccess) return e;
   hipLaunchKernelGGL(k1, dim3((unsigned)(a.B * a.H * (D / 32))), dim3(thr1), lds1, stream, a);
   e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  // delta: the token gradients of chunk pairs (even checkpoints, odd Gb)
+  if constexpr (RULE == 0) return chunk_bwd_pair_launch(a, D, stream);
+  auto k2 = chunk_bwd_tok<D, RULE>;
+  e = hipFuncSetAttribute((const void*)k2, hipFuncAttributeMaxDynamicSharedMemorySize, lds2);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(k2, dim3((unsigned)(a.B * a.H * a.N)), dim3(thr2), lds2, stream, a);
   return hipGetLastError();

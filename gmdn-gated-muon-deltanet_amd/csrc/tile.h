@@ -250,6 +250,11 @@ GMDN_DEV f32x4 unsplit_piece(const bf16x8& p) {
   return f32x4{(float)p[0] + (float)p[4], (float)p[1] + (float)p[5], (float)p[2] + (float)p[6],
                (float)p[3] + (float)p[7]};
 }
+// -x of eight bf16 values (sign bits flipped)
+GMDN_DEV bf16x8 neg8(const bf16x8& x) {
+  using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
+  return __builtin_bit_cast(bf16x8, __builtin_bit_cast(u32x4, x) ^ 0x80008000u);
+}
 // Pieces of columns k0 .. k0+3 and k0+4 .. k0+7 -> split operand, natural k order
 GMDN_DEV Op<2> join_pieces(const bf16x8& a, const bf16x8& b) {
   Op<2> r;

@@ -59,7 +59,7 @@ def _forward(w, seed=0):
 
 
 @pytest.mark.parametrize("d", [64, 128])
-@pytest.mark.parametrize("T", [64, 256])
+@pytest.mark.parametrize("T", [64, 192, 256])
 def test_delta_small(T, d):
     err, _, _ = _forward(Workload("t", "delta", 1, 2, T, d))
     assert err <= TOL
@@ -170,8 +170,10 @@ def _grads(w, seed=0, layout=None):
 
 
 @pytest.mark.parametrize("d", [64, 128])
-@pytest.mark.parametrize("T", [64, 256])
+@pytest.mark.parametrize("T", [64, 192, 256, 320])
 def test_delta_grads_small(T, d):
+    """Odd and even chunk counts: the backward forms gradients of chunk pairs
+    and a last unpaired chunk when the count is odd."""
     errs = _grads(Workload("t", "delta", 1, 2, T, d))
     assert all(e <= TOL for e, _ in errs.values()), errs
 
