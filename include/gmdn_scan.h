@@ -147,16 +147,17 @@ typedef struct gmdn_chunk_desc {
   int64_t sq[3], sk[3], sv[3], so[3];
 } gmdn_chunk_desc;
 
-/* Bytes of the per-chunk state checkpoint gmdn_chunk_fwd writes when
- * `states` is non-NULL (what gmdn_chunk_bwd consumes; its layout is private
- * to the library). */
+/* Bytes of the state checkpoint gmdn_chunk_fwd writes when `states` is
+ * non-NULL (what gmdn_chunk_bwd consumes; for rules 0 and 2 its layout is
+ * private to the library: rule 0 keeps the even chunks' states only, d x d
+ * float32 each). */
 size_t gmdn_chunk_states_bytes(const gmdn_chunk_desc* desc);
 
 /* Forward: o = mixer core(q, k, v, beta, g[, gmu][, gnu]).  g, gmu, gnu are
  * log-gates; each is clamped at log(1e-6) as the reference clamps the gate
  * at 1e-6 before its log (train_ablation.py:155, :170-175).  gmu is needed
- * for rules 1 and 2, gnu for rule 2.  `states` receives the pre-update state
- * of every chunk for the backward; it may be NULL for rules 0 and 2 when no
+ * for rules 1 and 2, gnu for rule 2.  `states` receives the chunk states the
+ * backward needs (gmdn_chunk_states_bytes); it may be NULL for rules 0 and 2 when no
  * backward follows.  Rule 1 (muon) always needs it: its output kernel reads
  * the chunk states (S_i, M_i float32 (B, H, N, d, d) planes, the layout
  * gmdn_scan_bwd takes as S_all, M_all).  Rule 1 has no gmdn_chunk_bwd: its
