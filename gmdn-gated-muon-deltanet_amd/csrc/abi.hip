@@ -23,6 +23,14 @@ int launch_status(hipError_t e) { return e == hipSuccess ? GMDN_OK : GMDN_ERR_LA
 
 bool dh_ok(int32_t dh) { return dh == 32 || dh == 64 || dh == 128; }
 
+// Smallest workspace the backward runs with: the muon backward's segments
+// shrink to one chunk; the other rules need their full partial sums.
+size_t scan_bwd_min_workspace(int64_t BH, int64_t N, int32_t dh, int32_t rule, int32_t ns, int32_t precision) {
+  if (rule != 1) return gmdn_scan_bwd_workspace_bytes(BH, N, dh, rule, ns);
+  if (precision == GMDN_PREC_IEEE) return (size_t)(BH * muon_bwd_ws_floats(dh, ns)) * sizeof(float);
+  return (size_t)muon_bwd_ws_segment_floats(BH, 1, dh, ns) * sizeof(float);
+}
+
 int check_scan_common(const float* U, const float* K, const float* a, const float* b,
                       const float* m, const float* n, int64_t BH, int64_t N, int32_t dh,
                       int32_t rule, int32_t ns, int32_t precision) {
@@ -111,7 +119,9 @@ int gmdn_scan_bwd(const float* U, const float* K, const float* a, const float* b
   if (!S_all || !gS || !dU || !dK || !da || !db || !dm || !dn) return GMDN_ERR_ARG;
   if (rule >= 1 && !M_all) return GMDN_ERR_ARG;
   if (rule == 2 && !V_all) return GMDN_ERR_ARG;
-  const size_t need = gmdn_scan_bwd_workspace_bytes(BH, N, dh, rule, ns);
+  // muon: any workspace from the one-chunk segment up (the segments use what
+  // is given); gmdn_scan_bwd_workspace_bytes is the default size
+  const size_t need = scan_bwd_min_workspace(BH, N, dh, rule, ns, precision);
   if (need > 0 && (!workspace || workspace_bytes < need)) return GMDN_ERR_WORKSPACE;
   ScanArgs s{};
   s.U = U; s.K = K; s.a = a; s.b = b; s.m = m; s.n = n;
@@ -123,7 +133,7 @@ int gmdn_scan_bwd(const float* U, const float* K, const float* a, const float* b
   hipError_t e;
   float* part = static_cast<float*>(workspace);
   if (rule == 1) {
-    e = scan_bwd_muon_launch(s, part);
+    e = scan_bwd_muon_launch(s, part, (int64_t)(workspace_bytes / sizeof(float)));
   } else {
     e = scan_bwd_rows_launch(s, part);
   }
@@ -138,7 +148,7 @@ int gmdn_scan_bwd_noalloc(const float* U, const float* K, const float* a, const 
                           int32_t rule, int32_t ns, int32_t precision, void* stream) {
   int rc = check_scan_common(U, K, a, b, m, n, BH, N, dh, rule, ns, precision);
   if (rc != GMDN_OK || BH * N == 0) return rc;
-  if (gmdn_scan_bwd_workspace_bytes(BH, N, dh, rule, ns) > GMDN_NOALLOC_SCRATCH_BYTES) return GMDN_ERR_WORKSPACE;
+  if (scan_bwd_min_workspace(BH, N, dh, rule, ns, precision) > GMDN_NOALLOC_SCRATCH_BYTES) return GMDN_ERR_WORKSPACE;
   void* ws = nullptr;
   rc = scratch_of_current_device(&ws);
   if (rc != GMDN_OK) return rc;

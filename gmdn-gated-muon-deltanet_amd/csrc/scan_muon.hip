@@ -236,23 +236,33 @@ scan_bwd_muon(const float* __restrict__ U, const float* __restrict__ K,
 //      K_i staged into B (row reads).
 // Mbar passes from chunk to chunk through the workspace as fp32 rows of their
 // wave.
+//
+// Segments: the chunks are processed NSEG at a time from the end (pre over
+// the segment, then x3 over it), so the per-chunk workspace holds NSEG
+// chunks per (b, h) whatever N is; Sb and Mbar carry from one segment to the
+// next through the workspace.
 template <int D>
 struct MuonBwdWs {
-  // per chunk: X_0 .. X_ns, Z_0 .. Z_{ns-1}, M_i; then Mbar per (b, h); then |M_i| per chunk
-  int64_t mat, per_chunk, BH, N;
-  GMDN_DEV MuonBwdWs(int64_t BH_, int64_t N_, int ns) : mat((int64_t)D * D), per_chunk((2 * ns + 2) * mat), BH(BH_), N(N_) {}
-  GMDN_DEV float* X(float* ws, int64_t si, int k) const { return ws + si * per_chunk + k * mat; }
-  GMDN_DEV float* Z(float* ws, int64_t si, int ns, int k) const { return ws + si * per_chunk + (ns + 1 + k) * mat; }
-  GMDN_DEV float* M(float* ws, int64_t si, int ns) const { return ws + si * per_chunk + (2 * ns + 1) * mat; }
-  GMDN_DEV float* Mbar(float* ws, int64_t bh) const { return ws + BH * N * per_chunk + bh * mat; }
-  GMDN_DEV float* norm(float* ws) const { return ws + BH * N * per_chunk + BH * mat; }
+  // per (b, h) and chunk of the segment (local index c = i - i0):
+  // X_0 .. X_ns, Z_0 .. Z_{ns-1}, M_i; then Mbar and Sb per (b, h); then |M_i|
+  int64_t mat, per_chunk, BH, nseg;
+  GMDN_DEV MuonBwdWs(int64_t BH_, int64_t nseg_, int ns)
+      : mat((int64_t)D * D), per_chunk((2 * ns + 2) * mat), BH(BH_), nseg(nseg_) {}
+  GMDN_DEV int64_t slot(int64_t bh, int c) const { return bh * nseg + c; }
+  GMDN_DEV float* X(float* ws, int64_t sl, int k) const { return ws + sl * per_chunk + k * mat; }
+  GMDN_DEV float* Z(float* ws, int64_t sl, int ns, int k) const { return ws + sl * per_chunk + (ns + 1 + k) * mat; }
+  GMDN_DEV float* M(float* ws, int64_t sl, int ns) const { return ws + sl * per_chunk + (2 * ns + 1) * mat; }
+  GMDN_DEV float* Mbar(float* ws, int64_t bh) const { return ws + BH * nseg * per_chunk + bh * mat; }
+  GMDN_DEV float* Sbar(float* ws, int64_t bh) const { return ws + BH * nseg * per_chunk + (BH + bh) * mat; }
+  GMDN_DEV float* norm(float* ws) const { return ws + BH * nseg * per_chunk + 2 * BH * mat; }
 };
 
 template <int D>
 __global__ void __launch_bounds__(D * 4)
 scan_bwd_muon_pre(const float* __restrict__ U, const float* __restrict__ K,
                   const float* __restrict__ mv, const float* __restrict__ S_all,
-                  const float* __restrict__ M_all, float* __restrict__ ws, int64_t BH, int N, int ns) {
+                  const float* __restrict__ M_all, float* __restrict__ ws, int64_t BH, int N, int ns,
+                  int i0, int ncur, int nseg) {
   using NSX = NSSplit<D>;
   using P = PrecX3;
   using Op = P::Op;
@@ -261,8 +271,10 @@ scan_bwd_muon_pre(const float* __restrict__ U, const float* __restrict__ K,
   const lds_ptr SA = lds_base(smem), SB = SA + NSX::BYTES;
   float* red = smem + 2 * NSX::BYTES / 4;
   const NSX nsx;
-  const MuonBwdWs<D> W(BH, N, ns);
-  const int64_t si = blockIdx.x;  // = bh * N + i
+  const MuonBwdWs<D> W(BH, nseg, ns);
+  const int64_t bh = blockIdx.x / ncur;
+  const int c = (int)(blockIdx.x % ncur);  // chunk i0 + c of the segment
+  const int64_t si = bh * N + i0 + c, sl = W.slot(bh, c);
   const int l = lane_id(), G = l >> 4, rl = l & 15;
   const int r0 = 16 * wave_id();
   const int64_t mat = (int64_t)D * D;
@@ -279,7 +291,7 @@ scan_bwd_muon_pre(const float* __restrict__ U, const float* __restrict__ K,
   }
   __syncthreads();  // K_i staged
   const float gm = mv[si];
-  float* WM = W.M(ws, si, ns);
+  float* WM = W.M(ws, sl, ns);
   f32x4 X[NT];
   float sq = 0.f;
 #pragma unroll
@@ -293,15 +305,15 @@ scan_bwd_muon_pre(const float* __restrict__ U, const float* __restrict__ K,
     sq += X[t][0] * X[t][0] + X[t][1] * X[t][1] + X[t][2] * X[t][2] + X[t][3] * X[t][3];
   }
   const float nf = sqrtf(block_sum<NW>(sq, red));  // (its barriers also retire B's K_i reads)
-  if (threadIdx.x == 0) W.norm(ws)[si] = nf;
+  if (threadIdx.x == 0) W.norm(ws)[sl] = nf;
   const float scale = 1.f / (nf + 1e-7f);
 #pragma unroll
   for (int t = 0; t < NT; ++t) X[t] = X[t] * scale;
   for (int k = 0; k < ns; ++k) {
-    NSX::store_own(W.X(ws, si, k), X);
-    nsx.step(X, SA, SB, W.Z(ws, si, ns, k));
+    NSX::store_own(W.X(ws, sl, k), X);
+    nsx.step(X, SA, SB, W.Z(ws, sl, ns, k));
   }
-  NSX::store_own(W.X(ws, si, ns), X);
+  NSX::store_own(W.X(ws, sl, ns), X);
 }
 
 template <int D>
@@ -311,7 +323,7 @@ scan_bwd_muon_x3(const float* __restrict__ K, const float* __restrict__ av,
                  const float* __restrict__ S_all, const float* __restrict__ M_all,
                  const float* __restrict__ gS, float* __restrict__ dU, float* __restrict__ da,
                  float* __restrict__ db, float* __restrict__ dm, float* __restrict__ dn,
-                 float* __restrict__ ws, int64_t BH, int N, int ns) {
+                 float* __restrict__ ws, int64_t BH, int N, int ns, int i0, int i1, int nseg) {
   using NSX = NSSplit<D>;
   using P = PrecX3;
   using Op = P::Op;
@@ -322,7 +334,7 @@ scan_bwd_muon_x3(const float* __restrict__ K, const float* __restrict__ av,
 
   const NSX nsx;
   const uint32_t tb = NSX::tbase();
-  const MuonBwdWs<D> W(BH, N, ns);
+  const MuonBwdWs<D> W(BH, nseg, ns);
   const int64_t bh = blockIdx.x;
   const int l = lane_id(), G = l >> 4, rl = l & 15;
   const int r0 = 16 * wave_id();
@@ -330,17 +342,19 @@ scan_bwd_muon_x3(const float* __restrict__ K, const float* __restrict__ av,
   float* WMb = W.Mbar(ws, bh);  // Mbar carried to chunk i-1
   auto roff = [&](int t) { return (int64_t)(r0 + rl) * D + 16 * t + 4 * G; };
 
+  // Sb from the segment after this one (zero after the last chunk)
+  float* WSb = W.Sbar(ws, bh);
   f32x4 Sb[NT];
 #pragma unroll
-  for (int t = 0; t < NT; ++t) Sb[t] = zero4();
+  for (int t = 0; t < NT; ++t) Sb[t] = i1 == N ? zero4() : *reinterpret_cast<const f32x4*>(WSb + roff(t));
 
-  for (int i = N - 1; i >= 0; --i) {
-    const int64_t si = bh * N + i;
+  for (int i = i1 - 1; i >= i0; --i) {
+    const int64_t si = bh * N + i, sl = W.slot(bh, i - i0);
     const float ga = av[si], gb = bv[si], gm = mv[si];
     // ---- 1. da_i = <Sb, S_i>, db_i = <Sb, msign(M_i)>
     float pda = 0.f, pdb = 0.f;
     {
-      const float* Xs = W.X(ws, si, ns);
+      const float* Xs = W.X(ws, sl, ns);
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         const f32x4 Si = *reinterpret_cast<const f32x4*>(S_all + si * mat + roff(t));
@@ -357,14 +371,14 @@ scan_bwd_muon_x3(const float* __restrict__ K, const float* __restrict__ av,
     for (int t = 0; t < NT; ++t) X[t] = gb * Sb[t];
     if (ns > 0) {
       nsx.publish(SA, X);
-      nsx.stage_own(SB, W.X(ws, si, ns - 1));
+      nsx.stage_own(SB, W.X(ws, sl, ns - 1));
       __syncthreads();
     }
     for (int k = ns - 1; k >= 0; --k) {
       f32x4 Q[NT], Bs[NT];
       {
         Op Bz[NKB];
-        NSX::load_own(W.Z(ws, si, ns, k), Bz);
+        NSX::load_own(W.Z(ws, sl, ns, k), Bz);
 #pragma unroll
         for (int tc = 0; tc < NT; ++tc) Q[tc] = NS_A * X[tc];
         nsx.colprod_all(SA, Bz, Q);
@@ -415,13 +429,13 @@ scan_bwd_muon_x3(const float* __restrict__ K, const float* __restrict__ av,
       __syncthreads();  // every read of A and B done
       if (k > 0) {
         nsx.publish(SA, X);
-        nsx.stage_own(SB, W.X(ws, si, k - 1));
+        nsx.stage_own(SB, W.X(ws, sl, k - 1));
         __syncthreads();
       }
     }
     // ---- 3. normalisation: Mbar = Xbar/nrm - <Xbar, M_i>/nrm^2 * M_i/max(|M_i|, 1e-12)
-    const float* WM = W.M(ws, si, ns);
-    const float nf = W.norm(ws)[si];
+    const float* WM = W.M(ws, sl, ns);
+    const float nf = W.norm(ws)[sl];
     const float nrm = nf + 1e-7f;
     float pdot = 0.f;
 #pragma unroll
@@ -467,6 +481,10 @@ scan_bwd_muon_x3(const float* __restrict__ K, const float* __restrict__ av,
     }
     __syncthreads();  // B's K_i read by every wave before chunk i-1 publishes into A and B
   }
+  if (i0 > 0) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) *reinterpret_cast<f32x4*>(WSb + roff(t)) = Sb[t];
+  }
 }
 
 template <int D, int PREC>
@@ -481,7 +499,7 @@ static hipError_t launch_fwd_muon(const ScanArgs& s) {
 }
 
 template <int D, int PREC>
-static hipError_t launch_bwd_muon(const ScanArgs& s, float* ws) {
+static hipError_t launch_bwd_muon(const ScanArgs& s, float* ws, int64_t ws_floats) {
   if constexpr (PREC == 0) {
     const int lds = 2 * NSSplit<D>::BYTES + 64;
     auto kp = scan_bwd_muon_pre<D>;
@@ -489,11 +507,20 @@ static hipError_t launch_bwd_muon(const ScanArgs& s, float* ws) {
     hipError_t e = hipFuncSetAttribute((const void*)kp, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e == hipSuccess) e = hipFuncSetAttribute((const void*)k3, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(kp, dim3((unsigned)(s.BH * s.N)), dim3(D * 4), lds, s.stream, s.U, s.K, s.m, s.S_all,
-                       s.M_all, ws, s.BH, (int)s.N, s.ns);
-    hipLaunchKernelGGL(k3, dim3((unsigned)s.BH), dim3(D * 4), lds, s.stream, s.K, s.a, s.b, s.m, s.S_all,
-                       s.M_all, s.gS, s.dU, s.da, s.db, s.dm, s.dn, ws, s.BH, (int)s.N, s.ns);
-    return hipGetLastError();
+    // segments of nseg chunks from the end: the iterates of a segment, then
+    // its reverse pass (Sb and Mbar carried through the workspace)
+    const int nseg = (int)muon_bwd_segment(s.BH, s.N, D, s.ns, ws_floats);
+    if (nseg < 1) return hipErrorInvalidValue;
+    for (int i1 = (int)s.N; i1 > 0; i1 -= nseg) {
+      const int i0 = i1 > nseg ? i1 - nseg : 0;
+      hipLaunchKernelGGL(kp, dim3((unsigned)(s.BH * (i1 - i0))), dim3(D * 4), lds, s.stream, s.U, s.K, s.m,
+                         s.S_all, s.M_all, ws, s.BH, (int)s.N, s.ns, i0, i1 - i0, nseg);
+      hipLaunchKernelGGL(k3, dim3((unsigned)s.BH), dim3(D * 4), lds, s.stream, s.K, s.a, s.b, s.m, s.S_all,
+                         s.M_all, s.gS, s.dU, s.da, s.db, s.dm, s.dn, ws, s.BH, (int)s.N, s.ns, i0, i1, nseg);
+      hipError_t e2 = hipGetLastError();
+      if (e2 != hipSuccess) return e2;
+    }
+    return hipSuccess;
   } else {
     auto kern = scan_bwd_muon<D, PREC>;
     hipLaunchKernelGGL(kern, dim3((unsigned)s.BH), dim3(D * 4), 0, s.stream, s.U, s.K, s.a, s.b, s.m,
@@ -512,12 +539,12 @@ hipError_t scan_fwd_muon_launch(const ScanArgs& s) {
   return hipErrorInvalidValue;
 }
 
-hipError_t scan_bwd_muon_launch(const ScanArgs& s, float* ws) {
+hipError_t scan_bwd_muon_launch(const ScanArgs& s, float* ws, int64_t ws_floats) {
   const bool x3 = s.precision == 0;
   switch (s.dh) {
-    case 32: return x3 ? launch_bwd_muon<32, 0>(s, ws) : launch_bwd_muon<32, 1>(s, ws);
-    case 64: return x3 ? launch_bwd_muon<64, 0>(s, ws) : launch_bwd_muon<64, 1>(s, ws);
-    case 128: return x3 ? launch_bwd_muon<128, 0>(s, ws) : launch_bwd_muon<128, 1>(s, ws);
+    case 32: return x3 ? launch_bwd_muon<32, 0>(s, ws, ws_floats) : launch_bwd_muon<32, 1>(s, ws, ws_floats);
+    case 64: return x3 ? launch_bwd_muon<64, 0>(s, ws, ws_floats) : launch_bwd_muon<64, 1>(s, ws, ws_floats);
+    case 128: return x3 ? launch_bwd_muon<128, 0>(s, ws, ws_floats) : launch_bwd_muon<128, 1>(s, ws, ws_floats);
   }
   return hipErrorInvalidValue;
 }

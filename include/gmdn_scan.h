@@ -84,10 +84,15 @@ int gmdn_scan_fwd(const float* U, const float* K, const float* a, const float* b
                   int32_t ns, int32_t precision, void* stream);
 
 /* Workspace bytes gmdn_scan_bwd needs for these sizes (0 if none): adam
- * keeps per-row-tile partial sums of its scalar gradients, muon keeps per
- * (b, h) the ns Newton-Schulz iterates and products of the chunk being
- * differentiated plus two state-sized matrices (max(2 ns + 2, 4 + ns) dh^2
- * floats). */
+ * keeps per-row-tile partial sums of its scalar gradients.  Muon ('tf32')
+ * runs the chunks in segments from the end and keeps, per chunk of a segment
+ * and (b, h), the Newton-Schulz iterates X_0 .. X_ns, the products
+ * Z_0 .. Z_{ns-1} and M_i (2 ns + 2 dh^2 floats) and |M_i|, plus two carried
+ * dh^2 matrices per (b, h); the size returned here has as many chunks per
+ * segment as fit in 512 MiB (at least one, at most N), and gmdn_scan_bwd also
+ * accepts any smaller workspace down to one-chunk segments, using as many
+ * chunks per segment as it holds.  Muon ('ieee'): 4 + ns dh^2 matrices per
+ * (b, h). */
 size_t gmdn_scan_bwd_workspace_bytes(int64_t BH, int64_t N, int32_t dh, int32_t rule,
                                      int32_t ns);
 
@@ -114,9 +119,9 @@ int gmdn_scan_bwd(const float* U, const float* K, const float* a, const float* b
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
  * workspace lives in a file-scope device array of GMDN_NOALLOC_SCRATCH_BYTES
  * (64 MiB), one per GPU the library runs on, held until the process ends;
- * the call allocates nothing.  Problems whose workspace
- * (gmdn_scan_bwd_workspace_bytes) exceeds that size are refused with
- * GMDN_ERR_WORKSPACE before any launch.  Every call on one GPU shares that
+ * the call allocates nothing.  Problems whose smallest workspace (for muon
+ * in 'tf32', one-chunk segments; otherwise gmdn_scan_bwd_workspace_bytes)
+ * exceeds that size are refused with GMDN_ERR_WORKSPACE before any launch.  Every call on one GPU shares that
  * GPU's scratch: calls that overlap on one GPU (other streams, other host
  * threads) race and must be serialised by the caller.  Nothing a previous
  * call left in the scratch is read.  Same arguments, results and error codes

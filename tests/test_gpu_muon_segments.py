@@ -1,0 +1,66 @@
+"""The drop-in muon backward (gmdn_scan_bwd, rule 1, 'tf32') runs its chunks
+in segments from the end, as many chunks per segment as the workspace holds:
+with workspaces sized for one-chunk and three-chunk segments the results are
+bit-identical to the default workspace (the same per-chunk arithmetic; the
+state and momentum cotangents carry across segments as exact float32)."""
+import pytest
+import torch
+
+from gmdn_amd import _native as nat
+from gmdn_amd import ops  # noqa: F401  -- registers torch.ops.gmdn.*
+from oracle import scan as osc
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda:0")
+
+
+def _segment_bytes(BH, nseg, dh, ns):
+    mat = dh * dh
+    return 4 * (BH * nseg * ((2 * ns + 2) * mat + 1) + 2 * BH * mat)
+
+
+def _bwd(lib, ins, S_all, M_all, gS, ns, ws_bytes):
+    B, H, N, dh, _ = ins[0].shape
+    U = ins[0]
+    dU, dK = torch.full_like(U, float("nan")), torch.full_like(U, float("nan"))
+    ds = [torch.full_like(ins[2], float("nan")) for _ in range(4)]
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=U.device)
+    args = [nat.ptr(t) for t in ins] + [nat.ptr(S_all), nat.ptr(M_all), None, nat.ptr(gS), nat.ptr(dU),
+                                        nat.ptr(dK)] + [nat.ptr(t) for t in ds]
+    rc = lib.gmdn_scan_bwd(*args, nat.ptr(ws), ws_bytes, B * H, N, dh, 1, ns, nat.PREC_TF32, nat.stream_of(U))
+    nat.check(rc, "gmdn_scan_bwd")
+    torch.cuda.synchronize()
+    return [dU, dK] + ds
+
+
+@pytest.mark.parametrize("B,H,N,dh,ns", [(1, 3, 7, 64, 3), (1, 2, 5, 128, 5)])
+def test_muon_backward_segments_bit_identical(B, H, N, dh, ns):
+    dev = _dev()
+    lib = nat.load()
+    print(f"muon segments B{B} H{H} N{N} d{dh} ns{ns}", flush=True)
+    gen = torch.Generator().manual_seed(N * 10 + dh)
+    ins = [t.to(dev).float().contiguous() for t in osc.make_scan_inputs(B, H, N, 64, dh, generator=gen)]
+    gS = torch.randn(B, H, N, dh, dh, generator=gen).to(dev)
+    S_all, M_all, _ = torch.ops.gmdn.state_scan(*ins, 1, ns, nat.PREC_TF32, True)
+    full = lib.gmdn_scan_bwd_workspace_bytes(B * H, N, dh, 1, ns)
+    assert full == _segment_bytes(B * H, N, dh, ns)  # small problems: one segment
+    want = _bwd(lib, ins, S_all, M_all, gS, ns, full)
+    assert all(torch.isfinite(t).all() for t in want)
+    for nseg in (1, 3):
+        got = _bwd(lib, ins, S_all, M_all, gS, ns, _segment_bytes(B * H, nseg, dh, ns))
+        for name, g_, w_ in zip("dU dK da db dm dn".split(), got, want):
+            assert torch.equal(g_, w_), (nseg, name)
+
+
+def test_muon_backward_refuses_workspace_below_one_chunk():
+    """Below the one-chunk segment the call is refused before any launch."""
+    lib = nat.load()
+    BH, N, dh, ns = 2, 4, 64, 3
+    p = [0x1000] * 16
+    small = _segment_bytes(BH, 1, dh, ns) - 4
+    assert lib.gmdn_scan_bwd(*p, 0x1000, small, BH, N, dh, 1, ns, nat.PREC_TF32, None) == 3

@@ -69,11 +69,20 @@ def test_noalloc_matches_workspace_entry_point(rule, ns):
             assert torch.equal(g_, w_), name
 
 
+def _muon_min_workspace(BH, dh, ns):
+    """Bytes of the muon backward's one-chunk segments: per (b, h) 2 ns + 2
+    dh^2 matrices and |M_i|, plus the two carried dh^2 matrices."""
+    mat = dh * dh
+    return 4 * (BH * ((2 * ns + 2) * mat + 1) + 2 * BH * mat)
+
+
 def test_noalloc_refuses_problems_beyond_the_scratch():
-    """A muon backward whose workspace exceeds the 64 MiB scratch is refused
-    with GMDN_ERR_WORKSPACE before any launch (the pointers are never read)."""
+    """A muon backward whose smallest workspace (one-chunk segments) exceeds
+    the 64 MiB scratch is refused with GMDN_ERR_WORKSPACE before any launch
+    (the pointers are never read)."""
     lib = nat.load()
-    BH, N, dh, ns = 16, 64, 128, 5
+    BH, N, dh, ns = 128, 64, 128, 5
+    assert _muon_min_workspace(BH, dh, ns) > SCRATCH
     assert lib.gmdn_scan_bwd_workspace_bytes(BH, N, dh, 1, ns) > SCRATCH
     p = [0x1000] * 16
     assert lib.gmdn_scan_bwd_noalloc(*p, BH, N, dh, 1, ns, nat.PREC_TF32, None) == 3
