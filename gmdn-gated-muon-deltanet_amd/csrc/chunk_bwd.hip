@@ -18,13 +18,17 @@
 //  * the reverse recurrence of Sb.  Row r of Sb_i needs only row r of Sb_{i+1}
 //    (dE[:, r] = A^T dO[:, r] + diag(w) K Sb[r, :]^T), so one workgroup owns 32
 //    rows, with an LDS-DMA ring of Q, K and the workgroup's dO columns, and
-//    writes Gb_i for every chunk: chunk_bwd_dstate (delta; state, token and
-//    memory waves) and chunk_bwd_state (adam; 4 waves, wave (rt, h) holds 16
-//    rows x column half h and the moment cotangents in registers).
-//  * chunk_bwd_tok: chunk-parallel, one workgroup per (b, h, chunk).  From S_i
-//    (saved by the forward) and Gb_i it recomputes E, A and dE and forms dQ,
-//    dK, dV and the gate gradients; every contraction over the state's rows is
-//    local to the workgroup.
+//    writes Gb_i: chunk_bwd_dstate (delta, odd chunks only; state, token and
+//    memory waves) and chunk_bwd_state (adam, every chunk; 4 waves, wave
+//    (rt, h) holds 16 rows x column half h and the moment cotangents in
+//    registers).
+//  * the token gradients, chunk-parallel.  From S_i (saved by the forward)
+//    and Gb_i they recompute E, A and dE and form dQ, dK, dV and the gate
+//    gradients; every contraction over the state's rows is local to the
+//    workgroup.  chunk_bwd_tok (adam) takes one chunk per workgroup; the
+//    delta rule runs the same phases over chunk pairs (chunk_bwd_pair.hip).
+//    The kernel's template still carries the delta branches those phases
+//    share.
 #include "../../include/gmdn_scan.h"
 #include "chunk_b.h"
 
@@ -50,8 +54,8 @@ struct StateBwdLds {
   static constexpr int XS0 = G0 + RING * GT;                       // Gb^T operand exchange
   static constexpr int XE0 = XS0 + CB_WAVES * NKBH * 2 * 1024;     // -dE operand exchange
   static constexpr int XN0 = XE0 + CB_WAVES * 2 * 1024;            // adam: -E operand exchange
-  static constexpr int P0 = XN0 + (ADAM ? CB_WAVES * 2 * 1024 : 0);  // adam: 4 partial sums
-  static constexpr int BYTES = P0 + 16;
+  static constexpr int P0 = XN0 + (ADAM ? CB_WAVES * 2 * 1024 : 0);  // adam: 4 partial sums per wave
+  static constexpr int BYTES = P0 + CB_WAVES * 16;
   static_assert(BYTES <= 160 * 1024, "state backward LDS exceeds the 160 KiB of a CU");
   static constexpr int DMA_OPS = 2 * (CB_C * D / 8) / CB_THREADS + (ADAM ? 2 : 1) * (CB_C * 32 / 8) / CB_THREADS;
 };
@@ -184,7 +188,6 @@ __global__ void __launch_bounds__(CB_THREADS) chunk_bwd_state(ChunkArgs p) {
   // chunks are visited in reverse: step j handles chunk N-1-j, ring stage j % RING
   for (int j = 0; j < RING - 1 && j < p.N; ++j) issue_loads(p.N - 1 - j, j);
   if (p.N > 0) load_states(p.N - 1);
-  if (threadIdx.x < 4) psum[threadIdx.x] = 0.f;
   wait_vmem();
   __syncthreads();
   if (p.N > 0) chunk_scalars(0);
@@ -280,17 +283,17 @@ __global__ void __launch_bounds__(CB_THREADS) chunk_bwd_state(ChunkArgs p) {
         db = wave_sum(db);
         dm = wave_sum(dm);
         dn = wave_sum(dn);
-        if (l == 0) {
-          atomicAdd(psum + 0, da);
-          atomicAdd(psum + 1, db);
-          atomicAdd(psum + 2, dm);
-          atomicAdd(psum + 3, dn);
+        if (l == 0) {  // the wave's own slots, summed below in a fixed order
+          psum[4 * w + 0] = da;
+          psum[4 * w + 1] = db;
+          psum[4 * w + 2] = dm;
+          psum[4 * w + 3] = dn;
         }
       }
       __syncthreads();  // Gb halves and the partial sums published
       if (w == 0 && l < 4) {
-        p.part[((bh * p.N + i) * (D / 32) + blk) * 4 + l] = psum[l];
-        psum[l] = 0.f;
+        static_assert(CB_WAVES == 4, "four partial slots per scalar");
+        p.part[((bh * p.N + i) * (D / 32) + blk) * 4 + l] = (psum[l] + psum[4 + l]) + (psum[8 + l] + psum[12 + l]);
       }
     }
     // ---------------- segment 1: dE for this wave's tokens 32H .. 32H+31
@@ -778,8 +781,9 @@ struct TokBwdLds {
   static constexpr int DH0 = 6 * TILE, DL0 = 7 * TILE;    // dE
   static constexpr int AP = CB_C * CB_C * 2;
   static constexpr int AH0 = 8 * TILE, AL0 = AH0 + AP;    // dA diag(beta), transposed (rows s)
-  static constexpr int R0 = AL0 + AP;                     // floats: dbeta, beta, g, gmu, gnu, da
-  static constexpr int BYTES = R0 + (5 * CB_C + 4) * 4;
+  // floats: per-wave dbeta partials [NW][64], beta, g, gmu, gnu, per-wave da partials [NW]
+  static constexpr int R0 = AL0 + AP;
+  static constexpr int BYTES = R0 + (NW * CB_C + 4 * CB_C + NW) * 4;
   static_assert(BYTES <= 160 * 1024, "token backward LDS exceeds the 160 KiB of a CU");
 };
 
@@ -802,13 +806,15 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
   bf16* Dl = reinterpret_cast<bf16*>(smem + L::DL0);
   bf16* Ah = reinterpret_cast<bf16*>(smem + L::AH0);
   bf16* Al = reinterpret_cast<bf16*>(smem + L::AL0);
+  // dbeta and da are summed per wave into the wave's own slots, then over
+  // the waves in a fixed order: the gradients are bitwise reproducible
   float* red = reinterpret_cast<float*>(smem + L::R0);
-  float* rdbeta = red;               // [64]
-  float* rbeta = red + CB_C;         // [64]
-  float* rg = red + 2 * CB_C;        // [64]
-  float* rgmu = red + 3 * CB_C;      // [64] (adam)
-  float* rgnu = red + 4 * CB_C;      // [64] (adam)
-  float* rda = red + 5 * CB_C;       // [1]
+  float* pdbeta = red;               // [NW][64]
+  float* rbeta = red + NW * CB_C;    // [64]
+  float* rg = rbeta + CB_C;          // [64]
+  float* rgmu = rbeta + 2 * CB_C;    // [64] (adam)
+  float* rgnu = rbeta + 3 * CB_C;    // [64] (adam)
+  float* pda = rbeta + 4 * CB_C;     // [NW]
 
   const int64_t bh = blockIdx.x / p.N;
   const int i = (int)(blockIdx.x % p.N);
@@ -860,14 +866,12 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
   wait_vmem_le<4 * NKB>();
   if (threadIdx.x < CB_C) {
     const int e = threadIdx.x;
-    rdbeta[e] = 0.f;
     rbeta[e] = gv[0];
     rg[e] = gv[1];
     if constexpr (RULE == 2) {
       rgmu[e] = gv[2];
       rgnu[e] = gv[3];
     }
-    if (e == 0) rda[0] = 0.f;
   }
   __syncthreads();
 
@@ -968,7 +972,7 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
       for (int st = 0; st < 4; ++st) dbp[st] = group_sum(dbp[st]);
       if (G == 0) {
 #pragma unroll
-        for (int st = 0; st < 4; ++st) atomicAdd(rdbeta + 16 * st + lc, dbp[st]);
+        for (int st = 0; st < 4; ++st) pdbeta[w * CB_C + 16 * st + lc] = dbp[st];
       }
       // delta: Gb_i = Sb_{i+1}, so da_i = <Gb_i, S_i>: the trace of this
       // wave's 16 x 16 diagonal block of Gb_i S_i^T (A = Gb rows, B = S rows)
@@ -978,7 +982,10 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
       // lane (n, G) holds entries (4G + jj, n): the diagonal is jj = n - 4G
       const float dpart = (lc >> 2) == G ? T[lc & 3] : 0.f;
       const float da_w = wave_sum(dpart);
-      if (l == 0) atomicAdd(rda, da_w);
+      if (l == 0) pda[w] = da_w;
+    } else if (G == 0) {
+#pragma unroll
+      for (int st = 0; st < 4; ++st) pdbeta[w * CB_C + 16 * st + lc] = 0.f;
     }
   }
   __syncthreads();
@@ -1019,11 +1026,17 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
     *reinterpret_cast<bf16x4*>(Ah + ao) = ah;
     *reinterpret_cast<bf16x4*>(Al + ao) = al;
   }
+  {
+    // the wave's tiles k = w + NW kk all have st = w % 4
+    static_assert(NW % 4 == 0, "a wave's phase IIa tiles share one token tile");
+    float db = 0.f;
 #pragma unroll
-  for (int kk = 0; kk < 16 / NW; ++kk) {
-    const int k = w + NW * kk, tt = k >> 2, st = k & 3;
-    const float db = group_sum(dbk[kk]);
-    if (tt >= st && G == 0) atomicAdd(rdbeta + 16 * st + lc, db);
+    for (int kk = 0; kk < 16 / NW; ++kk) {
+      const int k = w + NW * kk, tt = k >> 2, st = k & 3;
+      const float v = group_sum(dbk[kk]);
+      if (tt >= st) db += v;
+    }
+    if (G == 0) pdbeta[w * CB_C + 16 * (w & 3) + lc] += db;
   }
   __syncthreads();
 
@@ -1031,9 +1044,15 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
   if (w == 0) {
     const int64_t o = bh * p.T + t0 + l;
     const float a = expf(wave_sum(fmaxf(rg[l], LOG_FLOOR)));
+    float rdb = 0.f;
+#pragma unroll
+    for (int q = 0; q < NW; ++q) rdb += pdbeta[q * CB_C + l];
     if constexpr (RULE == 0) {
-      p.dbeta[o] = rdbeta[l];
-      p.dg[o] = rg[l] >= LOG_FLOOR ? rda[0] * a : 0.f;
+      float da = 0.f;
+#pragma unroll
+      for (int q = 0; q < NW; ++q) da += pda[q];
+      p.dbeta[o] = rdb;
+      p.dg[o] = rg[l] >= LOG_FLOOR ? da * a : 0.f;
     } else {
       // da, db, dm, dn: sums of the reverse scan's per-row-block partials
       float sc[4] = {0.f, 0.f, 0.f, 0.f};
@@ -1044,7 +1063,7 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
         for (int c = 0; c < 4; ++c) sc[c] += pp[4 * r + c];
       const float m = expf(wave_sum(fmaxf(rgmu[l], LOG_FLOOR)));
       const float n = expf(wave_sum(fmaxf(rgnu[l], LOG_FLOOR)));
-      p.dbeta[o] = rdbeta[l] + sc[1] * (1.f / CB_C);  // b = mean(beta)
+      p.dbeta[o] = rdb + sc[1] * (1.f / CB_C);  // b = mean(beta)
       p.dg[o] = rg[l] >= LOG_FLOOR ? sc[0] * a : 0.f;
       p.dgmu[o] = rgmu[l] >= LOG_FLOOR ? sc[2] * m : 0.f;
       p.dgnu[o] = rgnu[l] >= LOG_FLOOR ? sc[3] * n : 0.f;
@@ -1167,13 +1186,16 @@ static hipError_t launch_bwd(const ChunkArgs& a, hipStream_t stream) {
   hipLaunchKernelGGL(k1, dim3((unsigned)(a.B * a.H * (D / 32))), dim3(thr1), lds1, stream, a);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  // delta: the token gradients of chunk pairs (even checkpoints, odd Gb)
-  if constexpr (RULE == 0) return chunk_bwd_pair_launch(a, D, stream);
-  auto k2 = chunk_bwd_tok<D, RULE>;
-  e = hipFuncSetAttribute((const void*)k2, hipFuncAttributeMaxDynamicSharedMemorySize, lds2);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k2, dim3((unsigned)(a.B * a.H * a.N)), dim3(thr2), lds2, stream, a);
-  return hipGetLastError();
+  if constexpr (RULE == 0) {
+    // delta: the token gradients of chunk pairs (even checkpoints, odd Gb)
+    return chunk_bwd_pair_launch(a, D, stream);
+  } else {
+    auto k2 = chunk_bwd_tok<D, RULE>;
+    e = hipFuncSetAttribute((const void*)k2, hipFuncAttributeMaxDynamicSharedMemorySize, lds2);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k2, dim3((unsigned)(a.B * a.H * a.N)), dim3(thr2), lds2, stream, a);
+    return hipGetLastError();
+  }
 }
 
 hipError_t chunk_bwd_launch(const ChunkArgs& a, int d, int rule, hipStream_t s) {

@@ -32,8 +32,9 @@ struct PairLds {
   static constexpr int DH0 = 6 * TILE, DL0 = 7 * TILE;    // dE
   static constexpr int AP = CB_C * CB_C * 2;
   static constexpr int AH0 = 8 * TILE, AL0 = AH0 + AP;    // A^T, then dA diag(beta) (rows s)
-  static constexpr int R0 = AL0 + AP;                     // floats: dbeta, beta, g, da
-  static constexpr int BYTES = R0 + (3 * CB_C + 4) * 4;
+  // floats: per-wave dbeta partials [NW][64], beta, g, per-wave da partials [NW]
+  static constexpr int R0 = AL0 + AP;
+  static constexpr int BYTES = R0 + (NW * CB_C + 2 * CB_C + NW) * 4;
   static_assert(BYTES <= 160 * 1024, "pair backward LDS exceeds the 160 KiB of a CU");
 };
 
@@ -58,10 +59,12 @@ struct PairCtx {
   GMDN_DEV bf16* Dl() const { return reinterpret_cast<bf16*>(smem + L::DL0); }
   GMDN_DEV bf16* Ah() const { return reinterpret_cast<bf16*>(smem + L::AH0); }
   GMDN_DEV bf16* Al() const { return reinterpret_cast<bf16*>(smem + L::AL0); }
-  GMDN_DEV float* rdbeta() const { return reinterpret_cast<float*>(smem + L::R0); }
-  GMDN_DEV float* rbeta() const { return rdbeta() + CB_C; }
-  GMDN_DEV float* rg() const { return rdbeta() + 2 * CB_C; }
-  GMDN_DEV float* rda() const { return rdbeta() + 3 * CB_C; }
+  // dbeta and da are summed per wave into the wave's own slots, then over
+  // the waves in a fixed order: the gradients are bitwise reproducible
+  GMDN_DEV float* pdbeta() const { return reinterpret_cast<float*>(smem + L::R0); }  // [NW][64]
+  GMDN_DEV float* rbeta() const { return pdbeta() + L::NW * CB_C; }
+  GMDN_DEV float* rg() const { return rbeta() + CB_C; }
+  GMDN_DEV float* pda() const { return rg() + CB_C; }  // [NW]
 
   // Chunk i's gate rows into wave 0's lanes (token l)
   GMDN_DEV void load_gates(int i, float& b, float& g) const {
@@ -83,13 +86,11 @@ struct PairCtx {
     pl.init(wv, sx[2]);
     pl.issue(x + bb * sx[0] + hh * sx[1] + (int64_t)i * CB_C * sx[2], lds_addr(smem) + dst, w);
   }
-  // The gate rows into LDS, the gradient sums cleared (the caller synchronises)
+  // The gate rows into LDS (the caller synchronises)
   GMDN_DEV void publish_gates(float b, float g) const {
     if (w == 0) {
-      rdbeta()[l] = 0.f;
       rbeta()[l] = b;
       rg()[l] = g;
-      if (l == 0) rda()[0] = 0.f;
     }
   }
 
@@ -169,9 +170,10 @@ struct PairCtx {
     bf16* Dl_ = Dl();
     bf16* Ah_ = Ah();
     bf16* Al_ = Al();
-    float* rdbeta_ = rdbeta();
+    float* pdb = pdbeta() + w * CB_C;  // this wave's dbeta slots
     const float* rbeta_ = rbeta();
     constexpr int NW = L::NW;
+    static_assert(NW % 4 == 0, "a wave's phase IIa tiles share one token tile");
 
     // ---- A^T = (tril(Q K^T) diag(beta))^T split into the A planes (rows s)
 #pragma unroll
@@ -238,7 +240,7 @@ struct PairCtx {
       for (int st = 0; st < 4; ++st) dbp[st] = group_sum(dbp[st]);
       if (G == 0) {
 #pragma unroll
-        for (int st = 0; st < 4; ++st) atomicAdd(rdbeta_ + 16 * st + lc, dbp[st]);
+        for (int st = 0; st < 4; ++st) pdb[16 * st + lc] = dbp[st];  // every token slot
       }
       // da_i = <Gb, S>: the trace of the wave's diagonal block of Gb S^T
       f32x4 T = zero4();
@@ -246,7 +248,7 @@ struct PairCtx {
       for (int kb = 0; kb < NKB; ++kb) T = mma<2, 2>(Ga[kb], Sa[kb], T);
       const float dpart = (lc >> 2) == G ? T[lc & 3] : 0.f;
       const float da_w = wave_sum(dpart);
-      if (l == 0) atomicAdd(rda(), da_w);
+      if (l == 0) pda()[w] = da_w;
     }
     __syncthreads();
 
@@ -301,11 +303,16 @@ struct PairCtx {
       *reinterpret_cast<bf16x4*>(Ah_ + ao) = ah;
       *reinterpret_cast<bf16x4*>(Al_ + ao) = al;
     }
+    {
+      // the wave's tiles k = w + NW kk all have st = w % 4
+      float db = 0.f;
 #pragma unroll
-    for (int kk = 0; kk < 16 / NW; ++kk) {
-      const int k = w + NW * kk, tt = k >> 2, st = k & 3;
-      const float db = group_sum(dbk[kk]);
-      if (tt >= st && G == 0) atomicAdd(rdbeta_ + 16 * st + lc, db);
+      for (int kk = 0; kk < 16 / NW; ++kk) {
+        const int k = w + NW * kk, tt = k >> 2, st = k & 3;
+        const float v = group_sum(dbk[kk]);
+        if (tt >= st) db += v;
+      }
+      if (G == 0) pdb[16 * (w & 3) + lc] += db;
     }
     __syncthreads();
 
@@ -313,8 +320,14 @@ struct PairCtx {
     if (w == 0) {
       const int64_t o = bh * p->T + t0 + l;
       const float a = chunk_decay();
-      p->dbeta[o] = rdbeta_[l];
-      p->dg[o] = rg()[l] >= LOG_FLOOR ? rda()[0] * a : 0.f;
+      float db = 0.f, da = 0.f;
+#pragma unroll
+      for (int q = 0; q < NW; ++q) {
+        db += pdbeta()[q * CB_C + l];
+        da += pda()[q];
+      }
+      p->dbeta[o] = db;
+      p->dg[o] = rg()[l] >= LOG_FLOOR ? da * a : 0.f;
     }
     {
       bf16* dvg = p->dv + bb * p->sv[0] + hh * p->sv[1] + t0 * p->sv[2];

@@ -194,6 +194,24 @@ def test_gated_delta_grads_full_size():
     assert all(e <= TOL for e, _ in errs.values()), errs
 
 
+@pytest.mark.parametrize("rule,d", [("delta", 128), ("delta", 64), ("adam", 64)])
+def test_fused_backward_bitwise_reproducible(rule, d):
+    """The fused backward sums the gate gradients per wave and then over the
+    waves in a fixed order (no float atomics): two runs give identical bits."""
+    dev = _dev()
+    w = Workload("t", rule, 2, 4, 1024, d)
+    inp = make_inputs(w, seed=5, with_grad_out=True)
+    names = [n for n in ALL_INPUTS if inp[n] is not None]
+    runs = []
+    for _ in range(2):
+        xs = {n: inp[n].to(dev).detach().requires_grad_(True) for n in names}
+        o = gc.chunk_scan(*(xs.get(n) for n in ALL_INPUTS), rule=w.rule, ns=w.ns)
+        runs.append(torch.autograd.grad(o, [xs[n] for n in names], inp["dO"].to(dev)))
+    torch.cuda.synchronize()
+    for n, a, b in zip(names, *runs):
+        assert torch.equal(a, b), n
+
+
 @pytest.mark.parametrize("seed", [1, 2])
 def test_adam_grads_small(seed):
     errs = _grads(Workload("t", "adam", 1, 2, 256, 64), seed=seed)
