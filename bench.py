@@ -562,13 +562,13 @@ def chunk_leg(w, steps: int, warmup: int, with_bwd: bool) -> dict:
                 "alg_bytes": alg_bytes, "alg_flops": alg_flops}
 
     chunks = w.B * w.H * (w.T // w.chunk)
-    fwd_name = (f"scan_fwd_muon<{w.d}> + phase-1/3 GEMMs" if rid == 1 else f"chunk_fwd<{w.d},{rid}>")
+    fwd_name = (f"chunk_fwd_muon<{w.d}> + chunk_out<{w.d}>" if rid == 1 else f"chunk_fwd<{w.d},{rid}>")
     out["roofline_fwd"] = roof(fwd_name, fwd_bytes_per_token_head(w) * units,
                                fwd_flops_per_chunk_head(w) * chunks, out["fwd_kernel_ms"],
                                f"chunk_fwd_{w.name}_traffic.md")
     if with_bwd:
         if rid == 1:
-            bwd_name = f"scan_bwd_muon_x3<{w.d}> + scan_bwd_dk8<{w.d},1> + autograd GEMMs"
+            bwd_name = f"chunk_prep_muon<{w.d}> + scan_bwd_muon_pre/x3<{w.d}> + chunk_bwd_tok<{w.d},1>"
         elif chunk.fused_backward(w.rule, w.d):
             bwd_name = (f"chunk_bwd_dstate<{w.d}> + chunk_bwd_pair<{w.d}>" if rid == 0
                         else f"chunk_bwd_state<{w.d},{rid}> + chunk_bwd_tok<{w.d},{rid}>")

@@ -87,6 +87,13 @@ hipError_t chunk_fwd_muon_launch(const ChunkArgs& a, int d, float* S_out, float*
 size_t wy_workspace_floats(int64_t B, int64_t H, int64_t T, int d);
 hipError_t wy_fwd_launch(const ChunkArgs& a, int d, float* ws, hipStream_t s);
 hipError_t chunk_bwd_launch(const ChunkArgs& a, int d, int rule, hipStream_t s);
+// muon: per-chunk Kw, Uv, gS (B, H, N, d, d) and a, b, m (three B H N arrays)
+hipError_t chunk_prep_muon_launch(const ChunkArgs& a, int d, float* Kw, float* Uv, float* gS, float* abm,
+                                  hipStream_t s);
+// muon backward (workspace floats; states = S_i then M_i planes of every chunk)
+size_t chunk_bwd_muon_ws_floats(int64_t BH, int64_t N, int d, int ns);
+hipError_t chunk_bwd_muon_launch(const ChunkArgs& a, int d, int ns, int precision, float* ws, size_t ws_floats,
+                                 hipStream_t s);
 // delta rule: token gradients of chunk pairs (i0 = 2p from the forward's
 // checkpoint, i1 = 2p + 1 from the reverse scan's Gb)
 hipError_t chunk_bwd_pair_launch(const ChunkArgs& a, int d, hipStream_t s);

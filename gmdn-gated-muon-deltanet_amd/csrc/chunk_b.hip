@@ -632,6 +632,10 @@ int gmdn_wy_fwd(const gmdn_chunk_desc* desc, const void* q, const void* k, const
 
 size_t gmdn_chunk_bwd_workspace_bytes(const gmdn_chunk_desc* desc) {
   if (check_desc(desc) != GMDN_OK) return 0;
+  // muon: Kw, Uv, gS and dU per chunk, the chunk scalars and their
+  // gradients, and the drop-in muon backward's workspace
+  if (desc->rule == 1)
+    return chunk_bwd_muon_ws_floats(desc->B * desc->H, desc->T / CB_C, desc->d, desc->ns) * sizeof(float);
   // Gb_i, the cotangent of a chunk's state update (fp32 d x d per chunk; the
   // delta rule keeps the odd chunks' only), then per (chunk, row block)
   // partial sums of the chunk scalars' gradients
@@ -651,7 +655,8 @@ int gmdn_chunk_bwd(const gmdn_chunk_desc* desc, const void* q, const void* k, co
     return GMDN_ERR_ARG;
   if (desc->rule >= 1 && (!gmu || !dgmu)) return GMDN_ERR_ARG;
   if (desc->rule == 2 && (!gnu || !dgnu)) return GMDN_ERR_ARG;
-  if (desc->rule == 1) return GMDN_ERR_UNSUPPORTED;
+  if (desc->rule == 1 && desc->precision != GMDN_PREC_TF32 && desc->precision != GMDN_PREC_IEEE)
+    return GMDN_ERR_ARG;
   // adam at d = 128: the sign-like update M / (sqrt(V) + eps) amplifies the
   // rounding of the split-bf16 state products beyond the gradient tolerance
   if (desc->rule == 2 && desc->d != 64) return GMDN_ERR_UNSUPPORTED;
@@ -675,6 +680,11 @@ int gmdn_chunk_bwd(const gmdn_chunk_desc* desc, const void* q, const void* k, co
   a.dg = dg;
   a.dgmu = dgmu;
   a.dgnu = dgnu;
+  if (desc->rule == 1)
+    return chunk_bwd_muon_launch(a, desc->d, desc->ns, desc->precision, (float*)workspace,
+                                 workspace_bytes / sizeof(float), (hipStream_t)stream) == hipSuccess
+               ? GMDN_OK
+               : GMDN_ERR_LAUNCH;
   return chunk_bwd_launch(a, desc->d, desc->rule, (hipStream_t)stream) == hipSuccess ? GMDN_OK
                                                                                      : GMDN_ERR_LAUNCH;
 }

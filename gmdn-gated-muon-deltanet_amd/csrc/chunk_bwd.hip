@@ -31,6 +31,7 @@
 //    share.
 #include "../../include/gmdn_scan.h"
 #include "chunk_b.h"
+#include "scan_a.h"
 
 #include <type_traits>
 
@@ -781,9 +782,10 @@ struct TokBwdLds {
   static constexpr int DH0 = 6 * TILE, DL0 = 7 * TILE;    // dE
   static constexpr int AP = CB_C * CB_C * 2;
   static constexpr int AH0 = 8 * TILE, AL0 = AH0 + AP;    // dA diag(beta), transposed (rows s)
-  // floats: per-wave dbeta partials [NW][64], beta, g, gmu, gnu, per-wave da partials [NW]
+  // floats: per-wave dbeta and (muon) dw partials [NW][64] each, beta, g,
+  // gmu, gnu (muon: w), per-wave da partials [NW]
   static constexpr int R0 = AL0 + AP;
-  static constexpr int BYTES = R0 + (NW * CB_C + 4 * CB_C + NW) * 4;
+  static constexpr int BYTES = R0 + (2 * NW * CB_C + 4 * CB_C + NW) * 4;
   static_assert(BYTES <= 160 * 1024, "token backward LDS exceeds the 160 KiB of a CU");
 };
 
@@ -810,11 +812,20 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
   // the waves in a fixed order: the gradients are bitwise reproducible
   float* red = reinterpret_cast<float*>(smem + L::R0);
   float* pdbeta = red;               // [NW][64]
-  float* rbeta = red + NW * CB_C;    // [64]
+  float* pdw = red + NW * CB_C;      // [NW][64] (muon: dL/dw_t)
+  float* rbeta = red + 2 * NW * CB_C;  // [64]
   float* rg = rbeta + CB_C;          // [64]
-  float* rgmu = rbeta + 2 * CB_C;    // [64] (adam)
-  float* rgnu = rbeta + 3 * CB_C;    // [64] (adam)
+  float* rgmu = rbeta + 2 * CB_C;    // [64] (muon, adam)
+  float* rgnu = rbeta + 3 * CB_C;    // [64] (adam; muon: the token weights w)
   float* pda = rbeta + 4 * CB_C;     // [NW]
+  // muon reads S_i and Gb_i as float32 rows (the drop-in scan's layout), the
+  // others as split pieces: the conversion waits until the rows are used
+  auto piece = [](const bf16x8& x) {
+    if constexpr (RULE == 1)
+      return split_piece(__builtin_bit_cast(f32x4, x));
+    else
+      return x;
+  };
 
   const int64_t bh = blockIdx.x / p.N;
   const int i = (int)(blockIdx.x % p.N);
@@ -835,10 +846,8 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
     const int64_t e = bh * p.T + t0 + threadIdx.x;
     gv[0] = p.beta[e];
     gv[1] = p.g[e];
-    if constexpr (RULE == 2) {
-      gv[2] = p.gmu[e];
-      gv[3] = p.gnu[e];
-    }
+    if constexpr (RULE >= 1) gv[2] = p.gmu[e];
+    if constexpr (RULE == 2) gv[3] = p.gnu[e];
   }
   {
     DmaPlan<LQ, CB_C, NTHR> pq, pk, pv, po;
@@ -868,9 +877,19 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
     const int e = threadIdx.x;
     rbeta[e] = gv[0];
     rg[e] = gv[1];
-    if constexpr (RULE == 2) {
-      rgmu[e] = gv[2];
-      rgnu[e] = gv[3];
+    if constexpr (RULE >= 1) rgmu[e] = gv[2];
+    if constexpr (RULE == 2) rgnu[e] = gv[3];
+    if constexpr (RULE == 1) {
+      // w_t = exp(sum_{s > t} max(gmu_s, log 1e-6)) (train_ablation.py:154-156)
+      const float lm = fmaxf(gv[2], LOG_FLOOR);
+      const float msum = wave_sum(lm);
+      float incl = lm;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const float y = __shfl_up(incl, o, 64);
+        if (e >= o) incl += y;
+      }
+      rgnu[e] = expf(msum - incl);
     }
   }
   __syncthreads();
@@ -911,7 +930,7 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
   {
     float ws[4], dbp[4];
 #pragma unroll
-    for (int st = 0; st < 4; ++st) ws[st] = RULE == 0 ? rbeta[16 * st + lc] : 1.f;
+    for (int st = 0; st < 4; ++st) ws[st] = RULE == 0 ? rbeta[16 * st + lc] : RULE == 1 ? rgnu[16 * st + lc] : 1.f;
     // column block by column block: the MFMA chains of block kb start as soon
     // as its rows have landed (the loads complete in issue order)
     f32x4 Ets[4], GKs[4];
@@ -924,8 +943,8 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
     }
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
-      Sa[kb] = join_pieces(srow[kb][0], srow[kb][1]);
-      Ga[kb] = join_pieces(grow[kb][0], grow[kb][1]);
+      Sa[kb] = join_pieces(piece(srow[kb][0]), piece(srow[kb][1]));
+      Ga[kb] = join_pieces(piece(grow[kb][0]), piece(grow[kb][1]));
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
         const Op<1> kr{{row8<LQ>(Ks, 16 * st + lc, 32 * kb)}};
@@ -983,9 +1002,20 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
       const float dpart = (lc >> 2) == G ? T[lc & 3] : 0.f;
       const float da_w = wave_sum(dpart);
       if (l == 0) pda[w] = da_w;
-    } else if (G == 0) {
+    } else {
+      if constexpr (RULE == 1) {
+        // muon: sum_r E[s][r] (Gb k_s)[r] is dL/dw_s (w depends on gmu only)
 #pragma unroll
-      for (int st = 0; st < 4; ++st) pdbeta[w * CB_C + 16 * st + lc] = 0.f;
+        for (int st = 0; st < 4; ++st) dbp[st] = group_sum(dbp[st]);
+        if (G == 0) {
+#pragma unroll
+          for (int st = 0; st < 4; ++st) pdw[w * CB_C + 16 * st + lc] = dbp[st];
+        }
+      }
+      if (G == 0) {
+#pragma unroll
+        for (int st = 0; st < 4; ++st) pdbeta[w * CB_C + 16 * st + lc] = 0.f;
+      }
     }
   }
   __syncthreads();
@@ -1053,6 +1083,25 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
       for (int q = 0; q < NW; ++q) da += pda[q];
       p.dbeta[o] = rdb;
       p.dg[o] = rg[l] >= LOG_FLOOR ? da * a : 0.f;
+    } else if constexpr (RULE == 1) {
+      // da, db, dm from the drop-in scan's backward: part = [da | db | dm] (B H N each)
+      const int64_t BHN = p.B * p.H * p.N, si = bh * p.N + i;
+      const float da = p.part[si], db = p.part[BHN + si], dm = p.part[2 * BHN + si];
+      const float m = expf(wave_sum(fmaxf(rgmu[l], LOG_FLOOR)));
+      float dw = 0.f;
+#pragma unroll
+      for (int q = 0; q < NW; ++q) dw += pdw[q * CB_C + l];
+      // d/dlm_t: m (all t) and w_s for s < t (w_s = exp(sum_{u > s} lm_u))
+      const float x = dw * rgnu[l];
+      float incl = x;
+#pragma unroll
+      for (int q = 1; q < 64; q <<= 1) {
+        const float y = __shfl_up(incl, q, 64);
+        if (l >= q) incl += y;
+      }
+      p.dbeta[o] = rdb + db * (1.f / CB_C);  // b = mean(beta)
+      p.dg[o] = rg[l] >= LOG_FLOOR ? da * a : 0.f;
+      p.dgmu[o] = rgmu[l] >= LOG_FLOOR ? (incl - x) + dm * m : 0.f;
     } else {
       // da, db, dm, dn: sums of the reverse scan's per-row-block partials
       float sc[4] = {0.f, 0.f, 0.f, 0.f};
@@ -1157,6 +1206,7 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
   for (int st = 0; st < 4; ++st) {
     f32x4 e = eg[st];
     if constexpr (RULE == 0) e = e * rbeta[16 * st + lc];  // diag(w) E Gb, w = beta of token 16 st + lc
+    if constexpr (RULE == 1) e = e * rgnu[16 * st + lc];   // muon: w_t
     const f32x4 acc = dka[st] - des[st] + e;
     *reinterpret_cast<bf16x4*>(dks + LQ::off(16 * st + lc, j0 + 4 * G)) =
         bf16x4{(bf16)acc[0], (bf16)acc[1], (bf16)acc[2], (bf16)acc[3]};
@@ -1196,6 +1246,55 @@ static hipError_t launch_bwd(const ChunkArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL(k2, dim3((unsigned)(a.B * a.H * a.N)), dim3(thr2), lds2, stream, a);
     return hipGetLastError();
   }
+}
+
+// Muon: the matrix form's per-chunk Kw, Uv and gS (chunk_prep_muon), the
+// drop-in muon scan's backward on the forward's S_i, M_i (Newton-Schulz VJP,
+// chunks in segments), then the token gradients with Gb_i = dU_i.
+size_t chunk_bwd_muon_ws_floats(int64_t BH, int64_t N, int d, int ns) {
+  const int64_t BHN = BH * N;
+  // (+64: the scan's workspace starts 256-byte aligned after the scalars)
+  return (size_t)(4 * BHN * (int64_t)d * d + 7 * BHN + 64 + muon_bwd_ws_total(BH, N, d, ns));
+}
+
+template <int D>
+static hipError_t launch_bwd_muon_chunks(const ChunkArgs& a, int ns, int precision, float* ws, size_t ws_floats,
+                                         hipStream_t stream) {
+  const int64_t BH = a.B * a.H, BHN = BH * a.N, mat = (int64_t)D * D;
+  float* Kw = ws;
+  float* Uv = Kw + BHN * mat;
+  float* gS = Uv + BHN * mat;
+  float* dU = gS + BHN * mat;
+  float* abm = dU + BHN * mat;  // a, b, m
+  float* part = abm + 3 * BHN;  // da, db, dm, dn
+  float* sws = ws + ((part + 4 * BHN - ws + 63) & ~(int64_t)63);  // 16-byte pieces: aligned
+  const int64_t sws_floats = (int64_t)ws_floats - (sws - ws);
+  hipError_t e = chunk_prep_muon_launch(a, D, Kw, Uv, gS, abm, stream);
+  if (e != hipSuccess) return e;
+  ScanArgs sa{};
+  sa.U = Uv; sa.K = Kw; sa.a = abm; sa.b = abm + BHN; sa.m = abm + 2 * BHN; sa.n = nullptr;
+  sa.S_all = a.states; sa.M_all = a.states + BHN * mat; sa.V_all = nullptr; sa.gS = gS;
+  sa.dU = dU; sa.dK = nullptr;
+  sa.da = part; sa.db = part + BHN; sa.dm = part + 2 * BHN; sa.dn = part + 3 * BHN;
+  sa.BH = BH; sa.N = a.N; sa.dh = D; sa.rule = 1; sa.ns = ns; sa.precision = precision;
+  sa.stream = stream;
+  e = scan_bwd_muon_launch(sa, sws, sws_floats);
+  if (e != hipSuccess) return e;
+  ChunkArgs t = a;
+  t.gb = dU;
+  t.part = part;
+  auto k = chunk_bwd_tok<D, 1>;
+  e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, TokBwdLds<D>::BYTES);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k, dim3((unsigned)BHN), dim3(TokBwdLds<D>::NTHR), TokBwdLds<D>::BYTES, stream, t);
+  return hipGetLastError();
+}
+
+hipError_t chunk_bwd_muon_launch(const ChunkArgs& a, int d, int ns, int precision, float* ws, size_t ws_floats,
+                                 hipStream_t s) {
+  if (d == 128) return launch_bwd_muon_chunks<128>(a, ns, precision, ws, ws_floats, s);
+  if (d == 64) return launch_bwd_muon_chunks<64>(a, ns, precision, ws, ws_floats, s);
+  return hipErrorNotSupported;
 }
 
 hipError_t chunk_bwd_launch(const ChunkArgs& a, int d, int rule, hipStream_t s) {

@@ -37,7 +37,7 @@ class ChunkDesc(ctypes.Structure):
     _fields_ = [
         ("B", c_i64), ("H", c_i64), ("T", c_i64),
         ("d", c_i32), ("C", c_i32), ("rule", c_i32), ("ns", c_i32),
-        ("dtype", c_i32), ("reserved", c_i32), ("eps", ctypes.c_float),
+        ("dtype", c_i32), ("precision", c_i32), ("eps", ctypes.c_float),
         ("sq", c_i64 * 3), ("sk", c_i64 * 3), ("sv", c_i64 * 3), ("so", c_i64 * 3),
     ]
 

@@ -23,8 +23,9 @@ state cotangent and a chunk-parallel token-gradient kernel).  Muon's msign
 couples the whole state: its forward is a serial HIP kernel per (b, h) that
 streams the k, v tiles and forms each chunk's update in the E-form before
 the Newton-Schulz steps, plus a chunk-parallel output kernel; its backward
-recomputes phases 1 and 3 in float32 around the drop-in muon scan's
-backward kernels.  Adam at d = 128 trains through the drop-in scan with
+is HIP too: a chunk-parallel kernel forms each chunk's Kw, Uv and dL/dS_i,
+the drop-in muon scan's backward kernels run the Newton-Schulz VJP, and the
+token-gradient kernel finishes in the E-form.  Adam at d = 128 trains through the drop-in scan with
 phases 1 and 3 as batched GEMMs around it, the scan in exact float32 (its
 inference forward stays fused).
 """
@@ -43,7 +44,7 @@ LOG_FLOOR = math.log(1e-6)
 SUPPORTED_D = (64, 128)
 
 
-BWD_RULES = (0, 1, 2)  # rules with a backward (muon: through the scan kernel's VJP)
+BWD_RULES = (0, 1, 2)  # rules with a backward
 
 
 def backward_supported(rule, d: int = 128) -> bool:
@@ -57,8 +58,8 @@ def backward_supported(rule, d: int = 128) -> bool:
 
 def fused_backward(rule, d: int) -> bool:
     """Whether ``rule`` at head dim ``d`` trains through the fused forward
-    (delta and adam at d = 64: fused backward kernels; muon: phases 1 and 3
-    recomputed around the drop-in scan's backward kernels)."""
+    (delta and adam at d = 64; muon at both head dims, its Newton-Schulz
+    VJP through the drop-in scan's backward kernels)."""
     r = _rule_id(rule)
     return r in (0, 1) or (r == 2 and d == 64)
 

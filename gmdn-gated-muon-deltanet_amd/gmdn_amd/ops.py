@@ -124,13 +124,16 @@ state_scan.register_autograd(_state_scan_backward, setup_context=_state_scan_set
 
 
 # ------------------------------------------------------------------ Level B
-def chunk_desc(q: Tensor, k: Tensor, v: Tensor, o: Tensor, rule: int, ns: int, eps: float):
+def chunk_desc(q: Tensor, k: Tensor, v: Tensor, o: Tensor, rule: int, ns: int, eps: float,
+               precision: int = nat.PREC_TF32):
     """The ``gmdn_chunk_desc`` of a call: sizes, rule and the element strides
-    of the (B, H, T, d) token streams."""
+    of the (B, H, T, d) token streams (``precision``: rule 1's Newton-Schulz
+    VJP in the backward)."""
     B, H, T, d = q.shape
     desc = nat.ChunkDesc()
     desc.B, desc.H, desc.T, desc.d, desc.C = B, H, T, d, CHUNK
     desc.rule, desc.ns, desc.dtype, desc.eps = rule, ns, nat.DTYPE_BF16, eps
+    desc.precision = precision
     for name, t in (("sq", q), ("sk", k), ("sv", v), ("so", o)):
         arr = getattr(desc, name)
         for i in range(3):
@@ -203,6 +206,12 @@ def _chunk_fwd_fake(q, k, v, beta, g, gmu, gnu, rule, ns, eps, record):
 def chunk_bwd(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, g: Tensor, gmu: Optional[Tensor],
               gnu: Optional[Tensor], states: Tensor, dO: Tensor, rule: int, ns: int,
               eps: float) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    return _chunk_bwd_call(q, k, v, beta, g, gmu, gnu, states, dO, rule, ns, eps, nat.PREC_TF32)
+
+
+def _chunk_bwd_call(q, k, v, beta, g, gmu, gnu, states, dO, rule, ns, eps, precision):
+    """gmdn_chunk_bwd: the fused backward of every rule (muon: the drop-in
+    scan's Newton-Schulz VJP in ``precision`` between chunk-parallel kernels)."""
     lib = nat.load()
     _check_tokens(q, k, v)
     qc, kc, vc = _tok(q), _tok(k), _tok(v)
@@ -213,7 +222,7 @@ def chunk_bwd(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, g: Tensor, gmu: Opt
     dbeta, dg = torch.empty_like(bc), torch.empty_like(gc)
     dgmu = torch.empty_like(mc) if mc is not None else _empty(q)
     dgnu = torch.empty_like(nc) if nc is not None else _empty(q)
-    desc = chunk_desc(qc, kc, vc, dOc, rule, ns, eps)
+    desc = chunk_desc(qc, kc, vc, dOc, rule, ns, eps, precision)
     ws_bytes = lib.gmdn_chunk_bwd_workspace_bytes(desc)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
     with torch.cuda.device(q.device):
@@ -297,31 +306,18 @@ chunk_fwd.register_autograd(_chunk_fwd_backward, setup_context=_chunk_fwd_setup)
 def chunk_bwd_muon(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, g: Tensor, gmu: Tensor, states: Tensor,
                    dO: Tensor, ns: int, precision: int) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
     """Backward of the fused muon core given the forward's chunk states
-    (S_i, M_i): phases 1 and 3 recomputed and differentiated in float32
-    (``phases.py``) around the drop-in muon scan's backward kernels
-    (``gmdn_scan_bwd``, Newton-Schulz VJP on the GPU)."""
-    from . import phases
-    B, H, T, d = q.shape
-    N = T // CHUNK
-    plane = B * H * N * d * d
-    S_all = states[:plane].view(B, H, N, d, d)
-    M_all = states[plane:2 * plane].view(B, H, N, d, d)
-    ph = phases.phase1(q, k, v, beta, g, gmu)
-    dQt, dOv, gS = phases.phase3_vjp(ph, S_all, dO)
-    ones = torch.ones_like(ph["a"])
-    dUv, dKw, da, db, dm, _ = torch.ops.gmdn.state_scan_bwd(ph["Uv"], ph["Kw"], ph["a"].contiguous(),
-                                                            ph["b"].contiguous(), ph["m"].contiguous(), ones,
-                                                            S_all, M_all, _empty(q), gS.contiguous(), 1, ns,
-                                                            precision)
-    dq, dk, dv, dbeta, dg, dgmu = phases.phase1_vjp(ph, g, gmu, dKw, dUv, dQt, dOv, da, db, dm)
-    return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dbeta.to(beta.dtype), dg.to(g.dtype),
-            dgmu.to(gmu.dtype))
+    (S_i, M_i), all in HIP (``gmdn_chunk_bwd`` with rule 1): the per-chunk
+    Kw, Uv and dL/dS_i, the drop-in muon scan's backward (Newton-Schulz VJP
+    in ``precision``), then the token gradients."""
+    dq, dk, dv, dbeta, dg, dgmu, _ = _chunk_bwd_call(q, k, v, beta, g, gmu, None, states, dO, 1, ns, 1e-6,
+                                                     precision)
+    return dq, dk, dv, dbeta.to(beta.dtype), dg.to(g.dtype), dgmu.to(gmu.dtype)
 
 
 @chunk_bwd_muon.register_fake
 def _chunk_bwd_muon_fake(q, k, v, beta, g, gmu, states, dO, ns, precision):
-    return (q.new_empty(q.shape), k.new_empty(k.shape), v.new_empty(v.shape), beta.new_empty(beta.shape),
-            g.new_empty(g.shape), gmu.new_empty(gmu.shape))
+    dq, dk, dv = (t.new_empty_strided(t.shape, _kernel_strides(t)) for t in (q, k, v))
+    return dq, dk, dv, beta.new_empty(beta.shape), g.new_empty(g.shape), gmu.new_empty(gmu.shape)
 
 
 # ------------------------------------------------------- mixer front-end

@@ -146,7 +146,7 @@ typedef struct gmdn_chunk_desc {
   int32_t rule;         /* GMDN_RULE_* */
   int32_t ns;           /* Newton-Schulz steps (rule 1) */
   int32_t dtype;        /* GMDN_DTYPE_* of q, k, v, o, dO, dq, dk, dv */
-  int32_t reserved;
+  int32_t precision;    /* GMDN_PREC_* of rule 1's Newton-Schulz VJP (backward) */
   float eps;            /* adam denominator epsilon (reference: 1e-6) */
   /* element strides (B, H, T) of each token stream; d is unit-stride */
   int64_t sq[3], sk[3], sv[3], so[3];
