@@ -165,8 +165,7 @@ size_t gmdn_chunk_states_bytes(const gmdn_chunk_desc* desc);
  * backward needs (gmdn_chunk_states_bytes); it may be NULL for rules 0 and 2 when no
  * backward follows.  Rule 1 (muon) always needs it: its output kernel reads
  * the chunk states (S_i, M_i float32 (B, H, N, d, d) planes, the layout
- * gmdn_scan_bwd takes as S_all, M_all).  Rule 1 has no gmdn_chunk_bwd: its
- * backward runs the drop-in muon backward (gmdn_scan_bwd) on those states. */
+ * gmdn_scan_bwd takes as S_all, M_all), which its backward reads too. */
 int gmdn_chunk_fwd(const gmdn_chunk_desc* desc, const void* q, const void* k,
                    const void* v, const float* beta, const float* g,
                    const float* gmu, const float* gnu, void* o, void* states,
@@ -191,7 +190,10 @@ size_t gmdn_chunk_bwd_workspace_bytes(const gmdn_chunk_desc* desc);
 /* Backward given dO (strides desc->so) and the forward's `states`.  Writes
  * dq, dk, dv (strides desc->sq, sk, sv) and dbeta, dg[, dgmu][, dgnu]
  * (contiguous (B, H, T) float32).  Matches torch autograd through the
- * reference's phases 1-3 and scan_eager. */
+ * reference's phases 1-3 and scan_eager.  Rule 1 (muon) forms each chunk's
+ * Kw, Uv and dL/dS_i, runs the drop-in muon reverse scan (Newton-Schulz VJP
+ * in desc->precision) on the forward's S_i, M_i, then the token gradients;
+ * adam (rule 2) is built at d = 64. */
 int gmdn_chunk_bwd(const gmdn_chunk_desc* desc, const void* q, const void* k,
                    const void* v, const float* beta, const float* g,
                    const float* gmu, const float* gnu, const void* states,
