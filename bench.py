@@ -569,11 +569,12 @@ def chunk_leg(w, steps: int, warmup: int, with_bwd: bool) -> dict:
     if with_bwd:
         if rid == 1:
             bwd_name = f"chunk_prep_muon<{w.d}> + scan_bwd_muon_pre/x3<{w.d}> + chunk_bwd_tok<{w.d},1>"
-        elif chunk.fused_backward(w.rule, w.d):
-            bwd_name = (f"chunk_bwd_dstate<{w.d}> + chunk_bwd_pair<{w.d}>" if rid == 0
-                        else f"chunk_bwd_state<{w.d},{rid}> + chunk_bwd_tok<{w.d},{rid}>")
+        elif rid == 0:
+            bwd_name = f"chunk_bwd_dstate<{w.d}> + chunk_bwd_pair<{w.d}>"
+        elif w.d == 128:
+            bwd_name = "chunk_prep<128,2> + scan_bwd_rows<128,2> (fp32) + chunk_bwd_tok<128,2>"
         else:
-            bwd_name = "drop-in scan backward + autograd GEMMs"
+            bwd_name = f"chunk_bwd_state<{w.d},{rid}> + chunk_bwd_tok<{w.d},{rid}>"
         out["roofline"] = roof(bwd_name, bwd_bytes_per_token_head(w) * units,
                                bwd_flops_per_chunk_head(w) * chunks, out["bwd_ms"],
                                f"chunk_bwd_{w.name}_traffic.md")

@@ -87,13 +87,23 @@ hipError_t chunk_fwd_muon_launch(const ChunkArgs& a, int d, float* S_out, float*
 size_t wy_workspace_floats(int64_t B, int64_t H, int64_t T, int d);
 hipError_t wy_fwd_launch(const ChunkArgs& a, int d, float* ws, hipStream_t s);
 hipError_t chunk_bwd_launch(const ChunkArgs& a, int d, int rule, hipStream_t s);
-// muon: per-chunk Kw, Uv, gS (B, H, N, d, d) and a, b, m (three B H N arrays)
-hipError_t chunk_prep_muon_launch(const ChunkArgs& a, int d, float* Kw, float* Uv, float* gS, float* abm,
-                                  hipStream_t s);
+// the matrix form's per-chunk Kw, Uv (fwd) and gS (bwd) as (B, H, N, d, d)
+// float32, and a, b, m, n (four B H N arrays): muon (fwd and bwd together,
+// for its backward) and adam at d = 128 (fwd: training forward, bwd: backward)
+hipError_t chunk_prep_launch(const ChunkArgs& a, int d, int rule, bool fwd, bool bwd, float* Kw, float* Uv,
+                             float* gS, float* abm, hipStream_t s);
+// o = Q S_i^T + A E from float32 S_i planes (chunk-parallel)
+hipError_t chunk_out_launch(const ChunkArgs& a, int d, const float* S_all, hipStream_t s);
 // muon backward (workspace floats; states = S_i then M_i planes of every chunk)
 size_t chunk_bwd_muon_ws_floats(int64_t BH, int64_t N, int d, int ns);
 hipError_t chunk_bwd_muon_launch(const ChunkArgs& a, int d, int ns, int precision, float* ws, size_t ws_floats,
                                  hipStream_t s);
+// adam at d = 128, exact float32 scan: training forward (states = S, M, V,
+// Kw, Uv planes and the four scalar arrays) and backward
+size_t chunk_adam_mat_states_floats(int64_t BH, int64_t N, int d);
+hipError_t chunk_fwd_adam_mat_launch(const ChunkArgs& a, int d, float* states, hipStream_t s);
+size_t chunk_bwd_adam_mat_ws_floats(int64_t BH, int64_t N, int d);
+hipError_t chunk_bwd_adam_mat_launch(const ChunkArgs& a, int d, float* ws, hipStream_t s);
 // delta rule: token gradients of chunk pairs (i0 = 2p from the forward's
 // checkpoint, i1 = 2p + 1 from the reverse scan's Gb)
 hipError_t chunk_bwd_pair_launch(const ChunkArgs& a, int d, hipStream_t s);

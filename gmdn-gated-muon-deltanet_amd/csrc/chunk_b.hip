@@ -576,6 +576,9 @@ size_t gmdn_chunk_states_bytes(const gmdn_chunk_desc* desc) {
   const int64_t N = desc->T / CB_C;
   const size_t sq = (size_t)desc->d * desc->d * sizeof(float);
   if (desc->rule == 0) return (size_t)(desc->B * desc->H * ((N + 1) / 2)) * sq;
+  // adam at d = 128 trains through the exact float32 scan: S, M, V, Kw, Uv
+  // planes of every chunk and the chunk scalars
+  if (desc->rule == 2 && desc->d == 128) return chunk_adam_mat_states_floats(desc->B * desc->H, N, desc->d) * 4;
   const size_t planes = desc->rule == 2 ? 3 : 2;
   return planes * (size_t)(desc->B * desc->H * N) * sq;
 }
@@ -605,6 +608,14 @@ int gmdn_chunk_fwd(const gmdn_chunk_desc* desc, const void* q, const void* k, co
     float* S_out = static_cast<float*>(states);
     float* M_out = S_out + a.B * a.H * a.N * (int64_t)desc->d * desc->d;
     return chunk_fwd_muon_launch(a, desc->d, S_out, M_out, desc->ns, s) == hipSuccess ? GMDN_OK : GMDN_ERR_LAUNCH;
+  }
+  if (desc->rule == 2 && desc->d == 128 && states) {
+    // training: the drop-in adam scan in exact float32 between chunk-parallel
+    // kernels (its epsilon is the reference's 1e-6, fast_scan.py:94)
+    if (!aligned16(states)) return GMDN_ERR_ARG;
+    if (desc->eps != 1e-6f) return GMDN_ERR_UNSUPPORTED;
+    return chunk_fwd_adam_mat_launch(a, desc->d, static_cast<float*>(states), s) == hipSuccess ? GMDN_OK
+                                                                                               : GMDN_ERR_LAUNCH;
   }
   return chunk_fwd_launch(a, desc->d, desc->rule, s) == hipSuccess ? GMDN_OK : GMDN_ERR_LAUNCH;
 }
@@ -636,6 +647,8 @@ size_t gmdn_chunk_bwd_workspace_bytes(const gmdn_chunk_desc* desc) {
   // gradients, and the drop-in muon backward's workspace
   if (desc->rule == 1)
     return chunk_bwd_muon_ws_floats(desc->B * desc->H, desc->T / CB_C, desc->d, desc->ns) * sizeof(float);
+  if (desc->rule == 2 && desc->d == 128)
+    return chunk_bwd_adam_mat_ws_floats(desc->B * desc->H, desc->T / CB_C, desc->d) * sizeof(float);
   // Gb_i, the cotangent of a chunk's state update (fp32 d x d per chunk; the
   // delta rule keeps the odd chunks' only), then per (chunk, row block)
   // partial sums of the chunk scalars' gradients
@@ -657,9 +670,9 @@ int gmdn_chunk_bwd(const gmdn_chunk_desc* desc, const void* q, const void* k, co
   if (desc->rule == 2 && (!gnu || !dgnu)) return GMDN_ERR_ARG;
   if (desc->rule == 1 && desc->precision != GMDN_PREC_TF32 && desc->precision != GMDN_PREC_IEEE)
     return GMDN_ERR_ARG;
-  // adam at d = 128: the sign-like update M / (sqrt(V) + eps) amplifies the
-  // rounding of the split-bf16 state products beyond the gradient tolerance
-  if (desc->rule == 2 && desc->d != 64) return GMDN_ERR_UNSUPPORTED;
+  // adam at d = 128 runs its scan in exact float32 (the split-bf16 state
+  // products exceed the gradient tolerance there): the reference's epsilon
+  if (desc->rule == 2 && desc->d == 128 && desc->eps != 1e-6f) return GMDN_ERR_UNSUPPORTED;
   if (desc->B * desc->H * (desc->T / CB_C) >= ((int64_t)1 << 31)) return GMDN_ERR_ARG;  // one workgroup per chunk
   if (!workspace || workspace_bytes < gmdn_chunk_bwd_workspace_bytes(desc)) return GMDN_ERR_WORKSPACE;
   // dO tiles arrive by 16-byte LDS-DMA loads and dq, dk, dv leave in 16-byte
@@ -680,6 +693,10 @@ int gmdn_chunk_bwd(const gmdn_chunk_desc* desc, const void* q, const void* k, co
   a.dg = dg;
   a.dgmu = dgmu;
   a.dgnu = dgnu;
+  if (desc->rule == 2 && desc->d == 128)
+    return chunk_bwd_adam_mat_launch(a, desc->d, (float*)workspace, (hipStream_t)stream) == hipSuccess
+               ? GMDN_OK
+               : GMDN_ERR_LAUNCH;
   if (desc->rule == 1)
     return chunk_bwd_muon_launch(a, desc->d, desc->ns, desc->precision, (float*)workspace,
                                  workspace_bytes / sizeof(float), (hipStream_t)stream) == hipSuccess

@@ -789,7 +789,10 @@ struct TokBwdLds {
   static_assert(BYTES <= 160 * 1024, "token backward LDS exceeds the 160 KiB of a CU");
 };
 
-template <int D, int RULE>
+// MAT: S_i and Gb_i are the drop-in scan's float32 rows and the chunk
+// scalars' gradients arrive as arrays [da | db | dm | dn] (B H N each) in
+// p.part -- muon always, adam when its scan ran in exact float32 (d = 128)
+template <int D, int RULE, bool MAT = RULE == 1>
 __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p) {
   using LQ = BSwz<D>;
   using LA = BSwz<CB_C>;
@@ -821,7 +824,7 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
   // muon reads S_i and Gb_i as float32 rows (the drop-in scan's layout), the
   // others as split pieces: the conversion waits until the rows are used
   auto piece = [](const bf16x8& x) {
-    if constexpr (RULE == 1)
+    if constexpr (MAT)
       return split_piece(__builtin_bit_cast(f32x4, x));
     else
       return x;
@@ -1103,13 +1106,20 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
       p.dg[o] = rg[l] >= LOG_FLOOR ? da * a : 0.f;
       p.dgmu[o] = rgmu[l] >= LOG_FLOOR ? (incl - x) + dm * m : 0.f;
     } else {
-      // da, db, dm, dn: sums of the reverse scan's per-row-block partials
+      // da, db, dm, dn: sums of the reverse scan's per-row-block partials,
+      // or (MAT) the drop-in scan's per-chunk gradients
       float sc[4] = {0.f, 0.f, 0.f, 0.f};
-      const float* pp = p.part + (bh * p.N + i) * (int64_t)(D / 32) * 4;
+      if constexpr (MAT) {
+        const int64_t BHN = p.B * p.H * p.N, si = bh * p.N + i;
 #pragma unroll
-      for (int r = 0; r < D / 32; ++r)
+        for (int c = 0; c < 4; ++c) sc[c] = p.part[c * BHN + si];
+      } else {
+        const float* pp = p.part + (bh * p.N + i) * (int64_t)(D / 32) * 4;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) sc[c] += pp[4 * r + c];
+        for (int r = 0; r < D / 32; ++r)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) sc[c] += pp[4 * r + c];
+      }
       const float m = expf(wave_sum(fmaxf(rgmu[l], LOG_FLOOR)));
       const float n = expf(wave_sum(fmaxf(rgnu[l], LOG_FLOOR)));
       p.dbeta[o] = rdb + sc[1] * (1.f / CB_C);  // b = mean(beta)
@@ -1254,7 +1264,7 @@ static hipError_t launch_bwd(const ChunkArgs& a, hipStream_t stream) {
 size_t chunk_bwd_muon_ws_floats(int64_t BH, int64_t N, int d, int ns) {
   const int64_t BHN = BH * N;
   // (+64: the scan's workspace starts 256-byte aligned after the scalars)
-  return (size_t)(4 * BHN * (int64_t)d * d + 7 * BHN + 64 + muon_bwd_ws_total(BH, N, d, ns));
+  return (size_t)(4 * BHN * (int64_t)d * d + 8 * BHN + 64 + muon_bwd_ws_total(BH, N, d, ns));
 }
 
 template <int D>
@@ -1265,11 +1275,11 @@ static hipError_t launch_bwd_muon_chunks(const ChunkArgs& a, int ns, int precisi
   float* Uv = Kw + BHN * mat;
   float* gS = Uv + BHN * mat;
   float* dU = gS + BHN * mat;
-  float* abm = dU + BHN * mat;  // a, b, m
-  float* part = abm + 3 * BHN;  // da, db, dm, dn
+  float* abm = dU + BHN * mat;  // a, b, m, n
+  float* part = abm + 4 * BHN;  // da, db, dm, dn
   float* sws = ws + ((part + 4 * BHN - ws + 63) & ~(int64_t)63);  // 16-byte pieces: aligned
   const int64_t sws_floats = (int64_t)ws_floats - (sws - ws);
-  hipError_t e = chunk_prep_muon_launch(a, D, Kw, Uv, gS, abm, stream);
+  hipError_t e = chunk_prep_launch(a, D, 1, true, true, Kw, Uv, gS, abm, stream);
   if (e != hipSuccess) return e;
   ScanArgs sa{};
   sa.U = Uv; sa.K = Kw; sa.a = abm; sa.b = abm + BHN; sa.m = abm + 2 * BHN; sa.n = nullptr;
@@ -1284,6 +1294,51 @@ static hipError_t launch_bwd_muon_chunks(const ChunkArgs& a, int ns, int precisi
   t.gb = dU;
   t.part = part;
   auto k = chunk_bwd_tok<D, 1>;
+  e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, TokBwdLds<D>::BYTES);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k, dim3((unsigned)BHN), dim3(TokBwdLds<D>::NTHR), TokBwdLds<D>::BYTES, stream, t);
+  return hipGetLastError();
+}
+
+// Adam at d = 128 (exact float32 scan): gS per chunk, the drop-in adam
+// reverse scan on the forward's S, M, V and stored Kw, Uv, scalars, then the
+// token gradients with Gb_i = dU_i.  states = [S | M | V | Kw | Uv | a b m n].
+size_t chunk_bwd_adam_mat_ws_floats(int64_t BH, int64_t N, int d) {
+  const int64_t BHN = BH * N;
+  return (size_t)(3 * BHN * (int64_t)d * d + 8 * BHN + BHN * (d / 16) * 4 + 64);
+}
+
+hipError_t chunk_bwd_adam_mat_launch(const ChunkArgs& a, int d, float* ws, hipStream_t stream) {
+  if (d != 128) return hipErrorNotSupported;
+  constexpr int D = 128;
+  const int64_t BH = a.B * a.H, BHN = BH * a.N, mat = (int64_t)D * D;
+  const float* S = a.states;
+  const float* Kw = S + 3 * BHN * mat;
+  const float* Uv = S + 4 * BHN * mat;
+  const float* abm = S + 5 * BHN * mat;
+  float* gS = ws;
+  float* dU = gS + BHN * mat;
+  float* dK = dU + BHN * mat;
+  float* abm2 = dK + BHN * mat;  // the prep kernel's copy of the scalars (unused)
+  float* sc = abm2 + 4 * BHN;    // da, db, dm, dn
+  float* part = ws + ((sc + 4 * BHN - ws + 63) & ~(int64_t)63);
+  hipError_t e = chunk_prep_launch(a, D, 2, false, true, nullptr, nullptr, gS, abm2, stream);
+  if (e != hipSuccess) return e;
+  ScanArgs sa{};
+  sa.U = Uv; sa.K = Kw; sa.a = abm; sa.b = abm + BHN; sa.m = abm + 2 * BHN; sa.n = abm + 3 * BHN;
+  sa.S_all = a.states; sa.M_all = a.states + BHN * mat; sa.V_all = a.states + 2 * BHN * mat;
+  sa.gS = gS; sa.dU = dU; sa.dK = dK;
+  sa.da = sc; sa.db = sc + BHN; sa.dm = sc + 2 * BHN; sa.dn = sc + 3 * BHN;
+  sa.BH = BH; sa.N = a.N; sa.dh = D; sa.rule = 2; sa.ns = 0; sa.precision = GMDN_PREC_IEEE;
+  sa.stream = stream;
+  e = scan_bwd_rows_launch(sa, part);
+  if (e != hipSuccess) return e;
+  e = scan_bwd_dk_launch(sa, part);
+  if (e != hipSuccess) return e;
+  ChunkArgs t = a;
+  t.gb = dU;
+  t.part = sc;
+  auto k = chunk_bwd_tok<D, 2, true>;
   e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, TokBwdLds<D>::BYTES);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(k, dim3((unsigned)BHN), dim3(TokBwdLds<D>::NTHR), TokBwdLds<D>::BYTES, stream, t);

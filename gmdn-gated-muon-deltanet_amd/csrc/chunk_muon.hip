@@ -297,6 +297,18 @@ static hipError_t launch_muon(const ChunkArgs& a, float* S_out, float* M_out, in
   return hipGetLastError();
 }
 
+hipError_t chunk_out_launch(const ChunkArgs& a, int d, const float* S_all, hipStream_t s) {
+  if (d == 128 || d == 64) {
+    auto ko = d == 128 ? chunk_out<128> : chunk_out<64>;
+    const int lo = d == 128 ? OutLds<128>::BYTES : OutLds<64>::BYTES;
+    hipError_t e = hipFuncSetAttribute((const void*)ko, hipFuncAttributeMaxDynamicSharedMemorySize, lo);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(ko, dim3((unsigned)(a.B * a.H * a.N)), dim3(d * 4), lo, s, a, S_all);
+    return hipGetLastError();
+  }
+  return hipErrorInvalidValue;
+}
+
 hipError_t chunk_fwd_muon_launch(const ChunkArgs& a, int d, float* S_out, float* M_out, int ns, hipStream_t s) {
   if (d == 128) return launch_muon<128>(a, S_out, M_out, ns, s);
   if (d == 64) return launch_muon<64>(a, S_out, M_out, ns, s);

@@ -1,19 +1,22 @@
 // Level B: the per-chunk matrices of the reference's matrix form
-// (train_ablation.py:161-167, :186), chunk-parallel, for the rules whose
-// backward runs the drop-in scan's backward kernels (muon):
+// (train_ablation.py:161-167, :186), chunk-parallel, for the paths that run
+// the drop-in scan kernels between chunk-parallel stages (muon's backward;
+// adam's training at d = 128, whose scan runs in exact float32):
 //
-//   Kw = K^T diag(w) K,  Uv = V^T diag(w) K                  (:164-165)
-//   gS = dL/dS_i = dO^T Qt = dO^T Q - (A^T dO)^T K           (:166, :186)
-//   a = exp(sum max(g, log 1e-6)), b = mean beta, m = exp(sum max(gmu, log 1e-6))
+//   FWD: Kw = K^T diag(w) K,  Uv = V^T diag(w) K               (:164-165)
+//   BWD: gS = dL/dS_i = dO^T Qt = dO^T Q - (A^T dO)^T K        (:166, :186)
+//   a = exp(sum max(g, log 1e-6)), b = mean beta, m = exp(sum max(gmu, log 1e-6)),
+//   n = exp(sum max(gnu, log 1e-6)) (adam; 1 for muon)
 //
 // with A = tril(Q K^T) diag(beta) and the rule's token weights w (muon:
-// w_t = exp(sum_{s > t} max(gmu_s, log 1e-6)), :154-156).  One workgroup of
-// D/16 waves per (b, h, chunk); every product contracts the chunk's 64
-// tokens.  Wave w forms rows 16w .. 16w+15 of each d x d output from
+// w_t = exp(sum_{s > t} max(gmu_s, log 1e-6)), :154-156; adam: 1, :158).
+// One workgroup of D/16 waves per (b, h, chunk); every product contracts the
+// chunk's 64 tokens.  Wave w forms rows 16w .. 16w+15 of each d x d output from
 // transposed tiles (lane <-> output row, registers <-> four consecutive
 // columns), so each lane stores 16 contiguous bytes per tile.
 #include "../../include/gmdn_scan.h"
 #include "chunk_b.h"
+#include "scan_a.h"
 
 namespace gmdn {
 
@@ -32,11 +35,11 @@ struct PrepLds {
   static_assert(BYTES <= 160 * 1024, "prep LDS exceeds the 160 KiB of a CU");
 };
 
-template <int D>
-__global__ void __launch_bounds__(PrepLds<D>::NTHR) chunk_prep_muon(ChunkArgs p, float* __restrict__ Kw,
-                                                                   float* __restrict__ Uv,
-                                                                   float* __restrict__ gS,
-                                                                   float* __restrict__ abm) {
+template <int D, int RULE, bool FWD, bool BWD>
+__global__ void __launch_bounds__(PrepLds<D>::NTHR) chunk_prep(ChunkArgs p, float* __restrict__ Kw,
+                                                              float* __restrict__ Uv, float* __restrict__ gS,
+                                                              float* __restrict__ abm) {
+  static_assert(RULE == 1 || RULE == 2, "the matrix-form stages serve muon and adam");
   using LQ = BSwz<D>;
   using LA = BSwz<CB_C>;
   using L = PrepLds<D>;
@@ -64,31 +67,40 @@ __global__ void __launch_bounds__(PrepLds<D>::NTHR) chunk_prep_muon(ChunkArgs p,
   const int64_t mat = (int64_t)D * D;
 
   // ---- tiles and gates
-  float gbeta = 0.f, gg = 0.f, gm = 0.f;
+  float gbeta = 0.f, gg = 0.f, gm = 0.f, gn = 0.f;
   if (w == 0) {
     const int64_t e = bh * p.T + t0 + l;
     gbeta = p.beta[e];
     gg = p.g[e];
     gm = p.gmu[e];
+    if constexpr (RULE == 2) gn = p.gnu[e];
   }
   {
-    DmaPlan<LQ, CB_C, NTHR> pq, pk, pv, po;
-    pq.init(w, p.sq[2]);
+    DmaPlan<LQ, CB_C, NTHR> pk;
     pk.init(w, p.sk[2]);
-    pv.init(w, p.sv[2]);
-    po.init(w, p.so[2]);
     const uint32_t lds0 = lds_addr(smem);
-    pq.issue(p.q + bb * p.sq[0] + hh * p.sq[1] + t0 * p.sq[2], lds0 + L::Q0, w);
     pk.issue(p.k + bb * p.sk[0] + hh * p.sk[1] + t0 * p.sk[2], lds0 + L::K0, w);
-    pv.issue(p.v + bb * p.sv[0] + hh * p.sv[1] + t0 * p.sv[2], lds0 + L::V0, w);
-    po.issue(p.o + bb * p.so[0] + hh * p.so[1] + t0 * p.so[2], lds0 + L::O0, w);
+    if constexpr (FWD) {
+      DmaPlan<LQ, CB_C, NTHR> pv;
+      pv.init(w, p.sv[2]);
+      pv.issue(p.v + bb * p.sv[0] + hh * p.sv[1] + t0 * p.sv[2], lds0 + L::V0, w);
+    }
+    if constexpr (BWD) {
+      DmaPlan<LQ, CB_C, NTHR> pq, po;
+      pq.init(w, p.sq[2]);
+      po.init(w, p.so[2]);
+      pq.issue(p.q + bb * p.sq[0] + hh * p.sq[1] + t0 * p.sq[2], lds0 + L::Q0, w);
+      po.issue(p.o + bb * p.so[0] + hh * p.so[1] + t0 * p.so[2], lds0 + L::O0, w);
+    }
   }
   wait_vmem();
   if (w == 0) {
+    const int64_t BHN = p.B * p.H * p.N;
     const float lg = fmaxf(gg, LOG_FLOOR), lm = fmaxf(gm, LOG_FLOOR);
     const float a = expf(wave_sum(lg));
     const float b = wave_sum(gbeta) * (1.f / CB_C);
     const float msum = wave_sum(lm);
+    const float n = RULE == 2 ? expf(wave_sum(fmaxf(gn, LOG_FLOOR))) : 1.f;
     float incl = lm;  // inclusive prefix sum over the tokens
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
@@ -96,135 +108,186 @@ __global__ void __launch_bounds__(PrepLds<D>::NTHR) chunk_prep_muon(ChunkArgs p,
       if (l >= o) incl += y;
     }
     rbeta[l] = gbeta;
-    rw[l] = expf(msum - incl);  // w_t = exp(sum_{s > t} lm_s)
+    rw[l] = RULE == 1 ? expf(msum - incl) : 1.f;  // muon: w_t = exp(sum_{s > t} lm_s)
     if (l == 0) {
       abm[si] = a;
-      abm[p.B * p.H * p.N + si] = b;
-      abm[2 * p.B * p.H * p.N + si] = expf(msum);
+      abm[BHN + si] = b;
+      abm[2 * BHN + si] = expf(msum);
+      abm[3 * BHN + si] = n;
     }
   }
   __syncthreads();
 
-  // ---- w K (split planes) and A^T (split planes, tiles above the diagonal zero)
-  for (int e = threadIdx.x; e < CB_C * D / 8; e += NTHR) {
-    const int t = e / (D / 8), c8 = (e % (D / 8)) * 8;
-    const int off = LQ::off(t, c8);
-    const bf16x8 kv = *reinterpret_cast<const bf16x8*>(Ks + off);
-    const float wt = rw[t];
-    bf16x8 hi, lo;
+  if constexpr (FWD) {
+    // ---- w K (split planes)
+    for (int e = threadIdx.x; e < CB_C * D / 8; e += NTHR) {
+      const int t = e / (D / 8), c8 = (e % (D / 8)) * 8;
+      const int off = LQ::off(t, c8);
+      const bf16x8 kv = *reinterpret_cast<const bf16x8*>(Ks + off);
+      const float wt = rw[t];
+      bf16x8 hi, lo;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      bf16 h, o;
-      split2(wt * (float)kv[j], h, o);
-      hi[j] = h;
-      lo[j] = o;
+      for (int j = 0; j < 8; ++j) {
+        bf16 h, o;
+        split2(wt * (float)kv[j], h, o);
+        hi[j] = h;
+        lo[j] = o;
+      }
+      *reinterpret_cast<bf16x8*>(Wh + off) = hi;
+      *reinterpret_cast<bf16x8*>(Wl + off) = lo;
     }
-    *reinterpret_cast<bf16x8*>(Wh + off) = hi;
-    *reinterpret_cast<bf16x8*>(Wl + off) = lo;
   }
+  if constexpr (BWD) {
+    // ---- A^T (split planes, tiles above the diagonal zero)
 #pragma unroll
-  for (int kk = 0; kk < 16 / NW; ++kk) {
-    const int k = w + NW * kk, tt = k >> 2, st = k & 3;
-    bf16x4 ah, al;
-    if (tt < st) {
-      ah = al = bf16x4{(bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f};
-    } else {
-      f32x4 X = zero4();
+    for (int kk = 0; kk < 16 / NW; ++kk) {
+      const int k = w + NW * kk, tt = k >> 2, st = k & 3;
+      bf16x4 ah, al;
+      if (tt < st) {
+        ah = al = bf16x4{(bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f};
+      } else {
+        f32x4 X = zero4();
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb)
-        X = mfma(row8<LQ>(Qs, 16 * tt + lc, 32 * kb), row8<LQ>(Ks, 16 * st + lc, 32 * kb), X);
-      // lane (s, G) holds A[t = 16 tt + 4G + jj][s = 16 st + lc]
-      const float bs = rbeta[16 * st + lc];
+        for (int kb = 0; kb < NKB; ++kb)
+          X = mfma(row8<LQ>(Qs, 16 * tt + lc, 32 * kb), row8<LQ>(Ks, 16 * st + lc, 32 * kb), X);
+        // lane (s, G) holds A[t = 16 tt + 4G + jj][s = 16 st + lc]
+        const float bs = rbeta[16 * st + lc];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const float x = (tt > st || 4 * G + jj >= lc) ? X[jj] * bs : 0.f;
+          bf16 hv, lv;
+          split2(x, hv, lv);
+          ah[jj] = hv;
+          al[jj] = lv;
+        }
+      }
+      const int ao = LA::off(16 * st + lc, 16 * tt + 4 * G);
+      *reinterpret_cast<bf16x4*>(Ah + ao) = ah;
+      *reinterpret_cast<bf16x4*>(Al + ao) = al;
+    }
+    __syncthreads();  // A^T published (w K too, when formed)
+
+    // ---- P = A^T dO for this wave's 16 dO columns r0 .. : lane (s, G) of tile
+    // st holds P^T[r0 + 4G + jj][16 st + s]; published as [s][r] split planes
+    const int r0 = 16 * w;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      f32x4 Pt = zero4();
+#pragma unroll
+      for (int kbt = 0; kbt < 2; ++kbt) {
+        if (32 * kbt + 31 < 16 * st) continue;
+        const Op<1> dOt{{col8<LQ>(Os, 32 * kbt, r0)}};
+        const Op<2> At{{row8<LA>(Ah, 16 * st + lc, 32 * kbt), row8<LA>(Al, 16 * st + lc, 32 * kbt)}};
+        Pt = mma<1, 2>(dOt, At, Pt);
+      }
+      bf16x4 h4, l4;
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
-        const float x = (tt > st || 4 * G + jj >= lc) ? X[jj] * bs : 0.f;
         bf16 hv, lv;
-        split2(x, hv, lv);
-        ah[jj] = hv;
-        al[jj] = lv;
+        split2(Pt[jj], hv, lv);
+        h4[jj] = hv;
+        l4[jj] = lv;
       }
+      const int po = LQ::off(16 * st + lc, r0 + 4 * G);
+      *reinterpret_cast<bf16x4*>(Ph + po) = h4;
+      *reinterpret_cast<bf16x4*>(Pl + po) = l4;
     }
-    const int ao = LA::off(16 * st + lc, 16 * tt + 4 * G);
-    *reinterpret_cast<bf16x4*>(Ah + ao) = ah;
-    *reinterpret_cast<bf16x4*>(Al + ao) = al;
   }
   __syncthreads();
 
-  // ---- P = A^T dO for this wave's 16 dO columns r0 .. : lane (s, G) of tile
-  // st holds P^T[r0 + 4G + jj][16 st + s]; published as [s][r] split planes
-  const int r0 = 16 * w;
-#pragma unroll
-  for (int st = 0; st < 4; ++st) {
-    f32x4 Pt = zero4();
-#pragma unroll
-    for (int kbt = 0; kbt < 2; ++kbt) {
-      if (32 * kbt + 31 < 16 * st) continue;
-      const Op<1> dOt{{col8<LQ>(Os, 32 * kbt, r0)}};
-      const Op<2> At{{row8<LA>(Ah, 16 * st + lc, 32 * kbt), row8<LA>(Al, 16 * st + lc, 32 * kbt)}};
-      Pt = mma<1, 2>(dOt, At, Pt);
-    }
-    bf16x4 h4, l4;
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      bf16 hv, lv;
-      split2(Pt[jj], hv, lv);
-      h4[jj] = hv;
-      l4[jj] = lv;
-    }
-    const int po = LQ::off(16 * st + lc, r0 + 4 * G);
-    *reinterpret_cast<bf16x4*>(Ph + po) = h4;
-    *reinterpret_cast<bf16x4*>(Pl + po) = l4;
-  }
-  __syncthreads();
-
-  // ---- the three d x d outputs, rows a0 + lc of each: out[a][b] = sum_t X[t][a] Y[t][b]
+  // ---- the d x d outputs, rows a0 + lc of each: out[a][b] = sum_t X[t][a] Y[t][b]
   // as transposed tiles D[b][a] (A operand: Y columns b, B operand: X columns a)
   const int a0 = 16 * w;
-  Op<1> Vc[2], Oc[2];
-  Op<2> Wc[2], Pc[2];
-#pragma unroll
-  for (int kt = 0; kt < 2; ++kt) {
-    Vc[kt].v[0] = col8<LQ>(Vs, 32 * kt, a0);
-    Oc[kt].v[0] = col8<LQ>(Os, 32 * kt, a0);
-    Wc[kt] = Op<2>{{col8<LQ>(Wh, 32 * kt, a0), col8<LQ>(Wl, 32 * kt, a0)}};
-    Pc[kt] = Op<2>{{col8<LQ>(Ph, 32 * kt, a0), col8<LQ>(Pl, 32 * kt, a0)}};
-  }
-  float* kwo = Kw + si * mat + (int64_t)(a0 + lc) * D + 4 * G;
-  float* uvo = Uv + si * mat + (int64_t)(a0 + lc) * D + 4 * G;
-  float* gso = gS + si * mat + (int64_t)(a0 + lc) * D + 4 * G;
-#pragma unroll
-  for (int bt = 0; bt < NT; ++bt) {
-    f32x4 kw = zero4(), uv = zero4(), gs = zero4();
+  const int64_t orow = si * mat + (int64_t)(a0 + lc) * D + 4 * G;
+  if constexpr (FWD) {
+    Op<1> Vc[2];
+    Op<2> Wc[2];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
-      const bf16x8 kcol = col8<LQ>(Ks, 32 * kt, 16 * bt);
-      const Op<2> wcol{{col8<LQ>(Wh, 32 * kt, 16 * bt), col8<LQ>(Wl, 32 * kt, 16 * bt)}};
-      kw = mma<1, 2>(Op<1>{{kcol}}, Wc[kt], kw);                      // sum_t K[t][b] (w K)[t][a]
-      uv = mma<2, 1>(wcol, Vc[kt], uv);                               // sum_t (w K)[t][b] V[t][a]
-      gs = mma<1, 1>(Op<1>{{col8<LQ>(Qs, 32 * kt, 16 * bt)}}, Oc[kt], gs);  // sum_t Q[t][b] dO[t][a]
-      gs = mma<1, 2>(Op<1>{{neg8(kcol)}}, Pc[kt], gs);                 // - sum_t K[t][b] P[t][a]
+      Vc[kt].v[0] = col8<LQ>(Vs, 32 * kt, a0);
+      Wc[kt] = Op<2>{{col8<LQ>(Wh, 32 * kt, a0), col8<LQ>(Wl, 32 * kt, a0)}};
     }
-    *reinterpret_cast<f32x4*>(kwo + 16 * bt) = kw;
-    *reinterpret_cast<f32x4*>(uvo + 16 * bt) = uv;
-    *reinterpret_cast<f32x4*>(gso + 16 * bt) = gs;
+#pragma unroll
+    for (int bt = 0; bt < NT; ++bt) {
+      f32x4 kw = zero4(), uv = zero4();
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        const Op<2> wcol{{col8<LQ>(Wh, 32 * kt, 16 * bt), col8<LQ>(Wl, 32 * kt, 16 * bt)}};
+        kw = mma<1, 2>(Op<1>{{col8<LQ>(Ks, 32 * kt, 16 * bt)}}, Wc[kt], kw);  // sum_t K[t][b] (w K)[t][a]
+        uv = mma<2, 1>(wcol, Vc[kt], uv);                                     // sum_t (w K)[t][b] V[t][a]
+      }
+      *reinterpret_cast<f32x4*>(Kw + orow + 16 * bt) = kw;
+      *reinterpret_cast<f32x4*>(Uv + orow + 16 * bt) = uv;
+    }
+  }
+  if constexpr (BWD) {
+    Op<1> Oc[2];
+    Op<2> Pc[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      Oc[kt].v[0] = col8<LQ>(Os, 32 * kt, a0);
+      Pc[kt] = Op<2>{{col8<LQ>(Ph, 32 * kt, a0), col8<LQ>(Pl, 32 * kt, a0)}};
+    }
+#pragma unroll
+    for (int bt = 0; bt < NT; ++bt) {
+      f32x4 gs = zero4();
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        gs = mma<1, 1>(Op<1>{{col8<LQ>(Qs, 32 * kt, 16 * bt)}}, Oc[kt], gs);           // sum_t Q[t][b] dO[t][a]
+        gs = mma<1, 2>(Op<1>{{neg8(col8<LQ>(Ks, 32 * kt, 16 * bt))}}, Pc[kt], gs);     // - sum_t K[t][b] P[t][a]
+      }
+      *reinterpret_cast<f32x4*>(gS + orow + 16 * bt) = gs;
+    }
   }
 }
 
-hipError_t chunk_prep_muon_launch(const ChunkArgs& a, int d, float* Kw, float* Uv, float* gS, float* abm,
-                                  hipStream_t s) {
-  const int64_t grid = a.B * a.H * a.N;
-  if (d == 128) {
-    auto k = chunk_prep_muon<128>;
-    hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, PrepLds<128>::BYTES);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(PrepLds<128>::NTHR), PrepLds<128>::BYTES, s, a, Kw, Uv, gS, abm);
-  } else {
-    auto k = chunk_prep_muon<64>;
-    hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, PrepLds<64>::BYTES);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(PrepLds<64>::NTHR), PrepLds<64>::BYTES, s, a, Kw, Uv, gS, abm);
-  }
+template <int D, int RULE, bool FWD, bool BWD>
+static hipError_t launch_prep(const ChunkArgs& a, float* Kw, float* Uv, float* gS, float* abm, hipStream_t s) {
+  auto k = chunk_prep<D, RULE, FWD, BWD>;
+  hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, PrepLds<D>::BYTES);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k, dim3((unsigned)(a.B * a.H * a.N)), dim3(PrepLds<D>::NTHR), PrepLds<D>::BYTES, s, a, Kw, Uv,
+                     gS, abm);
   return hipGetLastError();
+}
+
+hipError_t chunk_prep_launch(const ChunkArgs& a, int d, int rule, bool fwd, bool bwd, float* Kw, float* Uv,
+                             float* gS, float* abm, hipStream_t s) {
+  // muon's backward: Kw, Uv and gS; adam: Kw, Uv (training forward), gS (backward)
+  if (d == 128) {
+    if (rule == 1 && fwd && bwd) return launch_prep<128, 1, true, true>(a, Kw, Uv, gS, abm, s);
+    if (rule == 2 && fwd && !bwd) return launch_prep<128, 2, true, false>(a, Kw, Uv, gS, abm, s);
+    if (rule == 2 && !fwd && bwd) return launch_prep<128, 2, false, true>(a, Kw, Uv, gS, abm, s);
+  } else if (d == 64) {
+    if (rule == 1 && fwd && bwd) return launch_prep<64, 1, true, true>(a, Kw, Uv, gS, abm, s);
+  }
+  return hipErrorNotSupported;
+}
+
+// Adam at d = 128, training forward: Kw, Uv and the chunk scalars, the
+// drop-in adam scan in exact float32 (S, M, V of every chunk), then
+// o = Q S_i^T + A E from S_i.  states = [S | M | V | Kw | Uv | a b m n].
+size_t chunk_adam_mat_states_floats(int64_t BH, int64_t N, int d) {
+  return (size_t)(5 * BH * N * (int64_t)d * d + 4 * BH * N);
+}
+
+hipError_t chunk_fwd_adam_mat_launch(const ChunkArgs& a, int d, float* states, hipStream_t s) {
+  if (d != 128) return hipErrorNotSupported;
+  const int64_t BH = a.B * a.H, BHN = BH * a.N, mat = (int64_t)d * d;
+  float* S = states;
+  float* Kw = S + 3 * BHN * mat;
+  float* Uv = S + 4 * BHN * mat;
+  float* abm = S + 5 * BHN * mat;
+  hipError_t e = chunk_prep_launch(a, d, 2, true, false, Kw, Uv, nullptr, abm, s);
+  if (e != hipSuccess) return e;
+  ScanArgs sa{};
+  sa.U = Uv; sa.K = Kw; sa.a = abm; sa.b = abm + BHN; sa.m = abm + 2 * BHN; sa.n = abm + 3 * BHN;
+  sa.S_all = S; sa.M_all = S + BHN * mat; sa.V_all = S + 2 * BHN * mat;
+  sa.BH = BH; sa.N = a.N; sa.dh = d; sa.rule = 2; sa.ns = 0; sa.precision = GMDN_PREC_IEEE;
+  sa.stream = s;
+  e = scan_fwd_rows_launch(sa);
+  if (e != hipSuccess) return e;
+  return chunk_out_launch(a, d, S, s);
 }
 
 }  // namespace gmdn

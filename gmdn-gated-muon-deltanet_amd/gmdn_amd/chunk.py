@@ -25,9 +25,10 @@ streams the k, v tiles and forms each chunk's update in the E-form before
 the Newton-Schulz steps, plus a chunk-parallel output kernel; its backward
 is HIP too: a chunk-parallel kernel forms each chunk's Kw, Uv and dL/dS_i,
 the drop-in muon scan's backward kernels run the Newton-Schulz VJP, and the
-token-gradient kernel finishes in the E-form.  Adam at d = 128 trains through the drop-in scan with
-phases 1 and 3 as batched GEMMs around it, the scan in exact float32 (its
-inference forward stays fused).
+token-gradient kernel finishes in the E-form.  Adam at d = 128 trains with
+its scan in exact float32: a chunk-parallel kernel forms Kw, Uv, the drop-in
+adam scan kernels run forward and backward, the output and token-gradient
+kernels work from the float32 states (its inference forward stays fused).
 """
 from __future__ import annotations
 
@@ -36,7 +37,6 @@ import math
 import torch
 
 from . import ops  # noqa: F401  -- registers torch.ops.gmdn.*
-from .scan import hip_state_scan
 
 RULES = {"delta": 0, "muon": 1, "adam": 2}
 CHUNK = 64
@@ -49,19 +49,17 @@ BWD_RULES = (0, 1, 2)  # rules with a backward
 
 def backward_supported(rule, d: int = 128) -> bool:
     """Whether ``rule`` at head dim ``d`` has a backward: every rule and head
-    dim.  (The fused adam backward kernel is limited to d = 64 -- at d = 128
-    its sign-like update amplifies the rounding of the split-bf16 state
-    products past the gradient tolerance -- so adam at d = 128 trains through
-    the composed path of ``_composed_core``.)"""
+    dim.  (Adam at d = 128 trains with its scan in exact float32: at that head
+    dim its sign-like update amplifies the rounding of split-bf16 state
+    products past the gradient tolerance.)"""
     return _rule_id(rule) in BWD_RULES
 
 
 def fused_backward(rule, d: int) -> bool:
-    """Whether ``rule`` at head dim ``d`` trains through the fused forward
-    (delta and adam at d = 64; muon at both head dims, its Newton-Schulz
-    VJP through the drop-in scan's backward kernels)."""
-    r = _rule_id(rule)
-    return r in (0, 1) or (r == 2 and d == 64)
+    """Whether ``rule`` at head dim ``d`` trains through the fused op
+    ``gmdn::chunk_fwd`` and its HIP backward: every rule and head dim."""
+    _rule_id(rule)
+    return d in SUPPORTED_D
 
 
 def _rule_id(rule) -> int:
@@ -96,45 +94,6 @@ def _check(q, k, v, beta, g, gmu, gnu, rule):
         raise RuntimeError("adam rule needs gnu")
 
 
-def _composed_core(q, k, v, beta, g, gmu, gnu, rule, ns, precision=None):
-    """The mixer core as the reference composes it: phases 1 and 3
-    (train_ablation.py:150-167, :184-187) as plain batched GEMMs in float32
-    around the drop-in scan kernels, with autograd supplying the backward
-    through the scan's own backward kernels.
-
-    Adam at d = 128 trains this way with the scan in exact float32
-    (precision 'ieee'), where the fused kernels' split products would exceed
-    the gradient tolerance."""
-    B, H, T, d = q.shape
-    N = T // CHUNK
-    qf, kf, vf = (t.float().reshape(B, H, N, CHUNK, d) for t in (q, k, v))
-    bt = beta.float().reshape(B, H, N, CHUNK)
-    lg = torch.clamp(g.float(), min=LOG_FLOOR).reshape(B, H, N, CHUNK)
-    lmu = torch.clamp(gmu.float(), min=LOG_FLOOR).reshape(B, H, N, CHUNK)
-    a = lg.sum(-1).exp()
-    b = bt.mean(-1)
-    m = lmu.sum(-1).exp()
-    if rule == 2:
-        n = torch.clamp(gnu.float(), min=LOG_FLOOR).reshape(B, H, N, CHUNK).sum(-1).exp()
-        w = torch.ones_like(bt)  # adam weighs every token of a chunk equally (train_ablation.py:158)
-    else:
-        n = torch.ones_like(m)
-        # token weights prod_{s' > s} mu_{s'} (train_ablation.py:154-156)
-        w = torch.exp(torch.flip(torch.cumsum(torch.flip(lmu, [-1]), -1), [-1]) - lmu)
-    causal = torch.tril(torch.ones(CHUNK, CHUNK, dtype=torch.bool, device=q.device))
-    # float32 batched products take the transposed views as they are (strided
-    # GEMM operands), so no transposed copy is made of k, the weighted tiles
-    # or the (B, H, N, d, d) state stack
-    A = torch.where(causal, torch.matmul(qf, kf.transpose(-1, -2)) * bt.unsqueeze(-2), 0.0)
-    Kw = torch.matmul((kf * w.unsqueeze(-1)).transpose(-1, -2), kf)
-    Uv = torch.matmul((vf * w.unsqueeze(-1)).transpose(-1, -2), kf)
-    Qt = qf - torch.matmul(A, kf)
-    Ov = torch.matmul(A, vf)
-    S_all = hip_state_scan(Uv, Kw, a, b, m, n, rule, ns, precision)
-    o = torch.matmul(Qt, S_all.transpose(-1, -2)) + Ov
-    return o.reshape(B, H, T, d).to(q.dtype)
-
-
 def chunk_scan(q, k, v, beta, g, gmu=None, gnu=None, *, rule="delta", ns: int = 3, eps: float = 1e-6):
     """Fused mixer core; see the module docstring."""
     r = _rule_id(rule)
@@ -143,11 +102,9 @@ def chunk_scan(q, k, v, beta, g, gmu=None, gnu=None, *, rule="delta", ns: int = 
     _check(q, k, v, beta, g, gmu, gnu, r)
     # the state checkpoint is written only when a backward can follow
     record = torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (q, k, v, beta, g, gmu, gnu))
-    if record and not fused_backward(r, q.shape[-1]):
-        if eps != 1e-6:
-            raise RuntimeError("adam at d = 128 trains through the drop-in scan, whose epsilon is 1e-6 "
-                               f"(fast_scan.py:94); got eps={eps}")
-        return _composed_core(q, k, v, beta, g, gmu, gnu, r, ns, precision="ieee")
+    if record and r == 2 and q.shape[-1] == 128 and eps != 1e-6:
+        raise RuntimeError("adam at d = 128 trains through the drop-in scan, whose epsilon is 1e-6 "
+                           f"(fast_scan.py:94); got eps={eps}")
     gates = [None if t is None else t.to(torch.float32) for t in (beta, g, gmu, gnu)]
     o, _ = torch.ops.gmdn.chunk_fwd(q, k, v, *gates, r, ns, eps, record)
     return o

@@ -285,9 +285,6 @@ def _chunk_fwd_backward(ctx, dO, dstates):
     if not ctx.record:
         raise RuntimeError("gmdn::chunk_fwd ran without recording its state checkpoint "
                            "(grad mode was off at the call); it has no backward")
-    if ctx.rule == 2 and q.shape[-1] != 64:
-        raise RuntimeError(f"the fused backward of rule 2 at head dim {q.shape[-1]} is not built "
-                           "(adam's backward is built at d = 64)")
     if ctx.rule == 1:
         from .scan import _prec_code
         dq, dk, dv, dbeta, dg, dgmu = torch.ops.gmdn.chunk_bwd_muon(q, k, v, beta, g, gmu, states, dO, ctx.ns,

@@ -254,15 +254,35 @@ def _grads_vs_f32(w, seed=0):
 
 @pytest.mark.parametrize("seed", [1, 2])
 def test_adam_grads_d128(seed):
-    """Adam at d = 128 trains through the composed path (float32 batched
-    GEMMs around the drop-in scan in exact float32), since the fused
-    kernels' split products exceed the gradient tolerance there.  Its
-    sign-like update makes dk and dv ill-conditioned already at T = 256 (the
-    bf16 rounding of the float64 gradient alone is 0.11 and 0.15 of RMS), so
-    the gradients are bounded as in the full-size adam case."""
-    assert not gc.fused_backward("adam", 128) and gc.backward_supported("adam", 128)
+    """Adam at d = 128 trains with its scan in exact float32 (the drop-in adam
+    scan kernels between the chunk-parallel Kw/Uv, output, dL/dS and token
+    kernels), since split-bf16 state products exceed the gradient tolerance
+    there.  Its sign-like update makes dk and dv ill-conditioned already at
+    T = 256 (the bf16 rounding of the float64 gradient alone is 0.11 and 0.15
+    of RMS), so the gradients are bounded as in the full-size adam case."""
+    assert gc.fused_backward("adam", 128) and gc.backward_supported("adam", 128)
     bad = _adam_grads_vs_f32(Workload("t", "adam", 1, 2, 256, 128), seed=seed)
     assert not bad, bad
+
+
+def test_adam_d128_training_forward_matches_inference():
+    """The adam d = 128 training forward (exact float32 scan) and the fused
+    inference forward (split-bf16) agree to the bf16 bound."""
+    dev = _dev()
+    w = Workload("t", "adam", 1, 4, 1024, 128)
+    inp = make_inputs(w, seed=8, with_grad_out=False)
+    d = {k: (None if t is None else t.to(dev)) for k, t in inp.items()}
+    with torch.no_grad():
+        o_inf = gc.chunk_scan(d["q"], d["k"], d["v"], d["beta"], d["g"], d["gmu"], d["gnu"], rule="adam")
+    xs = {k: (None if t is None else t.detach().requires_grad_(True)) for k, t in d.items()}
+    o_tr = gc.chunk_scan(xs["q"], xs["k"], xs["v"], xs["beta"], xs["g"], xs["gmu"], xs["gnu"], rule="adam")
+    torch.cuda.synchronize()
+    ref = _oracle(inp, w).float()
+    rms = ref.pow(2).mean().sqrt()
+    for name, o in (("inference", o_inf), ("training", o_tr)):
+        excess = ((o.detach().float().cpu() - ref).abs() - _bf16_half_ulp(ref)).clamp_min(0).max() / rms
+        print(f"adam d128 {name} forward: excess over half a bf16 ulp {excess.item():.2e}")
+        assert excess <= TOL, (name, excess.item())
 
 
 def test_adam_grads_config():
