@@ -192,8 +192,10 @@ size_t gmdn_chunk_bwd_workspace_bytes(const gmdn_chunk_desc* desc);
  * (contiguous (B, H, T) float32).  Matches torch autograd through the
  * reference's phases 1-3 and scan_eager.  Rule 1 (muon) forms each chunk's
  * Kw, Uv and dL/dS_i, runs the drop-in muon reverse scan (Newton-Schulz VJP
- * in desc->precision) on the forward's S_i, M_i, then the token gradients;
- * adam (rule 2) is built at d = 64. */
+ * in desc->precision) on the forward's S_i, M_i, then the token gradients.
+ * Adam (rule 2) at d = 128 runs the drop-in adam scan in exact float32
+ * between chunk-parallel kernels, forward (when `states` is requested) and
+ * backward; its epsilon must then be the reference's 1e-6. */
 int gmdn_chunk_bwd(const gmdn_chunk_desc* desc, const void* q, const void* k,
                    const void* v, const float* beta, const float* g,
                    const float* gmu, const float* gnu, const void* states,
