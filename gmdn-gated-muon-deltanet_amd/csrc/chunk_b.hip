@@ -14,6 +14,8 @@
 // (train_ablation.py:150-158, :169-175).  Only q, k, v, beta and the
 // log-gates stream from HBM; o streams out; S stays in registers.
 //
+// The delta rule's forward runs chunk_fwd_delta (csrc/chunk_fwd_delta.hip);
+// the kernel below serves adam.
 // Work split (forward).  A workgroup of 4 waves owns 32 rows of S for the
 // whole sequence; wave (rt, h) owns row tile rt (16 rows) and column half h
 // of S, the token half h of E and of o, and the column half h of G.  Two LDS
@@ -198,13 +200,7 @@ __global__ void __launch_bounds__(FW_THREADS) chunk_fwd(ChunkArgs p) {
   // split a D-layout tile into hi / lo bf16 and store both 8-byte pieces
   auto put_split = [&](uint32_t off, uint32_t plane, const f32x4& x) {
     bf16x4 hi, lo;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      bf16 a_, b_;
-      split2(x[j], a_, b_);
-      hi[j] = a_;
-      lo[j] = b_;
-    }
+    split4(x, hi, lo);
     lds_st<bf16x4>(L0 + off, hi);
     lds_st<bf16x4>(L0 + (off + plane), lo);
   };
@@ -260,15 +256,11 @@ __global__ void __launch_bounds__(FW_THREADS) chunk_fwd(ChunkArgs p) {
     for (int kb = 0; kb < NKB; ++kb) acc = mfma(ka[kb], qa[kb], acc);
     // lane (t, G) holds (Q K^T)[t][s] for s = 16 st + 4G + j
     const f32x4 bs = *reinterpret_cast<const f32x4*>(gates + 16 * st + 4 * G);
-    bf16x4 hi4, lo4;
+    f32x4 val;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float val = (st < tt || 4 * G + j <= lc) ? -acc[j] * bs[j] : 0.f;
-      bf16 hv, lv;
-      split2(val, hv, lv);
-      hi4[j] = hv;
-      lo4[j] = lv;
-    }
+    for (int j = 0; j < 4; ++j) val[j] = (st < tt || 4 * G + j <= lc) ? -acc[j] * bs[j] : 0.f;
+    bf16x4 hi4, lo4;
+    split4(val, hi4, lo4);
     const int ao = LA::off(16 * tt + lc, 16 * st + 4 * G);
     *reinterpret_cast<bf16x4*>(Ahi + ao) = hi4;
     *reinterpret_cast<bf16x4*>(Alo + ao) = lo4;
@@ -436,7 +428,7 @@ __global__ void __launch_bounds__(FW_THREADS) chunk_fwd(ChunkArgs p) {
 #pragma unroll
       for (int u = 0; u < 2; ++u)
         *reinterpret_cast<bf16x4*>(stage + (16 * u + lc) * 16 + 4 * G) =
-            bf16x4{(bf16)O[u][0], (bf16)O[u][1], (bf16)O[u][2], (bf16)O[u][3]};
+            to_bf16x4(O[u]);
       const int tok = l >> 1, half = l & 1;  // lanes: 32 tokens x 2 pieces of 8 columns
       const bf16x8 piece = *reinterpret_cast<const bf16x8*>(stage + tok * 16 + 8 * half);
       *reinterpret_cast<bf16x8*>(og - lc + ((int64_t)i * CB_C + 32 * h + tok) * p.so[2] + 8 * half) = piece;
@@ -505,8 +497,8 @@ static hipError_t launch_fwd(const ChunkArgs& a, hipStream_t stream) {
 }
 
 hipError_t chunk_fwd_launch(const ChunkArgs& a, int d, int rule, hipStream_t s) {
-  if (d == 128) return rule == 0 ? launch_fwd<128, 0>(a, s) : launch_fwd<128, 2>(a, s);
-  return rule == 0 ? launch_fwd<64, 0>(a, s) : launch_fwd<64, 2>(a, s);
+  if (rule == 0) return chunk_fwd_delta_launch(a, d, s);
+  return d == 128 ? launch_fwd<128, 2>(a, s) : launch_fwd<64, 2>(a, s);
 }
 
 }  // namespace gmdn

@@ -499,13 +499,7 @@ __global__ void __launch_bounds__(DS_THREADS) chunk_bwd_dstate(ChunkArgs p) {
     }
     auto put_split = [&](uint32_t off, uint32_t plane, const f32x4& x) {
       bf16x4 hi, lo;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        bf16 a_, b_;
-        split2(x[j], a_, b_);
-        hi[j] = a_;
-        lo[j] = b_;
-      }
+      split4(x, hi, lo);
       lds_st<bf16x4>(L0 + off, hi);
       lds_st<bf16x4>(L0 + (off + plane), lo);
     };
@@ -913,14 +907,10 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
         X = mfma(row8<LQ>(Qs, 16 * tt + lc, 32 * kb), row8<LQ>(Ks, 16 * st + lc, 32 * kb), X);
       // lane (s, G) holds A[t = 16 tt + 4G + jj][s = 16 st + lc]
       const float bs = rbeta[16 * st + lc];
+      f32x4 xv;
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        const float x = (tt > st || 4 * G + jj >= lc) ? X[jj] * bs : 0.f;
-        bf16 hi, lo;
-        split2(x, hi, lo);
-        ah[jj] = hi;
-        al[jj] = lo;
-      }
+      for (int jj = 0; jj < 4; ++jj) xv[jj] = (tt > st || 4 * G + jj >= lc) ? X[jj] * bs : 0.f;
+      split4(xv, ah, al);
     }
     const int ao = LA::off(16 * st + lc, 16 * tt + 4 * G);
     *reinterpret_cast<bf16x4*>(Ah + ao) = ah;
@@ -972,16 +962,8 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
         dEt = mma<1, 2>(dOt, At, dEt);  // (k = t, n = s)
       }
       bf16x4 eh, el, dh, dl;
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        bf16 x, y;
-        split2(Et[jj], x, y);
-        eh[jj] = x;
-        el[jj] = y;
-        split2(dEt[jj], x, y);
-        dh[jj] = x;
-        dl[jj] = y;
-      }
+      split4(Et, eh, el);
+      split4(dEt, dh, dl);
       const int eo = LQ::off(16 * st + lc, r0 + 4 * G);
       *reinterpret_cast<bf16x4*>(Eh + eo) = eh;
       *reinterpret_cast<bf16x4*>(El + eo) = el;
@@ -1044,15 +1026,14 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
       }
       const float bs = rbeta[16 * st + lc];
       float db = 0.f;
+      f32x4 pb;
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
         const float pv = (tt > st || 4 * G + jj >= lc) ? P[jj] : 0.f;
         db += pv * QK[jj];
-        bf16 x, y;
-        split2(pv * bs, x, y);
-        ah[jj] = x;
-        al[jj] = y;
+        pb[jj] = pv * bs;
       }
+      split4(pb, ah, al);
       dbk[kk] = db;
     }
     const int ao = LA::off(16 * st + lc, 16 * tt + 4 * G);
@@ -1211,7 +1192,7 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt)
     *reinterpret_cast<bf16x4*>(dqs + LQ::off(16 * tt + lc, j0 + 4 * G)) =
-        bf16x4{(bf16)dqa[tt][0], (bf16)dqa[tt][1], (bf16)dqa[tt][2], (bf16)dqa[tt][3]};
+        to_bf16x4(dqa[tt]);
 #pragma unroll
   for (int st = 0; st < 4; ++st) {
     f32x4 e = eg[st];
@@ -1219,7 +1200,7 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
     if constexpr (RULE == 1) e = e * rgnu[16 * st + lc];   // muon: w_t
     const f32x4 acc = dka[st] - des[st] + e;
     *reinterpret_cast<bf16x4*>(dks + LQ::off(16 * st + lc, j0 + 4 * G)) =
-        bf16x4{(bf16)acc[0], (bf16)acc[1], (bf16)acc[2], (bf16)acc[3]};
+        to_bf16x4(acc);
   }
   __syncthreads();
   for (int e = threadIdx.x; e < CB_C * D / 8; e += NTHR) {

@@ -117,13 +117,7 @@ struct PairCtx {
   // the D-layout tile t of a [s][r] matrix -> split planes at (s = 16 st + lc, r = r0 + 4G ..)
   GMDN_DEV void put_sr(bf16* hi, bf16* lo, int st, const f32x4& t) const {
     bf16x4 h, o;
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      bf16 x, y;
-      split2(t[jj], x, y);
-      h[jj] = x;
-      o[jj] = y;
-    }
+    split4(t, h, o);
     const int off = LQ::off(16 * st + lc, r0 + 4 * G);
     *reinterpret_cast<bf16x4*>(hi + off) = h;
     *reinterpret_cast<bf16x4*>(lo + off) = o;
@@ -188,14 +182,10 @@ struct PairCtx {
         for (int kb = 0; kb < NKB; ++kb)
           X = mfma(row8<LQ>(Qs_, 16 * tt + lc, 32 * kb), row8<LQ>(Ks_, 16 * st + lc, 32 * kb), X);
         const float bs = rbeta_[16 * st + lc];
+        f32x4 xv;
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const float x = (tt > st || 4 * G + jj >= lc) ? X[jj] * bs : 0.f;
-          bf16 hi, lo;
-          split2(x, hi, lo);
-          ah[jj] = hi;
-          al[jj] = lo;
-        }
+        for (int jj = 0; jj < 4; ++jj) xv[jj] = (tt > st || 4 * G + jj >= lc) ? X[jj] * bs : 0.f;
+        split4(xv, ah, al);
       }
       const int ao = LA::off(16 * st + lc, 16 * tt + 4 * G);
       *reinterpret_cast<bf16x4*>(Ah_ + ao) = ah;
@@ -288,15 +278,14 @@ struct PairCtx {
         }
         const float bs = rbeta_[16 * st + lc];
         float db = 0.f;
+        f32x4 pb;
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
           const float pv = (tt > st || 4 * G + jj >= lc) ? P[jj] : 0.f;
           db += pv * QK[jj];
-          bf16 x, y;
-          split2(pv * bs, x, y);
-          ah[jj] = x;
-          al[jj] = y;
+          pb[jj] = pv * bs;
         }
+        split4(pb, ah, al);
         dbk[kk] = db;
       }
       const int ao = LA::off(16 * st + lc, 16 * tt + 4 * G);
@@ -402,13 +391,13 @@ struct PairCtx {
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt)
       *reinterpret_cast<bf16x4*>(dqs + LQ::off(16 * tt + lc, j0 + 4 * G)) =
-          bf16x4{(bf16)dqa[tt][0], (bf16)dqa[tt][1], (bf16)dqa[tt][2], (bf16)dqa[tt][3]};
+          to_bf16x4(dqa[tt]);
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
       const f32x4 e = eg[st] * rbeta_[16 * st + lc];
       const f32x4 acc = dka[st] - des[st] + e;
       *reinterpret_cast<bf16x4*>(dks + LQ::off(16 * st + lc, j0 + 4 * G)) =
-          bf16x4{(bf16)acc[0], (bf16)acc[1], (bf16)acc[2], (bf16)acc[3]};
+          to_bf16x4(acc);
     }
     __syncthreads();
     next();

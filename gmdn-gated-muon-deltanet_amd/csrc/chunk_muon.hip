@@ -238,14 +238,10 @@ __global__ void __launch_bounds__(D * 4) chunk_out(ChunkArgs p, const float* __r
       for (int kb = 0; kb < NKB; ++kb)
         acc = mfma(b_row<LQ>(Ks, 16 * st, 32 * kb), b_row<LQ>(Qs, 16 * tt, 32 * kb), acc);
       const f32x4 bs = *reinterpret_cast<const f32x4*>(bet + 16 * st + 4 * G);
+      f32x4 val;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float val = (st < tt || 4 * G + j <= lc) ? -acc[j] * bs[j] : 0.f;
-        bf16 hv, lv;
-        split2(val, hv, lv);
-        hi4[j] = hv;
-        lo4[j] = lv;
-      }
+      for (int j = 0; j < 4; ++j) val[j] = (st < tt || 4 * G + j <= lc) ? -acc[j] * bs[j] : 0.f;
+      split4(val, hi4, lo4);
     }
     const int ao = LA::off(16 * tt + lc, 16 * st + 4 * G);
     *reinterpret_cast<bf16x4*>(Ahi + ao) = hi4;
@@ -278,7 +274,7 @@ __global__ void __launch_bounds__(D * 4) chunk_out(ChunkArgs p, const float* __r
     }
     // lane (t, G): o[16 tt + t][r0 + 4G .. +3]
     *reinterpret_cast<bf16x4*>(og + (16 * tt + lc) * p.so[2]) =
-        bf16x4{(bf16)O[0], (bf16)O[1], (bf16)O[2], (bf16)O[3]};
+        to_bf16x4(O);
   }
 }
 

@@ -125,14 +125,10 @@ __global__ void __launch_bounds__(PrepLds<D>::NTHR) chunk_prep(ChunkArgs p, floa
       const int off = LQ::off(t, c8);
       const bf16x8 kv = *reinterpret_cast<const bf16x8*>(Ks + off);
       const float wt = rw[t];
-      bf16x8 hi, lo;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        bf16 h, o;
-        split2(wt * (float)kv[j], h, o);
-        hi[j] = h;
-        lo[j] = o;
-      }
+      bf16x4 h0, l0, h1, l1;
+      split4(f32x4{wt * (float)kv[0], wt * (float)kv[1], wt * (float)kv[2], wt * (float)kv[3]}, h0, l0);
+      split4(f32x4{wt * (float)kv[4], wt * (float)kv[5], wt * (float)kv[6], wt * (float)kv[7]}, h1, l1);
+      const bf16x8 hi = cat8(h0, h1), lo = cat8(l0, l1);
       *reinterpret_cast<bf16x8*>(Wh + off) = hi;
       *reinterpret_cast<bf16x8*>(Wl + off) = lo;
     }
@@ -152,14 +148,10 @@ __global__ void __launch_bounds__(PrepLds<D>::NTHR) chunk_prep(ChunkArgs p, floa
           X = mfma(row8<LQ>(Qs, 16 * tt + lc, 32 * kb), row8<LQ>(Ks, 16 * st + lc, 32 * kb), X);
         // lane (s, G) holds A[t = 16 tt + 4G + jj][s = 16 st + lc]
         const float bs = rbeta[16 * st + lc];
+        f32x4 xv;
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const float x = (tt > st || 4 * G + jj >= lc) ? X[jj] * bs : 0.f;
-          bf16 hv, lv;
-          split2(x, hv, lv);
-          ah[jj] = hv;
-          al[jj] = lv;
-        }
+        for (int jj = 0; jj < 4; ++jj) xv[jj] = (tt > st || 4 * G + jj >= lc) ? X[jj] * bs : 0.f;
+        split4(xv, ah, al);
       }
       const int ao = LA::off(16 * st + lc, 16 * tt + 4 * G);
       *reinterpret_cast<bf16x4*>(Ah + ao) = ah;
@@ -181,13 +173,7 @@ __global__ void __launch_bounds__(PrepLds<D>::NTHR) chunk_prep(ChunkArgs p, floa
         Pt = mma<1, 2>(dOt, At, Pt);
       }
       bf16x4 h4, l4;
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        bf16 hv, lv;
-        split2(Pt[jj], hv, lv);
-        h4[jj] = hv;
-        l4[jj] = lv;
-      }
+      split4(Pt, h4, l4);
       const int po = LQ::off(16 * st + lc, r0 + 4 * G);
       *reinterpret_cast<bf16x4*>(Ph + po) = h4;
       *reinterpret_cast<bf16x4*>(Pl + po) = l4;

@@ -36,9 +36,7 @@ struct Row8<bf16> {
     for (int j = 0; j < 8; ++j) x[j] = (float)v[j];
   }
   static GMDN_DEV void store(bf16* p, const float (&x)[8]) {
-    bf16x8 v;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = (bf16)x[j];
+    const bf16x8 v = cat8(to_bf16x4(f32x4{x[0], x[1], x[2], x[3]}), to_bf16x4(f32x4{x[4], x[5], x[6], x[7]}));
     *reinterpret_cast<bf16x8*>(p) = v;
   }
 };

@@ -217,13 +217,7 @@ struct NSSplit {
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
       bf16x4 hi, lo;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        bf16 h_, l_;
-        split2(x[q][e], h_, l_);
-        hi[e] = h_;
-        lo[e] = l_;
-      }
+      split4(x[q], hi, lo);
       lds_st<bf16x4>(m + (dst + q * RSTEP * ROWB), hi);
       lds_st<bf16x4>(m + (dst + q * RSTEP * ROWB + PLANE), lo);
     }
@@ -235,16 +229,10 @@ struct NSSplit {
   GMDN_DEV void publish(lds_ptr m, const f32x4 (&t)[NT]) const {
 #pragma unroll
     for (int c = 0; c < NT; c += 2) {
-      bf16x8 hi, lo;
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          bf16 h_, l_;
-          split2(t[c + h][j], h_, l_);
-          hi[4 * h + j] = h_;
-          lo[4 * h + j] = l_;
-        }
+      bf16x4 h0, l0, h1, l1;
+      split4(t[c], h0, l0);
+      split4(t[c + 1], h1, l1);
+      const bf16x8 hi = cat8(h0, h1), lo = cat8(l0, l1);
       lds_st<bf16x8>(m + ppub[c], hi);
       lds_st<bf16x8>(m + (ppub[c] + PLANE), lo);
     }

@@ -26,12 +26,11 @@ struct PrecX3 {
   };
   static GMDN_DEV Op from8(const float (&x)[8]) {
     Op r;
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      bf16 h = (bf16)x[s];
-      r.hi[s] = h;
-      r.lo[s] = (bf16)(x[s] - (float)h);
-    }
+    bf16x4 h0, l0, h1, l1;
+    split4(f32x4{x[0], x[1], x[2], x[3]}, h0, l0);
+    split4(f32x4{x[4], x[5], x[6], x[7]}, h1, l1);
+    r.hi = cat8(h0, h1);
+    r.lo = cat8(l0, l1);
     return r;
   }
   static GMDN_DEV Op pack(const f32x4& t0, const f32x4& t1) {

@@ -208,13 +208,7 @@ scan_fwd_rows8(const float* __restrict__ U, const float* __restrict__ K,
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
       bf16x4 hi, lo;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        bf16 h_, l_;
-        split2(Kpre[q][e], h_, l_);
-        hi[e] = h_;
-        lo[e] = l_;
-      }
+      split4(Kpre[q], hi, lo);
       const uint32_t o = R::K0 + buf * 2 * R::PLANE + kdst + q * RSTEP * ROWB;
       lds_st<bf16x4>(L0 + o, hi);
       lds_st<bf16x4>(L0 + (o + R::PLANE), lo);
@@ -248,13 +242,7 @@ scan_fwd_rows8(const float* __restrict__ U, const float* __restrict__ K,
       }
       // this wave's split S tile -> the exchange planes
       bf16x4 hi, lo;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        bf16 h_, l_;
-        split2(S[u][j], h_, l_);
-        hi[j] = h_;
-        lo[j] = l_;
-      }
+      split4(S[u], hi, lo);
       lds_st<bf16x4>(L0 + (R::XS0 + xsw[u]), hi);
       lds_st<bf16x4>(L0 + (R::XS0 + xsw[u] + R::XSP), lo);
     }
@@ -494,13 +482,7 @@ scan_bwd_rows8(const float* __restrict__ U, const float* __restrict__ K,
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
       bf16x4 hi, lo;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        bf16 h_, l_;
-        split2(Kpre[q][e], h_, l_);
-        hi[e] = h_;
-        lo[e] = l_;
-      }
+      split4(Kpre[q], hi, lo);
       const uint32_t o = R::K0 + buf * 2 * R::PLANE + kdst + q * RSTEP * ROWB;
       lds_st<bf16x4>(L0 + o, hi);
       lds_st<bf16x4>(L0 + (o + R::PLANE), lo);
@@ -608,13 +590,7 @@ scan_bwd_rows8(const float* __restrict__ U, const float* __restrict__ K,
     for (int u = 0; u < TPW; ++u) {
       *reinterpret_cast<f32x4*>(dU + si * mat + roff(u)) = Gb[u];
       bf16x4 hi, lo;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        bf16 h_, l_;
-        split2(-Gb[u][j], h_, l_);
-        hi[j] = h_;
-        lo[j] = l_;
-      }
+      split4(-Gb[u], hi, lo);
       lds_st<bf16x4>(L0 + (R::XS0 + xsw[u]), hi);
       lds_st<bf16x4>(L0 + (R::XS0 + xsw[u] + R::XSP), lo);
     }
@@ -787,22 +763,10 @@ scan_bwd_dk8(const float* __restrict__ S_all, const float* __restrict__ dU,
     for (int q = 0; q < NQ; ++q) {
       const uint32_t o = dst + q * RSTEP * ROWB;
       bf16x4 hi, lo;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        bf16 h_, l_;
-        split2(xs[q][e], h_, l_);
-        hi[e] = h_;
-        lo[e] = l_;
-      }
+      split4(xs[q], hi, lo);
       lds_st<bf16x4>(L0 + (R::S0 + o), hi);
       lds_st<bf16x4>(L0 + (R::S0 + R::PLANE + o), lo);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        bf16 h_, l_;
-        split2(xg[q][e], h_, l_);
-        hi[e] = h_;
-        lo[e] = l_;
-      }
+      split4(xg[q], hi, lo);
       lds_st<bf16x4>(L0 + (R::G0 + o), hi);
       lds_st<bf16x4>(L0 + (R::G0 + R::PLANE + o), lo);
       if constexpr (RULE == 0) dot += xs[q][0] * xg[q][0] + xs[q][1] * xg[q][1] + xs[q][2] * xg[q][2] + xs[q][3] * xg[q][3];

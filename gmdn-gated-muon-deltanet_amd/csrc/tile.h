@@ -78,25 +78,40 @@ GMDN_DEV void split2(float x, bf16& hi, bf16& lo) {
   lo = (bf16)(x - (float)hi);
 }
 
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// Two floats rounded to bf16 (to nearest even) by one v_cvt_pk_bf16_f32.
+GMDN_DEV bf16x2 to_bf16x2(float a, float b) { return __builtin_convertvector(f32x2{a, b}, bf16x2); }
+GMDN_DEV bf16x4 to_bf16x4(const f32x4& x) {
+  return __builtin_shufflevector(to_bf16x2(x[0], x[1]), to_bf16x2(x[2], x[3]), 0, 1, 2, 3);
+}
+
+// split2 of four values, two per conversion (hi's value as a float is its
+// bits shifted into the upper half): the same bits in about three
+// instructions per value instead of five.
+GMDN_DEV void split4(const f32x4& x, bf16x4& hi, bf16x4& lo) {
+  const bf16x2 h01 = to_bf16x2(x[0], x[1]), h23 = to_bf16x2(x[2], x[3]);
+  const uint32_t a = __builtin_bit_cast(uint32_t, h01), b = __builtin_bit_cast(uint32_t, h23);
+  const bf16x2 l01 = to_bf16x2(x[0] - __builtin_bit_cast(float, a << 16), x[1] - __builtin_bit_cast(float, a & 0xffff0000u));
+  const bf16x2 l23 = to_bf16x2(x[2] - __builtin_bit_cast(float, b << 16), x[3] - __builtin_bit_cast(float, b & 0xffff0000u));
+  hi = __builtin_shufflevector(h01, h23, 0, 1, 2, 3);
+  lo = __builtin_shufflevector(l01, l23, 0, 1, 2, 3);
+}
+
 // Two D-layout tiles stacked along k (t0: k rows 0..15, t1: rows 16..31)
 // -> pair-order operand.
 template <int P>
 GMDN_DEV Op<P> pack_tiles(const f32x4& t0, const f32x4& t1) {
   Op<P> r;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    if constexpr (P == 1) {
-      r.v[0][j] = (bf16)t0[j];
-      r.v[0][4 + j] = (bf16)t1[j];
-    } else {
-      bf16 h, l;
-      split2(t0[j], h, l);
-      r.v[0][j] = h;
-      r.v[1][j] = l;
-      split2(t1[j], h, l);
-      r.v[0][4 + j] = h;
-      r.v[1][4 + j] = l;
-    }
+  if constexpr (P == 1) {
+    r.v[0] = __builtin_shufflevector(to_bf16x4(t0), to_bf16x4(t1), 0, 1, 2, 3, 4, 5, 6, 7);
+  } else {
+    bf16x4 h0, l0, h1, l1;
+    split4(t0, h0, l0);
+    split4(t1, h1, l1);
+    r.v[0] = __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7);
+    r.v[1] = __builtin_shufflevector(l0, l1, 0, 1, 2, 3, 4, 5, 6, 7);
   }
   return r;
 }
@@ -235,15 +250,9 @@ GMDN_DEV bf16x8 cat8(const bf16x4& a, const bf16x4& b) {
 // (x = hi + lo, hi = bf16(x), lo = bf16(x - hi)), the form their MFMA
 // operands take, in the bytes the fp32 values would occupy.
 GMDN_DEV bf16x8 split_piece(const f32x4& x) {
-  bf16x8 r;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    bf16 hi, lo;
-    split2(x[j], hi, lo);
-    r[j] = hi;
-    r[4 + j] = lo;
-  }
-  return r;
+  bf16x4 hi, lo;
+  split4(x, hi, lo);
+  return cat8(hi, lo);
 }
 GMDN_DEV bf16x8 split_piece(const bf16x4& hi, const bf16x4& lo) { return cat8(hi, lo); }
 GMDN_DEV f32x4 unsplit_piece(const bf16x8& p) {
