@@ -5,26 +5,36 @@
 //   E = V - K S_i^T,   S_{i+1} = a S_i + E^T diag(beta) K,
 //   o = Q S_i^T + tril(Q K^T) diag(beta) E = Q S_i^T + tril(Q K^T) (beta E).
 //
-// Work split.  A workgroup of four waves, one per SIMD, owns 32 rows of S for
-// the whole sequence (B H D / 32 workgroups, the D/32 of one (b, h) on one XCD).
+// Work split.  A workgroup of eight waves, two per SIMD, owns 32 rows of S
+// for the whole sequence (B H D / 32 workgroups, the D/32 of one (b, h) on
+// one XCD).  Wave w runs on SIMD w % 4.
 //  * State waves 0, 1 each own 16 whole rows.  The chunk's recurrence stays in
 //    the wave's registers: E is formed as D-layout tiles (token rows, state-row
 //    columns), and two such tiles stacked along the tokens are the pair-order
-//    operand of the next product, so E -> G -> S_{i+1} -> the next E needs no
-//    exchange and no barrier.  The state is held negated (Sf = -S): then
-//    E = V + K Sf^T and Sf_{i+1} = a Sf + K^T (-beta E), all plain sums.
-//  * Output waves 2, 3 each own two of the four token tiles ({0, 3} | {1, 2},
-//    five causal A tiles each) for all 32 rows.  They form A^T = (K Q^T) tiles
-//    in registers (again directly the pair-order operand), Q Sf^T from the
-//    S pieces the state waves publish, and A (-beta E) one chunk later, when
-//    the state waves have published -beta E; all the LDS-DMA traffic, the o
-//    stores and the checkpoint stores are theirs.
+//    operand of G.  G's tiles come out transposed with the state columns of a
+//    32-column block permuted (tile u of block kb holds, in lane group G,
+//    columns 32 kb + 8G + 4u .. +3: its K^T operand is read with that column
+//    permutation), so the two tiles of a block are the next E's operand in
+//    natural column order and every K, Q row operand is one 16-byte read.
+//    E -> G -> S_{i+1} -> the next E needs no exchange and no barrier.  The state is held negated (Sf = -S): then
+//    E = V + K Sf^T and Sf_{i+1} = a Sf + K^T (-beta E), all plain sums.  Each
+//    product is ordered so that its first half's results can be split into
+//    pieces (and published) while its second half is still in the MFMA pipe.
+//  * Output waves 2, 3, 6, 7 own token tiles 3, 2, 0, 1 (so SIMDs 2 and 3 each
+//    carry 5 of the 10 causal A tiles) for all 32 rows.  They form A^T = K Q^T
+//    tiles in registers (again directly the pair-order operand), Q Sf^T from
+//    the S pieces the state waves publish, and A (-beta E) one chunk later,
+//    when the state waves have published -beta E; they store o and the
+//    checkpoint.
+//  * Copy waves 4, 5 (on the state waves' SIMDs) issue every LDS-DMA copy,
+//    wait for it and reduce the chunk decay a_i into an LDS slot, so no
+//    compute wave waits on vector memory or on the issue of a copy.
 // One barrier per chunk.  In interval i (between barriers i and i + 1) the
 // state waves run chunk i and publish -beta E_i and Sf_{i+1}; the output
-// waves issue the copies of chunk i + 2, finish and store o_{i-1}, and form
-// A_i and Q_i Sf_i^T.  The published operands are double-buffered by chunk
-// parity and kept in register order (lane l's 16 bytes at 16 l), so they are
-// written and read with conflict-free 16-byte accesses and no index math.
+// waves finish and store o_{i-1} and form A_i and Q_i Sf_i^T; the copy waves
+// issue chunk i + 2 and wait for chunk i + 1.  The published operands are
+// double-buffered by chunk parity and kept in register order (lane l's 16
+// bytes at 16 l): conflict-free 16-byte writes and reads, no index math.
 #include "../../include/gmdn_scan.h"
 #include "chunk_b.h"
 
@@ -32,7 +42,16 @@
 
 namespace gmdn {
 
-constexpr int FD_WAVES = 4;
+// An LDS base the compiler cannot see into: per-region bases that share the
+// same lane offset are otherwise merged into one register plus the region's
+// offset, which no longer fits the 16-bit immediate of ds_read / ds_write.
+GMDN_DEV lds_cptr opaque_base(lds_cptr p) {
+  uint32_t v = (uint32_t)(uintptr_t)p;
+  asm volatile("" : "+v"(v));
+  return (lds_cptr)(uintptr_t)v;
+}
+
+constexpr int FD_WAVES = 8;
 constexpr int FD_THREADS = 64 * FD_WAVES;
 
 template <int D>
@@ -51,13 +70,16 @@ struct FwdDeltaLds {
   static constexpr int EPW = 2 * 2 * 1024;
   static constexpr int SP0 = G0 + RING * GT;
   static constexpr int EP0 = SP0 + 2 * 2 * SPW;
-  static constexpr int BYTES = EP0 + 2 * 2 * EPW;
+  static constexpr int SC0 = EP0 + 2 * 2 * EPW;  // chunk decay a per ring stage
+  static constexpr int BYTES = SC0 + RING * 16;
   static_assert(BYTES <= 160 * 1024, "delta forward LDS exceeds the 160 KiB of a CU");
 };
 
 template <int D>
 __global__ void __launch_bounds__(FD_THREADS) chunk_fwd_delta(ChunkArgs p) {
-  using LQ = BSwz<D>;
+  // Q, K tiles: the row swizzle whose transposing reads of four rows by
+  // four 16-byte groups (G's permuted K^T operand) hit 16 distinct groups
+  using LQ = NSwz<D>;
   using LV = BSwz<32>;
   using L = FwdDeltaLds<D>;
   constexpr int NKB = D / 32;  // k-blocks over the state's columns
@@ -76,102 +98,190 @@ __global__ void __launch_bounds__(FD_THREADS) chunk_fwd_delta(ChunkArgs p) {
   const lds_ptr L0 = lds_base(smem);
   const int N = p.N;
 
-  // pair-order row operand of a Q or K tile: lane (m, G) takes row 16 rb + m,
-  // columns 32 kb + 4G .. +3 (slots 0-3) and 32 kb + 16 + 4G .. +3 (4-7).
-  // Whole 16-row tiles leave the row's swizzle term unchanged, so the row
-  // tile, region and stage parts are immediates on a per-(kb, half) base.
-  lds_cptr rowp[NKB][2];
+  if (w == 4 || w == 5) {
+    // ========================================================= copy waves
+    const int cw = w - 4;
+    const uint32_t lds0 = lds_addr(smem);
+    const bf16* qg = p.q + bb * p.sq[0] + hh * p.sq[1];
+    const bf16* kg = p.k + bb * p.sk[0] + hh * p.sk[1];
+    const bf16* vg = p.v + bb * p.sv[0] + hh * p.sv[1] + 32 * blk;
+    // gates: lanes 0-15 beta, 16-31 g (16 bytes each); copied by wave 4's low half
+    const float* gsrc = (G == 1 ? p.g : p.beta) + bh * p.T + 4 * lc;
+    DQ dq, dk;
+    DV dv;
+    dq.init(cw, p.sq[2]);
+    dk.init(cw, p.sk[2]);
+    dv.init(cw, p.sv[2]);
+    auto issue_loads = [&](int i, int stg) {
+      const int64_t t0 = (int64_t)i * CB_C;
+      dq.issue(qg + t0 * p.sq[2], lds0 + L::Q0 + stg * L::TILE, cw);
+      dk.issue(kg + t0 * p.sk[2], lds0 + L::K0 + stg * L::TILE, cw);
+      dv.issue(vg + t0 * p.sv[2], lds0 + L::V0 + stg * L::VT, cw);
+      if (cw == 0 && l < 32) lds_dma16(gsrc + t0, smem + L::G0 + stg * L::GT);
+    };
+    // vector-memory operations this wave issues per chunk copy
+    constexpr int ND = 2 * DQ::NOPS + DV::NOPS;
+    // chunk i + 1 landed (the copy of chunk i + 2, if issued, in flight)
+    auto wait_next = [&](bool issued) {
+      if (!issued)
+        wait_vmem();
+      else if (cw == 0)
+        wait_vmem_le<ND + 1>();
+      else
+        wait_vmem_le<ND>();
+    };
+    // a = exp(sum over the chunk of max(g, log 1e-6)) of the chunk in stage stg
+    auto decay = [&](int stg) {
+      if (cw == 0) {
+        const float a = expf(wave_sum(fmaxf(lds_ld<float>(L0 + (L::G0 + stg * L::GT + 256 + 4 * l)), LOG_FLOOR)));
+        if (l == 0) *reinterpret_cast<float*>(smem + L::SC0 + stg * 16) = a;
+      }
+    };
+    issue_loads(0, 0);
+    if (N > 1) issue_loads(1, 1);
+    wait_next(N > 1);
+    decay(0);
+    __syncthreads();  // barrier 0
+    for (int i = 0; i < N; ++i) {
+      const bool dma = i + 2 < N;
+      if (dma) issue_loads(i + 2, (i + 2) % RING);
+      if (i + 1 < N) {
+        wait_next(dma);
+        decay((i + 1) % RING);
+      }
+      __syncthreads();  // barrier i + 1
+    }
+    return;
+  }
+
+  // natural-order row operand of a Q or K tile: lane (m, G) takes row
+  // 16 rb + m, columns 32 kb + 8G .. +7 (one 16-byte read).  Whole 16-row
+  // tiles leave the row's swizzle term unchanged, so the row tile and stage
+  // parts are immediates on a per-(region, kb) base: one base set per region
+  // keeps every immediate within 16 bits.
+  lds_cptr rowK[NKB], rowQ[NKB];
 #pragma unroll
-  for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-    for (int h = 0; h < 2; ++h) rowp[kb][h] = L0 + swz_off<LQ>(lc, 32 * kb + 16 * h + 4 * G);
-  auto row_op = [&](uint32_t off, int kb) {
-    return cat8(lds_ld<bf16x4>(rowp[kb][0] + off), lds_ld<bf16x4>(rowp[kb][1] + off));
-  };
+  for (int kb = 0; kb < NKB; ++kb) {
+    rowK[kb] = opaque_base(L0 + (L::K0 + swz_off<LQ>(lc, 32 * kb + 8 * G)));
+    rowQ[kb] = opaque_base(L0 + (L::Q0 + swz_off<LQ>(lc, 32 * kb + 8 * G)));
+  }
+  auto row_op = [&](const lds_cptr (&base)[NKB], uint32_t off, int kb) { return lds_ld<bf16x8>(base[kb] + off); };
 
   if (w < 2) {
     // ======================================================== state waves
-    // transposing reads of K columns 16 ct + i (rows 32 kb + 16 h + 4G + i/4)
+    // K^T operand of G's tile ct = 2 kb + u: lane (m, G) takes K[s][c] for
+    // the pair-order tokens s of block kt and column c = 32 kb + 4u + 8 (m / 4)
+    // + m % 4; in transposing reads lane (i, G) addresses row
+    // 32 kt + 16 h + 4G + i / 4, columns 32 kb + 4u + 8 (i % 4) ..
     lds_cptr colp[NCT];
 #pragma unroll
-    for (int ct = 0; ct < NCT; ++ct) colp[ct] = L0 + swz_off<LQ>(4 * G + (lc >> 2), 16 * ct + 4 * (lc & 3));
-    auto col_op = [&](uint32_t off, int ct, int kb) {
-      return cat8(lds_tr16(colp[ct] + off + 32 * kb * ROWB), lds_tr16(colp[ct] + off + (32 * kb + 16) * ROWB));
+    for (int ct = 0; ct < NCT; ++ct)
+      colp[ct] = opaque_base(
+          L0 + (L::K0 + swz_off<LQ>(4 * G + (lc >> 2), 32 * (ct >> 1) + 4 * (ct & 1) + 8 * (lc & 3))));
+    auto col_op = [&](uint32_t off, int ct, int kt) {
+      return cat8(lds_tr16(colp[ct] + off + 32 * kt * ROWB), lds_tr16(colp[ct] + off + (32 * kt + 16) * ROWB));
     };
     // V: tokens 16 st + 4G + j of the wave's column 16 w + lc
     const lds_cptr vp = L0 + swz_off<LV>(4 * G + (lc >> 2), 16 * w + 4 * (lc & 3));
-    const lds_cptr bp = L0 + (L::G0 + 16 * G);      // beta[16 st + 4G ..]
-    const lds_cptr gp = L0 + (L::G0 + 256 + 4 * l);  // g[l]
+    const lds_cptr bp = L0 + (L::G0 + 16 * G);  // beta[16 st + 4G ..]
     const lds_ptr spw = L0 + (L::SP0 + w * L::SPW + 16 * l);
     const lds_ptr epw = L0 + (L::EP0 + w * L::EPW + 16 * l);
 
-    f32x4 Sf[NCT];  // -S, lane (r, G): columns 16 ct + 4G + j of row r
-    Op<2> Sp[NKB];  // its pieces, pair order
+    f32x4 Sf[NCT];  // -S, lane (r, G): columns 32 (ct / 2) + 8G + 4 (ct % 2) + j of row r
+    Op<2> Sp[NKB];  // its pieces, natural order
 #pragma unroll
     for (int ct = 0; ct < NCT; ++ct) Sf[ct] = zero4();
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) Sp[kb] = pack_tiles<2>(Sf[2 * kb], Sf[2 * kb + 1]);
-    auto publish_S = [&](int par) {
-      const uint32_t po = (uint32_t)par * (2 * L::SPW);
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb)
+    for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-        for (int u = 0; u < 2; ++u) lds_st<bf16x8>(spw + po + (kb * 2 + u) * 1024, Sp[kb].v[u]);
-    };
-    publish_S(0);
+      for (int u = 0; u < 2; ++u) lds_st<bf16x8>(spw + (kb * 2 + u) * 1024, Sp[kb].v[u]);
     __syncthreads();  // barrier 0: chunk 0 landed, Sf_0 published
 
     auto state_chunk = [&](auto stg_tag, int i) {
       constexpr int STG = decltype(stg_tag)::value;
       constexpr uint32_t SQK = STG * L::TILE;
-      const float a = expf(wave_sum(fmaxf(lds_ld<float>(gp + STG * L::GT), LOG_FLOOR)));
-      // E = V + K Sf^T, token tiles st (lane (r, G): tokens 16 st + 4G + j)
+      // E = V + K Sf^T, token tiles st (lane (r, G): tokens 16 st + 4G + j),
+      // one token block (two tiles) at a time: the first block's -beta E is
+      // split and published while the second block is in the MFMA pipe
       f32x4 E[4];
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
         const bf16x4 vb = lds_tr16(vp + (L::V0 + STG * L::VT + st * 16 * 64));
         E[st] = f32x4{(float)vb[0], (float)vb[1], (float)vb[2], (float)vb[3]};
       }
+      f32x4 bt[4];
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) {
-        bf16x8 Kr[4];
+      for (int st = 0; st < 4; ++st) bt[st] = lds_ld<f32x4>(bp + (STG * L::GT + st * 64));
+      bf16x8 Kr[4][NKB], Kc[2][NCT];
 #pragma unroll
-        for (int st = 0; st < 4; ++st) Kr[st] = row_op(L::K0 + SQK + st * 16 * ROWB, kb);
+      for (int st = 0; st < 4; ++st)
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+        for (int kb = 0; kb < NKB; ++kb) Kr[st][kb] = row_op(rowK, SQK + st * 16 * ROWB, kb);
+      // LDS reads return in issue order and at most 15 are counted in flight:
+      // G's operands are read between E's products, each well ahead of its use
+      __builtin_amdgcn_sched_barrier(0);
+      auto e_block = [&](int kt) {
 #pragma unroll
-          for (int st = 0; st < 4; ++st) E[st] = mfma(Kr[st], Sp[kb].v[u], E[st]);
-      }
-      // -beta E pieces: the operand of G and of the output waves' A (-beta E)
-      Op<2> WE[2];
+        for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        const f32x4 b0 = lds_ld<f32x4>(bp + (STG * L::GT + 2 * kt * 64));
-        const f32x4 b1 = lds_ld<f32x4>(bp + (STG * L::GT + (2 * kt + 1) * 64));
-        WE[kt] = pack_tiles<2>(-(b0 * E[2 * kt]), -(b1 * E[2 * kt + 1]));
-      }
+          for (int u = 0; u < 2; ++u) {
+            E[2 * kt] = mfma(Kr[2 * kt][kb], Sp[kb].v[u], E[2 * kt]);
+            E[2 * kt + 1] = mfma(Kr[2 * kt + 1][kb], Sp[kb].v[u], E[2 * kt + 1]);
+          }
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) Kc[kt][ct] = col_op(SQK, ct, kt);
+      };
       const uint32_t eo = (uint32_t)(i & 1) * (2 * L::EPW);
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
+      Op<2> WE[2];
+      auto we_block = [&](int kt) {
+        WE[kt] = pack_tiles<2>(-(bt[2 * kt] * E[2 * kt]), -(bt[2 * kt + 1] * E[2 * kt + 1]));
 #pragma unroll
         for (int u = 0; u < 2; ++u) lds_st<bf16x8>(epw + eo + (kt * 2 + u) * 1024, WE[kt].v[u]);
-      // Sf_{i+1} = a Sf_i + K^T (-beta E), column tiles ct (transposed tiles:
-      // lane (r, G) gets columns 16 ct + 4G + j of row r)
+      };
+      // token block 0: 4 NKB products, 2 NCT column reads interleaved
+      e_block(0);
+#pragma unroll
+      for (int k = 0; k < 4 * NKB; ++k) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (k < 2 * NCT) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // block 0's -beta E split and published while block 1 is in the pipe
+      we_block(0);
+      e_block(1);
+#pragma unroll
+      for (int k = 0; k < 4 * NKB; ++k) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (k < 2 * NCT) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      we_block(1);
+      // Sf_{i+1} = a Sf_i + K^T (-beta E), column tiles ct (transposed tiles in
+      // the permuted column order above): token block 0 for every tile, then
+      // block 1 tile pair by tile pair, each pair split and published while
+      // the next is in the MFMA pipe
+      const float a = lds_ld<float>(L0 + (L::SC0 + STG * 16));
 #pragma unroll
       for (int ct = 0; ct < NCT; ++ct) Sf[ct] = a * Sf[ct];
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        bf16x8 Kc[NCT];
+      for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int ct = 0; ct < NCT; ++ct) Kc[ct] = col_op(L::K0 + SQK, ct, kt);
+        for (int ct = 0; ct < NCT; ++ct) Sf[ct] = mfma(Kc[0][ct], WE[0].v[u], Sf[ct]);
+      const uint32_t po = (uint32_t)((i + 1) & 1) * (2 * L::SPW);
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+      for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
-          for (int ct = 0; ct < NCT; ++ct) Sf[ct] = mfma(Kc[ct], WE[kt].v[u], Sf[ct]);
+        for (int u = 0; u < 2; ++u) {
+          Sf[2 * kb] = mfma(Kc[1][2 * kb], WE[1].v[u], Sf[2 * kb]);
+          Sf[2 * kb + 1] = mfma(Kc[1][2 * kb + 1], WE[1].v[u], Sf[2 * kb + 1]);
+        }
+        Sp[kb] = pack_tiles<2>(Sf[2 * kb], Sf[2 * kb + 1]);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) lds_st<bf16x8>(spw + po + (kb * 2 + u) * 1024, Sp[kb].v[u]);
       }
-#pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) Sp[kb] = pack_tiles<2>(Sf[2 * kb], Sf[2 * kb + 1]);
-      publish_S((i + 1) & 1);
       __syncthreads();  // barrier i + 1
     };
     for (int i = 0; i < N; i += RING) {
@@ -183,200 +293,115 @@ __global__ void __launch_bounds__(FD_THREADS) chunk_fwd_delta(ChunkArgs p) {
   }
 
   // ========================================================== output waves
-  const int ow = w - 2;
-  const uint32_t lds0 = lds_addr(smem);
-  const bf16* qg = p.q + bb * p.sq[0] + hh * p.sq[1];
-  const bf16* kg = p.k + bb * p.sk[0] + hh * p.sk[1];
-  const bf16* vg = p.v + bb * p.sv[0] + hh * p.sv[1] + 32 * blk;
+  // token tile TT of waves 2, 3, 6, 7: 3, 2, 0, 1; the checkpoint share of
+  // wave index ow (0..3): row tile ow & 1, k-blocks of half ow >> 1
+  const int ow = (w & 1) | ((w >> 1) & 2);  // 2 -> 0, 3 -> 1, 6 -> 2, 7 -> 3
   bf16* og = p.o + bb * p.so[0] + hh * p.so[1] + 32 * blk + 4 * G;
-  // gates: lanes 0-15 beta, 16-31 g (16 bytes each); copied by wave 2's low half
-  const float* gsrc = (G == 1 ? p.g : p.beta) + bh * p.T + 4 * lc;
-  DQ dq, dk;
-  DV dv;
-  dq.init(ow, p.sq[2]);
-  dk.init(ow, p.sk[2]);
-  dv.init(ow, p.sv[2]);
-  auto issue_loads = [&](int i, int stg) {
-    const int64_t t0 = (int64_t)i * CB_C;
-    dq.issue(qg + t0 * p.sq[2], lds0 + L::Q0 + stg * L::TILE, ow);
-    dk.issue(kg + t0 * p.sk[2], lds0 + L::K0 + stg * L::TILE, ow);
-    dv.issue(vg + t0 * p.sv[2], lds0 + L::V0 + stg * L::VT, ow);
-    if (ow == 0 && l < 32) lds_dma16(gsrc + t0, smem + L::G0 + stg * L::GT);
-  };
-  // vector-memory operations this wave issues per chunk copy
-  constexpr int ND1 = 2 * DQ::NOPS + DV::NOPS;
   const lds_cptr spr = L0 + (L::SP0 + 16 * l);
   const lds_cptr epr = L0 + (L::EP0 + 16 * l);
-
-  // prologue: chunks 0 and 1 in flight, chunk 0 waited for
-  issue_loads(0, 0);
-  if (N > 1) {
-    issue_loads(1, 1);
-    if (ow == 0)
-      wait_vmem_le<ND1 + 1>();
-    else
-      wait_vmem_le<ND1>();
-  } else {
-    wait_vmem();
-  }
   __syncthreads();  // barrier 0
 
-  // token tiles TA, TB of this wave; A pieces per (token tile, key block)
-  auto run = [&](auto ta_tag, auto tb_tag) {
-    constexpr int TT[2] = {decltype(ta_tag)::value, decltype(tb_tag)::value};
-    Op<2> Ap[2][2], Aq[2][2];  // this chunk's and the previous chunk's
-    f32x4 O[2][2], Oq[2][2];   // -o^T tiles [row tile][token tile], likewise
+  auto run = [&](auto tt_tag) {
+    constexpr int TT = decltype(tt_tag)::value;
+    constexpr int NKT = TT >= 2 ? 2 : 1;  // token blocks of A with s <= t
+    constexpr int OW = TT == 3 ? 0 : TT == 2 ? 1 : TT == 0 ? 2 : 3;  // == ow
+    Op<2> Ap[2], Aq[2];  // this chunk's and the previous chunk's A pieces
+    f32x4 O[2], Oq[2];   // -o^T tiles [row tile], likewise
     const bf16x8 z8 = bf16x8{(bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f};
 #pragma unroll
-    for (int a_ = 0; a_ < 2; ++a_)
-#pragma unroll
-      for (int b_ = 0; b_ < 2; ++b_) {
-        Ap[a_][b_].v[0] = Ap[a_][b_].v[1] = z8;
-        Aq[a_][b_] = Ap[a_][b_];
-        O[a_][b_] = Oq[a_][b_] = zero4();
-      }
+    for (int x = 0; x < 2; ++x) {
+      Ap[x].v[0] = Ap[x].v[1] = z8;
+      Aq[x] = Ap[x];
+      O[x] = Oq[x] = zero4();
+    }
     auto finish_prev = [&](int i) {  // o_{i-1} += A (-beta E), stored
       const uint32_t eo = (uint32_t)((i - 1) & 1) * (2 * L::EPW);
       Op<2> WE[2][2];
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
+        for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
           for (int u = 0; u < 2; ++u) WE[rt][kt].v[u] = lds_ld<bf16x8>(epr + eo + rt * L::EPW + (kt * 2 + u) * 1024);
       // (hi, hi), (hi, lo), (lo, hi) of each operand pair
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
+      for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
         for (int pc = 0; pc < 3; ++pc)
 #pragma unroll
           for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-            for (int x = 0; x < 2; ++x)
-              if (2 * kt <= TT[x])
-                Oq[rt][x] = mfma(WE[rt][kt].v[pc == 2 ? 1 : 0], Aq[x][kt].v[pc == 1 ? 1 : 0], Oq[rt][x]);
-      // lane (t, G) of tile (rt, x): token 16 TT[x] + t, columns 16 rt + 4G ..
+            Oq[rt] = mfma(WE[rt][kt].v[pc == 2 ? 1 : 0], Aq[kt].v[pc == 1 ? 1 : 0], Oq[rt]);
+      // lane (t, G) of row tile rt: token 16 TT + t, columns 16 rt + 4G ..
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-        for (int x = 0; x < 2; ++x) {
-          const f32x4 v = Oq[rt][x];
-          *reinterpret_cast<bf16x4*>(og + ((int64_t)(i - 1) * CB_C + 16 * TT[x] + lc) * p.so[2] + 16 * rt) =
-              to_bf16x4(-v);
-        }
+        *reinterpret_cast<bf16x4*>(og + ((int64_t)(i - 1) * CB_C + 16 * TT + lc) * p.so[2] + 16 * rt) =
+            to_bf16x4(-Oq[rt]);
     };
     auto out_chunk = [&](auto stg_tag, int i) {
       constexpr int STG = decltype(stg_tag)::value;
       constexpr uint32_t SQK = STG * L::TILE;
-      const bool dma = i + 2 < N, prev = i >= 1;
-      const bool ck = p.states && (i & 1) == 0;
-      if (dma) issue_loads(i + 2, (STG + 2) % RING);
-      if (prev) finish_prev(i);
+      if (i >= 1) finish_prev(i);
       // A^T tiles (K Q^T, causal part) -> pair-order A operands of chunk i
-      bf16x8 Qr[2][NKB];
+      bf16x8 Qr[NKB];
 #pragma unroll
-      for (int x = 0; x < 2; ++x)
+      for (int kb = 0; kb < NKB; ++kb) Qr[kb] = row_op(rowQ, SQK + TT * 16 * ROWB, kb);
+      f32x4 At[4];
 #pragma unroll
-        for (int kb = 0; kb < NKB; ++kb) Qr[x][kb] = row_op(L::Q0 + SQK + TT[x] * 16 * ROWB, kb);
-      f32x4 At[2][4];
-#pragma unroll
-      for (int x = 0; x < 2; ++x)
-#pragma unroll
-        for (int st = 0; st < 4; ++st) At[x][st] = zero4();
+      for (int st = 0; st < 4; ++st) At[st] = zero4();
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb) {
-        bf16x8 Kr[4];
+        bf16x8 Kr[TT + 1];
 #pragma unroll
-        for (int st = 0; st < 4; ++st)
-          if (st <= TT[1]) Kr[st] = row_op(L::K0 + SQK + st * 16 * ROWB, kb);
+        for (int st = 0; st <= TT; ++st) Kr[st] = row_op(rowK, SQK + st * 16 * ROWB, kb);
 #pragma unroll
-        for (int st = 0; st < 4; ++st)
-#pragma unroll
-          for (int x = 0; x < 2; ++x)
-            if (st <= TT[x]) At[x][st] = mfma(Kr[st], Qr[x][kb], At[x][st]);
+        for (int st = 0; st <= TT; ++st) At[st] = mfma(Kr[st], Qr[kb], At[st]);
       }
+      // keep s <= t on the diagonal tile: lane (t, G) row 4G + j is s
 #pragma unroll
-      for (int x = 0; x < 2; ++x) {
-        // keep s <= t on the diagonal tile: lane (t, G) row 4G + j is s
+      for (int j = 0; j < 4; ++j)
+        if (4 * G + j > lc) At[TT][j] = 0.f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if (4 * G + j > lc) At[x][TT[x]][j] = 0.f;
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-          if (2 * kt <= TT[x]) Ap[x][kt] = pack_tiles<2>(At[x][2 * kt], At[x][2 * kt + 1]);
-      }
+      for (int kt = 0; kt < NKT; ++kt) Ap[kt] = pack_tiles<2>(At[2 * kt], At[2 * kt + 1]);
       // -o^T = Sf Q^T (+ A (-beta E) next interval)
       const uint32_t sbo = (uint32_t)(i & 1) * (2 * L::SPW);
+      Op<2> Sr[2][NKB];
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt) {
-        Op<2> Sr[NKB];
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-          for (int u = 0; u < 2; ++u) Sr[kb].v[u] = lds_ld<bf16x8>(spr + sbo + rt * L::SPW + (kb * 2 + u) * 1024);
-        O[rt][0] = O[rt][1] = zero4();
+      for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
           for (int u = 0; u < 2; ++u)
+            Sr[rt][kb].v[u] = lds_ld<bf16x8>(spr + sbo + rt * L::SPW + (kb * 2 + u) * 1024);
+      O[0] = O[1] = zero4();
 #pragma unroll
-            for (int x = 0; x < 2; ++x) O[rt][x] = mfma(Sr[kb].v[u], Qr[x][kb], O[rt][x]);
-        // checkpoint S_i of the even chunks (the backward rebuilds the odd
-        // ones): rows 16 ow + lc from the pieces just read, negated back
-        if (ck && rt == ow) {
-          const int64_t plane = bh * ((N + 1) / 2) + i / 2;
-          float* sp = p.states + (plane * D + 32 * blk + 16 * ow + lc) * (int64_t)D + 4 * G;
+      for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-          for (int kb = 0; kb < NKB; ++kb) {
-            *reinterpret_cast<bf16x8*>(sp + 32 * kb) =
-                neg8(__builtin_shufflevector(Sr[kb].v[0], Sr[kb].v[1], 0, 1, 2, 3, 8, 9, 10, 11));
-            *reinterpret_cast<bf16x8*>(sp + 32 * kb + 16) =
-                neg8(__builtin_shufflevector(Sr[kb].v[0], Sr[kb].v[1], 4, 5, 6, 7, 12, 13, 14, 15));
-          }
-        }
-      }
-      // chunk i + 1 must have landed; what this wave issued after its copy
-      // (the copy of chunk i + 2, o_{i-1}, the checkpoint) may stay in flight
-      if (i + 1 < N) {
-        constexpr int C = 2 * NKB;
-        if (ow == 0) {
-          if (dma) {
-            if (prev) {
-              if (ck) wait_vmem_le<ND1 + 1 + 4 + C>(); else wait_vmem_le<ND1 + 1 + 4>();
-            } else {
-              if (ck) wait_vmem_le<ND1 + 1 + C>(); else wait_vmem_le<ND1 + 1>();
-            }
-          } else {
-            if (prev) {
-              if (ck) wait_vmem_le<4 + C>(); else wait_vmem_le<4>();
-            } else {
-              if (ck) wait_vmem_le<C>(); else wait_vmem_le<0>();
-            }
-          }
-        } else {
-          if (dma) {
-            if (prev) {
-              if (ck) wait_vmem_le<ND1 + 4 + C>(); else wait_vmem_le<ND1 + 4>();
-            } else {
-              if (ck) wait_vmem_le<ND1 + C>(); else wait_vmem_le<ND1>();
-            }
-          } else {
-            if (prev) {
-              if (ck) wait_vmem_le<4 + C>(); else wait_vmem_le<4>();
-            } else {
-              if (ck) wait_vmem_le<C>(); else wait_vmem_le<0>();
-            }
-          }
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int rt = 0; rt < 2; ++rt) O[rt] = mfma(Sr[rt][kb].v[u], Qr[kb], O[rt]);
+      // checkpoint S_i of the even chunks (the backward rebuilds the odd
+      // ones) from the pieces just read, negated back: this wave's row tile
+      // and half of the k-blocks
+      if (p.states && (i & 1) == 0) {
+        constexpr int rt = OW & 1;
+        const int64_t plane = bh * ((N + 1) / 2) + i / 2;
+        float* sp = p.states + (plane * D + 32 * blk + 16 * rt + lc) * (int64_t)D + 8 * G;
+#pragma unroll
+        for (int kh = 0; kh < NKB / 2; ++kh) {
+          const int kb = (OW >> 1) * (NKB / 2) + kh;
+          const Op<2> x = Sr[rt][kb];
+          *reinterpret_cast<bf16x8*>(sp + 32 * kb) =
+              neg8(__builtin_shufflevector(x.v[0], x.v[1], 0, 1, 2, 3, 8, 9, 10, 11));
+          *reinterpret_cast<bf16x8*>(sp + 32 * kb + 4) =
+              neg8(__builtin_shufflevector(x.v[0], x.v[1], 4, 5, 6, 7, 12, 13, 14, 15));
         }
       }
       __syncthreads();  // barrier i + 1
 #pragma unroll
-      for (int a_ = 0; a_ < 2; ++a_)
-#pragma unroll
-        for (int b_ = 0; b_ < 2; ++b_) {
-          Aq[a_][b_] = Ap[a_][b_];
-          Oq[a_][b_] = O[a_][b_];
-        }
+      for (int x = 0; x < 2; ++x) {
+        Aq[x] = Ap[x];
+        Oq[x] = O[x];
+      }
     };
     for (int i = 0; i < N; i += RING) {
       out_chunk(std::integral_constant<int, 0>{}, i);
@@ -385,10 +410,12 @@ __global__ void __launch_bounds__(FD_THREADS) chunk_fwd_delta(ChunkArgs p) {
     }
     finish_prev(N);
   };
-  if (ow == 0)
-    run(std::integral_constant<int, 0>{}, std::integral_constant<int, 3>{});
-  else
-    run(std::integral_constant<int, 1>{}, std::integral_constant<int, 2>{});
+  switch (ow) {
+    case 0: run(std::integral_constant<int, 3>{}); break;
+    case 1: run(std::integral_constant<int, 2>{}); break;
+    case 2: run(std::integral_constant<int, 0>{}); break;
+    default: run(std::integral_constant<int, 1>{}); break;
+  }
 }
 
 template <int D>
