@@ -571,7 +571,7 @@ def chunk_leg(w, steps: int, warmup: int, with_bwd: bool) -> dict:
         if rid == 1:
             bwd_name = f"chunk_prep_muon<{w.d}> + scan_bwd_muon_pre/x3<{w.d}> + chunk_bwd_tok<{w.d},1>"
         elif rid == 0:
-            bwd_name = f"chunk_bwd_dstate<{w.d}> + chunk_bwd_pair<{w.d}>"
+            bwd_name = f"chunk_bwd_dscan<{w.d}> + chunk_bwd_pair<{w.d}>"
         elif w.d == 128:
             bwd_name = "chunk_prep<128,2> + scan_bwd_rows<128,2> (fp32) + chunk_bwd_tok<128,2>"
         else:

@@ -44,16 +44,18 @@ GMDN_DEV void map_block(int64_t BH, int nblk, int64_t& bh, int& blk) {
 }
 
 // ------------------------------------------------- LDS operand helpers
-// lane (m, G) takes X[r][k0 + 8G .. k0 + 8G + 7] (natural k order, 16 bytes)
+// lane (m, G) takes X[r][k0 + 8G .. k0 + 8G + 7] (natural k order, 16 bytes).
+// The helpers take the lane index (lane_id() by default): a caller in a loop
+// passes its own copy so that the addresses are not hoisted out of the loop.
 template <class L>
-GMDN_DEV bf16x8 row8(const bf16* X, int r, int k0) {
-  return *reinterpret_cast<const bf16x8*>(X + L::off(r, k0 + 8 * (lane_id() >> 4)));
+GMDN_DEV bf16x8 row8(const bf16* X, int r, int k0, int l = lane_id()) {
+  return *reinterpret_cast<const bf16x8*>(X + L::off(r, k0 + 8 * (l >> 4)));
 }
 
 // lane (i, G) takes X[k0 + 8G + j][c0 + i], j = 0..7 (two transposing reads)
 template <class L>
-GMDN_DEV bf16x8 col8(const bf16* X, int k0, int c0) {
-  const int l = lane_id(), i = l & 15, G = l >> 4;
+GMDN_DEV bf16x8 col8(const bf16* X, int k0, int c0, int l = lane_id()) {
+  const int i = l & 15, G = l >> 4;
   const int rr = k0 + 8 * G + (i >> 2), cc = c0 + 4 * (i & 3);
   const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(X + L::off(rr, cc)));
   const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(X + L::off(rr + 4, cc)));
@@ -71,8 +73,8 @@ GMDN_DEV float dot4(const f32x4& a, const f32x4& b) {
 // eight consecutive columns 32 kb + 8 G' .. +7 of one pair of state-row
 // pieces (the order the checkpoints keep).
 template <class L>
-GMDN_DEV bf16x8 col8p(const bf16* X, int k0, int cb) {
-  const int l = lane_id(), i = l & 15, G = l >> 4;
+GMDN_DEV bf16x8 col8p(const bf16* X, int k0, int cb, int l = lane_id()) {
+  const int i = l & 15, G = l >> 4;
   const int rr = k0 + 8 * G + (i >> 2), cc = cb + 8 * (i & 3);
   const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(X + L::off(rr, cc)));
   const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(X + L::off(rr + 4, cc)));
@@ -89,6 +91,8 @@ hipError_t chunk_fwd_muon_launch(const ChunkArgs& a, int d, float* S_out, float*
 size_t wy_workspace_floats(int64_t B, int64_t H, int64_t T, int d);
 hipError_t wy_fwd_launch(const ChunkArgs& a, int d, float* ws, hipStream_t s);
 hipError_t chunk_bwd_launch(const ChunkArgs& a, int d, int rule, hipStream_t s);
+// delta rule: the reverse scan of the state cotangent (Gb of the odd chunks)
+hipError_t chunk_bwd_dscan_launch(const ChunkArgs& a, int d, hipStream_t s);
 // the matrix form's per-chunk Kw, Uv (fwd) and gS (bwd) as (B, H, N, d, d)
 // float32, and a, b, m, n (four B H N arrays): muon (fwd and bwd together,
 // for its backward) and adam at d = 128 (fwd: training forward, bwd: backward)

@@ -18,8 +18,8 @@
 //  * the reverse recurrence of Sb.  Row r of Sb_i needs only row r of Sb_{i+1}
 //    (dE[:, r] = A^T dO[:, r] + diag(w) K Sb[r, :]^T), so one workgroup owns 32
 //    rows, with an LDS-DMA ring of Q, K and the workgroup's dO columns, and
-//    writes Gb_i: chunk_bwd_dstate (delta, odd chunks only; state, token and
-//    memory waves) and chunk_bwd_state (adam, every chunk; 4 waves, wave
+//    writes Gb_i: chunk_bwd_dscan (delta, odd chunks only;
+//    chunk_bwd_dscan.hip) and chunk_bwd_state (adam, every chunk; 4 waves, wave
 //    (rt, h) holds 16 rows x column half h and the moment cotangents in
 //    registers).
 //  * the token gradients, chunk-parallel.  From S_i (saved by the forward)
@@ -38,7 +38,7 @@
 namespace gmdn {
 
 // ============================================================ chunk_bwd_state
-// The adam rule's reverse scan (the delta rule's is chunk_bwd_dstate below).
+// The adam rule's reverse scan (the delta rule's is chunk_bwd_dscan).
 template <int D, int RULE>
 struct StateBwdLds {
   static_assert(RULE == 2, "the 4-wave reverse scan serves the adam rule");
@@ -395,370 +395,6 @@ __global__ void __launch_bounds__(CB_THREADS) chunk_bwd_state(ChunkArgs p) {
     chunk(std::integral_constant<int, 0>{}, j);
     if (j + 1 < p.N) chunk(std::integral_constant<int, 1>{}, j + 1);
     if (j + 2 < p.N) chunk(std::integral_constant<int, 2>{}, j + 2);
-  }
-}
-
-// ======================================================= chunk_bwd_dstate (delta)
-// The delta rule's reverse scan with roles, 8 waves (two per SIMD):
-//  * state waves 0..3, (rt, h) = (w >> 1, w & 1): the recurrence only, on
-//    LDS operands (no global memory access);
-//  * token waves 4..6: one step ahead, the state-independent part of dE,
-//    P = A^T dO, for the token tiles st = 0 | 1 | 2, 3 of both row tiles;
-//  * memory wave 7: every LDS-DMA load and the gate scalar a_i; token waves
-//    4 and 5 store Gb_i (half each).  Vector-memory issue is limited per
-//    wave and per CU, so the state waves never wait behind it.
-// Per step j (chunk i = N-1-j), between the barriers X (end of step j-1) and Y:
-//   state : dE = diag(beta) K Gb_i^T + P_i (tokens 32h.., rows rt) -> XE
-//   token : (Q K^T) tiles of step j+1; waves 4, 5: Gb_i = Sb_{i+1} read back
-//           from XS and stored
-//   memory: loads of step j+2; a_i
-// and between Y and X:
-//   state : Sb_i = a_i Sb_{i+1} + dO^T Q - dE^T K (column half h) -> XS
-//   token : P of step j+1 -> P slots
-//   memory: waits for the loads of step j+2, which X then publishes
-template <int D>
-struct DStateLds {
-  static constexpr int TILE = CB_C * D * 2;     // one Q or K chunk (bytes)
-  static constexpr int OT = CB_C * 32 * 2;      // the workgroup's 32 columns of dO
-  static constexpr int GT = 4 * CB_C * 4;       // gate chunk
-  static constexpr int Q0 = 0;
-  static constexpr int K0 = Q0 + RING * TILE;
-  static constexpr int O0 = K0 + RING * TILE;
-  static constexpr int G0 = O0 + RING * OT;
-  static constexpr int XSP = 32 * D * 2;        // Sb exchange: [32 rows][D] bf16, hi then lo
-  static constexpr int XS0 = G0 + RING * GT;
-  static constexpr int XEP = 32 * CB_C * 2;     // -dE exchange: [32 rows][64 tokens] bf16, hi then lo
-  static constexpr int XE0 = XS0 + 2 * XSP;
-  static constexpr int PB = 8 * 64 * 16;        // P: 8 D-layout tiles (row tile rt, token tile st)
-  static constexpr int P0 = XE0 + 2 * XEP;
-  static constexpr int SC0 = P0 + PB;           // gate scalar a per ring stage
-  static constexpr int BYTES = SC0 + RING * 16;
-  static_assert(BYTES <= 160 * 1024, "delta state backward LDS exceeds the 160 KiB of a CU");
-};
-
-constexpr int DS_THREADS = 2 * CB_THREADS;
-
-template <int D>
-__global__ void __launch_bounds__(DS_THREADS) chunk_bwd_dstate(ChunkArgs p) {
-  using LQ = BSwz<D>;
-  using LO = BSwz<32>;
-  using LX = BSwz<CB_C>;
-  using L = DStateLds<D>;
-  using std::integral_constant;
-  constexpr int NKB = D / 32;   // k-blocks over the state's columns
-  constexpr int NTH = D / 32;   // column tiles in a half
-  constexpr int ROWB = D * 2;   // bytes per Q/K row
-  extern __shared__ __align__(16) char smem[];
-
-  int64_t bh;
-  int blk;
-  map_block(p.B * p.H, D / 32, bh, blk);
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int l = lane_id(), G = l >> 4, lc = l & 15;
-  const int64_t bb = bh / p.H, hh = bh % p.H;
-  const uint32_t lds0 = lds_addr(smem);
-  const lds_ptr L0 = lds_base(smem);
-  float* const scal = reinterpret_cast<float*>(smem + L::SC0);
-  // P slot of (row tile rt, token tile st): written after Y, read before the next Y
-  auto pslot = [&](int rt, int st) { return reinterpret_cast<f32x4*>(smem + L::P0 + ((4 * rt + st) * 64 + l) * 16); };
-
-  if (w < CB_WAVES) {
-    // ================================================================ state
-    const int rt = w >> 1, h = w & 1;
-    lds_cptr krow[NKB], xsr[NKB];
-#pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) {
-      const uint32_t rb = swz_off<LQ>(lc, 32 * kb + 8 * G);
-      krow[kb] = L0 + (rb + L::K0);
-      xsr[kb] = L0 + (rb + L::XS0);
-    }
-    // transposing reads of Q / K columns 16 (h NTH + t) + i, natural k (rows 8G + lc/4, +4)
-    lds_cptr qc0[NTH], qc1[NTH], kc0[NTH], kc1[NTH];
-#pragma unroll
-    for (int t = 0; t < NTH; ++t) {
-      const uint32_t a0 = swz_off<LQ>(8 * G + (lc >> 2), 16 * (h * NTH + t) + 4 * (lc & 3));
-      const uint32_t a1 = swz_off<LQ>(8 * G + 4 + (lc >> 2), 16 * (h * NTH + t) + 4 * (lc & 3));
-      qc0[t] = L0 + (a0 + L::Q0);
-      qc1[t] = L0 + (a1 + L::Q0);
-      kc0[t] = L0 + (a0 + L::K0);
-      kc1[t] = L0 + (a1 + L::K0);
-    }
-    // dO columns 16 rt + i, natural k
-    const lds_cptr on0 = L0 + (swz_off<LO>(8 * G + (lc >> 2), 16 * rt + 4 * (lc & 3)) + L::O0);
-    const lds_cptr on1 = L0 + (swz_off<LO>(8 * G + 4 + (lc >> 2), 16 * rt + 4 * (lc & 3)) + L::O0);
-    // Sb exchange writes (row 16 rt + lc, columns 16 (h NTH + t) + 4G)
-    uint32_t xsw[NTH];
-#pragma unroll
-    for (int t = 0; t < NTH; ++t) xsw[t] = swz_off<LQ>(16 * rt + lc, 16 * (h * NTH + t) + 4 * G);
-    // -dE exchange: written at tokens 32h + 16u + 4G, read at 32u + 8G (row 16 rt + lc)
-    uint32_t xew[2], xer[2];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      xew[u] = swz_off<LX>(16 * rt + lc, 32 * h + 16 * u + 4 * G);
-      xer[u] = swz_off<LX>(16 * rt + lc, 32 * u + 8 * G);
-    }
-    auto put_split = [&](uint32_t off, uint32_t plane, const f32x4& x) {
-      bf16x4 hi, lo;
-      split4(x, hi, lo);
-      lds_st<bf16x4>(L0 + off, hi);
-      lds_st<bf16x4>(L0 + (off + plane), lo);
-    };
-    auto read_op = [&](lds_cptr addr, uint32_t plane) {
-      Op<2> x;
-      x.v[0] = lds_ld<bf16x8>(addr);
-      x.v[1] = lds_ld<bf16x8>(addr + plane);
-      return x;
-    };
-
-    f32x4 Sb[NTH];  // dL/dS_{i+1}: row 32 blk + 16 rt + lc, columns of half h
-#pragma unroll
-    for (int t = 0; t < NTH; ++t) {
-      Sb[t] = zero4();
-      put_split(xsw[t] + L::XS0, L::XSP, Sb[t]);
-    }
-    __syncthreads();
-    __syncthreads();  // prologue: step 0's P
-
-    auto step = [&](auto stg_tag) {
-      constexpr int STG = decltype(stg_tag)::value;
-      constexpr uint32_t SQK = STG * L::TILE;
-      constexpr uint32_t OC = STG * L::OT;
-      const float* gates = reinterpret_cast<const float*>(smem + L::G0 + STG * L::GT);
-      auto seg = [&](auto rt_tag, auto h_tag) {
-        constexpr int RT = decltype(rt_tag)::value, H = decltype(h_tag)::value;
-        Op<2> Sop[NKB];  // Gb_i^T operands (k = c natural, n = r), rows of row tile RT
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb) Sop[kb] = read_op(xsr[kb] + RT * 16 * ROWB, L::XSP);
-        f32x4 dE[2] = {zero4(), zero4()};
-        bf16x8 Kr[2][NKB];
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-          for (int kb = 0; kb < NKB; ++kb) Kr[u][kb] = lds_ld<bf16x8>(krow[kb] + SQK + (2 * H + u) * 16 * ROWB);
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-          for (int u = 0; u < 2; ++u) dE[u] = mma<1, 2>(Op<1>{{Kr[u][kb]}}, Sop[kb], dE[u]);
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const f32x4 bt = *reinterpret_cast<const f32x4*>(gates + 32 * H + 16 * u + 4 * G);
-          dE[u] = dE[u] * bt + *pslot(RT, 2 * H + u);
-          put_split(xew[u] + L::XE0, L::XEP, -dE[u]);
-        }
-      };
-      switch (w) {
-        case 0: seg(integral_constant<int, 0>{}, integral_constant<int, 0>{}); break;
-        case 1: seg(integral_constant<int, 0>{}, integral_constant<int, 1>{}); break;
-        case 2: seg(integral_constant<int, 1>{}, integral_constant<int, 0>{}); break;
-        default: seg(integral_constant<int, 1>{}, integral_constant<int, 1>{}); break;
-      }
-      __syncthreads();  // Y: -dE published
-      const float a = scal[4 * STG];
-      Op<2> ND[2];
-#pragma unroll
-      for (int kbs = 0; kbs < 2; ++kbs) ND[kbs] = read_op(L0 + (xer[kbs] + L::XE0), L::XEP);
-      f32x4 acc[NTH];
-#pragma unroll
-      for (int t = 0; t < NTH; ++t) acc[t] = a * Sb[t];
-#pragma unroll
-      for (int kbs = 0; kbs < 2; ++kbs) {
-        const bf16x8 dO8 = cat8(lds_tr16(on0 + (OC + kbs * 32 * 64)), lds_tr16(on1 + (OC + kbs * 32 * 64)));
-#pragma unroll
-        for (int t = 0; t < NTH; ++t) {
-          const uint32_t ro = SQK + kbs * 32 * ROWB;
-          const bf16x8 qc = cat8(lds_tr16(qc0[t] + ro), lds_tr16(qc1[t] + ro));
-          const bf16x8 kc = cat8(lds_tr16(kc0[t] + ro), lds_tr16(kc1[t] + ro));
-          acc[t] = mfma(qc, dO8, acc[t]);
-          acc[t] = mma<1, 2>(Op<1>{{kc}}, ND[kbs], acc[t]);
-        }
-      }
-#pragma unroll
-      for (int t = 0; t < NTH; ++t) {
-        Sb[t] = acc[t];
-        put_split(xsw[t] + L::XS0, L::XSP, Sb[t]);
-      }
-      __syncthreads();  // X: Sb_i published
-    };
-    for (int j = 0; j < p.N; j += RING) {
-      step(integral_constant<int, 0>{});
-      if (j + 1 < p.N) step(integral_constant<int, 1>{});
-      if (j + 2 < p.N) step(integral_constant<int, 2>{});
-    }
-  } else if (w < CB_WAVES + 3) {
-    // ================================================================ token
-    // token tiles st of this wave: {0}, {1} or {2, 3}
-    const int tw = w - CB_WAVES;
-    lds_cptr qrow[NKB], krow[NKB];
-#pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) {
-      const uint32_t rb = swz_off<LQ>(lc, 32 * kb + 8 * G);
-      qrow[kb] = L0 + (rb + L::Q0);
-      krow[kb] = L0 + (rb + L::K0);
-    }
-    // dO columns 16 rt + i, pair order (rows 4G + lc/4, +16)
-    lds_cptr opr[2];
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt) opr[rt] = L0 + (swz_off<LO>(4 * G + (lc >> 2), 16 * rt + 4 * (lc & 3)) + L::O0);
-    // A^T operands (m = s of token tile ST, k = t pair order over token block kbs)
-    // from (Q K^T) D-layout tiles; A[t][s] = 0 for t < s
-    auto tiles = [&](auto ns_tag, auto st_tag, Op<2> (&Aop)[2]) {
-      constexpr int NS = decltype(ns_tag)::value, ST = decltype(st_tag)::value;
-      constexpr uint32_t SQK = NS * L::TILE;
-      const float* gates = reinterpret_cast<const float*>(smem + L::G0 + NS * L::GT);
-      const float bs = gates[16 * ST + lc];
-      bf16x8 Kr[NKB];
-#pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) Kr[kb] = lds_ld<bf16x8>(krow[kb] + SQK + ST * 16 * ROWB);
-#pragma unroll
-      for (int kbs = ST / 2; kbs < 2; ++kbs) {
-        f32x4 X[2];
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-          const int tt = 2 * kbs + hf;
-          X[hf] = zero4();
-          if (tt < ST) continue;
-#pragma unroll
-          for (int kb = 0; kb < NKB; ++kb) X[hf] = mfma(lds_ld<bf16x8>(qrow[kb] + SQK + tt * 16 * ROWB), Kr[kb], X[hf]);
-#pragma unroll
-          for (int jj = 0; jj < 4; ++jj) X[hf][jj] = (tt > ST || 4 * G + jj >= lc) ? X[hf][jj] * bs : 0.f;
-        }
-        Aop[kbs] = pack_tiles<2>(X[0], X[1]);
-      }
-    };
-    auto pmul = [&](auto ns_tag, auto st_tag, const Op<2> (&Aop)[2]) {
-      constexpr int NS = decltype(ns_tag)::value, ST = decltype(st_tag)::value;
-      constexpr uint32_t OC = NS * L::OT;
-#pragma unroll
-      for (int rt = 0; rt < 2; ++rt) {
-        f32x4 P = zero4();
-#pragma unroll
-        for (int kbs = ST / 2; kbs < 2; ++kbs) {
-          const bf16x8 dO8 = cat8(lds_tr16(opr[rt] + (OC + (32 * kbs) * 64)), lds_tr16(opr[rt] + (OC + (32 * kbs + 16) * 64)));
-          P = mma<2, 1>(Aop[kbs], Op<1>{{dO8}}, P);
-        }
-        *pslot(rt, ST) = P;
-      }
-    };
-    // the wave's share of a step's P: tiles before Y, products after
-    using I0 = integral_constant<int, 0>;
-    using I1 = integral_constant<int, 1>;
-    using I2 = integral_constant<int, 2>;
-    using I3 = integral_constant<int, 3>;
-    auto share_tiles = [&](auto ns_tag, Op<2> (&A0)[2], Op<2> (&A1)[2]) {
-      if (tw == 0) {
-        tiles(ns_tag, I0{}, A0);
-      } else if (tw == 1) {
-        tiles(ns_tag, I1{}, A0);
-      } else {
-        tiles(ns_tag, I2{}, A0);
-        tiles(ns_tag, I3{}, A1);
-      }
-    };
-    auto share_p = [&](auto ns_tag, const Op<2> (&A0)[2], const Op<2> (&A1)[2]) {
-      if (tw == 0) {
-        pmul(ns_tag, I0{}, A0);
-      } else if (tw == 1) {
-        pmul(ns_tag, I1{}, A0);
-      } else {
-        pmul(ns_tag, I2{}, A0);
-        pmul(ns_tag, I3{}, A1);
-      }
-    };
-    // Gb_i = Sb_{i+1}, published at the last X, stored as split pieces by
-    // token waves 0 and 1 (half of the 32 x D exchange each, 16-byte groups
-    // g = 64 k + l), so that the memory wave issues loads only.  Only the odd
-    // chunks' (plane i / 2): the token kernel forms Gb of the even ones.
-    constexpr int GPR = D / 8, NG = 32 * GPR / 64, NGW = NG / 2;
-    static_assert(NG % 2 == 0, "Gb groups split over two waves");
-    uint32_t xso[NGW];
-#pragma unroll
-    for (int k = 0; k < NGW; ++k) {
-      const int g = 64 * (NGW * tw + k) + l;
-      xso[k] = swz_off<LQ>(g / GPR, 8 * (g % GPR));
-    }
-    auto store_gb = [&](int i) {
-      bf16x8 hi[NGW], lo[NGW];
-#pragma unroll
-      for (int k = 0; k < NGW; ++k) {
-        hi[k] = lds_ld<bf16x8>(L0 + (xso[k] + L::XS0));
-        lo[k] = lds_ld<bf16x8>(L0 + (xso[k] + L::XS0 + L::XSP));
-      }
-      float* gp = p.gb + ((bh * (p.N / 2) + i / 2) * D + 32 * blk) * (int64_t)D;
-#pragma unroll
-      for (int k = 0; k < NGW; ++k) {
-        const int g = 64 * (NGW * tw + k) + l;
-        float* dst = gp + (g / GPR) * D + 8 * (g % GPR);
-        *reinterpret_cast<bf16x8*>(dst) = __builtin_shufflevector(hi[k], lo[k], 0, 1, 2, 3, 8, 9, 10, 11);
-        *reinterpret_cast<bf16x8*>(dst + 4) = __builtin_shufflevector(hi[k], lo[k], 4, 5, 6, 7, 12, 13, 14, 15);
-      }
-    };
-    auto step = [&](auto ns_tag, int j) {  // step j: P of step j+1 (stage NS)
-      const bool next = j + 1 < p.N;
-      Op<2> A0[2], A1[2];
-      if (next) share_tiles(ns_tag, A0, A1);
-      if (tw < 2 && ((p.N - 1 - j) & 1)) store_gb(p.N - 1 - j);  // reads the exchange before Y overwrites it
-      __syncthreads();  // Y
-      if (next) share_p(ns_tag, A0, A1);
-      __syncthreads();  // X
-    };
-    __syncthreads();  // prologue: tiles of steps 0 and 1 landed
-    if (p.N > 0) {
-      Op<2> A0[2], A1[2];
-      share_tiles(I0{}, A0, A1);
-      share_p(I0{}, A0, A1);
-    }
-    __syncthreads();  // step 0's P published
-    for (int j = 0; j < p.N; j += RING) {
-      step(I1{}, j);
-      if (j + 1 < p.N) step(I2{}, j + 1);
-      if (j + 2 < p.N) step(I0{}, j + 2);
-    }
-  } else {
-    // ================================================================ memory
-    const bf16* qg = p.q + bb * p.sq[0] + hh * p.sq[1];
-    const bf16* kg = p.k + bb * p.sk[0] + hh * p.sk[1];
-    const bf16* og = p.o + bb * p.so[0] + hh * p.so[1] + 32 * blk;  // dO columns of the block
-    const float* gsrc = (G == 1 ? p.g : p.beta) + bh * p.T + 4 * lc;
-    DmaPlan<LQ, CB_C, CB_THREADS> dmq[CB_WAVES], dmk[CB_WAVES];
-    DmaPlan<LO, CB_C, CB_THREADS> dmo[CB_WAVES];
-#pragma unroll
-    for (int ww = 0; ww < CB_WAVES; ++ww) {
-      dmq[ww].init(ww, p.sq[2]);
-      dmk[ww].init(ww, p.sk[2]);
-      dmo[ww].init(ww, p.so[2]);
-    }
-    auto issue_loads = [&](int i, int stg) {
-      const int64_t t0 = (int64_t)i * CB_C;
-#pragma unroll
-      for (int ww = 0; ww < CB_WAVES; ++ww) {
-        dmq[ww].issue(qg + t0 * p.sq[2], lds0 + L::Q0 + stg * L::TILE, ww);
-        dmk[ww].issue(kg + t0 * p.sk[2], lds0 + L::K0 + stg * L::TILE, ww);
-        dmo[ww].issue(og + t0 * p.so[2], lds0 + L::O0 + stg * L::OT, ww);
-      }
-      lds_dma16(gsrc + t0, smem + L::G0 + stg * L::GT);
-    };
-    for (int j = 0; j < RING - 1 && j < p.N; ++j) issue_loads(p.N - 1 - j, j);
-    wait_vmem();
-    __syncthreads();
-    __syncthreads();  // prologue: step 0's P
-    auto step = [&](auto stg_tag, int j) {
-      constexpr int STG = decltype(stg_tag)::value;
-      // step j+2 goes to the stage of step j-1, free since the last X
-      if (j + RING - 1 < p.N) issue_loads(p.N - 1 - (j + RING - 1), (STG + RING - 1) % RING);
-      {
-        const float* gg = reinterpret_cast<const float*>(smem + L::G0 + STG * L::GT);
-        const float a = expf(wave_sum(fmaxf(gg[CB_C + l], LOG_FLOOR)));
-        if (l == 0) scal[4 * STG] = a;
-      }
-      __syncthreads();  // Y
-      wait_vmem();      // step j+2's tiles
-      __syncthreads();  // X
-    };
-    for (int j = 0; j < p.N; j += RING) {
-      step(integral_constant<int, 0>{}, j);
-      if (j + 1 < p.N) step(integral_constant<int, 1>{}, j + 1);
-      if (j + 2 < p.N) step(integral_constant<int, 2>{}, j + 2);
-    }
   }
 }
 
@@ -1212,25 +848,22 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
 
 template <int D, int RULE>
 static hipError_t launch_bwd(const ChunkArgs& a, hipStream_t stream) {
-  using KStateLds = std::conditional_t<RULE == 0, DStateLds<D>, StateBwdLds<D, 2>>;
-  constexpr int lds1 = KStateLds::BYTES;
-  constexpr int thr1 = RULE == 0 ? DS_THREADS : CB_THREADS;
-  constexpr int lds2 = TokBwdLds<D>::BYTES;
-  constexpr int thr2 = TokBwdLds<D>::NTHR;
-  void (*k1)(ChunkArgs);
-  if constexpr (RULE == 0)
-    k1 = chunk_bwd_dstate<D>;
-  else
-    k1 = chunk_bwd_state<D, RULE>;
-  hipError_t e = hipFuncSetAttribute((const void*)k1, hipFuncAttributeMaxDynamicSharedMemorySize, lds1);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k1, dim3((unsigned)(a.B * a.H * (D / 32))), dim3(thr1), lds1, stream, a);
-  e = hipGetLastError();
-  if (e != hipSuccess) return e;
   if constexpr (RULE == 0) {
-    // delta: the token gradients of chunk pairs (even checkpoints, odd Gb)
+    // delta: the reverse scan (Gb of the odd chunks), then the token
+    // gradients of chunk pairs (even checkpoints, odd Gb)
+    hipError_t e = chunk_bwd_dscan_launch(a, D, stream);
+    if (e != hipSuccess) return e;
     return chunk_bwd_pair_launch(a, D, stream);
   } else {
+    constexpr int lds1 = StateBwdLds<D, 2>::BYTES;
+    constexpr int lds2 = TokBwdLds<D>::BYTES;
+    constexpr int thr2 = TokBwdLds<D>::NTHR;
+    auto k1 = chunk_bwd_state<D, RULE>;
+    hipError_t e = hipFuncSetAttribute((const void*)k1, hipFuncAttributeMaxDynamicSharedMemorySize, lds1);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k1, dim3((unsigned)(a.B * a.H * (D / 32))), dim3(CB_THREADS), lds1, stream, a);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
     auto k2 = chunk_bwd_tok<D, RULE>;
     e = hipFuncSetAttribute((const void*)k2, hipFuncAttributeMaxDynamicSharedMemorySize, lds2);
     if (e != hipSuccess) return e;

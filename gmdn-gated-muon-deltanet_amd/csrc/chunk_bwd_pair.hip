@@ -1,7 +1,7 @@
 // Level B backward, delta rule: token gradients of chunk pairs.
 //
 // The forward keeps the state checkpoint S_i of the even chunks only, and
-// the reverse scan (chunk_bwd_dstate) writes the state cotangent
+// the reverse scan (chunk_bwd_dscan) writes the state cotangent
 // Gb_i = Sb_{i+1} of the odd chunks only: half of the checkpoint's HBM
 // writes and reads and of Gb's.  One workgroup per (b, h, pair i0 = 2p,
 // i1 = 2p + 1) rebuilds what it lacks on chip:
