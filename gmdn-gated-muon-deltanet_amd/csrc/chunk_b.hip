@@ -14,8 +14,8 @@
 // (train_ablation.py:150-158, :169-175).  Only q, k, v, beta and the
 // log-gates stream from HBM; o streams out; S stays in registers.
 //
-// The delta rule's forward runs chunk_fwd_delta (csrc/chunk_fwd_delta.hip);
-// the kernel below serves adam.
+// The delta rule's forward, and adam's at d = 64, run chunk_fwd_rows
+// (csrc/chunk_fwd_rows.hip); the kernel below serves adam at d = 128.
 // Work split (forward).  A workgroup of 4 waves owns 32 rows of S for the
 // whole sequence; wave (rt, h) owns row tile rt (16 rows) and column half h
 // of S, the token half h of E and of o, and the column half h of G.  Two LDS
@@ -497,8 +497,10 @@ static hipError_t launch_fwd(const ChunkArgs& a, hipStream_t stream) {
 }
 
 hipError_t chunk_fwd_launch(const ChunkArgs& a, int d, int rule, hipStream_t s) {
-  if (rule == 0) return chunk_fwd_delta_launch(a, d, s);
-  return d == 128 ? launch_fwd<128, 2>(a, s) : launch_fwd<64, 2>(a, s);
+  // row-owned state waves: the delta rule, and adam at d = 64 (at d = 128
+  // adam's three state tiles per row block exceed that kernel's registers)
+  if (rule == 0 || d == 64) return chunk_fwd_rows_launch(a, d, rule, s);
+  return launch_fwd<128, 2>(a, s);
 }
 
 }  // namespace gmdn

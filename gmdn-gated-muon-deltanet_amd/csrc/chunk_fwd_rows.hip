@@ -1,9 +1,13 @@
-// Level B forward of the delta rule: state rows owned by single waves.
+// Level B forward with state rows owned by single waves: the delta rule and
+// adam.
 //
-// Same mathematics as chunk_fwd<D, 0> (reference train_ablation.py:142-187
+// Same mathematics as chunk_fwd<D, RULE> (reference train_ablation.py:142-187
 // with fast_scan.py:72-95, E-form): per (b, h) and chunk i with state S_i,
-//   E = V - K S_i^T,   S_{i+1} = a S_i + E^T diag(beta) K,
-//   o = Q S_i^T + tril(Q K^T) diag(beta) E = Q S_i^T + tril(Q K^T) (beta E).
+//   E = V - K S_i^T,   o = Q S_i^T + tril(Q K^T) diag(beta) E,
+//   delta: S_{i+1} = a S_i + E^T diag(beta) K
+//   adam : G = E^T K,  M <- m M + (1-m) G,  V <- n V + (1-n) G^2,
+//          S_{i+1} = a S_i + b M / (sqrt(V) + eps)
+// (fast_scan.py:86-94), with b = mean beta and m, n from gmu, gnu as a from g.
 //
 // Work split.  A workgroup of eight waves, two per SIMD, owns 32 rows of S
 // for the whole sequence (B H D / 32 workgroups, the D/32 of one (b, h) on
@@ -16,8 +20,10 @@
 //    columns 32 kb + 8G + 4u .. +3: its K^T operand is read with that column
 //    permutation), so the two tiles of a block are the next E's operand in
 //    natural column order and every K, Q row operand is one 16-byte read.
-//    E -> G -> S_{i+1} -> the next E needs no exchange and no barrier.  The state is held negated (Sf = -S): then
-//    E = V + K Sf^T and Sf_{i+1} = a Sf + K^T (-beta E), all plain sums.  Each
+//    E -> G -> S_{i+1} -> the next E needs no exchange and no barrier (adam's
+//    moments M, V sit beside S in the same layout).  The state is held
+//    negated (Sf = -S): then E = V + K Sf^T and, for delta,
+//    Sf_{i+1} = a Sf + K^T (-beta E), all plain sums.  Each
 //    product is ordered so that its first half's results can be split into
 //    pieces (and published) while its second half is still in the MFMA pipe.
 //  * Output waves 2, 3, 6, 7 own token tiles 3, 2, 0, 1 (so SIMDs 2 and 3 each
@@ -54,12 +60,13 @@ GMDN_DEV lds_cptr opaque_base(lds_cptr p) {
 constexpr int FD_WAVES = 8;
 constexpr int FD_THREADS = 64 * FD_WAVES;
 
-template <int D>
-struct FwdDeltaLds {
+template <int D, int RULE>
+struct FwdRowsLds {
   static constexpr int NKB = D / 32;
   static constexpr int TILE = CB_C * D * 2;  // one Q or K chunk (bytes)
   static constexpr int VT = CB_C * 32 * 2;   // the workgroup's 32 columns of V
-  static constexpr int GT = 2 * CB_C * 4;    // beta and g of a chunk
+  // beta and g of a chunk (adam: and gmu, gnu)
+  static constexpr int GT = (RULE == 2 ? 4 : 2) * CB_C * 4;
   static constexpr int Q0 = 0;
   static constexpr int K0 = Q0 + RING * TILE;
   static constexpr int V0 = K0 + RING * TILE;
@@ -70,18 +77,19 @@ struct FwdDeltaLds {
   static constexpr int EPW = 2 * 2 * 1024;
   static constexpr int SP0 = G0 + RING * GT;
   static constexpr int EP0 = SP0 + 2 * 2 * SPW;
-  static constexpr int SC0 = EP0 + 2 * 2 * EPW;  // chunk decay a per ring stage
+  // chunk scalars {a, b, m, n} per ring stage (delta: a only)
+  static constexpr int SC0 = EP0 + 2 * 2 * EPW;
   static constexpr int BYTES = SC0 + RING * 16;
   static_assert(BYTES <= 160 * 1024, "delta forward LDS exceeds the 160 KiB of a CU");
 };
 
-template <int D>
-__global__ void __launch_bounds__(FD_THREADS) chunk_fwd_delta(ChunkArgs p) {
+template <int D, int RULE>
+__global__ void __launch_bounds__(FD_THREADS) chunk_fwd_rows(ChunkArgs p) {
   // Q, K tiles: the row swizzle whose transposing reads of four rows by
   // four 16-byte groups (G's permuted K^T operand) hit 16 distinct groups
   using LQ = NSwz<D>;
   using LV = BSwz<32>;
-  using L = FwdDeltaLds<D>;
+  using L = FwdRowsLds<D, RULE>;
   constexpr int NKB = D / 32;  // k-blocks over the state's columns
   constexpr int NCT = D / 16;  // column tiles of a state row block
   constexpr int ROWB = D * 2;  // bytes per Q / K row
@@ -105,8 +113,11 @@ __global__ void __launch_bounds__(FD_THREADS) chunk_fwd_delta(ChunkArgs p) {
     const bf16* qg = p.q + bb * p.sq[0] + hh * p.sq[1];
     const bf16* kg = p.k + bb * p.sk[0] + hh * p.sk[1];
     const bf16* vg = p.v + bb * p.sv[0] + hh * p.sv[1] + 32 * blk;
-    // gates: lanes 0-15 beta, 16-31 g (16 bytes each); copied by wave 4's low half
-    const float* gsrc = (G == 1 ? p.g : p.beta) + bh * p.T + 4 * lc;
+    // gates, 16 bytes per lane: wave 4 lanes 0-15 beta, 16-31 g; adam's
+    // wave 5 lanes 0-15 gmu, 16-31 gnu (each wave reduces what it copies)
+    const bool gcopy = cw == 0 || RULE == 2;
+    const float* gsrc =
+        (cw == 0 ? (G == 0 ? p.beta : p.g) : (G == 0 ? p.gmu : p.gnu)) + bh * p.T + 4 * lc;
     DQ dq, dk;
     DV dv;
     dq.init(cw, p.sq[2]);
@@ -117,7 +128,7 @@ __global__ void __launch_bounds__(FD_THREADS) chunk_fwd_delta(ChunkArgs p) {
       dq.issue(qg + t0 * p.sq[2], lds0 + L::Q0 + stg * L::TILE, cw);
       dk.issue(kg + t0 * p.sk[2], lds0 + L::K0 + stg * L::TILE, cw);
       dv.issue(vg + t0 * p.sv[2], lds0 + L::V0 + stg * L::VT, cw);
-      if (cw == 0 && l < 32) lds_dma16(gsrc + t0, smem + L::G0 + stg * L::GT);
+      if (gcopy && l < 32) lds_dma16(gsrc + t0, smem + L::G0 + stg * L::GT + 512 * cw);
     };
     // vector-memory operations this wave issues per chunk copy
     constexpr int ND = 2 * DQ::NOPS + DV::NOPS;
@@ -125,16 +136,29 @@ __global__ void __launch_bounds__(FD_THREADS) chunk_fwd_delta(ChunkArgs p) {
     auto wait_next = [&](bool issued) {
       if (!issued)
         wait_vmem();
-      else if (cw == 0)
+      else if (gcopy)
         wait_vmem_le<ND + 1>();
       else
         wait_vmem_le<ND>();
     };
-    // a = exp(sum over the chunk of max(g, log 1e-6)) of the chunk in stage stg
+    // a = exp(sum over the chunk of max(g, log 1e-6)) of the chunk in stage
+    // stg (wave 4); adam: b = mean(beta) (wave 4), m, n as a from gmu, gnu
+    // (wave 5).  The copy waves share SIMDs with the state waves, so the
+    // reductions run as two interleaved chains per wave.
     auto decay = [&](int stg) {
+      const lds_cptr gg = L0 + (L::G0 + stg * L::GT + 4 * l);
+      float* sc = reinterpret_cast<float*>(smem + L::SC0 + stg * 16);
       if (cw == 0) {
-        const float a = expf(wave_sum(fmaxf(lds_ld<float>(L0 + (L::G0 + stg * L::GT + 256 + 4 * l)), LOG_FLOOR)));
-        if (l == 0) *reinterpret_cast<float*>(smem + L::SC0 + stg * 16) = a;
+        if constexpr (RULE == 2) {
+          const f32x2 s = wave_sum2(fmaxf(lds_ld<float>(gg + 256), LOG_FLOOR), lds_ld<float>(gg));
+          if (l == 0) *reinterpret_cast<f32x2*>(sc) = f32x2{expf(s[0]), s[1] * (1.f / CB_C)};
+        } else {
+          const float a = expf(wave_sum(fmaxf(lds_ld<float>(gg + 256), LOG_FLOOR)));
+          if (l == 0) *sc = a;
+        }
+      } else if constexpr (RULE == 2) {
+        const f32x2 s = wave_sum2(fmaxf(lds_ld<float>(gg + 512), LOG_FLOOR), fmaxf(lds_ld<float>(gg + 768), LOG_FLOOR));
+        if (l == 0) *reinterpret_cast<f32x2*>(sc + 2) = f32x2{expf(s[0]), expf(s[1])};
       }
     };
     issue_loads(0, 0);
@@ -189,8 +213,9 @@ __global__ void __launch_bounds__(FD_THREADS) chunk_fwd_delta(ChunkArgs p) {
 
     f32x4 Sf[NCT];  // -S, lane (r, G): columns 32 (ct / 2) + 8G + 4 (ct % 2) + j of row r
     Op<2> Sp[NKB];  // its pieces, natural order
+    f32x4 Mm[NCT], Vv[NCT];  // adam's moments, same layout
 #pragma unroll
-    for (int ct = 0; ct < NCT; ++ct) Sf[ct] = zero4();
+    for (int ct = 0; ct < NCT; ++ct) Sf[ct] = Mm[ct] = Vv[ct] = zero4();
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) Sp[kb] = pack_tiles<2>(Sf[2 * kb], Sf[2 * kb + 1]);
 #pragma unroll
@@ -202,6 +227,18 @@ __global__ void __launch_bounds__(FD_THREADS) chunk_fwd_delta(ChunkArgs p) {
     auto state_chunk = [&](auto stg_tag, int i) {
       constexpr int STG = decltype(stg_tag)::value;
       constexpr uint32_t SQK = STG * L::TILE;
+      if constexpr (RULE == 2) {
+        if (p.states) {  // adam: M_i, V_i (float32 planes) for the backward
+          const int64_t plane = p.B * p.H * (int64_t)N * D * D;
+          float* mp = p.states + plane + ((bh * N + i) * D + 32 * blk + 16 * w + lc) * (int64_t)D + 8 * G;
+#pragma unroll
+          for (int ct = 0; ct < NCT; ++ct) {
+            const int c = 32 * (ct >> 1) + 4 * (ct & 1);
+            *reinterpret_cast<f32x4*>(mp + c) = Mm[ct];
+            *reinterpret_cast<f32x4*>(mp + plane + c) = Vv[ct];
+          }
+        }
+      }
       // E = V + K Sf^T, token tiles st (lane (r, G): tokens 16 st + 4G + j),
       // one token block (two tiles) at a time: the first block's -beta E is
       // split and published while the second block is in the MFMA pipe
@@ -212,8 +249,10 @@ __global__ void __launch_bounds__(FD_THREADS) chunk_fwd_delta(ChunkArgs p) {
         E[st] = f32x4{(float)vb[0], (float)vb[1], (float)vb[2], (float)vb[3]};
       }
       f32x4 bt[4];
+      if constexpr (RULE == 0) {
 #pragma unroll
-      for (int st = 0; st < 4; ++st) bt[st] = lds_ld<f32x4>(bp + (STG * L::GT + st * 64));
+        for (int st = 0; st < 4; ++st) bt[st] = lds_ld<f32x4>(bp + (STG * L::GT + st * 64));
+      }
       bf16x8 Kr[4][NKB], Kc[2][NCT];
 #pragma unroll
       for (int st = 0; st < 4; ++st)
@@ -235,8 +274,11 @@ __global__ void __launch_bounds__(FD_THREADS) chunk_fwd_delta(ChunkArgs p) {
       };
       const uint32_t eo = (uint32_t)(i & 1) * (2 * L::EPW);
       Op<2> WE[2];
-      auto we_block = [&](int kt) {
-        WE[kt] = pack_tiles<2>(-(bt[2 * kt] * E[2 * kt]), -(bt[2 * kt + 1] * E[2 * kt + 1]));
+      auto we_block = [&](int kt) {  // -beta E (delta), -E (adam)
+        if constexpr (RULE == 0)
+          WE[kt] = pack_tiles<2>(-(bt[2 * kt] * E[2 * kt]), -(bt[2 * kt + 1] * E[2 * kt + 1]));
+        else
+          WE[kt] = pack_tiles<2>(-E[2 * kt], -E[2 * kt + 1]);
 #pragma unroll
         for (int u = 0; u < 2; ++u) lds_st<bf16x8>(epw + eo + (kt * 2 + u) * 1024, WE[kt].v[u]);
       };
@@ -259,28 +301,63 @@ __global__ void __launch_bounds__(FD_THREADS) chunk_fwd_delta(ChunkArgs p) {
       }
       __builtin_amdgcn_sched_barrier(0);
       we_block(1);
-      // Sf_{i+1} = a Sf_i + K^T (-beta E), column tiles ct (transposed tiles in
-      // the permuted column order above): token block 0 for every tile, then
-      // block 1 tile pair by tile pair, each pair split and published while
-      // the next is in the MFMA pipe
-      const float a = lds_ld<float>(L0 + (L::SC0 + STG * 16));
-#pragma unroll
-      for (int ct = 0; ct < NCT; ++ct) Sf[ct] = a * Sf[ct];
-#pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int ct = 0; ct < NCT; ++ct) Sf[ct] = mfma(Kc[0][ct], WE[0].v[u], Sf[ct]);
       const uint32_t po = (uint32_t)((i + 1) & 1) * (2 * L::SPW);
+      if constexpr (RULE == 0) {
+        // Sf_{i+1} = a Sf_i + K^T (-beta E), column tiles ct (transposed tiles
+        // in the permuted column order above): token block 0 for every tile,
+        // then block 1 tile pair by tile pair, each pair split and published
+        // while the next is in the MFMA pipe
+        const float a = lds_ld<float>(L0 + (L::SC0 + STG * 16));
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) {
+        for (int ct = 0; ct < NCT; ++ct) Sf[ct] = a * Sf[ct];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          Sf[2 * kb] = mfma(Kc[1][2 * kb], WE[1].v[u], Sf[2 * kb]);
-          Sf[2 * kb + 1] = mfma(Kc[1][2 * kb + 1], WE[1].v[u], Sf[2 * kb + 1]);
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int ct = 0; ct < NCT; ++ct) Sf[ct] = mfma(Kc[0][ct], WE[0].v[u], Sf[ct]);
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            Sf[2 * kb] = mfma(Kc[1][2 * kb], WE[1].v[u], Sf[2 * kb]);
+            Sf[2 * kb + 1] = mfma(Kc[1][2 * kb + 1], WE[1].v[u], Sf[2 * kb + 1]);
+          }
+          Sp[kb] = pack_tiles<2>(Sf[2 * kb], Sf[2 * kb + 1]);
+#pragma unroll
+          for (int u = 0; u < 2; ++u) lds_st<bf16x8>(spw + po + (kb * 2 + u) * 1024, Sp[kb].v[u]);
         }
-        Sp[kb] = pack_tiles<2>(Sf[2 * kb], Sf[2 * kb + 1]);
+      } else {
+        // adam: Gn = K^T (-E) = -G^T tiles, then per tile pair
+        //   M = m M + (1 - m) G,  V = n V + (1 - n) G^2,
+        //   Sf = a Sf - b M / (sqrt(V) + eps)
+        // split and published while the next pair is in the MFMA pipe
+        const f32x4 sc = lds_ld<f32x4>(L0 + (L::SC0 + STG * 16));
+        const float a = sc[0], b = sc[1], m = sc[2], n = sc[3];
+        f32x4 Gn[NCT];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) lds_st<bf16x8>(spw + po + (kb * 2 + u) * 1024, Sp[kb].v[u]);
+        for (int ct = 0; ct < NCT; ++ct) Gn[ct] = zero4();
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int ct = 0; ct < NCT; ++ct) Gn[ct] = mfma(Kc[0][ct], WE[0].v[u], Gn[ct]);
+        auto update = [&](int ct) {
+          Mm[ct] = m * Mm[ct] - (1.f - m) * Gn[ct];
+          Vv[ct] = n * Vv[ct] + (1.f - n) * (Gn[ct] * Gn[ct]);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) Sf[ct][j] = a * Sf[ct][j] - b * Mm[ct][j] * hw_rcp(hw_sqrt(Vv[ct][j]) + p.eps);
+        };
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            Gn[2 * kb] = mfma(Kc[1][2 * kb], WE[1].v[u], Gn[2 * kb]);
+            Gn[2 * kb + 1] = mfma(Kc[1][2 * kb + 1], WE[1].v[u], Gn[2 * kb + 1]);
+          }
+          update(2 * kb);
+          update(2 * kb + 1);
+          Sp[kb] = pack_tiles<2>(Sf[2 * kb], Sf[2 * kb + 1]);
+#pragma unroll
+          for (int u = 0; u < 2; ++u) lds_st<bf16x8>(spw + po + (kb * 2 + u) * 1024, Sp[kb].v[u]);
+        }
       }
       __syncthreads();  // barrier i + 1
     };
@@ -356,6 +433,11 @@ __global__ void __launch_bounds__(FD_THREADS) chunk_fwd_delta(ChunkArgs p) {
 #pragma unroll
         for (int st = 0; st <= TT; ++st) At[st] = mfma(Kr[st], Qr[kb], At[st]);
       }
+      // adam publishes -E (not -beta E): beta goes on A's columns s
+      if constexpr (RULE == 2) {
+#pragma unroll
+        for (int st = 0; st <= TT; ++st) At[st] *= lds_ld<f32x4>(L0 + (L::G0 + STG * L::GT + 4 * (16 * st + 4 * G)));
+      }
       // keep s <= t on the diagonal tile: lane (t, G) row 4G + j is s
 #pragma unroll
       for (int j = 0; j < 4; ++j)
@@ -379,12 +461,12 @@ __global__ void __launch_bounds__(FD_THREADS) chunk_fwd_delta(ChunkArgs p) {
         for (int u = 0; u < 2; ++u)
 #pragma unroll
           for (int rt = 0; rt < 2; ++rt) O[rt] = mfma(Sr[rt][kb].v[u], Qr[kb], O[rt]);
-      // checkpoint S_i of the even chunks (the backward rebuilds the odd
-      // ones) from the pieces just read, negated back: this wave's row tile
-      // and half of the k-blocks
-      if (p.states && (i & 1) == 0) {
+      // checkpoint S_i from the pieces just read, negated back: this wave's
+      // row tile and half of the k-blocks.  The delta rule keeps the even
+      // chunks only (its backward rebuilds the odd ones); adam every chunk.
+      if (p.states && (RULE == 2 || (i & 1) == 0)) {
         constexpr int rt = OW & 1;
-        const int64_t plane = bh * ((N + 1) / 2) + i / 2;
+        const int64_t plane = RULE == 2 ? bh * N + i : bh * ((N + 1) / 2) + i / 2;
         float* sp = p.states + (plane * D + 32 * blk + 16 * rt + lc) * (int64_t)D + 8 * G;
 #pragma unroll
         for (int kh = 0; kh < NKB / 2; ++kh) {
@@ -418,10 +500,10 @@ __global__ void __launch_bounds__(FD_THREADS) chunk_fwd_delta(ChunkArgs p) {
   }
 }
 
-template <int D>
-static hipError_t launch_fwd_delta(const ChunkArgs& a, hipStream_t stream) {
-  auto kern = chunk_fwd_delta<D>;
-  constexpr int lds = FwdDeltaLds<D>::BYTES;
+template <int D, int RULE>
+static hipError_t launch_fwd_rows(const ChunkArgs& a, hipStream_t stream) {
+  auto kern = chunk_fwd_rows<D, RULE>;
+  constexpr int lds = FwdRowsLds<D, RULE>::BYTES;
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   if (e != hipSuccess) return e;
   const int64_t grid = a.B * a.H * (D / 32);
@@ -429,8 +511,10 @@ static hipError_t launch_fwd_delta(const ChunkArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-hipError_t chunk_fwd_delta_launch(const ChunkArgs& a, int d, hipStream_t s) {
-  return d == 128 ? launch_fwd_delta<128>(a, s) : launch_fwd_delta<64>(a, s);
+hipError_t chunk_fwd_rows_launch(const ChunkArgs& a, int d, int rule, hipStream_t s) {
+  if (rule == 0) return d == 128 ? launch_fwd_rows<128, 0>(a, s) : launch_fwd_rows<64, 0>(a, s);
+  if (rule == 2 && d == 64) return launch_fwd_rows<64, 2>(a, s);
+  return hipErrorNotSupported;
 }
 
 }  // namespace gmdn

@@ -349,6 +349,23 @@ GMDN_DEV float wave_sum(float x) {
   return (r0 + r1) + (r2 + r3);
 }
 
+// wave_sum of two values at once: two independent DPP chains interleaved,
+// half the dependent latency of two calls.
+GMDN_DEV f32x2 wave_sum2(float x, float y) {
+  x += dpp_mov<0xB1>(x);
+  y += dpp_mov<0xB1>(y);
+  x += dpp_mov<0x4E>(x);
+  y += dpp_mov<0x4E>(y);
+  x += dpp_mov<0x124>(x);
+  y += dpp_mov<0x124>(y);
+  x += dpp_mov<0x128>(x);
+  y += dpp_mov<0x128>(y);
+  const int xi = __builtin_bit_cast(int, x), yi = __builtin_bit_cast(int, y);
+  auto rl = [](int v, int lane) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(v, lane)); };
+  return f32x2{(rl(xi, 0) + rl(xi, 16)) + (rl(xi, 32) + rl(xi, 48)),
+               (rl(yi, 0) + rl(yi, 16)) + (rl(yi, 32) + rl(yi, 48))};
+}
+
 // Sum over the 4 lane groups (G) of a value held per lane: result equal in
 // all lanes sharing l%16.
 GMDN_DEV float group_sum(float x) {
