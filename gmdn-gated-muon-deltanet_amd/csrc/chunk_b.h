@@ -93,6 +93,9 @@ hipError_t wy_fwd_launch(const ChunkArgs& a, int d, float* ws, hipStream_t s);
 hipError_t chunk_bwd_launch(const ChunkArgs& a, int d, int rule, hipStream_t s);
 // delta rule: the reverse scan of the state cotangent (Gb of the odd chunks)
 hipError_t chunk_bwd_dscan_launch(const ChunkArgs& a, int d, hipStream_t s);
+// adam at d = 64: the reverse scan of the state and moment cotangents (Gb of
+// every chunk; partial sums of da, db, dm, dn per chunk and 16-row block)
+hipError_t chunk_bwd_ascan_launch(const ChunkArgs& a, int d, hipStream_t s);
 // the matrix form's per-chunk Kw, Uv (fwd) and gS (bwd) as (B, H, N, d, d)
 // float32, and a, b, m, n (four B H N arrays): muon (fwd and bwd together,
 // for its backward) and adam at d = 128 (fwd: training forward, bwd: backward)

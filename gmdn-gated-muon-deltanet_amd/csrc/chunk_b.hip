@@ -647,7 +647,7 @@ size_t gmdn_chunk_bwd_workspace_bytes(const gmdn_chunk_desc* desc) {
   // delta rule keeps the odd chunks' only), then per (chunk, row block)
   // partial sums of the chunk scalars' gradients
   const size_t chunks = (size_t)(desc->B * desc->H * (desc->T / CB_C));
-  return gb_planes(desc) * desc->d * desc->d * sizeof(float) + chunks * (desc->d / 32) * 4 * sizeof(float);
+  return gb_planes(desc) * desc->d * desc->d * sizeof(float) + chunks * (desc->d / 16) * 4 * sizeof(float);
 }
 
 int gmdn_chunk_bwd(const gmdn_chunk_desc* desc, const void* q, const void* k, const void* v,

@@ -16,12 +16,11 @@
 //
 // Two kernels per rule:
 //  * the reverse recurrence of Sb.  Row r of Sb_i needs only row r of Sb_{i+1}
-//    (dE[:, r] = A^T dO[:, r] + diag(w) K Sb[r, :]^T), so one workgroup owns 32
-//    rows, with an LDS-DMA ring of Q, K and the workgroup's dO columns, and
-//    writes Gb_i: chunk_bwd_dscan (delta, odd chunks only;
-//    chunk_bwd_dscan.hip) and chunk_bwd_state (adam, every chunk; 4 waves, wave
-//    (rt, h) holds 16 rows x column half h and the moment cotangents in
-//    registers).
+//    (dE[:, r] = A^T dO[:, r] + diag(w) K Sb[r, :]^T), so one workgroup owns a
+//    row block, with an LDS-DMA ring of the chunk's tiles, and writes Gb_i:
+//    chunk_bwd_dscan (delta, odd chunks only; chunk_bwd_dscan.hip) and
+//    chunk_bwd_ascan (adam at d = 64, every chunk, with the moment
+//    cotangents; chunk_bwd_ascan.hip).
 //  * the token gradients, chunk-parallel.  From S_i (saved by the forward)
 //    and Gb_i they recompute E, A and dE and form dQ, dK, dV and the gate
 //    gradients; every contraction over the state's rows is local to the
@@ -36,367 +35,6 @@
 #include <type_traits>
 
 namespace gmdn {
-
-// ============================================================ chunk_bwd_state
-// The adam rule's reverse scan (the delta rule's is chunk_bwd_dscan).
-template <int D, int RULE>
-struct StateBwdLds {
-  static_assert(RULE == 2, "the 4-wave reverse scan serves the adam rule");
-  static constexpr bool ADAM = RULE == 2;
-  static constexpr int NKBH = D / 64;
-  static constexpr int TILE = CB_C * D * 2;   // one Q or K chunk (bytes)
-  static constexpr int OT = CB_C * 32 * 2;    // the workgroup's 32 columns of dO (or V)
-  static constexpr int GT = 4 * CB_C * 4;     // gate chunk
-  static constexpr int Q0 = 0;
-  static constexpr int K0 = Q0 + RING * TILE;
-  static constexpr int O0 = K0 + RING * TILE;
-  static constexpr int V0 = O0 + RING * OT;                        // adam: V columns (E recompute)
-  static constexpr int G0 = V0 + (ADAM ? RING * OT : 0);
-  static constexpr int XS0 = G0 + RING * GT;                       // Gb^T operand exchange
-  static constexpr int XE0 = XS0 + CB_WAVES * NKBH * 2 * 1024;     // -dE operand exchange
-  static constexpr int XN0 = XE0 + CB_WAVES * 2 * 1024;            // adam: -E operand exchange
-  static constexpr int P0 = XN0 + (ADAM ? CB_WAVES * 2 * 1024 : 0);  // adam: 4 partial sums per wave
-  static constexpr int BYTES = P0 + CB_WAVES * 16;
-  static_assert(BYTES <= 160 * 1024, "state backward LDS exceeds the 160 KiB of a CU");
-  static constexpr int DMA_OPS = 2 * (CB_C * D / 8) / CB_THREADS + (ADAM ? 2 : 1) * (CB_C * 32 / 8) / CB_THREADS;
-};
-
-template <int D, int RULE>
-__global__ void __launch_bounds__(CB_THREADS) chunk_bwd_state(ChunkArgs p) {
-  using LQ = BSwz<D>;
-  using LO = BSwz<32>;
-  using L = StateBwdLds<D, RULE>;
-  constexpr int NKB = D / 32;   // k-blocks over the state's columns
-  constexpr int NTH = D / 32;   // column tiles in a half
-  constexpr int NKBH = L::NKBH;
-  constexpr int ROWB = D * 2;   // bytes per Q/K row
-  extern __shared__ __align__(16) char smem[];
-
-  int64_t bh;
-  int blk;
-  map_block(p.B * p.H, D / 32, bh, blk);
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int l = lane_id(), G = l >> 4, lc = l & 15;
-  const int rt = w >> 1, h = w & 1;
-  const int r0 = 32 * blk + 16 * rt;  // first state row of this wave
-  const int64_t bb = bh / p.H, hh = bh % p.H;
-  const bf16* qg = p.q + bb * p.sq[0] + hh * p.sq[1];
-  const bf16* kg = p.k + bb * p.sk[0] + hh * p.sk[1];
-  const bf16* og = p.o + bb * p.so[0] + hh * p.so[1] + 32 * blk;  // dO columns of the block
-  const bf16* vg = p.v + bb * p.sv[0] + hh * p.sv[1] + 32 * blk;  // V columns (adam)
-  const float* gsrc = (G == 0 ? p.beta : G == 1 ? p.g : G == 2 ? (RULE == 2 ? p.gmu : p.beta)
-                                                               : (RULE == 2 ? p.gnu : p.beta)) +
-                      bh * p.T + 4 * lc;
-
-  // per-lane LDS byte offsets (stage, row-tile and k offsets are immediates)
-  uint32_t rowoff[NKB][2];
-#pragma unroll
-  for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-    for (int hf = 0; hf < 2; ++hf) rowoff[kb][hf] = swz_off<LQ>(lc, 32 * kb + 16 * hf + 4 * G);
-  uint32_t coloff[NTH];
-#pragma unroll
-  for (int t = 0; t < NTH; ++t) coloff[t] = swz_off<LQ>(4 * G + (lc >> 2), 16 * (h * NTH + t) + 4 * (lc & 3));
-  // transposing reads of dO (rows 32 kbs + 16 u + 4G + lc/4, columns 16 rt + 4 (lc & 3))
-  const uint32_t ooff = swz_off<LO>(4 * G + (lc >> 2), 16 * rt + 4 * (lc & 3));
-  const uint32_t lds0 = lds_addr(smem);
-  const lds_ptr L0 = lds_base(smem);
-  lds_cptr qrow[NKB][2], krow[NKB][2];
-#pragma unroll
-  for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
-      qrow[kb][hf] = L0 + (rowoff[kb][hf] + L::Q0);
-      krow[kb][hf] = L0 + (rowoff[kb][hf] + L::K0);
-    }
-  lds_cptr qcol[NTH], kcol[NTH];
-#pragma unroll
-  for (int t = 0; t < NTH; ++t) {
-    qcol[t] = L0 + (coloff[t] + L::Q0);
-    kcol[t] = L0 + (coloff[t] + L::K0);
-  }
-  const lds_cptr oaddr = L0 + (ooff + L::O0);
-  const lds_cptr vaddr = L0 + (ooff + L::V0);
-  const lds_ptr xsaddr = L0 + (16 * l + L::XS0);
-  const lds_ptr xeaddr = L0 + (16 * l + L::XE0);
-  const lds_ptr xnaddr = L0 + (16 * l + L::XN0);
-  float* psum = reinterpret_cast<float*>(smem + L::P0);
-
-  DmaPlan<LQ, CB_C, CB_THREADS> dmq, dmk;
-  DmaPlan<LO, CB_C, CB_THREADS> dmo, dmv;
-  dmq.init(w, p.sq[2]);
-  dmk.init(w, p.sk[2]);
-  dmo.init(w, p.so[2]);
-  if constexpr (RULE == 2) dmv.init(w, p.sv[2]);
-  auto issue_loads = [&](int i, int stg) {
-    const int64_t t0 = (int64_t)i * CB_C;
-    dmq.issue(qg + t0 * p.sq[2], lds0 + L::Q0 + stg * L::TILE, w);
-    dmk.issue(kg + t0 * p.sk[2], lds0 + L::K0 + stg * L::TILE, w);
-    dmo.issue(og + t0 * p.so[2], lds0 + L::O0 + stg * L::OT, w);
-    if constexpr (RULE == 2) dmv.issue(vg + t0 * p.sv[2], lds0 + L::V0 + stg * L::OT, w);
-    if (w == 0) lds_dma16(gsrc + t0, smem + L::G0 + stg * L::GT);
-  };
-
-  f32x4 Sb[NTH];   // dL/dS_{i+1}, this lane's row, the wave's column half
-  f32x4 Mb[NTH], Vb[NTH];  // adam: dL/dM_{i+1}, dL/dV_{i+1}
-#pragma unroll
-  for (int t = 0; t < NTH; ++t) Sb[t] = Mb[t] = Vb[t] = zero4();
-  // adam: chunk i's S_i row (pair-order pieces of all columns) and M_i, V_i
-  // (the wave's column half), loaded one chunk ahead
-  f32x4 Sraw[NKB][2], Mp[NTH], Vp[NTH];
-  auto load_states = [&](int i) {
-    const int64_t plane = p.B * p.H * p.N * (int64_t)D * D;
-    const float* sp = p.states + ((bh * p.N + i) * D + r0 + lc) * (int64_t)D;
-#pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) {
-      Sraw[kb][0] = unsplit_piece(*reinterpret_cast<const bf16x8*>(sp + 32 * kb + 4 * G));
-      Sraw[kb][1] = unsplit_piece(*reinterpret_cast<const bf16x8*>(sp + 32 * kb + 16 + 4 * G));
-    }
-#pragma unroll
-    for (int t = 0; t < NTH; ++t) {
-      Mp[t] = *reinterpret_cast<const f32x4*>(sp + plane + 16 * (h * NTH + t) + 4 * G);
-      Vp[t] = *reinterpret_cast<const f32x4*>(sp + 2 * plane + 16 * (h * NTH + t) + 4 * G);
-    }
-  };
-  auto xn_addr = [&](int ww) { return xnaddr + (ww * 2) * 1024; };
-  auto xs_addr = [&](int ww, int k) { return xsaddr + ((ww * NKBH + k) * 2) * 1024; };
-  auto xe_addr = [&](int ww) { return xeaddr + (ww * 2) * 1024; };
-  auto publish_Gb = [&](const f32x4 (&X)[NTH]) {
-#pragma unroll
-    for (int kbl = 0; kbl < NKBH; ++kbl) {
-      const Op<2> x = pack_tiles<2>(X[2 * kbl], X[2 * kbl + 1]);
-      lds_st<bf16x8>(xs_addr(w, kbl), x.v[0]);
-      lds_st<bf16x8>(xs_addr(w, kbl) + 1024, x.v[1]);
-    }
-  };
-  auto read_op = [&](lds_cptr addr) {
-    Op<2> x;
-    x.v[0] = lds_ld<bf16x8>(addr);
-    x.v[1] = lds_ld<bf16x8>(addr + 1024);
-    return x;
-  };
-  float a = 0.f, bsc = 0.f, msc = 0.f, nsc = 0.f;
-  auto chunk_scalars = [&](int stg) {
-    const float* gg = reinterpret_cast<const float*>(smem + L::G0 + stg * L::GT);
-    a = expf(wave_sum(fmaxf(gg[CB_C + l], LOG_FLOOR)));
-    if constexpr (RULE == 2) {
-      bsc = wave_sum(gg[l]) * (1.f / CB_C);
-      msc = expf(wave_sum(fmaxf(gg[2 * CB_C + l], LOG_FLOOR)));
-      nsc = expf(wave_sum(fmaxf(gg[3 * CB_C + l], LOG_FLOOR)));
-    }
-  };
-
-  // chunks are visited in reverse: step j handles chunk N-1-j, ring stage j % RING
-  for (int j = 0; j < RING - 1 && j < p.N; ++j) issue_loads(p.N - 1 - j, j);
-  if (p.N > 0) load_states(p.N - 1);
-  wait_vmem();
-  __syncthreads();
-  if (p.N > 0) chunk_scalars(0);
-
-  auto chunk = [&](auto stg_tag, int j) {
-    constexpr int STG = decltype(stg_tag)::value;
-    constexpr uint32_t SQK = STG * L::TILE;
-    constexpr uint32_t OC = STG * L::OT;
-    const float* gates = reinterpret_cast<const float*>(smem + L::G0 + STG * L::GT);
-    const int i = p.N - 1 - j;
-    const bool ahead = j + RING - 1 < p.N;
-    if (ahead) issue_loads(p.N - 1 - (j + RING - 1), (STG + RING - 1) % RING);
-    float* gp = p.gb + ((bh * p.N + i) * D + r0 + lc) * (int64_t)D + 4 * G;
-    auto rows = [&](const lds_cptr (&base)[NKB][2], int rowtile, int kb) {
-      return cat8(lds_ld<bf16x4>(base[kb][0] + SQK + rowtile * 16 * ROWB),
-                  lds_ld<bf16x4>(base[kb][1] + SQK + rowtile * 16 * ROWB));
-    };
-    // dO operand (k = tokens 32 kbs + pair order, n = this lane's state row)
-    auto dop = [&](int kbs) {
-      return cat8(lds_tr16(oaddr + (OC + (32 * kbs) * 64)), lds_tr16(oaddr + (OC + (32 * kbs + 16) * 64)));
-    };
-    using std::integral_constant;
-    using I0 = integral_constant<int, 0>;
-    using I1 = integral_constant<int, 1>;
-    if constexpr (RULE == 2) {
-      // ---------------- adam A: -E = K S_i^T - V for this wave's tokens (reference
-      // fast_scan.py:89-94 recomputed: G_i is needed by the moment VJP)
-      auto segA = [&](auto rt_tag, auto h_tag) {
-        constexpr int RT = decltype(rt_tag)::value, H = decltype(h_tag)::value;
-        constexpr uint32_t VC = STG * L::OT;
-        Op<2> Sop[NKB];
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb) Sop[kb] = pack_tiles<2>(Sraw[kb][0], Sraw[kb][1]);
-        f32x4 Nt[2];
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const bf16x4 vb = lds_tr16(vaddr + (VC + (32 * H + 16 * u) * 64));
-          Nt[u] = f32x4{-(float)vb[0], -(float)vb[1], -(float)vb[2], -(float)vb[3]};
-#pragma unroll
-          for (int kb = 0; kb < NKB; ++kb) Nt[u] = mma<1, 2>(Op<1>{{rows(krow, 2 * H + u, kb)}}, Sop[kb], Nt[u]);
-        }
-        const Op<2> en = pack_tiles<2>(Nt[0], Nt[1]);
-        lds_st<bf16x8>(xn_addr(2 * RT + H), en.v[0]);
-        lds_st<bf16x8>(xn_addr(2 * RT + H) + 1024, en.v[1]);
-      };
-      switch (w) {
-        case 0: segA(I0{}, I0{}); break;
-        case 1: segA(I0{}, I1{}); break;
-        case 2: segA(I1{}, I0{}); break;
-        default: segA(I1{}, I1{}); break;
-      }
-      __syncthreads();  // -E halves published
-      // ---------------- adam B: G_i, the moment VJP (reference fast_scan.py:167-182)
-      {
-        Op<2> EN[2];
-#pragma unroll
-        for (int hs = 0; hs < 2; ++hs) EN[hs] = read_op(xn_addr(2 * rt + hs));
-        f32x4 Gb[NTH];
-        float da = 0.f, db = 0.f, dm = 0.f, dn = 0.f;
-#pragma unroll
-        for (int t = 0; t < NTH; ++t) {
-          f32x4 acc = zero4();
-#pragma unroll
-          for (int kbs = 0; kbs < 2; ++kbs) {
-            const uint32_t ro = SQK + kbs * 32 * ROWB;
-            const bf16x8 kc = cat8(lds_tr16(kcol[t] + ro), lds_tr16(kcol[t] + ro + 16 * ROWB));
-            acc = mma<1, 2>(Op<1>{{kc}}, EN[kbs], acc);
-          }
-          const int ct = h * NTH + t;  // column tile of S_i held in Sraw
-          const f32x4 Si = Sraw[ct >> 1][ct & 1];
-#pragma unroll
-          for (int jj = 0; jj < 4; ++jj) {
-            const float g = -acc[jj];
-            const float mn = msc * Mp[t][jj] + (1.f - msc) * g;
-            const float vn = nsc * Vp[t][jj] + (1.f - nsc) * g * g;
-            const float sq = hw_sqrt(vn);
-            const float rden = hw_rcp(sq + p.eps);
-            const float sb = Sb[t][jj];
-            da += sb * Si[jj];
-            db += sb * mn * rden;
-            const float mt = Mb[t][jj] + bsc * sb * rden;
-            const float vt = Vb[t][jj] - bsc * sb * mn * rden * rden * hw_rcp(2.f * fmaxf(sq, 1e-12f));
-            dm += mt * (Mp[t][jj] - g);
-            dn += vt * (Vp[t][jj] - g * g);
-            Gb[t][jj] = (1.f - msc) * mt + (1.f - nsc) * 2.f * g * vt;
-            Mb[t][jj] = msc * mt;
-            Vb[t][jj] = nsc * vt;
-          }
-          *reinterpret_cast<bf16x8*>(gp + 16 * (h * NTH + t)) = split_piece(Gb[t]);
-        }
-        publish_Gb(Gb);
-        da = wave_sum(da);
-        db = wave_sum(db);
-        dm = wave_sum(dm);
-        dn = wave_sum(dn);
-        if (l == 0) {  // the wave's own slots, summed below in a fixed order
-          psum[4 * w + 0] = da;
-          psum[4 * w + 1] = db;
-          psum[4 * w + 2] = dm;
-          psum[4 * w + 3] = dn;
-        }
-      }
-      __syncthreads();  // Gb halves and the partial sums published
-      if (w == 0 && l < 4) {
-        static_assert(CB_WAVES == 4, "four partial slots per scalar");
-        p.part[((bh * p.N + i) * (D / 32) + blk) * 4 + l] = (psum[l] + psum[4 + l]) + (psum[8 + l] + psum[12 + l]);
-      }
-    }
-    // ---------------- segment 1: dE for this wave's tokens 32H .. 32H+31
-    auto segment1 = [&](auto rt_tag, auto h_tag) {
-      constexpr int RT = decltype(rt_tag)::value, H = decltype(h_tag)::value;
-      Op<2> Sop[NKB];
-#pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) Sop[kb] = read_op(xs_addr(2 * RT + kb / NKBH, kb % NKBH));
-      f32x4 dE[2] = {zero4(), zero4()};
-      {  // diag(w) K Gb^T
-        bf16x8 Kr[2][NKB];
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-          for (int kb = 0; kb < NKB; ++kb) Kr[u][kb] = rows(krow, 2 * H + u, kb);
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-          for (int u = 0; u < 2; ++u) dE[u] = mma<1, 2>(Op<1>{{Kr[u][kb]}}, Sop[kb], dE[u]);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      // + A^T dO over the token blocks kbs >= H (A[t][s] = 0 for t < s).  The
-      // A^T operand (m = s, k = t) is the D-layout of (Q K^T) tiles.
-#pragma unroll
-      for (int kbs = H; kbs < 2; ++kbs) {
-        const bf16x8 dO8 = dop(kbs);
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int st = 2 * H + u;
-          const float bs = gates[16 * st + lc];
-          f32x4 X[2];
-#pragma unroll
-          for (int hf = 0; hf < 2; ++hf) {
-            const int tt = 2 * kbs + hf;
-            X[hf] = zero4();
-            if (tt >= st) {
-#pragma unroll
-              for (int kb = 0; kb < NKB; ++kb) X[hf] = mfma(rows(qrow, tt, kb), rows(krow, st, kb), X[hf]);
-#pragma unroll
-              for (int jj = 0; jj < 4; ++jj)
-                X[hf][jj] = (tt > st || 4 * G + jj >= lc) ? X[hf][jj] * bs : 0.f;
-            }
-          }
-          dE[u] = mma<2, 1>(pack_tiles<2>(X[0], X[1]), Op<1>{{dO8}}, dE[u]);
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      const Op<2> nd = pack_tiles<2>(-dE[0], -dE[1]);
-      lds_st<bf16x8>(xe_addr(2 * RT + H), nd.v[0]);
-      lds_st<bf16x8>(xe_addr(2 * RT + H) + 1024, nd.v[1]);
-    };
-    switch (w) {
-      case 0: segment1(I0{}, I0{}); break;
-      case 1: segment1(I0{}, I1{}); break;
-      case 2: segment1(I1{}, I0{}); break;
-      default: segment1(I1{}, I1{}); break;
-    }
-    __syncthreads();  // -dE halves published
-    // ---------------- segment 2: Sb_i = a Sb_{i+1} + dO^T Q - dE^T K (column half h)
-    {
-      Op<2> ND[2];
-#pragma unroll
-      for (int hs = 0; hs < 2; ++hs) ND[hs] = read_op(xe_addr(2 * rt + hs));
-      f32x4 acc[NTH];
-#pragma unroll
-      for (int t = 0; t < NTH; ++t) acc[t] = a * Sb[t];
-#pragma unroll
-      for (int kbs = 0; kbs < 2; ++kbs) {
-        const bf16x8 dO8 = dop(kbs);
-#pragma unroll
-        for (int t = 0; t < NTH; ++t) {
-          const uint32_t ro = SQK + kbs * 32 * ROWB;
-          const bf16x8 qc = cat8(lds_tr16(qcol[t] + ro), lds_tr16(qcol[t] + ro + 16 * ROWB));
-          const bf16x8 kc = cat8(lds_tr16(kcol[t] + ro), lds_tr16(kcol[t] + ro + 16 * ROWB));
-          acc[t] = mfma(qc, dO8, acc[t]);
-          acc[t] = mma<1, 2>(Op<1>{{kc}}, ND[kbs], acc[t]);
-        }
-      }
-#pragma unroll
-      for (int t = 0; t < NTH; ++t) Sb[t] = acc[t];
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    if (i > 0) load_states(i - 1);
-    __builtin_amdgcn_sched_barrier(0);
-    if (ahead) {
-      if (w == 0)
-        wait_vmem_le<L::DMA_OPS + 1>();
-      else
-        wait_vmem_le<L::DMA_OPS>();
-    } else {
-      wait_vmem();
-    }
-    __syncthreads();  // next chunk's tiles landed, (delta) Sb_i halves published
-    if (j + 1 < p.N) chunk_scalars((STG + 1) % RING);
-  };
-
-  for (int j = 0; j < p.N; j += RING) {
-    chunk(std::integral_constant<int, 0>{}, j);
-    if (j + 1 < p.N) chunk(std::integral_constant<int, 1>{}, j + 1);
-    if (j + 2 < p.N) chunk(std::integral_constant<int, 2>{}, j + 2);
-  }
-}
 
 // ============================================================== chunk_bwd_tok
 // One wave per 16 state rows (phase I) and per 16 state columns (phase IIb):
@@ -731,9 +369,9 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
 #pragma unroll
         for (int c = 0; c < 4; ++c) sc[c] = p.part[c * BHN + si];
       } else {
-        const float* pp = p.part + (bh * p.N + i) * (int64_t)(D / 32) * 4;
+        const float* pp = p.part + (bh * p.N + i) * (int64_t)(D / 16) * 4;
 #pragma unroll
-        for (int r = 0; r < D / 32; ++r)
+        for (int r = 0; r < D / 16; ++r)
 #pragma unroll
           for (int c = 0; c < 4; ++c) sc[c] += pp[4 * r + c];
       }
@@ -855,14 +493,11 @@ static hipError_t launch_bwd(const ChunkArgs& a, hipStream_t stream) {
     if (e != hipSuccess) return e;
     return chunk_bwd_pair_launch(a, D, stream);
   } else {
-    constexpr int lds1 = StateBwdLds<D, 2>::BYTES;
     constexpr int lds2 = TokBwdLds<D>::BYTES;
     constexpr int thr2 = TokBwdLds<D>::NTHR;
-    auto k1 = chunk_bwd_state<D, RULE>;
-    hipError_t e = hipFuncSetAttribute((const void*)k1, hipFuncAttributeMaxDynamicSharedMemorySize, lds1);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k1, dim3((unsigned)(a.B * a.H * (D / 32))), dim3(CB_THREADS), lds1, stream, a);
-    e = hipGetLastError();
+    // adam: the reverse scan of the state and moment cotangents (Gb of every
+    // chunk, per-row-block partial sums), then the token gradients
+    hipError_t e = chunk_bwd_ascan_launch(a, D, stream);
     if (e != hipSuccess) return e;
     auto k2 = chunk_bwd_tok<D, RULE>;
     e = hipFuncSetAttribute((const void*)k2, hipFuncAttributeMaxDynamicSharedMemorySize, lds2);
