@@ -79,7 +79,11 @@ struct FwdRowsLds {
   static constexpr int EP0 = SP0 + 2 * 2 * SPW;
   // chunk scalars {a, b, m, n} per ring stage (delta: a only)
   static constexpr int SC0 = EP0 + 2 * 2 * EPW;
-  static constexpr int BYTES = SC0 + RING * 16;
+  // adam's training forward: M_i, V_i staged by the state waves for the
+  // output waves' stores, [chunk parity][state wave][M, V][column tile]
+  static constexpr int MV0 = SC0 + RING * 16;
+  static constexpr int MVW = 2 * (D / 16) * 1024;
+  static constexpr int BYTES = MV0 + (RULE == 2 ? 2 * 2 * MVW : 0);
   static_assert(BYTES <= 160 * 1024, "delta forward LDS exceeds the 160 KiB of a CU");
 };
 
@@ -228,14 +232,12 @@ __global__ void __launch_bounds__(FD_THREADS) chunk_fwd_rows(ChunkArgs p) {
       constexpr int STG = decltype(stg_tag)::value;
       constexpr uint32_t SQK = STG * L::TILE;
       if constexpr (RULE == 2) {
-        if (p.states) {  // adam: M_i, V_i (float32 planes) for the backward
-          const int64_t plane = p.B * p.H * (int64_t)N * D * D;
-          float* mp = p.states + plane + ((bh * N + i) * D + 32 * blk + 16 * w + lc) * (int64_t)D + 8 * G;
+        if (p.states) {  // adam: M_i, V_i for the backward, staged (the output waves store them)
+          const lds_ptr mv = L0 + (L::MV0 + ((i & 1) * 2 + w) * L::MVW + 16 * l);
 #pragma unroll
           for (int ct = 0; ct < NCT; ++ct) {
-            const int c = 32 * (ct >> 1) + 4 * (ct & 1);
-            *reinterpret_cast<f32x4*>(mp + c) = Mm[ct];
-            *reinterpret_cast<f32x4*>(mp + plane + c) = Vv[ct];
+            lds_st<f32x4>(mv + ct * 1024, Mm[ct]);
+            lds_st<f32x4>(mv + (NCT + ct) * 1024, Vv[ct]);
           }
         }
       }
@@ -375,6 +377,45 @@ __global__ void __launch_bounds__(FD_THREADS) chunk_fwd_rows(ChunkArgs p) {
   const int ow = (w & 1) | ((w >> 1) & 2);  // 2 -> 0, 3 -> 1, 6 -> 2, 7 -> 3
   bf16* og = p.o + bb * p.so[0] + hh * p.so[1] + 32 * blk + 4 * G;
   const lds_cptr spr = L0 + (L::SP0 + 16 * l);
+  // adam's M_i, V_i rows from the staging, as contiguous rows: output wave
+  // ow stores rows 8 (ow & 1) .. +7 of state wave ow >> 1's 16, D / 32
+  // instructions per moment; lane l of instruction k takes the 16-byte unit
+  // q = l % U of row 8 (ow & 1) + (64 k + l) / U (U = D / 4 units per row),
+  // which the state wave's tile 2 (q / 8) + q % 2 holds in lane r + 16 ((q / 2) % 4)
+  constexpr int UPR = D / 4, NMV = D / 32;
+  uint32_t mvo[NMV], mvg[NMV];
+#pragma unroll
+  for (int k = 0; k < NMV; ++k) {
+    const int f = 64 * k + l, r = 8 * (ow & 1) + f / UPR, q = f % UPR;
+    const int ct = 2 * (q >> 3) + (q & 1), gq = (q >> 1) & 3;
+    mvo[k] = (uint32_t)((ow >> 1) * L::MVW + ct * 1024 + 16 * (r + 16 * gq));
+    mvg[k] = (uint32_t)((16 * (ow >> 1) + r) * D + 4 * q);
+  }
+  // the checkpoint's rows: output wave ow stores units 64 (NCK ow + k) + l
+  // of the workgroup's 32 rows (row R = f / U, unit q = f % U: columns
+  // 4q .. 4q + 3), whose hi and lo halves state wave R / 16 published in the
+  // k-block q / 8 planes, lane R % 16 + 16 ((q / 2) % 4), half q % 2
+  constexpr int NCK = D / 32;
+  uint32_t cko[NCK], ckg[NCK];
+#pragma unroll
+  for (int k = 0; k < NCK; ++k) {
+    const int f = 64 * (NCK * ow + k) + l, R = f / UPR, q = f % UPR;
+    cko[k] = (uint32_t)((R >> 4) * L::SPW + (q >> 3) * 2 * 1024 + 16 * ((R & 15) + 16 * ((q >> 1) & 3)) + 8 * (q & 1));
+    ckg[k] = (uint32_t)(R * D + 4 * q);
+  }
+  auto store_mv = [&](int i) {
+    if (!p.states) return;
+    const int64_t plane = p.B * p.H * (int64_t)N * D * D;
+    float* mp = p.states + plane + ((bh * N + i) * D + 32 * blk) * (int64_t)D;
+    const uint32_t pb = L::MV0 + (i & 1) * 2 * L::MVW;
+#pragma unroll
+    for (int k = 0; k < NMV; ++k) {
+      const f32x4 m = lds_ld<f32x4>(L0 + (pb + mvo[k]));
+      const f32x4 v = lds_ld<f32x4>(L0 + (pb + mvo[k] + NCT * 1024));
+      *reinterpret_cast<f32x4*>(mp + mvg[k]) = m;
+      *reinterpret_cast<f32x4*>(mp + plane + mvg[k]) = v;
+    }
+  };
   const lds_cptr epr = L0 + (L::EP0 + 16 * l);
   __syncthreads();  // barrier 0
 
@@ -417,6 +458,7 @@ __global__ void __launch_bounds__(FD_THREADS) chunk_fwd_rows(ChunkArgs p) {
     auto out_chunk = [&](auto stg_tag, int i) {
       constexpr int STG = decltype(stg_tag)::value;
       constexpr uint32_t SQK = STG * L::TILE;
+      if (RULE == 2 && i >= 1) store_mv(i - 1);
       if (i >= 1) finish_prev(i);
       // A^T tiles (K Q^T, causal part) -> pair-order A operands of chunk i
       bf16x8 Qr[NKB];
@@ -461,21 +503,18 @@ __global__ void __launch_bounds__(FD_THREADS) chunk_fwd_rows(ChunkArgs p) {
         for (int u = 0; u < 2; ++u)
 #pragma unroll
           for (int rt = 0; rt < 2; ++rt) O[rt] = mfma(Sr[rt][kb].v[u], Qr[kb], O[rt]);
-      // checkpoint S_i from the pieces just read, negated back: this wave's
-      // row tile and half of the k-blocks.  The delta rule keeps the even
-      // chunks only (its backward rebuilds the odd ones); adam every chunk.
+      // checkpoint S_i from the published pieces, negated back, as
+      // contiguous rows (partial-line stores are slow).  The delta rule
+      // keeps the even chunks only (its backward rebuilds the odd ones);
+      // adam every chunk.
       if (p.states && (RULE == 2 || (i & 1) == 0)) {
-        constexpr int rt = OW & 1;
         const int64_t plane = RULE == 2 ? bh * N + i : bh * ((N + 1) / 2) + i / 2;
-        float* sp = p.states + (plane * D + 32 * blk + 16 * rt + lc) * (int64_t)D + 8 * G;
+        float* sp = p.states + (plane * D + 32 * blk) * (int64_t)D;
 #pragma unroll
-        for (int kh = 0; kh < NKB / 2; ++kh) {
-          const int kb = (OW >> 1) * (NKB / 2) + kh;
-          const Op<2> x = Sr[rt][kb];
-          *reinterpret_cast<bf16x8*>(sp + 32 * kb) =
-              neg8(__builtin_shufflevector(x.v[0], x.v[1], 0, 1, 2, 3, 8, 9, 10, 11));
-          *reinterpret_cast<bf16x8*>(sp + 32 * kb + 4) =
-              neg8(__builtin_shufflevector(x.v[0], x.v[1], 4, 5, 6, 7, 12, 13, 14, 15));
+        for (int k = 0; k < NCK; ++k) {
+          const lds_cptr src = L0 + (L::SP0 + sbo + cko[k]);
+          const bf16x4 hi = lds_ld<bf16x4>(src), lo = lds_ld<bf16x4>(src + 1024);
+          *reinterpret_cast<bf16x8*>(sp + ckg[k]) = neg8(cat8(hi, lo));
         }
       }
       __syncthreads();  // barrier i + 1
@@ -491,6 +530,7 @@ __global__ void __launch_bounds__(FD_THREADS) chunk_fwd_rows(ChunkArgs p) {
       if (i + 2 < N) out_chunk(std::integral_constant<int, 2>{}, i + 2);
     }
     finish_prev(N);
+    if (RULE == 2) store_mv(N - 1);
   };
   switch (ow) {
     case 0: run(std::integral_constant<int, 3>{}); break;
