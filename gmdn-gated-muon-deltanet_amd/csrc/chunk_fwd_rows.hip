@@ -226,13 +226,11 @@ __global__ void __launch_bounds__(FD_THREADS) chunk_fwd_rows(ChunkArgs p) {
     for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
       for (int u = 0; u < 2; ++u) lds_st<bf16x8>(spw + (kb * 2 + u) * 1024, Sp[kb].v[u]);
-    __syncthreads();  // barrier 0: chunk 0 landed, Sf_0 published
-
-    auto state_chunk = [&](auto stg_tag, int i) {
-      constexpr int STG = decltype(stg_tag)::value;
-      constexpr uint32_t SQK = STG * L::TILE;
+    // adam's training forward: M_i, V_i for the backward, staged for the
+    // output waves' stores at the end of chunk i - 1 (zeros for chunk 0)
+    auto stage_mv = [&](int i) {
       if constexpr (RULE == 2) {
-        if (p.states) {  // adam: M_i, V_i for the backward, staged (the output waves store them)
+        if (p.states) {
           const lds_ptr mv = L0 + (L::MV0 + ((i & 1) * 2 + w) * L::MVW + 16 * l);
 #pragma unroll
           for (int ct = 0; ct < NCT; ++ct) {
@@ -241,6 +239,13 @@ __global__ void __launch_bounds__(FD_THREADS) chunk_fwd_rows(ChunkArgs p) {
           }
         }
       }
+    };
+    stage_mv(0);
+    __syncthreads();  // barrier 0: chunk 0 landed, Sf_0 published
+
+    auto state_chunk = [&](auto stg_tag, int i) {
+      constexpr int STG = decltype(stg_tag)::value;
+      constexpr uint32_t SQK = STG * L::TILE;
       // E = V + K Sf^T, token tiles st (lane (r, G): tokens 16 st + 4G + j),
       // one token block (two tiles) at a time: the first block's -beta E is
       // split and published while the second block is in the MFMA pipe
@@ -361,6 +366,7 @@ __global__ void __launch_bounds__(FD_THREADS) chunk_fwd_rows(ChunkArgs p) {
           for (int u = 0; u < 2; ++u) lds_st<bf16x8>(spw + po + (kb * 2 + u) * 1024, Sp[kb].v[u]);
         }
       }
+      if (i + 1 < N) stage_mv(i + 1);  // M_{i+1}, V_{i+1}: chunk i + 1's
       __syncthreads();  // barrier i + 1
     };
     for (int i = 0; i < N; i += RING) {
@@ -458,7 +464,7 @@ __global__ void __launch_bounds__(FD_THREADS) chunk_fwd_rows(ChunkArgs p) {
     auto out_chunk = [&](auto stg_tag, int i) {
       constexpr int STG = decltype(stg_tag)::value;
       constexpr uint32_t SQK = STG * L::TILE;
-      if (RULE == 2 && i >= 1) store_mv(i - 1);
+      if (RULE == 2) store_mv(i);  // staged before barrier i
       if (i >= 1) finish_prev(i);
       // A^T tiles (K Q^T, causal part) -> pair-order A operands of chunk i
       bf16x8 Qr[NKB];
@@ -530,7 +536,6 @@ __global__ void __launch_bounds__(FD_THREADS) chunk_fwd_rows(ChunkArgs p) {
       if (i + 2 < N) out_chunk(std::integral_constant<int, 2>{}, i + 2);
     }
     finish_prev(N);
-    if (RULE == 2) store_mv(N - 1);
   };
   switch (ow) {
     case 0: run(std::integral_constant<int, 3>{}); break;
