@@ -25,16 +25,19 @@
 //    and Sb^T = a Sb^T + C + K^T (-dE).  It never waits on another wave's
 //    work of the same step.
 //  * Wave 1 forms, one step ahead, E of the next chunk (from the forward's S
-//    checkpoint) and publishes -E as G's operand, and the chunk scalars.
+//    checkpoint) and publishes -E as G's operand; after Y(j), the step's
+//    partial sums of da, db, dm, dn from what the state wave published.
 //  * Token waves 2, 3, 6, 7 (tile tw = 0, 1, 2, 3), one step ahead: before
 //    Y(j), the causal A tiles of key tile {0, 1, 3, 2}[tw] with P = A^T dO,
-//    and C = dO^T Q of column tile tw; after Y(j), G's column tile tw and
+//    C = dO^T Q of column tile tw, and (tw = 0) the chunk scalars; after
+//    Y(j), G's column tile tw and
 //    its elementwise factors (the forward's Mi, Vi recomputed); after X(j),
 //    Gb_i's store from the state wave's LDS staging.
-//  * Copy waves 4, 5 issue the LDS-DMA copies three steps ahead and wait
-//    for the next-but-one step's chunk.
-// LDS rings: K 4 stages (read until the step's own update), everything else
-// 3 stages (read only in the step before).
+//  * Copy waves 4, 5 issue the LDS-DMA copies (the chunk's tiles three
+//    steps ahead, the checkpoint's rows two) and wait for the next-but-one
+//    step's chunk.
+// LDS rings: K 4 stages (read until the step's own update), the checkpoint's
+// rows 2, everything else 3 (read only in the step before).
 #include "../../include/gmdn_scan.h"
 #include "chunk_b.h"
 
@@ -63,10 +66,11 @@ struct AScanLds {
   static constexpr int Q0 = K0 + RK * TILE;
   static constexpr int V0 = Q0 + RING * TILE;
   static constexpr int O0 = V0 + RING * CT;
+  // the checkpoint's rows: 2 stages, copied two steps ahead
   static constexpr int S0 = O0 + RING * CT;      // S_i pieces (rows)
-  static constexpr int M0 = S0 + RING * RT;      // M_i
-  static constexpr int W0 = M0 + RING * RT;      // V_i (the second moment)
-  static constexpr int G0 = W0 + RING * RT;
+  static constexpr int M0 = S0 + 2 * RT;         // M_i
+  static constexpr int W0 = M0 + 2 * RT;         // V_i (the second moment)
+  static constexpr int G0 = W0 + 2 * RT;
   // exchanges, 1 KiB per operand register set (lane l's 16 bytes at 16 l)
   static constexpr int EX0 = G0 + RING * GT;     // -E pieces [token block 2][hi, lo]
   static constexpr int NPRE = 7;                 // rden, qv, g2, upd, dMP, dVP, S
@@ -76,7 +80,10 @@ struct AScanLds {
   static constexpr int GB0 = C0 + 2 * 4 * 1024;      // Gb staging: hi plane, lo plane (16 rows)
   static constexpr int GBP = 16 * D * 2;
   static constexpr int SCL0 = GB0 + 2 * GBP;         // [parity] {a, b, m, n}
-  static constexpr int BYTES = SCL0 + 2 * 16;
+  // the state wave's Sb_{i+1}, Mtot, Vtot of the step [3][column tile 4],
+  // for wave 1's partial sums of da, db, dm, dn
+  static constexpr int XS0 = SCL0 + 2 * 16;
+  static constexpr int BYTES = XS0 + 3 * 4 * 1024;
   static_assert(BYTES <= 160 * 1024, "adam reverse scan LDS exceeds the 160 KiB of a CU");
 };
 
@@ -124,21 +131,25 @@ __global__ void __launch_bounds__(ASC_THREADS) chunk_bwd_ascan(ChunkArgs p) {
     dv.init(cw, p.sv[2]);
     dd.init(cw, p.so[2]);
     ds.init(cw, 2 * D);
-    auto issue_loads = [&](int j) {
+    auto issue_loads = [&](int j) {  // the tiles and gates of step j
       const int i = N - 1 - j, s3 = j % RING, s4 = j % L::RK;
       const int64_t t0 = (int64_t)i * CB_C;
-      const bf16* st = reinterpret_cast<const bf16*>(p.states + ((bh * N + i) * D + r0) * (int64_t)D);
       dk.issue(kg + t0 * p.sk[2], lds0 + L::K0 + s4 * L::TILE, cw);
       dq.issue(qg + t0 * p.sq[2], lds0 + L::Q0 + s3 * L::TILE, cw);
       dv.issue(vg + t0 * p.sv[2], lds0 + L::V0 + s3 * L::CT, cw);
       dd.issue(og + t0 * p.so[2], lds0 + L::O0 + s3 * L::CT, cw);
-      ds.issue(st, lds0 + L::S0 + s3 * L::RT, cw);
-      ds.issue(st + 2 * plane, lds0 + L::M0 + s3 * L::RT, cw);
-      ds.issue(st + 4 * plane, lds0 + L::W0 + s3 * L::RT, cw);
       if (cw == 0) lds_dma16(gsrc + t0, smem + L::G0 + s3 * L::GT);
     };
-    constexpr int ND = 2 * DQ::NOPS + 2 * DC::NOPS + 3 * DR::NOPS;
-    // the chunk of step j landed, with the copy of step j + 1 possibly in flight
+    auto issue_rows = [&](int j) {  // the checkpoint rows of step j
+      const int i = N - 1 - j, s2 = j & 1;
+      const bf16* st = reinterpret_cast<const bf16*>(p.states + ((bh * N + i) * D + r0) * (int64_t)D);
+      ds.issue(st, lds0 + L::S0 + s2 * L::RT, cw);
+      ds.issue(st + 2 * plane, lds0 + L::M0 + s2 * L::RT, cw);
+      ds.issue(st + 4 * plane, lds0 + L::W0 + s2 * L::RT, cw);
+    };
+    // operations of one issue_loads (wave 4: and the gates)
+    constexpr int ND = 2 * DQ::NOPS + 2 * DC::NOPS;
+    // everything issued before the last issue_loads landed
     auto wait_landed = [&](bool more) {
       if (!more)
         wait_vmem();
@@ -147,15 +158,24 @@ __global__ void __launch_bounds__(ASC_THREADS) chunk_bwd_ascan(ChunkArgs p) {
       else
         wait_vmem_le<ND>();
     };
-    for (int j = 0; j < 3 && j < N; ++j) issue_loads(j);
+    issue_loads(0);
+    issue_rows(0);
+    if (N > 1) {
+      issue_loads(1);
+      issue_rows(1);
+    }
+    if (N > 2) issue_loads(2);
     wait_landed(N > 2);  // steps 0 and 1
     __syncthreads();     // B0
     __syncthreads();     // B1
     __syncthreads();     // B2
+    // step j + 2's rows go into the stage step j's held: its last reader
+    // (the token waves' phase 2 of step j, in the step before) is done
     for (int j = 0; j < N; ++j) {
+      if (j + 2 < N) issue_rows(j + 2);
       if (j + 3 < N) issue_loads(j + 3);
-      if (j + 2 < N) wait_landed(j + 3 < N);
       __syncthreads();  // Y
+      if (j + 2 < N) wait_landed(j + 3 < N);
       __syncthreads();  // X
     }
     return;
@@ -242,8 +262,8 @@ __global__ void __launch_bounds__(ASC_THREADS) chunk_bwd_ascan(ChunkArgs p) {
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb) Gp[kb] = pack_tiles<2>(Gb[2 * kb], Gb[2 * kb + 1]);
       __builtin_amdgcn_sched_barrier(0);
-      // ---- X = K Gb^T (lane (r, G) of tile st: tokens 16 st + 4G + jj), with
-      // the partial sums' factors read and the sums formed meanwhile
+      // ---- X = K Gb^T (lane (r, G) of tile st: tokens 16 st + 4G + jj); Sb,
+      // Mtot, Vtot published for wave 1's partial sums meanwhile
       f32x4 X[4];
 #pragma unroll
       for (int st = 0; st < 4; ++st) X[st] = zero4();
@@ -253,20 +273,11 @@ __global__ void __launch_bounds__(ASC_THREADS) chunk_bwd_ascan(ChunkArgs p) {
         for (int u = 0; u < 2; ++u)
 #pragma unroll
           for (int st = 0; st < 4; ++st) X[st] = mfma(Kr[st][kb], Gp[kb].v[u], X[st]);
-      float da = 0.f, db = 0.f, dm = 0.f, dn = 0.f;
 #pragma unroll
       for (int ct = 0; ct < NCT; ++ct) {
-        const f32x4 upd = lds_ld<f32x4>(xl + (L::PRE0 + (3 * 4 + ct) * 1024));
-        const f32x4 dmp = lds_ld<f32x4>(xl + (L::PRE0 + (4 * 4 + ct) * 1024));
-        const f32x4 dvp = lds_ld<f32x4>(xl + (L::PRE0 + (5 * 4 + ct) * 1024));
-        const f32x4 sv = lds_ld<f32x4>(xl + (L::PRE0 + (6 * 4 + ct) * 1024));
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          da += S0[ct][jj] * sv[jj];
-          db += S0[ct][jj] * upd[jj];
-          dm += MT[ct][jj] * dmp[jj];
-          dn += VT[ct][jj] * dvp[jj];
-        }
+        lds_st<f32x4>(xl + (L::XS0 + (0 * 4 + ct) * 1024), S0[ct]);
+        lds_st<f32x4>(xl + (L::XS0 + (1 * 4 + ct) * 1024), MT[ct]);
+        lds_st<f32x4>(xl + (L::XS0 + (2 * 4 + ct) * 1024), VT[ct]);
       }
       bf16x8 Kc[2][NCT];
 #pragma unroll
@@ -276,16 +287,10 @@ __global__ void __launch_bounds__(ASC_THREADS) chunk_bwd_ascan(ChunkArgs p) {
 #pragma unroll
       for (int k = 0; k < 16; ++k) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
-        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
+        if (k < 12) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
       }
       __builtin_amdgcn_sched_barrier(0);
-      // the row block's partial sums of da, db, dm, dn
-      {
-        const f32x2 s0 = wave_sum2(da, db), s1 = wave_sum2(dm, dn);
-        if (l == 0)
-          *reinterpret_cast<f32x4*>(p.part + ((bh * N + i) * (D / 16) + blk) * 4) = f32x4{s0[0], s0[1], s1[0], s1[1]};
-      }
       __syncthreads();  // Y
       // ---- -dE = -(X + P), then Sb^T = a Sb^T + C + K^T (-dE)
       f32x4 Pt[4], Ct[NCT];
@@ -334,7 +339,7 @@ __global__ void __launch_bounds__(ASC_THREADS) chunk_bwd_ascan(ChunkArgs p) {
       Op<2> Sp[NKB];
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb)
-        Sp[kb] = join_pieces(lds_ld<bf16x8>(sp[kb][0] + s3 * L::RT), lds_ld<bf16x8>(sp[kb][1] + s3 * L::RT));
+        Sp[kb] = join_pieces(lds_ld<bf16x8>(sp[kb][0] + (t & 1) * L::RT), lds_ld<bf16x8>(sp[kb][1] + (t & 1) * L::RT));
       bf16x8 Kr[4][NKB];
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb)
@@ -358,21 +363,44 @@ __global__ void __launch_bounds__(ASC_THREADS) chunk_bwd_ascan(ChunkArgs p) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) lds_st<bf16x8>(xl + (L::EX0 + (kt * 2 + u) * 1024), ne.v[u]);
       }
-      // the chunk scalars a, b, m, n into slot t & 1
-      const lds_cptr gg = L0 + (L::G0 + s3 * L::GT + 4 * l);
-      const f32x2 s0 = wave_sum2(fmaxf(lds_ld<float>(gg + 256), LOG_FLOOR), lds_ld<float>(gg));
-      const f32x2 s1 = wave_sum2(fmaxf(lds_ld<float>(gg + 512), LOG_FLOOR), fmaxf(lds_ld<float>(gg + 768), LOG_FLOOR));
-      if (l == 0)
-        *reinterpret_cast<f32x4*>(smem + L::SCL0 + (t & 1) * 16) =
-            f32x4{expf(s0[0]), s0[1] * (1.f / CB_C), expf(s1[0]), expf(s1[1])};
     };
     __syncthreads();  // B0
     prep(0);
     __syncthreads();  // B1
     __syncthreads();  // B2
     for (int j = 0; j < N; ++j) {
+      // the partial sums' factors of step j (the token waves overwrite them
+      // after Y): Mi / den, Mp - G, Vp - G^2, S
+      f32x4 fu[4], fm[4], fv[4], fs[4];
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) {
+        fu[ct] = lds_ld<f32x4>(xl + (L::PRE0 + (3 * 4 + ct) * 1024));
+        fm[ct] = lds_ld<f32x4>(xl + (L::PRE0 + (4 * 4 + ct) * 1024));
+        fv[ct] = lds_ld<f32x4>(xl + (L::PRE0 + (5 * 4 + ct) * 1024));
+        fs[ct] = lds_ld<f32x4>(xl + (L::PRE0 + (6 * 4 + ct) * 1024));
+      }
       if (j + 1 < N) prep(j + 1);
       __syncthreads();  // Y
+      // da = <Sb, S>, db = <Sb, Mi / den>, dm = <Mtot, Mp - G>, dn = <Vtot, Vp - G^2>
+      // over the row block (the state wave published Sb, Mtot, Vtot before Y)
+      float da = 0.f, db = 0.f, dm = 0.f, dn = 0.f;
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) {
+        const f32x4 sb = lds_ld<f32x4>(xl + (L::XS0 + (0 * 4 + ct) * 1024));
+        const f32x4 mt = lds_ld<f32x4>(xl + (L::XS0 + (1 * 4 + ct) * 1024));
+        const f32x4 vt = lds_ld<f32x4>(xl + (L::XS0 + (2 * 4 + ct) * 1024));
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          da += sb[jj] * fs[ct][jj];
+          db += sb[jj] * fu[ct][jj];
+          dm += mt[jj] * fm[ct][jj];
+          dn += vt[jj] * fv[ct][jj];
+        }
+      }
+      const f32x2 s0 = wave_sum2(da, db), s1 = wave_sum2(dm, dn);
+      if (l == 0)
+        *reinterpret_cast<f32x4*>(p.part + ((bh * N + (N - 1 - j)) * (D / 16) + blk) * 4) =
+            f32x4{s0[0], s0[1], s1[0], s1[1]};
       __syncthreads();  // X
     }
     return;
@@ -442,6 +470,14 @@ __global__ void __launch_bounds__(ASC_THREADS) chunk_bwd_ascan(ChunkArgs p) {
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) Ct = mfma(col_op(colQ, s3 * L::TILE, kt), dO8[kt], Ct);
       lds_st<f32x4>(xl + (L::C0 + par * 4096 + tw * 1024), Ct);
+      if (tw == 0) {  // the chunk scalars a, b, m, n into slot t & 1
+        const lds_cptr gg = L0 + (L::G0 + s3 * L::GT + 4 * l);
+        const f32x2 s0 = wave_sum2(fmaxf(lds_ld<float>(gg + 256), LOG_FLOOR), lds_ld<float>(gg));
+        const f32x2 s1 = wave_sum2(fmaxf(lds_ld<float>(gg + 512), LOG_FLOOR), fmaxf(lds_ld<float>(gg + 768), LOG_FLOOR));
+        if (l == 0)
+          *reinterpret_cast<f32x4*>(smem + L::SCL0 + par * 16) =
+              f32x4{expf(s0[0]), s0[1] * (1.f / CB_C), expf(s1[0]), expf(s1[1])};
+      }
     };
     // phase 2 of step t: G's column tile tw and the elementwise factors
     auto phase2 = [&](int t) {
@@ -457,9 +493,10 @@ __global__ void __launch_bounds__(ASC_THREADS) chunk_bwd_ascan(ChunkArgs p) {
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) kc[kt] = col_op(colKt, SK, kt);
       const f32x4 sc = lds_ld<f32x4>(L0 + (L::SCL0 + par * 16));
-      const f32x4 Mp = lds_ld<f32x4>(L0 + (L::M0 + s3 * L::RT + rto));
-      const f32x4 Vp = lds_ld<f32x4>(L0 + (L::W0 + s3 * L::RT + rto));
-      const bf16x8 Spc = lds_ld<bf16x8>(L0 + (L::S0 + s3 * L::RT + rto));
+      const uint32_t s2 = (uint32_t)(t & 1) * L::RT;
+      const f32x4 Mp = lds_ld<f32x4>(L0 + (L::M0 + s2 + rto));
+      const f32x4 Vp = lds_ld<f32x4>(L0 + (L::W0 + s2 + rto));
+      const bf16x8 Spc = lds_ld<bf16x8>(L0 + (L::S0 + s2 + rto));
       __builtin_amdgcn_sched_barrier(0);
       f32x4 Gn = zero4();  // K^T (-E) = -G^T
 #pragma unroll
