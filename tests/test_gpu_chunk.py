@@ -218,6 +218,15 @@ def test_adam_grads_small(seed):
     assert all(e <= TOL for e, _ in errs.values()), errs
 
 
+@pytest.mark.parametrize("T", [64, 128, 192])
+def test_adam_grads_few_chunks(T):
+    """One, two and three chunks: the adam reverse scan copies its tiles
+    three steps ahead and the checkpoint rows two, so these counts take the
+    short prologues and the last steps without copies in flight."""
+    errs = _grads(Workload("t", "adam", 2, 2, T, 64), seed=3)
+    assert all(e <= TOL for e, _ in errs.values()), errs
+
+
 def _adam_grads_vs_f32(w, seed=0):
     """Adam's gradients against float64 autograd of the oracle, bounded by
     the float32 evaluation of the same reference algorithm: the HIP path may
