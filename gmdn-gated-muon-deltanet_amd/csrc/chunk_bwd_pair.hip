@@ -32,9 +32,11 @@ struct PairLds {
   static constexpr int DH0 = 6 * TILE, DL0 = 7 * TILE;    // dE
   static constexpr int AP = CB_C * CB_C * 2;
   static constexpr int AH0 = 8 * TILE, AL0 = AH0 + AP;    // A^T, then dA diag(beta) (rows s)
-  // floats: per-wave dbeta partials [NW][64], beta, g, per-wave da partials [NW]
+  // floats: per-wave dbeta partials [NW][64], two gate slots {beta, g}
+  // (chunk i0's stays published while chunk i1's is in use), per-wave da
+  // partials [NW]
   static constexpr int R0 = AL0 + AP;
-  static constexpr int BYTES = R0 + (NW * CB_C + 2 * CB_C + NW) * 4;
+  static constexpr int BYTES = R0 + (NW * CB_C + 4 * CB_C + NW) * 4;
   static_assert(BYTES <= 160 * 1024, "pair backward LDS exceeds the 160 KiB of a CU");
 };
 
@@ -48,6 +50,7 @@ struct PairCtx {
   const ChunkArgs* p;
   int64_t bh, bb, hh;
   int w, l, G, lc, r0;
+  int gs = 0;  // the gate slot in use
 
   GMDN_DEV const bf16* Qs() const { return reinterpret_cast<const bf16*>(smem + L::Q0); }
   GMDN_DEV const bf16* Ks() const { return reinterpret_cast<const bf16*>(smem + L::K0); }
@@ -62,9 +65,9 @@ struct PairCtx {
   // dbeta and da are summed per wave into the wave's own slots, then over
   // the waves in a fixed order: the gradients are bitwise reproducible
   GMDN_DEV float* pdbeta() const { return reinterpret_cast<float*>(smem + L::R0); }  // [NW][64]
-  GMDN_DEV float* rbeta() const { return pdbeta() + L::NW * CB_C; }
+  GMDN_DEV float* rbeta() const { return pdbeta() + L::NW * CB_C + gs * 2 * CB_C; }
   GMDN_DEV float* rg() const { return rbeta() + CB_C; }
-  GMDN_DEV float* pda() const { return rg() + CB_C; }  // [NW]
+  GMDN_DEV float* pda() const { return pdbeta() + L::NW * CB_C + 4 * CB_C; }  // [NW]
 
   // Chunk i's gate rows into wave 0's lanes (token l)
   GMDN_DEV void load_gates(int i, float& b, float& g) const {
@@ -86,7 +89,7 @@ struct PairCtx {
     pl.init(wv, sx[2]);
     pl.issue(x + bb * sx[0] + hh * sx[1] + (int64_t)i * CB_C * sx[2], lds_addr(smem) + dst, w);
   }
-  // The gate rows into LDS (the caller synchronises)
+  // The gate rows into LDS slot gs (the caller synchronises)
   GMDN_DEV void publish_gates(float b, float g) const {
     if (w == 0) {
       rbeta()[l] = b;
@@ -149,8 +152,8 @@ struct PairCtx {
   // dO tiles and the state rows may still be arriving: they are waited for
   // after phase I'), given its state rows S (pieces) and Gb (pieces).  With
   // want_sb, also Sb_i = a_i Gb + dO^T Q - dE^T K (pieces) into sb.  `next()`
-  // runs once the q, k and dO tiles are free (before the dq, dk stores); the
-  // V tile and the A planes stay in use until the return.
+  // runs once the q, k and dO tiles are free, after the dq, dk stores are
+  // issued; the V tile and the A planes stay in use until the return.
   template <class Next>
   GMDN_DEV void chunk_grads(int i, const bf16x8 (&srow)[NKB][2], const bf16x8 (&grow)[NKB][2], bool want_sb,
                             bf16x8 (&sb)[NKB][2], Next&& next) const {
@@ -400,12 +403,15 @@ struct PairCtx {
           to_bf16x4(acc);
     }
     __syncthreads();
-    next();
+    // the stores go out before next()'s copies and loads: vector-memory
+    // instructions leave a CU in issue order, so stores issued behind 100+
+    // KiB of loads wait for them
     for (int e = threadIdx.x; e < CB_C * D / 8; e += L::NTHR) {
       const int r = e / (D / 8), c8 = (e % (D / 8)) * 8;
       *reinterpret_cast<bf16x8*>(dqg + r * p->sq[2] + c8) = *reinterpret_cast<const bf16x8*>(dqs + LQ::off(r, c8));
       *reinterpret_cast<bf16x8*>(dkg + r * p->sk[2] + c8) = *reinterpret_cast<const bf16x8*>(dks + LQ::off(r, c8));
     }
+    next();
     __syncthreads();  // the staging tiles are read before the next chunk's copies land
   }
 
@@ -502,14 +508,15 @@ __global__ void __launch_bounds__(PairLds<D>::NTHR) chunk_bwd_pair(ChunkArgs p) 
       c.issue_tile(p.k, p.sk, i1, L::K0);
       c.issue_tile(p.v, p.sv, i1, L::V0);
       c.issue_tile(p.o, p.so, i1, L::O0);
+      c.load_gates(i1, b1, g1);
+      load_rows(p.gb + (c.bh * NO + pi) * (int64_t)D * D, gr);  // Gb_{i1}: odd plane pi
       c.state_step(reinterpret_cast<const bf16*>(smem + L::DH0), reinterpret_cast<const bf16*>(smem + L::DL0),
                    s0, sr);  // S_{i1}
     }
-    c.load_gates(i1, b1, g1);
-    load_rows(p.gb + (c.bh * NO + pi) * (int64_t)D * D, gr);  // Gb_{i1}: odd plane pi
     wait_vmem_le<2 * NKB>();  // chunk i1's tiles and gates landed; the Gb rows may be in flight
     held1(b1);
     held1(g1);
+    c.gs = 1;  // chunk i0's gates stay in slot 0
     c.publish_gates(b1, g1);
     __syncthreads();
     // chunk i1, and Gb_{i0} = Sb_{i1}; chunk i0's q, k, dO tiles and its S
@@ -524,6 +531,7 @@ __global__ void __launch_bounds__(PairLds<D>::NTHR) chunk_bwd_pair(ChunkArgs p) 
     // chunk i0's q, k (and dO) landed; in flight at most: the S rows, the
     // v tile and chunk i1's dq, dk stores
     wait_vmem_le<2 * NKB + 2>();
+    c.gs = 0;
   } else {
     const bf16x8 z8 = bf16x8{(bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f};
 #pragma unroll
@@ -539,8 +547,8 @@ __global__ void __launch_bounds__(PairLds<D>::NTHR) chunk_bwd_pair(ChunkArgs p) 
     held(sr);
     held1(b0);
     held1(g0);
+    c.publish_gates(b0, g0);
   }
-  c.publish_gates(b0, g0);
   __syncthreads();
   c.chunk_grads(i0, sr, gn, false, gr, [] {});
 }
