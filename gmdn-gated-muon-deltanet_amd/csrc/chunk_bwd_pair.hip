@@ -355,16 +355,18 @@ struct PairCtx {
         dka[st] = mma<1, 2>(Op<1>{{col8<LQ>(Qs_, 32 * kt, j0)}}, dAT, dka[st]);
       }
     }
-    // S and Gb by columns: the rows pass through the (now free) Q and K
-    // tiles one 32-row block at a time as split planes
-    bf16* Sh = reinterpret_cast<bf16*>(smem + L::Q0);
-    bf16* Sl = Sh + 32 * D;
-    bf16* Gh = reinterpret_cast<bf16*>(smem + L::K0);
-    bf16* Gl = Gh + 32 * D;
-    __syncthreads();  // Q and K tiles free
-#pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) {
+    // S and Gb by columns: the rows pass through free tiles one 32-row block
+    // at a time as split planes, double-buffered (the Q and K tiles; the V
+    // tile, free since phase I, and the A planes, free since dQ, dK's first
+    // products): block kb + 1 is written while block kb is read
+    bf16* const Sbuf[2] = {reinterpret_cast<bf16*>(smem + L::Q0), reinterpret_cast<bf16*>(smem + L::V0)};
+    bf16* const Gbuf[2] = {reinterpret_cast<bf16*>(smem + L::K0), Ah_};
+    auto put_rows = [&](int kb) {
       if ((w >> 1) == kb) {
+        bf16* Sh = Sbuf[kb & 1];
+        bf16* Sl = Sh + 32 * D;
+        bf16* Gh = Gbuf[kb & 1];
+        bf16* Gl = Gh + 32 * D;
         const int lr = 16 * (w & 1) + lc;
 #pragma unroll
         for (int kc = 0; kc < NKB; ++kc) {
@@ -375,7 +377,17 @@ struct PairCtx {
           *reinterpret_cast<bf16x8*>(Gl + so) = Ga[kc].v[1];
         }
       }
-      __syncthreads();
+    };
+    __syncthreads();  // Q and K tiles free
+    put_rows(0);
+    __syncthreads();
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      if (kb + 1 < NKB) put_rows(kb + 1);
+      const bf16* Sh = Sbuf[kb & 1];
+      const bf16* Sl = Sh + 32 * D;
+      const bf16* Gh = Gbuf[kb & 1];
+      const bf16* Gl = Gh + 32 * D;
       const Op<2> sc{{col8<LQ>(Sh, 0, j0), col8<LQ>(Sl, 0, j0)}};
       const Op<2> gc{{col8<LQ>(Gh, 0, j0), col8<LQ>(Gl, 0, j0)}};
 #pragma unroll
@@ -387,7 +399,7 @@ struct PairCtx {
         eg[st] = mma<2, 2>(gc, Er, eg[st]);
         des[st] = mma<2, 2>(sc, Dr, des[st]);
       }
-      if (kb + 1 < NKB) __syncthreads();
+      __syncthreads();  // block kb read, block kb + 1 written
     }
     bf16* dqs = reinterpret_cast<bf16*>(smem + L::V0);
     bf16* dks = Ah_;
