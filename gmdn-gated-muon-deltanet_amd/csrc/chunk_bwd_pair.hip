@@ -329,30 +329,43 @@ struct PairCtx {
       }
     }
 
-    // ---- dQ and dK for this wave's 16 state columns (operands swapped:
-    // lane <-> token, registers <-> 4 consecutive state columns)
-    const int j0 = 16 * w;
+    // ---- dQ and dK for this wave's two state-column tiles 2 cp, 2 cp + 1
+    // and two token tiles 2 th, 2 th + 1 (operands swapped: lane <-> token,
+    // registers <-> 4 consecutive state columns).  Per 32-row block a wave
+    // reads 18 KiB of operands, where one column tile by four token tiles
+    // would read 24 KiB for the same products.
+    constexpr int NCP = NW / 2;
+    const int cp = w % NCP, th = w / NCP;
+    const int jb = 32 * cp;
     bf16* dqg = p->dq + bb * p->sq[0] + hh * p->sq[1] + t0 * p->sq[2];
     bf16* dkg = p->dk + bb * p->sk[0] + hh * p->sk[1] + t0 * p->sk[2];
-    f32x4 dqa[4], dka[4], des[4], eg[4];
+    f32x4 dqa[2][2], dka[2][2], des[2][2], eg[2][2];  // [column tile][token tile]
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      dqa[tt] = zero4();
+    for (int ti = 0; ti < 2; ++ti) {
+      const int tt = 2 * th + ti;
+#pragma unroll
+      for (int ci = 0; ci < 2; ++ci) dqa[ci][ti] = zero4();
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         if (32 * ks > 16 * tt + 15) continue;
         const Op<2> dA{{col8<LA>(Ah_, 32 * ks, 16 * tt), col8<LA>(Al_, 32 * ks, 16 * tt)}};
-        dqa[tt] = mma<1, 2>(Op<1>{{col8<LQ>(Ks_, 32 * ks, j0)}}, dA, dqa[tt]);
+#pragma unroll
+        for (int ci = 0; ci < 2; ++ci)
+          dqa[ci][ti] = mma<1, 2>(Op<1>{{col8<LQ>(Ks_, 32 * ks, jb + 16 * ci)}}, dA, dqa[ci][ti]);
       }
     }
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      dka[st] = des[st] = eg[st] = zero4();
+    for (int si = 0; si < 2; ++si) {
+      const int st = 2 * th + si;
+#pragma unroll
+      for (int ci = 0; ci < 2; ++ci) dka[ci][si] = des[ci][si] = eg[ci][si] = zero4();
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) {
         if (32 * kt + 31 < 16 * st) continue;
         const Op<2> dAT{{row8<LA>(Ah_, 16 * st + lc, 32 * kt), row8<LA>(Al_, 16 * st + lc, 32 * kt)}};
-        dka[st] = mma<1, 2>(Op<1>{{col8<LQ>(Qs_, 32 * kt, j0)}}, dAT, dka[st]);
+#pragma unroll
+        for (int ci = 0; ci < 2; ++ci)
+          dka[ci][si] = mma<1, 2>(Op<1>{{col8<LQ>(Qs_, 32 * kt, jb + 16 * ci)}}, dAT, dka[ci][si]);
       }
     }
     // S and Gb by columns: the rows pass through free tiles one 32-row block
@@ -388,31 +401,44 @@ struct PairCtx {
       const bf16* Sl = Sh + 32 * D;
       const bf16* Gh = Gbuf[kb & 1];
       const bf16* Gl = Gh + 32 * D;
-      const Op<2> sc{{col8<LQ>(Sh, 0, j0), col8<LQ>(Sl, 0, j0)}};
-      const Op<2> gc{{col8<LQ>(Gh, 0, j0), col8<LQ>(Gl, 0, j0)}};
+      Op<2> sc[2], gc[2];
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) dqa[tt] = mma<2, 1>(sc, Op<1>{{row8<LQ>(Os_, 16 * tt + lc, 32 * kb)}}, dqa[tt]);
+      for (int ci = 0; ci < 2; ++ci) {
+        sc[ci] = Op<2>{{col8<LQ>(Sh, 0, jb + 16 * ci), col8<LQ>(Sl, 0, jb + 16 * ci)}};
+        gc[ci] = Op<2>{{col8<LQ>(Gh, 0, jb + 16 * ci), col8<LQ>(Gl, 0, jb + 16 * ci)}};
+      }
 #pragma unroll
-      for (int st = 0; st < 4; ++st) {
+      for (int ti = 0; ti < 2; ++ti) {
+        const Op<1> Or{{row8<LQ>(Os_, 16 * (2 * th + ti) + lc, 32 * kb)}};
+#pragma unroll
+        for (int ci = 0; ci < 2; ++ci) dqa[ci][ti] = mma<2, 1>(sc[ci], Or, dqa[ci][ti]);
+      }
+#pragma unroll
+      for (int si = 0; si < 2; ++si) {
+        const int st = 2 * th + si;
         const Op<2> Er{{row8<LQ>(Eh_, 16 * st + lc, 32 * kb), row8<LQ>(El_, 16 * st + lc, 32 * kb)}};
         const Op<2> Dr{{row8<LQ>(Dh_, 16 * st + lc, 32 * kb), row8<LQ>(Dl_, 16 * st + lc, 32 * kb)}};
-        eg[st] = mma<2, 2>(gc, Er, eg[st]);
-        des[st] = mma<2, 2>(sc, Dr, des[st]);
+#pragma unroll
+        for (int ci = 0; ci < 2; ++ci) {
+          eg[ci][si] = mma<2, 2>(gc[ci], Er, eg[ci][si]);
+          des[ci][si] = mma<2, 2>(sc[ci], Dr, des[ci][si]);
+        }
       }
       __syncthreads();  // block kb read, block kb + 1 written
     }
     bf16* dqs = reinterpret_cast<bf16*>(smem + L::V0);
     bf16* dks = Ah_;
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt)
-      *reinterpret_cast<bf16x4*>(dqs + LQ::off(16 * tt + lc, j0 + 4 * G)) =
-          to_bf16x4(dqa[tt]);
+    for (int ti = 0; ti < 2; ++ti) {
+      const int t = 16 * (2 * th + ti) + lc;
+      const float rb = rbeta_[t];
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      const f32x4 e = eg[st] * rbeta_[16 * st + lc];
-      const f32x4 acc = dka[st] - des[st] + e;
-      *reinterpret_cast<bf16x4*>(dks + LQ::off(16 * st + lc, j0 + 4 * G)) =
-          to_bf16x4(acc);
+      for (int ci = 0; ci < 2; ++ci) {
+        const int c = jb + 16 * ci + 4 * G;
+        *reinterpret_cast<bf16x4*>(dqs + LQ::off(t, c)) = to_bf16x4(dqa[ci][ti]);
+        const f32x4 acc = dka[ci][ti] - des[ci][ti] + eg[ci][ti] * rb;
+        *reinterpret_cast<bf16x4*>(dks + LQ::off(t, c)) = to_bf16x4(acc);
+      }
     }
     __syncthreads();
     // the stores go out before next()'s copies and loads: vector-memory
