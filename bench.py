@@ -11,6 +11,14 @@ resident in HBM before the timed region starts.
 
 prints one JSON line.  ``value`` is tokens/s (B*T per step) of the forward +
 backward step when the backward of the rule is built, else of the forward.
+For the delta and adam rules the training step (forward + backward) is
+captured into one HIP graph (its first replay checked bit for bit against an
+eager step) and ``value`` times K graph replays bracketed by
+synchronisations; the inference forward (one kernel) is timed over K eager
+launches.  ``step_us`` keeps both kinds of time (``train_step_eager``: K eager
+steps, whose host launch work is in the timed region;
+``fwd_inference_graph``) and the per-pass times (HIP events around the eager
+launches).
 ``roofline`` prices the dominant part of the step -- the backward pass (its
 two kernels) -- and ``roofline_fwd`` the inference forward kernel: average
 durations measured with HIP events on the launch stream inside the timed
@@ -548,6 +556,53 @@ def chunk_leg(w, steps: int, warmup: int, with_bwd: bool) -> dict:
         out["fwd_ms"] = (time.perf_counter() - t1) * 1e3 / steps
     out["fwd_kernel_ms"] = statistics.mean(e[0].elapsed_time(e[1]) for e in fwd_evs)
 
+    # The same step captured into one HIP graph and replayed: the launches
+    # cost no host time per step.  Delta and adam only (their capture is
+    # tested; the muon path is timed eagerly).  The capture's first replay
+    # must reproduce an eager step bit for bit.
+    if w.rule in ("delta", "adam"):
+        def graph_of(fn):
+            side = torch.cuda.Stream()
+            side.wait_stream(stream)
+            with torch.cuda.stream(side):
+                for _ in range(2):
+                    fn()
+            stream.wait_stream(side)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                outs = fn()
+            torch.cuda.synchronize()
+            ref = fn()
+            g.replay()
+            torch.cuda.synchronize()
+            for a, b in zip(outs, ref):
+                if not torch.equal(a, b):
+                    raise RuntimeError(f"{w.name}: the graph replay differs from the eager step")
+            return g
+
+        def replay_ms(g):
+            for _ in range(warmup):
+                g.replay()
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            for _ in range(steps):
+                g.replay()
+            torch.cuda.synchronize()
+            return (time.perf_counter() - t) * 1e3 / steps
+
+        def inference():
+            with torch.no_grad():
+                return (fwd(),)
+
+        out["graph_fwd_ms"] = replay_ms(graph_of(inference))
+        if with_bwd:
+            def train():
+                o = fwd()
+                return (o,) + tuple(torch.autograd.grad(o, grads_of, dO))
+
+            out["graph_ms_step"] = replay_ms(graph_of(train))
+
     units = w.B * w.H * w.T
     rid = {"delta": 0, "muon": 1, "adam": 2}[w.rule]
 
@@ -595,9 +650,14 @@ def config_leg(name: str, steps: int, warmup: int, cpu_budget: float | None, wit
            "fwd_tokens_per_s": w.tokens / (r["fwd_ms"] * 1e-3),
            "step_us": {"fwd_inference": r["fwd_kernel_ms"] * 1e3},
            "roofline_fwd": r["roofline_fwd"]}
+    if "graph_fwd_ms" in r:
+        leg["step_us"]["fwd_inference_graph"] = r["graph_fwd_ms"] * 1e3
     if with_bwd:
-        leg["fwd_bwd_tokens_per_s"] = w.tokens / (r["ms_step"] * 1e-3)
-        leg["step_us"].update(fwd_with_checkpoint=r["fwd_train_ms"] * 1e3, bwd=r["bwd_ms"] * 1e3)
+        leg["fwd_bwd_tokens_per_s"] = w.tokens / (r.get("graph_ms_step", r["ms_step"]) * 1e-3)
+        leg["step_us"].update(fwd_with_checkpoint=r["fwd_train_ms"] * 1e3, bwd=r["bwd_ms"] * 1e3,
+                              train_step_eager=r["ms_step"] * 1e3)
+        if "graph_ms_step" in r:
+            leg["step_us"]["train_step_graph"] = r["graph_ms_step"] * 1e3
         leg["roofline"] = r["roofline"]
     if cpu_budget:
         leg["cpu_baseline"] = cpu_baseline(w, cpu_budget, with_bwd, max_heads)
@@ -633,7 +693,12 @@ def main(argv=None):
     w = WORKLOADS[args.workload]
     with_bwd = chunk.backward_supported(w.rule, w.d) and not args.fwd_only
     r = chunk_leg(w, args.steps, args.warmup, with_bwd)
-    ms_step = r["ms_step"] if with_bwd else r["fwd_ms"]
+    # the graph-replayed training step where the rule's capture is built,
+    # else eager; the inference forward eager (one kernel: a graph replay
+    # adds more than the launch it saves)
+    ms_fwd = r["fwd_ms"]
+    ms_fb = r.get("graph_ms_step", r["ms_step"]) if with_bwd else None
+    ms_step = ms_fb if with_bwd else ms_fwd
     line = {
         "metric": METRIC,
         "value": w.tokens / (ms_step * 1e-3),
@@ -650,11 +715,17 @@ def main(argv=None):
         "config": {"workload": w.name, "rule": w.rule, "B": w.B, "H": w.H, "T": w.T, "d": w.d,
                    "chunk": w.chunk, "pass": "fwd+bwd" if with_bwd else "fwd",
                    "state": "fp32", "global_batch": w.B, "seq_len": w.T, "parallelism": "none"},
-        "fwd_tokens_per_s": w.tokens / (r["fwd_ms"] * 1e-3),
-        "fwd_bwd_tokens_per_s": w.tokens / (r["ms_step"] * 1e-3) if with_bwd else None,
+        "fwd_tokens_per_s": w.tokens / (ms_fwd * 1e-3),
+        "fwd_bwd_tokens_per_s": w.tokens / (ms_fb * 1e-3) if with_bwd else None,
+        "timing": ("fwd+bwd: HIP graph replays, fwd: eager launches" if with_bwd and "graph_ms_step" in r
+                   else "eager launches"),
         "step_us": {"fwd_with_checkpoint": r["fwd_train_ms"] * 1e3 if with_bwd else None,
                     "bwd": r["bwd_ms"] * 1e3 if with_bwd else None,
-                    "fwd_inference": r["fwd_kernel_ms"] * 1e3},
+                    "fwd_inference": r["fwd_kernel_ms"] * 1e3,
+                    "train_step_eager": r["ms_step"] * 1e3 if with_bwd else None,
+                    "train_step_graph": r["graph_ms_step"] * 1e3 if "graph_ms_step" in r else None,
+                    "fwd_inference_eager": r["fwd_ms"] * 1e3,
+                    "fwd_inference_graph": r["graph_fwd_ms"] * 1e3 if "graph_fwd_ms" in r else None},
         "roofline": r["roofline"] if with_bwd else r["roofline_fwd"],
         "roofline_fwd": r["roofline_fwd"],
     }
