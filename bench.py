@@ -563,7 +563,8 @@ def chunk_leg(w, steps: int, warmup: int, with_bwd: bool) -> dict:
     # The same step captured into one HIP graph and replayed: the launches
     # cost no host time per step.  Delta and adam only (their capture is
     # tested; the muon path is timed eagerly).  The capture's first replay
-    # must reproduce an eager step bit for bit.
+    # must reproduce an eager step bit for bit; if it does not, the line says
+    # so in ``graph_check`` and keeps the eager times.
     if w.rule in ("delta", "adam"):
         def graph_of(fn):
             side = torch.cuda.Stream()
@@ -580,12 +581,17 @@ def chunk_leg(w, steps: int, warmup: int, with_bwd: bool) -> dict:
             ref = fn()
             g.replay()
             torch.cuda.synchronize()
-            for a, b in zip(outs, ref):
-                if not torch.equal(a, b):
-                    raise RuntimeError(f"{w.name}: the graph replay differs from the eager step")
+            if not all(torch.equal(a, b) for a, b in zip(outs, ref)):
+                print(f"bench.py: {w.name}: a graph replay differs from the eager step; eager times kept",
+                      file=sys.stderr)
+                out["graph_check"] = "replay differs from the eager step"
+                return None
+            out.setdefault("graph_check", "replays equal the eager step bit for bit")
             return g
 
         def replay_ms(g):
+            if g is None:
+                return None
             for _ in range(warmup):
                 g.replay()
             torch.cuda.synchronize()
@@ -599,7 +605,9 @@ def chunk_leg(w, steps: int, warmup: int, with_bwd: bool) -> dict:
             with torch.no_grad():
                 return (fwd(),)
 
-        out["graph_fwd_ms"] = replay_ms(graph_of(inference))
+        gf = replay_ms(graph_of(inference))
+        if gf is not None:
+            out["graph_fwd_ms"] = gf
         if with_bwd:
             # fresh leaves: the eager steps above ran on another stream, and
             # leaves with that autograd history make the capture add
@@ -611,7 +619,9 @@ def chunk_leg(w, steps: int, warmup: int, with_bwd: bool) -> dict:
                 o = chunk.chunk_scan(*gxs, rule=w.rule, ns=w.ns)
                 return (o,) + tuple(torch.autograd.grad(o, gwrt, dO))
 
-            out["graph_ms_step"] = replay_ms(graph_of(train))
+            gs = replay_ms(graph_of(train))
+            if gs is not None:
+                out["graph_ms_step"] = gs
 
     units = w.B * w.H * w.T
     rid = {"delta": 0, "muon": 1, "adam": 2}[w.rule]
@@ -662,6 +672,8 @@ def config_leg(name: str, steps: int, warmup: int, cpu_budget: float | None, wit
            "roofline_fwd": r["roofline_fwd"]}
     if "graph_fwd_ms" in r:
         leg["step_us"]["fwd_inference_graph"] = r["graph_fwd_ms"] * 1e3
+    if "graph_check" in r:
+        leg["graph_check"] = r["graph_check"]
     if with_bwd:
         leg["fwd_bwd_tokens_per_s"] = w.tokens / (r.get("graph_ms_step", r["ms_step"]) * 1e-3)
         leg["step_us"].update(fwd_with_checkpoint=r["fwd_train_ms"] * 1e3, bwd=r["bwd_ms"] * 1e3,
@@ -729,6 +741,7 @@ def main(argv=None):
         "fwd_bwd_tokens_per_s": w.tokens / (ms_fb * 1e-3) if with_bwd else None,
         "timing": ("fwd+bwd: HIP graph replays, fwd: eager launches" if with_bwd and "graph_ms_step" in r
                    else "eager launches"),
+        "graph_check": r.get("graph_check"),
         "step_us": {"fwd_with_checkpoint": r["fwd_train_ms"] * 1e3 if with_bwd else None,
                     "bwd": r["bwd_ms"] * 1e3 if with_bwd else None,
                     "fwd_inference": r["fwd_kernel_ms"] * 1e3,
