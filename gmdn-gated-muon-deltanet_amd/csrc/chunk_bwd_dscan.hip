@@ -26,8 +26,8 @@
 //    C = dO^T Q of step j + 1 (two column tiles each).  Both are D-layout
 //    tiles in the state waves' register order.
 //  * Copy waves 4, 5 issue the LDS-DMA copies (step j + 2's chunk after
-//    X(j - 1)), wait for step j + 1's chunk before Y(j) and reduce its decay
-//    a into an LDS slot.
+//    X(j - 1)), wait for step j + 1's chunk before Y(j) and, between Y(j)
+//    and X(j), reduce its decay a into an LDS slot.
 #include "../../include/gmdn_scan.h"
 #include "chunk_b.h"
 
@@ -139,11 +139,12 @@ __global__ void __launch_bounds__(DSC_THREADS) chunk_bwd_dscan(ChunkArgs p) {
     for (int j = 0; j < N; ++j) {
       const bool dma = j + 2 < N;
       if (dma) issue_loads(N - 3 - j, (j + 2) % RING);
-      if (j + 1 < N) {
-        wait_next(dma);
-        decay((j + 1) % RING);
-      }
+      if (j + 1 < N) wait_next(dma);
       __syncthreads();  // Y
+      // step j + 1's decay is first read after X(j): reduced here, off the
+      // way to Y (the state waves wait at Y for the last wave to arrive, and
+      // this one shares a SIMD with state wave 0)
+      if (j + 1 < N) decay((j + 1) % RING);
       __syncthreads();  // X
     }
     return;
