@@ -69,12 +69,14 @@ struct PairCtx {
   GMDN_DEV float* rg() const { return rbeta() + CB_C; }
   GMDN_DEV float* pda() const { return pdbeta() + L::NW * CB_C + 4 * CB_C; }  // [NW]
 
-  // Chunk i's gate rows into wave 0's lanes (token l)
-  GMDN_DEV void load_gates(int i, float& b, float& g) const {
-    if (w == 0) {
-      const int64_t o = bh * p->T + (int64_t)i * CB_C + l;
-      b = p->beta[o];
-      g = p->g[o];
+  // Chunk i's gate rows {beta, g} into gate slot `slot` by one LDS-DMA
+  // operation of wave 0 (lanes 0-15 beta, 16-31 g; the caller waits and
+  // synchronises).  No register holds them, so the compiler places no wait
+  // of its own for them (such a wait drains every copy in flight).
+  GMDN_DEV void dma_gates(int i, int slot) const {
+    if (w == 0 && l < 32) {
+      const float* src = (G == 0 ? p->beta : p->g) + bh * p->T + (int64_t)i * CB_C + 4 * lc;
+      lds_dma16(src, smem + L::R0 + (L::NW * CB_C + slot * 2 * CB_C) * 4);
     }
   }
   // Asynchronous copy of one of chunk i's token tiles (rows of `x`, row
@@ -89,14 +91,6 @@ struct PairCtx {
     pl.init(wv, sx[2]);
     pl.issue(x + bb * sx[0] + hh * sx[1] + (int64_t)i * CB_C * sx[2], lds_addr(smem) + dst, w);
   }
-  // The gate rows into LDS slot gs (the caller synchronises)
-  GMDN_DEV void publish_gates(float b, float g) const {
-    if (w == 0) {
-      rbeta()[l] = b;
-      rg()[l] = g;
-    }
-  }
-
   // a = exp(sum over the chunk of max(g, log 1e-6)) (every lane)
   GMDN_DEV float chunk_decay() const { return expf(wave_sum(fmaxf(rg()[l], LOG_FLOOR))); }
 
@@ -482,7 +476,6 @@ struct PairCtx {
   }
 };
 
-GMDN_DEV void held1(float x) { asm volatile("" ::"v"(x)); }
 // Marks register pieces as used: the compiler completes their loads here.
 template <int NKB>
 GMDN_DEV void held(const bf16x8 (&x)[NKB][2]) {
@@ -522,9 +515,8 @@ __global__ void __launch_bounds__(PairLds<D>::NTHR) chunk_bwd_pair(ChunkArgs p) 
   };
   using L = PairLds<D>;
   const float* S0 = p.states + (c.bh * NP + pi) * (int64_t)D * D;  // S_{i0}: even checkpoint pi
-  float b0 = 0.f, g0 = 0.f, b1 = 0.f, g1 = 0.f;
   bf16x8 sr[NKB][2], gr[NKB][2], gn[NKB][2];
-  c.load_gates(i0, b0, g0);
+  c.dma_gates(i0, 0);
   if (i1 < p.N) {
     // Vector-memory operations complete in issue order.  Chunk i0's k, v go
     // to the dE planes (free until chunk i1's phase I) for the state step,
@@ -535,27 +527,21 @@ __global__ void __launch_bounds__(PairLds<D>::NTHR) chunk_bwd_pair(ChunkArgs p) 
       c.issue_tile(p.k, p.sk, i0, L::DH0);
       c.issue_tile(p.v, p.sv, i0, L::DL0);
       wait_vmem();
-      // the compiler's own waits for the S rows and gates go here, not after
-      // the copies below (it does not count them): they stay in flight
+      // the compiler's own wait for the S rows goes here, not after the
+      // copies below (it does not count them): they stay in flight
       held(s0);
-      held1(b0);
-      held1(g0);
-      c.publish_gates(b0, g0);
       __syncthreads();
       c.issue_tile(p.q, p.sq, i1, L::Q0);
       c.issue_tile(p.k, p.sk, i1, L::K0);
       c.issue_tile(p.v, p.sv, i1, L::V0);
       c.issue_tile(p.o, p.so, i1, L::O0);
-      c.load_gates(i1, b1, g1);
+      c.dma_gates(i1, 1);
       load_rows(p.gb + (c.bh * NO + pi) * (int64_t)D * D, gr);  // Gb_{i1}: odd plane pi
       c.state_step(reinterpret_cast<const bf16*>(smem + L::DH0), reinterpret_cast<const bf16*>(smem + L::DL0),
                    s0, sr);  // S_{i1}
     }
     wait_vmem_le<2 * NKB>();  // chunk i1's tiles and gates landed; the Gb rows may be in flight
-    held1(b1);
-    held1(g1);
     c.gs = 1;  // chunk i0's gates stay in slot 0
-    c.publish_gates(b1, g1);
     __syncthreads();
     // chunk i1, and Gb_{i0} = Sb_{i1}; chunk i0's q, k, dO tiles and its S
     // rows are fetched while chunk i1's dq, dk are stored
@@ -579,13 +565,10 @@ __global__ void __launch_bounds__(PairLds<D>::NTHR) chunk_bwd_pair(ChunkArgs p) 
     c.issue_tile(p.o, p.so, i0, L::O0);
     load_rows(S0, sr);
     c.issue_tile(p.v, p.sv, i0, L::V0);
-    // (a lone last chunk: no overlap sought) the compiler's waits for the
-    // gate and S registers are placed here, where they are already met
+    // (a lone last chunk: no overlap sought) the compiler's wait for the S
+    // registers is placed here, where it is already met
     wait_vmem();
     held(sr);
-    held1(b0);
-    held1(g0);
-    c.publish_gates(b0, g0);
   }
   __syncthreads();
   c.chunk_grads(i0, sr, gn, false, gr, [] {});
