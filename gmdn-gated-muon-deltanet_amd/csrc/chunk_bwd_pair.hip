@@ -145,12 +145,15 @@ struct PairCtx {
   // The gradients of chunk i, whose q, k tiles and gates are in LDS (the v,
   // dO tiles and the state rows may still be arriving: they are waited for
   // after phase I'), given its state rows S (pieces) and Gb (pieces).  With
-  // want_sb, also Sb_i = a_i Gb + dO^T Q - dE^T K (pieces) into sb.  `next()`
-  // runs once the q, k and dO tiles are free, after the dq, dk stores are
-  // issued; the V tile and the A planes stay in use until the return.
-  template <class Next>
+  // want_sb, also Sb_i = a_i Gb + dO^T Q - dE^T K (pieces) into sb.
+  // `rows_free()` runs once every wave has staged its S and Gb rows for
+  // phase IIb (srow and grow are not read after it), two blocks before
+  // the end of its products; `next()` runs once the
+  // q, k and dO tiles are free, after the dq, dk stores are issued; the V
+  // tile and the A planes stay in use until the return.
+  template <class RowsFree, class Next>
   GMDN_DEV void chunk_grads(int i, const bf16x8 (&srow)[NKB][2], const bf16x8 (&grow)[NKB][2], bool want_sb,
-                            bf16x8 (&sb)[NKB][2], Next&& next) const {
+                            bf16x8 (&sb)[NKB][2], RowsFree&& rows_free, Next&& next) const {
     const int64_t t0 = (int64_t)i * CB_C;
     const bf16* Qs_ = Qs();
     const bf16* Ks_ = Ks();
@@ -391,6 +394,7 @@ struct PairCtx {
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
       if (kb + 1 < NKB) put_rows(kb + 1);
+      if (kb + 2 == NKB) rows_free();  // every wave's rows staged
       const bf16* Sh = Sbuf[kb & 1];
       const bf16* Sl = Sh + 32 * D;
       const bf16* Gh = Gbuf[kb & 1];
@@ -543,18 +547,21 @@ __global__ void __launch_bounds__(PairLds<D>::NTHR) chunk_bwd_pair(ChunkArgs p) 
     wait_vmem_le<2 * NKB>();  // chunk i1's tiles and gates landed; the Gb rows may be in flight
     c.gs = 1;  // chunk i0's gates stay in slot 0
     __syncthreads();
-    // chunk i1, and Gb_{i0} = Sb_{i1}; chunk i0's q, k, dO tiles and its S
-    // rows are fetched while chunk i1's dq, dk are stored
-    c.chunk_grads(i1, sr, gr, true, gn, [&] {
-      c.issue_tile(p.q, p.sq, i0, L::Q0);
-      c.issue_tile(p.k, p.sk, i0, L::K0);
-      c.issue_tile(p.o, p.so, i0, L::O0);
-      load_rows(S0, sr);
-    });
+    // chunk i1, and Gb_{i0} = Sb_{i1}.  Chunk i0's S rows are requested once
+    // chunk i1's rows are staged for phase IIb (its last two blocks' products
+    // run meanwhile), chunk i0's q, k, dO tiles once chunk i1's dq, dk stores
+    // are issued.
+    c.chunk_grads(
+        i1, sr, gr, true, gn, [&] { load_rows(S0, sr); },
+        [&] {
+          c.issue_tile(p.q, p.sq, i0, L::Q0);
+          c.issue_tile(p.k, p.sk, i0, L::K0);
+          c.issue_tile(p.o, p.so, i0, L::O0);
+        });
     c.issue_tile(p.v, p.sv, i0, L::V0);
-    // chunk i0's q, k (and dO) landed; in flight at most: the S rows, the
-    // v tile and chunk i1's dq, dk stores
-    wait_vmem_le<2 * NKB + 2>();
+    // chunk i0's S rows and q, k, dO tiles landed (issued before them: the dq,
+    // dk stores); in flight at most: the v tile
+    wait_vmem_le<2>();
     c.gs = 0;
   } else {
     const bf16x8 z8 = bf16x8{(bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f};
@@ -571,7 +578,7 @@ __global__ void __launch_bounds__(PairLds<D>::NTHR) chunk_bwd_pair(ChunkArgs p) 
     held(sr);
   }
   __syncthreads();
-  c.chunk_grads(i0, sr, gn, false, gr, [] {});
+  c.chunk_grads(i0, sr, gn, false, gr, [] {}, [] {});
 }
 
 hipError_t chunk_bwd_pair_launch(const ChunkArgs& a, int d, hipStream_t s) {
