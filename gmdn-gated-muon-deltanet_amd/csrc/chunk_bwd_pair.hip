@@ -148,12 +148,14 @@ struct PairCtx {
   // want_sb, also Sb_i = a_i Gb + dO^T Q - dE^T K (pieces) into sb.
   // `rows_free()` runs once every wave has staged its S and Gb rows for
   // phase IIb (srow and grow are not read after it), two blocks before
-  // the end of its products; `next()` runs once the
-  // q, k and dO tiles are free, after the dq, dk stores are issued; the V
-  // tile and the A planes stay in use until the return.
-  template <class RowsFree, class Next>
+  // the end of its products; `qk_free()` once the q and k tiles (phase IIb's
+  // first staging buffer) are read for the last time, before the last
+  // block's products; `next()` once the dO tile is free, after the dq, dk
+  // stores are issued.  The V tile and the A planes stay in use until the
+  // return.
+  template <class RowsFree, class QkFree, class Next>
   GMDN_DEV void chunk_grads(int i, const bf16x8 (&srow)[NKB][2], const bf16x8 (&grow)[NKB][2], bool want_sb,
-                            bf16x8 (&sb)[NKB][2], RowsFree&& rows_free, Next&& next) const {
+                            bf16x8 (&sb)[NKB][2], RowsFree&& rows_free, QkFree&& qk_free, Next&& next) const {
     const int64_t t0 = (int64_t)i * CB_C;
     const bf16* Qs_ = Qs();
     const bf16* Ks_ = Ks();
@@ -393,6 +395,7 @@ struct PairCtx {
     __syncthreads();
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
+      if (kb + 1 == NKB) qk_free();  // block NKB - 2 (buffer 0) read by every wave
       if (kb + 1 < NKB) put_rows(kb + 1);
       if (kb + 2 == NKB) rows_free();  // every wave's rows staged
       const bf16* Sh = Sbuf[kb & 1];
@@ -549,17 +552,17 @@ __global__ void __launch_bounds__(PairLds<D>::NTHR) chunk_bwd_pair(ChunkArgs p) 
     __syncthreads();
     // chunk i1, and Gb_{i0} = Sb_{i1}.  Chunk i0's S rows are requested once
     // chunk i1's rows are staged for phase IIb (its last two blocks' products
-    // run meanwhile), chunk i0's q, k, dO tiles once chunk i1's dq, dk stores
-    // are issued.
+    // run meanwhile), its q, k tiles before the last block's products, its
+    // dO tile once chunk i1's dq, dk stores are issued.
     c.chunk_grads(
         i1, sr, gr, true, gn, [&] { load_rows(S0, sr); },
         [&] {
           c.issue_tile(p.q, p.sq, i0, L::Q0);
           c.issue_tile(p.k, p.sk, i0, L::K0);
-          c.issue_tile(p.o, p.so, i0, L::O0);
-        });
+        },
+        [&] { c.issue_tile(p.o, p.so, i0, L::O0); });
     c.issue_tile(p.v, p.sv, i0, L::V0);
-    // chunk i0's S rows and q, k, dO tiles landed (issued before them: the dq,
+    // chunk i0's S rows and q, k, dO tiles landed (issued among them: the dq,
     // dk stores); in flight at most: the v tile
     wait_vmem_le<2>();
     c.gs = 0;
@@ -578,7 +581,7 @@ __global__ void __launch_bounds__(PairLds<D>::NTHR) chunk_bwd_pair(ChunkArgs p) 
     held(sr);
   }
   __syncthreads();
-  c.chunk_grads(i0, sr, gn, false, gr, [] {}, [] {});
+  c.chunk_grads(i0, sr, gn, false, gr, [] {}, [] {}, [] {});
 }
 
 hipError_t chunk_bwd_pair_launch(const ChunkArgs& a, int d, hipStream_t s) {
