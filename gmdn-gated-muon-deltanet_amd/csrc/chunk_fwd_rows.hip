@@ -57,8 +57,10 @@ GMDN_DEV lds_cptr opaque_base(lds_cptr p) {
   return (lds_cptr)(uintptr_t)v;
 }
 
-constexpr int FD_WAVES = 8;
-constexpr int FD_THREADS = 64 * FD_WAVES;
+// waves per workgroup: adam splits each row block's state work over two
+// waves (see the state waves below), the delta rule keeps one
+template <int RULE>
+constexpr int fd_threads() { return 64 * (RULE == 2 ? 10 : 8); }
 
 template <int D, int RULE>
 struct FwdRowsLds {
@@ -88,7 +90,7 @@ struct FwdRowsLds {
 };
 
 template <int D, int RULE>
-__global__ void __launch_bounds__(FD_THREADS) chunk_fwd_rows(ChunkArgs p) {
+__global__ void __launch_bounds__(fd_threads<RULE>()) chunk_fwd_rows(ChunkArgs p) {
   // Q, K tiles: the row swizzle whose transposing reads of four rows by
   // four 16-byte groups (G's permuted K^T operand) hit 16 distinct groups
   using LQ = NSwz<D>;
@@ -110,9 +112,12 @@ __global__ void __launch_bounds__(FD_THREADS) chunk_fwd_rows(ChunkArgs p) {
   const lds_ptr L0 = lds_base(smem);
   const int N = p.N;
 
-  if (w == 4 || w == 5) {
+  // adam: state waves 0-3, output waves 4-7, copy waves 8, 9; delta: state
+  // waves 0, 1, output waves 2, 3, 6, 7, copy waves 4, 5
+  constexpr bool SPLIT = RULE == 2;
+  if (SPLIT ? w >= 8 : (w == 4 || w == 5)) {
     // ========================================================= copy waves
-    const int cw = w - 4;
+    const int cw = SPLIT ? w - 8 : w - 4;
     const uint32_t lds0 = lds_addr(smem);
     const bf16* qg = p.q + bb * p.sq[0] + hh * p.sq[1];
     const bf16* kg = p.k + bb * p.sk[0] + hh * p.sk[1];
@@ -172,10 +177,20 @@ __global__ void __launch_bounds__(FD_THREADS) chunk_fwd_rows(ChunkArgs p) {
     __syncthreads();  // barrier 0
     for (int i = 0; i < N; ++i) {
       const bool dma = i + 2 < N;
-      if (dma) issue_loads(i + 2, (i + 2) % RING);
-      if (i + 1 < N) {
-        wait_next(dma);
-        decay((i + 1) % RING);
+      if constexpr (SPLIT) {
+        // chunk i's scalars (its tiles landed in interval i - 1) are first
+        // read after the mid-chunk barrier; the copies go out after it, off
+        // the way to it
+        if (i >= 1) decay(i % RING);
+        __syncthreads();  // the mid-chunk barrier of chunk i
+        if (dma) issue_loads(i + 2, (i + 2) % RING);
+        if (i + 1 < N) wait_next(dma);
+      } else {
+        if (dma) issue_loads(i + 2, (i + 2) % RING);
+        if (i + 1 < N) {
+          wait_next(dma);
+          decay((i + 1) % RING);
+        }
       }
       __syncthreads();  // barrier i + 1
     }
@@ -195,7 +210,202 @@ __global__ void __launch_bounds__(FD_THREADS) chunk_fwd_rows(ChunkArgs p) {
   }
   auto row_op = [&](const lds_cptr (&base)[NKB], uint32_t off, int kb) { return lds_ld<bf16x8>(base[kb] + off); };
 
-  if (w < 2) {
+  if (SPLIT && w < 4) {
+    // ================================================ state waves (adam)
+    // Wave w: row block rb = w & 1 (rows 16 rb .. 16 rb + 15 of the
+    // workgroup's 32) and half h = w >> 1, which forms E for token block h
+    // (tokens 32 h .. 32 h + 31) and the update for the state columns of
+    // k-blocks h NKB/2 .. (h + 1) NKB/2 - 1.  E's other k-blocks come from the
+    // other half's published S pieces, the update's other token block from
+    // its published -beta E pieces: the regions the output waves read.
+    const int rb = w & 1;
+    // K^T operand of G's tile ct = 2 kb + u: lane (m, G) takes K[s][c] for
+    // the pair-order tokens s of block kt and column c = 32 kb + 4u + 8 (m / 4)
+    // + m % 4; in transposing reads lane (i, G) addresses row
+    // 32 kt + 16 h + 4G + i / 4, columns 32 kb + 4u + 8 (i % 4) ..
+    lds_cptr colp[NCT];
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct)
+      colp[ct] = opaque_base(
+          L0 + (L::K0 + swz_off<LQ>(4 * G + (lc >> 2), 32 * (ct >> 1) + 4 * (ct & 1) + 8 * (lc & 3))));
+    auto col_op = [&](uint32_t off, int ct, int kt) {
+      return cat8(lds_tr16(colp[ct] + off + 32 * kt * ROWB), lds_tr16(colp[ct] + off + (32 * kt + 16) * ROWB));
+    };
+    // V: tokens 16 st + 4G + j of the row block's column 16 rb + lc
+    const lds_cptr vp = L0 + swz_off<LV>(4 * G + (lc >> 2), 16 * rb + 4 * (lc & 3));
+    const lds_cptr bp = L0 + (L::G0 + 16 * G);  // beta[16 st + 4G ..]
+    const lds_ptr spw = L0 + (L::SP0 + rb * L::SPW + 16 * l);
+    const lds_ptr epw = L0 + (L::EP0 + rb * L::EPW + 16 * l);
+
+    auto halves = [&](auto h_tag) {
+      constexpr int H = decltype(h_tag)::value;
+      constexpr int NKH = NKB / 2, NCH = NCT / 2;  // k-blocks, column tiles of a half
+      constexpr int KB0 = H * NKH, KBO = (1 - H) * NKH, CT0 = H * NCH;
+      // -S, lane (r, G) of tile c: columns 32 ((CT0 + c) / 2) + 8G + 4 (c % 2) + j
+      f32x4 Sf[NCH];
+      Op<2> Sp[NKH];  // its pieces, k-blocks KB0 .., natural order
+      f32x4 Mm[NCH], Vv[NCH];  // adam's moments, same layout
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) Sf[c] = Mm[c] = Vv[c] = zero4();
+#pragma unroll
+      for (int k = 0; k < NKH; ++k) Sp[k] = pack_tiles<2>(Sf[2 * k], Sf[2 * k + 1]);
+#pragma unroll
+      for (int k = 0; k < NKH; ++k)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) lds_st<bf16x8>(spw + ((KB0 + k) * 2 + u) * 1024, Sp[k].v[u]);
+      // adam's training forward: M_i, V_i for the backward, staged for the
+      // output waves' stores at the end of chunk i - 1 (zeros for chunk 0)
+      auto stage_mv = [&](int i) {
+        if constexpr (RULE == 2) {
+          if (p.states) {
+            const lds_ptr mv = L0 + (L::MV0 + ((i & 1) * 2 + rb) * L::MVW + 16 * l);
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) {
+              lds_st<f32x4>(mv + (CT0 + c) * 1024, Mm[c]);
+              lds_st<f32x4>(mv + (NCT + CT0 + c) * 1024, Vv[c]);
+            }
+          }
+        }
+      };
+      stage_mv(0);
+      __syncthreads();  // barrier 0: chunk 0 landed, Sf_0 published
+
+      auto state_chunk = [&](auto stg_tag, int i) {
+        constexpr int STG = decltype(stg_tag)::value;
+        constexpr uint32_t SQK = STG * L::TILE;
+        // E = V + K Sf^T, token tiles 2H, 2H + 1 (lane (r, G): tokens
+        // 16 st + 4G + j): the own k-blocks from registers, the other half's
+        // from its pieces published at the end of the last chunk
+        const uint32_t so = (uint32_t)(i & 1) * (2 * L::SPW);
+        Op<2> Sq[NKH];
+#pragma unroll
+        for (int k = 0; k < NKH; ++k)
+#pragma unroll
+          for (int u = 0; u < 2; ++u) Sq[k].v[u] = lds_ld<bf16x8>(spw + so + ((KBO + k) * 2 + u) * 1024);
+        f32x4 E[2];
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          const bf16x4 vb = lds_tr16(vp + (L::V0 + STG * L::VT + (2 * H + s) * 16 * 64));
+          E[s] = f32x4{(float)vb[0], (float)vb[1], (float)vb[2], (float)vb[3]};
+        }
+        bf16x8 Kr[2][NKB];
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+          for (int kb = 0; kb < NKB; ++kb) Kr[s][kb] = row_op(rowK, SQK + (2 * H + s) * 16 * ROWB, kb);
+#pragma unroll
+        for (int k = 0; k < NKH; ++k)
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            E[0] = mfma(Kr[0][KB0 + k], Sp[k].v[u], E[0]);
+            E[1] = mfma(Kr[1][KB0 + k], Sp[k].v[u], E[1]);
+          }
+#pragma unroll
+        for (int k = 0; k < NKH; ++k)
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            E[0] = mfma(Kr[0][KBO + k], Sq[k].v[u], E[0]);
+            E[1] = mfma(Kr[1][KBO + k], Sq[k].v[u], E[1]);
+          }
+        // -beta E (delta), -E (adam) of token block H, published for the
+        // other half and the output waves
+        const uint32_t eo = (uint32_t)(i & 1) * (2 * L::EPW);
+        Op<2> WE[2];  // [token block]
+        if constexpr (RULE == 0) {
+          f32x4 bt[2];
+#pragma unroll
+          for (int s = 0; s < 2; ++s) bt[s] = lds_ld<f32x4>(bp + (STG * L::GT + (2 * H + s) * 64));
+          WE[H] = pack_tiles<2>(-(bt[0] * E[0]), -(bt[1] * E[1]));
+        } else {
+          WE[H] = pack_tiles<2>(-E[0], -E[1]);
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) lds_st<bf16x8>(epw + eo + (H * 2 + u) * 1024, WE[H].v[u]);
+        // the update's K^T operands, read while the barrier waits
+        bf16x8 Kc[2][NCH];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int c = 0; c < NCH; ++c) Kc[kt][c] = col_op(SQK, CT0 + c, kt);
+        __syncthreads();  // mid-chunk barrier: both token blocks' -beta E published
+#pragma unroll
+        for (int u = 0; u < 2; ++u) WE[1 - H].v[u] = lds_ld<bf16x8>(epw + eo + ((1 - H) * 2 + u) * 1024);
+        const uint32_t po = (uint32_t)((i + 1) & 1) * (2 * L::SPW);
+        if constexpr (RULE == 0) {
+          // Sf_{i+1} = a Sf_i + K^T (-beta E) for the half's column tiles
+          // (transposed tiles in the permuted column order above): the own
+          // token block for every tile, then the other block tile pair by
+          // tile pair, each pair split and published while the next is in
+          // the MFMA pipe
+          const float a = lds_ld<float>(L0 + (L::SC0 + STG * 16));
+#pragma unroll
+          for (int c = 0; c < NCH; ++c) Sf[c] = a * Sf[c];
+#pragma unroll
+          for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) Sf[c] = mfma(Kc[H][c], WE[H].v[u], Sf[c]);
+#pragma unroll
+          for (int k = 0; k < NKH; ++k) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+              Sf[2 * k] = mfma(Kc[1 - H][2 * k], WE[1 - H].v[u], Sf[2 * k]);
+              Sf[2 * k + 1] = mfma(Kc[1 - H][2 * k + 1], WE[1 - H].v[u], Sf[2 * k + 1]);
+            }
+            Sp[k] = pack_tiles<2>(Sf[2 * k], Sf[2 * k + 1]);
+#pragma unroll
+            for (int u = 0; u < 2; ++u) lds_st<bf16x8>(spw + po + ((KB0 + k) * 2 + u) * 1024, Sp[k].v[u]);
+          }
+        } else {
+          // adam: Gn = K^T (-E) = -G^T tiles, then per tile pair
+          //   M = m M + (1 - m) G,  V = n V + (1 - n) G^2,
+          //   Sf = a Sf - b M / (sqrt(V) + eps)
+          // split and published while the next pair is in the MFMA pipe
+          const f32x4 sc = lds_ld<f32x4>(L0 + (L::SC0 + STG * 16));
+          const float a = sc[0], b = sc[1], m = sc[2], n = sc[3];
+          f32x4 Gn[NCH];
+#pragma unroll
+          for (int c = 0; c < NCH; ++c) Gn[c] = zero4();
+#pragma unroll
+          for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) Gn[c] = mfma(Kc[H][c], WE[H].v[u], Gn[c]);
+          auto update = [&](int c) {
+            Mm[c] = m * Mm[c] - (1.f - m) * Gn[c];
+            Vv[c] = n * Vv[c] + (1.f - n) * (Gn[c] * Gn[c]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) Sf[c][j] = a * Sf[c][j] - b * Mm[c][j] * hw_rcp(hw_sqrt(Vv[c][j]) + p.eps);
+          };
+#pragma unroll
+          for (int k = 0; k < NKH; ++k) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+              Gn[2 * k] = mfma(Kc[1 - H][2 * k], WE[1 - H].v[u], Gn[2 * k]);
+              Gn[2 * k + 1] = mfma(Kc[1 - H][2 * k + 1], WE[1 - H].v[u], Gn[2 * k + 1]);
+            }
+            update(2 * k);
+            update(2 * k + 1);
+            Sp[k] = pack_tiles<2>(Sf[2 * k], Sf[2 * k + 1]);
+#pragma unroll
+            for (int u = 0; u < 2; ++u) lds_st<bf16x8>(spw + po + ((KB0 + k) * 2 + u) * 1024, Sp[k].v[u]);
+          }
+        }
+        if (i + 1 < N) stage_mv(i + 1);  // M_{i+1}, V_{i+1}: chunk i + 1's
+        __syncthreads();  // barrier i + 1
+      };
+      for (int i = 0; i < N; i += RING) {
+        state_chunk(std::integral_constant<int, 0>{}, i);
+        if (i + 1 < N) state_chunk(std::integral_constant<int, 1>{}, i + 1);
+        if (i + 2 < N) state_chunk(std::integral_constant<int, 2>{}, i + 2);
+      }
+    };
+    if (w >> 1)
+      halves(std::integral_constant<int, 1>{});
+    else
+      halves(std::integral_constant<int, 0>{});
+    return;
+  }
+
+  if (!SPLIT && w < 2) {
     // ======================================================== state waves
     // K^T operand of G's tile ct = 2 kb + u: lane (m, G) takes K[s][c] for
     // the pair-order tokens s of block kt and column c = 32 kb + 4u + 8 (m / 4)
@@ -380,7 +590,9 @@ __global__ void __launch_bounds__(FD_THREADS) chunk_fwd_rows(ChunkArgs p) {
   // ========================================================== output waves
   // token tile TT of waves 2, 3, 6, 7: 3, 2, 0, 1; the checkpoint share of
   // wave index ow (0..3): row tile ow & 1, k-blocks of half ow >> 1
-  const int ow = (w & 1) | ((w >> 1) & 2);  // 2 -> 0, 3 -> 1, 6 -> 2, 7 -> 3
+  // (adam: waves 4, 5, 6, 7 take token tiles 0, 1, 3, 2, the lighter tiles
+  // on the copy waves' SIMDs)
+  const int ow = SPLIT ? ((w - 4) ^ 2) : ((w & 1) | ((w >> 1) & 2));
   bf16* og = p.o + bb * p.so[0] + hh * p.so[1] + 32 * blk + 4 * G;
   const lds_cptr spr = L0 + (L::SP0 + 16 * l);
   // adam's M_i, V_i rows from the staging, as contiguous rows: output wave
@@ -466,6 +678,7 @@ __global__ void __launch_bounds__(FD_THREADS) chunk_fwd_rows(ChunkArgs p) {
       constexpr uint32_t SQK = STG * L::TILE;
       if (RULE == 2) store_mv(i);  // staged before barrier i
       if (i >= 1) finish_prev(i);
+      if constexpr (SPLIT) __syncthreads();  // the mid-chunk barrier of chunk i
       // A^T tiles (K Q^T, causal part) -> pair-order A operands of chunk i
       bf16x8 Qr[NKB];
 #pragma unroll
@@ -552,7 +765,7 @@ static hipError_t launch_fwd_rows(const ChunkArgs& a, hipStream_t stream) {
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   if (e != hipSuccess) return e;
   const int64_t grid = a.B * a.H * (D / 32);
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(FD_THREADS), lds, stream, a);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(fd_threads<RULE>()), lds, stream, a);
   return hipGetLastError();
 }
 
