@@ -41,6 +41,19 @@
 // issue chunk i + 2 and wait for chunk i + 1.  The published operands are
 // double-buffered by chunk parity and kept in register order (lane l's 16
 // bytes at 16 l): conflict-free 16-byte writes and reads, no index math.
+//
+// Adam (d = 64) splits each row block's state work over two waves, ten waves
+// in all: state waves 0-3 (row block w & 1, half h = w >> 1), output waves
+// 4-7 (token tiles 0, 1, 3, 2), copy waves 8, 9.  State wave h forms E for
+// token block h from its own S pieces (k-blocks of half h) and the other
+// half's published ones, publishes -E of that block, and after a mid-chunk
+// barrier forms G and the moment update for the state columns of half h
+// from both blocks' -E.  The exchanges go through the regions the output
+// waves read anyway.  The update's VALU work (two quarter-rate
+// transcendentals per value) is halved per wave, which pays for the second
+// barrier; the copy waves reduce chunk i's scalars before it and issue the
+// next copies after it.  The delta rule keeps one state wave per row block:
+// split the same way it measured slower, its output waves becoming the chain.
 #include "../../include/gmdn_scan.h"
 #include "chunk_b.h"
 
