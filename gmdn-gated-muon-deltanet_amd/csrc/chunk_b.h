@@ -116,5 +116,16 @@ hipError_t chunk_bwd_adam_mat_launch(const ChunkArgs& a, int d, float* ws, hipSt
 // delta rule: token gradients of chunk pairs (i0 = 2p from the forward's
 // checkpoint, i1 = 2p + 1 from the reverse scan's Gb)
 hipError_t chunk_bwd_pair_launch(const ChunkArgs& a, int d, hipStream_t s);
+// float32 token streams (every rule, d = 32, 64, 128): the matrix form with
+// exact float32 products around the drop-in scan in 'ieee'.  The token
+// pointers of ChunkArgs hold float32 data.  states = S [, M] [, V] planes of
+// every chunk, Kw, Uv planes, then a, b, m, n (floats below); the backward
+// workspace holds gS, dU, dK, the scalar gradients and the drop-in
+// backward's own workspace.
+size_t chunk_f32_states_floats(int64_t BH, int64_t N, int d, int rule);
+size_t chunk_f32_bwd_ws_floats(int64_t BH, int64_t N, int d, int rule, int ns);
+hipError_t chunk_fwd_f32_launch(const ChunkArgs& a, int d, int rule, int ns, float* states, hipStream_t s);
+hipError_t chunk_bwd_f32_launch(const ChunkArgs& a, int d, int rule, int ns, const float* states, float* ws,
+                                size_t ws_floats, hipStream_t s);
 
 }  // namespace gmdn

@@ -515,8 +515,10 @@ int check_desc(const gmdn_chunk_desc* d) {
   if (!d) return GMDN_ERR_ARG;
   if (d->B < 0 || d->H < 0 || d->T < 0) return GMDN_ERR_ARG;
   if (d->rule < 0 || d->rule > 2 || d->ns < 0 || d->ns > 8) return GMDN_ERR_ARG;
-  if (d->C != CB_C || (d->d != 64 && d->d != 128)) return GMDN_ERR_UNSUPPORTED;
-  if (d->dtype != GMDN_DTYPE_BF16) return GMDN_ERR_UNSUPPORTED;
+  if (d->dtype != GMDN_DTYPE_BF16 && d->dtype != GMDN_DTYPE_F32) return GMDN_ERR_UNSUPPORTED;
+  // bf16 streams: d = 64, 128; float32 streams (the matrix form): also 32
+  const bool d_ok = d->d == 64 || d->d == 128 || (d->dtype == GMDN_DTYPE_F32 && d->d == 32);
+  if (d->C != CB_C || !d_ok) return GMDN_ERR_UNSUPPORTED;
   if (d->T % CB_C != 0) return GMDN_ERR_ARG;
   if (d->B * d->H > ((int64_t)1 << 31) || d->T / CB_C > ((int64_t)1 << 30)) return GMDN_ERR_ARG;
   // DMA tiles need 16-byte aligned rows: token strides in multiples of 8 elements
@@ -568,6 +570,8 @@ size_t gmdn_chunk_states_bytes(const gmdn_chunk_desc* desc) {
   // muon: S_i and its momentum M_i, adam: S_i and the moments M_i, V_i, of
   // every chunk
   const int64_t N = desc->T / CB_C;
+  if (desc->dtype == GMDN_DTYPE_F32)
+    return chunk_f32_states_floats(desc->B * desc->H, N, desc->d, desc->rule) * sizeof(float);
   const size_t sq = (size_t)desc->d * desc->d * sizeof(float);
   if (desc->rule == 0) return (size_t)(desc->B * desc->H * ((N + 1) / 2)) * sq;
   // adam at d = 128 trains through the exact float32 scan: S, M, V, Kw, Uv
@@ -594,6 +598,15 @@ int gmdn_chunk_fwd(const gmdn_chunk_desc* desc, const void* q, const void* k, co
   if (!aligned16(o) || (desc->so[0] & 7) || (desc->so[1] & 7) || (desc->so[2] & 7)) return GMDN_ERR_UNSUPPORTED;
   const ChunkArgs a = make_args(desc, q, k, v, beta, g, gmu, gnu, o, states);
   hipStream_t s = (hipStream_t)stream;
+  if (desc->dtype == GMDN_DTYPE_F32) {
+    // float32 streams: the matrix form around the drop-in scan, whose chunk
+    // states the output kernel reads -- `states` is required for inference too
+    if (!states || !aligned16(states)) return GMDN_ERR_ARG;
+    if (desc->rule == 2 && desc->eps != 1e-6f) return GMDN_ERR_UNSUPPORTED;  // the drop-in adam's epsilon
+    return chunk_fwd_f32_launch(a, desc->d, desc->rule, desc->ns, static_cast<float*>(states), s) == hipSuccess
+               ? GMDN_OK
+               : GMDN_ERR_LAUNCH;
+  }
   if (desc->rule == 1) {
     // muon: the output kernel reads the chunk states from `states`, which is
     // therefore required for inference too
@@ -623,6 +636,7 @@ int gmdn_wy_fwd(const gmdn_chunk_desc* desc, const void* q, const void* k, const
                 const float* g, void* o, void* workspace, size_t workspace_bytes, void* stream) {
   int rc = check_desc(desc);
   if (rc != GMDN_OK) return rc;
+  if (desc->dtype != GMDN_DTYPE_BF16) return GMDN_ERR_UNSUPPORTED;  // bf16 token streams only
   if (desc->B * desc->H * desc->T == 0) return GMDN_OK;
   if (!q || !k || !v || !beta || !g || !o) return GMDN_ERR_ARG;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return GMDN_ERR_UNSUPPORTED;
@@ -637,6 +651,9 @@ int gmdn_wy_fwd(const gmdn_chunk_desc* desc, const void* q, const void* k, const
 
 size_t gmdn_chunk_bwd_workspace_bytes(const gmdn_chunk_desc* desc) {
   if (check_desc(desc) != GMDN_OK) return 0;
+  if (desc->dtype == GMDN_DTYPE_F32)
+    return chunk_f32_bwd_ws_floats(desc->B * desc->H, desc->T / CB_C, desc->d, desc->rule, desc->ns) *
+           sizeof(float);
   // muon: Kw, Uv, gS and dU per chunk, the chunk scalars and their
   // gradients, and the drop-in muon backward's workspace
   if (desc->rule == 1)
@@ -666,7 +683,8 @@ int gmdn_chunk_bwd(const gmdn_chunk_desc* desc, const void* q, const void* k, co
     return GMDN_ERR_ARG;
   // adam at d = 128 runs its scan in exact float32 (the split-bf16 state
   // products exceed the gradient tolerance there): the reference's epsilon
-  if (desc->rule == 2 && desc->d == 128 && desc->eps != 1e-6f) return GMDN_ERR_UNSUPPORTED;
+  if (desc->rule == 2 && (desc->d == 128 || desc->dtype == GMDN_DTYPE_F32) && desc->eps != 1e-6f)
+    return GMDN_ERR_UNSUPPORTED;
   if (desc->B * desc->H * (desc->T / CB_C) >= ((int64_t)1 << 31)) return GMDN_ERR_ARG;  // one workgroup per chunk
   if (!workspace || workspace_bytes < gmdn_chunk_bwd_workspace_bytes(desc)) return GMDN_ERR_WORKSPACE;
   // dO tiles arrive by 16-byte LDS-DMA loads and dq, dk, dv leave in 16-byte
@@ -687,6 +705,11 @@ int gmdn_chunk_bwd(const gmdn_chunk_desc* desc, const void* q, const void* k, co
   a.dg = dg;
   a.dgmu = dgmu;
   a.dgnu = dgnu;
+  if (desc->dtype == GMDN_DTYPE_F32)
+    return chunk_bwd_f32_launch(a, desc->d, desc->rule, desc->ns, static_cast<const float*>(states),
+                                (float*)workspace, workspace_bytes / sizeof(float), (hipStream_t)stream) == hipSuccess
+               ? GMDN_OK
+               : GMDN_ERR_LAUNCH;
   if (desc->rule == 2 && desc->d == 128)
     return chunk_bwd_adam_mat_launch(a, desc->d, (float*)workspace, (hipStream_t)stream) == hipSuccess
                ? GMDN_OK

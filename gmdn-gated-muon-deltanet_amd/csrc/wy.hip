@@ -39,8 +39,8 @@ struct WyLds {
   static constexpr int K0 = 0, V0 = TILE, Q0 = 2 * TILE;   // Q's slot later holds P
   static constexpr int T0 = 3 * TILE, A0 = T0 + CC;          // A's slot later holds M, then M T
   static constexpr int X0 = A0 + CC;                         // 3 waves x 16 x 16 scratch
-  static constexpr int S0 = X0 + 3 * 256;                    // beta, gamma, beta gamma, gamma_C / gamma
-  static constexpr int FLOATS = S0 + 4 * CB_C;
+  static constexpr int S0 = X0 + 3 * 256;  // beta, gamma, beta gamma, gamma_C / gamma, log gamma
+  static constexpr int FLOATS = S0 + 5 * CB_C;
   static_assert(FLOATS * 4 <= 160 * 1024, "WY prep LDS exceeds the 160 KiB of a CU");
 };
 
@@ -77,6 +77,7 @@ wy_prep(ChunkArgs p, float* __restrict__ UA, float* __restrict__ KA, float* __re
   float* gam = bet + C;
   float* bg = gam + C;
   float* kd = bg + C;
+  float* lgam = kd + C;  // prefix sums of the clamped log-gates
 
   const int64_t bh = blockIdx.x / p.N;
   const int i = (int)(blockIdx.x % p.N);
@@ -116,11 +117,14 @@ wy_prep(ChunkArgs p, float* __restrict__ UA, float* __restrict__ KA, float* __re
     gam[l] = g_;
     bg[l] = bt * g_;
     kd[l] = expf(gC - gc);
+    lgam[l] = gc;
     if (l == 63) aout[bh * p.N + i] = g_;
   }
   __syncthreads();
 
-  // ---- A = strict_lower(diag(beta) (K K^T * Gamma)): causal tiles by wave
+  // ---- A = strict_lower(diag(beta) (K K^T * Gamma)): causal tiles by wave.
+  // Gamma[t, s] = exp(log gamma_t - log gamma_s) on the causal entries only:
+  // the ratio gamma_t / gamma_s of two underflowed products would be 0 / 0.
   const float* gm = gam;
   for (int tile = w; tile < 16; tile += 4) {
     const int tt = tile >> 2, st = tile & 3;
@@ -132,7 +136,7 @@ wy_prep(ChunkArgs p, float* __restrict__ UA, float* __restrict__ KA, float* __re
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int t = 16 * tt + 4 * G + j;
-        acc[j] = s < t ? bet[t] * acc[j] * (gm[t] / gm[s]) : 0.f;
+        acc[j] = s < t ? bet[t] * acc[j] * expf(lgam[t] - lgam[s]) : 0.f;
       }
     }
     st_tile(As, LDC, 16 * tt, 16 * st, acc);
@@ -199,7 +203,7 @@ wy_prep(ChunkArgs p, float* __restrict__ UA, float* __restrict__ KA, float* __re
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int t = 16 * tt + 4 * G + j;
-        acc[j] = s <= t ? acc[j] * (gm[t] / gm[s]) : 0.f;
+        acc[j] = s <= t ? acc[j] * expf(lgam[t] - lgam[s]) : 0.f;
       }
     }
     st_tile(As, LDC, 16 * tt, 16 * st, acc);

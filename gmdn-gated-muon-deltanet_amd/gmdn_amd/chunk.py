@@ -6,8 +6,14 @@ computes what ``FastWeightMixer.forward`` computes between its front-end and
 its per-head RMSNorm (reference train_ablation.py:142-187): the chunk
 transform A, Kw, Uv, Qt, Ov, the state scan, and ``o = Qt S^T + Ov``.
 
-* ``q, k, v``: (B, H, T, d) bfloat16, d contiguous (any strides over B, H, T
-  that are multiples of 8 elements), q and k L2-normalised per head.
+* ``q, k, v``: (B, H, T, d) bfloat16 or float32 (one dtype for all three),
+  d contiguous (any strides over B, H, T that are multiples of 8 elements),
+  q and k L2-normalised per head.  Head dims: 64 and 128 in bfloat16 (16
+  and 32 are zero-padded to 64), 32, 64 and 128 in float32 (16 is padded to
+  32).  Zero columns of q, k, v leave every rule's result unchanged in the
+  other columns: the padded rows and columns of S, M and V stay zero
+  (msign of a block-diagonal matrix with a zero block keeps the block zero
+  and has the same Frobenius norm; adam's update is 0 / (0 + eps) there).
 * ``beta``: (B, H, T) beta gate (sigmoid output).
 * ``g, gmu, gnu``: (B, H, T) log alpha, log mu, log nu gates.  The reference
   clamps each gate at 1e-6 before its log (train_ablation.py:155, :170-175);
@@ -16,6 +22,13 @@ transform A, Kw, Uv, Qt, Ov, the state scan, and ``o = Qt S^T + Ov``.
 * returns ``o`` (B, H, T, d) in q's dtype.
 
 Chunk length is 64 (the reference default and every configuration's).
+
+Float32 streams (the reference's precision when autocast is off, its CPU
+path, train_ablation.py:424, 465) run the reference's matrix form with exact
+float32 products: chunk-parallel HIP kernels form Kw, Uv and the chunk
+scalars, the drop-in scan's kernels run every rule in 'ieee', and
+chunk-parallel kernels form o and, backward, dL/dS_i and the token and gate
+gradients.
 
 Delta and adam run as one fused HIP kernel per direction (forward: the
 chunk transform, the scan and the output; backward: a reverse scan of the
@@ -41,7 +54,9 @@ from . import ops  # noqa: F401  -- registers torch.ops.gmdn.*
 RULES = {"delta": 0, "muon": 1, "adam": 2}
 CHUNK = 64
 LOG_FLOOR = math.log(1e-6)
-SUPPORTED_D = (64, 128)
+SUPPORTED_D = (64, 128)          # bfloat16 head dims with kernels
+SUPPORTED_D_F32 = (32, 64, 128)  # float32 head dims with kernels
+PADDED_D = {torch.bfloat16: {16: 64, 32: 64}, torch.float32: {16: 32}}
 
 
 BWD_RULES = (0, 1, 2)  # rules with a backward
@@ -55,11 +70,12 @@ def backward_supported(rule, d: int = 128) -> bool:
     return _rule_id(rule) in BWD_RULES
 
 
-def fused_backward(rule, d: int) -> bool:
+def fused_backward(rule, d: int, dtype=torch.bfloat16) -> bool:
     """Whether ``rule`` at head dim ``d`` trains through the fused op
-    ``gmdn::chunk_fwd`` and its HIP backward: every rule and head dim."""
+    ``gmdn::chunk_fwd`` and its HIP backward: every rule and head dim the
+    kernels are built for (padded head dims go through a padded call)."""
     _rule_id(rule)
-    return d in SUPPORTED_D
+    return d in (SUPPORTED_D_F32 if dtype == torch.float32 else SUPPORTED_D)
 
 
 def _rule_id(rule) -> int:
@@ -79,12 +95,15 @@ def _check(q, k, v, beta, g, gmu, gnu, rule):
         raise RuntimeError(f"q, k, v must be (B, H, T, d) of equal shape, got {tuple(q.shape)}, "
                            f"{tuple(k.shape)}, {tuple(v.shape)}")
     B, H, T, d = q.shape
-    if d not in SUPPORTED_D:
-        raise RuntimeError(f"chunk_scan supports head dims {SUPPORTED_D}, got {d}")
+    if q.dtype not in (torch.bfloat16, torch.float32) or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise RuntimeError(f"chunk_scan takes bfloat16 or float32 q, k, v of one dtype, got "
+                           f"{q.dtype}, {k.dtype}, {v.dtype}")
+    built = SUPPORTED_D_F32 if q.dtype == torch.float32 else SUPPORTED_D
+    if d not in built and d not in PADDED_D[q.dtype]:
+        raise RuntimeError(f"chunk_scan supports head dims {tuple(sorted(built + tuple(PADDED_D[q.dtype])))} "
+                           f"for {q.dtype}, got {d}")
     if T % CHUNK:
         raise RuntimeError(f"T must be a multiple of the chunk length {CHUNK}, got {T}")
-    if any(t.dtype != torch.bfloat16 for t in (q, k, v)):
-        raise RuntimeError("chunk_scan takes bfloat16 q, k, v")
     for name, t in (("beta", beta), ("g", g), ("gmu", gmu), ("gnu", gnu)):
         if t is not None and tuple(t.shape) != (B, H, T):
             raise RuntimeError(f"{name} must be (B, H, T) = {(B, H, T)}, got {tuple(t.shape)}")
@@ -102,9 +121,14 @@ def chunk_scan(q, k, v, beta, g, gmu=None, gnu=None, *, rule="delta", ns: int = 
     _check(q, k, v, beta, g, gmu, gnu, r)
     # the state checkpoint is written only when a backward can follow
     record = torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (q, k, v, beta, g, gmu, gnu))
-    if record and r == 2 and q.shape[-1] == 128 and eps != 1e-6:
-        raise RuntimeError("adam at d = 128 trains through the drop-in scan, whose epsilon is 1e-6 "
-                           f"(fast_scan.py:94); got eps={eps}")
+    d = q.shape[-1]
+    dp = PADDED_D[q.dtype].get(d, d)
+    f32 = q.dtype == torch.float32
+    if r == 2 and eps != 1e-6 and (f32 or (record and dp == 128)):
+        raise RuntimeError("adam runs through the drop-in scan here (float32 streams; bfloat16 training at "
+                           f"d = 128), whose epsilon is 1e-6 (fast_scan.py:94); got eps={eps}")
     gates = [None if t is None else t.to(torch.float32) for t in (beta, g, gmu, gnu)]
+    if dp != d:
+        q, k, v = (torch.nn.functional.pad(t, (0, dp - d)) for t in (q, k, v))
     o, _ = torch.ops.gmdn.chunk_fwd(q, k, v, *gates, r, ns, eps, record)
-    return o
+    return o if dp == d else o[..., :d]

@@ -80,7 +80,9 @@ class FastWeightMixer(nn.Module):
         if T % self.chunk:
             raise ValueError("seq_len must be a multiple of chunk size")
         q, k, v, beta, log_alpha, log_mu, log_nu = self.front_end(x)
-        dt = torch.bfloat16
+        # float32 activations (autocast off: the reference's precision there,
+        # train_ablation.py:424, 465) stay float32; others run in bfloat16
+        dt = torch.float32 if q.dtype == torch.float32 else torch.bfloat16
         o = chunk_scan(q.to(dt), k.to(dt), v.to(dt), beta, log_alpha, log_mu, log_nu, rule=self.inner,
                        ns=self.ns_steps)
         # per-head RMSNorm (HIP) on o's (B, T, H, dh) storage: the output is

@@ -132,7 +132,8 @@ def chunk_desc(q: Tensor, k: Tensor, v: Tensor, o: Tensor, rule: int, ns: int, e
     B, H, T, d = q.shape
     desc = nat.ChunkDesc()
     desc.B, desc.H, desc.T, desc.d, desc.C = B, H, T, d, CHUNK
-    desc.rule, desc.ns, desc.dtype, desc.eps = rule, ns, nat.DTYPE_BF16, eps
+    dtype = nat.DTYPE_F32 if q.dtype == torch.float32 else nat.DTYPE_BF16
+    desc.rule, desc.ns, desc.dtype, desc.eps = rule, ns, dtype, eps
     desc.precision = precision
     for name, t in (("sq", q), ("sk", k), ("sv", v), ("so", o)):
         arr = getattr(desc, name)
@@ -141,19 +142,26 @@ def chunk_desc(q: Tensor, k: Tensor, v: Tensor, o: Tensor, rule: int, ns: int, e
     return desc
 
 
-def _tok(t: Tensor) -> Tensor:
-    """bf16 token stream with a unit-stride last dim and 16-byte-aligned rows."""
-    if t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:3]) or t.data_ptr() % 16:
+def _tok(t: Tensor, dense: bool = False) -> Tensor:
+    """Token stream with a unit-stride last dim, B/H/T strides in multiples
+    of 8 elements and a 16-byte-aligned base.  ``dense``: also a dense
+    permutation -- the backward writes each stream's gradient with the
+    stream's own strides, which must then neither alias (expanded views) nor
+    leave holes (a slice of a wider tensor)."""
+    if (t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:3]) or t.data_ptr() % 16
+            or (dense and not _dense_permutation(t))):
         t = t.contiguous()
     return t
 
 
 def _check_tokens(*ts: Tensor) -> None:
-    """The fused core reads and writes bf16 token streams only (the C ABI's
-    dtype is fixed to bfloat16 by ``chunk_desc``)."""
+    """The fused core reads and writes bfloat16 or float32 token streams, all
+    of one dtype (``chunk_desc`` passes it to the C ABI)."""
     for t in ts:
-        if t.dtype != torch.bfloat16:
-            raise RuntimeError(f"gmdn::chunk_fwd / chunk_bwd take bfloat16 q, k, v, got {t.dtype}")
+        if t.dtype not in (torch.bfloat16, torch.float32):
+            raise RuntimeError(f"gmdn::chunk_fwd / chunk_bwd take bfloat16 or float32 q, k, v, got {t.dtype}")
+        if t.dtype != ts[0].dtype:
+            raise RuntimeError(f"q, k, v must share one dtype, got {[x.dtype for x in ts]}")
         if t.dim() != 4:
             raise RuntimeError(f"token streams are (B, H, T, d), got shape {tuple(t.shape)}")
 
@@ -182,8 +190,7 @@ def chunk_fwd(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, g: Tensor, gmu: Opt
     # norm and output projection read it without a transposing copy)
     o = torch.empty_strided(q.shape, _kernel_strides(q), dtype=q.dtype, device=q.device)
     desc = chunk_desc(qc, kc, vc, o, rule, ns, eps)
-    # muon's output kernel reads the chunk states: they are written for inference too
-    keep = record or rule == 1
+    keep = _keeps_states(q, rule, record)
     states = (torch.empty(lib.gmdn_chunk_states_bytes(desc) // 4, dtype=torch.float32, device=q.device)
               if keep else _empty(q))
     with torch.cuda.device(q.device):
@@ -194,10 +201,17 @@ def chunk_fwd(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, g: Tensor, gmu: Opt
     return o, states
 
 
+def _keeps_states(q: Tensor, rule: int, record: bool) -> bool:
+    """Whether the forward writes the chunk states: for a backward, and always
+    where the output kernel reads them (muon; float32 streams, whose matrix
+    form runs the drop-in scan between chunk-parallel kernels)."""
+    return record or rule == 1 or q.dtype == torch.float32
+
+
 @chunk_fwd.register_fake
 def _chunk_fwd_fake(q, k, v, beta, g, gmu, gnu, rule, ns, eps, record):
     o = q.new_empty_strided(q.shape, _kernel_strides(q))
-    keep = record or rule == 1
+    keep = _keeps_states(q, rule, record)
     states = q.new_empty((_states_numel(q, rule, ns, eps),), dtype=torch.float32) if keep else _empty(q)
     return o, states
 
@@ -214,10 +228,10 @@ def _chunk_bwd_call(q, k, v, beta, g, gmu, gnu, states, dO, rule, ns, eps, preci
     scan's Newton-Schulz VJP in ``precision`` between chunk-parallel kernels)."""
     lib = nat.load()
     _check_tokens(q, k, v)
-    qc, kc, vc = _tok(q), _tok(k), _tok(v)
+    qc, kc, vc = _tok(q, dense=True), _tok(k, dense=True), _tok(v, dense=True)
     bc, gc, mc, nc = _gate(beta), _gate(g), _gate(gmu), _gate(gnu)
-    dOc = _tok(dO.to(torch.bfloat16))
-    # the kernels write dq, dk, dv with the strides of q, k, v
+    dOc = _tok(dO.to(q.dtype))
+    # the kernels write dq, dk, dv with the strides of q, k, v (dense here)
     dq, dk, dv = (torch.empty_strided(t.shape, t.stride(), dtype=t.dtype, device=t.device) for t in (qc, kc, vc))
     dbeta, dg = torch.empty_like(bc), torch.empty_like(gc)
     dgmu = torch.empty_like(mc) if mc is not None else _empty(q)
@@ -234,18 +248,32 @@ def _chunk_bwd_call(q, k, v, beta, g, gmu, gnu, states, dO, rule, ns, eps, preci
                                 nat.ptr(ws), ws_bytes, nat.stream_of(q))
     nat.check(rc, "gmdn_chunk_bwd")
     # the fake implementation cannot see data pointers: a stream that _tok
-    # copied only for its alignment gets its gradient back in the strides the
-    # fake reports
+    # copied for its alignment or density gets its gradient back in the
+    # strides the fake reports
     dq, dk, dv = (_as_strided_like(d_, t) for d_, t in ((dq, q), (dk, k), (dv, v)))
     return dq, dk, dv, dbeta, dg, dgmu, dgnu
 
 
+def _dense_permutation(t: Tensor) -> bool:
+    """Whether ``t``'s elements fill its storage extent exactly once: its
+    strides are those of a contiguous tensor with permuted dimensions (no
+    zero strides from ``expand``, no gaps as in a slice of a wider tensor)."""
+    dims = sorted((st, sz) for st, sz in zip(t.stride(), t.shape) if sz != 1)
+    want = 1
+    for st, sz in dims:
+        if st != want:
+            return False
+        want *= sz
+    return True
+
+
 def _kernel_strides(t: Tensor):
-    """The strides of the gradient of token stream ``t``: its own when they
-    suit the kernels (unit-stride d, B/H/T strides in multiples of 8
-    elements), else contiguous.  Alignment of the data pointer does not
-    enter, so the real and fake implementations agree."""
-    if t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:3]):
+    """The strides of the output and gradient of token stream ``t``: its own
+    when they suit the kernels (unit-stride d, B/H/T strides in multiples of
+    8 elements) and ``t`` is a dense permutation (an expanded stream would
+    make rows alias, a gapped one would leave holes), else contiguous.  The
+    data pointer does not enter, so the real and fake implementations agree."""
+    if t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:3]) or not _dense_permutation(t):
         return t.new_empty(t.shape).stride()
     return t.stride()
 

@@ -62,9 +62,12 @@ def wy_chunk_terms(q, k, v, beta, g):
     bt = beta.float().reshape(B, H, N, C)
     gcum = torch.cumsum(torch.clamp(g.float(), min=LOG_FLOOR).reshape(B, H, N, C), -1)
     gam = torch.exp(gcum)
-    Gam = torch.exp(gcum.unsqueeze(-1) - gcum.unsqueeze(-2))
     strict = torch.ones(C, C, dtype=torch.bool, device=q.device).tril(-1)
     incl = torch.ones(C, C, dtype=torch.bool, device=q.device).tril()
+    # Gamma[t, s] = gamma_t / gamma_s on the causal entries; the exponent is
+    # masked before exp, so the (unused) upper triangle is exp(-inf) = 0 and
+    # never overflows (an inf there would turn where()'s backward into NaN)
+    Gam = torch.exp(torch.where(incl, gcum.unsqueeze(-1) - gcum.unsqueeze(-2), float("-inf")))
     A = torch.where(strict, bt.unsqueeze(-1) * torch.matmul(K, K.transpose(-1, -2)) * Gam, 0.0)
     eye = torch.eye(C, dtype=torch.float32, device=q.device)
     T_ = torch.linalg.solve_triangular(eye + A, eye.expand_as(A), upper=False, unitriangular=True)

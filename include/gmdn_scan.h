@@ -47,7 +47,13 @@ extern "C" {
 #define GMDN_PREC_TF32 0
 #define GMDN_PREC_IEEE 1
 
-/* element type of the Level-B token streams */
+/* element type of the Level-B token streams.  bf16 streams run the fused
+ * E-form kernels (d = 64, 128).  float32 streams (d = 32, 64, 128, every
+ * rule) run the reference's matrix form with exact float32 products, as the
+ * reference computes when autocast is off (train_ablation.py:424, 465):
+ * chunk-parallel kernels form Kw, Uv and the chunk scalars, the drop-in
+ * scan kernels run in GMDN_PREC_IEEE, chunk-parallel kernels form o and,
+ * backward, dL/dS_i and the token and gate gradients. */
 #define GMDN_DTYPE_BF16 0
 #define GMDN_DTYPE_F32 1
 
@@ -155,7 +161,8 @@ typedef struct gmdn_chunk_desc {
 /* Bytes of the state checkpoint gmdn_chunk_fwd writes when `states` is
  * non-NULL (what gmdn_chunk_bwd consumes; for rules 0 and 2 its layout is
  * private to the library: rule 0 keeps the even chunks' states only, d x d
- * float32 each). */
+ * float32 each).  float32 streams: S_i [, M_i] [, V_i] of every chunk, the
+ * chunks' Kw_i, Uv_i and their four scalars. */
 size_t gmdn_chunk_states_bytes(const gmdn_chunk_desc* desc);
 
 /* Forward: o = mixer core(q, k, v, beta, g[, gmu][, gnu]).  g, gmu, gnu are
@@ -165,7 +172,9 @@ size_t gmdn_chunk_states_bytes(const gmdn_chunk_desc* desc);
  * backward needs (gmdn_chunk_states_bytes); it may be NULL for rules 0 and 2 when no
  * backward follows.  Rule 1 (muon) always needs it: its output kernel reads
  * the chunk states (S_i, M_i float32 (B, H, N, d, d) planes, the layout
- * gmdn_scan_bwd takes as S_all, M_all), which its backward reads too. */
+ * gmdn_scan_bwd takes as S_all, M_all), which its backward reads too.
+ * float32 streams (every rule) always need it for the same reason, and
+ * adam's eps must then be the drop-in scan's 1e-6 (fast_scan.py:94). */
 int gmdn_chunk_fwd(const gmdn_chunk_desc* desc, const void* q, const void* k,
                    const void* v, const float* beta, const float* g,
                    const float* gmu, const float* gnu, void* o, void* states,
@@ -178,7 +187,8 @@ int gmdn_chunk_fwd(const gmdn_chunk_desc* desc, const void* q, const void* k,
  * alpha_t = exp(max(g_t, log 1e-6)), chunked by the WY/UT transform
  * (T = (I + strict_lower(diag(beta) (K K^T * Gamma)))^-1, U = T diag(beta) V,
  * W = T diag(beta gamma) K) with exact float32 products.  desc->rule, ns and
- * eps are ignored; q, k, v, o bf16 with the strides of desc. */
+ * eps are ignored; q, k, v, o bf16 (desc->dtype GMDN_DTYPE_BF16) with the
+ * strides of desc. */
 size_t gmdn_wy_fwd_workspace_bytes(const gmdn_chunk_desc* desc);
 int gmdn_wy_fwd(const gmdn_chunk_desc* desc, const void* q, const void* k, const void* v,
                 const float* beta, const float* g, void* o, void* workspace,

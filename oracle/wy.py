@@ -56,9 +56,10 @@ def wy_chunk_terms(q, k, v, beta, g, C: int):
     bt = beta.reshape(B, H, N, C)
     gc = torch.cumsum(torch.clamp(g, min=LOG_FLOOR).reshape(B, H, N, C), -1)
     gamma = torch.exp(gc)
-    Gam = torch.exp(gc[..., :, None] - gc[..., None, :])
     strict = torch.ones(C, C, dtype=torch.bool, device=q.device).tril(-1)
     incl = torch.ones(C, C, dtype=torch.bool, device=q.device).tril()
+    # the exponent is masked to the causal entries (s <= t) before exp
+    Gam = torch.exp(torch.where(incl, gc[..., :, None] - gc[..., None, :], float("-inf")))
     A = torch.where(strict, bt[..., :, None] * (K @ K.transpose(-1, -2)) * Gam, 0.0)
     eye = torch.eye(C, dtype=q.dtype, device=q.device)
     T = torch.linalg.solve_triangular(eye + A, eye.expand_as(A), upper=False, unitriangular=True)

@@ -11,7 +11,10 @@ weights:
   phases 1-3 in float64, to the bf16 bound: the error in excess of half a
   bf16 ulp of the reference (the output's own rounding), at most 2e-2 of its
   RMS;
-* the tail (RMSNorm, output projection) applied to the core's output.
+* the tail (RMSNorm, output projection) applied to the core's output at the
+  layer's own precision.
+A float32 layer (autocast off) is also checked whole, against the reference
+layer restated in float64.
 The backward is checked for reaching every parameter with finite values."""
 import copy
 import math
@@ -85,11 +88,38 @@ def test_mixer_parts_match_reference(inner, d_model, heads):
         half_ulp = torch.pow(2.0, torch.floor(torch.log2(o_ref.abs().clamp_min(1e-30))) - 8)
         excess = ((o.double().cpu() - o_ref).abs() - half_ulp).clamp_min(0).max() / o_ref.pow(2).mean().sqrt()
         assert excess <= 2e-2, float(excess)
-        # the tail on that output
+        # the tail on the core's output at the layer's own precision (the
+        # float32 module passes float32 streams to the core)
         B, T, D = x.shape
         y = mine(x.to(dev))
-        y_tail = mine.out(mine.norm(o.float()).transpose(1, 2).reshape(B, T, D))
+        o_layer = chunk_scan(*got[:3], *got[3:], rule=inner, ns=mine.ns_steps)
+        y_tail = mine.out(mine.norm(o_layer.float()).transpose(1, 2).reshape(B, T, D))
         torch.testing.assert_close(y, y_tail, rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.parametrize("inner", ["delta", "muon", "adam"])
+def test_mixer_fp32_layer_matches_reference(inner):
+    """Without autocast the layer runs in float32 end to end, as the
+    reference's does (train_ablation.py:424, 465): front-end, the fused core
+    on float32 streams (the matrix form in exact float32) and the tail.  The
+    whole layer is checked against the reference layer restated in float64
+    with the same weights, rel = max|y - y_ref| / max|y_ref| <= 1e-4."""
+    dev = _dev()
+    ref, mine = _layer(inner, 128, dev, 2)  # 2 heads x 64
+    x = torch.randn(1, 256, 128)
+    with torch.no_grad():
+        y = mine(x.to(dev))
+        assert y.dtype == torch.float32
+        r = copy.deepcopy(ref).double()
+        r.norm.eps = torch.finfo(torch.float32).eps  # the float32 layer's RMSNorm epsilon
+        q, k, v, beta, la, lm, ln = _reference_front_end(r, x.double())
+        rule = {"delta": 0, "muon": 1, "adam": 2}[inner]
+        o = oc.mixer_core(q, k, v, beta, la, lm, ln, rule=rule, ns=r.ns_steps, C=64)
+        B, T, D = x.shape
+        y_ref = r.out(r.norm(o).transpose(1, 2).reshape(B, T, D))
+    err = ((y.double().cpu() - y_ref).abs().max() / y_ref.abs().max()).item()
+    print(f"float32 {inner} layer: rel {err:.2e}")
+    assert err <= 1e-4
 
 
 @pytest.mark.parametrize("inner,d_model,heads", CASES)

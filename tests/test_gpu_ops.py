@@ -32,10 +32,13 @@ def test_opcheck_state_scan(rule):
     torch.library.opcheck(torch.ops.gmdn.state_scan.default, (*ins, rule, 2, 0, True), test_utils=STATIC_CHECKS)
 
 
-@pytest.mark.parametrize("rule,d", [("delta", 64), ("adam", 64), ("muon", 64), ("muon", 128)])
-def test_opcheck_chunk_fwd(rule, d):
+@pytest.mark.parametrize("rule,d,dtype", [("delta", 64, torch.bfloat16), ("adam", 64, torch.bfloat16),
+                                           ("muon", 64, torch.bfloat16), ("muon", 128, torch.bfloat16),
+                                           ("delta", 32, torch.float32), ("adam", 64, torch.float32),
+                                           ("muon", 64, torch.float32)])
+def test_opcheck_chunk_fwd(rule, d, dtype):
     dev = _dev()
-    inp = make_inputs(Workload("t", rule, 1, 2, 128, d), seed=0, device=dev)
+    inp = make_inputs(Workload("t", rule, 1, 2, 128, d), seed=0, device=dev, dtype=dtype)
     r = chunk.RULES[rule]
     args = (inp["q"], inp["k"], inp["v"], inp["beta"], inp["g"], inp["gmu"] if r >= 1 else None,
             inp["gnu"] if r == 2 else None)
@@ -80,3 +83,34 @@ def test_compiled_chunk_scan_matches_eager(rule):
     inp = make_inputs(Workload("t", rule, 1, 2, 256, 64), seed=1, device=dev, with_grad_out=True)
     names = ["q", "k", "v", "beta", "g"] + (["gmu"] if rule != "delta" else []) + (["gnu"] if rule == "adam" else [])
     _compiled_vs_eager(lambda *x: chunk.chunk_scan(*x, rule=rule, ns=3), [inp[n] for n in names], inp["dO"])
+
+
+@pytest.mark.parametrize("view", ["expanded", "qkv_slice"])
+def test_chunk_scan_on_aliased_and_gapped_streams(view):
+    """q as an expanded view (one head's stream broadcast over the heads: zero
+    stride, rows alias) and as a slice of a fused (B, H, T, 3 d) projection
+    (gaps between rows): outputs and gradients equal those of contiguous
+    copies, and o and dq come back dense (no aliased rows, no holes)."""
+    dev = _dev()
+    inp = make_inputs(Workload("t", "delta", 1, 4, 256, 64), seed=6, device=dev, with_grad_out=True)
+    if view == "expanded":
+        base = inp["q"][:, :1].detach().requires_grad_(True)
+        q = base.expand(-1, 4, -1, -1)
+    else:
+        fused = torch.cat([inp["q"], inp["k"], inp["v"]], dim=-1).detach().requires_grad_(True)
+        base = fused
+        q = fused[..., :64]
+    assert q.stride(1) == 0 or q.stride(2) == 192
+    k, v = (inp[n].detach().requires_grad_(True) for n in ("k", "v"))
+    o = chunk.chunk_scan(q, k, v, inp["beta"], inp["g"], rule="delta")
+    dq, dk, dv = torch.autograd.grad(o, (q, k, v), inp["dO"])
+    qc = q.detach().contiguous().requires_grad_(True)
+    kc, vc = (t.detach().clone().requires_grad_(True) for t in (k, v))
+    oc_ = chunk.chunk_scan(qc, kc, vc, inp["beta"], inp["g"], rule="delta")
+    gc_ = torch.autograd.grad(oc_, (qc, kc, vc), inp["dO"])
+    torch.cuda.synchronize()
+    assert torch.equal(o, oc_)
+    for a, b in zip((dq, dk, dv), gc_):
+        assert torch.equal(a, b)
+    for t in (o, dq):
+        assert ops._dense_permutation(t), t.stride()

@@ -82,3 +82,34 @@ def test_wy_gradients_match_token_recurrence(d):
         raw, exc = _excess(a.double().cpu(), r)
         print(f"wy d{d} d{name}: max-abs/rms {raw:.2e}, excess {exc:.2e}")
         assert (exc if name in ("q", "k", "v") else raw) <= TOL, name
+
+
+@pytest.mark.parametrize("gval", [-2.0, -20.0])
+def test_wy_strong_decay(gval):
+    """Log-gates of -2 per token, and at the floor log 1e-6 (-20 is clamped
+    to it): the decay products underflow within a chunk.  Output and
+    gradients stay finite and match the token recurrence."""
+    dev = _dev()
+    q, k, v, beta, g = _inputs(1, 2, 256, 64, seed=21)
+    g = torch.full_like(g, gval)
+    ref = owy.token_scan(*(t.double() for t in (q, k, v, beta, g)))
+    with torch.no_grad():
+        o = gwy.wy_scan(*(t.to(dev) for t in (q, k, v, beta, g)))
+    torch.cuda.synchronize()
+    assert torch.isfinite(o).all()
+    raw, exc = _excess(o.double().cpu(), ref)
+    print(f"wy strong decay g={gval}: max-abs/rms {raw:.2e}, excess {exc:.2e}")
+    assert exc <= TOL
+    dO = torch.randn(q.shape, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16)
+    xs = [t.to(dev).requires_grad_(True) for t in (q, k, v, beta, g)]
+    got = torch.autograd.grad(gwy.wy_scan(*xs), xs, dO.to(dev))
+    rs = [t.double().requires_grad_(True) for t in (q, k, v, beta, g)]
+    ref_g = torch.autograd.grad(owy.token_scan(*rs), rs, dO.double())
+    for name, a, r in zip(("q", "k", "v", "beta", "g"), got, ref_g):
+        assert torch.isfinite(a).all(), name
+        if r.abs().max() == 0:
+            assert a.abs().max() == 0, name
+            continue
+        raw, exc = _excess(a.double().cpu(), r)
+        print(f"wy strong decay g={gval} d{name}: max-abs/rms {raw:.2e}, excess {exc:.2e}")
+        assert (exc if name in ("q", "k", "v") else raw) <= TOL, name
