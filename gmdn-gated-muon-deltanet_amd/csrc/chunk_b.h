@@ -90,6 +90,10 @@ hipError_t chunk_fwd_muon_launch(const ChunkArgs& a, int d, float* S_out, float*
 // exact WY/UT mode: prep kernel, the delta scan, output kernel (workspace in floats)
 size_t wy_workspace_floats(int64_t B, int64_t H, int64_t T, int d);
 hipError_t wy_fwd_launch(const ChunkArgs& a, int d, float* ws, hipStream_t s);
+// its backward from the forward's workspace (the checkpoint) and dO (strides a.so)
+size_t wy_bwd_workspace_floats(int64_t B, int64_t H, int64_t T, int d);
+hipError_t wy_bwd_launch(const ChunkArgs& a, int d, float* ckpt, const void* dO, void* dq, void* dk, void* dv,
+                         float* dbeta, float* dg, float* ws, hipStream_t s);
 hipError_t chunk_bwd_launch(const ChunkArgs& a, int d, int rule, hipStream_t s);
 // delta rule: the reverse scan of the state cotangent (Gb of the odd chunks)
 hipError_t chunk_bwd_dscan_launch(const ChunkArgs& a, int d, hipStream_t s);

@@ -649,6 +649,31 @@ int gmdn_wy_fwd(const gmdn_chunk_desc* desc, const void* q, const void* k, const
              : GMDN_ERR_LAUNCH;
 }
 
+size_t gmdn_wy_bwd_workspace_bytes(const gmdn_chunk_desc* desc) {
+  if (check_desc(desc) != GMDN_OK || desc->dtype != GMDN_DTYPE_BF16) return 0;
+  return wy_bwd_workspace_floats(desc->B, desc->H, desc->T, desc->d) * sizeof(float);
+}
+
+int gmdn_wy_bwd(const gmdn_chunk_desc* desc, const void* q, const void* k, const void* v, const float* beta,
+                const float* g, const void* ckpt, const void* dO, void* dq, void* dk, void* dv, float* dbeta,
+                float* dg, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_desc(desc);
+  if (rc != GMDN_OK) return rc;
+  if (desc->dtype != GMDN_DTYPE_BF16) return GMDN_ERR_UNSUPPORTED;
+  if (desc->B * desc->H * desc->T == 0) return GMDN_OK;
+  if (!q || !k || !v || !beta || !g || !ckpt || !dO || !dq || !dk || !dv || !dbeta || !dg) return GMDN_ERR_ARG;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dO) || !aligned16(ckpt))
+    return GMDN_ERR_UNSUPPORTED;
+  if ((desc->so[0] & 7) || (desc->so[1] & 7) || (desc->so[2] & 7)) return GMDN_ERR_UNSUPPORTED;
+  if (!workspace || !aligned16(workspace) || workspace_bytes < gmdn_wy_bwd_workspace_bytes(desc))
+    return GMDN_ERR_WORKSPACE;
+  const ChunkArgs a = make_args(desc, q, k, v, beta, g, nullptr, nullptr, nullptr, nullptr);
+  return wy_bwd_launch(a, desc->d, const_cast<float*>(static_cast<const float*>(ckpt)), dO, dq, dk, dv, dbeta, dg,
+                       static_cast<float*>(workspace), (hipStream_t)stream) == hipSuccess
+             ? GMDN_OK
+             : GMDN_ERR_LAUNCH;
+}
+
 size_t gmdn_chunk_bwd_workspace_bytes(const gmdn_chunk_desc* desc) {
   if (check_desc(desc) != GMDN_OK) return 0;
   if (desc->dtype == GMDN_DTYPE_F32)

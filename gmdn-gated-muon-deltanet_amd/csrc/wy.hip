@@ -3,26 +3,48 @@
 // chunked with the WY/UT transform (the reference trains the chunk-frozen
 // E-form instead and leaves this mode out, train_ablation.py:12-18).
 //
-// Per (b, h) and chunk of C = 64 tokens, with gamma_t the decay product from
-// the chunk start (log-gates clamped at log 1e-6), Gamma[t, s] = gamma_t / gamma_s:
+// Per (b, h) and chunk of C = 64 tokens, with gc_t the prefix sum of the
+// clamped log-gates from the chunk start, gamma_t = exp(gc_t),
+// Gamma[t, s] = exp(gc_t - gc_s) (formed on the causal entries s <= t only,
+// so that no ratio of two underflowed products appears) and
+// kd_t = gamma_C / gamma_t:
 //     A = strict_lower(diag(beta) (K K^T * Gamma)),   T = (I + A)^-1
-//     X = U - W S^T with U = T diag(beta) V, W = T diag(beta gamma) K
+//     U = T diag(beta) V,  W = T diag(beta gamma) K,  X = U - W S^T
 //     o = diag(gamma) Q S^T + M X,   M = lower_incl(Q K^T * Gamma)
-//     S' = gamma_C S + X^T diag(gamma_C / gamma) K
+//     S' = gamma_C S + X^T diag(kd) K
 // The state recurrence is affine, S' = a S + U_A - S K_A, which is the
 // drop-in delta scan's (fast_scan.py:82) with
 //     a = gamma_C,  U_A = (diag(beta) V)^T P,  K_A = (diag(beta gamma) K)^T P,
-//     P = T^T diag(gamma_C / gamma) K,
+//     P = T^T diag(kd) K,
 // and the output is o = Qt S^T + Ov with
 //     Qt = diag(gamma) Q - (M T diag(beta gamma)) K,  Ov = (M T diag(beta)) V.
 //
-// wy_prep (one workgroup of 4 waves per (b, h, chunk)) forms a, U_A, K_A, Qt
-// and Ov with exact float32 MFMA (v_mfma_f32_16x16x4_f32) on float32 tiles
-// in LDS; T by blocked forward substitution (the four 16 x 16 diagonal
-// blocks by one wave each, the off-diagonal blocks in three levels).  The
-// delta scan kernels then carry S, and wy_out forms o = Qt S_i^T + Ov.
+// Forward: wy_prep (one workgroup of 4 waves per (b, h, chunk)) forms a, U_A,
+// K_A, Qt and Ov with exact float32 MFMA (v_mfma_f32_16x16x4_f32) on float32
+// tiles in LDS, T by blocked forward substitution; the drop-in delta scan
+// kernels carry S ('ieee'); wy_out forms o = Qt S_i^T + Ov.  Its workspace
+// [U_A | K_A | S_all | Qt | Ov | a] is the backward's checkpoint.
+//
+// Backward, given dO:
+//   wy_gs     gS_i = dL/dS_i through o = dO^T Qt                 (chunk-parallel)
+//   the drop-in delta scan's reverse kernel ('ieee') on (U_A, K_A, a, S_all,
+//             gS): its dU_i is Sb = dL/dS_{i+1}, the state cotangent after chunk i
+//   wy_tok1 / wy_tok2: the VJP of the chunk algebra in the X-form above, per
+//             chunk from S_i and Sb (chunk-parallel):
+//     dX  = M^T dO + diag(kd) K Sb^T,  dQt~ = dO S_i,  dM = lower_incl(dO X^T),
+//     dK~ = X Sb,  dW = -dX S_i,  dgamma_C = <Sb, S_i>,
+//     dT  = dX (diag(beta) V)^T + dW (diag(beta gamma) K)^T,
+//     d(diag(beta) V) = T^T dX,  d(diag(beta gamma) K) = T^T dW,
+//     dA  = strict_lower(-T^T dT T^T),
+//     then A, M, gamma, kd and Gamma back to q, k, v, beta and the log-gates
+//     (Gamma's exponent differences give dgc_t as row minus column sums of
+//     dGamma * Gamma; dg_u = sum_{t >= u} dgc_t where g_u is above its floor).
+//   wy_tok1 runs up to dT (dv final; partial dq, dk; T, dT, dM and per-token
+//   gate partials to the workspace), wy_tok2 the rest (dA, the A and M terms,
+//   the gate gradients).
 #include "../../include/gmdn_scan.h"
 #include "chunk_b.h"
+#include "f32mm.h"
 #include "scan_a.h"
 
 namespace gmdn {
@@ -39,112 +61,38 @@ struct WyLds {
   static constexpr int K0 = 0, V0 = TILE, Q0 = 2 * TILE;   // Q's slot later holds P
   static constexpr int T0 = 3 * TILE, A0 = T0 + CC;          // A's slot later holds M, then M T
   static constexpr int X0 = A0 + CC;                         // 3 waves x 16 x 16 scratch
-  static constexpr int S0 = X0 + 3 * 256;  // beta, gamma, beta gamma, gamma_C / gamma, log gamma
+  static constexpr int S0 = X0 + 3 * 256;  // beta, gamma, beta gamma, kd, log gamma
   static constexpr int FLOATS = S0 + 5 * CB_C;
   static_assert(FLOATS * 4 <= 160 * 1024, "WY prep LDS exceeds the 160 KiB of a CU");
 };
 
-// acc += sum_k A(m, k) B(k, n) over a 16 x 16 tile, k in steps of 4 (exact fp32
-// MFMA); a(i, k) / b(k, i) give the lane's operand element for row / column i.
-template <int K, class FA, class FB>
-GMDN_DEV f32x4 mm16(FA a, FB b, f32x4 acc) {
-  const int l = lane_id(), i = l & 15, G = l >> 4;
-#pragma unroll 4
-  for (int k = 0; k < K; k += 4) acc = mfma_f32(a(i, k + G), b(k + G, i), acc);
-  return acc;
+// Per-token gate quantities of the chunk (wave 0, lane = token): beta, gamma,
+// beta gamma, kd = gamma_C / gamma and log gamma (the prefix sums of the
+// clamped log-gates) into LDS; returns gamma of this lane's token.
+GMDN_DEV float wy_gates(const float* beta, const float* g, int64_t e, float* bet, float* gam, float* bg,
+                        float* kd, float* lgam) {
+  const int l = lane_id();
+  const float bt = beta[e];
+  const float gc = wave_incl_scan(fmaxf(g[e], LOG_FLOOR));
+  const float gC = __shfl(gc, 63, 64);
+  const float g_ = expf(gc);
+  bet[l] = bt;
+  gam[l] = g_;
+  bg[l] = bt * g_;
+  kd[l] = expf(gC - gc);
+  lgam[l] = gc;
+  return g_;
 }
 
-// D-layout tile -> row-major float matrix at (r0, c0)
-GMDN_DEV void st_tile(float* X, int ld, int r0, int c0, const f32x4& t) {
-  const int l = lane_id(), c = l & 15, G = l >> 4;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) X[(r0 + 4 * G + j) * ld + c0 + c] = t[j];
-}
-
-template <int D>
-__global__ void __launch_bounds__(WY_THREADS)
-wy_prep(ChunkArgs p, float* __restrict__ UA, float* __restrict__ KA, float* __restrict__ Qt,
-        float* __restrict__ Ov, float* __restrict__ aout) {
-  using L = WyLds<D>;
-  constexpr int C = CB_C, LDT = L::LDT, LDC = L::LDC, NT = D / 16;
-  extern __shared__ __align__(16) float sm[];
-  float* Ks = sm + L::K0;
-  float* Vs = sm + L::V0;
-  float* Qs = sm + L::Q0;
-  float* Ts = sm + L::T0;
-  float* As = sm + L::A0;
-  float* bet = sm + L::S0;
-  float* gam = bet + C;
-  float* bg = gam + C;
-  float* kd = bg + C;
-  float* lgam = kd + C;  // prefix sums of the clamped log-gates
-
-  const int64_t bh = blockIdx.x / p.N;
-  const int i = (int)(blockIdx.x % p.N);
-  const int64_t bb = bh / p.H, hh = bh % p.H, t0 = (int64_t)i * C;
+// T = (I + A)^-1 for a strictly lower C x C matrix A (row stride LDC) into Ts,
+// which must be zero on entry.  The four 16 x 16 diagonal blocks by forward
+// substitution (wave w, lane j < 16 holds column j of block w), then the
+// off-diagonal blocks T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj level by level
+// (d = i - j; wave w takes the block with j = w).  Xw: 3 x 256 floats of
+// scratch.  Ends with a barrier.
+template <int LDC>
+GMDN_DEV void tri_inverse(const float* As, float* Ts, float* Xw_all) {
   const int w = wave_id(), l = lane_id();
-
-  // ---- tiles as float32, gates, zeroed T
-  const bf16* qg = p.q + bb * p.sq[0] + hh * p.sq[1] + t0 * p.sq[2];
-  const bf16* kg = p.k + bb * p.sk[0] + hh * p.sk[1] + t0 * p.sk[2];
-  const bf16* vg = p.v + bb * p.sv[0] + hh * p.sv[1] + t0 * p.sv[2];
-  for (int e = threadIdx.x; e < C * D / 8; e += WY_THREADS) {
-    const int t = e / (D / 8), c = (e % (D / 8)) * 8;
-    const bf16x8 kq = *reinterpret_cast<const bf16x8*>(kg + t * p.sk[2] + c);
-    const bf16x8 vq = *reinterpret_cast<const bf16x8*>(vg + t * p.sv[2] + c);
-    const bf16x8 qq = *reinterpret_cast<const bf16x8*>(qg + t * p.sq[2] + c);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      Ks[t * LDT + c + j] = (float)kq[j];
-      Vs[t * LDT + c + j] = (float)vq[j];
-      Qs[t * LDT + c + j] = (float)qq[j];
-    }
-  }
-  for (int e = threadIdx.x; e < C * LDC; e += WY_THREADS) Ts[e] = 0.f;
-  if (w == 0) {
-    const float bt = p.beta[bh * p.T + t0 + l];
-    const float lg = fmaxf(p.g[bh * p.T + t0 + l], LOG_FLOOR);
-    // inclusive prefix sum of the log-gates over the chunk
-    float gc = lg;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const float y = __shfl_up(gc, o, 64);
-      if (l >= o) gc += y;
-    }
-    const float gC = __shfl(gc, 63, 64);
-    const float g_ = expf(gc);
-    bet[l] = bt;
-    gam[l] = g_;
-    bg[l] = bt * g_;
-    kd[l] = expf(gC - gc);
-    lgam[l] = gc;
-    if (l == 63) aout[bh * p.N + i] = g_;
-  }
-  __syncthreads();
-
-  // ---- A = strict_lower(diag(beta) (K K^T * Gamma)): causal tiles by wave.
-  // Gamma[t, s] = exp(log gamma_t - log gamma_s) on the causal entries only:
-  // the ratio gamma_t / gamma_s of two underflowed products would be 0 / 0.
-  const float* gm = gam;
-  for (int tile = w; tile < 16; tile += 4) {
-    const int tt = tile >> 2, st = tile & 3;
-    f32x4 acc = zero4();
-    if (st <= tt) {
-      acc = mm16<D>([&](int ii, int k) { return Ks[(16 * tt + ii) * LDT + k]; },
-                    [&](int k, int ii) { return Ks[(16 * st + ii) * LDT + k]; }, acc);
-      const int c = l & 15, G = l >> 4, s = 16 * st + c;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int t = 16 * tt + 4 * G + j;
-        acc[j] = s < t ? bet[t] * acc[j] * expf(lgam[t] - lgam[s]) : 0.f;
-      }
-    }
-    st_tile(As, LDC, 16 * tt, 16 * st, acc);
-  }
-  __syncthreads();
-
-  // ---- T = (I + A)^-1: diagonal 16 x 16 blocks by forward substitution
-  // (wave w, lane j < 16 holds column j of block w)
   if (l < 16) {
     const int o = 16 * w;
     float x[16];
@@ -159,9 +107,7 @@ wy_prep(ChunkArgs p, float* __restrict__ UA, float* __restrict__ KA, float* __re
     for (int t = 0; t < 16; ++t) Ts[(o + t) * LDC + o + l] = x[t];
   }
   __syncthreads();
-  // off-diagonal blocks T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj, level d = i - j;
-  // wave w takes the block with j = w; lane (r = l / 4, c = 4 (l % 4) ..)
-  float* Xw = sm + L::X0 + 256 * (w < 3 ? w : 0);
+  float* Xw = Xw_all + 256 * (w < 3 ? w : 0);
   for (int d = 1; d < 4; ++d) {
     const int j = w, ii = w + d;
     const int r = l >> 2, c = 4 * (l & 3);
@@ -191,6 +137,73 @@ wy_prep(ChunkArgs p, float* __restrict__ UA, float* __restrict__ KA, float* __re
     }
     __syncthreads();
   }
+}
+
+// ------------------------------------------------------------------ forward
+template <int D>
+__global__ void __launch_bounds__(WY_THREADS)
+wy_prep(ChunkArgs p, float* __restrict__ UA, float* __restrict__ KA, float* __restrict__ Qt,
+        float* __restrict__ Ov, float* __restrict__ aout) {
+  using L = WyLds<D>;
+  constexpr int C = CB_C, LDT = L::LDT, LDC = L::LDC, NT = D / 16;
+  extern __shared__ __align__(16) float sm[];
+  float* Ks = sm + L::K0;
+  float* Vs = sm + L::V0;
+  float* Qs = sm + L::Q0;
+  float* Ts = sm + L::T0;
+  float* As = sm + L::A0;
+  float* bet = sm + L::S0;
+  float* gam = bet + C;
+  float* bg = gam + C;
+  float* kd = bg + C;
+  float* lgam = kd + C;
+
+  const int64_t bh = blockIdx.x / p.N;
+  const int i = (int)(blockIdx.x % p.N);
+  const int64_t bb = bh / p.H, hh = bh % p.H, t0 = (int64_t)i * C;
+  const int w = wave_id(), l = lane_id();
+
+  // ---- tiles as float32, gates, zeroed T
+  const bf16* qg = p.q + bb * p.sq[0] + hh * p.sq[1] + t0 * p.sq[2];
+  const bf16* kg = p.k + bb * p.sk[0] + hh * p.sk[1] + t0 * p.sk[2];
+  const bf16* vg = p.v + bb * p.sv[0] + hh * p.sv[1] + t0 * p.sv[2];
+  for (int e = threadIdx.x; e < C * D / 8; e += WY_THREADS) {
+    const int t = e / (D / 8), c = (e % (D / 8)) * 8;
+    const bf16x8 kq = *reinterpret_cast<const bf16x8*>(kg + t * p.sk[2] + c);
+    const bf16x8 vq = *reinterpret_cast<const bf16x8*>(vg + t * p.sv[2] + c);
+    const bf16x8 qq = *reinterpret_cast<const bf16x8*>(qg + t * p.sq[2] + c);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      Ks[t * LDT + c + j] = (float)kq[j];
+      Vs[t * LDT + c + j] = (float)vq[j];
+      Qs[t * LDT + c + j] = (float)qq[j];
+    }
+  }
+  for (int e = threadIdx.x; e < C * LDC; e += WY_THREADS) Ts[e] = 0.f;
+  if (w == 0) {
+    const float g_ = wy_gates(p.beta, p.g, bh * p.T + t0 + l, bet, gam, bg, kd, lgam);
+    if (l == 63) aout[bh * p.N + i] = g_;
+  }
+  __syncthreads();
+
+  // ---- A = strict_lower(diag(beta) (K K^T * Gamma)): causal tiles by wave
+  for (int tile = w; tile < 16; tile += 4) {
+    const int tt = tile >> 2, st = tile & 3;
+    f32x4 acc = zero4();
+    if (st <= tt) {
+      acc = mm16<D>([&](int ii, int k) { return Ks[(16 * tt + ii) * LDT + k]; },
+                    [&](int k, int ii) { return Ks[(16 * st + ii) * LDT + k]; }, acc);
+      const int c = l & 15, G = l >> 4, s = 16 * st + c;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int t = 16 * tt + 4 * G + j;
+        acc[j] = s < t ? bet[t] * acc[j] * expf(lgam[t] - lgam[s]) : 0.f;
+      }
+    }
+    st_tile(As, LDC, 16 * tt, 16 * st, acc);
+  }
+  __syncthreads();
+  tri_inverse<LDC>(As, Ts, sm + L::X0);
 
   // ---- M = lower_incl(Q K^T * Gamma) into A's slot, then M T in place
   for (int tile = w; tile < 16; tile += 4) {
@@ -241,11 +254,11 @@ wy_prep(ChunkArgs p, float* __restrict__ UA, float* __restrict__ KA, float* __re
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int t = 16 * tt + 4 * G + j, col = 16 * tc + c;
-      Qt[tokbase + (int64_t)t * D + col] = gm[t] * Qs[t * LDT + col] - qa[j];
+      Qt[tokbase + (int64_t)t * D + col] = gam[t] * Qs[t * LDT + col] - qa[j];
       Ov[tokbase + (int64_t)t * D + col] = oa[j];
     }
   }
-  __syncthreads();  // Q's slot is free: P = T^T diag(gamma_C / gamma) K
+  __syncthreads();  // Q's slot is free: P = T^T diag(kd) K
   float* Ps = Qs;
   for (int tile = w; tile < 4 * NT; tile += 4) {
     const int st = tile / NT, tc = tile % NT;
@@ -262,13 +275,8 @@ wy_prep(ChunkArgs p, float* __restrict__ UA, float* __restrict__ KA, float* __re
                                 [&](int k, int ii) { return Ps[k * LDT + 16 * tc + ii]; }, zero4());
     const f32x4 ka = mm16<CB_C>([&](int ii, int k) { return Ks[k * LDT + 16 * tr + ii] * bg[k]; },
                                 [&](int k, int ii) { return Ps[k * LDT + 16 * tc + ii]; }, zero4());
-    const int c = l & 15, G = l >> 4;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t o = mbase + (int64_t)(16 * tr + 4 * G + j) * D + 16 * tc + c;
-      UA[o] = ua[j];
-      KA[o] = ka[j];
-    }
+    st_tile(UA + mbase, D, 16 * tr, 16 * tc, ua);
+    st_tile(KA + mbase, D, 16 * tr, 16 * tc, ka);
   }
 }
 
@@ -310,28 +318,467 @@ wy_out(ChunkArgs p, const float* __restrict__ Qt, const float* __restrict__ Ov, 
   }
 }
 
+// ----------------------------------------------------------------- backward
+struct WyBwd {
+  const float *UA, *KA, *S_all, *Qt, *av;  // forward checkpoint
+  const bf16* dO;                         // strides so
+  float* gS;                              // wy_gs output
+  const float* Sb;                        // the reverse scan's dU (= dL/dS_{i+1})
+  float *dQp, *dKp;                       // partial dq, dk (B H T d, float32)
+  float *Tp, *dTp, *dMp;                  // T, dT, dM per chunk (C x C, float32)
+  float* tokp;                            // per chunk: dgamma, dkd, dbeta partials (3 x C) and da
+  bf16 *dq, *dk, *dv;
+  float *dbeta, *dg;
+};
+
+// gS[r][c] = sum_t dO[t][r] Qt[t][c]
+template <int D>
+__global__ void __launch_bounds__(WY_THREADS) wy_gs(ChunkArgs p, WyBwd b) {
+  constexpr int C = CB_C, LDT = D + 4, NT = D / 16;
+  extern __shared__ __align__(16) float sm[];
+  float* Os = sm;
+  float* Qs = sm + C * LDT;
+  const int64_t bh = blockIdx.x / p.N;
+  const int i = (int)(blockIdx.x % p.N);
+  const int64_t bb = bh / p.H, hh = bh % p.H, t0 = (int64_t)i * C, si = bh * p.N + i;
+  const int w = wave_id();
+  const bf16* og = b.dO + bb * p.so[0] + hh * p.so[1] + t0 * p.so[2];
+  const float* qt = b.Qt + (bh * p.T + t0) * (int64_t)D;
+  for (int e = threadIdx.x; e < C * D / 8; e += WY_THREADS) {
+    const int t = e / (D / 8), c = (e % (D / 8)) * 8;
+    const bf16x8 x = *reinterpret_cast<const bf16x8*>(og + t * p.so[2] + c);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) Os[t * LDT + c + j] = (float)x[j];
+    *reinterpret_cast<f32x4*>(Qs + t * LDT + c) = *reinterpret_cast<const f32x4*>(qt + (int64_t)t * D + c);
+    *reinterpret_cast<f32x4*>(Qs + t * LDT + c + 4) = *reinterpret_cast<const f32x4*>(qt + (int64_t)t * D + c + 4);
+  }
+  __syncthreads();
+  float* gS = b.gS + si * (int64_t)D * D;
+  for (int tile = w; tile < NT * NT; tile += 4) {
+    const int tr = tile / NT, tc = tile % NT;
+    const f32x4 acc = mm16<C>([&](int r, int k) { return Os[k * LDT + 16 * tr + r]; },
+                              [&](int k, int c) { return Qs[k * LDT + 16 * tc + c]; }, zero4());
+    st_tile(gS, D, 16 * tr, 16 * tc, acc);
+  }
+}
+
+template <int D>
+struct WyBwdLds {
+  static constexpr int C = CB_C;
+  static constexpr int LDB = D + 8;        // bf16 stride of a token tile row
+  static constexpr int LDT = D + 4;        // float stride of a token tile row
+  static constexpr int LDC = C + 4;        // float stride of a C x C matrix row
+  static constexpr int BT = C * LDB * 2;   // bytes: bf16 token tile
+  static constexpr int FT = C * LDT * 4;   // bytes: float token tile
+  static constexpr int CC = C * LDC * 4;   // bytes: float C x C matrix
+  // wy_tok1: K, V, dO (bf16); F1: Q (bf16) in steps 0-1, then W / X / dW rows;
+  // F2: A in steps 1-2, then dX rows; T; M; then small float arrays
+  static constexpr int K0 = 0, V0 = BT, O0 = 2 * BT, F1 = 3 * BT, F2 = F1 + FT, T0 = F2 + FT, M0 = T0 + CC;
+  static constexpr int R0 = M0 + CC;
+  static constexpr int SMALL1 = 5 * C + 3 * 256 + 4;  // gates, tri_inverse scratch, per-wave <Sb, S_i>
+  static constexpr int TOK1_BYTES = R0 + SMALL1 * 4;
+  // wy_tok2: Q, K (bf16); T, dT, dM, Y = dT T^T, G_A, dM * Gamma; small arrays
+  static constexpr int Q2 = 0, K2 = BT, T2 = 2 * BT, DT2 = T2 + CC, DM2 = DT2 + CC, Y2 = DM2 + CC,
+                       GA2 = Y2 + CC, DG2 = GA2 + CC, R2 = DG2 + CC;
+  static constexpr int SMALL2 = 5 * C + 2 * C + 4 * C;  // gates, rowE, colE
+  static constexpr int TOK2_BYTES = R2 + SMALL2 * 4;
+  static_assert(TOK1_BYTES <= 160 * 1024 && TOK2_BYTES <= 160 * 1024, "WY backward LDS exceeds 160 KiB");
+  static_assert(BT <= FT && CC <= FT, "Q and A fit the slots they borrow");
+};
+
+template <int LDB>
+GMDN_DEV float bfx(const bf16* X, int r, int c) { return (float)X[r * LDB + c]; }
+
+template <int D>
+GMDN_DEV void load_bf16_rows(bf16* dst, const bf16* src, int64_t stride) {
+  constexpr int LDB = D + 8;
+  for (int e = threadIdx.x; e < CB_C * D / 8; e += WY_THREADS) {
+    const int t = e / (D / 8), c = (e % (D / 8)) * 8;
+    *reinterpret_cast<bf16x8*>(dst + t * LDB + c) = *reinterpret_cast<const bf16x8*>(src + t * stride + c);
+  }
+}
+
+template <int D>
+__global__ void __launch_bounds__(WY_THREADS) wy_tok1(ChunkArgs p, WyBwd b) {
+  using L = WyBwdLds<D>;
+  constexpr int C = CB_C, LDB = L::LDB, LDT = L::LDT, LDC = L::LDC, NT = D / 16;
+  extern __shared__ __align__(16) char smem[];
+  bf16* Ks = reinterpret_cast<bf16*>(smem + L::K0);
+  bf16* Vs = reinterpret_cast<bf16*>(smem + L::V0);
+  bf16* Os = reinterpret_cast<bf16*>(smem + L::O0);
+  bf16* Qs = reinterpret_cast<bf16*>(smem + L::F1);
+  float* F1 = reinterpret_cast<float*>(smem + L::F1);
+  float* As = reinterpret_cast<float*>(smem + L::F2);
+  float* F2 = reinterpret_cast<float*>(smem + L::F2);
+  float* Ts = reinterpret_cast<float*>(smem + L::T0);
+  float* Ms = reinterpret_cast<float*>(smem + L::M0);
+  float* bet = reinterpret_cast<float*>(smem + L::R0);
+  float* gam = bet + C;
+  float* bg = gam + C;
+  float* kd = bg + C;
+  float* lgam = kd + C;
+  float* Xw = lgam + C;      // 3 x 256
+  float* pda = Xw + 768;     // per wave: partial <Sb, S_i>
+
+  const int64_t bh = blockIdx.x / p.N;
+  const int i = (int)(blockIdx.x % p.N);
+  const int64_t bb = bh / p.H, hh = bh % p.H, t0 = (int64_t)i * C, si = bh * p.N + i;
+  const int w = wave_id(), l = lane_id(), lc = l & 15, G = l >> 4;
+  const int r0 = 16 * w;  // this wave's token rows
+  const int64_t mat = (int64_t)D * D;
+  const float* S = b.S_all + si * mat;
+  const float* Sb = b.Sb + si * mat;
+  const bf16* qg = p.q + bb * p.sq[0] + hh * p.sq[1] + t0 * p.sq[2];
+
+  // ---- step 0: tiles, gates, zeroed T
+  load_bf16_rows<D>(Qs, qg, p.sq[2]);
+  load_bf16_rows<D>(Ks, p.k + bb * p.sk[0] + hh * p.sk[1] + t0 * p.sk[2], p.sk[2]);
+  load_bf16_rows<D>(Vs, p.v + bb * p.sv[0] + hh * p.sv[1] + t0 * p.sv[2], p.sv[2]);
+  load_bf16_rows<D>(Os, b.dO + bb * p.so[0] + hh * p.so[1] + t0 * p.so[2], p.so[2]);
+  for (int e = threadIdx.x; e < C * LDC; e += WY_THREADS) Ts[e] = 0.f;
+  if (w == 0) wy_gates(p.beta, p.g, bh * p.T + t0 + l, bet, gam, bg, kd, lgam);
+  __syncthreads();
+  auto kb = [&](int r, int c) { return bfx<LDB>(Ks, r, c); };
+
+  // ---- step 1: rows of A and M
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+    f32x4 a = zero4(), m = zero4();
+    if (st <= w) {
+      const f32x4 kk = mm16<D>([&](int r, int k) { return kb(r0 + r, k); },
+                               [&](int k, int c) { return kb(16 * st + c, k); }, zero4());
+      const f32x4 qk = mm16<D>([&](int r, int k) { return bfx<LDB>(Qs, r0 + r, k); },
+                               [&](int k, int c) { return kb(16 * st + c, k); }, zero4());
+      const int s = 16 * st + lc;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int t = r0 + 4 * G + j;
+        const float e = s <= t ? expf(lgam[t] - lgam[s]) : 0.f;
+        a[j] = s < t ? bet[t] * kk[j] * e : 0.f;
+        m[j] = qk[j] * e;
+      }
+    }
+    st_tile(As, LDC, r0, 16 * st, a);
+    st_tile(Ms, LDC, r0, 16 * st, m);
+  }
+  __syncthreads();
+  // ---- step 2: T = (I + A)^-1
+  tri_inverse<LDC>(As, Ts, Xw);
+
+  // ---- step 3: W, U and X = U - W S_i^T for this wave's rows (Q is dead: F1 holds W, then X)
+  f32x4 X[NT];
+#pragma unroll
+  for (int tc = 0; tc < NT; ++tc) {
+    auto trow = [&](int r, int k) { return Ts[(r0 + r) * LDC + k]; };
+    const f32x4 wt = mm16<C>(trow, [&](int k, int c) { return bg[k] * kb(k, 16 * tc + c); }, zero4());
+    st_tile(F1, LDT, r0, 16 * tc, wt);
+    X[tc] = mm16<C>(trow, [&](int k, int c) { return bet[k] * bfx<LDB>(Vs, k, 16 * tc + c); }, zero4());
+  }
+#pragma unroll
+  for (int tc = 0; tc < NT; ++tc)
+    X[tc] -= mm16<D>([&](int r, int k) { return F1[(r0 + r) * LDT + k]; },
+                     [&](int k, int c) { return S[(int64_t)(16 * tc + c) * D + k]; }, zero4());
+#pragma unroll
+  for (int tc = 0; tc < NT; ++tc) st_tile(F1, LDT, r0, 16 * tc, X[tc]);
+  __syncthreads();  // X complete
+
+  // ---- step 4: dM = lower_incl(dO X^T), dQt~ = dO S_i, dK~ = X Sb; <Sb, S_i>
+  auto orow = [&](int r, int k) { return bfx<LDB>(Os, r0 + r, k); };
+  f32x4 dM[4];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+    dM[st] = zero4();
+    if (st <= w) {
+      dM[st] = mm16<D>(orow, [&](int k, int c) { return F1[(16 * st + c) * LDT + k]; }, zero4());
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (16 * st + lc > r0 + 4 * G + j) dM[st][j] = 0.f;
+    }
+  }
+  float dgam[4] = {0.f, 0.f, 0.f, 0.f}, dkd[4] = {0.f, 0.f, 0.f, 0.f};
+  float dbet[4] = {0.f, 0.f, 0.f, 0.f}, dbg[4] = {0.f, 0.f, 0.f, 0.f};
+  float* dqp = b.dQp + (bh * p.T + t0) * (int64_t)D;
+  float* dkp = b.dKp + (bh * p.T + t0) * (int64_t)D;
+  f32x4 dK[NT];
+#pragma unroll
+  for (int tc = 0; tc < NT; ++tc) {
+    const f32x4 dqt = mm16<D>(orow, [&](int k, int c) { return S[(int64_t)k * D + 16 * tc + c]; }, zero4());
+    const f32x4 dkt = mm16<D>([&](int r, int k) { return F1[(r0 + r) * LDT + k]; },
+                              [&](int k, int c) { return Sb[(int64_t)k * D + 16 * tc + c]; }, zero4());
+    f32x4 dq;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = r0 + 4 * G + j, c = 16 * tc + lc;
+      dgam[j] += dqt[j] * (float)qg[(int64_t)t * p.sq[2] + c];
+      dkd[j] += dkt[j] * kb(t, c);
+      dq[j] = gam[t] * dqt[j];
+      dK[tc][j] = kd[t] * dkt[j];
+    }
+    st_tile(dqp, D, r0, 16 * tc, dq);
+  }
+  {
+    float acc = 0.f;
+    for (int e = threadIdx.x; e < D * D / 4; e += WY_THREADS) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(S + 4 * (int64_t)e);
+      const f32x4 y = *reinterpret_cast<const f32x4*>(Sb + 4 * (int64_t)e);
+      acc += x[0] * y[0] + x[1] * y[1] + x[2] * y[2] + x[3] * y[3];
+    }
+    acc = wave_sum(acc);
+    if (l == 0) pda[w] = acc;
+  }
+
+  // ---- step 5: dX = M^T dO + diag(kd) K Sb^T (F2, A is dead), dW = -dX S_i
+#pragma unroll
+  for (int tc = 0; tc < NT; ++tc) {
+    f32x4 dx = mm16<C>([&](int r, int k) { return Ms[k * LDC + r0 + r]; },
+                       [&](int k, int c) { return bfx<LDB>(Os, k, 16 * tc + c); }, zero4());
+    dx = mm16<D>([&](int r, int k) { return kd[r0 + r] * kb(r0 + r, k); },
+                 [&](int k, int c) { return Sb[(int64_t)(16 * tc + c) * D + k]; }, dx);
+    st_tile(F2, LDT, r0, 16 * tc, dx);
+  }
+  f32x4 dW[NT];
+#pragma unroll
+  for (int tc = 0; tc < NT; ++tc)
+    dW[tc] = -mm16<D>([&](int r, int k) { return F2[(r0 + r) * LDT + k]; },
+                      [&](int k, int c) { return S[(int64_t)k * D + 16 * tc + c]; }, zero4());
+  __syncthreads();  // every wave has read X and written its dX rows
+#pragma unroll
+  for (int tc = 0; tc < NT; ++tc) st_tile(F1, LDT, r0, 16 * tc, dW[tc]);
+  __syncthreads();
+
+  // ---- step 6: dT (to the workspace), dv, and the T^T dW term of dk
+  float* dTp = b.dTp + si * C * C;
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+    f32x4 dt = mm16<D>([&](int r, int k) { return F2[(r0 + r) * LDT + k]; },
+                       [&](int k, int c) { return bet[16 * st + c] * bfx<LDB>(Vs, 16 * st + c, k); }, zero4());
+    dt = mm16<D>([&](int r, int k) { return F1[(r0 + r) * LDT + k]; },
+                 [&](int k, int c) { return bg[16 * st + c] * kb(16 * st + c, k); }, dt);
+    st_tile(dTp, C, r0, 16 * st, dt);
+  }
+  bf16* dvg = b.dv + bb * p.sv[0] + hh * p.sv[1] + t0 * p.sv[2];
+#pragma unroll
+  for (int tc = 0; tc < NT; ++tc) {
+    auto tcol = [&](int r, int k) { return Ts[k * LDC + r0 + r]; };
+    const f32x4 dvb = mm16<C>(tcol, [&](int k, int c) { return F2[k * LDT + 16 * tc + c]; }, zero4());
+    const f32x4 dkb = mm16<C>(tcol, [&](int k, int c) { return F1[k * LDT + 16 * tc + c]; }, zero4());
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = r0 + 4 * G + j, c = 16 * tc + lc;
+      dbet[j] += dvb[j] * bfx<LDB>(Vs, t, c);
+      dbg[j] += dkb[j] * kb(t, c);
+      dvg[(int64_t)t * p.sv[2] + c] = (bf16)(bet[t] * dvb[j]);
+      dK[tc][j] += bg[t] * dkb[j];
+    }
+    st_tile(dkp, D, r0, 16 * tc, dK[tc]);
+  }
+  // ---- T, dM and the per-token gate partials to the workspace
+  float* Tp = b.Tp + si * C * C;
+  float* dMp = b.dMp + si * C * C;
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+    st_tile(Tp, C, r0, 16 * st, ld_tile(Ts, LDC, r0, 16 * st));
+    st_tile(dMp, C, r0, 16 * st, dM[st]);
+  }
+  float* tp = b.tokp + si * (3 * C + 4);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int t = r0 + 4 * G + j;
+    const float sg = row16_sum(dgam[j]), sk = row16_sum(dkd[j]), sb = row16_sum(dbet[j]), sbg = row16_sum(dbg[j]);
+    if (lc == 0) {
+      tp[t] = sg + bet[t] * sbg;          // dL/dgamma_t (Q~ = diag(gamma) Q, and beta gamma)
+      tp[C + t] = sk;                     // dL/dkd_t
+      tp[2 * C + t] = sb + gam[t] * sbg;  // dL/dbeta_t from U and W
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) tp[3 * C] = (pda[0] + pda[1]) + (pda[2] + pda[3]);  // dL/dgamma_C = <Sb, S_i>
+}
+
+template <int D>
+__global__ void __launch_bounds__(WY_THREADS) wy_tok2(ChunkArgs p, WyBwd b) {
+  using L = WyBwdLds<D>;
+  constexpr int C = CB_C, LDB = L::LDB, LDC = L::LDC, NT = D / 16;
+  extern __shared__ __align__(16) char smem[];
+  bf16* Qs = reinterpret_cast<bf16*>(smem + L::Q2);
+  bf16* Ks = reinterpret_cast<bf16*>(smem + L::K2);
+  float* Ts = reinterpret_cast<float*>(smem + L::T2);
+  float* dTs = reinterpret_cast<float*>(smem + L::DT2);
+  float* dMs = reinterpret_cast<float*>(smem + L::DM2);
+  float* Ys = reinterpret_cast<float*>(smem + L::Y2);
+  float* GAs = reinterpret_cast<float*>(smem + L::GA2);
+  float* DGs = reinterpret_cast<float*>(smem + L::DG2);
+  float* bet = reinterpret_cast<float*>(smem + L::R2);
+  float* gam = bet + C;
+  float* bg = gam + C;
+  float* kd = bg + C;
+  float* lgam = kd + C;
+  float* rowE = lgam + C;   // per token: sum_s dGamma[t,s] Gamma[t,s] + the A term of dbeta (2 x C)
+  float* colE = rowE + 2 * C;  // per wave: column sums of dGamma * Gamma (4 x C)
+
+  const int64_t bh = blockIdx.x / p.N;
+  const int i = (int)(blockIdx.x % p.N);
+  const int64_t bb = bh / p.H, hh = bh % p.H, t0 = (int64_t)i * C, si = bh * p.N + i;
+  const int w = wave_id(), l = lane_id(), lc = l & 15, G = l >> 4;
+  const int r0 = 16 * w;
+  load_bf16_rows<D>(Qs, p.q + bb * p.sq[0] + hh * p.sq[1] + t0 * p.sq[2], p.sq[2]);
+  load_bf16_rows<D>(Ks, p.k + bb * p.sk[0] + hh * p.sk[1] + t0 * p.sk[2], p.sk[2]);
+  const float* Tp = b.Tp + si * C * C;
+  const float* dTp = b.dTp + si * C * C;
+  const float* dMp = b.dMp + si * C * C;
+  for (int e = threadIdx.x; e < C * C / 4; e += WY_THREADS) {
+    const int r = e / (C / 4), c = (e % (C / 4)) * 4;
+    *reinterpret_cast<f32x4*>(Ts + r * LDC + c) = *reinterpret_cast<const f32x4*>(Tp + r * C + c);
+    *reinterpret_cast<f32x4*>(dTs + r * LDC + c) = *reinterpret_cast<const f32x4*>(dTp + r * C + c);
+    *reinterpret_cast<f32x4*>(dMs + r * LDC + c) = *reinterpret_cast<const f32x4*>(dMp + r * C + c);
+  }
+  float graw = 0.f;
+  if (w == 0) {
+    graw = p.g[bh * p.T + t0 + l];
+    wy_gates(p.beta, p.g, bh * p.T + t0 + l, bet, gam, bg, kd, lgam);
+  }
+  __syncthreads();
+  auto kb = [&](int r, int c) { return bfx<LDB>(Ks, r, c); };
+
+  // ---- Y = dT T^T (rows of this wave)
+#pragma unroll
+  for (int st = 0; st < 4; ++st)
+    st_tile(Ys, LDC, r0, 16 * st,
+            mm16<C>([&](int r, int k) { return dTs[(r0 + r) * LDC + k]; },
+                    [&](int k, int c) { return Ts[(16 * st + c) * LDC + k]; }, zero4()));
+  __syncthreads();
+
+  // ---- dA = strict_lower(-T^T Y); the A and M terms: G_A = dA beta_t Gamma, dM Gamma,
+  // dbeta_t += sum_s dA R Gamma, E = dGamma * Gamma = (dA beta_t R + dM Rq) Gamma
+  float rsum[4] = {0.f, 0.f, 0.f, 0.f}, bsum[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+    f32x4 ga = zero4(), dg = zero4();
+    float csum = 0.f;
+    if (st <= w) {
+      const f32x4 dA = mm16<C>([&](int r, int k) { return Ts[k * LDC + r0 + r]; },
+                               [&](int k, int c) { return Ys[k * LDC + 16 * st + c]; }, zero4());
+      const f32x4 kk = mm16<D>([&](int r, int k) { return kb(r0 + r, k); },
+                               [&](int k, int c) { return kb(16 * st + c, k); }, zero4());
+      const f32x4 qk = mm16<D>([&](int r, int k) { return bfx<LDB>(Qs, r0 + r, k); },
+                               [&](int k, int c) { return kb(16 * st + c, k); }, zero4());
+      const int s = 16 * st + lc;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int t = r0 + 4 * G + j;
+        const float e = s <= t ? expf(lgam[t] - lgam[s]) : 0.f;
+        const float da = s < t ? -dA[j] : 0.f;
+        const float dm = s <= t ? dMs[t * LDC + s] : 0.f;
+        ga[j] = da * bet[t] * e;
+        dg[j] = dm * e;
+        bsum[j] += da * kk[j] * e;
+        const float E = (da * bet[t] * kk[j] + dm * qk[j]) * e;
+        rsum[j] += E;
+        csum += E;
+      }
+    }
+    st_tile(GAs, LDC, r0, 16 * st, ga);
+    st_tile(DGs, LDC, r0, 16 * st, dg);
+    csum = group_sum(csum);
+    if (G == 0) colE[w * C + 16 * st + lc] = csum;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float rs = row16_sum(rsum[j]), bs = row16_sum(bsum[j]);
+    if (lc == 0) {
+      rowE[r0 + 4 * G + j] = rs;
+      rowE[C + r0 + 4 * G + j] = bs;
+    }
+  }
+  __syncthreads();
+
+  // ---- dk = partial + G_A K + G_A^T K + (dM Gamma)^T Q,  dq = partial + (dM Gamma) K
+  const float* dqp = b.dQp + (bh * p.T + t0) * (int64_t)D;
+  const float* dkp = b.dKp + (bh * p.T + t0) * (int64_t)D;
+  bf16* dqg = b.dq + bb * p.sq[0] + hh * p.sq[1] + t0 * p.sq[2];
+  bf16* dkg = b.dk + bb * p.sk[0] + hh * p.sk[1] + t0 * p.sk[2];
+#pragma unroll
+  for (int tc = 0; tc < NT; ++tc) {
+    auto kcol = [&](int k, int c) { return kb(k, 16 * tc + c); };
+    f32x4 dk = ld_tile(dkp, D, r0, 16 * tc);
+    dk = mm16<C>([&](int r, int k) { return GAs[(r0 + r) * LDC + k]; }, kcol, dk);
+    dk = mm16<C>([&](int r, int k) { return GAs[k * LDC + r0 + r]; }, kcol, dk);
+    dk = mm16<C>([&](int r, int k) { return DGs[k * LDC + r0 + r]; },
+                 [&](int k, int c) { return bfx<LDB>(Qs, k, 16 * tc + c); }, dk);
+    f32x4 dq = ld_tile(dqp, D, r0, 16 * tc);
+    dq = mm16<C>([&](int r, int k) { return DGs[(r0 + r) * LDC + k]; }, kcol, dq);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t t = r0 + 4 * G + j;
+      const int c = 16 * tc + lc;
+      dkg[t * p.sk[2] + c] = (bf16)dk[j];
+      dqg[t * p.sq[2] + c] = (bf16)dq[j];
+    }
+  }
+
+  // ---- gate gradients (wave 0, lane = token)
+  if (w == 0) {
+    const float* tp = b.tokp + si * (3 * C + 4);
+    const float dgm = tp[l], dkdv = tp[C + l], dbu = tp[2 * C + l], dgC = tp[3 * C];
+    // dgc_t: gamma_t = exp(gc_t), kd_t = exp(gc_{C-1} - gc_t), the Gamma
+    // exponents (row minus column sums), and gamma_{C-1} = a of the scan
+    float dgc = dgm * gam[l] - dkdv * kd[l] + rowE[l] - ((colE[l] + colE[C + l]) + (colE[2 * C + l] + colE[3 * C + l]));
+    const float kdsum = wave_sum(dkdv * kd[l]);
+    if (l == C - 1) dgc += kdsum + dgC * gam[l];
+    // dlg_u = sum_{t >= u} dgc_t
+    const float dlg = wave_sum(dgc) - (wave_incl_scan(dgc) - dgc);
+    const int64_t o = bh * p.T + t0 + l;
+    b.dg[o] = graw >= LOG_FLOOR ? dlg : 0.f;
+    b.dbeta[o] = dbu + rowE[C + l];
+  }
+}
+
+template <int D>
+size_t ckpt_floats(int64_t B, int64_t H, int64_t T) {
+  const int64_t chunks = B * H * (T / CB_C), mat = (int64_t)D * D, tok = B * H * T * (int64_t)D;
+  return (size_t)(3 * chunks * mat + 2 * tok + chunks);
+}
+
+struct Ckpt {
+  float *UA, *KA, *S_all, *Qt, *Ov, *av;
+};
+Ckpt ckpt_of(float* ws, int64_t B, int64_t H, int64_t T, int d) {
+  const int64_t chunks = B * H * (T / CB_C), mat = (int64_t)d * d, tok = B * H * T * (int64_t)d;
+  Ckpt c;
+  c.UA = ws;
+  c.KA = c.UA + chunks * mat;
+  c.S_all = c.KA + chunks * mat;
+  c.Qt = c.S_all + chunks * mat;
+  c.Ov = c.Qt + tok;
+  c.av = c.Ov + tok;
+  return c;
+}
+
+template <class K>
+hipError_t launch_k(K kern, int bytes, int64_t grid, hipStream_t s, const ChunkArgs& a, const WyBwd& b) {
+  hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(WY_THREADS), bytes, s, a, b);
+  return hipGetLastError();
+}
+
 template <int D>
 hipError_t launch_wy(const ChunkArgs& a, float* ws, hipStream_t s) {
-  const int64_t chunks = a.B * a.H * a.N, mat = (int64_t)D * D, tok = a.B * a.H * a.T * (int64_t)D;
-  float* UA = ws;
-  float* KA = UA + chunks * mat;
-  float* S_all = KA + chunks * mat;
-  float* Qt = S_all + chunks * mat;
-  float* Ov = Qt + tok;
-  float* av = Ov + tok;
+  const int64_t chunks = a.B * a.H * a.N;
+  const Ckpt c = ckpt_of(ws, a.B, a.H, a.T, D);
   auto kp = wy_prep<D>;
   auto ko = wy_out<D>;
   const int lp = WyLds<D>::FLOATS * 4, lo = (CB_C + D) * (D + 4) * 4;
   hipError_t e = hipFuncSetAttribute((const void*)kp, hipFuncAttributeMaxDynamicSharedMemorySize, lp);
   if (e == hipSuccess) e = hipFuncSetAttribute((const void*)ko, hipFuncAttributeMaxDynamicSharedMemorySize, lo);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(kp, dim3((unsigned)chunks), dim3(WY_THREADS), lp, s, a, UA, KA, Qt, Ov, av);
+  hipLaunchKernelGGL(kp, dim3((unsigned)chunks), dim3(WY_THREADS), lp, s, a, c.UA, c.KA, c.Qt, c.Ov, c.av);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   ScanArgs sa{};
-  sa.U = UA;
-  sa.K = KA;
-  sa.a = av;
-  sa.S_all = S_all;
+  sa.U = c.UA;
+  sa.K = c.KA;
+  sa.a = c.av;
+  sa.S_all = c.S_all;
   sa.BH = a.B * a.H;
   sa.N = a.N;
   sa.dh = D;
@@ -340,21 +787,85 @@ hipError_t launch_wy(const ChunkArgs& a, float* ws, hipStream_t s) {
   sa.precision = GMDN_PREC_IEEE;  // exact float32 state products
   sa.stream = s;
   if ((e = scan_fwd_rows_launch(sa)) != hipSuccess) return e;
-  hipLaunchKernelGGL(ko, dim3((unsigned)chunks), dim3(WY_THREADS), lo, s, a, (const float*)Qt, (const float*)Ov,
-                     (const float*)S_all);
+  hipLaunchKernelGGL(ko, dim3((unsigned)chunks), dim3(WY_THREADS), lo, s, a, (const float*)c.Qt, (const float*)c.Ov,
+                     (const float*)c.S_all);
   return hipGetLastError();
+}
+
+// backward workspace (floats): gS, Sb (d x d per chunk), partial dq, dk
+// (B H T d), T, dT, dM (C x C per chunk), per-chunk gate partials (3 C + 4)
+size_t bwd_floats(int64_t B, int64_t H, int64_t T, int d) {
+  const int64_t chunks = B * H * (T / CB_C), mat = (int64_t)d * d, tok = B * H * T * (int64_t)d;
+  return (size_t)(2 * chunks * mat + 2 * tok + 3 * chunks * CB_C * CB_C + chunks * (3 * CB_C + 4));
+}
+
+template <int D>
+hipError_t launch_wy_bwd(const ChunkArgs& a, float* ckpt, const void* dO, void* dq, void* dk, void* dv, float* dbeta,
+                         float* dg, float* ws, hipStream_t s) {
+  using L = WyBwdLds<D>;
+  const int64_t chunks = a.B * a.H * a.N, mat = (int64_t)D * D, tok = a.B * a.H * a.T * (int64_t)D;
+  const Ckpt c = ckpt_of(ckpt, a.B, a.H, a.T, D);
+  WyBwd b{};
+  b.UA = c.UA;
+  b.KA = c.KA;
+  b.S_all = c.S_all;
+  b.Qt = c.Qt;
+  b.av = c.av;
+  b.dO = static_cast<const bf16*>(dO);
+  b.gS = ws;
+  float* Sb = ws + chunks * mat;
+  b.Sb = Sb;
+  b.dQp = Sb + chunks * mat;
+  b.dKp = b.dQp + tok;
+  b.Tp = b.dKp + tok;
+  b.dTp = b.Tp + chunks * CB_C * CB_C;
+  b.dMp = b.dTp + chunks * CB_C * CB_C;
+  b.tokp = b.dMp + chunks * CB_C * CB_C;
+  b.dq = static_cast<bf16*>(dq);
+  b.dk = static_cast<bf16*>(dk);
+  b.dv = static_cast<bf16*>(dv);
+  b.dbeta = dbeta;
+  b.dg = dg;
+  hipError_t e = launch_k(wy_gs<D>, 2 * CB_C * (D + 4) * 4, chunks, s, a, b);
+  if (e != hipSuccess) return e;
+  // the delta scan's reverse kernel: dU_i = dL/dS_{i+1} (its dK and da are not needed)
+  ScanArgs sa{};
+  sa.U = c.UA;
+  sa.K = c.KA;
+  sa.a = c.av;
+  sa.S_all = c.S_all;
+  sa.gS = b.gS;
+  sa.dU = Sb;
+  sa.BH = a.B * a.H;
+  sa.N = a.N;
+  sa.dh = D;
+  sa.rule = 0;
+  sa.ns = 0;
+  sa.precision = GMDN_PREC_IEEE;
+  sa.stream = s;
+  if ((e = scan_bwd_rows_launch(sa, nullptr)) != hipSuccess) return e;
+  if ((e = launch_k(wy_tok1<D>, L::TOK1_BYTES, chunks, s, a, b)) != hipSuccess) return e;
+  return launch_k(wy_tok2<D>, L::TOK2_BYTES, chunks, s, a, b);
 }
 
 }  // namespace
 
 size_t wy_workspace_floats(int64_t B, int64_t H, int64_t T, int d) {
-  const int64_t chunks = B * H * (T / CB_C), mat = (int64_t)d * d, tok = B * H * T * (int64_t)d;
-  return (size_t)(3 * chunks * mat + 2 * tok + chunks);
+  return d == 128 ? ckpt_floats<128>(B, H, T) : ckpt_floats<64>(B, H, T);
 }
 
 hipError_t wy_fwd_launch(const ChunkArgs& a, int d, float* ws, hipStream_t s) {
   if (d == 128) return launch_wy<128>(a, ws, s);
   if (d == 64) return launch_wy<64>(a, ws, s);
+  return hipErrorInvalidValue;
+}
+
+size_t wy_bwd_workspace_floats(int64_t B, int64_t H, int64_t T, int d) { return bwd_floats(B, H, T, d); }
+
+hipError_t wy_bwd_launch(const ChunkArgs& a, int d, float* ckpt, const void* dO, void* dq, void* dk, void* dv,
+                         float* dbeta, float* dg, float* ws, hipStream_t s) {
+  if (d == 128) return launch_wy_bwd<128>(a, ckpt, dO, dq, dk, dv, dbeta, dg, ws, s);
+  if (d == 64) return launch_wy_bwd<64>(a, ckpt, dO, dq, dk, dv, dbeta, dg, ws, s);
   return hipErrorInvalidValue;
 }
 

@@ -55,6 +55,8 @@ SIGNATURES = {
     "gmdn_chunk_bwd_workspace_bytes": (c_size, [ctypes.POINTER(ChunkDesc)]),
     "gmdn_wy_fwd_workspace_bytes": (c_size, [ctypes.POINTER(ChunkDesc)]),
     "gmdn_wy_fwd": (c_i32, [ctypes.POINTER(ChunkDesc)] + [c_vp] * 7 + [c_size, c_vp]),
+    "gmdn_wy_bwd_workspace_bytes": (c_size, [ctypes.POINTER(ChunkDesc)]),
+    "gmdn_wy_bwd": (c_i32, [ctypes.POINTER(ChunkDesc)] + [c_vp] * 13 + [c_size, c_vp]),
     "gmdn_chunk_bwd": (c_i32, [ctypes.POINTER(ChunkDesc)] + [c_vp] * 17 + [c_size, c_vp]),
     # include/gmdn_front.h
     "gmdn_front_fwd": (c_i32, [c_vp] * 6 + [c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_vp]),

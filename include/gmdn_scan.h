@@ -194,6 +194,23 @@ int gmdn_wy_fwd(const gmdn_chunk_desc* desc, const void* q, const void* k, const
                 const float* beta, const float* g, void* o, void* workspace,
                 size_t workspace_bytes, void* stream);
 
+/* Backward of gmdn_wy_fwd (no counterpart in the reference, like the mode
+ * itself).  `ckpt` is the workspace of the forward call on the same inputs,
+ * kept unchanged since (the chunks' U_A, K_A, states S_i, Qt, Ov and decay a
+ * that the forward formed).  Given dO (bf16, strides desc->so), writes dq,
+ * dk, dv (bf16, strides desc->sq, sk, sv) and dbeta, dg (contiguous
+ * (B, H, T) float32): the reverse delta scan ('ieee') gives each chunk's
+ * state cotangent, then chunk-parallel kernels differentiate the WY/UT chunk
+ * algebra (T = (I + A)^-1, U, W, the decay masks) with exact float32
+ * products.  The workspace (gmdn_wy_bwd_workspace_bytes) holds gS and the
+ * state cotangents (d x d per chunk), partial dq, dk, and T, dT, dM
+ * (C x C per chunk). */
+size_t gmdn_wy_bwd_workspace_bytes(const gmdn_chunk_desc* desc);
+int gmdn_wy_bwd(const gmdn_chunk_desc* desc, const void* q, const void* k, const void* v,
+                const float* beta, const float* g, const void* ckpt, const void* dO,
+                void* dq, void* dk, void* dv, float* dbeta, float* dg, void* workspace,
+                size_t workspace_bytes, void* stream);
+
 /* Workspace bytes gmdn_chunk_bwd needs. */
 size_t gmdn_chunk_bwd_workspace_bytes(const gmdn_chunk_desc* desc);
 
