@@ -34,7 +34,9 @@ own roofline.  ``cpu_baseline`` times the CPU restatement of the reference matri
 sub-object per other configuration: the muon rule at B=2, H=16, T=8192,
 d=128, ns=5 and the adam rule at B=2, H=8, T=4096, d=64 (inference forward
 and forward + backward, their rooflines and a CPU baseline on a bounded
-sample), and the 12-layer LM's training step (tokens/s only).  The CPU
+sample), the exact WY/UT mode at the default workload's shape (inference
+forward and forward + backward, eager), and the 12-layer LM's training step
+(tokens/s only).  The CPU
 baselines use every CPU of the process's affinity, capped by
 OMP_NUM_THREADS when set, and report the host (lscpu model, sockets,
 physical cores, torch threads).
@@ -686,6 +688,53 @@ def config_leg(name: str, steps: int, warmup: int, cpu_budget: float | None, wit
     return leg
 
 
+def wy_leg(steps: int, warmup: int) -> dict:
+    """The exact WY/UT mode (``wy_scan``) at the headline shape B=4, H=16,
+    T=4096, d=128 (bf16 q, k, v): inference forward and forward + backward,
+    eager launches, HIP events on the launch stream.  Priced on the same
+    algorithmic bytes as the fused core (the op's inputs and outputs)."""
+    import torch
+    from gmdn_amd import wy
+    from gmdn_amd.workloads import WORKLOADS, make_inputs
+
+    w = WORKLOADS[DEFAULT_WORKLOAD]
+    dev = torch.device("cuda:0")
+    inp = make_inputs(w, seed=0, device=dev, with_grad_out=True)
+    xs = [inp[n].detach().requires_grad_(True) for n in ("q", "k", "v", "beta", "g")]
+    stream = torch.cuda.current_stream(dev)
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        evs = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(2)) for _ in range(steps)]
+        for e in evs:
+            e[0].record(stream)
+            fn()
+            e[1].record(stream)
+        torch.cuda.synchronize()
+        return statistics.mean(e[0].elapsed_time(e[1]) for e in evs)
+
+    def fwd():
+        with torch.no_grad():
+            wy.wy_scan(*xs)
+
+    def fwd_bwd():
+        o = wy.wy_scan(*xs)
+        torch.autograd.grad(o, xs, inp["dO"])
+
+    ms_f, ms_fb = timed(fwd), timed(fwd_bwd)
+    units = w.B * w.H * w.T
+    bf, bb = fwd_bytes_per_token_head(w) * units, (fwd_bytes_per_token_head(w) + bwd_bytes_per_token_head(w)) * units
+    return {"workload": "wy_" + DEFAULT_WORKLOAD, "B": w.B, "H": w.H, "T": w.T, "d": w.d,
+            "fwd_tokens_per_s": w.tokens / (ms_f * 1e-3), "fwd_bwd_tokens_per_s": w.tokens / (ms_fb * 1e-3),
+            "step_us": {"fwd_inference": ms_f * 1e3, "fwd_bwd": ms_fb * 1e3},
+            "hbm_frac_fwd": bf / (ms_f * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "hbm_frac_fwd_bwd": bb / (ms_fb * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "kernels": "wy_prep + scan_fwd_rows8<128,0> + wy_out; bwd: wy_gs + scan_bwd_rows8<128,0> + "
+                       "wy_tok1 + wy_tok2 (chunk algebra in exact fp32 MFMA, state products split-bf16)"}
+
+
 def main(argv=None):
     args = parse_args(argv)
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -768,6 +817,7 @@ def main(argv=None):
                                                  True, max_heads=2),
             "adam_b2_h8_t4096_d64": config_leg("adam_b2_h8_t4096_d64", args.steps, args.warmup, budget, True),
         }
+        line["configs"]["wy_" + DEFAULT_WORKLOAD] = wy_leg(min(args.steps, 10), min(max(args.warmup, 1), 5))
         lm = lm_line(args)
         line["configs"][LM_WORKLOAD] = {k: lm[k] for k in ("value", "unit", "ms_per_step", "config",
                                                            "train_step_tokens_per_s", "fwd_tokens_per_s",

@@ -22,12 +22,12 @@
 // Forward: wy_prep (one workgroup of 4 waves per (b, h, chunk)) forms a, U_A,
 // K_A, Qt and Ov with exact float32 MFMA (v_mfma_f32_16x16x4_f32) on float32
 // tiles in LDS, T by blocked forward substitution; the drop-in delta scan
-// kernels carry S ('ieee'); wy_out forms o = Qt S_i^T + Ov.  Its workspace
+// kernels carry S (split-bf16 state products); wy_out forms o = Qt S_i^T + Ov.  Its workspace
 // [U_A | K_A | S_all | Qt | Ov | a] is the backward's checkpoint.
 //
 // Backward, given dO:
 //   wy_gs     gS_i = dL/dS_i through o = dO^T Qt                 (chunk-parallel)
-//   the drop-in delta scan's reverse kernel ('ieee') on (U_A, K_A, a, S_all,
+//   the drop-in delta scan's reverse kernel (split-bf16) on (U_A, K_A, a, S_all,
 //             gS): its dU_i is Sb = dL/dS_{i+1}, the state cotangent after chunk i
 //   wy_tok1 / wy_tok2: the VJP of the chunk algebra in the X-form above, per
 //             chunk from S_i and Sb (chunk-parallel):
@@ -784,7 +784,9 @@ hipError_t launch_wy(const ChunkArgs& a, float* ws, hipStream_t s) {
   sa.dh = D;
   sa.rule = 0;
   sa.ns = 0;
-  sa.precision = GMDN_PREC_IEEE;  // exact float32 state products
+  // split-bf16 state products (about 2^-16 relative error each, far below
+  // the bf16 output's rounding): the 8-wave delta scan kernel
+  sa.precision = GMDN_PREC_TF32;
   sa.stream = s;
   if ((e = scan_fwd_rows_launch(sa)) != hipSuccess) return e;
   hipLaunchKernelGGL(ko, dim3((unsigned)chunks), dim3(WY_THREADS), lo, s, a, (const float*)c.Qt, (const float*)c.Ov,
@@ -841,7 +843,7 @@ hipError_t launch_wy_bwd(const ChunkArgs& a, float* ckpt, const void* dO, void* 
   sa.dh = D;
   sa.rule = 0;
   sa.ns = 0;
-  sa.precision = GMDN_PREC_IEEE;
+  sa.precision = GMDN_PREC_TF32;
   sa.stream = s;
   if ((e = scan_bwd_rows_launch(sa, nullptr)) != hipSuccess) return e;
   if ((e = launch_k(wy_tok1<D>, L::TOK1_BYTES, chunks, s, a, b)) != hipSuccess) return e;

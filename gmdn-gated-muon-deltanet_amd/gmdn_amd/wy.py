@@ -14,7 +14,8 @@ float32 beta, g (B, H, T).  Forward and backward are HIP:
   triangular inverse T = (I + A)^-1 and the products that reduce each chunk
   to the affine state update S' = a S + U_A - S K_A and the output
   o = Qt S^T + Ov, in exact float32 MFMA), the drop-in delta scan kernels
-  ('ieee') and an output kernel.  Its workspace is the backward's checkpoint.
+  (split-bf16 state products) and an output kernel.  Its workspace is the
+  backward's checkpoint.
 * backward (``gmdn_wy_bwd``): dL/dS_i through o, the drop-in delta scan's
   reverse kernel for the state cotangents, then chunk-parallel kernels that
   differentiate the chunk algebra (T, U, W, the decay masks) back to q, k,

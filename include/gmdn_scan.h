@@ -186,7 +186,8 @@ int gmdn_chunk_fwd(const gmdn_chunk_desc* desc, const void* q, const void* k,
  *   S_t = alpha_t S_{t-1} (I - beta_t k_t k_t^T) + beta_t v_t k_t^T,  o_t = S_t q_t,
  * alpha_t = exp(max(g_t, log 1e-6)), chunked by the WY/UT transform
  * (T = (I + strict_lower(diag(beta) (K K^T * Gamma)))^-1, U = T diag(beta) V,
- * W = T diag(beta gamma) K) with exact float32 products.  desc->rule, ns and
+ * W = T diag(beta gamma) K) with exact float32 chunk products and split-bf16
+ * state products.  desc->rule, ns and
  * eps are ignored; q, k, v, o bf16 (desc->dtype GMDN_DTYPE_BF16) with the
  * strides of desc. */
 size_t gmdn_wy_fwd_workspace_bytes(const gmdn_chunk_desc* desc);
@@ -199,7 +200,7 @@ int gmdn_wy_fwd(const gmdn_chunk_desc* desc, const void* q, const void* k, const
  * kept unchanged since (the chunks' U_A, K_A, states S_i, Qt, Ov and decay a
  * that the forward formed).  Given dO (bf16, strides desc->so), writes dq,
  * dk, dv (bf16, strides desc->sq, sk, sv) and dbeta, dg (contiguous
- * (B, H, T) float32): the reverse delta scan ('ieee') gives each chunk's
+ * (B, H, T) float32): the reverse delta scan (split-bf16) gives each chunk's
  * state cotangent, then chunk-parallel kernels differentiate the WY/UT chunk
  * algebra (T = (I + A)^-1, U, W, the decay masks) with exact float32
  * products.  The workspace (gmdn_wy_bwd_workspace_bytes) holds gS and the
