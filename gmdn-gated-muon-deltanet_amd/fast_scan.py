@@ -28,6 +28,11 @@ Differences from the reference, on purpose:
   the kernels cover 32, 64 and 128, and 16 by zero-padding to 32.
 * gfx950 has no TF32 MFMA; 'tf32' maps to bf16x3 split products (more
   accurate than TF32) and 'ieee' to fp32 MFMA.
+* Adam (rule 2) run with gradients enabled takes 'ieee' for its forward
+  whatever ``set_precision`` says: its backward amplifies the rounding of
+  the saved moments past the gradient tolerance under split products.  So
+  under 'tf32' its S_all with grad enabled can differ in the last bits from
+  the same call without grad.
 * Gradients of gates the rule does not use are zeros (the reference's Triton
   backward leaves them uninitialised, reference :387-389).
 """

@@ -9,12 +9,14 @@ Usage, after ``rocprofv3 ... --output-format csv -d DIR -o NAME -- <program>``:
 
     python -m gmdn_amd.profiling mfma DIR [--kernel REGEX] [--simds 1024]
 
-``mfma`` reads one PMC pass of SQ_INSTS_VALU_MFMA_MOPS_BF16,
-SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE and gives per kernel (medians
-over its dispatches): the bf16 MFMA flops issued (MOPS x 512), their rate
-over the dispatch's own duration, that rate as a fraction of the 2.5 PFLOP/s
-dense bf16 peak, and MfmaUtil = busy cycles / (one XCD's GUI-active cycles
-x SIMDs), rocprofv3's own definition.
+``mfma`` reads one PMC pass of SQ_INSTS_VALU_MFMA_MOPS_BF16 (and, when
+collected, SQ_INSTS_VALU_MFMA_MOPS_F32), SQ_VALU_MFMA_BUSY_CYCLES and
+GRBM_GUI_ACTIVE and gives per kernel (medians over its dispatches): the bf16
+MFMA flops issued (MOPS x 512), their rate over the dispatch's own duration,
+that rate as a fraction of the 2.5 PFLOP/s dense bf16 peak, the fp32 MFMA
+flops and their fraction of the 157.3 TFLOP/s fp32 peak, and MfmaUtil =
+busy cycles / (one XCD's GUI-active cycles x SIMDs), rocprofv3's own
+definition.
 
 ``traffic`` turns the FETCH_SIZE / WRITE_SIZE derived counters (KiB per
 dispatch) into HBM bytes per launch of the kernels matching REGEX (summed
@@ -133,6 +135,7 @@ def read_traffic(path: str):
 
 
 BF16_PEAK_TFLOPS = 2500.0
+F32_PEAK_TFLOPS = 157.3
 
 
 def mfma_by_kernel(d: str, kernel_regex: str = "", simds: int = 1024, xcds: int = 8):
@@ -155,22 +158,26 @@ def mfma_by_kernel(d: str, kernel_regex: str = "", simds: int = 1024, xcds: int 
     out = {}
     for name, es in per.items():
         flops = statistics.median(e.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0.0) * 512 for e in es)
+        f32 = statistics.median(e.get("SQ_INSTS_VALU_MFMA_MOPS_F32", 0.0) * 512 for e in es)
         ns = statistics.median(e["ns"] for e in es)
         busy = statistics.median(e.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) for e in es)
         gui = statistics.median(e.get("GRBM_GUI_ACTIVE", 0.0) for e in es)
         tflops = flops / ns / 1e3 if ns else 0.0
+        f32_tflops = f32 / ns / 1e3 if ns else 0.0
         out[name] = {"dispatches": len(es), "flops": flops, "us": ns / 1e3, "tflops": tflops,
-                     "frac": tflops / BF16_PEAK_TFLOPS,
+                     "frac": tflops / BF16_PEAK_TFLOPS, "f32_flops": f32, "f32_frac": f32_tflops / F32_PEAK_TFLOPS,
                      "util": 100.0 * busy / (gui / xcds * simds) if gui else 0.0}
     return out
 
 
 def _mfma_md(d: str, kernel_regex: str, simds: int, xcds: int) -> str:
-    rows = ["| kernel | dispatches | bf16 MFMA GFLOP issued | us | TFLOP/s | of bf16 peak | MfmaUtil % |",
-            "|---|---|---|---|---|---|---|"]
-    for name, m in sorted(mfma_by_kernel(d, kernel_regex, simds, xcds).items(), key=lambda kv: -kv[1]["flops"]):
+    rows = ["| kernel | dispatches | bf16 MFMA GFLOP issued | us | TFLOP/s | of bf16 peak | fp32 MFMA GFLOP | "
+            "of fp32 peak | MfmaUtil % |",
+            "|---|---|---|---|---|---|---|---|---|"]
+    for name, m in sorted(mfma_by_kernel(d, kernel_regex, simds, xcds).items(),
+                          key=lambda kv: -(kv[1]["flops"] + kv[1]["f32_flops"])):
         rows.append(f"| `{name}` | {m['dispatches']} | {m['flops'] / 1e9:.2f} | {m['us']:.1f} | {m['tflops']:.1f} | "
-                    f"{m['frac']:.3f} | {m['util']:.1f} |")
+                    f"{m['frac']:.3f} | {m['f32_flops'] / 1e9:.2f} | {m['f32_frac']:.3f} | {m['util']:.1f} |")
     return "\n".join(rows)
 
 

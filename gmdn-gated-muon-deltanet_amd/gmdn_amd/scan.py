@@ -56,6 +56,17 @@ def _prec_code_of(precision: str) -> int:
     return nat.PREC_TF32 if precision == "tf32" else nat.PREC_IEEE
 
 
+def _effective_prec(rule: int, save: bool, prec: int) -> int:
+    """The product precision a forward actually runs in: adam keeping its
+    moments for a backward runs in exact float32 ('ieee') whatever the
+    setting, since its backward amplifies the rounding of the saved moments
+    (split-bf16 products there put dK 0.29 from float64, in Frobenius norm,
+    at BH = 64, N = 64, dh = 128, where float32 gives 3e-3).  The library
+    applies the same rule (gmdn_scan_fwd); stating it here makes the choice
+    visible at the Python boundary."""
+    return nat.PREC_IEEE if (rule == 2 and save) else prec
+
+
 def _check_inputs(U, K, a, b, m, n, rule, ns):
     if not (U.is_cuda and K.is_cuda):
         raise RuntimeError("HIP scan needs GPU tensors")
@@ -87,7 +98,7 @@ def hip_state_scan(U, K, a, b, m, n, rule: int, ns: int, precision: str | None =
     kd = _padded_dh(dh)
     ins = [_f32(t) for t in (_pad_sq(U, kd), _pad_sq(K, kd), a, b, m, n)]
     save = torch.is_grad_enabled() and any(t.requires_grad for t in (U, K, a, b, m, n))
-    prec = _prec_code() if precision is None else _prec_code_of(precision)
+    prec = _effective_prec(rule, save, _prec_code() if precision is None else _prec_code_of(precision))
     S_all, _, _ = torch.ops.gmdn.state_scan(*ins, rule, ns, prec, save)
     if kd != dh:
         S_all = S_all[..., :dh, :dh]
@@ -103,8 +114,9 @@ class HipScan(torch.autograd.Function):
         dh = U.shape[-1]
         kd = _padded_dh(dh)
         ins = [_f32(t.detach()) for t in (_pad_sq(U, kd), _pad_sq(K, kd), a, b, m, n)]
-        prec = _prec_code()
-        S_all, M_all, V_all = torch.ops.gmdn.state_scan(*ins, rule, ns, prec, any(ctx.needs_input_grad[:6]))
+        save = any(ctx.needs_input_grad[:6])
+        prec = _effective_prec(rule, save, _prec_code())
+        S_all, M_all, V_all = torch.ops.gmdn.state_scan(*ins, rule, ns, prec, save)
         ctx.save_for_backward(*ins, S_all, M_all, V_all)
         ctx.rule, ctx.ns, ctx.prec, ctx.dh = rule, ns, prec, dh
         ctx.dtypes = tuple(t.dtype for t in (U, K, a, b, m, n))
