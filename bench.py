@@ -41,6 +41,11 @@ baselines use every CPU of the process's affinity, capped by
 OMP_NUM_THREADS when set, and report the host (lscpu model, sockets,
 physical cores, torch threads).
 
+``measured_peaks`` (default workload, with ``configs``) gives what the GPU
+sustains beside the datasheet peaks the rooflines are priced on: the HBM
+bandwidth of a 2 GiB device copy and the bf16 throughput of an 8192^3
+torch.matmul.
+
 ``--workload lm_b8_t2048_muon`` times the 12-layer LM stack around the
 fused core end to end (forward + backward, tokens/s only).
 ``--workload outer_muon_lm12_d1024`` times one outer Muon optimizer step
@@ -421,6 +426,45 @@ def copy_calibration(nbytes: int) -> None:
         torch.mul(src, 1.0, out=dst)
     torch.cuda.synchronize()
     print(json.dumps({"copy_calibration_bytes": nbytes}))
+
+
+def measured_peaks(steps: int = 10) -> dict:
+    """What this GPU sustains beside the datasheet peaks the rooflines use:
+    HBM bandwidth of a device copy of 2 GiB (torch's elementwise copy: 2 GiB
+    read + 2 GiB written per call) and dense bf16 MFMA throughput of an
+    8192 x 8192 x 8192 torch.matmul (hipBLASLt), HIP events around each."""
+    import torch
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        evs = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(2)) for _ in range(steps)]
+        for e in evs:
+            e[0].record(stream)
+            fn()
+            e[1].record(stream)
+        torch.cuda.synchronize()
+        return statistics.median(e[0].elapsed_time(e[1]) for e in evs)
+
+    n = 1 << 29  # float32 elements: 2 GiB
+    src = torch.ones(n, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    ms_copy = timed(lambda: dst.copy_(src))
+    del src, dst
+    m = 8192
+    a = torch.randn(m, m, device=dev, dtype=torch.bfloat16)
+    b = torch.randn(m, m, device=dev, dtype=torch.bfloat16)
+    ms_mm = timed(lambda: torch.matmul(a, b))
+    del a, b
+    hbm = 2 * n * 4 / (ms_copy * 1e-3) / 1e9
+    tf = 2 * m ** 3 / (ms_mm * 1e-3) / 1e12
+    return {"hbm_copy_GBs": hbm, "hbm_datasheet_GBs": HBM_PEAK_GBS, "hbm_measured_frac": hbm / HBM_PEAK_GBS,
+            "bf16_matmul_TFLOPs": tf, "bf16_datasheet_TFLOPs": BF16_PEAK_TFLOPS,
+            "bf16_measured_frac": tf / BF16_PEAK_TFLOPS,
+            "how": "2 GiB device copy (read + write) and an 8192^3 bf16 torch.matmul, medians of HIP events"}
 
 
 def cpu_info() -> dict:
@@ -818,6 +862,7 @@ def main(argv=None):
             "adam_b2_h8_t4096_d64": config_leg("adam_b2_h8_t4096_d64", args.steps, args.warmup, budget, True),
         }
         line["configs"]["wy_" + DEFAULT_WORKLOAD] = wy_leg(min(args.steps, 10), min(max(args.warmup, 1), 5))
+        line["measured_peaks"] = measured_peaks()
         lm = lm_line(args)
         line["configs"][LM_WORKLOAD] = {k: lm[k] for k in ("value", "unit", "ms_per_step", "config",
                                                            "train_step_tokens_per_s", "fwd_tokens_per_s",
