@@ -19,11 +19,12 @@
 // and the output is o = Qt S^T + Ov with
 //     Qt = diag(gamma) Q - (M T diag(beta gamma)) K,  Ov = (M T diag(beta)) V.
 //
-// Forward: wy_prep (one workgroup of 4 waves per (b, h, chunk)) forms a, U_A,
-// K_A, Qt and Ov with exact float32 MFMA (v_mfma_f32_16x16x4_f32) on float32
-// tiles in LDS, T by blocked forward substitution; the drop-in delta scan
-// kernels carry S (split-bf16 state products); wy_out forms o = Qt S_i^T + Ov.  Its workspace
-// [U_A | K_A | S_all | Qt | Ov | a] is the backward's checkpoint.
+// Forward: wy_prep (one workgroup of 8 waves per (b, h, chunk)) forms a, U_A,
+// K_A, Qt and Ov: bf16 q, k, v enter the products exactly, float32
+// intermediates as split hi + lo bf16 operands; T by blocked forward
+// substitution in float32.  The drop-in delta scan kernels carry S
+// (split-bf16 state products); wy_out forms o = Qt S_i^T + Ov (split-bf16).
+// Its workspace [U_A | K_A | S_all | Qt | Ov | a] is the backward's checkpoint.
 //
 // Backward, given dO:
 //   wy_gs     gS_i = dL/dS_i through o = dO^T Qt                 (chunk-parallel)
@@ -52,20 +53,6 @@ namespace {
 
 constexpr int WY_THREADS = 256;
 
-template <int D>
-struct WyLds {
-  static constexpr int LDT = D + 4;   // float stride of a token tile row
-  static constexpr int LDC = CB_C + 4;  // float stride of a C x C matrix row
-  static constexpr int TILE = CB_C * LDT;   // floats
-  static constexpr int CC = CB_C * LDC;     // floats
-  static constexpr int K0 = 0, V0 = TILE, Q0 = 2 * TILE;   // Q's slot later holds P
-  static constexpr int T0 = 3 * TILE, A0 = T0 + CC;          // A's slot later holds M, then M T
-  static constexpr int X0 = A0 + CC;                         // 3 waves x 16 x 16 scratch
-  static constexpr int S0 = X0 + 3 * 256;  // beta, gamma, beta gamma, kd, log gamma
-  static constexpr int FLOATS = S0 + 5 * CB_C;
-  static_assert(FLOATS * 4 <= 160 * 1024, "WY prep LDS exceeds the 160 KiB of a CU");
-};
-
 // Per-token gate quantities of the chunk (wave 0, lane = token): beta, gamma,
 // beta gamma, kd = gamma_C / gamma and log gamma (the prefix sums of the
 // clamped log-gates) into LDS; returns gamma of this lane's token.
@@ -88,12 +75,13 @@ GMDN_DEV float wy_gates(const float* beta, const float* g, int64_t e, float* bet
 // which must be zero on entry.  The four 16 x 16 diagonal blocks by forward
 // substitution (wave w, lane j < 16 holds column j of block w), then the
 // off-diagonal blocks T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj level by level
-// (d = i - j; wave w takes the block with j = w).  Xw: 3 x 256 floats of
-// scratch.  Ends with a barrier.
+// (d = i - j; wave w takes the block with j = w).  Waves 0-3 work; any
+// further waves of the workgroup only take part in the barriers.  Xw: 3 x 256
+// floats of scratch.  Ends with a barrier.
 template <int LDC>
 GMDN_DEV void tri_inverse(const float* As, float* Ts, float* Xw_all) {
   const int w = wave_id(), l = lane_id();
-  if (l < 16) {
+  if (w < 4 && l < 16) {
     const int o = 16 * w;
     float x[16];
 #pragma unroll
@@ -140,19 +128,67 @@ GMDN_DEV void tri_inverse(const float* As, float* Ts, float* Xw_all) {
 }
 
 // ------------------------------------------------------------------ forward
+// wy_prep: one workgroup of 8 waves per (b, h, chunk).  q, k, v stay bf16 in
+// LDS (row swizzle BSwz) and enter the products exactly; A, T, M and the
+// decays are float32, and every float32 operand of a product is split into
+// hi + lo bf16 (three MFMAs for two split operands, two for one: about
+// 2^-16 relative error per product).
+//   A  = strict_lower(diag(beta)(K K^T * Gamma))     float32 tiles, for T
+//   T  = (I + A)^-1                                 forward substitution (float32)
+//   M  = lower_incl(Q K^T * Gamma)                  split planes, rows t
+//   (M T)^T tiles [u][t], scaled by beta gamma_u (Qt) or beta_u (Ov) per
+//       row, are directly the pair-order operand of the next product:
+//   Qt = diag(gamma) Q - (M T diag(beta gamma)) K,  Ov = (M T diag(beta)) V
+//   P  = T^T diag(kd) K, tiles [s][c], scaled by beta_s / beta gamma_s:
+//   U_A = V^T (diag(beta) P),  K_A = K^T (diag(beta gamma) P)
+// (the same algebra, with diag(beta) moved onto P.)
+constexpr int WYP_THREADS = 512;
+
 template <int D>
-__global__ void __launch_bounds__(WY_THREADS)
+struct WyPrepLds {
+  static constexpr int C = CB_C;
+  static constexpr int TB = C * D * 2;    // bf16 token tile (bytes)
+  static constexpr int CP = C * C * 2;    // one bf16 C x C plane
+  static constexpr int LDC = C + 4;       // float stride of A and T rows
+  static constexpr int CF = C * LDC * 4;  // float C x C
+  static constexpr int K0 = 0, Q0 = TB, V0 = 2 * TB;
+  static constexpr int A0 = 3 * TB, T0 = A0 + CF;
+  static constexpr int X0 = T0 + CF;  // tri_inverse scratch, 3 x 256 floats
+  // split planes (hi, lo) of T, diag(kd) T and M
+  static constexpr int TH0 = X0 + 3 * 1024, TL0 = TH0 + CP, KH0 = TL0 + CP, KL0 = KH0 + CP, MH0 = KL0 + CP,
+                       ML0 = MH0 + CP;
+  static constexpr int R0 = ML0 + CP;  // beta, gamma, beta gamma, kd, log gamma
+  static constexpr int BYTES = R0 + 5 * C * 4;
+  static_assert(BYTES <= 160 * 1024, "WY prep LDS exceeds the 160 KiB of a CU");
+};
+
+// the causal 16 x 16 tiles (row tile >= column tile) of a C x C matrix
+GMDN_DEV void causal_tile(int idx, int& tt, int& st) {
+  tt = idx < 1 ? 0 : idx < 3 ? 1 : idx < 6 ? 2 : 3;
+  st = idx - tt * (tt + 1) / 2;
+}
+
+template <int D>
+__global__ void __launch_bounds__(WYP_THREADS)
 wy_prep(ChunkArgs p, float* __restrict__ UA, float* __restrict__ KA, float* __restrict__ Qt,
         float* __restrict__ Ov, float* __restrict__ aout) {
-  using L = WyLds<D>;
-  constexpr int C = CB_C, LDT = L::LDT, LDC = L::LDC, NT = D / 16;
-  extern __shared__ __align__(16) float sm[];
-  float* Ks = sm + L::K0;
-  float* Vs = sm + L::V0;
-  float* Qs = sm + L::Q0;
-  float* Ts = sm + L::T0;
-  float* As = sm + L::A0;
-  float* bet = sm + L::S0;
+  using L = WyPrepLds<D>;
+  using LT = BSwz<D>;      // token tiles
+  using LP = BSwz<CB_C>;   // C x C planes
+  constexpr int C = CB_C, LDC = L::LDC, NT = D / 16, NKB = D / 32;
+  extern __shared__ __align__(16) char smem[];
+  bf16* Kb = reinterpret_cast<bf16*>(smem + L::K0);
+  bf16* Qb = reinterpret_cast<bf16*>(smem + L::Q0);
+  bf16* Vb = reinterpret_cast<bf16*>(smem + L::V0);
+  float* As = reinterpret_cast<float*>(smem + L::A0);
+  float* Ts = reinterpret_cast<float*>(smem + L::T0);
+  bf16* Th = reinterpret_cast<bf16*>(smem + L::TH0);
+  bf16* Tl = reinterpret_cast<bf16*>(smem + L::TL0);
+  bf16* KTh = reinterpret_cast<bf16*>(smem + L::KH0);
+  bf16* KTl = reinterpret_cast<bf16*>(smem + L::KL0);
+  bf16* Mh = reinterpret_cast<bf16*>(smem + L::MH0);
+  bf16* Ml = reinterpret_cast<bf16*>(smem + L::ML0);
+  float* bet = reinterpret_cast<float*>(smem + L::R0);
   float* gam = bet + C;
   float* bg = gam + C;
   float* kd = bg + C;
@@ -161,158 +197,209 @@ wy_prep(ChunkArgs p, float* __restrict__ UA, float* __restrict__ KA, float* __re
   const int64_t bh = blockIdx.x / p.N;
   const int i = (int)(blockIdx.x % p.N);
   const int64_t bb = bh / p.H, hh = bh % p.H, t0 = (int64_t)i * C;
-  const int w = wave_id(), l = lane_id();
+  const int w = wave_id(), l = lane_id(), lc = l & 15, G = l >> 4;
 
-  // ---- tiles as float32, gates, zeroed T
+  // ---- bf16 tiles, gates; T and the M planes zeroed
   const bf16* qg = p.q + bb * p.sq[0] + hh * p.sq[1] + t0 * p.sq[2];
   const bf16* kg = p.k + bb * p.sk[0] + hh * p.sk[1] + t0 * p.sk[2];
   const bf16* vg = p.v + bb * p.sv[0] + hh * p.sv[1] + t0 * p.sv[2];
-  for (int e = threadIdx.x; e < C * D / 8; e += WY_THREADS) {
+  for (int e = threadIdx.x; e < C * D / 8; e += WYP_THREADS) {
     const int t = e / (D / 8), c = (e % (D / 8)) * 8;
-    const bf16x8 kq = *reinterpret_cast<const bf16x8*>(kg + t * p.sk[2] + c);
-    const bf16x8 vq = *reinterpret_cast<const bf16x8*>(vg + t * p.sv[2] + c);
-    const bf16x8 qq = *reinterpret_cast<const bf16x8*>(qg + t * p.sq[2] + c);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      Ks[t * LDT + c + j] = (float)kq[j];
-      Vs[t * LDT + c + j] = (float)vq[j];
-      Qs[t * LDT + c + j] = (float)qq[j];
-    }
+    *reinterpret_cast<bf16x8*>(Kb + LT::off(t, c)) = *reinterpret_cast<const bf16x8*>(kg + t * p.sk[2] + c);
+    *reinterpret_cast<bf16x8*>(Qb + LT::off(t, c)) = *reinterpret_cast<const bf16x8*>(qg + t * p.sq[2] + c);
+    *reinterpret_cast<bf16x8*>(Vb + LT::off(t, c)) = *reinterpret_cast<const bf16x8*>(vg + t * p.sv[2] + c);
   }
-  for (int e = threadIdx.x; e < C * LDC; e += WY_THREADS) Ts[e] = 0.f;
+  for (int e = threadIdx.x; e < C * LDC / 4; e += WYP_THREADS) reinterpret_cast<f32x4*>(Ts)[e] = zero4();
+  for (int e = threadIdx.x; e < 2 * L::CP / 16; e += WYP_THREADS) reinterpret_cast<f32x4*>(Mh)[e] = zero4();
   if (w == 0) {
     const float g_ = wy_gates(p.beta, p.g, bh * p.T + t0 + l, bet, gam, bg, kd, lgam);
     if (l == 63) aout[bh * p.N + i] = g_;
   }
   __syncthreads();
 
-  // ---- A = strict_lower(diag(beta) (K K^T * Gamma)): causal tiles by wave
-  for (int tile = w; tile < 16; tile += 4) {
-    const int tt = tile >> 2, st = tile & 3;
-    f32x4 acc = zero4();
-    if (st <= tt) {
-      acc = mm16<D>([&](int ii, int k) { return Ks[(16 * tt + ii) * LDT + k]; },
-                    [&](int k, int ii) { return Ks[(16 * st + ii) * LDT + k]; }, acc);
-      const int c = l & 15, G = l >> 4, s = 16 * st + c;
+  // ---- A's causal tiles (float32, for the substitution) and M's (split
+  //      planes): jobs 0-9 and 10-19 over the waves
+  for (int job = w; job < 20; job += WYP_THREADS / 64) {
+    int tt, st;
+    causal_tile(job % 10, tt, st);
+    if (job < 10) {
+      // A[t][s] = beta_t Gamma[t][s] sum_c K[t][c] K[s][c]
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb)
+        acc = mfma(row8<LT>(Kb, 16 * tt + lc, 32 * kb), row8<LT>(Kb, 16 * st + lc, 32 * kb), acc);
+      const int s = 16 * st + lc;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int t = 16 * tt + 4 * G + j;
         acc[j] = s < t ? bet[t] * acc[j] * expf(lgam[t] - lgam[s]) : 0.f;
       }
+      st_tile(As, LDC, 16 * tt, 16 * st, acc);
+    } else {
+      // M^T[s][t] = Gamma[t][s] sum_c K[s][c] Q[t][c], stored as rows t of M
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb)
+        acc = mfma(row8<LT>(Kb, 16 * st + lc, 32 * kb), row8<LT>(Qb, 16 * tt + lc, 32 * kb), acc);
+      const int t = 16 * tt + lc;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int s = 16 * st + 4 * G + j;
+        acc[j] = s <= t ? acc[j] * expf(lgam[t] - lgam[s]) : 0.f;
+      }
+      bf16x4 h, o;
+      split4(acc, h, o);
+      *reinterpret_cast<bf16x4*>(Mh + LP::off(t, 16 * st + 4 * G)) = h;
+      *reinterpret_cast<bf16x4*>(Ml + LP::off(t, 16 * st + 4 * G)) = o;
     }
-    st_tile(As, LDC, 16 * tt, 16 * st, acc);
   }
   __syncthreads();
-  tri_inverse<LDC>(As, Ts, sm + L::X0);
+  tri_inverse<LDC>(As, Ts, reinterpret_cast<float*>(smem + L::X0));
 
-  // ---- M = lower_incl(Q K^T * Gamma) into A's slot, then M T in place
-  for (int tile = w; tile < 16; tile += 4) {
-    const int tt = tile >> 2, st = tile & 3;
-    f32x4 acc = zero4();
-    if (st <= tt) {
-      acc = mm16<D>([&](int ii, int k) { return Qs[(16 * tt + ii) * LDT + k]; },
-                    [&](int k, int ii) { return Ks[(16 * st + ii) * LDT + k]; }, acc);
-      const int c = l & 15, G = l >> 4, s = 16 * st + c;
+  // ---- split planes of T and diag(kd) T (one 8-column group per thread)
+  {
+    const int r = threadIdx.x >> 3, c = (threadIdx.x & 7) * 8;
+    const f32x4 x0 = *reinterpret_cast<const f32x4*>(Ts + r * LDC + c);
+    const f32x4 x1 = *reinterpret_cast<const f32x4*>(Ts + r * LDC + c + 4);
+    bf16x4 h0, o0, h1, o1;
+    split4(x0, h0, o0);
+    split4(x1, h1, o1);
+    *reinterpret_cast<bf16x8*>(Th + LP::off(r, c)) = cat8(h0, h1);
+    *reinterpret_cast<bf16x8*>(Tl + LP::off(r, c)) = cat8(o0, o1);
+    const float k_ = kd[r];
+    split4(k_ * x0, h0, o0);
+    split4(k_ * x1, h1, o1);
+    *reinterpret_cast<bf16x8*>(KTh + LP::off(r, c)) = cat8(h0, h1);
+    *reinterpret_cast<bf16x8*>(KTl + LP::off(r, c)) = cat8(o0, o1);
+  }
+  __syncthreads();
+
+  const int64_t tokbase = (bh * p.T + t0) * (int64_t)D;
+  // ---- Qt (waves 0-3) or Ov (waves 4-7) of token tile tt
+  {
+    const bool ov = w >= 4;
+    const int tt = w & 3;
+    // (M T)^T[u][t] = sum_s T[s][u] M[t][s], causal (u <= t)
+    f32x4 mt[4];
+#pragma unroll
+    for (int ut = 0; ut < 4; ++ut) {
+      mt[ut] = zero4();
+      if (ut <= tt) {
+        for (int kb = ut >> 1; kb <= (tt >> 1); ++kb)
+          mt[ut] = mma<2, 2>(Op<2>{{col8<LP>(Th, 32 * kb, 16 * ut), col8<LP>(Tl, 32 * kb, 16 * ut)}},
+                             Op<2>{{row8<LP>(Mh, 16 * tt + lc, 32 * kb), row8<LP>(Ml, 16 * tt + lc, 32 * kb)}},
+                             mt[ut]);
+        const float* sc = ov ? bet : bg;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) mt[ut][j] *= sc[16 * ut + 4 * G + j];
+      }
+    }
+    // pair order over u: the operand's free index is t
+    const Op<2> a0 = pack_tiles<2>(mt[0], mt[1]), a1 = pack_tiles<2>(mt[2], mt[3]);
+    const bf16* Bt = ov ? Vb : Kb;
+    float* out = (ov ? Ov : Qt) + tokbase;
+#pragma unroll 2
+    for (int tc = 0; tc < NT; ++tc) {
+      f32x4 acc = mma<2, 1>(a0, Op<1>{{b_col<LT>(Bt, 0, 16 * tc)}}, zero4());
+      if (tt >= 2) acc = mma<2, 1>(a1, Op<1>{{b_col<LT>(Bt, 32, 16 * tc)}}, acc);
+      const int c = 16 * tc + lc;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int t = 16 * tt + 4 * G + j;
-        acc[j] = s <= t ? acc[j] * expf(lgam[t] - lgam[s]) : 0.f;
+        out[(int64_t)t * D + c] = ov ? acc[j] : gam[t] * (float)Qb[LT::off(t, c)] - acc[j];
       }
     }
-    st_tile(As, LDC, 16 * tt, 16 * st, acc);
   }
-  __syncthreads();
-  {
-    f32x4 mt[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int tile = w + 4 * q, tt = tile >> 2, st = tile & 3;
-      mt[q] = zero4();
-      if (st <= tt)
-        mt[q] = mm16<CB_C>([&](int ii, int k) { return As[(16 * tt + ii) * LDC + k]; },
-                           [&](int k, int ii) { return Ts[k * LDC + 16 * st + ii]; }, mt[q]);
-    }
-    __syncthreads();  // every wave has read M
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int tile = w + 4 * q, tt = tile >> 2, st = tile & 3;
-      st_tile(As, LDC, 16 * tt, 16 * st, mt[q]);
-    }
-  }
-  __syncthreads();
 
-  // ---- Qt = diag(gamma) Q - (M T diag(beta gamma)) K and Ov = (M T diag(beta)) V
-  //      (float32, (B, H, T, d) contiguous); lane (c, G) of tile (tt, tc)
-  const int64_t tokbase = (bh * p.T + t0) * (int64_t)D;
-  for (int tile = w; tile < 4 * NT; tile += 4) {
-    const int tt = tile / NT, tc = tile % NT;
-    f32x4 qa = mm16<CB_C>([&](int ii, int k) { return As[(16 * tt + ii) * LDC + k] * bg[k]; },
-                          [&](int k, int ii) { return Ks[k * LDT + 16 * tc + ii]; }, zero4());
-    f32x4 oa = mm16<CB_C>([&](int ii, int k) { return As[(16 * tt + ii) * LDC + k] * bet[k]; },
-                          [&](int k, int ii) { return Vs[k * LDT + 16 * tc + ii]; }, zero4());
-    const int c = l & 15, G = l >> 4;
+  // ---- P column tile ct, then U_A and K_A columns ct over the wave's row tiles
+  {
+    constexpr int WPC = (WYP_THREADS / 64) / NT;  // waves per column tile
+    const int ct = w % NT, part = w / NT;
+    f32x4 pt[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int t = 16 * tt + 4 * G + j, col = 16 * tc + c;
-      Qt[tokbase + (int64_t)t * D + col] = gam[t] * Qs[t * LDT + col] - qa[j];
-      Ov[tokbase + (int64_t)t * D + col] = oa[j];
+    for (int st = 0; st < 4; ++st) {
+      // P[s][c] = sum_t kd_t T[t][s] K[t][c], T[t][s] = 0 for t < s
+      pt[st] = zero4();
+      for (int kb = st >> 1; kb < 2; ++kb)
+        pt[st] = mma<2, 1>(Op<2>{{col8<LP>(KTh, 32 * kb, 16 * st), col8<LP>(KTl, 32 * kb, 16 * st)}},
+                           Op<1>{{col8<LT>(Kb, 32 * kb, 16 * ct)}}, pt[st]);
     }
-  }
-  __syncthreads();  // Q's slot is free: P = T^T diag(kd) K
-  float* Ps = Qs;
-  for (int tile = w; tile < 4 * NT; tile += 4) {
-    const int st = tile / NT, tc = tile % NT;
-    const f32x4 pa = mm16<CB_C>([&](int ii, int k) { return Ts[k * LDC + 16 * st + ii] * kd[k]; },
-                                [&](int k, int ii) { return Ks[k * LDT + 16 * tc + ii]; }, zero4());
-    st_tile(Ps, LDT, 16 * st, 16 * tc, pa);
-  }
-  __syncthreads();
-  // ---- U_A = (diag(beta) V)^T P, K_A = (diag(beta gamma) K)^T P  (d x d, float32)
-  const int64_t mbase = (bh * p.N + i) * (int64_t)D * D;
-  for (int tile = w; tile < NT * NT; tile += 4) {
-    const int tr = tile / NT, tc = tile % NT;
-    const f32x4 ua = mm16<CB_C>([&](int ii, int k) { return Vs[k * LDT + 16 * tr + ii] * bet[k]; },
-                                [&](int k, int ii) { return Ps[k * LDT + 16 * tc + ii]; }, zero4());
-    const f32x4 ka = mm16<CB_C>([&](int ii, int k) { return Ks[k * LDT + 16 * tr + ii] * bg[k]; },
-                                [&](int k, int ii) { return Ps[k * LDT + 16 * tc + ii]; }, zero4());
-    st_tile(UA + mbase, D, 16 * tr, 16 * tc, ua);
-    st_tile(KA + mbase, D, 16 * tr, 16 * tc, ka);
+    f32x4 pb[4], pg[4];
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int s = 16 * st + 4 * G + j;
+        pb[st][j] = bet[s] * pt[st][j];
+        pg[st][j] = bg[s] * pt[st][j];
+      }
+    const Op<2> bp[2] = {pack_tiles<2>(pb[0], pb[1]), pack_tiles<2>(pb[2], pb[3])};
+    const Op<2> bq[2] = {pack_tiles<2>(pg[0], pg[1]), pack_tiles<2>(pg[2], pg[3])};
+    const int64_t mbase = (bh * p.N + i) * (int64_t)D * D;
+    constexpr int RPW = NT / WPC;
+#pragma unroll 2
+    for (int rt = part * RPW; rt < (part + 1) * RPW; ++rt) {
+      f32x4 ua = zero4(), ka = zero4();
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        ua = mma<1, 2>(Op<1>{{b_col<LT>(Vb, 32 * kb, 16 * rt)}}, bp[kb], ua);
+        ka = mma<1, 2>(Op<1>{{b_col<LT>(Kb, 32 * kb, 16 * rt)}}, bq[kb], ka);
+      }
+      st_tile(UA + mbase, D, 16 * rt, 16 * ct, ua);
+      st_tile(KA + mbase, D, 16 * rt, 16 * ct, ka);
+    }
   }
 }
 
-// o = Qt S_i^T + Ov for one (b, h, chunk): Qt rows and S_i staged in LDS as float32
+// o = Qt S_i^T + Ov for one (b, h, chunk): S_i as split planes in LDS (rows r),
+// Qt rows of the wave's token tile split in registers
 template <int D>
 __global__ void __launch_bounds__(WY_THREADS)
 wy_out(ChunkArgs p, const float* __restrict__ Qt, const float* __restrict__ Ov, const float* __restrict__ Sst) {
-  constexpr int C = CB_C, LDT = D + 4, NT = D / 16;
-  extern __shared__ __align__(16) float sm[];
-  float* Qs = sm;             // C x D
-  float* Ss = sm + C * LDT;   // D x D
+  using LS = BSwz<D>;
+  constexpr int C = CB_C, NT = D / 16, NKB = D / 32;
+  extern __shared__ __align__(16) char smem[];
+  bf16* Sh = reinterpret_cast<bf16*>(smem);
+  bf16* Sl = Sh + D * D;
   const int64_t bh = blockIdx.x / p.N;
   const int i = (int)(blockIdx.x % p.N);
   const int64_t bb = bh / p.H, hh = bh % p.H, t0 = (int64_t)i * C;
-  const int w = wave_id(), l = lane_id();
+  const int w = wave_id(), l = lane_id(), lc = l & 15, G = l >> 4;
   const int64_t tokbase = (bh * p.T + t0) * (int64_t)D;
   const float* S = Sst + (bh * p.N + i) * (int64_t)D * D;
-  for (int e = threadIdx.x; e < C * D / 4; e += WY_THREADS) {
-    const int t = e / (D / 4), c = (e % (D / 4)) * 4;
-    *reinterpret_cast<f32x4*>(Qs + t * LDT + c) = *reinterpret_cast<const f32x4*>(Qt + tokbase + (int64_t)t * D + c);
+  for (int e = threadIdx.x; e < D * D / 8; e += WY_THREADS) {
+    const int r = e / (D / 8), c = (e % (D / 8)) * 8;
+    bf16x4 h0, o0, h1, o1;
+    split4(*reinterpret_cast<const f32x4*>(S + (int64_t)r * D + c), h0, o0);
+    split4(*reinterpret_cast<const f32x4*>(S + (int64_t)r * D + c + 4), h1, o1);
+    *reinterpret_cast<bf16x8*>(Sh + LS::off(r, c)) = cat8(h0, h1);
+    *reinterpret_cast<bf16x8*>(Sl + LS::off(r, c)) = cat8(o0, o1);
   }
-  for (int e = threadIdx.x; e < D * D / 4; e += WY_THREADS) {
-    const int r = e / (D / 4), c = (e % (D / 4)) * 4;
-    *reinterpret_cast<f32x4*>(Ss + r * LDT + c) = *reinterpret_cast<const f32x4*>(S + (int64_t)r * D + c);
+  // lane (t, G) of k-block kb: Qt[16 w + t][32 kb + 8G .. +7]
+  Op<2> qa[NKB];
+  {
+    const float* qr = Qt + tokbase + (int64_t)(16 * w + lc) * D + 8 * G;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      bf16x4 h0, o0, h1, o1;
+      split4(*reinterpret_cast<const f32x4*>(qr + 32 * kb), h0, o0);
+      split4(*reinterpret_cast<const f32x4*>(qr + 32 * kb + 4), h1, o1);
+      qa[kb] = Op<2>{{cat8(h0, h1), cat8(o0, o1)}};
+    }
   }
   __syncthreads();
   bf16* og = p.o + bb * p.so[0] + hh * p.so[1] + t0 * p.so[2];
-  for (int tile = w; tile < 4 * NT; tile += 4) {
-    const int tt = tile / NT, tr = tile % NT;
+#pragma unroll 2
+  for (int rt = 0; rt < NT; ++rt) {
     // tile [t][r] = sum_c Qt[t][c] S[r][c]
-    const f32x4 acc = mm16<D>([&](int ii, int k) { return Qs[(16 * tt + ii) * LDT + k]; },
-                              [&](int k, int ii) { return Ss[(16 * tr + ii) * LDT + k]; }, zero4());
-    const int c = l & 15, G = l >> 4;
+    f32x4 acc = zero4();
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+      acc = mma<2, 2>(qa[kb], Op<2>{{row8<LS>(Sh, 16 * rt + lc, 32 * kb), row8<LS>(Sl, 16 * rt + lc, 32 * kb)}}, acc);
+    const int r = 16 * rt + lc;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int t = 16 * tt + 4 * G + j, r = 16 * tr + c;
+      const int t = 16 * w + 4 * G + j;
       og[t * p.so[2] + r] = (bf16)(acc[j] + Ov[tokbase + (int64_t)t * D + r]);
     }
   }
@@ -768,11 +855,11 @@ hipError_t launch_wy(const ChunkArgs& a, float* ws, hipStream_t s) {
   const Ckpt c = ckpt_of(ws, a.B, a.H, a.T, D);
   auto kp = wy_prep<D>;
   auto ko = wy_out<D>;
-  const int lp = WyLds<D>::FLOATS * 4, lo = (CB_C + D) * (D + 4) * 4;
+  const int lp = WyPrepLds<D>::BYTES, lo = 2 * D * D * 2;
   hipError_t e = hipFuncSetAttribute((const void*)kp, hipFuncAttributeMaxDynamicSharedMemorySize, lp);
   if (e == hipSuccess) e = hipFuncSetAttribute((const void*)ko, hipFuncAttributeMaxDynamicSharedMemorySize, lo);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(kp, dim3((unsigned)chunks), dim3(WY_THREADS), lp, s, a, c.UA, c.KA, c.Qt, c.Ov, c.av);
+  hipLaunchKernelGGL(kp, dim3((unsigned)chunks), dim3(WYP_THREADS), lp, s, a, c.UA, c.KA, c.Qt, c.Ov, c.av);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   ScanArgs sa{};
   sa.U = c.UA;
