@@ -776,7 +776,8 @@ def wy_leg(steps: int, warmup: int) -> dict:
             "hbm_frac_fwd": bf / (ms_f * 1e-3) / 1e9 / HBM_PEAK_GBS,
             "hbm_frac_fwd_bwd": bb / (ms_fb * 1e-3) / 1e9 / HBM_PEAK_GBS,
             "kernels": "wy_prep + scan_fwd_rows8<128,0> + wy_out; bwd: wy_gs + scan_bwd_rows8<128,0> + "
-                       "wy_tok1 + wy_tok2 (chunk algebra in exact fp32 MFMA, state products split-bf16)"}
+                       "wy_ka + wy_kb + wy_kc1 + wy_kc2 (split-bf16 MFMA throughout; T by float32 "
+                       "forward substitution)"}
 
 
 def main(argv=None):

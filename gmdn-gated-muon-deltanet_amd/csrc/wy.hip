@@ -168,6 +168,71 @@ GMDN_DEV void causal_tile(int idx, int& tt, int& st) {
   st = idx - tt * (tt + 1) / 2;
 }
 
+// Staging through registers with every global load of a phase issued before
+// the first LDS store (one memory latency per phase, not one per loop trip).
+// Rows x W floats (row stride ld) -> split planes BSwz<W>.
+template <int W, int ROWS, int NTHR>
+struct SplitRows {
+  static constexpr int PER = ROWS * (W / 8) / NTHR;
+  static_assert(ROWS * (W / 8) % NTHR == 0, "whole 8-column groups per thread");
+  f32x4 x[PER][2];
+  GMDN_DEV void load(const float* src, int64_t ld) {
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int e = threadIdx.x + q * NTHR, r = e / (W / 8), c = (e % (W / 8)) * 8;
+      x[q][0] = *reinterpret_cast<const f32x4*>(src + r * ld + c);
+      x[q][1] = *reinterpret_cast<const f32x4*>(src + r * ld + c + 4);
+    }
+  }
+  // zero the entries above the diagonal (square matrices)
+  GMDN_DEV void lower() {
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int e = threadIdx.x + q * NTHR, r = e / (W / 8), c = (e % (W / 8)) * 8;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (c + j > r) x[q][0][j] = 0.f;
+        if (c + 4 + j > r) x[q][1][j] = 0.f;
+      }
+    }
+  }
+  GMDN_DEV void store(bf16* hi, bf16* lo) const {
+    using LW = BSwz<W>;
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int e = threadIdx.x + q * NTHR, r = e / (W / 8), c = (e % (W / 8)) * 8;
+      bf16x4 h0, o0, h1, o1;
+      split4(x[q][0], h0, o0);
+      split4(x[q][1], h1, o1);
+      *reinterpret_cast<bf16x8*>(hi + LW::off(r, c)) = cat8(h0, h1);
+      *reinterpret_cast<bf16x8*>(lo + LW::off(r, c)) = cat8(o0, o1);
+    }
+  }
+};
+
+// A chunk's bf16 token rows (row stride `stride`) -> BSwz<D> tile
+template <int D, int NTHR>
+struct TokRows {
+  static constexpr int PER = CB_C * (D / 8) / NTHR;
+  static_assert(CB_C * (D / 8) % NTHR == 0, "whole 8-column groups per thread");
+  bf16x8 x[PER];
+  GMDN_DEV void load(const bf16* src, int64_t stride) {
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int e = threadIdx.x + q * NTHR, t = e / (D / 8), c = (e % (D / 8)) * 8;
+      x[q] = *reinterpret_cast<const bf16x8*>(src + t * stride + c);
+    }
+  }
+  GMDN_DEV void store(bf16* dst) const {
+    using LT = BSwz<D>;
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int e = threadIdx.x + q * NTHR, t = e / (D / 8), c = (e % (D / 8)) * 8;
+      *reinterpret_cast<bf16x8*>(dst + LT::off(t, c)) = x[q];
+    }
+  }
+};
+
 template <int D>
 __global__ void __launch_bounds__(WYP_THREADS)
 wy_prep(ChunkArgs p, float* __restrict__ UA, float* __restrict__ KA, float* __restrict__ Qt,
@@ -203,11 +268,14 @@ wy_prep(ChunkArgs p, float* __restrict__ UA, float* __restrict__ KA, float* __re
   const bf16* qg = p.q + bb * p.sq[0] + hh * p.sq[1] + t0 * p.sq[2];
   const bf16* kg = p.k + bb * p.sk[0] + hh * p.sk[1] + t0 * p.sk[2];
   const bf16* vg = p.v + bb * p.sv[0] + hh * p.sv[1] + t0 * p.sv[2];
-  for (int e = threadIdx.x; e < C * D / 8; e += WYP_THREADS) {
-    const int t = e / (D / 8), c = (e % (D / 8)) * 8;
-    *reinterpret_cast<bf16x8*>(Kb + LT::off(t, c)) = *reinterpret_cast<const bf16x8*>(kg + t * p.sk[2] + c);
-    *reinterpret_cast<bf16x8*>(Qb + LT::off(t, c)) = *reinterpret_cast<const bf16x8*>(qg + t * p.sq[2] + c);
-    *reinterpret_cast<bf16x8*>(Vb + LT::off(t, c)) = *reinterpret_cast<const bf16x8*>(vg + t * p.sv[2] + c);
+  {
+    TokRows<D, WYP_THREADS> tk, tq, tv;
+    tk.load(kg, p.sk[2]);
+    tq.load(qg, p.sq[2]);
+    tv.load(vg, p.sv[2]);
+    tk.store(Kb);
+    tq.store(Qb);
+    tv.store(Vb);
   }
   for (int e = threadIdx.x; e < C * LDC / 4; e += WYP_THREADS) reinterpret_cast<f32x4*>(Ts)[e] = zero4();
   for (int e = threadIdx.x; e < 2 * L::CP / 16; e += WYP_THREADS) reinterpret_cast<f32x4*>(Mh)[e] = zero4();
@@ -367,14 +435,8 @@ wy_out(ChunkArgs p, const float* __restrict__ Qt, const float* __restrict__ Ov, 
   const int w = wave_id(), l = lane_id(), lc = l & 15, G = l >> 4;
   const int64_t tokbase = (bh * p.T + t0) * (int64_t)D;
   const float* S = Sst + (bh * p.N + i) * (int64_t)D * D;
-  for (int e = threadIdx.x; e < D * D / 8; e += WY_THREADS) {
-    const int r = e / (D / 8), c = (e % (D / 8)) * 8;
-    bf16x4 h0, o0, h1, o1;
-    split4(*reinterpret_cast<const f32x4*>(S + (int64_t)r * D + c), h0, o0);
-    split4(*reinterpret_cast<const f32x4*>(S + (int64_t)r * D + c + 4), h1, o1);
-    *reinterpret_cast<bf16x8*>(Sh + LS::off(r, c)) = cat8(h0, h1);
-    *reinterpret_cast<bf16x8*>(Sl + LS::off(r, c)) = cat8(o0, o1);
-  }
+  SplitRows<D, D, WY_THREADS> sr;
+  sr.load(S, D);
   // lane (t, G) of k-block kb: Qt[16 w + t][32 kb + 8G .. +7]
   Op<2> qa[NKB];
   {
@@ -387,6 +449,7 @@ wy_out(ChunkArgs p, const float* __restrict__ Qt, const float* __restrict__ Ov, 
       qa[kb] = Op<2>{{cat8(h0, h1), cat8(o0, o1)}};
     }
   }
+  sr.store(Sh, Sl);
   __syncthreads();
   bf16* og = p.o + bb * p.so[0] + hh * p.so[1] + t0 * p.so[2];
 #pragma unroll 2
@@ -406,417 +469,709 @@ wy_out(ChunkArgs p, const float* __restrict__ Qt, const float* __restrict__ Ov, 
 }
 
 // ----------------------------------------------------------------- backward
+// Chunk-parallel kernels of 8 waves; intermediates of one chunk pass
+// through the workspace.  Split-bf16 products as in the forward; S_i and Sb
+// are staged in LDS as split planes (rows r, BSwz), one of them per kernel.
+// Wave w takes token tile tt = w % 4 and the feature half h = w / 4 of
+// every C x d result.
+//   wy_gs  gS = dO^T Qt
+//   wy_ka  (S_i)  A, T (to the workspace); W, U; X = U - W S^T;
+//                 dq1 = diag(gamma) dO S; Z = diag(beta) V - diag(beta gamma) K S^T
+//   wy_kb  (Sb)   M; dM = lower_incl(dO X^T); dX = M^T dO + diag(kd) K Sb^T;
+//                 dk2 = diag(kd) X Sb; <Sb, S_i>
+//   wy_kc1 (S_i)  R = T^T dX: dv = diag(beta) R; dk2 -= diag(beta gamma) R S;
+//                 dT = dX Z^T (the lower tiles; with dW = -dX S, dW (diag(beta gamma) K)^T
+//                 = -dX (diag(beta gamma) K S^T)^T)
+//   wy_kc2        dA = strict_lower(-T^T dT T^T); the A and M terms of dq, dk; the gates
+// Per-token partial sums (one slot per feature half) go to the chunk's
+// `tokp` record and are added in a fixed order: the gradients are bitwise
+// reproducible.
 struct WyBwd {
   const float *UA, *KA, *S_all, *Qt, *av;  // forward checkpoint
   const bf16* dO;                         // strides so
   float* gS;                              // wy_gs output
   const float* Sb;                        // the reverse scan's dU (= dL/dS_{i+1})
-  float *dQp, *dKp;                       // partial dq, dk (B H T d, float32)
-  float *Tp, *dTp, *dMp;                  // T, dT, dM per chunk (C x C, float32)
-  float* tokp;                            // per chunk: dgamma, dkd, dbeta partials (3 x C) and da
+  float *T, *dM, *dT;                     // C x C per chunk
+  float *X, *Z, *dX, *dq1, *dk2;          // B H T d each
+  float* tokp;                            // per chunk, TOKP floats (below)
   bf16 *dq, *dk, *dv;
   float *dbeta, *dg;
 };
+// tokp record: [dgamma from q: 2 C][dkd: 2 C][beta-side of U: 2 C][beta gamma-side of W: 2 C][<Sb, S_i>]
+constexpr int TOKP = 8 * CB_C + 4;
+constexpr int TP_GQ = 0, TP_KD = 2 * CB_C, TP_SB = 4 * CB_C, TP_SBG = 6 * CB_C, TP_DA = 8 * CB_C;
+
+constexpr int WYB_THREADS = 512;
+
+// split operand from a float row in global memory: lane (i, G) takes
+// X[r0 + i][k0 + 8G .. +7] (natural k order)
+GMDN_DEV Op<2> gl_row_op(const float* X, int64_t ld, int r0, int k0) {
+  const int l = lane_id();
+  const float* s = X + (int64_t)(r0 + (l & 15)) * ld + k0 + 8 * (l >> 4);
+  bf16x4 h0, o0, h1, o1;
+  split4(*reinterpret_cast<const f32x4*>(s), h0, o0);
+  split4(*reinterpret_cast<const f32x4*>(s + 4), h1, o1);
+  return Op<2>{{cat8(h0, h1), cat8(o0, o1)}};
+}
+
+// split planes' natural-order row / column operands
+template <class L>
+GMDN_DEV Op<2> prow(const bf16* hi, const bf16* lo, int r, int k0) {
+  return Op<2>{{row8<L>(hi, r, k0), row8<L>(lo, r, k0)}};
+}
+template <class L>
+GMDN_DEV Op<2> pcol(const bf16* hi, const bf16* lo, int k0, int c0) {
+  return Op<2>{{col8<L>(hi, k0, c0), col8<L>(lo, k0, c0)}};
+}
+// pair-order row / column operands
+template <class L>
+GMDN_DEV Op<2> prow_p(const bf16* hi, const bf16* lo, int r0, int k0) {
+  return Op<2>{{b_row<L>(hi, r0, k0), b_row<L>(lo, r0, k0)}};
+}
+template <class L>
+GMDN_DEV Op<2> pcol_p(const bf16* hi, const bf16* lo, int k0, int c0) {
+  return Op<2>{{b_col<L>(hi, k0, c0), b_col<L>(lo, k0, c0)}};
+}
+// a natural-order split row operand scaled per k by sc[k0 + 8G + j]
+GMDN_DEV Op<2> scale_op(const Op<2>& x, const float* sc, int k0) {
+  const int G = lane_id() >> 4;
+  f32x4 a, b;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    a[j] = ((float)x.v[0][j] + (float)x.v[1][j]) * sc[k0 + 8 * G + j];
+    b[j] = ((float)x.v[0][4 + j] + (float)x.v[1][4 + j]) * sc[k0 + 8 * G + 4 + j];
+  }
+  bf16x4 h0, o0, h1, o1;
+  split4(a, h0, o0);
+  split4(b, h1, o1);
+  return Op<2>{{cat8(h0, h1), cat8(o0, o1)}};
+}
 
 // gS[r][c] = sum_t dO[t][r] Qt[t][c]
 template <int D>
 __global__ void __launch_bounds__(WY_THREADS) wy_gs(ChunkArgs p, WyBwd b) {
-  constexpr int C = CB_C, LDT = D + 4, NT = D / 16;
-  extern __shared__ __align__(16) float sm[];
-  float* Os = sm;
-  float* Qs = sm + C * LDT;
+  using LT = BSwz<D>;
+  constexpr int C = CB_C, NT = D / 16;
+  extern __shared__ __align__(16) char smem[];
+  bf16* Ob = reinterpret_cast<bf16*>(smem);
+  bf16* Qh = Ob + C * D;
+  bf16* Ql = Qh + C * D;
   const int64_t bh = blockIdx.x / p.N;
   const int i = (int)(blockIdx.x % p.N);
   const int64_t bb = bh / p.H, hh = bh % p.H, t0 = (int64_t)i * C, si = bh * p.N + i;
   const int w = wave_id();
-  const bf16* og = b.dO + bb * p.so[0] + hh * p.so[1] + t0 * p.so[2];
-  const float* qt = b.Qt + (bh * p.T + t0) * (int64_t)D;
-  for (int e = threadIdx.x; e < C * D / 8; e += WY_THREADS) {
-    const int t = e / (D / 8), c = (e % (D / 8)) * 8;
-    const bf16x8 x = *reinterpret_cast<const bf16x8*>(og + t * p.so[2] + c);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) Os[t * LDT + c + j] = (float)x[j];
-    *reinterpret_cast<f32x4*>(Qs + t * LDT + c) = *reinterpret_cast<const f32x4*>(qt + (int64_t)t * D + c);
-    *reinterpret_cast<f32x4*>(Qs + t * LDT + c + 4) = *reinterpret_cast<const f32x4*>(qt + (int64_t)t * D + c + 4);
+  {
+    TokRows<D, WY_THREADS> to;
+    SplitRows<D, CB_C, WY_THREADS> sq;
+    to.load(b.dO + bb * p.so[0] + hh * p.so[1] + t0 * p.so[2], p.so[2]);
+    sq.load(b.Qt + (bh * p.T + t0) * (int64_t)D, D);
+    to.store(Ob);
+    sq.store(Qh, Ql);
   }
   __syncthreads();
   float* gS = b.gS + si * (int64_t)D * D;
-  for (int tile = w; tile < NT * NT; tile += 4) {
-    const int tr = tile / NT, tc = tile % NT;
-    const f32x4 acc = mm16<C>([&](int r, int k) { return Os[k * LDT + 16 * tr + r]; },
-                              [&](int k, int c) { return Qs[k * LDT + 16 * tc + c]; }, zero4());
-    st_tile(gS, D, 16 * tr, 16 * tc, acc);
+  for (int tile = w; tile < NT * NT; tile += WY_THREADS / 64) {
+    const int rt = tile / NT, ct = tile % NT;
+    f32x4 acc = zero4();
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+      acc = mma<1, 2>(Op<1>{{col8<LT>(Ob, 32 * kb, 16 * rt)}}, pcol<LT>(Qh, Ql, 32 * kb, 16 * ct), acc);
+    st_tile(gS, D, 16 * rt, 16 * ct, acc);
   }
 }
 
 template <int D>
-struct WyBwdLds {
-  static constexpr int C = CB_C;
-  static constexpr int LDB = D + 8;        // bf16 stride of a token tile row
-  static constexpr int LDT = D + 4;        // float stride of a token tile row
-  static constexpr int LDC = C + 4;        // float stride of a C x C matrix row
-  static constexpr int BT = C * LDB * 2;   // bytes: bf16 token tile
-  static constexpr int FT = C * LDT * 4;   // bytes: float token tile
-  static constexpr int CC = C * LDC * 4;   // bytes: float C x C matrix
-  // wy_tok1: K, V, dO (bf16); F1: Q (bf16) in steps 0-1, then W / X / dW rows;
-  // F2: A in steps 1-2, then dX rows; T; M; then small float arrays
-  static constexpr int K0 = 0, V0 = BT, O0 = 2 * BT, F1 = 3 * BT, F2 = F1 + FT, T0 = F2 + FT, M0 = T0 + CC;
-  static constexpr int R0 = M0 + CC;
-  static constexpr int SMALL1 = 5 * C + 3 * 256 + 4;  // gates, tri_inverse scratch, per-wave <Sb, S_i>
-  static constexpr int TOK1_BYTES = R0 + SMALL1 * 4;
-  // wy_tok2: Q, K (bf16); T, dT, dM, Y = dT T^T, G_A, dM * Gamma; small arrays
-  static constexpr int Q2 = 0, K2 = BT, T2 = 2 * BT, DT2 = T2 + CC, DM2 = DT2 + CC, Y2 = DM2 + CC,
-                       GA2 = Y2 + CC, DG2 = GA2 + CC, R2 = DG2 + CC;
-  static constexpr int SMALL2 = 5 * C + 2 * C + 4 * C;  // gates, rowE, colE
-  static constexpr int TOK2_BYTES = R2 + SMALL2 * 4;
-  static_assert(TOK1_BYTES <= 160 * 1024 && TOK2_BYTES <= 160 * 1024, "WY backward LDS exceeds 160 KiB");
-  static_assert(BT <= FT && CC <= FT, "Q and A fit the slots they borrow");
+struct WyKaLds {
+  static constexpr int C = CB_C, TB = C * D * 2, CP = C * C * 2, LDC = C + 4, CF = C * LDC * 4;
+  static constexpr int K0 = 0, V0 = TB, O0 = 2 * TB, R0 = 3 * TB;
+  // region R: A, T (float32) and the substitution's scratch, then the S_i planes
+  static constexpr int RB = 4 * D * D > 2 * CF + 3072 ? 4 * D * D : 2 * CF + 3072;
+  static constexpr int TH0 = R0 + RB, TL0 = TH0 + CP, G0 = TL0 + CP;
+  static constexpr int BYTES = G0 + 5 * C * 4;
+  static_assert(BYTES <= 160 * 1024, "WY backward LDS exceeds the 160 KiB of a CU");
 };
 
-template <int LDB>
-GMDN_DEV float bfx(const bf16* X, int r, int c) { return (float)X[r * LDB + c]; }
-
 template <int D>
-GMDN_DEV void load_bf16_rows(bf16* dst, const bf16* src, int64_t stride) {
-  constexpr int LDB = D + 8;
-  for (int e = threadIdx.x; e < CB_C * D / 8; e += WY_THREADS) {
-    const int t = e / (D / 8), c = (e % (D / 8)) * 8;
-    *reinterpret_cast<bf16x8*>(dst + t * LDB + c) = *reinterpret_cast<const bf16x8*>(src + t * stride + c);
-  }
-}
-
-template <int D>
-__global__ void __launch_bounds__(WY_THREADS) wy_tok1(ChunkArgs p, WyBwd b) {
-  using L = WyBwdLds<D>;
-  constexpr int C = CB_C, LDB = L::LDB, LDT = L::LDT, LDC = L::LDC, NT = D / 16;
+__global__ void __launch_bounds__(WYB_THREADS) wy_ka(ChunkArgs p, WyBwd b) {
+  using L = WyKaLds<D>;
+  using LT = BSwz<D>;
+  using LP = BSwz<CB_C>;
+  constexpr int C = CB_C, LDC = L::LDC, NT = D / 16, NKB = D / 32, NH = NT / 2;
   extern __shared__ __align__(16) char smem[];
-  bf16* Ks = reinterpret_cast<bf16*>(smem + L::K0);
-  bf16* Vs = reinterpret_cast<bf16*>(smem + L::V0);
-  bf16* Os = reinterpret_cast<bf16*>(smem + L::O0);
-  bf16* Qs = reinterpret_cast<bf16*>(smem + L::F1);
-  float* F1 = reinterpret_cast<float*>(smem + L::F1);
-  float* As = reinterpret_cast<float*>(smem + L::F2);
-  float* F2 = reinterpret_cast<float*>(smem + L::F2);
-  float* Ts = reinterpret_cast<float*>(smem + L::T0);
-  float* Ms = reinterpret_cast<float*>(smem + L::M0);
-  float* bet = reinterpret_cast<float*>(smem + L::R0);
+  bf16* Kb = reinterpret_cast<bf16*>(smem + L::K0);
+  bf16* Vb = reinterpret_cast<bf16*>(smem + L::V0);
+  bf16* Ob = reinterpret_cast<bf16*>(smem + L::O0);
+  float* As = reinterpret_cast<float*>(smem + L::R0);
+  float* Ts = As + C * LDC;
+  bf16* Sh = reinterpret_cast<bf16*>(smem + L::R0);
+  bf16* Sl = Sh + D * D;
+  bf16* Th = reinterpret_cast<bf16*>(smem + L::TH0);
+  bf16* Tl = reinterpret_cast<bf16*>(smem + L::TL0);
+  float* bet = reinterpret_cast<float*>(smem + L::G0);
   float* gam = bet + C;
   float* bg = gam + C;
   float* kd = bg + C;
   float* lgam = kd + C;
-  float* Xw = lgam + C;      // 3 x 256
-  float* pda = Xw + 768;     // per wave: partial <Sb, S_i>
 
   const int64_t bh = blockIdx.x / p.N;
   const int i = (int)(blockIdx.x % p.N);
   const int64_t bb = bh / p.H, hh = bh % p.H, t0 = (int64_t)i * C, si = bh * p.N + i;
   const int w = wave_id(), l = lane_id(), lc = l & 15, G = l >> 4;
-  const int r0 = 16 * w;  // this wave's token rows
-  const int64_t mat = (int64_t)D * D;
-  const float* S = b.S_all + si * mat;
-  const float* Sb = b.Sb + si * mat;
+  const int64_t tokbase = (bh * p.T + t0) * (int64_t)D;
   const bf16* qg = p.q + bb * p.sq[0] + hh * p.sq[1] + t0 * p.sq[2];
 
-  // ---- step 0: tiles, gates, zeroed T
-  load_bf16_rows<D>(Qs, qg, p.sq[2]);
-  load_bf16_rows<D>(Ks, p.k + bb * p.sk[0] + hh * p.sk[1] + t0 * p.sk[2], p.sk[2]);
-  load_bf16_rows<D>(Vs, p.v + bb * p.sv[0] + hh * p.sv[1] + t0 * p.sv[2], p.sv[2]);
-  load_bf16_rows<D>(Os, b.dO + bb * p.so[0] + hh * p.so[1] + t0 * p.so[2], p.so[2]);
-  for (int e = threadIdx.x; e < C * LDC; e += WY_THREADS) Ts[e] = 0.f;
+  // S_i's loads stay in flight through A and T (its planes replace them in region R)
+  SplitRows<D, D, WYB_THREADS> sr;
+  {
+    TokRows<D, WYB_THREADS> tk, tv, to;
+    tk.load(p.k + bb * p.sk[0] + hh * p.sk[1] + t0 * p.sk[2], p.sk[2]);
+    tv.load(p.v + bb * p.sv[0] + hh * p.sv[1] + t0 * p.sv[2], p.sv[2]);
+    to.load(b.dO + bb * p.so[0] + hh * p.so[1] + t0 * p.so[2], p.so[2]);
+    sr.load(b.S_all + si * (int64_t)D * D, D);
+    tk.store(Kb);
+    tv.store(Vb);
+    to.store(Ob);
+  }
+  for (int e = threadIdx.x; e < C * LDC / 4; e += WYB_THREADS) reinterpret_cast<f32x4*>(Ts)[e] = zero4();
   if (w == 0) wy_gates(p.beta, p.g, bh * p.T + t0 + l, bet, gam, bg, kd, lgam);
   __syncthreads();
-  auto kb = [&](int r, int c) { return bfx<LDB>(Ks, r, c); };
-
-  // ---- step 1: rows of A and M
+  // ---- A's causal tiles, T
+  for (int job = w; job < 10; job += WYB_THREADS / 64) {
+    int tt, st;
+    causal_tile(job, tt, st);
+    f32x4 acc = zero4();
 #pragma unroll
-  for (int st = 0; st < 4; ++st) {
-    f32x4 a = zero4(), m = zero4();
-    if (st <= w) {
-      const f32x4 kk = mm16<D>([&](int r, int k) { return kb(r0 + r, k); },
-                               [&](int k, int c) { return kb(16 * st + c, k); }, zero4());
-      const f32x4 qk = mm16<D>([&](int r, int k) { return bfx<LDB>(Qs, r0 + r, k); },
-                               [&](int k, int c) { return kb(16 * st + c, k); }, zero4());
-      const int s = 16 * st + lc;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int t = r0 + 4 * G + j;
-        const float e = s <= t ? expf(lgam[t] - lgam[s]) : 0.f;
-        a[j] = s < t ? bet[t] * kk[j] * e : 0.f;
-        m[j] = qk[j] * e;
-      }
-    }
-    st_tile(As, LDC, r0, 16 * st, a);
-    st_tile(Ms, LDC, r0, 16 * st, m);
-  }
-  __syncthreads();
-  // ---- step 2: T = (I + A)^-1
-  tri_inverse<LDC>(As, Ts, Xw);
-
-  // ---- step 3: W, U and X = U - W S_i^T for this wave's rows (Q is dead: F1 holds W, then X)
-  f32x4 X[NT];
-#pragma unroll
-  for (int tc = 0; tc < NT; ++tc) {
-    auto trow = [&](int r, int k) { return Ts[(r0 + r) * LDC + k]; };
-    const f32x4 wt = mm16<C>(trow, [&](int k, int c) { return bg[k] * kb(k, 16 * tc + c); }, zero4());
-    st_tile(F1, LDT, r0, 16 * tc, wt);
-    X[tc] = mm16<C>(trow, [&](int k, int c) { return bet[k] * bfx<LDB>(Vs, k, 16 * tc + c); }, zero4());
-  }
-#pragma unroll
-  for (int tc = 0; tc < NT; ++tc)
-    X[tc] -= mm16<D>([&](int r, int k) { return F1[(r0 + r) * LDT + k]; },
-                     [&](int k, int c) { return S[(int64_t)(16 * tc + c) * D + k]; }, zero4());
-#pragma unroll
-  for (int tc = 0; tc < NT; ++tc) st_tile(F1, LDT, r0, 16 * tc, X[tc]);
-  __syncthreads();  // X complete
-
-  // ---- step 4: dM = lower_incl(dO X^T), dQt~ = dO S_i, dK~ = X Sb; <Sb, S_i>
-  auto orow = [&](int r, int k) { return bfx<LDB>(Os, r0 + r, k); };
-  f32x4 dM[4];
-#pragma unroll
-  for (int st = 0; st < 4; ++st) {
-    dM[st] = zero4();
-    if (st <= w) {
-      dM[st] = mm16<D>(orow, [&](int k, int c) { return F1[(16 * st + c) * LDT + k]; }, zero4());
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (16 * st + lc > r0 + 4 * G + j) dM[st][j] = 0.f;
-    }
-  }
-  float dgam[4] = {0.f, 0.f, 0.f, 0.f}, dkd[4] = {0.f, 0.f, 0.f, 0.f};
-  float dbet[4] = {0.f, 0.f, 0.f, 0.f}, dbg[4] = {0.f, 0.f, 0.f, 0.f};
-  float* dqp = b.dQp + (bh * p.T + t0) * (int64_t)D;
-  float* dkp = b.dKp + (bh * p.T + t0) * (int64_t)D;
-  f32x4 dK[NT];
-#pragma unroll
-  for (int tc = 0; tc < NT; ++tc) {
-    const f32x4 dqt = mm16<D>(orow, [&](int k, int c) { return S[(int64_t)k * D + 16 * tc + c]; }, zero4());
-    const f32x4 dkt = mm16<D>([&](int r, int k) { return F1[(r0 + r) * LDT + k]; },
-                              [&](int k, int c) { return Sb[(int64_t)k * D + 16 * tc + c]; }, zero4());
-    f32x4 dq;
+    for (int kb = 0; kb < NKB; ++kb)
+      acc = mfma(row8<LT>(Kb, 16 * tt + lc, 32 * kb), row8<LT>(Kb, 16 * st + lc, 32 * kb), acc);
+    const int s = 16 * st + lc;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int t = r0 + 4 * G + j, c = 16 * tc + lc;
-      dgam[j] += dqt[j] * (float)qg[(int64_t)t * p.sq[2] + c];
-      dkd[j] += dkt[j] * kb(t, c);
-      dq[j] = gam[t] * dqt[j];
-      dK[tc][j] = kd[t] * dkt[j];
+      const int t = 16 * tt + 4 * G + j;
+      acc[j] = s < t ? bet[t] * acc[j] * expf(lgam[t] - lgam[s]) : 0.f;
     }
-    st_tile(dqp, D, r0, 16 * tc, dq);
+    st_tile(As, LDC, 16 * tt, 16 * st, acc);
   }
+  __syncthreads();
+  tri_inverse<LDC>(As, Ts, Ts + C * LDC);
   {
-    float acc = 0.f;
-    for (int e = threadIdx.x; e < D * D / 4; e += WY_THREADS) {
-      const f32x4 x = *reinterpret_cast<const f32x4*>(S + 4 * (int64_t)e);
-      const f32x4 y = *reinterpret_cast<const f32x4*>(Sb + 4 * (int64_t)e);
-      acc += x[0] * y[0] + x[1] * y[1] + x[2] * y[2] + x[3] * y[3];
-    }
-    acc = wave_sum(acc);
-    if (l == 0) pda[w] = acc;
+    // T's split planes, and T itself for the later kernels
+    const int r = threadIdx.x >> 3, c = (threadIdx.x & 7) * 8;
+    const f32x4 x0 = *reinterpret_cast<const f32x4*>(Ts + r * LDC + c);
+    const f32x4 x1 = *reinterpret_cast<const f32x4*>(Ts + r * LDC + c + 4);
+    bf16x4 h0, o0, h1, o1;
+    split4(x0, h0, o0);
+    split4(x1, h1, o1);
+    *reinterpret_cast<bf16x8*>(Th + LP::off(r, c)) = cat8(h0, h1);
+    *reinterpret_cast<bf16x8*>(Tl + LP::off(r, c)) = cat8(o0, o1);
+    float* Tg = b.T + si * C * C + r * C + c;
+    *reinterpret_cast<f32x4*>(Tg) = x0;
+    *reinterpret_cast<f32x4*>(Tg + 4) = x1;
   }
-
-  // ---- step 5: dX = M^T dO + diag(kd) K Sb^T (F2, A is dead), dW = -dX S_i
-#pragma unroll
-  for (int tc = 0; tc < NT; ++tc) {
-    f32x4 dx = mm16<C>([&](int r, int k) { return Ms[k * LDC + r0 + r]; },
-                       [&](int k, int c) { return bfx<LDB>(Os, k, 16 * tc + c); }, zero4());
-    dx = mm16<D>([&](int r, int k) { return kd[r0 + r] * kb(r0 + r, k); },
-                 [&](int k, int c) { return Sb[(int64_t)(16 * tc + c) * D + k]; }, dx);
-    st_tile(F2, LDT, r0, 16 * tc, dx);
-  }
-  f32x4 dW[NT];
-#pragma unroll
-  for (int tc = 0; tc < NT; ++tc)
-    dW[tc] = -mm16<D>([&](int r, int k) { return F2[(r0 + r) * LDT + k]; },
-                      [&](int k, int c) { return S[(int64_t)k * D + 16 * tc + c]; }, zero4());
-  __syncthreads();  // every wave has read X and written its dX rows
-#pragma unroll
-  for (int tc = 0; tc < NT; ++tc) st_tile(F1, LDT, r0, 16 * tc, dW[tc]);
+  __syncthreads();  // region R is free: the S_i planes
+  sr.store(Sh, Sl);
   __syncthreads();
 
-  // ---- step 6: dT (to the workspace), dv, and the T^T dW term of dk
-  float* dTp = b.dTp + si * C * C;
+  const int tt = w & 3, h = w >> 2;
+  const int kbt = tt >> 1;  // T[t][s] = 0 for s > t: k-blocks 0 .. kbt
+  // rows t of diag(beta)-, diag(beta gamma)-scaled T (k = s)
+  Op<2> tb[2], tg[2];
 #pragma unroll
-  for (int st = 0; st < 4; ++st) {
-    f32x4 dt = mm16<D>([&](int r, int k) { return F2[(r0 + r) * LDT + k]; },
-                       [&](int k, int c) { return bet[16 * st + c] * bfx<LDB>(Vs, 16 * st + c, k); }, zero4());
-    dt = mm16<D>([&](int r, int k) { return F1[(r0 + r) * LDT + k]; },
-                 [&](int k, int c) { return bg[16 * st + c] * kb(16 * st + c, k); }, dt);
-    st_tile(dTp, C, r0, 16 * st, dt);
+  for (int kb = 0; kb < 2; ++kb) {
+    const Op<2> x = prow<LP>(Th, Tl, 16 * tt + lc, 32 * kb);
+    tb[kb] = scale_op(x, bet, 32 * kb);
+    tg[kb] = scale_op(x, bg, 32 * kb);
   }
-  bf16* dvg = b.dv + bb * p.sv[0] + hh * p.sv[1] + t0 * p.sv[2];
+  // -W^T tiles [c][t] = -sum_s K[s][c] beta gamma_s T[t][s], packed: the
+  // pair-order operand (k = c, free t) of X's W S^T term
+  Op<2> wn[NKB];
 #pragma unroll
-  for (int tc = 0; tc < NT; ++tc) {
-    auto tcol = [&](int r, int k) { return Ts[k * LDC + r0 + r]; };
-    const f32x4 dvb = mm16<C>(tcol, [&](int k, int c) { return F2[k * LDT + 16 * tc + c]; }, zero4());
-    const f32x4 dkb = mm16<C>(tcol, [&](int k, int c) { return F1[k * LDT + 16 * tc + c]; }, zero4());
+  for (int kp = 0; kp < NKB; ++kp) {
+    f32x4 a0 = zero4(), a1 = zero4();
+    for (int kb = 0; kb <= kbt; ++kb) {
+      a0 = mma<1, 2>(Op<1>{{col8<LT>(Kb, 32 * kb, 32 * kp)}}, tg[kb], a0);
+      a1 = mma<1, 2>(Op<1>{{col8<LT>(Kb, 32 * kb, 32 * kp + 16)}}, tg[kb], a1);
+    }
+    wn[kp] = pack_tiles<2>(-a0, -a1);
+  }
+#pragma unroll 1
+  for (int q = 0; q < NH; ++q) {
+    const int rt = h * NH + q;
+    // X = U - W S^T, U[t][r] = sum_s beta_s T[t][s] V[s][r]
+    f32x4 x = zero4();
+    for (int kb = 0; kb <= kbt; ++kb) x = mma<2, 1>(tb[kb], Op<1>{{col8<LT>(Vb, 32 * kb, 16 * rt)}}, x);
+#pragma unroll
+    for (int kp = 0; kp < NKB; ++kp) x = mma<2, 2>(wn[kp], prow_p<LT>(Sh, Sl, 16 * rt, 32 * kp), x);
+    st_tile(b.X + tokbase, D, 16 * tt, 16 * rt, x);
+    // Z = diag(beta) V - diag(beta gamma) K S^T
+    f32x4 ks = zero4();
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+      ks = mma<1, 2>(Op<1>{{row8<LT>(Kb, 16 * tt + lc, 32 * kb)}}, prow<LT>(Sh, Sl, 16 * rt + lc, 32 * kb), ks);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int t = r0 + 4 * G + j, c = 16 * tc + lc;
-      dbet[j] += dvb[j] * bfx<LDB>(Vs, t, c);
-      dbg[j] += dkb[j] * kb(t, c);
-      dvg[(int64_t)t * p.sv[2] + c] = (bf16)(bet[t] * dvb[j]);
-      dK[tc][j] += bg[t] * dkb[j];
+      const int t = 16 * tt + 4 * G + j;
+      ks[j] = bet[t] * (float)Vb[LT::off(t, 16 * rt + lc)] - bg[t] * ks[j];
     }
-    st_tile(dkp, D, r0, 16 * tc, dK[tc]);
+    st_tile(b.Z + tokbase, D, 16 * tt, 16 * rt, ks);
   }
-  // ---- T, dM and the per-token gate partials to the workspace
-  float* Tp = b.Tp + si * C * C;
-  float* dMp = b.dMp + si * C * C;
+  // dq1 = diag(gamma) dO S; dL/dgamma_t through diag(gamma) Q: sum_c (dO S)[t][c] q[t][c]
+  float dgq[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+  for (int q = 0; q < NH; ++q) {
+    const int ct = h * NH + q;
+    f32x4 y = zero4();
 #pragma unroll
-  for (int st = 0; st < 4; ++st) {
-    st_tile(Tp, C, r0, 16 * st, ld_tile(Ts, LDC, r0, 16 * st));
-    st_tile(dMp, C, r0, 16 * st, dM[st]);
+    for (int kb = 0; kb < NKB; ++kb)
+      y = mma<1, 2>(Op<1>{{row8<LT>(Ob, 16 * tt + lc, 32 * kb)}}, pcol<LT>(Sh, Sl, 32 * kb, 16 * ct), y);
+    const int c = 16 * ct + lc;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = 16 * tt + 4 * G + j;
+      dgq[j] += y[j] * (float)qg[t * p.sq[2] + c];
+      y[j] *= gam[t];
+    }
+    st_tile(b.dq1 + tokbase, D, 16 * tt, 16 * ct, y);
   }
-  float* tp = b.tokp + si * (3 * C + 4);
+  float* tp = b.tokp + si * TOKP;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int t = r0 + 4 * G + j;
-    const float sg = row16_sum(dgam[j]), sk = row16_sum(dkd[j]), sb = row16_sum(dbet[j]), sbg = row16_sum(dbg[j]);
-    if (lc == 0) {
-      tp[t] = sg + bet[t] * sbg;          // dL/dgamma_t (Q~ = diag(gamma) Q, and beta gamma)
-      tp[C + t] = sk;                     // dL/dkd_t
-      tp[2 * C + t] = sb + gam[t] * sbg;  // dL/dbeta_t from U and W
-    }
+    const float s = row16_sum(dgq[j]);
+    if (lc == 0) tp[TP_GQ + h * C + 16 * tt + 4 * G + j] = s;
   }
-  __syncthreads();
-  if (threadIdx.x == 0) tp[3 * C] = (pda[0] + pda[1]) + (pda[2] + pda[3]);  // dL/dgamma_C = <Sb, S_i>
 }
 
 template <int D>
-__global__ void __launch_bounds__(WY_THREADS) wy_tok2(ChunkArgs p, WyBwd b) {
-  using L = WyBwdLds<D>;
-  constexpr int C = CB_C, LDB = L::LDB, LDC = L::LDC, NT = D / 16;
+struct WyKbLds {
+  static constexpr int C = CB_C, TB = C * D * 2, CP = C * C * 2;
+  static constexpr int K0 = 0, Q0 = TB, O0 = 2 * TB;
+  static constexpr int SH0 = 3 * TB, SL0 = SH0 + 2 * D * D, MH0 = SL0 + 2 * D * D, ML0 = MH0 + CP;
+  static constexpr int G0 = ML0 + CP, DA0 = G0 + 5 * C * 4;
+  static constexpr int BYTES = DA0 + 8 * 4;
+  static_assert(BYTES <= 160 * 1024, "WY backward LDS exceeds the 160 KiB of a CU");
+};
+
+template <int D>
+__global__ void __launch_bounds__(WYB_THREADS) wy_kb(ChunkArgs p, WyBwd b) {
+  using L = WyKbLds<D>;
+  using LT = BSwz<D>;
+  using LP = BSwz<CB_C>;
+  constexpr int C = CB_C, NT = D / 16, NKB = D / 32, NH = NT / 2;
   extern __shared__ __align__(16) char smem[];
-  bf16* Qs = reinterpret_cast<bf16*>(smem + L::Q2);
-  bf16* Ks = reinterpret_cast<bf16*>(smem + L::K2);
-  float* Ts = reinterpret_cast<float*>(smem + L::T2);
-  float* dTs = reinterpret_cast<float*>(smem + L::DT2);
-  float* dMs = reinterpret_cast<float*>(smem + L::DM2);
-  float* Ys = reinterpret_cast<float*>(smem + L::Y2);
-  float* GAs = reinterpret_cast<float*>(smem + L::GA2);
-  float* DGs = reinterpret_cast<float*>(smem + L::DG2);
-  float* bet = reinterpret_cast<float*>(smem + L::R2);
+  bf16* Kb = reinterpret_cast<bf16*>(smem + L::K0);
+  bf16* Qb = reinterpret_cast<bf16*>(smem + L::Q0);
+  bf16* Ob = reinterpret_cast<bf16*>(smem + L::O0);
+  bf16* Sh = reinterpret_cast<bf16*>(smem + L::SH0);
+  bf16* Sl = reinterpret_cast<bf16*>(smem + L::SL0);
+  bf16* Mh = reinterpret_cast<bf16*>(smem + L::MH0);
+  bf16* Ml = reinterpret_cast<bf16*>(smem + L::ML0);
+  float* bet = reinterpret_cast<float*>(smem + L::G0);
   float* gam = bet + C;
   float* bg = gam + C;
   float* kd = bg + C;
   float* lgam = kd + C;
-  float* rowE = lgam + C;   // per token: sum_s dGamma[t,s] Gamma[t,s] + the A term of dbeta (2 x C)
-  float* colE = rowE + 2 * C;  // per wave: column sums of dGamma * Gamma (4 x C)
+  float* dap = reinterpret_cast<float*>(smem + L::DA0);
 
   const int64_t bh = blockIdx.x / p.N;
   const int i = (int)(blockIdx.x % p.N);
   const int64_t bb = bh / p.H, hh = bh % p.H, t0 = (int64_t)i * C, si = bh * p.N + i;
   const int w = wave_id(), l = lane_id(), lc = l & 15, G = l >> 4;
-  const int r0 = 16 * w;
-  load_bf16_rows<D>(Qs, p.q + bb * p.sq[0] + hh * p.sq[1] + t0 * p.sq[2], p.sq[2]);
-  load_bf16_rows<D>(Ks, p.k + bb * p.sk[0] + hh * p.sk[1] + t0 * p.sk[2], p.sk[2]);
-  const float* Tp = b.Tp + si * C * C;
-  const float* dTp = b.dTp + si * C * C;
-  const float* dMp = b.dMp + si * C * C;
-  for (int e = threadIdx.x; e < C * C / 4; e += WY_THREADS) {
-    const int r = e / (C / 4), c = (e % (C / 4)) * 4;
-    *reinterpret_cast<f32x4*>(Ts + r * LDC + c) = *reinterpret_cast<const f32x4*>(Tp + r * C + c);
-    *reinterpret_cast<f32x4*>(dTs + r * LDC + c) = *reinterpret_cast<const f32x4*>(dTp + r * C + c);
-    *reinterpret_cast<f32x4*>(dMs + r * LDC + c) = *reinterpret_cast<const f32x4*>(dMp + r * C + c);
+  const int64_t tokbase = (bh * p.T + t0) * (int64_t)D, mat = (int64_t)D * D;
+
+  {
+    // Sb's planes, and <Sb, S_i> from the same pieces of both
+    TokRows<D, WYB_THREADS> tk, tq, to;
+    SplitRows<D, D, WYB_THREADS> sb, sx;
+    tk.load(p.k + bb * p.sk[0] + hh * p.sk[1] + t0 * p.sk[2], p.sk[2]);
+    tq.load(p.q + bb * p.sq[0] + hh * p.sq[1] + t0 * p.sq[2], p.sq[2]);
+    to.load(b.dO + bb * p.so[0] + hh * p.so[1] + t0 * p.so[2], p.so[2]);
+    sb.load(b.Sb + si * mat, D);
+    sx.load(b.S_all + si * mat, D);
+    tk.store(Kb);
+    tq.store(Qb);
+    to.store(Ob);
+    float acc = 0.f;
+#pragma unroll
+    for (int q = 0; q < sb.PER; ++q) acc += dot4(sx.x[q][0], sb.x[q][0]) + dot4(sx.x[q][1], sb.x[q][1]);
+    sb.store(Sh, Sl);
+    acc = wave_sum(acc);
+    if (l == 0) dap[w] = acc;
   }
+  for (int e = threadIdx.x; e < 2 * L::CP / 16; e += WYB_THREADS) reinterpret_cast<f32x4*>(Mh)[e] = zero4();
+  if (w == 0) wy_gates(p.beta, p.g, bh * p.T + t0 + l, bet, gam, bg, kd, lgam);
+  __syncthreads();
+  // ---- M's causal tiles (split planes, rows t) and dM = lower_incl(dO X^T) (to the workspace)
+  for (int job = w; job < 20; job += WYB_THREADS / 64) {
+    int tt, st;
+    causal_tile(job % 10, tt, st);
+    if (job < 10) {
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb)
+        acc = mfma(row8<LT>(Kb, 16 * st + lc, 32 * kb), row8<LT>(Qb, 16 * tt + lc, 32 * kb), acc);
+      const int t = 16 * tt + lc;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int s = 16 * st + 4 * G + j;
+        acc[j] = s <= t ? acc[j] * expf(lgam[t] - lgam[s]) : 0.f;
+      }
+      bf16x4 h, o;
+      split4(acc, h, o);
+      *reinterpret_cast<bf16x4*>(Mh + LP::off(t, 16 * st + 4 * G)) = h;
+      *reinterpret_cast<bf16x4*>(Ml + LP::off(t, 16 * st + 4 * G)) = o;
+    } else {
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb)
+        acc = mma<1, 2>(Op<1>{{row8<LT>(Ob, 16 * tt + lc, 32 * kb)}}, gl_row_op(b.X + tokbase, D, 16 * st, 32 * kb),
+                        acc);
+      const int s = 16 * st + lc;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (s > 16 * tt + 4 * G + j) acc[j] = 0.f;
+      st_tile(b.dM + si * C * C, C, 16 * tt, 16 * st, acc);
+    }
+  }
+  __syncthreads();
+  const int tt = w & 3, h = w >> 2;
+  // dX = M^T dO + diag(kd) K Sb^T  (M^T[t][s] = M[s][t] = 0 for s < t)
+#pragma unroll 1
+  for (int q = 0; q < NH; ++q) {
+    const int rt = h * NH + q;
+    f32x4 m = zero4(), ks = zero4();
+    for (int kb = tt >> 1; kb < 2; ++kb)
+      m = mma<2, 1>(pcol<LP>(Mh, Ml, 32 * kb, 16 * tt), Op<1>{{col8<LT>(Ob, 32 * kb, 16 * rt)}}, m);
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+      ks = mma<1, 2>(Op<1>{{row8<LT>(Kb, 16 * tt + lc, 32 * kb)}}, prow<LT>(Sh, Sl, 16 * rt + lc, 32 * kb), ks);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) m[j] += kd[16 * tt + 4 * G + j] * ks[j];
+    st_tile(b.dX + tokbase, D, 16 * tt, 16 * rt, m);
+  }
+  // dk2 = diag(kd) X Sb; dL/dkd_t = sum_c (X Sb)[t][c] K[t][c]
+  Op<2> xo[NKB];
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb) xo[kb] = gl_row_op(b.X + tokbase, D, 16 * tt, 32 * kb);
+  float dkd[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+  for (int q = 0; q < NH; ++q) {
+    const int ct = h * NH + q;
+    f32x4 y = zero4();
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) y = mma<2, 2>(xo[kb], pcol<LT>(Sh, Sl, 32 * kb, 16 * ct), y);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = 16 * tt + 4 * G + j;
+      dkd[j] += y[j] * (float)Kb[LT::off(t, 16 * ct + lc)];
+      y[j] *= kd[t];
+    }
+    st_tile(b.dk2 + tokbase, D, 16 * tt, 16 * ct, y);
+  }
+  float* tp = b.tokp + si * TOKP;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float s = row16_sum(dkd[j]);
+    if (lc == 0) tp[TP_KD + h * C + 16 * tt + 4 * G + j] = s;
+  }
+  if (threadIdx.x == 0)
+    tp[TP_DA] = ((dap[0] + dap[1]) + (dap[2] + dap[3])) + ((dap[4] + dap[5]) + (dap[6] + dap[7]));
+}
+
+template <int D>
+struct WyKc1Lds {
+  static constexpr int C = CB_C, TB = C * D * 2, CP = C * C * 2;
+  static constexpr int SH0 = 0, SL0 = 2 * D * D, TH0 = 4 * D * D, TL0 = TH0 + CP, XH0 = TL0 + CP, XL0 = XH0 + TB;
+  static constexpr int G0 = XL0 + TB;
+  static constexpr int BYTES = G0 + 5 * C * 4;
+  static_assert(BYTES <= 160 * 1024, "WY backward LDS exceeds the 160 KiB of a CU");
+};
+
+template <int D>
+__global__ void __launch_bounds__(WYB_THREADS) wy_kc1(ChunkArgs p, WyBwd b) {
+  using L = WyKc1Lds<D>;
+  using LT = BSwz<D>;
+  using LP = BSwz<CB_C>;
+  constexpr int C = CB_C, NT = D / 16, NKB = D / 32, NH = NT / 2;
+  extern __shared__ __align__(16) char smem[];
+  bf16* Sh = reinterpret_cast<bf16*>(smem + L::SH0);
+  bf16* Sl = reinterpret_cast<bf16*>(smem + L::SL0);
+  bf16* Th = reinterpret_cast<bf16*>(smem + L::TH0);
+  bf16* Tl = reinterpret_cast<bf16*>(smem + L::TL0);
+  bf16* Xh = reinterpret_cast<bf16*>(smem + L::XH0);  // dX planes (rows t)
+  bf16* Xl = reinterpret_cast<bf16*>(smem + L::XL0);
+  float* bet = reinterpret_cast<float*>(smem + L::G0);
+  float* gam = bet + C;
+  float* bg = gam + C;
+  float* kd = bg + C;
+  float* lgam = kd + C;
+
+  const int64_t bh = blockIdx.x / p.N;
+  const int i = (int)(blockIdx.x % p.N);
+  const int64_t bb = bh / p.H, hh = bh % p.H, t0 = (int64_t)i * C, si = bh * p.N + i;
+  const int w = wave_id(), l = lane_id(), lc = l & 15, G = l >> 4;
+  const int64_t tokbase = (bh * p.T + t0) * (int64_t)D;
+  const bf16* kg = p.k + bb * p.sk[0] + hh * p.sk[1] + t0 * p.sk[2];
+  const bf16* vg = p.v + bb * p.sv[0] + hh * p.sv[1] + t0 * p.sv[2];
+
+  {
+    SplitRows<D, D, WYB_THREADS> ss;
+    SplitRows<C, C, WYB_THREADS> st;
+    SplitRows<D, C, WYB_THREADS> sx;
+    ss.load(b.S_all + si * (int64_t)D * D, D);
+    st.load(b.T + si * C * C, C);
+    sx.load(b.dX + tokbase, D);
+    ss.store(Sh, Sl);
+    st.store(Th, Tl);
+    sx.store(Xh, Xl);
+  }
+  if (w == 0) wy_gates(p.beta, p.g, bh * p.T + t0 + l, bet, gam, bg, kd, lgam);
+  __syncthreads();
+  const int tt = w & 3, h = w >> 2;
+  const int kbt = tt >> 1;  // T[s][t] = 0 for s < t: k-blocks kbt .. 1
+  // R^T tiles [r][t] = sum_s dX[s][r] T[s][t], packed: the pair-order operand (k = r, free t) of R S
+  Op<2> ro[NKB];
+#pragma unroll
+  for (int kp = 0; kp < NKB; ++kp) {
+    f32x4 a0 = zero4(), a1 = zero4();
+    for (int kb = kbt; kb < 2; ++kb) {
+      const Op<2> tb = pcol_p<LP>(Th, Tl, 32 * kb, 16 * tt);
+      a0 = mma<2, 2>(pcol_p<LT>(Xh, Xl, 32 * kb, 32 * kp), tb, a0);
+      a1 = mma<2, 2>(pcol_p<LT>(Xh, Xl, 32 * kb, 32 * kp + 16), tb, a1);
+    }
+    ro[kp] = pack_tiles<2>(a0, a1);
+  }
+  float sbg[4] = {0.f, 0.f, 0.f, 0.f}, sb[4] = {0.f, 0.f, 0.f, 0.f};
+  bf16* dvg = b.dv + bb * p.sv[0] + hh * p.sv[1] + t0 * p.sv[2];
+#pragma unroll 1
+  for (int q = 0; q < NH; ++q) {
+    const int ct = h * NH + q;
+    const int c = 16 * ct + lc;
+    // dk2 -= diag(beta gamma) R S;  dL/d(beta gamma)_t through W: -sum_c (R S)[t][c] K[t][c]
+    f32x4 rs = zero4();
+#pragma unroll
+    for (int kp = 0; kp < NKB; ++kp) rs = mma<2, 2>(ro[kp], pcol_p<LT>(Sh, Sl, 32 * kp, 16 * ct), rs);
+    f32x4 dk = ld_tile(b.dk2 + tokbase, D, 16 * tt, 16 * ct);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = 16 * tt + 4 * G + j;
+      sbg[j] -= rs[j] * (float)kg[t * p.sk[2] + c];
+      dk[j] -= bg[t] * rs[j];
+    }
+    st_tile(b.dk2 + tokbase, D, 16 * tt, 16 * ct, dk);
+    // R = T^T dX: dv = diag(beta) R, dL/dbeta_t through U: sum_r R[t][r] V[t][r]
+    f32x4 rr = zero4();
+    for (int kb = kbt; kb < 2; ++kb)
+      rr = mma<2, 2>(pcol<LP>(Th, Tl, 32 * kb, 16 * tt), pcol<LT>(Xh, Xl, 32 * kb, 16 * ct), rr);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = 16 * tt + 4 * G + j;
+      sb[j] += rr[j] * (float)vg[t * p.sv[2] + c];
+      dvg[t * p.sv[2] + c] = (bf16)(bet[t] * rr[j]);
+    }
+  }
+  float* tp = b.tokp + si * TOKP;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float s1 = row16_sum(sbg[j]), s2 = row16_sum(sb[j]);
+    if (lc == 0) {
+      tp[TP_SBG + h * C + 16 * tt + 4 * G + j] = s1;
+      tp[TP_SB + h * C + 16 * tt + 4 * G + j] = s2;
+    }
+  }
+  // dT = dX Z^T, the causal tiles (the strictly upper part of dT does not reach dA)
+  for (int job = w; job < 10; job += WYB_THREADS / 64) {
+    int at, st;
+    causal_tile(job, at, st);
+    f32x4 acc = zero4();
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+      acc = mma<2, 2>(prow<LT>(Xh, Xl, 16 * at + lc, 32 * kb), gl_row_op(b.Z + tokbase, D, 16 * st, 32 * kb), acc);
+    st_tile(b.dT + si * C * C, C, 16 * at, 16 * st, acc);
+  }
+}
+
+template <int D>
+struct WyKc2Lds {
+  static constexpr int C = CB_C, TB = C * D * 2, CP = C * C * 2;
+  static constexpr int Q0 = 0, K0 = TB;
+  // split planes: T, dT, Y (rows t), H = G_A^T and DG^T (rows s)
+  static constexpr int TH0 = 2 * TB, DT0 = TH0 + 2 * CP, Y0 = DT0 + 2 * CP, H0 = Y0 + 2 * CP, DG0 = H0 + 2 * CP;
+  static constexpr int G0 = DG0 + 2 * CP;
+  // per causal tile: row sums of E and of the A term of dbeta, column sums of E (16 each)
+  static constexpr int P0 = G0 + 5 * C * 4;
+  static constexpr int BYTES = P0 + 3 * 10 * 16 * 4;
+  static_assert(BYTES <= 160 * 1024, "WY backward LDS exceeds the 160 KiB of a CU");
+};
+
+template <int D>
+__global__ void __launch_bounds__(WYB_THREADS) wy_kc2(ChunkArgs p, WyBwd b) {
+  using L = WyKc2Lds<D>;
+  using LT = BSwz<D>;
+  using LP = BSwz<CB_C>;
+  constexpr int C = CB_C, NT = D / 16, NKB = D / 32, NH = NT / 2, CP = L::CP / 2;  // CP: bf16 per plane
+  extern __shared__ __align__(16) char smem[];
+  bf16* Qb = reinterpret_cast<bf16*>(smem + L::Q0);
+  bf16* Kb = reinterpret_cast<bf16*>(smem + L::K0);
+  bf16* Th = reinterpret_cast<bf16*>(smem + L::TH0);
+  bf16* Tl = Th + CP;
+  bf16* Dh = reinterpret_cast<bf16*>(smem + L::DT0);
+  bf16* Dl = Dh + CP;
+  bf16* Yh = reinterpret_cast<bf16*>(smem + L::Y0);
+  bf16* Yl = Yh + CP;
+  bf16* Hh = reinterpret_cast<bf16*>(smem + L::H0);
+  bf16* Hl = Hh + CP;
+  bf16* Gh = reinterpret_cast<bf16*>(smem + L::DG0);
+  bf16* Gl = Gh + CP;
+  float* bet = reinterpret_cast<float*>(smem + L::G0);
+  float* gam = bet + C;
+  float* bg = gam + C;
+  float* kd = bg + C;
+  float* lgam = kd + C;
+  float* rowP = reinterpret_cast<float*>(smem + L::P0);  // [10][16]
+  float* bsP = rowP + 160;                               // [10][16]
+  float* colP = bsP + 160;                               // [10][16]
+
+  const int64_t bh = blockIdx.x / p.N;
+  const int i = (int)(blockIdx.x % p.N);
+  const int64_t bb = bh / p.H, hh = bh % p.H, t0 = (int64_t)i * C, si = bh * p.N + i;
+  const int w = wave_id(), l = lane_id(), lc = l & 15, G = l >> 4;
+  const int64_t tokbase = (bh * p.T + t0) * (int64_t)D;
+  {
+    // dT's planes with its strictly upper part (not written) as zeros; H and DG^T zeroed
+    TokRows<D, WYB_THREADS> tq, tk;
+    SplitRows<C, C, WYB_THREADS> st, sd;
+    tq.load(p.q + bb * p.sq[0] + hh * p.sq[1] + t0 * p.sq[2], p.sq[2]);
+    tk.load(p.k + bb * p.sk[0] + hh * p.sk[1] + t0 * p.sk[2], p.sk[2]);
+    st.load(b.T + si * C * C, C);
+    sd.load(b.dT + si * C * C, C);
+    tq.store(Qb);
+    tk.store(Kb);
+    st.store(Th, Tl);
+    sd.lower();
+    sd.store(Dh, Dl);
+  }
+  for (int e = threadIdx.x; e < 4 * L::CP / 16; e += WYB_THREADS) reinterpret_cast<f32x4*>(Hh)[e] = zero4();
   float graw = 0.f;
   if (w == 0) {
     graw = p.g[bh * p.T + t0 + l];
     wy_gates(p.beta, p.g, bh * p.T + t0 + l, bet, gam, bg, kd, lgam);
   }
   __syncthreads();
-  auto kb = [&](int r, int c) { return bfx<LDB>(Ks, r, c); };
-
-  // ---- Y = dT T^T (rows of this wave)
+  // ---- Y = dT T^T as planes of rows t: tiles Y^T[u][t] = sum_s T[u][s] dT[t][s], stored transposed
+  for (int tile = w; tile < 16; tile += WYB_THREADS / 64) {
+    const int ut = tile >> 2, tt = tile & 3;
+    f32x4 acc = zero4();
 #pragma unroll
-  for (int st = 0; st < 4; ++st)
-    st_tile(Ys, LDC, r0, 16 * st,
-            mm16<C>([&](int r, int k) { return dTs[(r0 + r) * LDC + k]; },
-                    [&](int k, int c) { return Ts[(16 * st + c) * LDC + k]; }, zero4()));
-  __syncthreads();
-
-  // ---- dA = strict_lower(-T^T Y); the A and M terms: G_A = dA beta_t Gamma, dM Gamma,
-  // dbeta_t += sum_s dA R Gamma, E = dGamma * Gamma = (dA beta_t R + dM Rq) Gamma
-  float rsum[4] = {0.f, 0.f, 0.f, 0.f}, bsum[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int st = 0; st < 4; ++st) {
-    f32x4 ga = zero4(), dg = zero4();
-    float csum = 0.f;
-    if (st <= w) {
-      const f32x4 dA = mm16<C>([&](int r, int k) { return Ts[k * LDC + r0 + r]; },
-                               [&](int k, int c) { return Ys[k * LDC + 16 * st + c]; }, zero4());
-      const f32x4 kk = mm16<D>([&](int r, int k) { return kb(r0 + r, k); },
-                               [&](int k, int c) { return kb(16 * st + c, k); }, zero4());
-      const f32x4 qk = mm16<D>([&](int r, int k) { return bfx<LDB>(Qs, r0 + r, k); },
-                               [&](int k, int c) { return kb(16 * st + c, k); }, zero4());
-      const int s = 16 * st + lc;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int t = r0 + 4 * G + j;
-        const float e = s <= t ? expf(lgam[t] - lgam[s]) : 0.f;
-        const float da = s < t ? -dA[j] : 0.f;
-        const float dm = s <= t ? dMs[t * LDC + s] : 0.f;
-        ga[j] = da * bet[t] * e;
-        dg[j] = dm * e;
-        bsum[j] += da * kk[j] * e;
-        const float E = (da * bet[t] * kk[j] + dm * qk[j]) * e;
-        rsum[j] += E;
-        csum += E;
-      }
-    }
-    st_tile(GAs, LDC, r0, 16 * st, ga);
-    st_tile(DGs, LDC, r0, 16 * st, dg);
-    csum = group_sum(csum);
-    if (G == 0) colE[w * C + 16 * st + lc] = csum;
-  }
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float rs = row16_sum(rsum[j]), bs = row16_sum(bsum[j]);
-    if (lc == 0) {
-      rowE[r0 + 4 * G + j] = rs;
-      rowE[C + r0 + 4 * G + j] = bs;
-    }
+    for (int kb = 0; kb < 2; ++kb)
+      acc = mma<2, 2>(prow<LP>(Th, Tl, 16 * ut + lc, 32 * kb), prow<LP>(Dh, Dl, 16 * tt + lc, 32 * kb), acc);
+    bf16x4 h, o;
+    split4(acc, h, o);
+    *reinterpret_cast<bf16x4*>(Yh + LP::off(16 * tt + lc, 16 * ut + 4 * G)) = h;
+    *reinterpret_cast<bf16x4*>(Yl + LP::off(16 * tt + lc, 16 * ut + 4 * G)) = o;
   }
   __syncthreads();
-
-  // ---- dk = partial + G_A K + G_A^T K + (dM Gamma)^T Q,  dq = partial + (dM Gamma) K
-  const float* dqp = b.dQp + (bh * p.T + t0) * (int64_t)D;
-  const float* dkp = b.dKp + (bh * p.T + t0) * (int64_t)D;
-  bf16* dqg = b.dq + bb * p.sq[0] + hh * p.sq[1] + t0 * p.sq[2];
-  bf16* dkg = b.dk + bb * p.sk[0] + hh * p.sk[1] + t0 * p.sk[2];
+  // ---- causal tiles [t][s]: dA = strict_lower(-T^T Y), G_A = dA beta_t Gamma, DG = dM Gamma,
+  //      E = dGamma * Gamma = (dA beta_t (K K^T) + dM (Q K^T)) Gamma, the A term of dbeta
+  for (int job = w; job < 10; job += WYB_THREADS / 64) {
+    int tt, st;
+    causal_tile(job, tt, st);
+    f32x4 ta = zero4(), kk = zero4(), qk = zero4();
+    for (int kb = tt >> 1; kb < 2; ++kb)
+      ta = mma<2, 2>(pcol<LP>(Th, Tl, 32 * kb, 16 * tt), pcol<LP>(Yh, Yl, 32 * kb, 16 * st), ta);
 #pragma unroll
-  for (int tc = 0; tc < NT; ++tc) {
-    auto kcol = [&](int k, int c) { return kb(k, 16 * tc + c); };
-    f32x4 dk = ld_tile(dkp, D, r0, 16 * tc);
-    dk = mm16<C>([&](int r, int k) { return GAs[(r0 + r) * LDC + k]; }, kcol, dk);
-    dk = mm16<C>([&](int r, int k) { return GAs[k * LDC + r0 + r]; }, kcol, dk);
-    dk = mm16<C>([&](int r, int k) { return DGs[k * LDC + r0 + r]; },
-                 [&](int k, int c) { return bfx<LDB>(Qs, k, 16 * tc + c); }, dk);
-    f32x4 dq = ld_tile(dqp, D, r0, 16 * tc);
-    dq = mm16<C>([&](int r, int k) { return DGs[(r0 + r) * LDC + k]; }, kcol, dq);
+    for (int kb = 0; kb < NKB; ++kb) {
+      const bf16x8 ks = row8<LT>(Kb, 16 * st + lc, 32 * kb);
+      kk = mfma(row8<LT>(Kb, 16 * tt + lc, 32 * kb), ks, kk);
+      qk = mfma(row8<LT>(Qb, 16 * tt + lc, 32 * kb), ks, qk);
+    }
+    const int s = 16 * st + lc;
+    const f32x4 dmt = ld_tile(b.dM + si * C * C, C, 16 * tt, 16 * st);
+    f32x4 ga, dg;
+    float rs[4], bs[4], cs = 0.f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int64_t t = r0 + 4 * G + j;
-      const int c = 16 * tc + lc;
+      const int t = 16 * tt + 4 * G + j;
+      const float e = s <= t ? expf(lgam[t] - lgam[s]) : 0.f;
+      const float da = s < t ? -ta[j] : 0.f;
+      const float dm = s <= t ? dmt[j] : 0.f;
+      ga[j] = da * bet[t] * e;
+      dg[j] = dm * e;
+      bs[j] = da * kk[j] * e;
+      const float E = (da * bet[t] * kk[j] + dm * qk[j]) * e;
+      rs[j] = E;
+      cs += E;
+    }
+    // H = G_A^T and DG^T as planes of rows s
+    bf16x4 h, o;
+    split4(ga, h, o);
+    *reinterpret_cast<bf16x4*>(Hh + LP::off(s, 16 * tt + 4 * G)) = h;
+    *reinterpret_cast<bf16x4*>(Hl + LP::off(s, 16 * tt + 4 * G)) = o;
+    split4(dg, h, o);
+    *reinterpret_cast<bf16x4*>(Gh + LP::off(s, 16 * tt + 4 * G)) = h;
+    *reinterpret_cast<bf16x4*>(Gl + LP::off(s, 16 * tt + 4 * G)) = o;
+    cs = group_sum(cs);
+    if (G == 0) colP[job * 16 + lc] = cs;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float r1 = row16_sum(rs[j]), r2 = row16_sum(bs[j]);
+      if (lc == 0) {
+        rowP[job * 16 + 4 * G + j] = r1;
+        bsP[job * 16 + 4 * G + j] = r2;
+      }
+    }
+  }
+  __syncthreads();
+  // ---- dk = dk2 + G_A K + G_A^T K + DG^T Q,  dq = dq1 + DG K
+  const int tt = w & 3, h = w >> 2;
+  bf16* dqg = b.dq + bb * p.sq[0] + hh * p.sq[1] + t0 * p.sq[2];
+  bf16* dkg = b.dk + bb * p.sk[0] + hh * p.sk[1] + t0 * p.sk[2];
+#pragma unroll 1
+  for (int q = 0; q < NH; ++q) {
+    const int ct = h * NH + q;
+    f32x4 dk = ld_tile(b.dk2 + tokbase, D, 16 * tt, 16 * ct);
+    f32x4 dq = ld_tile(b.dq1 + tokbase, D, 16 * tt, 16 * ct);
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const Op<1> kc{{col8<LT>(Kb, 32 * kb, 16 * ct)}};
+      dk = mma<2, 1>(pcol<LP>(Hh, Hl, 32 * kb, 16 * tt), kc, dk);                // G_A[t][s] = H[s][t]
+      dk = mma<2, 1>(prow<LP>(Hh, Hl, 16 * tt + lc, 32 * kb), kc, dk);           // G_A[s][t] = H[t][s]
+      dk = mma<2, 1>(prow<LP>(Gh, Gl, 16 * tt + lc, 32 * kb), Op<1>{{col8<LT>(Qb, 32 * kb, 16 * ct)}}, dk);
+      dq = mma<2, 1>(pcol<LP>(Gh, Gl, 32 * kb, 16 * tt), kc, dq);                // DG[t][s] = DG^T[s][t]
+    }
+    const int c = 16 * ct + lc;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t t = 16 * tt + 4 * G + j;
       dkg[t * p.sk[2] + c] = (bf16)dk[j];
       dqg[t * p.sq[2] + c] = (bf16)dq[j];
     }
   }
-
   // ---- gate gradients (wave 0, lane = token)
   if (w == 0) {
-    const float* tp = b.tokp + si * (3 * C + 4);
-    const float dgm = tp[l], dkdv = tp[C + l], dbu = tp[2 * C + l], dgC = tp[3 * C];
+    const float* tp = b.tokp + si * TOKP;
+    const float sbg = tp[TP_SBG + l] + tp[TP_SBG + C + l];
+    const float dgm = (tp[TP_GQ + l] + tp[TP_GQ + C + l]) + bet[l] * sbg;  // dL/dgamma_t
+    const float dkdv = tp[TP_KD + l] + tp[TP_KD + C + l];                   // dL/dkd_t
+    const float dbu = (tp[TP_SB + l] + tp[TP_SB + C + l]) + gam[l] * sbg;   // dL/dbeta_t from U and W
+    const float dgC = tp[TP_DA];                                            // dL/dgamma_C = <Sb, S_i>
+    // row and column sums of E over the causal tiles of this token, in a fixed order
+    const int tl = l >> 4, lr = l & 15;
+    float rowE = 0.f, bsum = 0.f, colE = 0.f;
+    for (int st = 0; st <= tl; ++st) {
+      const int job = tl * (tl + 1) / 2 + st;
+      rowE += rowP[job * 16 + lr];
+      bsum += bsP[job * 16 + lr];
+    }
+    for (int tt2 = tl; tt2 < 4; ++tt2) colE += colP[(tt2 * (tt2 + 1) / 2 + tl) * 16 + lr];
     // dgc_t: gamma_t = exp(gc_t), kd_t = exp(gc_{C-1} - gc_t), the Gamma
     // exponents (row minus column sums), and gamma_{C-1} = a of the scan
-    float dgc = dgm * gam[l] - dkdv * kd[l] + rowE[l] - ((colE[l] + colE[C + l]) + (colE[2 * C + l] + colE[3 * C + l]));
+    float dgc = dgm * gam[l] - dkdv * kd[l] + rowE - colE;
     const float kdsum = wave_sum(dkdv * kd[l]);
     if (l == C - 1) dgc += kdsum + dgC * gam[l];
     // dlg_u = sum_{t >= u} dgc_t
     const float dlg = wave_sum(dgc) - (wave_incl_scan(dgc) - dgc);
     const int64_t o = bh * p.T + t0 + l;
     b.dg[o] = graw >= LOG_FLOOR ? dlg : 0.f;
-    b.dbeta[o] = dbu + rowE[C + l];
+    b.dbeta[o] = dbu + bsum;
   }
 }
 
@@ -842,10 +1197,10 @@ Ckpt ckpt_of(float* ws, int64_t B, int64_t H, int64_t T, int d) {
 }
 
 template <class K>
-hipError_t launch_k(K kern, int bytes, int64_t grid, hipStream_t s, const ChunkArgs& a, const WyBwd& b) {
+hipError_t launch_k(K kern, int threads, int bytes, int64_t grid, hipStream_t s, const ChunkArgs& a, const WyBwd& b) {
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(WY_THREADS), bytes, s, a, b);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(threads), bytes, s, a, b);
   return hipGetLastError();
 }
 
@@ -881,18 +1236,18 @@ hipError_t launch_wy(const ChunkArgs& a, float* ws, hipStream_t s) {
   return hipGetLastError();
 }
 
-// backward workspace (floats): gS, Sb (d x d per chunk), partial dq, dk
-// (B H T d), T, dT, dM (C x C per chunk), per-chunk gate partials (3 C + 4)
+// backward workspace (floats): gS, Sb (d x d per chunk); T, dM, dT (C x C
+// per chunk); X, Z, dX, dq1, dk2 (B H T d each); the per-chunk tokp records
 size_t bwd_floats(int64_t B, int64_t H, int64_t T, int d) {
   const int64_t chunks = B * H * (T / CB_C), mat = (int64_t)d * d, tok = B * H * T * (int64_t)d;
-  return (size_t)(2 * chunks * mat + 2 * tok + 3 * chunks * CB_C * CB_C + chunks * (3 * CB_C + 4));
+  return (size_t)(2 * chunks * mat + 3 * chunks * CB_C * CB_C + 5 * tok + chunks * TOKP);
 }
 
 template <int D>
 hipError_t launch_wy_bwd(const ChunkArgs& a, float* ckpt, const void* dO, void* dq, void* dk, void* dv, float* dbeta,
                          float* dg, float* ws, hipStream_t s) {
-  using L = WyBwdLds<D>;
   const int64_t chunks = a.B * a.H * a.N, mat = (int64_t)D * D, tok = a.B * a.H * a.T * (int64_t)D;
+  const int64_t cc = (int64_t)CB_C * CB_C;
   const Ckpt c = ckpt_of(ckpt, a.B, a.H, a.T, D);
   WyBwd b{};
   b.UA = c.UA;
@@ -904,18 +1259,21 @@ hipError_t launch_wy_bwd(const ChunkArgs& a, float* ckpt, const void* dO, void* 
   b.gS = ws;
   float* Sb = ws + chunks * mat;
   b.Sb = Sb;
-  b.dQp = Sb + chunks * mat;
-  b.dKp = b.dQp + tok;
-  b.Tp = b.dKp + tok;
-  b.dTp = b.Tp + chunks * CB_C * CB_C;
-  b.dMp = b.dTp + chunks * CB_C * CB_C;
-  b.tokp = b.dMp + chunks * CB_C * CB_C;
+  b.T = Sb + chunks * mat;
+  b.dM = b.T + chunks * cc;
+  b.dT = b.dM + chunks * cc;
+  b.X = b.dT + chunks * cc;
+  b.Z = b.X + tok;
+  b.dX = b.Z + tok;
+  b.dq1 = b.dX + tok;
+  b.dk2 = b.dq1 + tok;
+  b.tokp = b.dk2 + tok;
   b.dq = static_cast<bf16*>(dq);
   b.dk = static_cast<bf16*>(dk);
   b.dv = static_cast<bf16*>(dv);
   b.dbeta = dbeta;
   b.dg = dg;
-  hipError_t e = launch_k(wy_gs<D>, 2 * CB_C * (D + 4) * 4, chunks, s, a, b);
+  hipError_t e = launch_k(wy_gs<D>, WY_THREADS, 3 * CB_C * D * 2, chunks, s, a, b);
   if (e != hipSuccess) return e;
   // the delta scan's reverse kernel: dU_i = dL/dS_{i+1} (its dK and da are not needed)
   ScanArgs sa{};
@@ -933,8 +1291,10 @@ hipError_t launch_wy_bwd(const ChunkArgs& a, float* ckpt, const void* dO, void* 
   sa.precision = GMDN_PREC_TF32;
   sa.stream = s;
   if ((e = scan_bwd_rows_launch(sa, nullptr)) != hipSuccess) return e;
-  if ((e = launch_k(wy_tok1<D>, L::TOK1_BYTES, chunks, s, a, b)) != hipSuccess) return e;
-  return launch_k(wy_tok2<D>, L::TOK2_BYTES, chunks, s, a, b);
+  if ((e = launch_k(wy_ka<D>, WYB_THREADS, WyKaLds<D>::BYTES, chunks, s, a, b)) != hipSuccess) return e;
+  if ((e = launch_k(wy_kb<D>, WYB_THREADS, WyKbLds<D>::BYTES, chunks, s, a, b)) != hipSuccess) return e;
+  if ((e = launch_k(wy_kc1<D>, WYB_THREADS, WyKc1Lds<D>::BYTES, chunks, s, a, b)) != hipSuccess) return e;
+  return launch_k(wy_kc2<D>, WYB_THREADS, WyKc2Lds<D>::BYTES, chunks, s, a, b);
 }
 
 }  // namespace

@@ -11,15 +11,18 @@ for bfloat16 q, k, v (B, H, T, d) (d = 64 or 128, T a multiple of 64) and
 float32 beta, g (B, H, T).  Forward and backward are HIP:
 
 * forward (``gmdn_wy_fwd``): a chunk-parallel prep kernel (decay masks, the
-  triangular inverse T = (I + A)^-1 and the products that reduce each chunk
-  to the affine state update S' = a S + U_A - S K_A and the output
-  o = Qt S^T + Ov, in exact float32 MFMA), the drop-in delta scan kernels
-  (split-bf16 state products) and an output kernel.  Its workspace is the
-  backward's checkpoint.
+  triangular inverse T = (I + A)^-1 by float32 forward substitution, and
+  the products that reduce each chunk to the affine state update
+  S' = a S + U_A - S K_A and the output o = Qt S^T + Ov), the drop-in delta
+  scan kernels and an output kernel.  Its workspace is the backward's
+  checkpoint.
 * backward (``gmdn_wy_bwd``): dL/dS_i through o, the drop-in delta scan's
   reverse kernel for the state cotangents, then chunk-parallel kernels that
   differentiate the chunk algebra (T, U, W, the decay masks) back to q, k,
   v, beta and g.
+
+Every product is split-bf16 MFMA: bf16 q, k, v enter exactly, float32
+operands as hi + lo bf16 (about 2^-16 relative error per product).
 
 ``wy_chunk_terms`` restates the chunk algebra as float32 tensor operations;
 it documents the prep kernel's quantities and is checked on the CPU against

@@ -186,8 +186,9 @@ int gmdn_chunk_fwd(const gmdn_chunk_desc* desc, const void* q, const void* k,
  *   S_t = alpha_t S_{t-1} (I - beta_t k_t k_t^T) + beta_t v_t k_t^T,  o_t = S_t q_t,
  * alpha_t = exp(max(g_t, log 1e-6)), chunked by the WY/UT transform
  * (T = (I + strict_lower(diag(beta) (K K^T * Gamma)))^-1, U = T diag(beta) V,
- * W = T diag(beta gamma) K) with exact float32 chunk products and split-bf16
- * state products.  desc->rule, ns and
+ * W = T diag(beta gamma) K): T by forward substitution in float32, every
+ * product split-bf16 (bf16 q, k, v exact, float32 intermediates as hi + lo,
+ * about 2^-16 relative error per product).  desc->rule, ns and
  * eps are ignored; q, k, v, o bf16 (desc->dtype GMDN_DTYPE_BF16) with the
  * strides of desc. */
 size_t gmdn_wy_fwd_workspace_bytes(const gmdn_chunk_desc* desc);
@@ -202,10 +203,11 @@ int gmdn_wy_fwd(const gmdn_chunk_desc* desc, const void* q, const void* k, const
  * dk, dv (bf16, strides desc->sq, sk, sv) and dbeta, dg (contiguous
  * (B, H, T) float32): the reverse delta scan (split-bf16) gives each chunk's
  * state cotangent, then chunk-parallel kernels differentiate the WY/UT chunk
- * algebra (T = (I + A)^-1, U, W, the decay masks) with exact float32
+ * algebra (T = (I + A)^-1, U, W, the decay masks) with split-bf16
  * products.  The workspace (gmdn_wy_bwd_workspace_bytes) holds gS and the
- * state cotangents (d x d per chunk), partial dq, dk, and T, dT, dM
- * (C x C per chunk). */
+ * state cotangents (d x d per chunk), T, dM, dT (C x C per chunk), the
+ * chunk intermediates X, Z, dX and partial dq, dk (B H T d each) and
+ * per-token partial sums of the gate gradients. */
 size_t gmdn_wy_bwd_workspace_bytes(const gmdn_chunk_desc* desc);
 int gmdn_wy_bwd(const gmdn_chunk_desc* desc, const void* q, const void* k, const void* v,
                 const float* beta, const float* g, const void* ckpt, const void* dO,
