@@ -280,6 +280,19 @@ struct NSSplit {
 #pragma unroll
       for (int tc = 0; tc < NT; ++tc) acc[tc] = P::mma(col(pub, kb, tc), B[kb], acc[tc]);
   }
+  // stage_own in two halves, so that the loads can be issued early
+  static GMDN_DEV void load_pieces(const float* g, bf16x8 (&pc)[NT]) {
+    const int l = lane_id(), row = 16 * wave_id() + (l & 15);
+#pragma unroll
+    for (int c = 0; c < NT; ++c) pc[c] = *reinterpret_cast<const bf16x8*>(g + row * D + 16 * c + 4 * (l >> 4));
+  }
+  GMDN_DEV void store_pieces(lds_ptr m, const bf16x8 (&pc)[NT]) const {
+#pragma unroll
+    for (int c = 0; c < NT; ++c) {
+      lds_st<bf16x4>(m + ppub[c], __builtin_shufflevector(pc[c], pc[c], 0, 1, 2, 3));
+      lds_st<bf16x4>(m + (ppub[c] + PLANE), __builtin_shufflevector(pc[c], pc[c], 4, 5, 6, 7));
+    }
+  }
   // The wave's rows of a matrix kept in global memory as split pieces (the
   // layout `store_own` writes) -> planes at m
   GMDN_DEV void stage_own(lds_ptr m, const float* g) const {
@@ -324,9 +337,9 @@ struct NSSplit {
                  (float)h[3] + (float)o[3]};
   }
   // One quintic step on the wave's rows XT (D-layout tiles of X^T); the same
-  // products as NSBlock::step.  With zst, Z = b P + c P^2 (symmetric) is also
-  // stored as the wave's rows in split pieces.
-  GMDN_DEV void step(f32x4 (&XT)[NT], lds_ptr XM, lds_ptr PM, float* zst = nullptr) const {
+  // products as NSBlock::step.  With zst / pst, Z = b P + c P^2 and P = X X^T
+  // (both symmetric) are also stored as the wave's rows in split pieces.
+  GMDN_DEV void step(f32x4 (&XT)[NT], lds_ptr XM, lds_ptr PM, float* zst = nullptr, float* pst = nullptr) const {
     publish(XM, XT);
     __syncthreads();
     Op Bx[NKB];
@@ -337,6 +350,7 @@ struct NSSplit {
     rowprod_all(XM, Bx, Pc);
     // P is symmetric: the column block is also the wave's rows of P
     publish(PM, Pc);
+    if (pst) store_own(pst, Pc);
     __syncthreads();
     Op Bp[NKB];
     pack_all(Pc, Bp);

@@ -27,12 +27,13 @@ hipError_t scan_bwd_muon_launch(const ScanArgs& s, float* ws, int64_t ws_floats)
 // workspace floats per (b, h) of the fp32 ('ieee') muon backward: 4 + ns matrices
 __host__ __device__ inline int64_t muon_bwd_ws_floats(int dh, int ns) { return (int64_t)(4 + ns) * dh * dh; }
 // The bf16x3 muon backward keeps, per chunk of a segment, the iterates
-// X_0 .. X_ns, the products Z_0 .. Z_{ns-1} and M_i (2 ns + 2 matrices) and
+// X_0 .. X_ns, the products Z_0 .. Z_{ns-1}, P_0 .. P_{ns-1} and M_i
+// (3 ns + 2 matrices) and
 // |M_i|; per (b, h) the carried Mbar and Sb.  Workspace floats for segments of
 // nseg chunks:
 inline int64_t muon_bwd_ws_segment_floats(int64_t BH, int64_t nseg, int dh, int ns) {
   const int64_t mat = (int64_t)dh * dh;
-  return BH * nseg * ((2 * ns + 2) * mat + 1) + 2 * BH * mat;
+  return BH * nseg * ((3 * ns + 2) * mat + 1) + 2 * BH * mat;
 }
 // The default workspace: segments of as many chunks as fit in
 // MUON_BWD_WS_BUDGET bytes (at least one chunk, at most N), or the fp32
@@ -40,14 +41,14 @@ inline int64_t muon_bwd_ws_segment_floats(int64_t BH, int64_t nseg, int dh, int 
 constexpr int64_t MUON_BWD_WS_BUDGET = (int64_t)512 << 20;
 inline int64_t muon_bwd_segment(int64_t BH, int64_t N, int dh, int ns, int64_t ws_floats) {
   const int64_t mat = (int64_t)dh * dh;
-  const int64_t per = BH * ((2 * ns + 2) * mat + 1), fixed = 2 * BH * mat;
+  const int64_t per = BH * ((3 * ns + 2) * mat + 1), fixed = 2 * BH * mat;
   if (ws_floats < fixed + per) return 0;
   const int64_t n = (ws_floats - fixed) / per;
   return n < N ? n : N;
 }
 inline int64_t muon_bwd_ws_total(int64_t BH, int64_t N, int dh, int ns) {
   const int64_t mat = (int64_t)dh * dh;
-  const int64_t per = BH * ((2 * ns + 2) * mat + 1);
+  const int64_t per = BH * ((3 * ns + 2) * mat + 1);
   int64_t nseg = (MUON_BWD_WS_BUDGET / 4 - 2 * BH * mat) / per;
   if (nseg < 1) nseg = 1;
   if (nseg > N) nseg = N;

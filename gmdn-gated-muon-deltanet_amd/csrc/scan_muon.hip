@@ -220,18 +220,22 @@ scan_bwd_muon(const float* __restrict__ U, const float* __restrict__ K,
 // not depend on the cotangent, so they are rebuilt for every chunk at once
 // across the chip.  K_i staged into B; G = U - S_i K_i; M_i = m M_{i-1} + G;
 // X_0 = M_i / (|M_i| + eps); then the ns steps, storing each iterate X_k
-// (k = 0 .. ns) and each Z_k = b P_k + c P_k^2 as the wave's rows in split
-// pieces, M_i in fp32 and |M_i|.  Workspace per chunk: 2 ns + 2 matrices.
+// (k = 0 .. ns), each P_k = X_k X_k^T and Z_k = b P_k + c P_k^2 as the
+// wave's rows in split pieces, M_i in fp32 and |M_i|.  Workspace per chunk:
+// 3 ns + 2 matrices.
 //
 // scan_bwd_muon_x3, one workgroup per (b, h), chunks in reverse order:
 //   1. da_i = <Sb, S_i>, db_i = <Sb, X_ns>; Xbar = b Sb.
 //   2. The VJP steps, k = ns-1 .. 0, with Xbar published in A and X_k in B:
 //        Q    = a Xbar + Z_k Xbar                 (A column reads, Z_k rows)
-//        Bs   = Bbar + Bbar^T, Bbar = Xbar X_k^T  (A and B row reads)
-//        Y    = X_k (X_k^T Bs) = P_k Bs           (B column, then row reads)
+//        Bbar = Xbar X_k^T                        (A and B row reads)
+//        Bs   = Bbar + Bbar^T: Bbar published in A, read back transposed
+//        Y    = Bs P_k                            (Bs published in A, P_k rows)
 //        Y^T  read back transposed after publishing Y in A
 //        Xbar <- Q + (b Bs + c (Y + Y^T)) X_k     (B column reads)
-//      (P_k, Bs and Z_k are symmetric.)  Six D^3 products per step.
+//      (P_k, Bs and Z_k are symmetric.)  Four D^3 products per step: the
+//      transposes are LDS reads of the published copies, and P_k comes from
+//      the first kernel instead of X_k (X_k^T Bs).
 //   3. The normalisation VJP, Gb = dU_i, and Sb <- a Sb - Gb K_i^T + gS with
 //      K_i staged into B (row reads).
 // Mbar passes from chunk to chunk through the workspace as fp32 rows of their
@@ -244,14 +248,16 @@ scan_bwd_muon(const float* __restrict__ U, const float* __restrict__ K,
 template <int D>
 struct MuonBwdWs {
   // per (b, h) and chunk of the segment (local index c = i - i0):
-  // X_0 .. X_ns, Z_0 .. Z_{ns-1}, M_i; then Mbar and Sb per (b, h); then |M_i|
+  // X_0 .. X_ns, Z_0 .. Z_{ns-1}, P_0 .. P_{ns-1}, M_i; then Mbar and Sb per
+  // (b, h); then |M_i|
   int64_t mat, per_chunk, BH, nseg;
   GMDN_DEV MuonBwdWs(int64_t BH_, int64_t nseg_, int ns)
-      : mat((int64_t)D * D), per_chunk((2 * ns + 2) * mat), BH(BH_), nseg(nseg_) {}
+      : mat((int64_t)D * D), per_chunk((3 * ns + 2) * mat), BH(BH_), nseg(nseg_) {}
   GMDN_DEV int64_t slot(int64_t bh, int c) const { return bh * nseg + c; }
   GMDN_DEV float* X(float* ws, int64_t sl, int k) const { return ws + sl * per_chunk + k * mat; }
   GMDN_DEV float* Z(float* ws, int64_t sl, int ns, int k) const { return ws + sl * per_chunk + (ns + 1 + k) * mat; }
-  GMDN_DEV float* M(float* ws, int64_t sl, int ns) const { return ws + sl * per_chunk + (2 * ns + 1) * mat; }
+  GMDN_DEV float* P(float* ws, int64_t sl, int ns, int k) const { return ws + sl * per_chunk + (2 * ns + 1 + k) * mat; }
+  GMDN_DEV float* M(float* ws, int64_t sl, int ns) const { return ws + sl * per_chunk + (3 * ns + 1) * mat; }
   GMDN_DEV float* Mbar(float* ws, int64_t bh) const { return ws + BH * nseg * per_chunk + bh * mat; }
   GMDN_DEV float* Sbar(float* ws, int64_t bh) const { return ws + BH * nseg * per_chunk + (BH + bh) * mat; }
   GMDN_DEV float* norm(float* ws) const { return ws + BH * nseg * per_chunk + 2 * BH * mat; }
@@ -311,7 +317,7 @@ scan_bwd_muon_pre(const float* __restrict__ U, const float* __restrict__ K,
   for (int t = 0; t < NT; ++t) X[t] = X[t] * scale;
   for (int k = 0; k < ns; ++k) {
     NSX::store_own(W.X(ws, sl, k), X);
-    nsx.step(X, SA, SB, W.Z(ws, sl, ns, k));
+    nsx.step(X, SA, SB, W.Z(ws, sl, ns, k), W.P(ws, sl, ns, k));
   }
   NSX::store_own(W.X(ws, sl, ns), X);
 }
@@ -376,6 +382,7 @@ scan_bwd_muon_x3(const float* __restrict__ K, const float* __restrict__ av,
     }
     for (int k = ns - 1; k >= 0; --k) {
       f32x4 Q[NT], Bs[NT];
+      Op Bp[NKB];  // P_k's own rows, loaded where Y needs them
       {
         Op Bz[NKB];
         NSX::load_own(W.Z(ws, sl, ns, k), Bz);
@@ -385,36 +392,39 @@ scan_bwd_muon_x3(const float* __restrict__ K, const float* __restrict__ av,
       }
       __builtin_amdgcn_sched_barrier(0);  // keep the phases' operands apart
       {
-        // the wave's own rows of X_k (B) and Xbar (A) as B operands, read
-        // from the published planes one k-block at a time
+        // Bbar[r'][r] = sum_k Xbar[r'][k] X_k[r][k]: the wave's own rows of
+        // X_k (B) as the B operand, read one k-block at a time
         const int w = wave_id();
 #pragma unroll
         for (int tr = 0; tr < NT; ++tr) Bs[tr] = zero4();
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb) {
-          const Op ok = nsx.row(SB, w, kb), ox = nsx.row(SA, w, kb);
+          const Op ok = nsx.row(SB, w, kb);
 #pragma unroll
-          for (int tr = 0; tr < NT; ++tr) {
-            Bs[tr] = P::mma(nsx.row(SA, tr, kb), ok, Bs[tr]);  // Bbar[r'][r]
-            Bs[tr] = P::mma(nsx.row(SB, tr, kb), ox, Bs[tr]);  // Bbar[r][r']
-          }
+          for (int tr = 0; tr < NT; ++tr) Bs[tr] = P::mma(nsx.row(SA, tr, kb), ok, Bs[tr]);
         }
       }
-      __builtin_amdgcn_sched_barrier(0);
+      __syncthreads();  // every read of Xbar in A done
+      nsx.publish(SA, Bs);
+      __syncthreads();
+      // Bs = Bbar + Bbar^T, the transpose read back from the published copy
+#pragma unroll
+      for (int tr = 0; tr < NT; ++tr) Bs[tr] += NSX::tview(SA, tb, tr);
+      __syncthreads();  // every transposed read of A done
+      nsx.publish(SA, Bs);  // Bs is symmetric
+      __syncthreads();
       f32x4 Y[NT];
       {
-        Op Bso[NKB], Wo[NKB];
-        NSX::pack_all(Bs, Bso);
-        f32x4 Wt[NT];
-#pragma unroll
-        for (int tc = 0; tc < NT; ++tc) Wt[tc] = zero4();
-        nsx.colprod_all(SB, Bso, Wt);  // (X_k^T Bs)[c][r]
-        NSX::pack_all(Wt, Wo);
+        // Y[r'][r] = (Bs P_k)[r'][r]: P_k's own rows (= columns) as the B operand
+        NSX::load_own(W.P(ws, sl, ns, k), Bp);
 #pragma unroll
         for (int tr = 0; tr < NT; ++tr) Y[tr] = zero4();
-        nsx.rowprod_all(SB, Wo, Y);    // (X_k W)[r'][r]
+        nsx.rowprod_all(SA, Bp, Y);
       }
-      __syncthreads();  // every read of Xbar in A done
+      // X_{k-1}'s pieces for B, in flight through the Y exchange and the last product
+      bf16x8 xn[NT];
+      if (k > 0) NSX::load_pieces(W.X(ws, sl, k - 1), xn);
+      __syncthreads();  // every read of Bs in A done
       nsx.publish(SA, Y);  // A holds Y^T
       __syncthreads();
       {
@@ -429,21 +439,26 @@ scan_bwd_muon_x3(const float* __restrict__ K, const float* __restrict__ av,
       __syncthreads();  // every read of A and B done
       if (k > 0) {
         nsx.publish(SA, X);
-        nsx.stage_own(SB, W.X(ws, sl, k - 1));
+        nsx.store_pieces(SB, xn);
         __syncthreads();
       }
     }
     // ---- 3. normalisation: Mbar = Xbar/nrm - <Xbar, M_i>/nrm^2 * M_i/max(|M_i|, 1e-12)
+    // (the rows of M_i and M_{i-1} are loaded together with K_i's: one memory
+    // latency instead of three; loading Mbar and gS with them as well spills)
     const float* WM = W.M(ws, sl, ns);
     const float nf = W.norm(ws)[sl];
     const float nrm = nf + 1e-7f;
-    float pdot = 0.f;
+    f32x4 Mi[NT], Mp[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const f32x4 Mi = *reinterpret_cast<const f32x4*>(WM + roff(t));
-      pdot += X[t][0] * Mi[0] + X[t][1] * Mi[1] + X[t][2] * Mi[2] + X[t][3] * Mi[3];
+      Mi[t] = *reinterpret_cast<const f32x4*>(WM + roff(t));
+      Mp[t] = *reinterpret_cast<const f32x4*>(M_all + si * mat + roff(t));
     }
     NSX::template stage<D * 4>(SB, K + si * mat);  // K_i, for the row reads of the Sb update
+    float pdot = 0.f;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) pdot += X[t][0] * Mi[t][0] + X[t][1] * Mi[t][1] + X[t][2] * Mi[t][2] + X[t][3] * Mi[t][3];
     const float dot = block_sum<NW>(pdot, red);     // (its barriers also publish K_i in B)
     const float cM = dot / (nrm * nrm) / fmaxf(nf, 1e-12f);
     float pdm = 0.f;
@@ -452,11 +467,9 @@ scan_bwd_muon_x3(const float* __restrict__ K, const float* __restrict__ av,
       f32x4 Gb[NT];
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        const f32x4 Mi = *reinterpret_cast<const f32x4*>(WM + roff(t));
-        const f32x4 Mp = *reinterpret_cast<const f32x4*>(M_all + si * mat + roff(t));
         const f32x4 Mb = i == N - 1 ? zero4() : *reinterpret_cast<const f32x4*>(WMb + roff(t));
-        const f32x4 Mtot = Mb + X[t] / nrm - cM * Mi;
-        pdm += Mtot[0] * Mp[0] + Mtot[1] * Mp[1] + Mtot[2] * Mp[2] + Mtot[3] * Mp[3];
+        const f32x4 Mtot = Mb + X[t] / nrm - cM * Mi[t];
+        pdm += Mtot[0] * Mp[t][0] + Mtot[1] * Mp[t][1] + Mtot[2] * Mp[t][2] + Mtot[3] * Mp[t][3];
         *reinterpret_cast<f32x4*>(WMb + roff(t)) = gm * Mtot;
         Gb[t] = Mtot;
         *reinterpret_cast<f32x4*>(dU + si * mat + roff(t)) = Mtot;
