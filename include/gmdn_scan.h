@@ -93,7 +93,8 @@ int gmdn_scan_fwd(const float* U, const float* K, const float* a, const float* b
  * keeps per-row-tile partial sums of its scalar gradients.  Muon ('tf32')
  * runs the chunks in segments from the end and keeps, per chunk of a segment
  * and (b, h), the Newton-Schulz iterates X_0 .. X_ns, the products
- * Z_0 .. Z_{ns-1} and M_i (2 ns + 2 dh^2 floats) and |M_i|, plus two carried
+ * Z_0 .. Z_{ns-1}, P_0 .. P_{ns-1} and M_i (3 ns + 2 dh^2 floats) and |M_i|,
+ * plus two carried
  * dh^2 matrices per (b, h); the size returned here has as many chunks per
  * segment as fit in 512 MiB (at least one, at most N), and gmdn_scan_bwd also
  * accepts any smaller workspace down to one-chunk segments, using as many

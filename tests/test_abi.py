@@ -72,17 +72,17 @@ def test_scan_bwd_workspace_contract():
     lib = _native.load()
     assert lib.gmdn_scan_bwd_workspace_bytes(4, 16, 64, 0, 3) == 0
     assert lib.gmdn_scan_bwd_workspace_bytes(4, 16, 64, 2, 3) == 4 * 16 * 4 * 4 * 4
-    # muon: per chunk of a segment 2 ns + 2 d x d matrices and |M_i|, per
+    # muon: per chunk of a segment 3 ns + 2 d x d matrices and |M_i|, per
     # (b, h) two carried matrices (at least the 4 + ns matrices per (b, h) of
     # the fp32 kernel); small problems are one segment of N chunks
     BH, N, mat = 4, 16, 64 * 64
     for ns in (1, 3, 5):
-        x3 = BH * N * ((2 * ns + 2) * mat + 1) + 2 * BH * mat
+        x3 = BH * N * ((3 * ns + 2) * mat + 1) + 2 * BH * mat
         assert lib.gmdn_scan_bwd_workspace_bytes(BH, N, 64, 1, ns) == 4 * max(x3, BH * (4 + ns) * mat)
     assert lib.gmdn_scan_bwd_workspace_bytes(1, 1, 64, 1, 0) == 4 * max(2 * mat + 1 + 2 * mat, 4 * mat)
     # large problems: segments of as many chunks as fit in 512 MiB
     BH, N, dh, ns = 32, 128, 128, 5
-    per = BH * ((2 * ns + 2) * dh * dh + 1)
+    per = BH * ((3 * ns + 2) * dh * dh + 1)
     nseg = ((512 << 20) // 4 - 2 * BH * dh * dh) // per
     assert 1 <= nseg < N
     assert lib.gmdn_scan_bwd_workspace_bytes(BH, N, dh, 1, ns) == 4 * (nseg * per + 2 * BH * dh * dh)

@@ -21,7 +21,7 @@ def _dev():
 
 def _segment_bytes(BH, nseg, dh, ns):
     mat = dh * dh
-    return 4 * (BH * nseg * ((2 * ns + 2) * mat + 1) + 2 * BH * mat)
+    return 4 * (BH * nseg * ((3 * ns + 2) * mat + 1) + 2 * BH * mat)
 
 
 def _bwd(lib, ins, S_all, M_all, gS, ns, ws_bytes):

@@ -70,10 +70,10 @@ def test_noalloc_matches_workspace_entry_point(rule, ns):
 
 
 def _muon_min_workspace(BH, dh, ns):
-    """Bytes of the muon backward's one-chunk segments: per (b, h) 2 ns + 2
+    """Bytes of the muon backward's one-chunk segments: per (b, h) 3 ns + 2
     dh^2 matrices and |M_i|, plus the two carried dh^2 matrices."""
     mat = dh * dh
-    return 4 * (BH * ((2 * ns + 2) * mat + 1) + 2 * BH * mat)
+    return 4 * (BH * ((3 * ns + 2) * mat + 1) + 2 * BH * mat)
 
 
 def test_noalloc_refuses_problems_beyond_the_scratch():
