@@ -156,6 +156,29 @@ struct NSwz {
   static GMDN_DEV int off(int r, int c) { return r * COLS + ((((c >> 3) ^ f(r)) << 3) | (c & 7)); }
 };
 
+// Row swizzle of the Newton-Schulz planes (stored column order of NSSplit).
+// LDS serves a 16-byte access in cycles of 16 lanes -- within each half of
+// the wave, the four-lane quads q = 0..7 of equal parity of popcount(q) --
+// and an 8-byte access in cycles of 32 consecutive lanes, 64 banks of 4 bytes
+// (measured on gfx950).  Among the XOR swizzles linear in the row bits, f
+// below makes the planes' 16-byte row reads conflict-free and leaves their
+// transposing column reads two-way, the least that the stored column order
+// allows (those touch one 8-byte half of four groups in each of eight rows).
+template <int COLS>
+struct NSPlaneSwz {
+  static constexpr int GPR = COLS / 8;  // 16-byte groups per row
+  static constexpr int MASK = 15;       // the pattern repeats every 16 rows
+  static GMDN_DEV int f(int r) {
+    if constexpr (COLS >= 128)
+      return ((r & 1) << 3) | ((r & 2) << 1) | ((r & 4) >> 1);
+    else if constexpr (COLS == 64)
+      return ((r & 2) << 1) | ((r & 4) >> 1);
+    else
+      return (r & 4) >> 1;
+  }
+  static GMDN_DEV int xr(int r) { return f(r); }
+  static GMDN_DEV int off(int r, int c) { return r * COLS + ((((c >> 3) ^ f(r)) << 3) | (c & 7)); }
+};
 
 // Byte offset of element (r, c) of a swizzled bf16 tile (c % 4 == 0 for the
 // 8-byte pieces the kernels read).
