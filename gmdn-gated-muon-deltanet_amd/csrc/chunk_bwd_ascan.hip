@@ -89,7 +89,7 @@ struct AScanLds {
 
 template <int D>
 __global__ void __launch_bounds__(ASC_THREADS) chunk_bwd_ascan(ChunkArgs p) {
-  using LQ = NSwz<D>;      // Q, K tiles
+  using LQ = RowSwz<D>;    // Q, K tiles
   using LC = BSwz<16>;     // the workgroup's V, dO columns
   using LR = BSwz<128>;    // float32 / piece rows (256 bytes, as 128 bf16)
   using L = AScanLds<D>;

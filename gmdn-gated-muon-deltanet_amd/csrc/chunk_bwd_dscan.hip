@@ -75,7 +75,7 @@ template <int D>
 __global__ void __launch_bounds__(DSC_THREADS) chunk_bwd_dscan(ChunkArgs p) {
   // Q, K tiles: the row swizzle under which the permuted transposing reads
   // (four rows by four 16-byte groups per 16 lanes) hit 16 distinct groups
-  using LQ = NSwz<D>;
+  using LQ = RowSwz<D>;
   using LO = BSwz<32>;
   using L = DScanLds<D>;
   constexpr int NKB = D / 32;  // k-blocks over the state's columns

@@ -43,8 +43,8 @@ struct PairLds {
 template <int D>
 struct PairCtx {
   static constexpr int NKB = D / 32;
-  using LQ = BSwz<D>;
-  using LA = BSwz<CB_C>;
+  using LQ = PairSwz<D>;
+  using LA = PairSwz<CB_C>;
   using L = PairLds<D>;
   char* smem;
   const ChunkArgs* p;

@@ -104,9 +104,8 @@ struct FwdRowsLds {
 
 template <int D, int RULE>
 __global__ void __launch_bounds__(fd_threads<RULE>()) chunk_fwd_rows(ChunkArgs p) {
-  // Q, K tiles: the row swizzle whose transposing reads of four rows by
-  // four 16-byte groups (G's permuted K^T operand) hit 16 distinct groups
-  using LQ = NSwz<D>;
+  // Q, K tiles: conflict-free row operands, two-way permuted K^T operands
+  using LQ = RowSwz<D>;
   using LV = BSwz<32>;
   using L = FwdRowsLds<D, RULE>;
   constexpr int NKB = D / 32;  // k-blocks over the state's columns

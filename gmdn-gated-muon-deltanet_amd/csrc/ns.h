@@ -152,7 +152,7 @@ struct NSBlock {
 
 // The forward quintic step with bf16x3 products and the shared matrices kept
 // as split bf16 planes in LDS (hi plane then lo plane, each D x D in the
-// 16-byte-group XOR swizzle NSPlaneSwz).  Within every 32 columns
+// 16-byte-group XOR swizzle RowSwz).  Within every 32 columns
 // the 4-column blocks are stored in the order 0 4 1 5 2 6 3 7, so the eight
 // values of a row operand in the pair k order of the register operands
 // (columns 4G .. 4G+3 and 16+4G .. 16+4G+3) are one 16-byte row read per
@@ -167,7 +167,7 @@ struct NSSplit {
   static constexpr uint32_t PLANE = (uint32_t)D * D * 2;  // bytes of one plane
   static constexpr uint32_t BYTES = 2 * PLANE;             // one published matrix
   static constexpr uint32_t ROWB = D * 2;                  // bytes per row of a plane
-  using L = NSPlaneSwz<D>;
+  using L = RowSwz<D>;
   using P = PrecX3;
   using Op = P::Op;
   static_assert(L::MASK < 16, "row tiles of 16 must keep the swizzle");

@@ -156,16 +156,20 @@ struct NSwz {
   static GMDN_DEV int off(int r, int c) { return r * COLS + ((((c >> 3) ^ f(r)) << 3) | (c & 7)); }
 };
 
-// Row swizzle of the Newton-Schulz planes (stored column order of NSSplit).
-// LDS serves a 16-byte access in cycles of 16 lanes -- within each half of
-// the wave, the four-lane quads q = 0..7 of equal parity of popcount(q) --
-// and an 8-byte access in cycles of 32 consecutive lanes, 64 banks of 4 bytes
-// (measured on gfx950).  Among the XOR swizzles linear in the row bits, f
-// below makes the planes' 16-byte row reads conflict-free and leaves their
-// transposing column reads two-way, the least that the stored column order
-// allows (those touch one 8-byte half of four groups in each of eight rows).
+// LDS bank model (measured on gfx950 with SQ_LDS_BANK_CONFLICT): 64 banks of
+// 4 bytes; a 16-byte access is served in cycles of 16 lanes -- within each
+// half of the wave, the four-lane quads q = 0..7 of equal parity of
+// popcount(q) -- and an 8-byte access (ds_read_b64, ds_read_b64_tr_b16) in
+// cycles of 32 consecutive lanes.  The swizzles below are the XOR patterns
+// linear in the row bits that do best under it for the access patterns named.
+//
+// RowSwz: 16-byte row reads (16 rows x one group per lane group) are
+// conflict-free; the transposing reads that take four rows x 8-byte pieces
+// of four groups (the Newton-Schulz planes' column operands in their stored
+// column order; the K^T operands of the delta forward and reverse scans,
+// columns 8 (i % 4) + 4u) are two-way, the least those patterns allow.
 template <int COLS>
-struct NSPlaneSwz {
+struct RowSwz {
   static constexpr int GPR = COLS / 8;  // 16-byte groups per row
   static constexpr int MASK = 15;       // the pattern repeats every 16 rows
   static GMDN_DEV int f(int r) {
@@ -175,6 +179,24 @@ struct NSPlaneSwz {
       return ((r & 2) << 1) | ((r & 4) >> 1);
     else
       return (r & 4) >> 1;
+  }
+  static GMDN_DEV int xr(int r) { return f(r); }
+  static GMDN_DEV int off(int r, int c) { return r * COLS + ((((c >> 3) ^ f(r)) << 3) | (c & 7)); }
+};
+
+// PairSwz: 16-byte row reads, natural-order transposing column reads (col8:
+// rows 8G + i/4, columns 4 (i % 4)) and 8-byte row pieces are conflict-free;
+// the permuted transposing reads (col8p: columns 8 (i % 4)) two-way.  For the
+// token-gradient kernels, which use all four.
+template <int COLS>
+struct PairSwz {
+  static constexpr int GPR = COLS / 8;  // 16-byte groups per row
+  static constexpr int MASK = 15;       // the pattern repeats every 16 rows
+  static GMDN_DEV int f(int r) {
+    if constexpr (COLS >= 128)
+      return ((r & 1) << 3) ^ ((r & 2) << 1) ^ (((r >> 2) & 1) * 3) ^ (((r >> 3) & 1) * 2);
+    else
+      return ((r & 2) << 1) ^ (((r >> 2) & 1) * 3) ^ (((r >> 3) & 1) * 2);
   }
   static GMDN_DEV int xr(int r) { return f(r); }
   static GMDN_DEV int off(int r, int c) { return r * COLS + ((((c >> 3) ^ f(r)) << 3) | (c & 7)); }
