@@ -265,20 +265,39 @@ struct NSSplit {
     return acc;
   }
   // All NT tiles of a product at once, k-block outer: consecutive MFMAs go
-  // to independent accumulators and a k-block's reads issue together.
+  // to independent accumulators.  The operands are software-pipelined PIPE
+  // ahead of their MFMAs (a scheduling barrier per step keeps the order): left
+  // to itself, at the register pressure of the scan kernels, the compiler
+  // waits for each operand read right before its MFMAs, exposing the LDS
+  // latency on every read.
+  static constexpr int PIPE = 2;
   // acc[tr] += tile [r'][r] = sum_k pub[r'][k] B[k][r]
   GMDN_DEV void rowprod_all(lds_cptr pub, const Op (&B)[NKB], f32x4 (&acc)[NT]) const {
+    constexpr int NJ = NKB * NT;
+    Op a[PIPE];
 #pragma unroll
-    for (int kb = 0; kb < NKB; ++kb)
+    for (int j = 0; j < PIPE; ++j) a[j] = row(pub, j % NT, j / NT);
 #pragma unroll
-      for (int tr = 0; tr < NT; ++tr) acc[tr] = P::mma(row(pub, tr, kb), B[kb], acc[tr]);
+    for (int j = 0; j < NJ; ++j) {
+      const Op cur = a[j % PIPE];
+      if (j + PIPE < NJ) a[j % PIPE] = row(pub, (j + PIPE) % NT, (j + PIPE) / NT);
+      __builtin_amdgcn_sched_barrier(0);
+      acc[j % NT] = P::mma(cur, B[j / NT], acc[j % NT]);
+    }
   }
   // acc[tc] += tile [c][r] = sum_k pub[k][c] B[k][r]
   GMDN_DEV void colprod_all(lds_cptr pub, const Op (&B)[NKB], f32x4 (&acc)[NT]) const {
+    constexpr int NJ = NKB * NT;
+    Op a[PIPE];
 #pragma unroll
-    for (int kb = 0; kb < NKB; ++kb)
+    for (int j = 0; j < PIPE; ++j) a[j] = col(pub, j / NT, j % NT);
 #pragma unroll
-      for (int tc = 0; tc < NT; ++tc) acc[tc] = P::mma(col(pub, kb, tc), B[kb], acc[tc]);
+    for (int j = 0; j < NJ; ++j) {
+      const Op cur = a[j % PIPE];
+      if (j + PIPE < NJ) a[j % PIPE] = col(pub, (j + PIPE) / NT, (j + PIPE) % NT);
+      __builtin_amdgcn_sched_barrier(0);
+      acc[j % NT] = P::mma(cur, B[j / NT], acc[j % NT]);
+    }
   }
   // stage_own in two halves, so that the loads can be issued early
   static GMDN_DEV void load_pieces(const float* g, bf16x8 (&pc)[NT]) {
