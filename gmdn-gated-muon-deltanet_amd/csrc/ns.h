@@ -285,6 +285,24 @@ struct NSSplit {
       acc[j % NT] = P::mma(cur, B[j / NT], acc[j % NT]);
     }
   }
+  // rowprod_all with the B operand the wave's own rows of the planes at bm
+  // (row tile w), each k-block's read one k-block ahead
+  GMDN_DEV void rowprod_own(lds_cptr pub, lds_cptr bm, f32x4 (&acc)[NT]) const {
+    const int w = wave_id();
+    constexpr int NJ = NKB * NT;
+    Op a[PIPE], b[2];
+    b[0] = row(bm, w, 0);
+#pragma unroll
+    for (int j = 0; j < PIPE; ++j) a[j] = row(pub, j % NT, j / NT);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const Op cur = a[j % PIPE];
+      if (j + PIPE < NJ) a[j % PIPE] = row(pub, (j + PIPE) % NT, (j + PIPE) / NT);
+      if (j % NT == 0 && j / NT + 1 < NKB) b[(j / NT + 1) & 1] = row(bm, w, j / NT + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      acc[j % NT] = P::mma(cur, b[(j / NT) & 1], acc[j % NT]);
+    }
+  }
   // acc[tc] += tile [c][r] = sum_k pub[k][c] B[k][r]
   GMDN_DEV void colprod_all(lds_cptr pub, const Op (&B)[NKB], f32x4 (&acc)[NT]) const {
     constexpr int NJ = NKB * NT;

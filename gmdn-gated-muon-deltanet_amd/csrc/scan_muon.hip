@@ -375,6 +375,10 @@ scan_bwd_muon_x3(const float* __restrict__ K, const float* __restrict__ av,
     f32x4 X[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) X[t] = gb * Sb[t];
+    // Sb waits in its workspace rows through the VJP steps (their registers
+    // are the scarce resource there); the tail reads it back
+#pragma unroll
+    for (int t = 0; t < NT; ++t) *reinterpret_cast<f32x4*>(WSb + roff(t)) = Sb[t];
     if (ns > 0) {
       nsx.publish(SA, X);
       nsx.stage_own(SB, W.X(ws, sl, ns - 1));
@@ -393,16 +397,10 @@ scan_bwd_muon_x3(const float* __restrict__ K, const float* __restrict__ av,
       __builtin_amdgcn_sched_barrier(0);  // keep the phases' operands apart
       {
         // Bbar[r'][r] = sum_k Xbar[r'][k] X_k[r][k]: the wave's own rows of
-        // X_k (B) as the B operand, read one k-block at a time
-        const int w = wave_id();
+        // X_k (B) as the B operand
 #pragma unroll
         for (int tr = 0; tr < NT; ++tr) Bs[tr] = zero4();
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb) {
-          const Op ok = nsx.row(SB, w, kb);
-#pragma unroll
-          for (int tr = 0; tr < NT; ++tr) Bs[tr] = P::mma(nsx.row(SA, tr, kb), ok, Bs[tr]);
-        }
+        nsx.rowprod_own(SA, SB, Bs);
       }
       __syncthreads();  // every read of Xbar in A done
       nsx.publish(SA, Bs);
@@ -454,6 +452,7 @@ scan_bwd_muon_x3(const float* __restrict__ K, const float* __restrict__ av,
     for (int t = 0; t < NT; ++t) {
       Mi[t] = *reinterpret_cast<const f32x4*>(WM + roff(t));
       Mp[t] = *reinterpret_cast<const f32x4*>(M_all + si * mat + roff(t));
+      Sb[t] = *reinterpret_cast<const f32x4*>(WSb + roff(t));
     }
     NSX::template stage<D * 4>(SB, K + si * mat);  // K_i, for the row reads of the Sb update
     float pdot = 0.f;
@@ -480,12 +479,8 @@ scan_bwd_muon_x3(const float* __restrict__ K, const float* __restrict__ av,
     const float dmv = block_sum<NW>(pdm, red);
     // Sb <- a Sb - Gb K^T + gS : A = K rows
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      f32x4 acc = ga * Sb[t] + *reinterpret_cast<const f32x4*>(gS + si * mat + roff(t));
-#pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) acc = P::mma(nsx.row(SB, t, kb), Bg[kb], acc);
-      Sb[t] = acc;
-    }
+    for (int t = 0; t < NT; ++t) Sb[t] = ga * Sb[t] + *reinterpret_cast<const f32x4*>(gS + si * mat + roff(t));
+    nsx.rowprod_all(SB, Bg, Sb);
     if (threadIdx.x == 0) {
       da[si] = dav;
       db[si] = dbv;
