@@ -130,16 +130,22 @@ struct PairCtx {
       Y[kt].v[0] = col8<LQ>(Yh, 32 * kt, r0);
       if constexpr (PB == 2) Y[kt].v[1] = col8<LQ>(Yl, 32 * kt, r0);
     }
+    // the X operands software-pipelined two ahead of their MFMAs (left to
+    // itself the compiler waits for each read right before its MFMA)
+    constexpr int NJ = NKB * 4, PIPE = 2;
+    auto xop = [&](int j) { return col8p<LQ>(X, 32 * (j & 1), 32 * (j >> 2) + 4 * ((j >> 1) & 1)); };
+    bf16x8 xs[PIPE];
 #pragma unroll
-    for (int kb = 0; kb < NKB; ++kb)
+    for (int j = 0; j < PIPE; ++j) xs[j] = xop(j);
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-          bf16x8 x = col8p<LQ>(X, 32 * kt, 32 * kb + 4 * u);
-          if constexpr (NEG) x = neg8(x);
-          acc[kb][u] = mma<1, PB>(Op<1>{{x}}, Y[kt], acc[kb][u]);
-        }
+    for (int j = 0; j < NJ; ++j) {
+      bf16x8 x = xs[j % PIPE];
+      if (j + PIPE < NJ) xs[j % PIPE] = xop(j + PIPE);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (NEG) x = neg8(x);
+      const int kb = j >> 2, u = (j >> 1) & 1, kt = j & 1;
+      acc[kb][u] = mma<1, PB>(Op<1>{{x}}, Y[kt], acc[kb][u]);
+    }
   }
 
   // The gradients of chunk i, whose q, k tiles and gates are in LDS (the v,
