@@ -225,7 +225,8 @@ def drop_in_leg(w, steps: int, warmup: int) -> dict:
     fwd_f, bwd_f = drop_in_flops_per_chunk(w.rule, d, w.ns)
     fwd_flops, bwd_flops = fwd_f * chunks, bwd_f * chunks
     return {"op": "fast_state_scan", "shape": {"B": B, "H": H, "N": N, "d": d, "rule": w.rule, "ns": w.ns},
-            "precision": "tf32 (bf16x3 split products)",
+            "precision": ("tf32 (bf16x3 split products); fwd+bwd in exact float32 (adam keeps its moments)"
+                          if w.rule == "adam" else "tf32 (bf16x3 split products)"),
             "fwd_tokens_per_s": B * N * w.chunk / (fwd_ms * 1e-3),
             "fwd_bwd_tokens_per_s": B * N * w.chunk / (fb_ms * 1e-3),
             "roofline_fwd": roof(fwd_ms, fwd_b * chunks, fwd_flops),
