@@ -37,6 +37,26 @@ GMDN_DEV float block_sum(float x, float* red) {
   return t;
 }
 
+// block_sum of two values under one pair of barriers (red: 2 NW floats); each
+// sum is formed in the order block_sum uses
+template <int NW>
+GMDN_DEV f32x2 block_sum2(float x, float y, float* red) {
+  const f32x2 s = wave_sum2(x, y);
+  if (lane_id() == 0) {
+    red[2 * wave_id()] = s[0];
+    red[2 * wave_id() + 1] = s[1];
+  }
+  __syncthreads();
+  f32x2 t = {0.f, 0.f};
+#pragma unroll
+  for (int q = 0; q < NW; ++q) {
+    t[0] += red[2 * q];
+    t[1] += red[2 * q + 1];
+  }
+  __syncthreads();
+  return t;
+}
+
 template <class P, class L, int D>
 struct NSBlock {
   static constexpr int NT = D / 16;
@@ -348,6 +368,16 @@ struct NSSplit {
     const int l = lane_id(), row = 16 * wave_id() + (l & 15);
 #pragma unroll
     for (int c = 0; c < NT; ++c) *reinterpret_cast<bf16x8*>(g + row * D + 16 * c + 4 * (l >> 4)) = split_piece(t[c]);
+  }
+  // operands of the wave's rows from pieces already loaded by load_pieces
+  // (register moves only: placed right before their product, they do not
+  // make the loads wait early)
+  static GMDN_DEV void own_ops(const bf16x8 (&pc)[NT], Op (&o)[NKB]) {
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      o[kb].hi = __builtin_shufflevector(pc[2 * kb], pc[2 * kb + 1], 0, 1, 2, 3, 8, 9, 10, 11);
+      o[kb].lo = __builtin_shufflevector(pc[2 * kb], pc[2 * kb + 1], 4, 5, 6, 7, 12, 13, 14, 15);
+    }
   }
   // operands of the wave's rows from those pieces (the split of pack_all)
   static GMDN_DEV void load_own(const float* g, Op (&o)[NKB]) {

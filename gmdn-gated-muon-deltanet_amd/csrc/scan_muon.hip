@@ -15,6 +15,8 @@
 #include "ns.h"
 #include "scan_a.h"
 
+#include <type_traits>
+
 namespace gmdn {
 
 template <int D, int PREC>
@@ -225,7 +227,9 @@ scan_bwd_muon(const float* __restrict__ U, const float* __restrict__ K,
 // 3 ns + 2 matrices.
 //
 // scan_bwd_muon_x3, one workgroup per (b, h), chunks in reverse order:
-//   1. da_i = <Sb, S_i>, db_i = <Sb, X_ns>; Xbar = b Sb.
+//   1. da_i = <Sb, S_i>, db_i = <Sb, X_ns> (S_i, X_ns and gS requested at
+//      the end of the previous chunk); Xbar = b Sb; a Sb + gS parked in Sb's
+//      workspace rows until the tail.
 //   2. The VJP steps, k = ns-1 .. 0, with Xbar published in A and X_k in B:
 //        Q    = a Xbar + Z_k Xbar                 (A column reads, Z_k rows)
 //        Bbar = Xbar X_k^T                        (A and B row reads)
@@ -236,8 +240,9 @@ scan_bwd_muon(const float* __restrict__ U, const float* __restrict__ K,
 //      (P_k, Bs and Z_k are symmetric.)  Four D^3 products per step: the
 //      transposes are LDS reads of the published copies, and P_k comes from
 //      the first kernel instead of X_k (X_k^T Bs).
-//   3. The normalisation VJP, Gb = dU_i, and Sb <- a Sb - Gb K_i^T + gS with
-//      K_i staged into B (row reads).
+//   3. The normalisation VJP, Gb = dU_i, and Sb <- (a Sb + gS) - Gb K_i^T
+//      with K_i staged into B (row reads).  Each phase issues its global
+//      loads together ahead of their first use.
 // Mbar passes from chunk to chunk through the workspace as fp32 rows of their
 // wave.
 //
@@ -346,7 +351,15 @@ scan_bwd_muon_x3(const float* __restrict__ K, const float* __restrict__ av,
   const int r0 = 16 * wave_id();
   const int64_t mat = (int64_t)D * D;
   float* WMb = W.Mbar(ws, bh);  // Mbar carried to chunk i-1
-  auto roff = [&](int t) { return (int64_t)(r0 + rl) * D + 16 * t + 4 * G; };
+  // 32-bit lane offsets, opaque at every use: the loads and stores then take
+  // a scalar base and one offset register; left visible, the compiler hoists
+  // a 64-bit address pair per array out of the chunk loop and spills them
+  const uint32_t lane_row = (uint32_t)((r0 + rl) * D + 4 * G);
+  auto roff = [&](int t) {
+    uint32_t o = lane_row;
+    asm volatile("" : "+v"(o));
+    return o + (uint32_t)(16 * t);
+  };
 
   // Sb from the segment after this one (zero after the last chunk)
   float* WSb = W.Sbar(ws, bh);
@@ -354,44 +367,83 @@ scan_bwd_muon_x3(const float* __restrict__ K, const float* __restrict__ av,
 #pragma unroll
   for (int t = 0; t < NT; ++t) Sb[t] = i1 == N ? zero4() : *reinterpret_cast<const f32x4*>(WSb + roff(t));
 
+  // Chunk i's first-phase inputs S_i, X_ns's pieces and gS, requested
+  // together and one chunk ahead (at the end of the previous chunk's tail),
+  // so that their latency is not exposed at the chunk's start.
+  f32x4 Si[NT], Gs[NT];
+  bf16x8 Xn[NT];
+  auto request_start = [&](int i) {
+    const int64_t si = bh * N + i;
+    const float* Xs = W.X(ws, W.slot(bh, i - i0), ns);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) Si[t] = *reinterpret_cast<const f32x4*>(S_all + si * mat + roff(t));
+#pragma unroll
+    for (int t = 0; t < NT; ++t) Xn[t] = *reinterpret_cast<const bf16x8*>(Xs + roff(t));
+#pragma unroll
+    for (int t = 0; t < NT; ++t) Gs[t] = *reinterpret_cast<const f32x4*>(gS + si * mat + roff(t));
+  };
+  request_start(i1 - 1);
+
   for (int i = i1 - 1; i >= i0; --i) {
     const int64_t si = bh * N + i, sl = W.slot(bh, i - i0);
     const float ga = av[si], gb = bv[si], gm = mv[si];
     // ---- 1. da_i = <Sb, S_i>, db_i = <Sb, msign(M_i)>
     float pda = 0.f, pdb = 0.f;
-    {
-      const float* Xs = W.X(ws, sl, ns);
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const f32x4 Si = *reinterpret_cast<const f32x4*>(S_all + si * mat + roff(t));
-        const f32x4 Xn = unsplit_piece(*reinterpret_cast<const bf16x8*>(Xs + roff(t)));
-        pda += Sb[t][0] * Si[0] + Sb[t][1] * Si[1] + Sb[t][2] * Si[2] + Sb[t][3] * Si[3];
-        pdb += Sb[t][0] * Xn[0] + Sb[t][1] * Xn[1] + Sb[t][2] * Xn[2] + Sb[t][3] * Xn[3];
-      }
+    for (int t = 0; t < NT; ++t) {
+      const f32x4 Xs = unsplit_piece(Xn[t]);
+      pda += Sb[t][0] * Si[t][0] + Sb[t][1] * Si[t][1] + Sb[t][2] * Si[t][2] + Sb[t][3] * Si[t][3];
+      pdb += Sb[t][0] * Xs[0] + Sb[t][1] * Xs[1] + Sb[t][2] * Xs[2] + Sb[t][3] * Xs[3];
     }
-    const float dbv = block_sum<NW>(pdb, red);
-    const float dav = block_sum<NW>(pda, red);
+    const f32x2 dsum = block_sum2<NW>(pdb, pda, red);
+    const float dbv = dsum[0], dav = dsum[1];
     // ---- 2. Xbar = b Sb pulled back through the ns steps (X is its register home)
     f32x4 X[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) X[t] = gb * Sb[t];
-    // Sb waits in its workspace rows through the VJP steps (their registers
-    // are the scarce resource there); the tail reads it back
+    // The tail's a Sb + gS waits in Sb's workspace rows through the VJP
+    // steps (their registers are the scarce resource there).
+    auto park_sb = [&] {
 #pragma unroll
-    for (int t = 0; t < NT; ++t) *reinterpret_cast<f32x4*>(WSb + roff(t)) = Sb[t];
+      for (int t = 0; t < NT; ++t) *reinterpret_cast<f32x4*>(WSb + roff(t)) = ga * Sb[t] + Gs[t];
+    };
     if (ns > 0) {
       nsx.publish(SA, X);
-      nsx.stage_own(SB, W.X(ws, sl, ns - 1));
+      bf16x8 xs[NT];
+      NSX::load_pieces(W.X(ws, sl, ns - 1), xs);
+      park_sb();
+      nsx.store_pieces(SB, xs);
       __syncthreads();
+    } else {
+      park_sb();
     }
-    for (int k = ns - 1; k >= 0; --k) {
+    // the tail's M_i and Mbar rows, requested during the last VJP step
+    const float* WM = W.M(ws, sl, ns);
+    f32x4 Mi[NT], Mb[NT];
+    auto request_tail = [&] {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) Mi[t] = *reinterpret_cast<const f32x4*>(WM + roff(t));
+#pragma unroll
+      for (int t = 0; t < NT; ++t) Mb[t] = i == N - 1 ? zero4() : *reinterpret_cast<const f32x4*>(WMb + roff(t));
+    };
+    // One VJP step; the last one (k = 0) requests the tail's rows where the
+    // others request the next step's.  (Peeled, so that no register array is
+    // defined on one path of a step only: such an array stays live through
+    // every step.)
+    auto vjp_step = [&](int k, auto last_tag) {
+      constexpr bool LAST = decltype(last_tag)::value;
       f32x4 Q[NT], Bs[NT];
-      Op Bp[NKB];  // P_k's own rows, loaded where Y needs them
+      // Z_k's and P_k's own rows as pieces, P_k in flight through the first
+      // two products (Z_k requested a step ahead, in flight through the last
+      // product, measured slower: that product's operand reads wait behind it)
+      bf16x8 zr[NT], pr[NT];
+      NSX::load_pieces(W.Z(ws, sl, ns, k), zr);
+      NSX::load_pieces(W.P(ws, sl, ns, k), pr);
+#pragma unroll
+      for (int tc = 0; tc < NT; ++tc) Q[tc] = NS_A * X[tc];
       {
         Op Bz[NKB];
-        NSX::load_own(W.Z(ws, sl, ns, k), Bz);
-#pragma unroll
-        for (int tc = 0; tc < NT; ++tc) Q[tc] = NS_A * X[tc];
+        NSX::own_ops(zr, Bz);
         nsx.colprod_all(SA, Bz, Q);
       }
       __builtin_amdgcn_sched_barrier(0);  // keep the phases' operands apart
@@ -414,14 +466,21 @@ scan_bwd_muon_x3(const float* __restrict__ K, const float* __restrict__ av,
       f32x4 Y[NT];
       {
         // Y[r'][r] = (Bs P_k)[r'][r]: P_k's own rows (= columns) as the B operand
-        NSX::load_own(W.P(ws, sl, ns, k), Bp);
 #pragma unroll
         for (int tr = 0; tr < NT; ++tr) Y[tr] = zero4();
+        Op Bp[NKB];
+        __builtin_amdgcn_sched_barrier(0);
+        NSX::own_ops(pr, Bp);
         nsx.rowprod_all(SA, Bp, Y);
       }
-      // X_{k-1}'s pieces for B, in flight through the Y exchange and the last product
+      // the next step's X_{k-1} pieces for B (after the last step: the tail's
+      // rows), in flight through the Y exchange and the last product
       bf16x8 xn[NT];
-      if (k > 0) NSX::load_pieces(W.X(ws, sl, k - 1), xn);
+      if constexpr (!LAST) {
+        NSX::load_pieces(W.X(ws, sl, k - 1), xn);
+      } else {
+        request_tail();
+      }
       __syncthreads();  // every read of Bs in A done
       nsx.publish(SA, Y);  // A holds Y^T
       __syncthreads();
@@ -435,52 +494,54 @@ scan_bwd_muon_x3(const float* __restrict__ K, const float* __restrict__ av,
         for (int tc = 0; tc < NT; ++tc) X[tc] = Q[tc];
       }
       __syncthreads();  // every read of A and B done
-      if (k > 0) {
+      if constexpr (!LAST) {
         nsx.publish(SA, X);
         nsx.store_pieces(SB, xn);
         __syncthreads();
       }
-    }
+    };
+    for (int k = ns - 1; k >= 1; --k) vjp_step(k, std::false_type{});
+    if (ns > 0)
+      vjp_step(0, std::true_type{});
+    else
+      request_tail();
     // ---- 3. normalisation: Mbar = Xbar/nrm - <Xbar, M_i>/nrm^2 * M_i/max(|M_i|, 1e-12)
-    // (the rows of M_i and M_{i-1} are loaded together with K_i's: one memory
-    // latency instead of three; loading Mbar and gS with them as well spills)
-    const float* WM = W.M(ws, sl, ns);
     const float nf = W.norm(ws)[sl];
     const float nrm = nf + 1e-7f;
-    f32x4 Mi[NT], Mp[NT];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      Mi[t] = *reinterpret_cast<const f32x4*>(WM + roff(t));
-      Mp[t] = *reinterpret_cast<const f32x4*>(M_all + si * mat + roff(t));
-      Sb[t] = *reinterpret_cast<const f32x4*>(WSb + roff(t));
-    }
+    for (int t = 0; t < NT; ++t) Sb[t] = *reinterpret_cast<const f32x4*>(WSb + roff(t));  // a Sb + gS
     NSX::template stage<D * 4>(SB, K + si * mat);  // K_i, for the row reads of the Sb update
     float pdot = 0.f;
 #pragma unroll
     for (int t = 0; t < NT; ++t) pdot += X[t][0] * Mi[t][0] + X[t][1] * Mi[t][1] + X[t][2] * Mi[t][2] + X[t][3] * Mi[t][3];
     const float dot = block_sum<NW>(pdot, red);     // (its barriers also publish K_i in B)
     const float cM = dot / (nrm * nrm) / fmaxf(nf, 1e-12f);
-    float pdm = 0.f;
+    // M_{i-1} for dm, in flight through the Sb update
+    f32x4 Mp[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) Mp[t] = *reinterpret_cast<const f32x4*>(M_all + si * mat + roff(t));
+    f32x4 Mt[NT];  // dU_i = Gb_i, the total cotangent of M_i
+    const float rn = 1.f / nrm;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) Mt[t] = Mb[t] + X[t] * rn - cM * Mi[t];
     Op Bg[NKB];
-    {
-      f32x4 Gb[NT];
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const f32x4 Mb = i == N - 1 ? zero4() : *reinterpret_cast<const f32x4*>(WMb + roff(t));
-        const f32x4 Mtot = Mb + X[t] / nrm - cM * Mi[t];
-        pdm += Mtot[0] * Mp[t][0] + Mtot[1] * Mp[t][1] + Mtot[2] * Mp[t][2] + Mtot[3] * Mp[t][3];
-        *reinterpret_cast<f32x4*>(WMb + roff(t)) = gm * Mtot;
-        Gb[t] = Mtot;
-        *reinterpret_cast<f32x4*>(dU + si * mat + roff(t)) = Mtot;
-      }
-#pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) Bg[kb] = P::pack(-Gb[2 * kb], -Gb[2 * kb + 1]);
-    }
-    const float dmv = block_sum<NW>(pdm, red);
-    // Sb <- a Sb - Gb K^T + gS : A = K rows
-#pragma unroll
-    for (int t = 0; t < NT; ++t) Sb[t] = ga * Sb[t] + *reinterpret_cast<const f32x4*>(gS + si * mat + roff(t));
+    for (int kb = 0; kb < NKB; ++kb) Bg[kb] = P::pack(-Mt[2 * kb], -Mt[2 * kb + 1]);
+    // Sb <- a Sb + gS - Gb K^T : A = K rows
     nsx.rowprod_all(SB, Bg, Sb);
+    __builtin_amdgcn_sched_barrier(0);  // dm's wait for M_{i-1} after the product, not inside it
+    float pdm = 0.f;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) pdm += Mt[t][0] * Mp[t][0] + Mt[t][1] * Mp[t][1] + Mt[t][2] * Mp[t][2] + Mt[t][3] * Mp[t][3];
+    // (chunk i0 requests itself again: a def on one path only would keep the
+    // arrays live through the VJP steps)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      *reinterpret_cast<f32x4*>(WMb + roff(t)) = gm * Mt[t];
+      *reinterpret_cast<f32x4*>(dU + si * mat + roff(t)) = Mt[t];
+    }
+    request_start(i > i0 ? i - 1 : i0);
+    const float dmv = block_sum<NW>(pdm, red);
     if (threadIdx.x == 0) {
       da[si] = dav;
       db[si] = dbv;
