@@ -14,6 +14,8 @@
 #include "../../include/gmdn_front.h"
 #include "tile.h"
 
+#include <type_traits>
+
 namespace gmdn {
 namespace {
 
@@ -88,17 +90,19 @@ struct Raw8<float> {
 };
 
 // sum over the dh / 8 lanes of one head, in DPP moves (all lanes of the
-// wave take part): the two quad-permute steps sum each quad; a 128-wide head
-// is a 16-lane row (row_ror 4 and 8 add the other quads), a 64-wide head a
-// half-row (row_half_mirror adds the other quad of the 8)
+// wave take part; a head's lanes are an aligned group since D is a multiple
+// of dh): the first quad-permute step sums lane pairs (a 16-wide head), the
+// second each quad (32); a 128-wide head is a 16-lane row (row_ror 4 and 8
+// add the other quads), a 64-wide head a half-row (row_half_mirror adds the
+// other quad of the 8)
 template <int DH>
 GMDN_DEV float head_sum(float s) {
-  static_assert(DH == 64 || DH == 128, "head dims 64 and 128");
+  static_assert(DH == 16 || DH == 32 || DH == 64 || DH == 128, "head dims 16, 32, 64 and 128");
   s += dpp_mov<0xB1>(s);  // quad_perm [1,0,3,2]
-  s += dpp_mov<0x4E>(s);  // quad_perm [2,3,0,1]
+  if constexpr (DH >= 32) s += dpp_mov<0x4E>(s);  // quad_perm [2,3,0,1]
   if constexpr (DH == 64) {
     s += dpp_mov<0x141>(s);  // row_half_mirror
-  } else {
+  } else if constexpr (DH == 128) {
     s += dpp_mov<0x124>(s);  // row_ror:4
     s += dpp_mov<0x128>(s);  // row_ror:8
   }
@@ -341,7 +345,7 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 int check_front(const void* y, const float* w, const float* bias, int64_t B, int64_t T, int32_t D, int32_t dh,
                 int32_t K, int32_t dtype) {
   if (B < 0 || T < 0 || D <= 0 || K < 1 || K > FT_KMAX) return GMDN_ERR_ARG;
-  if (dh != 64 && dh != 128) return GMDN_ERR_UNSUPPORTED;
+  if (dh != 16 && dh != 32 && dh != 64 && dh != 128) return GMDN_ERR_UNSUPPORTED;
   if (D % dh) return GMDN_ERR_ARG;
   if (dtype != GMDN_DTYPE_BF16 && dtype != GMDN_DTYPE_F32) return GMDN_ERR_UNSUPPORTED;
   if (B * T == 0) return GMDN_OK;
@@ -374,6 +378,17 @@ hipError_t launch_bwd(const void* y, const float* w, const float* bias, const vo
   return hipGetLastError();
 }
 
+// f(std::integral_constant<int, DH>{}) for the built head dims
+template <class F>
+hipError_t with_dh(int dh, F&& f) {
+  switch (dh) {
+    case 16: return f(std::integral_constant<int, 16>{});
+    case 32: return f(std::integral_constant<int, 32>{});
+    case 64: return f(std::integral_constant<int, 64>{});
+    default: return f(std::integral_constant<int, 128>{});
+  }
+}
+
 }  // namespace
 }  // namespace gmdn
 
@@ -388,12 +403,11 @@ int gmdn_front_fwd(const void* y, const float* weight, const float* bias, void* 
   if (!q || !k || !v || !aligned16(q) || !aligned16(k) || !aligned16(v)) return GMDN_ERR_ARG;
   const hipStream_t st = (hipStream_t)stream;
   hipError_t e;
-  if (dtype == GMDN_DTYPE_BF16)
-    e = dh == 64 ? launch_fwd<bf16, 64>(y, weight, bias, q, k, v, B, T, D, K, st)
-                 : launch_fwd<bf16, 128>(y, weight, bias, q, k, v, B, T, D, K, st);
-  else
-    e = dh == 64 ? launch_fwd<float, 64>(y, weight, bias, q, k, v, B, T, D, K, st)
-                 : launch_fwd<float, 128>(y, weight, bias, q, k, v, B, T, D, K, st);
+  e = with_dh(dh, [&](auto c) {
+    constexpr int DH = decltype(c)::value;
+    return dtype == GMDN_DTYPE_BF16 ? launch_fwd<bf16, DH>(y, weight, bias, q, k, v, B, T, D, K, st)
+                                    : launch_fwd<float, DH>(y, weight, bias, q, k, v, B, T, D, K, st);
+  });
   return e == hipSuccess ? GMDN_OK : GMDN_ERR_LAUNCH;
 }
 
@@ -411,12 +425,11 @@ int gmdn_front_bwd(const void* y, const float* weight, const float* bias, const 
   if (!aligned16(dq) || !aligned16(dk) || !aligned16(dv) || !aligned16(dy)) return GMDN_ERR_ARG;
   const hipStream_t st = (hipStream_t)stream;
   hipError_t e;
-  if (dtype == GMDN_DTYPE_BF16)
-    e = dh == 64 ? launch_bwd<bf16, 64>(y, weight, bias, dq, dk, dv, dy, partial, B, T, D, K, st)
-                 : launch_bwd<bf16, 128>(y, weight, bias, dq, dk, dv, dy, partial, B, T, D, K, st);
-  else
-    e = dh == 64 ? launch_bwd<float, 64>(y, weight, bias, dq, dk, dv, dy, partial, B, T, D, K, st)
-                 : launch_bwd<float, 128>(y, weight, bias, dq, dk, dv, dy, partial, B, T, D, K, st);
+  e = with_dh(dh, [&](auto c) {
+    constexpr int DH = decltype(c)::value;
+    return dtype == GMDN_DTYPE_BF16 ? launch_bwd<bf16, DH>(y, weight, bias, dq, dk, dv, dy, partial, B, T, D, K, st)
+                                    : launch_bwd<float, DH>(y, weight, bias, dq, dk, dv, dy, partial, B, T, D, K, st);
+  });
   return e == hipSuccess ? GMDN_OK : GMDN_ERR_LAUNCH;
 }
 

@@ -14,6 +14,7 @@
 // gradient, summed per workgroup over its rows in LDS and then over the
 // workgroups by a second kernel (no atomics: the sum order is fixed).
 #include "../../include/gmdn_tail.h"
+#include <type_traits>
 #include "tile.h"
 
 namespace gmdn {
@@ -231,8 +232,22 @@ int check_gates(const void* y, int64_t B, int64_t T, int32_t H, int32_t nG, int3
   return GMDN_OK;
 }
 
+// head dims of the per-head norm: one row is d / 8 lanes of 8 elements
+bool norm_dim(int d) { return d == 16 || d == 32 || d == 64 || d == 128; }
+
+// f(std::integral_constant<int, D>{}) for the built head dims
+template <class F>
+void with_d(int d, F&& f) {
+  switch (d) {
+    case 16: f(std::integral_constant<int, 16>{}); break;
+    case 32: f(std::integral_constant<int, 32>{}); break;
+    case 64: f(std::integral_constant<int, 64>{}); break;
+    default: f(std::integral_constant<int, 128>{}); break;
+  }
+}
+
 int check_norm(const void* x, const float* w, int64_t rows, int32_t d, int32_t dtype) {
-  if (rows < 0 || (d != 64 && d != 128)) return rows < 0 ? GMDN_ERR_ARG : GMDN_ERR_UNSUPPORTED;
+  if (rows < 0 || !norm_dim(d)) return rows < 0 ? GMDN_ERR_ARG : GMDN_ERR_UNSUPPORTED;
   if (dtype != GMDN_DTYPE_BF16 && dtype != GMDN_DTYPE_F32) return GMDN_ERR_UNSUPPORTED;
   if (rows > 0 && (!x || !w || !aligned16(x))) return GMDN_ERR_ARG;
   return GMDN_OK;
@@ -282,26 +297,20 @@ int gmdn_head_norm_fwd(const void* x, const float* weight, void* out, float* rst
   if (!out || !rstd || !aligned16(out) || !(eps >= 0.f)) return GMDN_ERR_ARG;
   const dim3 grid((unsigned)hn_blocks(rows, d));
   const hipStream_t st = (hipStream_t)stream;
-  if (dtype == GMDN_DTYPE_BF16) {
-    if (d == 128)
-      hipLaunchKernelGGL((head_norm_fwd<bf16, 128>), grid, dim3(HN_THREADS), 0, st, (const bf16*)x, weight,
+  with_d(d, [&](auto c) {
+    constexpr int D = decltype(c)::value;
+    if (dtype == GMDN_DTYPE_BF16)
+      hipLaunchKernelGGL((head_norm_fwd<bf16, D>), grid, dim3(HN_THREADS), 0, st, (const bf16*)x, weight,
                          (bf16*)out, rstd, rows, eps);
     else
-      hipLaunchKernelGGL((head_norm_fwd<bf16, 64>), grid, dim3(HN_THREADS), 0, st, (const bf16*)x, weight,
-                         (bf16*)out, rstd, rows, eps);
-  } else {
-    if (d == 128)
-      hipLaunchKernelGGL((head_norm_fwd<float, 128>), grid, dim3(HN_THREADS), 0, st, (const float*)x, weight,
+      hipLaunchKernelGGL((head_norm_fwd<float, D>), grid, dim3(HN_THREADS), 0, st, (const float*)x, weight,
                          (float*)out, rstd, rows, eps);
-    else
-      hipLaunchKernelGGL((head_norm_fwd<float, 64>), grid, dim3(HN_THREADS), 0, st, (const float*)x, weight,
-                         (float*)out, rstd, rows, eps);
-  }
+  });
   return hipGetLastError() == hipSuccess ? GMDN_OK : GMDN_ERR_LAUNCH;
 }
 
 size_t gmdn_head_norm_bwd_workspace_floats(int64_t rows, int32_t d) {
-  if (rows <= 0 || (d != 64 && d != 128)) return 0;
+  if (rows <= 0 || !norm_dim(d)) return 0;
   return (size_t)hn_blocks(rows, d) * d;
 }
 
@@ -314,27 +323,22 @@ int gmdn_head_norm_bwd(const void* x, const float* weight, const float* rstd, co
   const int nb = hn_blocks(rows, d);
   if (!workspace || workspace_floats < (size_t)nb * d) return GMDN_ERR_WORKSPACE;
   const hipStream_t st = (hipStream_t)stream;
-  if (dtype == GMDN_DTYPE_BF16) {
-    if (d == 128)
-      hipLaunchKernelGGL((head_norm_bwd<bf16, 128>), dim3(nb), dim3(HN_THREADS), 0, st, (const bf16*)x, weight,
+  hipError_t e = hipSuccess;
+  with_d(d, [&](auto c) {
+    constexpr int D = decltype(c)::value;
+    if (dtype == GMDN_DTYPE_BF16)
+      hipLaunchKernelGGL((head_norm_bwd<bf16, D>), dim3(nb), dim3(HN_THREADS), 0, st, (const bf16*)x, weight,
                          rstd, (const bf16*)dout, (bf16*)dx, workspace, rows);
     else
-      hipLaunchKernelGGL((head_norm_bwd<bf16, 64>), dim3(nb), dim3(HN_THREADS), 0, st, (const bf16*)x, weight,
-                         rstd, (const bf16*)dout, (bf16*)dx, workspace, rows);
-  } else {
-    if (d == 128)
-      hipLaunchKernelGGL((head_norm_bwd<float, 128>), dim3(nb), dim3(HN_THREADS), 0, st, (const float*)x, weight,
+      hipLaunchKernelGGL((head_norm_bwd<float, D>), dim3(nb), dim3(HN_THREADS), 0, st, (const float*)x, weight,
                          rstd, (const float*)dout, (float*)dx, workspace, rows);
-    else
-      hipLaunchKernelGGL((head_norm_bwd<float, 64>), dim3(nb), dim3(HN_THREADS), 0, st, (const float*)x, weight,
-                         rstd, (const float*)dout, (float*)dx, workspace, rows);
-  }
-  if (hipGetLastError() != hipSuccess) return GMDN_ERR_LAUNCH;
-  if (d == 128)
-    hipLaunchKernelGGL(head_norm_dw<128>, dim3(1), dim3(HN_THREADS), 0, st, workspace, dweight, nb);
-  else
-    hipLaunchKernelGGL(head_norm_dw<64>, dim3(1), dim3(HN_THREADS), 0, st, workspace, dweight, nb);
-  return hipGetLastError() == hipSuccess ? GMDN_OK : GMDN_ERR_LAUNCH;
+    e = hipGetLastError();
+    if (e == hipSuccess) {
+      hipLaunchKernelGGL(head_norm_dw<D>, dim3(1), dim3(HN_THREADS), 0, st, workspace, dweight, nb);
+      e = hipGetLastError();
+    }
+  });
+  return e == hipSuccess ? GMDN_OK : GMDN_ERR_LAUNCH;
 }
 
 }  // extern "C"

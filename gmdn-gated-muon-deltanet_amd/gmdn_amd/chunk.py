@@ -21,7 +21,12 @@ transform A, Kw, Uv, Qt, Ov, the state scan, and ``o = Qt S^T + Ov``.
   ``gmu`` is needed by the muon and adam rules, ``gnu`` by adam.
 * returns ``o`` (B, H, T, d) in q's dtype.
 
-Chunk length is 64 (the reference default and every configuration's).
+Chunk length 64 (the reference default and every configuration's) runs the
+fused kernels below.  Other chunk lengths (the reference trainer's
+``--chunk``, train_ablation.py:555) run the reference's own schedule: phases
+1 and 3 as float32 library GEMMs over all chunks at once and phase 2 as the
+drop-in HIP scan (``hip_state_scan``, the precision ``set_precision``
+selects), with autograd through both.
 
 Float32 streams (the reference's precision when autocast is off, its CPU
 path, train_ablation.py:424, 465) run the reference's matrix form with exact
@@ -88,7 +93,7 @@ def _rule_id(rule) -> int:
     return int(rule)
 
 
-def _check(q, k, v, beta, g, gmu, gnu, rule):
+def _check(q, k, v, beta, g, gmu, gnu, rule, chunk=CHUNK):
     if not q.is_cuda:
         raise RuntimeError("chunk_scan needs GPU tensors")
     if q.dim() != 4 or k.shape != q.shape or v.shape != q.shape:
@@ -99,11 +104,16 @@ def _check(q, k, v, beta, g, gmu, gnu, rule):
         raise RuntimeError(f"chunk_scan takes bfloat16 or float32 q, k, v of one dtype, got "
                            f"{q.dtype}, {k.dtype}, {v.dtype}")
     built = SUPPORTED_D_F32 if q.dtype == torch.float32 else SUPPORTED_D
-    if d not in built and d not in PADDED_D[q.dtype]:
+    if chunk != CHUNK:
+        from .scan import SUPPORTED_DH
+        if d not in SUPPORTED_DH:
+            raise RuntimeError(f"chunk lengths other than {CHUNK} run the drop-in scan, which supports head "
+                               f"dims {SUPPORTED_DH}, got {d}")
+    elif d not in built and d not in PADDED_D[q.dtype]:
         raise RuntimeError(f"chunk_scan supports head dims {tuple(sorted(built + tuple(PADDED_D[q.dtype])))} "
                            f"for {q.dtype}, got {d}")
-    if T % CHUNK:
-        raise RuntimeError(f"T must be a multiple of the chunk length {CHUNK}, got {T}")
+    if chunk < 1 or T % chunk:
+        raise RuntimeError(f"T must be a multiple of the chunk length {chunk}, got {T}")
     for name, t in (("beta", beta), ("g", g), ("gmu", gmu), ("gnu", gnu)):
         if t is not None and tuple(t.shape) != (B, H, T):
             raise RuntimeError(f"{name} must be (B, H, T) = {(B, H, T)}, got {tuple(t.shape)}")
@@ -113,12 +123,56 @@ def _check(q, k, v, beta, g, gmu, gnu, rule):
         raise RuntimeError("adam rule needs gnu")
 
 
-def chunk_scan(q, k, v, beta, g, gmu=None, gnu=None, *, rule="delta", ns: int = 3, eps: float = 1e-6):
+def _matrix_form(q, k, v, beta, g, gmu, gnu, rule: int, ns: int, C: int):
+    """Phases 1-3 of the reference mixer at chunk length C, its own schedule
+    (train_ablation.py:142-187): the chunk transform and the output as float32
+    GEMMs batched over every chunk, the state scan through the drop-in HIP
+    scan.  Gate floors as the fused kernels apply them (log 1e-6)."""
+    from .scan import hip_state_scan
+    B, H, T, d = q.shape
+    N = T // C
+    f = torch.float32
+    qn, kn, vn = (t.to(f).reshape(B, H, N, C, d) for t in (q, k, v))
+    bn = beta.to(f).reshape(B, H, N, C)
+
+    def logs(t):
+        return t.to(f).clamp_min(LOG_FLOOR).reshape(B, H, N, C)
+
+    if rule == 0:
+        w = bn
+    elif rule == 1:
+        lm = logs(gmu)
+        # w_t = mu_{t+1} ... mu_C, the residual momentum decay to the chunk end
+        w = torch.exp(torch.flip(torch.cumsum(torch.flip(lm, [-1]), -1), [-1]) - lm)
+    else:
+        w = torch.ones_like(bn)
+    causal = torch.tril(torch.ones(C, C, device=q.device, dtype=torch.bool))
+    A = torch.matmul(qn, kn.transpose(-1, -2).contiguous()) * bn.unsqueeze(-2)
+    A = A.masked_fill(~causal, 0.0)
+    Kw = torch.matmul((kn * w.unsqueeze(-1)).transpose(-1, -2).contiguous(), kn)
+    Uv = torch.matmul((vn * w.unsqueeze(-1)).transpose(-1, -2).contiguous(), kn)
+    Qt = qn - torch.matmul(A, kn)
+    Ov = torch.matmul(A, vn)
+    a_c = torch.exp(logs(g).sum(-1))
+    b_c = bn.mean(-1)
+    m_c = torch.exp(logs(gmu).sum(-1)) if gmu is not None else torch.ones_like(a_c)
+    n_c = torch.exp(logs(gnu).sum(-1)) if gnu is not None else torch.ones_like(a_c)
+    S = hip_state_scan(Uv, Kw, a_c, b_c, m_c, n_c, rule, ns)
+    o = torch.matmul(Qt, S.transpose(-1, -2).contiguous()) + Ov
+    return o.reshape(B, H, T, d).to(q.dtype)
+
+
+def chunk_scan(q, k, v, beta, g, gmu=None, gnu=None, *, rule="delta", ns: int = 3, eps: float = 1e-6,
+               chunk: int = CHUNK):
     """Fused mixer core; see the module docstring."""
     r = _rule_id(rule)
     gmu = gmu if r >= 1 else None
     gnu = gnu if r == 2 else None
-    _check(q, k, v, beta, g, gmu, gnu, r)
+    _check(q, k, v, beta, g, gmu, gnu, r, chunk)
+    if chunk != CHUNK:
+        if r == 2 and eps != 1e-6:
+            raise RuntimeError(f"the drop-in adam scan's epsilon is 1e-6 (fast_scan.py:94), got eps={eps}")
+        return _matrix_form(q, k, v, beta, g, gmu, gnu, r, ns, chunk)
     # the state checkpoint is written only when a backward can follow
     record = torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (q, k, v, beta, g, gmu, gnu))
     d = q.shape[-1]

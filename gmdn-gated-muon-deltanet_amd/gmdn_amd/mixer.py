@@ -9,7 +9,9 @@ SiLU and norms run as one HIP kernel per direction
 (``torch.ops.gmdn.front_fwd``), the gate activations as another
 (``gates_fwd``); phases 1-3 of the mixer (train_ablation.py:142-187: gate
 reductions, the intra-chunk products, the state scan and the output) are one
-call of ``chunk_scan`` -- the fused HIP core -- whose output lands in the
+call of ``chunk_scan`` -- the fused HIP core at chunk length 64, the
+reference's schedule around the drop-in HIP scan at other lengths -- whose
+output lands in the
 (B, T, H, dh) layout that the per-head RMSNorm kernel (``head_norm_fwd``)
 and the output projection read.
 
@@ -26,7 +28,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import ops  # noqa: F401  -- registers torch.ops.gmdn.*
-from .chunk import CHUNK, chunk_scan
+from .chunk import chunk_scan
 
 
 class FastWeightMixer(nn.Module):
@@ -37,8 +39,6 @@ class FastWeightMixer(nn.Module):
         super().__init__()
         assert inner in ("delta", "muon", "adam")
         assert d_model % n_heads == 0
-        if chunk != CHUNK:
-            raise ValueError(f"the fused core is built for chunk {CHUNK}, got {chunk}")
         self.h, self.dh = n_heads, d_model // n_heads
         self.inner, self.chunk, self.ns_steps = inner, chunk, ns_steps
         self.qkv = nn.Linear(d_model, 3 * d_model, bias=False)
@@ -84,7 +84,7 @@ class FastWeightMixer(nn.Module):
         # train_ablation.py:424, 465) stay float32; others run in bfloat16
         dt = torch.float32 if q.dtype == torch.float32 else torch.bfloat16
         o = chunk_scan(q.to(dt), k.to(dt), v.to(dt), beta, log_alpha, log_mu, log_nu, rule=self.inner,
-                       ns=self.ns_steps)
+                       ns=self.ns_steps, chunk=self.chunk)
         # per-head RMSNorm (HIP) on o's (B, T, H, dh) storage: the output is
         # already the (B, T, D) input of the projection
         ot = o.transpose(1, 2).to(self.norm.weight.dtype)

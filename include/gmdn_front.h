@@ -26,8 +26,8 @@
 extern "C" {
 #endif
 
-/* Forward: q, k, v from y (replaces train_ablation.py:124-128).  dh is 64
- * or 128, K at most 4. */
+/* Forward: q, k, v from y (replaces train_ablation.py:124-128).  dh is 16,
+ * 32, 64 or 128, K at most 4. */
 int gmdn_front_fwd(const void* y, const float* weight, const float* bias, void* q, void* k, void* v,
                    int64_t B, int64_t T, int32_t D, int32_t dh, int32_t K, int32_t dtype, void* stream);
 

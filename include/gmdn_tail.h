@@ -42,7 +42,7 @@ int gmdn_gates_fwd(const void* y, float* out, int64_t B, int64_t T, int32_t H, i
 int gmdn_gates_bwd(const void* y, const float* dout, void* dy, int64_t B, int64_t T, int32_t H, int32_t nG,
                    int32_t dtype, void* stream);
 
-/* Replaces self.norm(o) (train_ablation.py:188).  d is 64 or 128; rstd
+/* Replaces self.norm(o) (train_ablation.py:188).  d is 16, 32, 64 or 128; rstd
  * receives 1 / sqrt(mean(x^2) + eps) per row for the backward. */
 int gmdn_head_norm_fwd(const void* x, const float* weight, void* out, float* rstd, int64_t rows, int32_t d,
                        float eps, int32_t dtype, void* stream);

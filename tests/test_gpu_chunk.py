@@ -17,7 +17,7 @@ import torch
 
 from oracle import chunk as oc
 from gmdn_amd import chunk as gc
-from gmdn_amd.workloads import Workload, make_inputs
+from gmdn_amd.workloads import WORKLOADS, Workload, make_inputs
 
 pytestmark = pytest.mark.gpu
 
@@ -336,4 +336,36 @@ def test_muon_grads_long_sequence():
     Bounded in Frobenius norm by twice the float32 evaluation of the
     reference algorithm's own error, or 2e-2."""
     bad = _grads_vs_f32(Workload("muon_b1_h2_t8192_d128", "muon", 1, 2, 8192, 128, ns=5), seed=6)
+    assert not bad, bad
+
+
+def test_muon_grads_config_heads():
+    """Muon forward + backward over the whole workload (B=2, H=16, T=8192,
+    d=128, ns=5) on the GPU; the (b, h) scans are independent, so the
+    gradients of two heads at opposite ends of the batch, (0, 0) and
+    (1, 15), are checked against the oracle run on those heads' inputs
+    alone, with the bound of the long-sequence case."""
+    dev = _dev()
+    w = WORKLOADS["muon_b2_h16_t8192_d128"]
+    inp = make_inputs(w, seed=0, with_grad_out=True)
+    names = [n for n in ALL_INPUTS if inp[n] is not None]
+    xs = {n: inp[n].to(dev).detach().requires_grad_(True) for n in names}
+    o = gc.chunk_scan(*(xs.get(n) for n in ALL_INPUTS), rule=w.rule, ns=w.ns)
+    got = torch.autograd.grad(o, [xs[n] for n in names], inp["dO"].to(dev))
+    torch.cuda.synchronize()
+    got = [g_.cpu() for g_ in got]
+    bad = {}
+    for b, h in ((0, 0), (1, 15)):
+        refs = {}
+        for dt in (torch.float64, torch.float32):
+            ri = {n: inp[n][b:b + 1, h:h + 1].to(dt).requires_grad_(True) for n in names}
+            ro = oc.mixer_core(*(ri.get(n) for n in ALL_INPUTS), rule=1, ns=w.ns, C=w.chunk)
+            refs[dt] = torch.autograd.grad(ro, [ri[n] for n in names], inp["dO"][b:b + 1, h:h + 1].to(dt))
+        for n, g_, r64, r32 in zip(names, got, refs[torch.float64], refs[torch.float32]):
+            x = g_[b:b + 1, h:h + 1].double()
+            nrm = r64.norm().item()
+            e_hip, e_f32 = (x - r64).norm().item() / nrm, (r32.double() - r64).norm().item() / nrm
+            print(f"muon config head ({b}, {h}) d{n}: frobenius rel error {e_hip:.2e} (float32 reference {e_f32:.2e})")
+            if e_hip > max(TOL, 2.0 * e_f32):
+                bad[(b, h, n)] = (e_hip, e_f32)
     assert not bad, bad

@@ -38,7 +38,8 @@ def _rel(a, b):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("B,T,D,dh,K", [(2, 200, 256, 128, 4), (1, 64, 512, 64, 4), (3, 1, 256, 128, 4),
-                                         (1, 130, 1024, 128, 3), (2, 70, 128, 64, 1)])
+                                         (1, 130, 1024, 128, 3), (2, 70, 128, 64, 1), (2, 256, 128, 32, 4),
+                                         (1, 100, 96, 32, 2), (2, 65, 160, 16, 4)])
 def test_front_matches_reference(B, T, D, dh, K, dtype):
     dev = _dev()
     gen = torch.Generator().manual_seed(T + D + K)

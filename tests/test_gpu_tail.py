@@ -58,7 +58,7 @@ def test_gates_forward_backward(B, T, H, nG, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("rows,d", [(4096, 128), (999, 64), (1, 128)])
+@pytest.mark.parametrize("rows,d", [(4096, 128), (999, 64), (1, 128), (777, 32), (300, 16)])
 def test_head_norm_forward_backward(rows, d, dtype):
     dev = _dev()
     gen = torch.Generator().manual_seed(rows + d)

@@ -46,3 +46,14 @@ def test_build_optimizers_splits_parameters_like_the_reference():
     assert adamw.param_groups[0]["betas"] == (0.9, 0.95) and adamw.param_groups[0]["lr"] == 4e-4
     plain = build_optimizers(model, "adamw", args)
     assert all(isinstance(o, torch.optim.AdamW) for o in plain)
+
+
+def test_mixer_accepts_the_reference_chunk_knob():
+    """--chunk (train_ablation.py:555) other than 64 builds the same layer
+    (it runs the reference's schedule around the drop-in scan); T must be a
+    multiple of it."""
+    m = FastWeightMixer(128, 4, "muon", chunk=32)
+    assert m.chunk == 32 and m.dh == 32
+    import pytest
+    with pytest.raises(ValueError):
+        m(torch.zeros(1, 48, 128))
