@@ -201,19 +201,32 @@ head_norm_bwd(const T* __restrict__ x, const float* __restrict__ w, const float*
   }
 }
 
-// dweight[c] = sum over the backward's workgroups of their partial sums
-template <int D>
+// dweight[c] = sum over the backward's workgroups of their partial sums.
+// Workgroup g sums columns 16 g .. 16 g + 15: 16 threads per column take every
+// 16th partial row, four independent sums each (the loads of a round are in
+// flight together), combined in a fixed order, then the 16 threads' sums in
+// a fixed order: the same bits on every run.
+constexpr int HN_DW_COLS = 16;
+constexpr int HN_DW_SPLIT = HN_THREADS / HN_DW_COLS;
 __global__ void __launch_bounds__(HN_THREADS) head_norm_dw(const float* __restrict__ part, float* __restrict__ dw,
-                                                           int nblk) {
-  __shared__ float red[HN_THREADS / D][D];
-  constexpr int SPLIT = HN_THREADS / D;
-  const int c = threadIdx.x % D, s = threadIdx.x / D;
-  float acc = 0.f;
-  for (int i = s; i < nblk; i += SPLIT) acc += part[(int64_t)i * D + c];
-  red[s][c] = acc;
+                                                           int d, int nblk) {
+  __shared__ float red[HN_DW_SPLIT][HN_DW_COLS];
+  const int cl = threadIdx.x % HN_DW_COLS, s = threadIdx.x / HN_DW_COLS;
+  const int c = blockIdx.x * HN_DW_COLS + cl;
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+  int i = s;
+  for (; i + 3 * HN_DW_SPLIT < nblk; i += 4 * HN_DW_SPLIT) {
+    a0 += part[(int64_t)i * d + c];
+    a1 += part[(int64_t)(i + HN_DW_SPLIT) * d + c];
+    a2 += part[(int64_t)(i + 2 * HN_DW_SPLIT) * d + c];
+    a3 += part[(int64_t)(i + 3 * HN_DW_SPLIT) * d + c];
+  }
+  for (; i < nblk; i += HN_DW_SPLIT) a0 += part[(int64_t)i * d + c];
+  red[s][cl] = (a0 + a1) + (a2 + a3);
   __syncthreads();
   if (s == 0) {
-    for (int i = 1; i < SPLIT; ++i) acc += red[i][c];
+    float acc = red[0][cl];
+    for (int k = 1; k < HN_DW_SPLIT; ++k) acc += red[k][cl];
     dw[c] = acc;
   }
 }
@@ -334,7 +347,7 @@ int gmdn_head_norm_bwd(const void* x, const float* weight, const float* rstd, co
                          rstd, (const float*)dout, (float*)dx, workspace, rows);
     e = hipGetLastError();
     if (e == hipSuccess) {
-      hipLaunchKernelGGL(head_norm_dw<D>, dim3(1), dim3(HN_THREADS), 0, st, workspace, dweight, nb);
+      hipLaunchKernelGGL(head_norm_dw, dim3(D / HN_DW_COLS), dim3(HN_THREADS), 0, st, workspace, dweight, D, nb);
       e = hipGetLastError();
     }
   });

@@ -86,11 +86,22 @@ class FastWeightMixer(nn.Module):
         o = chunk_scan(q.to(dt), k.to(dt), v.to(dt), beta, log_alpha, log_mu, log_nu, rule=self.inner,
                        ns=self.ns_steps, chunk=self.chunk)
         # per-head RMSNorm (HIP) on o's (B, T, H, dh) storage: the output is
-        # already the (B, T, D) input of the projection
-        ot = o.transpose(1, 2).to(self.norm.weight.dtype)
-        eps = self.norm.eps if self.norm.eps is not None else torch.finfo(ot.dtype).eps
+        # already the (B, T, D) input of the projection.  The reference norms
+        # in float32 (autocast runs RMSNorm in float32) and autocast rounds the
+        # result to bfloat16 for the projection; under bfloat16 autocast the
+        # kernel reads the bfloat16 o and writes that rounding itself (it
+        # computes in float32 either way), so no float32 copy is made.
+        ot = o.transpose(1, 2)
+        bf16_autocast = (ot.dtype == torch.bfloat16 and torch.is_autocast_enabled(ot.device.type)
+                         and torch.get_autocast_dtype(ot.device.type) == torch.bfloat16)
+        if not bf16_autocast:
+            ot = ot.to(self.norm.weight.dtype)
+        # (nn.RMSNorm's default eps is its input dtype's: float32 under autocast)
+        eps = self.norm.eps if self.norm.eps is not None else torch.finfo(
+            torch.float32 if bf16_autocast else ot.dtype).eps
         y, _ = torch.ops.gmdn.head_norm_fwd(ot, self.norm.weight.float(), eps)
-        return self.out(y.view(B, T, D).to(x.dtype))
+        y = y.view(B, T, D)
+        return self.out(y if bf16_autocast else y.to(x.dtype))
 
 
 class Block(nn.Module):

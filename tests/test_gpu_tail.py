@@ -96,3 +96,26 @@ def test_head_norm_weight_gradient_is_deterministic():
         (dw,) = torch.autograd.grad(out, w, g)
         dws.append(dw)
     assert torch.equal(dws[0], dws[1])
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_head_norm_bf16_io_equals_float32_then_rounded(d):
+    """Under bfloat16 autocast the mixer runs the head norm on the bfloat16
+    output directly (no float32 copy): that is bit for bit the float32 norm
+    rounded to bfloat16, as autocast rounds it before the projection (and its
+    input gradient likewise)."""
+    dev = _dev()
+    torch.manual_seed(0)
+    x = torch.randn(3000, d, device=dev).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(d, device=dev)).requires_grad_(True)
+    g = torch.randn(3000, d, device=dev).to(torch.bfloat16)
+    xa = x.clone().requires_grad_(True)
+    ya, _ = torch.ops.gmdn.head_norm_fwd(xa, w, 1e-6)
+    dxa, dwa = torch.autograd.grad(ya, (xa, w), g)
+    xb = x.float().requires_grad_(True)
+    yb, _ = torch.ops.gmdn.head_norm_fwd(xb, w, 1e-6)
+    dxb, dwb = torch.autograd.grad(yb, (xb, w), g.float())
+    torch.cuda.synchronize()
+    assert ya.dtype == torch.bfloat16 and torch.equal(ya, yb.to(torch.bfloat16))
+    assert torch.equal(dxa, dxb.to(torch.bfloat16))
+    assert torch.equal(dwa, dwb)
