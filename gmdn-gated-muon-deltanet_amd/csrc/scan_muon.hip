@@ -252,28 +252,49 @@ scan_bwd_muon(const float* __restrict__ U, const float* __restrict__ K,
 // next through the workspace.
 template <int D>
 struct MuonBwdWs {
-  // per (b, h) and chunk of the segment (local index c = i - i0):
-  // X_0 .. X_ns, Z_0 .. Z_{ns-1}, P_0 .. P_{ns-1}, M_i; then Mbar and Sb per
-  // (b, h); then |M_i|
-  int64_t mat, per_chunk, BH, nseg;
-  GMDN_DEV MuonBwdWs(int64_t BH_, int64_t nseg_, int ns)
-      : mat((int64_t)D * D), per_chunk((3 * ns + 2) * mat), BH(BH_), nseg(nseg_) {}
-  GMDN_DEV int64_t slot(int64_t bh, int c) const { return bh * nseg + c; }
+  // nbuf iterate buffers, each with per (b, h) and chunk of a segment (local
+  // index c = i - i0): X_0 .. X_ns, Z_0 .. Z_{ns-1}, P_0 .. P_{ns-1}, M_i;
+  // then Mbar and Sb per (b, h); then |M_i| per buffer, (b, h) and chunk
+  int64_t mat, per_chunk, BH, nseg, iters;
+  GMDN_DEV MuonBwdWs(int64_t BH_, int64_t nseg_, int ns, int nbuf)
+      : mat((int64_t)D * D), per_chunk((3 * ns + 2) * mat), BH(BH_), nseg(nseg_),
+        iters(nbuf * BH_ * nseg_ * per_chunk) {}
+  GMDN_DEV int64_t slot(int64_t bh, int c, int buf) const { return (buf * BH + bh) * nseg + c; }
   GMDN_DEV float* X(float* ws, int64_t sl, int k) const { return ws + sl * per_chunk + k * mat; }
   GMDN_DEV float* Z(float* ws, int64_t sl, int ns, int k) const { return ws + sl * per_chunk + (ns + 1 + k) * mat; }
   GMDN_DEV float* P(float* ws, int64_t sl, int ns, int k) const { return ws + sl * per_chunk + (2 * ns + 1 + k) * mat; }
   GMDN_DEV float* M(float* ws, int64_t sl, int ns) const { return ws + sl * per_chunk + (3 * ns + 1) * mat; }
-  GMDN_DEV float* Mbar(float* ws, int64_t bh) const { return ws + BH * nseg * per_chunk + bh * mat; }
-  GMDN_DEV float* Sbar(float* ws, int64_t bh) const { return ws + BH * nseg * per_chunk + (BH + bh) * mat; }
-  GMDN_DEV float* norm(float* ws) const { return ws + BH * nseg * per_chunk + 2 * BH * mat; }
+  GMDN_DEV float* Mbar(float* ws, int64_t bh) const { return ws + iters + bh * mat; }
+  GMDN_DEV float* Sbar(float* ws, int64_t bh) const { return ws + iters + (BH + bh) * mat; }
+  GMDN_DEV float* norm(float* ws) const { return ws + iters + 2 * BH * mat; }
 };
 
+// One launch of the segmented backward: the reverse pass over segment
+// [i0, i1) (blocks 0 .. nx3 - 1, nx3 = BH or 0) reading iterate buffer xbuf,
+// and the iterates of segment [j0, j0 + jcur) (the next blocks, BH jcur of
+// them, or none) written into buffer pbuf.  The two parts share nothing but
+// the launch, so the chunk-parallel iterates of the next segment fill the CUs
+// that the BH serial reverse scans leave idle.
+struct MuonSegArgs {
+  const float *U, *K, *av, *bv, *mv, *S_all, *M_all, *gS;
+  float *dU, *da, *db, *dm, *dn, *ws;
+  int64_t BH;
+  int N, ns, nseg, nbuf;
+  int nx3, i0, i1, xbuf;
+  int j0, jcur, pbuf;
+};
+
+// The iterates of chunk j0 + blk % jcur of head blk / jcur.
 template <int D>
-__global__ void __launch_bounds__(D * 4)
-scan_bwd_muon_pre(const float* __restrict__ U, const float* __restrict__ K,
-                  const float* __restrict__ mv, const float* __restrict__ S_all,
-                  const float* __restrict__ M_all, float* __restrict__ ws, int64_t BH, int N, int ns,
-                  int i0, int ncur, int nseg) {
+GMDN_DEV void muon_pre_body(const MuonSegArgs& sa, int64_t blk) {
+  const float* __restrict__ U = sa.U;
+  const float* __restrict__ K = sa.K;
+  const float* __restrict__ mv = sa.mv;
+  const float* __restrict__ S_all = sa.S_all;
+  const float* __restrict__ M_all = sa.M_all;
+  float* __restrict__ ws = sa.ws;
+  const int64_t BH = sa.BH;
+  const int N = sa.N, ns = sa.ns, i0 = sa.j0, ncur = sa.jcur;
   using NSX = NSSplit<D>;
   using P = PrecX3;
   using Op = P::Op;
@@ -282,10 +303,10 @@ scan_bwd_muon_pre(const float* __restrict__ U, const float* __restrict__ K,
   const lds_ptr SA = lds_base(smem), SB = SA + NSX::BYTES;
   float* red = smem + 2 * NSX::BYTES / 4;
   const NSX nsx;
-  const MuonBwdWs<D> W(BH, nseg, ns);
-  const int64_t bh = blockIdx.x / ncur;
-  const int c = (int)(blockIdx.x % ncur);  // chunk i0 + c of the segment
-  const int64_t si = bh * N + i0 + c, sl = W.slot(bh, c);
+  const MuonBwdWs<D> W(BH, sa.nseg, ns, sa.nbuf);
+  const int64_t bh = blk / ncur;
+  const int c = (int)(blk % ncur);  // chunk i0 + c of the segment
+  const int64_t si = bh * N + i0 + c, sl = W.slot(bh, c, sa.pbuf);
   const int l = lane_id(), G = l >> 4, rl = l & 15;
   const int r0 = 16 * wave_id();
   const int64_t mat = (int64_t)D * D;
@@ -327,14 +348,24 @@ scan_bwd_muon_pre(const float* __restrict__ U, const float* __restrict__ K,
   NSX::store_own(W.X(ws, sl, ns), X);
 }
 
+// The reverse pass of head bh over chunks i1 - 1 .. i0.
 template <int D>
-__global__ void __launch_bounds__(D * 4)
-scan_bwd_muon_x3(const float* __restrict__ K, const float* __restrict__ av,
-                 const float* __restrict__ bv, const float* __restrict__ mv,
-                 const float* __restrict__ S_all, const float* __restrict__ M_all,
-                 const float* __restrict__ gS, float* __restrict__ dU, float* __restrict__ da,
-                 float* __restrict__ db, float* __restrict__ dm, float* __restrict__ dn,
-                 float* __restrict__ ws, int64_t BH, int N, int ns, int i0, int i1, int nseg) {
+GMDN_DEV void muon_x3_body(const MuonSegArgs& sa, int64_t bh) {
+  const float* __restrict__ K = sa.K;
+  const float* __restrict__ av = sa.av;
+  const float* __restrict__ bv = sa.bv;
+  const float* __restrict__ mv = sa.mv;
+  const float* __restrict__ S_all = sa.S_all;
+  const float* __restrict__ M_all = sa.M_all;
+  const float* __restrict__ gS = sa.gS;
+  float* __restrict__ dU = sa.dU;
+  float* __restrict__ da = sa.da;
+  float* __restrict__ db = sa.db;
+  float* __restrict__ dm = sa.dm;
+  float* __restrict__ dn = sa.dn;
+  float* __restrict__ ws = sa.ws;
+  const int64_t BH = sa.BH;
+  const int N = sa.N, ns = sa.ns, i0 = sa.i0, i1 = sa.i1, xbuf = sa.xbuf;
   using NSX = NSSplit<D>;
   using P = PrecX3;
   using Op = P::Op;
@@ -345,8 +376,7 @@ scan_bwd_muon_x3(const float* __restrict__ K, const float* __restrict__ av,
 
   const NSX nsx;
   const uint32_t tb = NSX::tbase();
-  const MuonBwdWs<D> W(BH, nseg, ns);
-  const int64_t bh = blockIdx.x;
+  const MuonBwdWs<D> W(BH, sa.nseg, ns, sa.nbuf);
   const int l = lane_id(), G = l >> 4, rl = l & 15;
   const int r0 = 16 * wave_id();
   const int64_t mat = (int64_t)D * D;
@@ -374,7 +404,7 @@ scan_bwd_muon_x3(const float* __restrict__ K, const float* __restrict__ av,
   bf16x8 Xn[NT];
   auto request_start = [&](int i) {
     const int64_t si = bh * N + i;
-    const float* Xs = W.X(ws, W.slot(bh, i - i0), ns);
+    const float* Xs = W.X(ws, W.slot(bh, i - i0, xbuf), ns);
 #pragma unroll
     for (int t = 0; t < NT; ++t) Si[t] = *reinterpret_cast<const f32x4*>(S_all + si * mat + roff(t));
 #pragma unroll
@@ -385,7 +415,7 @@ scan_bwd_muon_x3(const float* __restrict__ K, const float* __restrict__ av,
   request_start(i1 - 1);
 
   for (int i = i1 - 1; i >= i0; --i) {
-    const int64_t si = bh * N + i, sl = W.slot(bh, i - i0);
+    const int64_t si = bh * N + i, sl = W.slot(bh, i - i0, xbuf);
     const float ga = av[si], gb = bv[si], gm = mv[si];
     // ---- 1. da_i = <Sb, S_i>, db_i = <Sb, msign(M_i)>
     float pda = 0.f, pdb = 0.f;
@@ -556,6 +586,17 @@ scan_bwd_muon_x3(const float* __restrict__ K, const float* __restrict__ av,
   }
 }
 
+// Blocks 0 .. nx3 - 1: the reverse pass of their head over segment [i0, i1);
+// the rest: the iterates of one chunk of segment [j0, j0 + jcur) each.
+template <int D>
+__global__ void __launch_bounds__(D * 4) scan_bwd_muon_seg(MuonSegArgs sa) {
+  const int64_t b = blockIdx.x;
+  if (b < sa.nx3)
+    muon_x3_body<D>(sa, b);
+  else
+    muon_pre_body<D>(sa, b - sa.nx3);
+}
+
 template <int D, int PREC>
 static hipError_t launch_fwd_muon(const ScanArgs& s) {
   const size_t lds = 2 * (size_t)D * D * sizeof(float);
@@ -571,25 +612,45 @@ template <int D, int PREC>
 static hipError_t launch_bwd_muon(const ScanArgs& s, float* ws, int64_t ws_floats) {
   if constexpr (PREC == 0) {
     const int lds = 2 * NSSplit<D>::BYTES + 64;
-    auto kp = scan_bwd_muon_pre<D>;
-    auto k3 = scan_bwd_muon_x3<D>;
-    hipError_t e = hipFuncSetAttribute((const void*)kp, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-    if (e == hipSuccess) e = hipFuncSetAttribute((const void*)k3, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    auto k = scan_bwd_muon_seg<D>;
+    hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return e;
-    // segments of nseg chunks from the end: the iterates of a segment, then
-    // its reverse pass (Sb and Mbar carried through the workspace)
-    const int nseg = (int)muon_bwd_segment(s.BH, s.N, D, s.ns, ws_floats);
-    if (nseg < 1) return hipErrorInvalidValue;
-    for (int i1 = (int)s.N; i1 > 0; i1 -= nseg) {
-      const int i0 = i1 > nseg ? i1 - nseg : 0;
-      hipLaunchKernelGGL(kp, dim3((unsigned)(s.BH * (i1 - i0))), dim3(D * 4), lds, s.stream, s.U, s.K, s.m,
-                         s.S_all, s.M_all, ws, s.BH, (int)s.N, s.ns, i0, i1 - i0, nseg);
-      hipLaunchKernelGGL(k3, dim3((unsigned)s.BH), dim3(D * 4), lds, s.stream, s.K, s.a, s.b, s.m, s.S_all,
-                         s.M_all, s.gS, s.dU, s.da, s.db, s.dm, s.dn, ws, s.BH, (int)s.N, s.ns, i0, i1, nseg);
-      hipError_t e2 = hipGetLastError();
-      if (e2 != hipSuccess) return e2;
+    // Segments of nseg chunks from the end; Sb and Mbar carry from one
+    // segment's reverse pass to the next through the workspace.  With two
+    // iterate buffers the iterates of segment k + 1 are formed in the launch
+    // that runs segment k's reverse pass (only the first segment's run
+    // alone); with one, each segment's iterates and then its reverse pass.
+    const MuonBwdPlan plan = muon_bwd_plan(s.BH, s.N, D, s.ns, ws_floats);
+    if (plan.nseg < 1) return hipErrorInvalidValue;
+    const int nseg = (int)plan.nseg;
+    MuonSegArgs sa{};
+    sa.U = s.U; sa.K = s.K; sa.av = s.a; sa.bv = s.b; sa.mv = s.m; sa.S_all = s.S_all; sa.M_all = s.M_all;
+    sa.gS = s.gS; sa.dU = s.dU; sa.da = s.da; sa.db = s.db; sa.dm = s.dm; sa.dn = s.dn; sa.ws = ws;
+    sa.BH = s.BH; sa.N = (int)s.N; sa.ns = s.ns; sa.nseg = nseg; sa.nbuf = plan.nbuf;
+    auto launch = [&](int nx3, int i0, int i1, int xbuf, int j0, int jcur, int pbuf) {
+      sa.nx3 = nx3; sa.i0 = i0; sa.i1 = i1; sa.xbuf = xbuf;
+      sa.j0 = j0; sa.jcur = jcur; sa.pbuf = pbuf;
+      const int64_t blocks = (int64_t)nx3 + s.BH * jcur;
+      hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(D * 4), lds, s.stream, sa);
+      return hipGetLastError();
+    };
+    const int bh = (int)s.BH;
+    int i1 = (int)s.N, i0 = i1 > nseg ? i1 - nseg : 0;
+    if (plan.nbuf == 2) {
+      e = launch(0, 0, 0, 0, i0, i1 - i0, 0);
+      for (int seg = 0; e == hipSuccess && i1 > 0; ++seg) {
+        const int j1 = i0, j0 = j1 > nseg ? j1 - nseg : 0;
+        e = launch(bh, i0, i1, seg & 1, j0, j1 - j0, (seg + 1) & 1);
+        i1 = i0;
+        i0 = j0;
+      }
+    } else {
+      for (; e == hipSuccess && i1 > 0; i1 = i0, i0 = i1 > nseg ? i1 - nseg : 0) {
+        e = launch(0, 0, 0, 0, i0, i1 - i0, 0);
+        if (e == hipSuccess) e = launch(bh, i0, i1, 0, 0, 0, 0);
+      }
     }
-    return hipSuccess;
+    return e;
   } else {
     auto kern = scan_bwd_muon<D, PREC>;
     hipLaunchKernelGGL(kern, dim3((unsigned)s.BH), dim3(D * 4), 0, s.stream, s.U, s.K, s.a, s.b, s.m,

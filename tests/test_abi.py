@@ -80,13 +80,14 @@ def test_scan_bwd_workspace_contract():
         x3 = BH * N * ((3 * ns + 2) * mat + 1) + 2 * BH * mat
         assert lib.gmdn_scan_bwd_workspace_bytes(BH, N, 64, 1, ns) == 4 * max(x3, BH * (4 + ns) * mat)
     assert lib.gmdn_scan_bwd_workspace_bytes(1, 1, 64, 1, 0) == 4 * max(2 * mat + 1 + 2 * mat, 4 * mat)
-    # large problems: segments of as many chunks as fit in 512 MiB
+    # large problems: two buffers of segments of as many chunks as fit in
+    # 512 MiB each
     BH, N, dh, ns = 32, 128, 128, 5
     per = BH * ((3 * ns + 2) * dh * dh + 1)
     nseg = ((512 << 20) // 4 - 2 * BH * dh * dh) // per
     assert 1 <= nseg < N
-    assert lib.gmdn_scan_bwd_workspace_bytes(BH, N, dh, 1, ns) == 4 * (nseg * per + 2 * BH * dh * dh)
-    assert lib.gmdn_scan_bwd_workspace_bytes(BH, N, dh, 1, ns) <= 512 << 20
+    assert lib.gmdn_scan_bwd_workspace_bytes(BH, N, dh, 1, ns) == 4 * (2 * nseg * per + 2 * BH * dh * dh)
+    assert lib.gmdn_scan_bwd_workspace_bytes(BH, N, dh, 1, ns) <= 1024 << 20
     p = [0x1000] * 16
     # adam / muon without workspace -> GMDN_ERR_WORKSPACE
     assert lib.gmdn_scan_bwd(*p, None, 0, 4, 16, 64, 2, 3, 0, None) == 3

@@ -1,8 +1,12 @@
 """The drop-in muon backward (gmdn_scan_bwd, rule 1, 'tf32') runs its chunks
-in segments from the end, as many chunks per segment as the workspace holds:
-with workspaces sized for one-chunk and three-chunk segments the results are
-bit-identical to the default workspace (the same per-chunk arithmetic; the
-state and momentum cotangents carry across segments as exact float32)."""
+in segments from the end, as many chunks per segment as the workspace holds,
+in one iterate buffer (each segment's iterates, then its reverse pass) or two
+(the next segment's iterates formed in the launch of the current segment's
+reverse pass).  With workspaces of one to six one-chunk segment buffers (one
+buffer of one chunk; two of one, two and three chunks; one of all chunks) the
+results are bit-identical to the default workspace (the same per-chunk
+arithmetic; the state and momentum cotangents carry across segments as exact
+float32)."""
 import pytest
 import torch
 
@@ -51,7 +55,7 @@ def test_muon_backward_segments_bit_identical(B, H, N, dh, ns):
     assert full == _segment_bytes(B * H, N, dh, ns)  # small problems: one segment
     want = _bwd(lib, ins, S_all, M_all, gS, ns, full)
     assert all(torch.isfinite(t).all() for t in want)
-    for nseg in (1, 3):
+    for nseg in (1, 2, 3, 4, 6):
         got = _bwd(lib, ins, S_all, M_all, gS, ns, _segment_bytes(B * H, nseg, dh, ns))
         for name, g_, w_ in zip("dU dK da db dm dn".split(), got, want):
             assert torch.equal(g_, w_), (nseg, name)
