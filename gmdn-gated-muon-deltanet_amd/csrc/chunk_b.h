@@ -109,6 +109,8 @@ hipError_t chunk_prep_launch(const ChunkArgs& a, int d, int rule, bool fwd, bool
 hipError_t chunk_out_launch(const ChunkArgs& a, int d, const float* S_all, hipStream_t s);
 // muon backward (workspace floats; states = S_i then M_i planes of every chunk)
 size_t chunk_bwd_muon_ws_floats(int64_t BH, int64_t N, int d, int ns);
+// the smallest workspace the 'tf32' muon backward runs with (one-chunk segments)
+size_t chunk_bwd_muon_min_ws_floats(int64_t BH, int64_t N, int d, int ns);
 hipError_t chunk_bwd_muon_launch(const ChunkArgs& a, int d, int ns, int precision, float* ws, size_t ws_floats,
                                  hipStream_t s);
 // adam at d = 128, exact float32 scan: training forward (states = S, M, V,

@@ -711,7 +711,11 @@ int gmdn_chunk_bwd(const gmdn_chunk_desc* desc, const void* q, const void* k, co
   if (desc->rule == 2 && (desc->d == 128 || desc->dtype == GMDN_DTYPE_F32) && desc->eps != 1e-6f)
     return GMDN_ERR_UNSUPPORTED;
   if (desc->B * desc->H * (desc->T / CB_C) >= ((int64_t)1 << 31)) return GMDN_ERR_ARG;  // one workgroup per chunk
-  if (!workspace || workspace_bytes < gmdn_chunk_bwd_workspace_bytes(desc)) return GMDN_ERR_WORKSPACE;
+  const size_t min_ws = desc->rule == 1 && desc->dtype != GMDN_DTYPE_F32 && desc->precision == GMDN_PREC_TF32
+                            ? chunk_bwd_muon_min_ws_floats(desc->B * desc->H, desc->T / CB_C, desc->d, desc->ns) *
+                                  sizeof(float)
+                            : gmdn_chunk_bwd_workspace_bytes(desc);
+  if (!workspace || workspace_bytes < min_ws) return GMDN_ERR_WORKSPACE;
   // dO tiles arrive by 16-byte LDS-DMA loads and dq, dk, dv leave in 16-byte
   // row pieces: every stream needs 16-byte aligned rows
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dO) || !aligned16(dq) ||

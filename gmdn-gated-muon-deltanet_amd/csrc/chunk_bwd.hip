@@ -30,6 +30,8 @@
 //    share.
 #include "../../include/gmdn_scan.h"
 #include "chunk_b.h"
+#include "chunk_prep.h"
+#include "muon_bwd.h"
 #include "scan_a.h"
 
 #include <type_traits>
@@ -61,7 +63,7 @@ struct TokBwdLds {
 // scalars' gradients arrive as arrays [da | db | dm | dn] (B H N each) in
 // p.part -- muon always, adam when its scan ran in exact float32 (d = 128)
 template <int D, int RULE, bool MAT = RULE == 1>
-__global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p) {
+GMDN_DEV void chunk_bwd_tok_body(const ChunkArgs& p, int64_t bh, int i) {
   using LQ = BSwz<D>;
   using LA = BSwz<CB_C>;
   using L = TokBwdLds<D>;
@@ -98,8 +100,6 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
       return x;
   };
 
-  const int64_t bh = blockIdx.x / p.N;
-  const int i = (int)(blockIdx.x % p.N);
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = lane_id(), G = l >> 4, lc = l & 15;
   const int64_t bb = bh / p.H, hh = bh % p.H;
@@ -484,6 +484,12 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
   }
 }
 
+// One workgroup per (b, h, chunk).
+template <int D, int RULE, bool MAT = RULE == 1>
+__global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p) {
+  chunk_bwd_tok_body<D, RULE, MAT>(p, blockIdx.x / p.N, (int)(blockIdx.x % p.N));
+}
+
 template <int D, int RULE>
 static hipError_t launch_bwd(const ChunkArgs& a, hipStream_t stream) {
   if constexpr (RULE == 0) {
@@ -516,6 +522,54 @@ size_t chunk_bwd_muon_ws_floats(int64_t BH, int64_t N, int d, int ns) {
   return (size_t)(4 * BHN * (int64_t)d * d + 8 * BHN + 64 + muon_bwd_ws_total(BH, N, d, ns));
 }
 
+size_t chunk_bwd_muon_min_ws_floats(int64_t BH, int64_t N, int d, int ns) {
+  const int64_t BHN = BH * N;
+  const int64_t prefix = (4 * BHN * (int64_t)d * d + 8 * BHN + 63) & ~(int64_t)63;
+  return (size_t)(prefix + muon_bwd_ws_segment_floats(BH, 1, d, ns));
+}
+
+// One launch of the pipelined muon backward: the reverse pass of segment k
+// (blocks 0 .. nx3 - 1), then blocks for the iterates of segment k + 1, the
+// matrix-form stage (Kw, Uv, gS, the chunk scalars) of chunks [p0, p0 + pcur)
+// and the token gradients of chunks [t0, t0 + tcur).  Every role but the
+// first is chunk-parallel and fills the CUs the B H serial reverse scans
+// leave idle; each reads only what earlier launches wrote.
+struct MuonPipeArgs {
+  MuonSegArgs seg;
+  ChunkArgs prep, tok;
+  float *Kw, *Uv, *gS, *abm;
+  int p0, pcur, t0, tcur;
+};
+
+template <int D>
+constexpr int muon_pipe_lds() {
+  constexpr int a = 2 * NSSplit<D>::BYTES + 64, b = PrepLds<D>::BYTES, c = TokBwdLds<D>::BYTES;
+  return a > b ? (a > c ? a : c) : (b > c ? b : c);
+}
+
+template <int D>
+__global__ void __launch_bounds__(D * 4) chunk_bwd_muon_pipe(MuonPipeArgs a) {
+  static_assert(PrepLds<D>::NTHR == D * 4 && TokBwdLds<D>::NTHR == D * 4, "one block size for every role");
+  int64_t b = blockIdx.x;
+  const int64_t npre = a.seg.BH * a.seg.jcur, nprep = a.seg.BH * a.pcur;
+  if (b < a.seg.nx3) {
+    muon_x3_body<D>(a.seg, b);
+    return;
+  }
+  b -= a.seg.nx3;
+  if (b < npre) {
+    muon_pre_body<D>(a.seg, b);
+    return;
+  }
+  b -= npre;
+  if (b < nprep) {
+    chunk_prep_body<D, 1, true, true>(a.prep, a.Kw, a.Uv, a.gS, a.abm, b / a.pcur, a.p0 + (int)(b % a.pcur));
+    return;
+  }
+  b -= nprep;
+  chunk_bwd_tok_body<D, 1>(a.tok, b / a.tcur, a.t0 + (int)(b % a.tcur));
+}
+
 template <int D>
 static hipError_t launch_bwd_muon_chunks(const ChunkArgs& a, int ns, int precision, float* ws, size_t ws_floats,
                                          hipStream_t stream) {
@@ -528,6 +582,51 @@ static hipError_t launch_bwd_muon_chunks(const ChunkArgs& a, int ns, int precisi
   float* part = abm + 4 * BHN;  // da, db, dm, dn
   float* sws = ws + ((part + 4 * BHN - ws + 63) & ~(int64_t)63);  // 16-byte pieces: aligned
   const int64_t sws_floats = (int64_t)ws_floats - (sws - ws);
+  const MuonBwdPlan plan = muon_bwd_plan(BH, a.N, D, ns, sws_floats);
+  if (precision == GMDN_PREC_TF32 && plan.nbuf == 2) {
+    // Segments k = 0, 1, .. of plan.nseg chunks from the end.  Launch k runs
+    // segment k's reverse pass, segment k + 1's iterates, segment k + 2's
+    // matrix-form stage and segment k - 1's token gradients; two launches
+    // before (the first two segments' stage, the first segment's iterates)
+    // and one after (the last segment's token gradients) fill the pipeline.
+    const int N = (int)a.N, nseg = (int)plan.nseg;
+    auto seg_lo = [&](int k) { return N - (k + 1) * nseg > 0 ? N - (k + 1) * nseg : 0; };
+    auto seg_hi = [&](int k) { return N - k * nseg > 0 ? N - k * nseg : 0; };
+    const int nsegs = (N + nseg - 1) / nseg;
+    MuonPipeArgs pa{};
+    MuonSegArgs& sg = pa.seg;
+    sg.U = Uv; sg.K = Kw; sg.av = abm; sg.bv = abm + BHN; sg.mv = abm + 2 * BHN;
+    sg.S_all = a.states; sg.M_all = a.states + BHN * mat; sg.gS = gS;
+    sg.dU = dU; sg.da = part; sg.db = part + BHN; sg.dm = part + 2 * BHN; sg.dn = part + 3 * BHN; sg.ws = sws;
+    sg.BH = BH; sg.N = N; sg.ns = ns; sg.nseg = nseg; sg.nbuf = 2;
+    pa.prep = a;
+    pa.tok = a;
+    pa.tok.gb = dU;
+    pa.tok.part = part;
+    pa.Kw = Kw; pa.Uv = Uv; pa.gS = gS; pa.abm = abm;
+    auto k = chunk_bwd_muon_pipe<D>;
+    constexpr int lds = muon_pipe_lds<D>();
+    hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    // x3 segment (or -1), pre segment, prep chunk range, tok segment
+    auto launch = [&](int kx, int kp, int p0, int p1, int kt) {
+      const bool x = kx >= 0 && kx < nsegs, pre = kp >= 0 && kp < nsegs, tok = kt >= 0 && kt < nsegs;
+      sg.nx3 = x ? (int)BH : 0;
+      sg.i0 = x ? seg_lo(kx) : 0; sg.i1 = x ? seg_hi(kx) : 0; sg.xbuf = x ? (kx & 1) : 0;
+      sg.j0 = pre ? seg_lo(kp) : 0; sg.jcur = pre ? seg_hi(kp) - seg_lo(kp) : 0; sg.pbuf = pre ? (kp & 1) : 0;
+      pa.p0 = p0; pa.pcur = p1 > p0 ? p1 - p0 : 0;
+      pa.t0 = tok ? seg_lo(kt) : 0; pa.tcur = tok ? seg_hi(kt) - seg_lo(kt) : 0;
+      const int64_t blocks = sg.nx3 + BH * (sg.jcur + pa.pcur + pa.tcur);
+      if (blocks == 0) return hipSuccess;
+      hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(D * 4), lds, stream, pa);
+      return hipGetLastError();
+    };
+    if (e == hipSuccess) e = launch(-1, -1, seg_lo(1), seg_hi(0), -1);
+    if (e == hipSuccess) e = launch(-1, 0, 0, 0, -1);
+    for (int kk = 0; e == hipSuccess && kk < nsegs; ++kk)
+      e = launch(kk, kk + 1, kk + 2 < nsegs ? seg_lo(kk + 2) : 0, kk + 2 < nsegs ? seg_hi(kk + 2) : 0, kk - 1);
+    if (e == hipSuccess) e = launch(-1, -1, 0, 0, nsegs - 1);
+    return e;
+  }
   hipError_t e = chunk_prep_launch(a, D, 1, true, true, Kw, Uv, gS, abm, stream);
   if (e != hipSuccess) return e;
   ScanArgs sa{};

@@ -215,7 +215,11 @@ int gmdn_wy_bwd(const gmdn_chunk_desc* desc, const void* q, const void* k, const
                 void* dq, void* dk, void* dv, float* dbeta, float* dg, void* workspace,
                 size_t workspace_bytes, void* stream);
 
-/* Workspace bytes gmdn_chunk_bwd needs. */
+/* Workspace bytes gmdn_chunk_bwd needs.  Muon (rule 1) on bfloat16 streams
+ * in 'tf32' also runs with any smaller workspace down to one-chunk segments
+ * of its reverse scan (the results do not depend on the segment length);
+ * this size gives segments of up to 512 MiB of iterates, in two buffers
+ * when they do not hold every chunk. */
 size_t gmdn_chunk_bwd_workspace_bytes(const gmdn_chunk_desc* desc);
 
 /* Backward given dO (strides desc->so) and the forward's `states`.  Writes
@@ -223,7 +227,9 @@ size_t gmdn_chunk_bwd_workspace_bytes(const gmdn_chunk_desc* desc);
  * (contiguous (B, H, T) float32).  Matches torch autograd through the
  * reference's phases 1-3 and scan_eager.  Rule 1 (muon) forms each chunk's
  * Kw, Uv and dL/dS_i, runs the drop-in muon reverse scan (Newton-Schulz VJP
- * in desc->precision) on the forward's S_i, M_i, then the token gradients.
+ * in desc->precision) on the forward's S_i, M_i, then the token gradients;
+ * in 'tf32' with two iterate buffers, the chunk-parallel stages of later
+ * and earlier segments run in the launches of the serial reverse scan.
  * Adam (rule 2) at d = 128 runs the drop-in adam scan in exact float32
  * between chunk-parallel kernels, forward (when `states` is requested) and
  * backward; its epsilon must then be the reference's 1e-6. */

@@ -172,3 +172,30 @@ def test_chunk_bwd_rejects_misaligned_streams():
     assert call(good, dk=p + 8) == 2
     assert call(good, dv=p + 4) == 2
     assert call(good, dO=p + 2) == 2
+
+
+def test_chunk_bwd_muon_workspace_floor():
+    """The fused muon backward in 'tf32' runs with any workspace down to
+    one-chunk segments of its reverse scan (its prefix -- Kw, Uv, gS, dU per
+    chunk and the chunk scalars and their gradients, 256-byte aligned -- plus
+    one chunk's iterates, |M_i| and the carried Mbar, Sb per (b, h)); below
+    that it is refused with GMDN_ERR_WORKSPACE before anything is launched,
+    and in 'ieee' below the default size."""
+    lib = _native.load()
+    p = 0x1000
+    B, H, T, d, ns = 1, 2, 448, 64, 3
+    desc = _chunk_desc(rule=1, d=d, T=T)
+    desc.precision = _native.PREC_TF32
+    BH, N, mat = B * H, T // 64, d * d
+    BHN = BH * N
+    prefix = (4 * BHN * mat + 8 * BHN + 63) // 64 * 64
+    floor = 4 * (prefix + BH * ((3 * ns + 2) * mat + 1) + 2 * BH * mat)
+    full = lib.gmdn_chunk_bwd_workspace_bytes(desc)
+    assert full > floor
+
+    def call(nbytes):
+        return lib.gmdn_chunk_bwd(desc, p, p, p, p, p, p, None, p, p, p, p, p, p, p, p, None, p, nbytes, None)
+
+    assert call(floor - 4) == 3
+    desc.precision = _native.PREC_IEEE
+    assert call(full - 4) == 3

@@ -68,3 +68,57 @@ def test_muon_backward_refuses_workspace_below_one_chunk():
     p = [0x1000] * 16
     small = _segment_bytes(BH, 1, dh, ns) - 4
     assert lib.gmdn_scan_bwd(*p, 0x1000, small, BH, N, dh, 1, ns, nat.PREC_TF32, None) == 3
+
+
+def _fused_bwd(lib, ins, states, ns, ws_bytes):
+    """gmdn_chunk_bwd (muon, 'tf32') with a workspace of ws_bytes."""
+    from gmdn_amd import ops
+    q, k, v, beta, g, gmu, dO = ins
+    outs = [torch.full_like(t, float("nan")) for t in (q, k, v, beta, g, gmu)]
+    desc = ops.chunk_desc(q, k, v, dO, 1, ns, 1e-6, nat.PREC_TF32)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    rc = lib.gmdn_chunk_bwd(desc, *[nat.ptr(t) for t in (q, k, v, beta, g, gmu)], None, nat.ptr(states),
+                            nat.ptr(dO), *[nat.ptr(t) for t in outs], None, nat.ptr(ws), ws_bytes,
+                            nat.stream_of(q))
+    nat.check(rc, "gmdn_chunk_bwd")
+    torch.cuda.synchronize()
+    return outs
+
+
+@pytest.mark.parametrize("d,ns", [(64, 3), (128, 5)])
+def test_fused_muon_backward_segments_bit_identical(d, ns):
+    """The fused core's muon backward (gmdn_chunk_bwd, 'tf32') accepts any
+    workspace down to one-chunk segments.  With two iterate buffers its
+    matrix-form stage, iterate rebuild and token gradients run in the
+    launches of the serial reverse scan, a segment or two ahead or behind;
+    with one-chunk segments in one buffer and with two buffers of one, two
+    and three chunks the gradients equal the default workspace's (one segment
+    of every chunk here) bit for bit."""
+    from gmdn_amd.workloads import Workload, make_inputs
+    dev = _dev()
+    lib = nat.load()
+    B, H, N = 1, 3, 7
+    print(f"fused muon segments B{B} H{H} N{N} d{d} ns{ns}", flush=True)
+    inp = make_inputs(Workload("seg", "muon", B, H, N * 64, d, ns=ns), seed=N + d, with_grad_out=True)
+    ins = [inp[n].to(dev).contiguous() for n in ("q", "k", "v", "beta", "g", "gmu", "dO")]
+    _, states = torch.ops.gmdn.chunk_fwd(*ins[:6], None, 1, ns, 1e-6, True)
+    BH, BHN, mat = B * H, B * H * N, d * d
+    prefix = (4 * BHN * mat + 8 * BHN + 63) // 64 * 64
+
+    def ws(nseg, nbuf):
+        return 4 * (prefix + nbuf * BH * nseg * ((3 * ns + 2) * mat + 1) + 2 * BH * mat)
+
+    full = lib.gmdn_chunk_bwd_workspace_bytes(ops_desc(ins, ns))
+    assert full >= ws(N, 1)
+    want = _fused_bwd(lib, ins, states, ns, full)
+    assert all(torch.isfinite(t).all() for t in want)
+    for nseg, nbuf in ((1, 1), (1, 2), (2, 2), (3, 2)):
+        got = _fused_bwd(lib, ins, states, ns, ws(nseg, nbuf))
+        for name, g_, w_ in zip("dq dk dv dbeta dg dgmu".split(), got, want):
+            assert torch.equal(g_, w_), (nseg, nbuf, name)
+
+
+def ops_desc(ins, ns):
+    from gmdn_amd import ops
+    q, k, v = ins[:3]
+    return ops.chunk_desc(q, k, v, ins[6], 1, ns, 1e-6, nat.PREC_TF32)
