@@ -691,7 +691,7 @@ def chunk_leg(w, steps: int, warmup: int, with_bwd: bool) -> dict:
                                f"chunk_fwd_{w.name}_traffic.md")
     if with_bwd:
         if rid == 1:
-            bwd_name = f"chunk_prep_muon<{w.d}> + scan_bwd_muon_pre/x3<{w.d}> + chunk_bwd_tok<{w.d},1>"
+            bwd_name = f"chunk_bwd_muon_pipe<{w.d}> (chunk_prep, muon_pre/x3, chunk_bwd_tok stages)"
         elif rid == 0:
             bwd_name = f"chunk_bwd_dscan<{w.d}> + chunk_bwd_pair<{w.d}>"
         elif w.d == 128:
