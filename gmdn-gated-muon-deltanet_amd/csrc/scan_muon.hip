@@ -10,8 +10,9 @@
 // Backward with fp32 products (precision 'ieee'): X_k, P, Xbar and Bbar
 // (4 D^2) exceed LDS at D = 128, so they live in a per-(b, h) global workspace
 // (L2 resident), followed by the ns stored iterates X_0 .. X_{ns-1} (written
-// and re-read by the same lanes).  The bf16x3 backward is described at its
-// kernels.
+// and re-read by the same lanes).  The bf16x3 backward's stages (iterate
+// rebuild, serial reverse scan) are in muon_bwd.h; scan_bwd_muon_seg runs
+// them a segment at a time.
 #include "muon_bwd.h"
 #include "ns.h"
 #include "scan_a.h"
