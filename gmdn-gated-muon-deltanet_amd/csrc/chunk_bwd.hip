@@ -587,8 +587,9 @@ static hipError_t launch_bwd_muon_chunks(const ChunkArgs& a, int ns, int precisi
     // Segments k = 0, 1, .. of plan.nseg chunks from the end.  Launch k runs
     // segment k's reverse pass, segment k + 1's iterates, segment k + 2's
     // matrix-form stage and segment k - 1's token gradients; two launches
-    // before (the first two segments' stage, the first segment's iterates)
-    // and one after (the last segment's token gradients) fill the pipeline.
+    // before (the first segment's stage, then its iterates with the second
+    // segment's stage) and one after (the last segment's token gradients)
+    // fill and drain the pipeline.
     const int N = (int)a.N, nseg = (int)plan.nseg;
     auto seg_lo = [&](int k) { return N - (k + 1) * nseg > 0 ? N - (k + 1) * nseg : 0; };
     auto seg_hi = [&](int k) { return N - k * nseg > 0 ? N - k * nseg : 0; };
@@ -620,8 +621,8 @@ static hipError_t launch_bwd_muon_chunks(const ChunkArgs& a, int ns, int precisi
       hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(D * 4), lds, stream, pa);
       return hipGetLastError();
     };
-    if (e == hipSuccess) e = launch(-1, -1, seg_lo(1), seg_hi(0), -1);
-    if (e == hipSuccess) e = launch(-1, 0, 0, 0, -1);
+    if (e == hipSuccess) e = launch(-1, -1, seg_lo(0), seg_hi(0), -1);
+    if (e == hipSuccess) e = launch(-1, 0, seg_lo(1), seg_hi(1), -1);
     for (int kk = 0; e == hipSuccess && kk < nsegs; ++kk)
       e = launch(kk, kk + 1, kk + 2 < nsegs ? seg_lo(kk + 2) : 0, kk + 2 < nsegs ? seg_hi(kk + 2) : 0, kk - 1);
     if (e == hipSuccess) e = launch(-1, -1, 0, 0, nsegs - 1);
