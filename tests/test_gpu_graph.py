@@ -23,11 +23,14 @@ def _dev():
     return torch.device("cuda:0")
 
 
-@pytest.mark.parametrize("rule,d,T", [("delta", 128, 512), ("delta", 64, 320), ("adam", 64, 512)])
-def test_training_step_graph_replays_match_eager(rule, d, T):
+# muon at B=2, H=16, T=1024, d=128: sixteen chunks in segments of fourteen,
+# so the backward runs its pipelined segment launches (two iterate buffers)
+@pytest.mark.parametrize("rule,d,T,H", [("delta", 128, 512, 2), ("delta", 64, 320, 2), ("adam", 64, 512, 2),
+                                        ("muon", 128, 1024, 16)])
+def test_training_step_graph_replays_match_eager(rule, d, T, H):
     dev = _dev()
-    w = Workload(f"graph_{rule}", rule, 2, 2, T, d)
-    print(f"case graph rule={rule} d={d} T={T}", flush=True)
+    w = Workload(f"graph_{rule}", rule, 2, H, T, d)
+    print(f"case graph rule={rule} d={d} T={T} H={H}", flush=True)
     inp = make_inputs(w, seed=3, device=dev)
     names = ("q", "k", "v", "beta", "g", "gmu", "gnu")
     xs = [None if inp[n] is None else inp[n].detach().requires_grad_(True) for n in names]
