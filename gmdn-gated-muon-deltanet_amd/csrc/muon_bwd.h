@@ -35,7 +35,7 @@ namespace gmdn {
 //        Xbar <- Q + (b Bs + c (Y + Y^T)) X_k     (B column reads)
 //      (P_k, Bs and Z_k are symmetric.)  Four D^3 products per step: the
 //      transposes are LDS reads of the published copies, and P_k comes from
-//      the first kernel instead of X_k (X_k^T Bs).
+//      the iterate stage instead of X_k (X_k^T Bs).
 //   3. The normalisation VJP, Gb = dU_i, and Sb <- (a Sb + gS) - Gb K_i^T
 //      with K_i staged into B (row reads).  Each phase issues its global
 //      loads together ahead of their first use.
