@@ -27,8 +27,8 @@ namespace gmdn {
 //      the end of the previous chunk); Xbar = b Sb; a Sb + gS parked in Sb's
 //      workspace rows until the tail.
 //   2. The VJP steps, k = ns-1 .. 0, with Xbar published in A and X_k in B:
-//        Q    = a Xbar + Z_k Xbar                 (A column reads, Z_k rows)
 //        Bbar = Xbar X_k^T                        (A and B row reads)
+//        Q    = a Xbar + Z_k Xbar                 (A column reads, Z_k rows)
 //        Bs   = Bbar + Bbar^T: Bbar published in A, read back transposed
 //        Y    = Bs P_k                            (Bs published in A, P_k rows)
 //        Y^T  read back transposed after publishing Y in A
