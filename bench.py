@@ -685,7 +685,8 @@ def chunk_leg(w, steps: int, warmup: int, with_bwd: bool) -> dict:
 
     chunks = w.B * w.H * (w.T // w.chunk)
     fwd_name = (f"chunk_fwd_muon<{w.d}> + chunk_out<{w.d}>" if rid == 1
-                else f"chunk_fwd_rows<{w.d},{rid}>" if rid == 0 or w.d == 64 else f"chunk_fwd<{w.d},{rid}>")
+                else f"chunk_fwd_rows<{w.d},0>" if rid == 0
+                else f"chunk_fwd_adam16<{w.d}>" if w.d == 64 else f"chunk_fwd<{w.d},{rid}>")
     out["roofline_fwd"] = roof(fwd_name, fwd_bytes_per_token_head(w) * units,
                                fwd_flops_per_chunk_head(w) * chunks, out["fwd_kernel_ms"],
                                f"chunk_fwd_{w.name}_traffic.md")

@@ -84,6 +84,8 @@ GMDN_DEV bf16x8 col8p(const bf16* X, int k0, int cb, int l = lane_id()) {
 hipError_t chunk_fwd_launch(const ChunkArgs& a, int d, int rule, hipStream_t s);
 // delta rule and adam: row-owned state waves, one barrier per chunk
 hipError_t chunk_fwd_rows_launch(const ChunkArgs& a, int d, int rule, hipStream_t s);
+// adam at d = 64: 16-row workgroups, four state waves per row block
+hipError_t chunk_fwd_adam16_launch(const ChunkArgs& a, int d, hipStream_t s);
 // rule 1: the serial muon scan (S_i, M_i of every chunk to S_out, M_out;
 // M_out may be null) and the chunk-parallel output kernel
 hipError_t chunk_fwd_muon_launch(const ChunkArgs& a, int d, float* S_out, float* M_out, int ns, hipStream_t s);

@@ -499,7 +499,8 @@ static hipError_t launch_fwd(const ChunkArgs& a, hipStream_t stream) {
 hipError_t chunk_fwd_launch(const ChunkArgs& a, int d, int rule, hipStream_t s) {
   // row-owned state waves: the delta rule, and adam at d = 64 (at d = 128
   // adam's three state tiles per row block exceed that kernel's registers)
-  if (rule == 0 || d == 64) return chunk_fwd_rows_launch(a, d, rule, s);
+  if (rule == 2 && d == 64) return chunk_fwd_adam16_launch(a, d, s);
+  if (rule == 0) return chunk_fwd_rows_launch(a, d, rule, s);
   return launch_fwd<128, 2>(a, s);
 }
 
