@@ -96,12 +96,17 @@ hipError_t wy_fwd_launch(const ChunkArgs& a, int d, float* ws, hipStream_t s);
 size_t wy_bwd_workspace_floats(int64_t B, int64_t H, int64_t T, int d);
 hipError_t wy_bwd_launch(const ChunkArgs& a, int d, float* ckpt, const void* dO, void* dq, void* dk, void* dv,
                          float* dbeta, float* dg, float* ws, hipStream_t s);
-hipError_t chunk_bwd_launch(const ChunkArgs& a, int d, int rule, hipStream_t s);
+// ascan_carry (adam at d = 64, B H d d * 3 floats, or null): the carry of
+// the reverse scan's segments; with it the scan runs in segments beside the
+// token gradients of the segment before, on a second stream
+hipError_t chunk_bwd_launch(const ChunkArgs& a, int d, int rule, float* ascan_carry, hipStream_t s);
 // delta rule: the reverse scan of the state cotangent (Gb of the odd chunks)
 hipError_t chunk_bwd_dscan_launch(const ChunkArgs& a, int d, hipStream_t s);
 // adam at d = 64: the reverse scan of the state and moment cotangents (Gb of
 // every chunk; partial sums of da, db, dm, dn per chunk and 16-row block)
-hipError_t chunk_bwd_ascan_launch(const ChunkArgs& a, int d, hipStream_t s);
+// over chunks c1 - 1 .. c0; the cotangents of chunk c1 enter from `carry`
+// (B H d d * 3 floats) unless c1 = N, and leave into it unless c0 = 0
+hipError_t chunk_bwd_ascan_launch(const ChunkArgs& a, int d, float* carry, int c0, int c1, hipStream_t s);
 // the matrix form's per-chunk Kw, Uv (fwd) and gS (bwd) as (B, H, N, d, d)
 // float32, and a, b, m, n (four B H N arrays): muon (fwd and bwd together,
 // for its backward) and adam at d = 128 (fwd: training forward, bwd: backward)

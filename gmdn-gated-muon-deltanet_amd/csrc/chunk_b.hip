@@ -561,6 +561,18 @@ size_t gb_planes(const gmdn_chunk_desc* desc) {
   return (size_t)(desc->B * desc->H * (desc->rule == 0 ? N / 2 : N));
 }
 
+// the delta rule's and adam's (d = 64) backward workspace without the carry:
+// Gb planes and the per-(chunk, row block) partial sums
+size_t chunk_bwd_min_ws_bytes(const gmdn_chunk_desc* desc) {
+  const size_t chunks = (size_t)(desc->B * desc->H * (desc->T / CB_C));
+  return gb_planes(desc) * desc->d * desc->d * sizeof(float) + chunks * (desc->d / 16) * 4 * sizeof(float);
+}
+
+// adam at d = 64: Sb, Mb, Vb between the reverse scan's segments
+size_t ascan_carry_bytes(const gmdn_chunk_desc* desc) {
+  return desc->rule == 2 && desc->d == 64 ? (size_t)(desc->B * desc->H) * desc->d * desc->d * 3 * sizeof(float) : 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -688,9 +700,9 @@ size_t gmdn_chunk_bwd_workspace_bytes(const gmdn_chunk_desc* desc) {
     return chunk_bwd_adam_mat_ws_floats(desc->B * desc->H, desc->T / CB_C, desc->d) * sizeof(float);
   // Gb_i, the cotangent of a chunk's state update (fp32 d x d per chunk; the
   // delta rule keeps the odd chunks' only), then per (chunk, row block)
-  // partial sums of the chunk scalars' gradients
-  const size_t chunks = (size_t)(desc->B * desc->H * (desc->T / CB_C));
-  return gb_planes(desc) * desc->d * desc->d * sizeof(float) + chunks * (desc->d / 16) * 4 * sizeof(float);
+  // partial sums of the chunk scalars' gradients; adam: then the carry of
+  // the reverse scan's segments
+  return chunk_bwd_min_ws_bytes(desc) + ascan_carry_bytes(desc);
 }
 
 int gmdn_chunk_bwd(const gmdn_chunk_desc* desc, const void* q, const void* k, const void* v,
@@ -712,10 +724,12 @@ int gmdn_chunk_bwd(const gmdn_chunk_desc* desc, const void* q, const void* k, co
   if (desc->rule == 2 && (desc->d == 128 || desc->dtype == GMDN_DTYPE_F32) && desc->eps != 1e-6f)
     return GMDN_ERR_UNSUPPORTED;
   if (desc->B * desc->H * (desc->T / CB_C) >= ((int64_t)1 << 31)) return GMDN_ERR_ARG;  // one workgroup per chunk
+  const bool bf16_rows = desc->dtype != GMDN_DTYPE_F32 && !(desc->rule == 2 && desc->d == 128);
   const size_t min_ws = desc->rule == 1 && desc->dtype != GMDN_DTYPE_F32 && desc->precision == GMDN_PREC_TF32
                             ? chunk_bwd_muon_min_ws_floats(desc->B * desc->H, desc->T / CB_C, desc->d, desc->ns) *
                                   sizeof(float)
-                            : gmdn_chunk_bwd_workspace_bytes(desc);
+                        : desc->rule != 1 && bf16_rows ? chunk_bwd_min_ws_bytes(desc)
+                                                       : gmdn_chunk_bwd_workspace_bytes(desc);
   if (!workspace || workspace_bytes < min_ws) return GMDN_ERR_WORKSPACE;
   // dO tiles arrive by 16-byte LDS-DMA loads and dq, dk, dv leave in 16-byte
   // row pieces: every stream needs 16-byte aligned rows
@@ -749,8 +763,12 @@ int gmdn_chunk_bwd(const gmdn_chunk_desc* desc, const void* q, const void* k, co
                                  workspace_bytes / sizeof(float), (hipStream_t)stream) == hipSuccess
                ? GMDN_OK
                : GMDN_ERR_LAUNCH;
-  return chunk_bwd_launch(a, desc->d, desc->rule, (hipStream_t)stream) == hipSuccess ? GMDN_OK
-                                                                                     : GMDN_ERR_LAUNCH;
+  // adam: the reverse scan in segments beside the token gradients when the
+  // workspace holds the carry (its default size), in one pass otherwise
+  const size_t base = chunk_bwd_min_ws_bytes(desc), carry = ascan_carry_bytes(desc);
+  float* ascan_carry = carry && workspace_bytes >= base + carry ? (float*)((char*)workspace + base) : nullptr;
+  return chunk_bwd_launch(a, desc->d, desc->rule, ascan_carry, (hipStream_t)stream) == hipSuccess ? GMDN_OK
+                                                                                                 : GMDN_ERR_LAUNCH;
 }
 
 }  // extern "C"

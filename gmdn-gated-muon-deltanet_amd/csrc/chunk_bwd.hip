@@ -34,6 +34,7 @@
 #include "muon_bwd.h"
 #include "scan_a.h"
 
+#include <mutex>
 #include <type_traits>
 
 namespace gmdn {
@@ -490,8 +491,102 @@ __global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok(ChunkArgs p)
   chunk_bwd_tok_body<D, RULE, MAT>(p, blockIdx.x / p.N, (int)(blockIdx.x % p.N));
 }
 
+// The token gradients of chunks c0 .. c1 - 1 of every (b, h): a grid-stride
+// loop over (b, h, chunk), so that a launch of fewer workgroups than CUs
+// leaves CUs to a reverse-scan segment running beside it.
 template <int D, int RULE>
-static hipError_t launch_bwd(const ChunkArgs& a, hipStream_t stream) {
+__global__ void __launch_bounds__(TokBwdLds<D>::NTHR) chunk_bwd_tok_range(ChunkArgs p, int c0, int c1) {
+  const int L = c1 - c0;
+  const int64_t n = p.B * p.H * (int64_t)L;
+  for (int64_t u = blockIdx.x; u < n; u += gridDim.x) {
+    if (u != blockIdx.x) __syncthreads();  // the previous chunk's LDS reads are done
+    chunk_bwd_tok_body<D, RULE>(p, u / L, c0 + (int)(u % L));
+  }
+}
+
+namespace {
+
+// A second stream per device (default priority) and the events that order
+// it against the caller's stream, created on first use; the mutex keeps one
+// call's records and waits together.
+struct AuxStream {
+  std::mutex mu;
+  bool tried = false, ok = false;
+  hipStream_t s = nullptr;
+  hipEvent_t ev[8] = {};
+  int cus = 0;
+};
+AuxStream g_aux[64];
+
+AuxStream* aux_stream() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  AuxStream& x = g_aux[dev];
+  std::lock_guard<std::mutex> lk(x.mu);
+  if (!x.tried) {
+    x.tried = true;
+    bool ok = hipStreamCreateWithFlags(&x.s, hipStreamNonBlocking) == hipSuccess &&
+              hipDeviceGetAttribute(&x.cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess;
+    for (int k = 0; ok && k < 8; ++k) ok = hipEventCreateWithFlags(&x.ev[k], hipEventDisableTiming) == hipSuccess;
+    x.ok = ok;
+  }
+  return x.ok ? &x : nullptr;
+}
+
+}  // namespace
+
+// adam at d = 64: the reverse scan in chunk segments (last chunks first) on
+// the caller's stream, each segment's token gradients on the second stream
+// beside the next segment's scan (chunk_bwd_tok_range on the CUs the scan's
+// B H D / 16 workgroups leave), joined back before returning.  The segments
+// shrink towards chunk 0 (half, a third, the rest of the chunks), so each
+// segment's token gradients finish under the next segment's scan and only the
+// smallest runs alone; each segment costs the scan a pipeline fill.  Without
+// a carry area, or with few chunks, one scan pass then the token kernel.
+template <int D>
+static hipError_t launch_bwd_adam(const ChunkArgs& a, float* carry, hipStream_t stream) {
+  constexpr int lds2 = TokBwdLds<D>::BYTES;
+  constexpr int thr2 = TokBwdLds<D>::NTHR;
+  const int N = a.N;
+  const int nseg = !carry ? 1 : N >= 32 ? 3 : N >= 16 ? 2 : 1;
+  AuxStream* ax = nseg > 1 ? aux_stream() : nullptr;
+  if (!ax) {
+    hipError_t e = chunk_bwd_ascan_launch(a, D, carry, 0, N, stream);
+    if (e != hipSuccess) return e;
+    auto k2 = chunk_bwd_tok<D, 2>;
+    e = hipFuncSetAttribute((const void*)k2, hipFuncAttributeMaxDynamicSharedMemorySize, lds2);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k2, dim3((unsigned)(a.B * a.H * N)), dim3(thr2), lds2, stream, a);
+    return hipGetLastError();
+  }
+  auto kr = chunk_bwd_tok_range<D, 2>;
+  hipError_t e = hipFuncSetAttribute((const void*)kr, hipFuncAttributeMaxDynamicSharedMemorySize, lds2);
+  if (e != hipSuccess) return e;
+  const int64_t scan_wgs = a.B * a.H * (D / 16);
+  std::lock_guard<std::mutex> lk(ax->mu);
+  // segment lengths: N / 2, N / 3, the rest (two segments: 2 N / 3, the rest)
+  const int len[3] = {nseg == 3 ? N / 2 : 2 * N / 3, N / 3, N};
+  int c1 = N;
+  for (int k = 0; k < nseg; ++k) {
+    const int c0 = k + 1 < nseg ? c1 - len[k] : 0;
+    if ((e = chunk_bwd_ascan_launch(a, D, carry, c0, c1, stream)) != hipSuccess) return e;
+    if ((e = hipEventRecord(ax->ev[k], stream)) != hipSuccess) return e;
+    if ((e = hipStreamWaitEvent(ax->s, ax->ev[k], 0)) != hipSuccess) return e;
+    // beside the next segment's scan: the CUs it leaves; the last segment's
+    // token gradients run alone
+    const int64_t units = a.B * a.H * (int64_t)(c1 - c0);
+    const int64_t free_cus = ax->cus - scan_wgs;
+    const int64_t grid = k + 1 < nseg && free_cus > 0 && free_cus < units ? free_cus : units;
+    hipLaunchKernelGGL(kr, dim3((unsigned)grid), dim3(thr2), lds2, ax->s, a, c0, c1);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    c1 = c0;
+  }
+  if ((e = hipEventRecord(ax->ev[7], ax->s)) != hipSuccess) return e;
+  return hipStreamWaitEvent(stream, ax->ev[7], 0);
+}
+
+template <int D, int RULE>
+static hipError_t launch_bwd(const ChunkArgs& a, float* carry, hipStream_t stream) {
   if constexpr (RULE == 0) {
     // delta: the reverse scan (Gb of the odd chunks), then the token
     // gradients of chunk pairs (even checkpoints, odd Gb)
@@ -499,17 +594,9 @@ static hipError_t launch_bwd(const ChunkArgs& a, hipStream_t stream) {
     if (e != hipSuccess) return e;
     return chunk_bwd_pair_launch(a, D, stream);
   } else {
-    constexpr int lds2 = TokBwdLds<D>::BYTES;
-    constexpr int thr2 = TokBwdLds<D>::NTHR;
     // adam: the reverse scan of the state and moment cotangents (Gb of every
     // chunk, per-row-block partial sums), then the token gradients
-    hipError_t e = chunk_bwd_ascan_launch(a, D, stream);
-    if (e != hipSuccess) return e;
-    auto k2 = chunk_bwd_tok<D, RULE>;
-    e = hipFuncSetAttribute((const void*)k2, hipFuncAttributeMaxDynamicSharedMemorySize, lds2);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k2, dim3((unsigned)(a.B * a.H * a.N)), dim3(thr2), lds2, stream, a);
-    return hipGetLastError();
+    return launch_bwd_adam<D>(a, carry, stream);
   }
 }
 
@@ -701,10 +788,10 @@ hipError_t chunk_bwd_muon_launch(const ChunkArgs& a, int d, int ns, int precisio
   return hipErrorNotSupported;
 }
 
-hipError_t chunk_bwd_launch(const ChunkArgs& a, int d, int rule, hipStream_t s) {
-  if (rule == 0) return d == 128 ? launch_bwd<128, 0>(a, s) : launch_bwd<64, 0>(a, s);
+hipError_t chunk_bwd_launch(const ChunkArgs& a, int d, int rule, float* ascan_carry, hipStream_t s) {
+  if (rule == 0) return d == 128 ? launch_bwd<128, 0>(a, nullptr, s) : launch_bwd<64, 0>(a, nullptr, s);
   // adam at d = 128 is refused by the caller: its VJP is ill-conditioned there
-  if (rule == 2 && d == 64) return launch_bwd<64, 2>(a, s);
+  if (rule == 2 && d == 64) return launch_bwd<64, 2>(a, ascan_carry, s);
   return hipErrorNotSupported;
 }
 

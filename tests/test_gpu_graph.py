@@ -26,7 +26,7 @@ def _dev():
 # muon at B=2, H=16, T=1024, d=128: sixteen chunks in segments of fourteen,
 # so the backward runs its pipelined segment launches (two iterate buffers)
 @pytest.mark.parametrize("rule,d,T,H", [("delta", 128, 512, 2), ("delta", 64, 320, 2), ("adam", 64, 512, 2),
-                                        ("muon", 128, 1024, 16)])
+                                        ("adam", 64, 2560, 2), ("muon", 128, 1024, 16)])
 def test_training_step_graph_replays_match_eager(rule, d, T, H):
     dev = _dev()
     w = Workload(f"graph_{rule}", rule, 2, H, T, d)
