@@ -14,8 +14,9 @@
 // (train_ablation.py:150-158, :169-175).  Only q, k, v, beta and the
 // log-gates stream from HBM; o streams out; S stays in registers.
 //
-// The delta rule's forward, and adam's at d = 64, run chunk_fwd_rows
-// (csrc/chunk_fwd_rows.hip); the kernel below serves adam at d = 128.
+// The delta rule's forward runs chunk_fwd_rows (csrc/chunk_fwd_rows.hip),
+// adam's at d = 64 chunk_fwd_adam16 (csrc/chunk_fwd_adam.hip); the kernel
+// below serves adam at d = 128.
 // Work split (forward).  A workgroup of 4 waves owns 32 rows of S for the
 // whole sequence; wave (rt, h) owns row tile rt (16 rows) and column half h
 // of S, the token half h of E and of o, and the column half h of G.  Two LDS

@@ -27,7 +27,9 @@
 //    workgroup.  chunk_bwd_tok (adam) takes one chunk per workgroup; the
 //    delta rule runs the same phases over chunk pairs (chunk_bwd_pair.hip).
 //    The kernel's template still carries the delta branches those phases
-//    share.
+//    share.  Adam at d = 64 runs the reverse scan in chunk segments with each
+//    segment's token gradients beside the next segment's scan, on a second
+//    stream (launch_bwd_adam below).
 #include "../../include/gmdn_scan.h"
 #include "chunk_b.h"
 #include "chunk_prep.h"

@@ -17,23 +17,23 @@
 // and the per-(chunk, row block) partial sums of da, db, dm, dn go to the
 // token-gradient kernel chunk_bwd_tok<64, 2>.
 //
-// Work split: ten waves; step j works on chunk N-1-j, with three barriers
-// Z(j), Y(j), X(j) (phases A, B, C end at them).
+// Work split: ten waves; step j works on chunk c1-1-j of the launch's
+// segment, with three barriers Z(j), Y(j), X(j) (phases A, B, C end at them).
 //  * State waves 0-3 (SIMDs 0-3): wave q owns column tile q of Sb, Mb, Vb
 //    (4 values per lane, the forward's column-permuted state layout) and
 //    token tile q of X and -dE.  A: the elementwise VJP of its tile from the
-//    step's precomputed factors; Gb's tile published as split pieces (the
-//    staging the store also reads); the partial products of da, db, dm, dn.
-//    B: X = K Gb^T of token tile q from every wave's Gb pieces, -dE = -(X + P)
-//    published.  C: Sb^T = a Sb^T + C + K^T (-dE) of column tile q from
-//    every token tile's -dE.  Each wave does a quarter of the row block's
-//    products and elementwise work.
+//    step's factors; Gb's tile published as split pieces (the staging the
+//    store also reads); the partial products of da, db, dm, dn.  B: X = K Gb^T
+//    of token tile q from every wave's Gb pieces, -dE = -(X + P) published.
+//    C: Sb^T = a Sb^T + C + K^T (-dE) of column tile q from every token
+//    tile's -dE, then, for the next step, G's column tile q from the
+//    published -E tiles and the tile's seven elementwise factors (the
+//    forward's Mi, Vi recomputed), kept in registers.  Each wave does a
+//    quarter of the row block's products and elementwise work.
 //  * Token waves 4-7 (tile tw = w - 4), one step ahead.  A: -E = K S^T - V of
-//    token tile tw of the next chunk (from the forward's S checkpoint).  B: G's
-//    column tile tw from all four -E tiles, and the seven elementwise factors
-//    of that tile (the forward's Mi, Vi recomputed).  C: the causal A tiles of
-//    key tile {0, 1, 3, 2}[tw] with P = A^T dO, C = dO^T Q of column tile tw;
-//    wave 6 also reduces the step's partial sums.
+//    token tile tw of the next chunk (from the forward's S checkpoint).
+//    B: the causal A tiles of key tile {0, 1, 3, 2}[tw] with P = A^T dO, and
+//    C = dO^T Q of column tile tw.  C: wave 6 reduces the step's partial sums.
 //  * Copy waves 8, 9: the LDS-DMA copies (the chunk's tiles three steps
 //    ahead, the checkpoint's rows two), Gb_i's store from the staging, and
 //    the chunk scalars a, b, m, n lane-parallel (lane c: chunk 64 J + c) from
