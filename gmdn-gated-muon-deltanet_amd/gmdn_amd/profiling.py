@@ -23,7 +23,8 @@ dispatch) into HBM bytes per launch of the kernels matching REGEX (summed
 over the kernels when the op runs several).  Each
 counter is scaled by what it reads for a plain device copy of N bytes
 (N read + N written), so the figure is in the same units as the algorithmic
-bytes.  The output is markdown; its ``traffic_bytes_per_launch:`` line is
+bytes.  ``--calls-per-op K`` sums K dispatches of each kernel per launch (their
+mean times K) for an op that runs its kernels in K segments.  The output is markdown; its ``traffic_bytes_per_launch:`` line is
 what bench.py reads back.
 """
 from __future__ import annotations
@@ -87,10 +88,16 @@ def counter_by_kernel(d: str, counter: str, kernel_regex: str):
     return out
 
 
-def _per_launch(d: str, counter: str, kernel_regex: str) -> float:
-    """Sum over the matching kernels of each one's median per-dispatch value:
-    the counter for one launch of the op when it runs those kernels once each."""
-    return sum(statistics.median(v) for v in counter_by_kernel(d, counter, kernel_regex).values())
+def _per_launch(d: str, counter: str, kernel_regex: str, calls_per_op: int = 1) -> float:
+    """The counter for one launch of the op: with calls_per_op = 1 (the op
+    runs each matching kernel once) the sum over the kernels of each one's
+    median per-dispatch value; otherwise each kernel's mean per dispatch times
+    calls_per_op (an op that runs every kernel that many times, in dispatches
+    of different sizes, such as a scan in chunk segments)."""
+    per = counter_by_kernel(d, counter, kernel_regex).values()
+    if calls_per_op == 1:
+        return sum(statistics.median(v) for v in per)
+    return sum(statistics.fmean(v) * calls_per_op for v in per)
 
 
 def _stats_md(d: str, kernel_regex: str = "") -> str:
@@ -105,8 +112,8 @@ def _stats_md(d: str, kernel_regex: str = "") -> str:
 
 def _traffic_md(a) -> str:
     kib = 1024.0
-    fetch = _per_launch(a.fetch, "FETCH_SIZE", a.kernel)
-    write = _per_launch(a.write, "WRITE_SIZE", a.kernel)
+    fetch = _per_launch(a.fetch, "FETCH_SIZE", a.kernel, a.calls_per_op)
+    write = _per_launch(a.write, "WRITE_SIZE", a.kernel, a.calls_per_op)
     cf = statistics.median(counter_per_dispatch(a.copy_fetch, "FETCH_SIZE", a.copy_kernel))
     cw = statistics.median(counter_per_dispatch(a.copy_write, "WRITE_SIZE", a.copy_kernel))
     sf, sw = a.copy_bytes / (cf * kib), a.copy_bytes / (cw * kib)
@@ -195,6 +202,8 @@ def main(argv=None):
     t.add_argument("--copy-fetch", required=True)
     t.add_argument("--copy-write", required=True)
     t.add_argument("--copy-bytes", type=int, required=True)
+    t.add_argument("--calls-per-op", type=int, default=1,
+                   help="dispatches of each matching kernel per launch of the op (segmented scans)")
     m = sub.add_parser("mfma")
     m.add_argument("dir")
     m.add_argument("--kernel", default="", help="only kernels whose name matches this regex")
