@@ -219,7 +219,13 @@ int gmdn_wy_bwd(const gmdn_chunk_desc* desc, const void* q, const void* k, const
  * in 'tf32' also runs with any smaller workspace down to one-chunk segments
  * of its reverse scan (the results do not depend on the segment length);
  * this size gives segments of up to 512 MiB of iterates, in two buffers
- * when they do not hold every chunk. */
+ * when they do not hold every chunk.  Adam (rule 2) at d = 64 on bfloat16
+ * streams: this size ends with a carry of the reverse scan's cotangents
+ * (B H d d * 3 floats), with which the scan runs in chunk segments and each
+ * segment's token gradients run on a second stream of the library's (one
+ * per device, default priority) beside the next segment's scan, joined back
+ * before the call returns; a workspace smaller by that carry runs one scan
+ * pass on the caller's stream.  Both give the same results bit for bit. */
 size_t gmdn_chunk_bwd_workspace_bytes(const gmdn_chunk_desc* desc);
 
 /* Backward given dO (strides desc->so) and the forward's `states`.  Writes
