@@ -698,7 +698,7 @@ def chunk_leg(w, steps: int, warmup: int, with_bwd: bool) -> dict:
         elif w.d == 128:
             bwd_name = "chunk_prep<128,2> + scan_bwd_rows<128,2> (fp32) + chunk_bwd_tok<128,2>"
         else:
-            bwd_name = f"chunk_bwd_ascan<{w.d}> + chunk_bwd_tok_range<{w.d},{rid}> (3 segments, two streams)"
+            bwd_name = f"chunk_bwd_ascan<{w.d}> + chunk_bwd_tok_range<{w.d},{rid}> (2 segments, two streams)"
         out["roofline"] = roof(bwd_name, bwd_bytes_per_token_head(w) * units,
                                bwd_flops_per_chunk_head(w) * chunks, out["bwd_ms"],
                                f"chunk_bwd_{w.name}_traffic.md")

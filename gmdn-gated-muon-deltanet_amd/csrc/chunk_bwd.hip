@@ -540,18 +540,21 @@ AuxStream* aux_stream() {
 // adam at d = 64: the reverse scan in chunk segments (last chunks first) on
 // the caller's stream, each segment's token gradients on the second stream
 // beside the next segment's scan (chunk_bwd_tok_range on the CUs the scan's
-// B H D / 16 workgroups leave), joined back before returning.  The segments
-// shrink towards chunk 0 (half, a third, the rest of the chunks), so each
-// segment's token gradients finish under the next segment's scan and only the
-// smallest runs alone; each segment costs the scan a pipeline fill.  Without
-// a carry area, or with few chunks, one scan pass then the token kernel.
+// B H D / 16 workgroups leave), joined back before returning.  Two segments:
+// the last holds the chunks whose token gradients fit one round of one
+// workgroup per CU (CUs / (B H) chunks, at most half), the token launch that
+// runs alone; each segment costs the scan a pipeline fill, so two beat three
+// or more.  Without a carry area, with few chunks, or when the scan's
+// workgroups fill more than half the CUs, one scan pass then the token
+// kernel.
 template <int D>
 static hipError_t launch_bwd_adam(const ChunkArgs& a, float* carry, hipStream_t stream) {
   constexpr int lds2 = TokBwdLds<D>::BYTES;
   constexpr int thr2 = TokBwdLds<D>::NTHR;
   const int N = a.N;
-  const int nseg = !carry ? 1 : N >= 32 ? 3 : N >= 16 ? 2 : 1;
-  AuxStream* ax = nseg > 1 ? aux_stream() : nullptr;
+  const int64_t scan_wgs = a.B * a.H * (D / 16);
+  AuxStream* ax = carry && N >= 16 ? aux_stream() : nullptr;
+  if (ax && 2 * scan_wgs > ax->cus) ax = nullptr;
   if (!ax) {
     hipError_t e = chunk_bwd_ascan_launch(a, D, carry, 0, N, stream);
     if (e != hipSuccess) return e;
@@ -564,10 +567,11 @@ static hipError_t launch_bwd_adam(const ChunkArgs& a, float* carry, hipStream_t 
   auto kr = chunk_bwd_tok_range<D, 2>;
   hipError_t e = hipFuncSetAttribute((const void*)kr, hipFuncAttributeMaxDynamicSharedMemorySize, lds2);
   if (e != hipSuccess) return e;
-  const int64_t scan_wgs = a.B * a.H * (D / 16);
   std::lock_guard<std::mutex> lk(ax->mu);
-  // segment lengths: N / 2, N / 3, the rest (two segments: 2 N / 3, the rest)
-  const int len[3] = {nseg == 3 ? N / 2 : 2 * N / 3, N / 3, N};
+  const int64_t fit = ax->cus / (a.B * a.H);
+  const int last = (int)(fit < 1 ? 1 : fit < N / 2 ? fit : N / 2);
+  const int nseg = 2;
+  const int len[2] = {N - last, last};
   int c1 = N;
   for (int k = 0; k < nseg; ++k) {
     const int c0 = k + 1 < nseg ? c1 - len[k] : 0;

@@ -131,7 +131,7 @@ def test_fused_adam_backward_segments_bit_identical(N):
     chunk segments and each segment's token gradients on a second stream
     beside the next segment's scan; a workspace without the carry runs one
     scan pass, then the token kernel.  The gradients are equal bit for bit
-    (2 segments at N = 16, 3 at N = 40 and 64)."""
+    (two segments: N / 2 each at B H = 2)."""
     from gmdn_amd import ops
     from gmdn_amd.workloads import Workload, make_inputs
     dev = _dev()
