@@ -62,6 +62,16 @@ struct TokBwdLds {
   static_assert(BYTES <= 160 * 1024, "token backward LDS exceeds the 160 KiB of a CU");
 };
 
+// Adam with four waves (d = 64) keeps its gates in registers and stores
+// dbeta per wave (each wave's dA tiles share one token tile), so it needs no
+// reduction area: 80 KiB, two workgroups per CU.
+// (Not MAT: the drop-in scan's per-chunk gradients keep the general path.)
+template <int D, int RULE, bool MAT>
+constexpr bool tok_regs() { return RULE == 2 && !MAT && TokBwdLds<D>::NW == 4; }
+template <int D, int RULE, bool MAT = false>
+constexpr int tok_lds_bytes() { return tok_regs<D, RULE, MAT>() ? TokBwdLds<D>::R0 : TokBwdLds<D>::BYTES; }
+static_assert(tok_lds_bytes<64, 2>() <= 80 * 1024, "two adam token workgroups per CU");
+
 // MAT: S_i and Gb_i are the drop-in scan's float32 rows and the chunk
 // scalars' gradients arrive as arrays [da | db | dm | dn] (B H N each) in
 // p.part -- muon always, adam when its scan ran in exact float32 (d = 128)
@@ -107,6 +117,10 @@ GMDN_DEV void chunk_bwd_tok_body(const ChunkArgs& p, int64_t bh, int i) {
   const int l = lane_id(), G = l >> 4, lc = l & 15;
   const int64_t bb = bh / p.H, hh = bh % p.H;
   const int64_t t0 = (int64_t)i * CB_C;
+  // adam at d = 64: beta of the wave's token tile (16 (w % 4) + lc) in a
+  // register; wave 0's lanes keep g, gmu, gnu of their token (gv below)
+  constexpr bool REGG = tok_regs<D, RULE, MAT>();
+  const float bw = REGG ? p.beta[bh * p.T + t0 + 16 * (w & 3) + lc] : 0.f;
   const float* S = p.states + (bh * p.N + i) * (int64_t)D * D;
   const float* Gb = p.gb + (bh * p.N + i) * (int64_t)D * D;
   const int r0 = 16 * w;  // this wave's state rows (phase I) ...
@@ -147,7 +161,7 @@ GMDN_DEV void chunk_bwd_tok_body(const ChunkArgs& p, int64_t bh, int i) {
   // vector-memory operations complete in issue order: with the 4 NKB row
   // loads still in flight, the gates and the four tiles have landed
   wait_vmem_le<4 * NKB>();
-  if (threadIdx.x < CB_C) {
+  if (!REGG && threadIdx.x < CB_C) {
     const int e = threadIdx.x;
     rbeta[e] = gv[0];
     rg[e] = gv[1];
@@ -183,7 +197,7 @@ GMDN_DEV void chunk_bwd_tok_body(const ChunkArgs& p, int64_t bh, int i) {
       for (int kb = 0; kb < NKB; ++kb)
         X = mfma(row8<LQ>(Qs, 16 * tt + lc, 32 * kb), row8<LQ>(Ks, 16 * st + lc, 32 * kb), X);
       // lane (s, G) holds A[t = 16 tt + 4G + jj][s = 16 st + lc]
-      const float bs = rbeta[16 * st + lc];
+      const float bs = REGG ? bw : rbeta[16 * st + lc];
       f32x4 xv;
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) xv[jj] = (tt > st || 4 * G + jj >= lc) ? X[jj] * bs : 0.f;
@@ -274,7 +288,7 @@ GMDN_DEV void chunk_bwd_tok_body(const ChunkArgs& p, int64_t bh, int i) {
           for (int st = 0; st < 4; ++st) pdw[w * CB_C + 16 * st + lc] = dbp[st];
         }
       }
-      if (G == 0) {
+      if (!REGG && G == 0) {
 #pragma unroll
         for (int st = 0; st < 4; ++st) pdbeta[w * CB_C + 16 * st + lc] = 0.f;
       }
@@ -301,7 +315,7 @@ GMDN_DEV void chunk_bwd_tok_body(const ChunkArgs& p, int64_t bh, int i) {
         P = mma<1, 2>(dOr, Er, P);
         QK = mfma(row8<LQ>(Qs, 16 * tt + lc, 32 * kb), row8<LQ>(Ks, 16 * st + lc, 32 * kb), QK);
       }
-      const float bs = rbeta[16 * st + lc];
+      const float bs = REGG ? bw : rbeta[16 * st + lc];
       float db = 0.f;
       f32x4 pb;
 #pragma unroll
@@ -327,17 +341,31 @@ GMDN_DEV void chunk_bwd_tok_body(const ChunkArgs& p, int64_t bh, int i) {
       const float v = group_sum(dbk[kk]);
       if (tt >= st) db += v;
     }
-    if (G == 0) pdbeta[w * CB_C + 16 * (w & 3) + lc] += db;
+    if constexpr (REGG) {
+      // adam: dbeta of the wave's tokens 16 w + lc, the A term and
+      // db / 64 (b = mean(beta); db from the reverse scan's partial sums)
+      if (G == 0) {
+        const float* pp = p.part + (bh * p.N + i) * (int64_t)(D / 16) * 4;
+        float sdb = 0.f;
+#pragma unroll
+        for (int r = 0; r < D / 16; ++r) sdb += pp[4 * r + 1];
+        p.dbeta[bh * p.T + t0 + 16 * w + lc] = db + sdb * (1.f / CB_C);
+      }
+    } else {
+      if (G == 0) pdbeta[w * CB_C + 16 * (w & 3) + lc] += db;
+    }
   }
   __syncthreads();
 
   // ---------------- gate gradients and dV
   if (w == 0) {
     const int64_t o = bh * p.T + t0 + l;
-    const float a = expf(wave_sum(fmaxf(rg[l], LOG_FLOOR)));
+    const float a = expf(wave_sum(fmaxf(REGG ? gv[1] : rg[l], LOG_FLOOR)));
     float rdb = 0.f;
+    if constexpr (!REGG) {
 #pragma unroll
-    for (int q = 0; q < NW; ++q) rdb += pdbeta[q * CB_C + l];
+      for (int q = 0; q < NW; ++q) rdb += pdbeta[q * CB_C + l];
+    }
     if constexpr (RULE == 0) {
       float da = 0.f;
 #pragma unroll
@@ -378,12 +406,20 @@ GMDN_DEV void chunk_bwd_tok_body(const ChunkArgs& p, int64_t bh, int i) {
 #pragma unroll
           for (int c = 0; c < 4; ++c) sc[c] += pp[4 * r + c];
       }
-      const float m = expf(wave_sum(fmaxf(rgmu[l], LOG_FLOOR)));
-      const float n = expf(wave_sum(fmaxf(rgnu[l], LOG_FLOOR)));
-      p.dbeta[o] = rdb + sc[1] * (1.f / CB_C);  // b = mean(beta)
-      p.dg[o] = rg[l] >= LOG_FLOOR ? sc[0] * a : 0.f;
-      p.dgmu[o] = rgmu[l] >= LOG_FLOOR ? sc[2] * m : 0.f;
-      p.dgnu[o] = rgnu[l] >= LOG_FLOOR ? sc[3] * n : 0.f;
+      if constexpr (REGG) {  // g, gmu, gnu of token l in this wave's registers
+        const float m = expf(wave_sum(fmaxf(gv[2], LOG_FLOOR)));
+        const float n = expf(wave_sum(fmaxf(gv[3], LOG_FLOOR)));
+        p.dg[o] = gv[1] >= LOG_FLOOR ? sc[0] * a : 0.f;
+        p.dgmu[o] = gv[2] >= LOG_FLOOR ? sc[2] * m : 0.f;
+        p.dgnu[o] = gv[3] >= LOG_FLOOR ? sc[3] * n : 0.f;
+      } else {
+        const float m = expf(wave_sum(fmaxf(rgmu[l], LOG_FLOOR)));
+        const float n = expf(wave_sum(fmaxf(rgnu[l], LOG_FLOOR)));
+        p.dbeta[o] = rdb + sc[1] * (1.f / CB_C);  // b = mean(beta)
+        p.dg[o] = rg[l] >= LOG_FLOOR ? sc[0] * a : 0.f;
+        p.dgmu[o] = rgmu[l] >= LOG_FLOOR ? sc[2] * m : 0.f;
+        p.dgnu[o] = rgnu[l] >= LOG_FLOOR ? sc[3] * n : 0.f;
+      }
     }
   }
   {
@@ -549,7 +585,7 @@ AuxStream* aux_stream() {
 // kernel.
 template <int D>
 static hipError_t launch_bwd_adam(const ChunkArgs& a, float* carry, hipStream_t stream) {
-  constexpr int lds2 = TokBwdLds<D>::BYTES;
+  constexpr int lds2 = tok_lds_bytes<D, 2>();
   constexpr int thr2 = TokBwdLds<D>::NTHR;
   const int N = a.N;
   const int64_t scan_wgs = a.B * a.H * (D / 16);
