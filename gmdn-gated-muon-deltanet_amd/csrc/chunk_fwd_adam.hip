@@ -1,7 +1,8 @@
 // Level B forward of the adam rule at d = 64 with 16-row workgroups.
 //
-// Mathematics as chunk_fwd_rows<64, 2> (reference train_ablation.py:142-187
-// with fast_scan.py:86-94, E-form): per (b, h) and chunk i with state S_i,
+// The fused E-form (reference train_ablation.py:142-187 with
+// fast_scan.py:86-94), as chunk_fwd<D, 2> computes it: per (b, h) and chunk i
+// with state S_i,
 //   E = V - K S_i^T,   o = Q S_i^T + tril(Q K^T) diag(beta) E,
 //   G = E^T K,  M <- m M + (1-m) G,  V <- n V + (1-n) G^2,
 //   S_{i+1} = a S_i + b M / (sqrt(V) + eps).
